@@ -1,0 +1,407 @@
+// C ABI of the quantized matrix-product path: contexts, device buffers,
+// repack marks, the matmul router and the op entry points. Declarations and
+// the reference interfaces they replace are in include/elffuss_amd.h.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/elffuss_amd.h"
+#include "eff_formats.h"
+#include "eff_kernels.h"
+
+using namespace eff;
+
+// Bytes allocated past every eff_buf_alloc request. Kernels read at most 4
+// bytes past a block (the reference's loader slack, model.js:248-254).
+static constexpr size_t kSlack = 256;
+
+struct eff_ctx {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  std::string error;
+  int64_t gemv_max_tokens = 8;
+  int64_t gemm_min_tokens = 64;
+  eff_stats stats{};
+  void *topk_scratch = nullptr;
+  size_t topk_scratch_bytes = 0;
+};
+
+struct eff_buf {
+  void *ptr = nullptr;
+  size_t size = 0;
+  bool owned = false;
+  int mark_type = 0;        // EFF_TYPE_Q8_0R when marked
+  uint32_t mark_blocks = 0; // N of the tensor
+};
+
+namespace {
+
+int fail(eff_ctx *ctx, int code, const char *fmt, ...) {
+  if (ctx) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    ctx->error = buf;
+  }
+  return code;
+}
+
+int hip_fail(eff_ctx *ctx, hipError_t e, const char *what) {
+  return fail(ctx, EFF_E_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define EFF_HIP(ctx, call)                              \
+  do {                                                  \
+    hipError_t e_ = (call);                             \
+    if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
+  } while (0)
+
+// Select the context's device for the calling thread.
+int use_device(eff_ctx *ctx) {
+  EFF_HIP(ctx, hipSetDevice(ctx->device));
+  return EFF_OK;
+}
+
+// Validate a matmul-shaped call and build the weight view. Mirrors the checks
+// of quant.matmul (ops.js:846-870): known type, k a multiple of the block,
+// repacked buffers marked with the tensor's N and not read beyond it.
+int weight_view(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k,
+                uint32_t tokens, WeightView &wv, const char *who) {
+  if (!ctx) return EFF_E_INVALID;
+  if (!w || !x || !y) return fail(ctx, EFF_E_INVALID, "%s: null buffer", who);
+  if (!type_known(type)) return fail(ctx, EFF_E_TYPE, "%s: unsupported quantization type %d", who, type);
+  if (rows == 0 || k == 0 || tokens == 0) return fail(ctx, EFF_E_INVALID, "%s: empty shape rows=%u k=%u tokens=%u", who, rows, k, tokens);
+  Geometry g = geometry(type);
+  if (k % g.elems) return fail(ctx, EFF_E_SHAPE, "%s %s: k=%u is not a multiple of %u", who, eff_type_name(type), k, g.elems);
+  const uint32_t bpr = k / g.elems;
+  const uint64_t nblocks = (uint64_t)rows * bpr;
+  wv.w = (const uint8_t *)w->ptr;
+  wv.type = type;
+  wv.rows = rows;
+  wv.k = k;
+  wv.bpr = bpr;
+  wv.row_bytes = (uint64_t)bpr * g.bytes;
+  wv.scales_off = 0;
+  if (type == EFF_TYPE_Q8_0R) {
+    if (w->mark_type != EFF_TYPE_Q8_0R)
+      return fail(ctx, EFF_E_MARK, "%s Q8_0R: the buffer does not carry the mark of a repacked tensor "
+                  "(eff_buf_mark_r); the scale region is located from the tensor's block count", who);
+    if (nblocks > w->mark_blocks)
+      return fail(ctx, EFF_E_MARK, "%s Q8_0R: the call reads %llu blocks and the tensor has %u", who,
+                  (unsigned long long)nblocks, w->mark_blocks);
+    wv.scales_off = (uint64_t)32 * w->mark_blocks;
+  } else if (nblocks * g.bytes > w->size) {
+    return fail(ctx, EFF_E_BOUNDS, "%s %s: W needs %llu bytes and the buffer has %zu", who, eff_type_name(type),
+                (unsigned long long)(nblocks * g.bytes), w->size);
+  }
+  if ((uint64_t)tokens * k * 4 > x->size)
+    return fail(ctx, EFF_E_BOUNDS, "%s: x needs %llu bytes and the buffer has %zu", who,
+                (unsigned long long)tokens * k * 4, x->size);
+  if ((uint64_t)tokens * rows * 4 > y->size)
+    return fail(ctx, EFF_E_BOUNDS, "%s: y needs %llu bytes and the buffer has %zu", who,
+                (unsigned long long)tokens * rows * 4, y->size);
+  if (((uintptr_t)x->ptr | (uintptr_t)y->ptr | (uintptr_t)w->ptr) & 15)
+    return fail(ctx, EFF_E_INVALID, "%s: device buffers must be 16-byte aligned", who);
+  return EFF_OK;
+}
+
+int run_gemv(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
+  GemvPlan p = plan_gemv(wv, tokens);
+  hipError_t e = launch_gemv(wv, x, y, tokens, p, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "gemv launch");
+  return EFF_OK;
+}
+
+int run_gemm(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
+  hipError_t e = launch_gemm(wv, x, y, tokens, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
+  return EFF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int eff_init(int device, eff_ctx **out) {
+  if (!out) return EFF_E_INVALID;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return EFF_E_DEVICE;
+  eff_ctx *ctx = new eff_ctx();
+  ctx->device = device;
+  if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking) != hipSuccess) {
+    delete ctx;
+    return EFF_E_DEVICE;
+  }
+  ctx->stream = ctx->own;
+  *out = ctx;
+  return EFF_OK;
+}
+
+int eff_shutdown(eff_ctx *ctx) {
+  if (!ctx) return EFF_E_INVALID;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->topk_scratch) (void)hipFree(ctx->topk_scratch);
+  if (ctx->own) (void)hipStreamDestroy(ctx->own);
+  delete ctx;
+  return EFF_OK;
+}
+
+const char *eff_last_error(const eff_ctx *ctx) { return ctx ? ctx->error.c_str() : "no context"; }
+
+void *eff_stream(eff_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int eff_set_stream(eff_ctx *ctx, void *hip_stream) {
+  if (!ctx) return EFF_E_INVALID;
+  ctx->stream = hip_stream ? (hipStream_t)hip_stream : ctx->own;
+  return EFF_OK;
+}
+
+int eff_sync(eff_ctx *ctx) {
+  if (!ctx) return EFF_E_INVALID;
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return EFF_OK;
+}
+
+int eff_set_option(eff_ctx *ctx, int option, int64_t value) {
+  if (!ctx) return EFF_E_INVALID;
+  switch (option) {
+    case EFF_OPT_GEMV_MAX_TOKENS:
+      if (value < 0 || value > 8) return fail(ctx, EFF_E_INVALID, "GEMV max tokens must be in 0..8, got %lld", (long long)value);
+      ctx->gemv_max_tokens = value;
+      return EFF_OK;
+    case EFF_OPT_GEMM_MIN_TOKENS:
+      if (value < 1) return fail(ctx, EFF_E_INVALID, "GEMM min tokens must be >= 1, got %lld", (long long)value);
+      ctx->gemm_min_tokens = value;
+      return EFF_OK;
+    default: return fail(ctx, EFF_E_INVALID, "unknown option %d", option);
+  }
+}
+
+int eff_get_stats(const eff_ctx *ctx, eff_stats *out) {
+  if (!ctx || !out) return EFF_E_INVALID;
+  *out = ctx->stats;
+  return EFF_OK;
+}
+
+int eff_buf_alloc(eff_ctx *ctx, size_t bytes, eff_buf **out) {
+  if (!ctx || !out) return EFF_E_INVALID;
+  *out = nullptr;
+  if (bytes == 0) return fail(ctx, EFF_E_INVALID, "buffer of 0 bytes");
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes + kSlack) != hipSuccess) return fail(ctx, EFF_E_NOMEM, "hipMalloc of %zu bytes failed", bytes + kSlack);
+  if (hipMemsetAsync(p, 0, bytes + kSlack, ctx->stream) != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess) {
+    (void)hipFree(p);
+    return fail(ctx, EFF_E_DEVICE, "clearing a new buffer failed");
+  }
+  eff_buf *b = new eff_buf();
+  b->ptr = p;
+  b->size = bytes;
+  b->owned = true;
+  *out = b;
+  return EFF_OK;
+}
+
+int eff_buf_wrap(eff_ctx *ctx, void *device_ptr, size_t bytes, eff_buf **out) {
+  if (!ctx || !out || !device_ptr || bytes == 0) return EFF_E_INVALID;
+  eff_buf *b = new eff_buf();
+  b->ptr = device_ptr;
+  b->size = bytes;
+  b->owned = false;
+  *out = b;
+  return EFF_OK;
+}
+
+int eff_buf_free(eff_ctx *ctx, eff_buf *buf) {
+  if (!ctx || !buf) return EFF_E_INVALID;
+  if (buf->owned) {
+    use_device(ctx);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(buf->ptr);
+  }
+  delete buf;
+  return EFF_OK;
+}
+
+size_t eff_buf_size(const eff_buf *buf) { return buf ? buf->size : 0; }
+void *eff_buf_device_ptr(const eff_buf *buf) { return buf ? buf->ptr : nullptr; }
+
+int eff_buf_write(eff_ctx *ctx, eff_buf *buf, size_t off, const void *src, size_t n) {
+  if (!ctx || !buf || (!src && n)) return EFF_E_INVALID;
+  if (off > buf->size || n > buf->size - off) return fail(ctx, EFF_E_BOUNDS, "write of %zu bytes at %zu past a %zu-byte buffer", n, off, buf->size);
+  if (!n) return EFF_OK;
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  // Synchronous with respect to `src`: the host memory may be reused on return.
+  EFF_HIP(ctx, hipMemcpyAsync((char *)buf->ptr + off, src, n, hipMemcpyHostToDevice, ctx->stream));
+  EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return EFF_OK;
+}
+
+int eff_buf_read(eff_ctx *ctx, eff_buf *buf, size_t off, void *dst, size_t n) {
+  if (!ctx || !buf || (!dst && n)) return EFF_E_INVALID;
+  if (off > buf->size || n > buf->size - off) return fail(ctx, EFF_E_BOUNDS, "read of %zu bytes at %zu past a %zu-byte buffer", n, off, buf->size);
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  if (n) EFF_HIP(ctx, hipMemcpyAsync(dst, (const char *)buf->ptr + off, n, hipMemcpyDeviceToHost, ctx->stream));
+  EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return EFF_OK;
+}
+
+int eff_buf_copy(eff_ctx *ctx, eff_buf *dst, size_t doff, eff_buf *src, size_t soff, size_t n) {
+  if (!ctx || !dst || !src) return EFF_E_INVALID;
+  if (doff > dst->size || n > dst->size - doff || soff > src->size || n > src->size - soff)
+    return fail(ctx, EFF_E_BOUNDS, "copy of %zu bytes out of bounds", n);
+  if (!n) return EFF_OK;
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  EFF_HIP(ctx, hipMemcpyAsync((char *)dst->ptr + doff, (const char *)src->ptr + soff, n, hipMemcpyDeviceToDevice, ctx->stream));
+  return EFF_OK;
+}
+
+int eff_buf_mark_r(eff_buf *buf, int type_r, uint32_t n) {
+  if (!buf) return EFF_E_INVALID;
+  if (type_r != EFF_TYPE_Q8_0R) return EFF_E_TYPE;
+  if (n == 0) return EFF_E_INVALID;
+  if (buf->size != eff_bytes_buffer_r(type_r, n)) return EFF_E_MARK;
+  buf->mark_type = type_r;
+  buf->mark_blocks = n;
+  return EFF_OK;
+}
+
+int eff_buf_blocks_r(const eff_buf *buf, uint32_t *n) {
+  if (!buf || !n) return EFF_E_INVALID;
+  if (buf->mark_type != EFF_TYPE_Q8_0R) return EFF_E_MARK;
+  *n = buf->mark_blocks;
+  return EFF_OK;
+}
+
+int eff_qgemv(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k, uint32_t tokens) {
+  if (!ctx) return EFF_E_INVALID;
+  if (tokens == 0 || (int64_t)tokens > ctx->gemv_max_tokens || tokens > 8) {
+    ++ctx->stats.not_applicable;
+    return EFF_NOT_APPLICABLE;
+  }
+  WeightView wv;
+  int rc = weight_view(ctx, type, w, x, y, rows, k, tokens, wv, "gemv");
+  if (rc) return rc;
+  if ((rc = use_device(ctx))) return rc;
+  rc = run_gemv(ctx, wv, (const float *)x->ptr, (float *)y->ptr, tokens);
+  if (!rc) ++ctx->stats.gemv;
+  return rc;
+}
+
+int eff_qgemm(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k, uint32_t tokens) {
+  if (!ctx) return EFF_E_INVALID;
+  if (tokens == 0 || (int64_t)tokens < ctx->gemm_min_tokens) {
+    ++ctx->stats.not_applicable;
+    return EFF_NOT_APPLICABLE;
+  }
+  WeightView wv;
+  int rc = weight_view(ctx, type, w, x, y, rows, k, tokens, wv, "gemm");
+  if (rc) return rc;
+  if ((rc = use_device(ctx))) return rc;
+  rc = run_gemm(ctx, wv, (const float *)x->ptr, (float *)y->ptr, tokens);
+  if (!rc) ++ctx->stats.gemm;
+  return rc;
+}
+
+int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k, uint32_t tokens) {
+  if (!ctx) return EFF_E_INVALID;
+  WeightView wv;
+  int rc = weight_view(ctx, type, w, x, y, rows, k, tokens, wv, "matmul");
+  if (rc) return rc;
+  if ((rc = use_device(ctx))) return rc;
+  const float *xp = (const float *)x->ptr;
+  float *yp = (float *)y->ptr;
+  if ((int64_t)tokens <= ctx->gemv_max_tokens && tokens <= 8) {
+    rc = run_gemv(ctx, wv, xp, yp, tokens);
+    if (!rc) ++ctx->stats.gemv;
+    return rc;
+  }
+  if ((int64_t)tokens >= ctx->gemm_min_tokens) {
+    rc = run_gemm(ctx, wv, xp, yp, tokens);
+    if (!rc) ++ctx->stats.gemm;
+    return rc;
+  }
+  // Between the two: the f32 GEMV over groups of up to 8 tokens. Y is
+  // token-major, so each group writes a contiguous slice.
+  for (uint32_t t0 = 0; t0 < tokens; t0 += 8) {
+    const uint32_t tn = tokens - t0 < 8 ? tokens - t0 : 8;
+    rc = run_gemv(ctx, wv, xp + (uint64_t)t0 * k, yp + (uint64_t)t0 * rows, tn);
+    if (rc) return rc;
+    ++ctx->stats.skinny;
+  }
+  return EFF_OK;
+}
+
+int eff_dequant(eff_ctx *ctx, int type, eff_buf *w, eff_buf *out, uint32_t n_blocks) {
+  if (!ctx) return EFF_E_INVALID;
+  if (!w || !out) return fail(ctx, EFF_E_INVALID, "dequant: null buffer");
+  if (!type_known(type)) return fail(ctx, EFF_E_TYPE, "dequant: unsupported quantization type %d", type);
+  if (n_blocks == 0) return EFF_OK;
+  Geometry g = geometry(type);
+  uint64_t scales_off = 0;
+  if (type == EFF_TYPE_Q8_0R) {
+    if (w->mark_type != EFF_TYPE_Q8_0R) return fail(ctx, EFF_E_MARK, "dequant Q8_0R: buffer without the repack mark");
+    if (n_blocks > w->mark_blocks) return fail(ctx, EFF_E_MARK, "dequant Q8_0R: %u blocks requested, tensor has %u", n_blocks, w->mark_blocks);
+    scales_off = (uint64_t)32 * w->mark_blocks;
+  } else if ((uint64_t)n_blocks * g.bytes > w->size) {
+    return fail(ctx, EFF_E_BOUNDS, "dequant: %u blocks need %llu bytes, buffer has %zu", n_blocks,
+                (unsigned long long)n_blocks * g.bytes, w->size);
+  }
+  if ((uint64_t)n_blocks * g.elems * 4 > out->size) return fail(ctx, EFF_E_BOUNDS, "dequant: output buffer too small");
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  hipError_t e = launch_dequant((const uint8_t *)w->ptr, type, scales_off, n_blocks, (float *)out->ptr, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "dequant launch");
+  ++ctx->stats.dequant;
+  return EFF_OK;
+}
+
+size_t eff_topk_out_bytes(void) { return sizeof(uint32_t) * (EFF_TOPK_HEADER + EFF_TOPK_P_MAX + 2 * EFF_TOPK_CAP); }
+
+int eff_topk(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint32_t m, const uint32_t *penal_ids,
+             uint32_t n_penal, uint32_t serial, eff_buf *out) {
+  if (!ctx) return EFF_E_INVALID;
+  if (!logits || !out) return fail(ctx, EFF_E_INVALID, "topk: null buffer");
+  if (n_penal && !penal_ids) return fail(ctx, EFF_E_INVALID, "topk: null penalised ids");
+  // Outside these limits the reference falls back to a full readback (ops.topk.js:104-105, topk.js:114-117).
+  if (vocab == 0 || vocab >= EFF_TOPK_N_MAX || m == 0 || m > EFF_TOPK_M_MAX || n_penal > EFF_TOPK_P_MAX) {
+    ++ctx->stats.not_applicable;
+    return EFF_NOT_APPLICABLE;
+  }
+  if (((uint64_t)base + vocab) * 4 > logits->size) return fail(ctx, EFF_E_BOUNDS, "topk: logits buffer too small");
+  if (out->size < eff_topk_out_bytes()) return fail(ctx, EFF_E_BOUNDS, "topk: output buffer needs %zu bytes", eff_topk_out_bytes());
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  size_t need = topk_scratch_bytes(vocab);
+  if (need > ctx->topk_scratch_bytes) {
+    if (ctx->topk_scratch) {
+      EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+      (void)hipFree(ctx->topk_scratch);
+      ctx->topk_scratch = nullptr;
+      ctx->topk_scratch_bytes = 0;
+    }
+    if (hipMalloc(&ctx->topk_scratch, need) != hipSuccess) return fail(ctx, EFF_E_NOMEM, "topk scratch of %zu bytes", need);
+    ctx->topk_scratch_bytes = need;
+  }
+  hipError_t e = launch_topk((const uint32_t *)logits->ptr, base, vocab, m, penal_ids, n_penal, serial,
+                             (uint32_t *)ctx->topk_scratch, (uint32_t *)out->ptr, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "topk launch");
+  ++ctx->stats.topk;
+  return EFF_OK;
+}
+
+}  // extern "C"

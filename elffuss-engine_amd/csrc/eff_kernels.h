@@ -1,0 +1,48 @@
+// Internal launch interface between the C ABI (eff_api.hip) and the kernels
+// (eff_kernels.hip). All launches are asynchronous on `stream`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace eff {
+
+// One quantized matrix W (rows x k) and its addressing.
+struct WeightView {
+  const uint8_t *w;       // device pointer to the tensor's first byte
+  int type;               // eff::Type
+  uint32_t rows, k, bpr;  // bpr = k / block_elems
+  uint64_t row_bytes;     // bpr * block_bytes (GGUF layouts)
+  uint64_t scales_off;    // Q8_0R: byte offset of the scale region (32 * N of the tensor)
+};
+
+// GEMV shape chosen by the host (see plan_gemv).
+struct GemvPlan {
+  int rows_per_wave;  // R
+  int ksplit;         // waves of a workgroup that share rows and split k (1, 2, 4)
+  uint32_t kc;        // k elements of x staged in LDS per pass
+  uint32_t grid;      // workgroups
+  size_t lds_bytes;   // dynamic LDS
+};
+
+GemvPlan plan_gemv(const WeightView &wv, uint32_t tokens);
+
+hipError_t launch_gemv(const WeightView &wv, const float *x, float *y, uint32_t tokens,
+                       const GemvPlan &p, hipStream_t stream);
+
+hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens,
+                       hipStream_t stream);
+
+hipError_t launch_dequant(const uint8_t *w, int type, uint64_t scales_off, uint32_t n_blocks,
+                          float *out, hipStream_t stream);
+
+// Top-k scratch: per chunk 2 u32 (count, flags) + 2 * kTopkChunkCap u32 (id, bits).
+constexpr uint32_t kTopkChunk = 4096;     // logits per chunk workgroup
+constexpr uint32_t kTopkChunkCap = 256;   // candidates kept per chunk (>= M max)
+size_t topk_scratch_bytes(uint32_t vocab);
+
+hipError_t launch_topk(const uint32_t *logits, uint32_t base, uint32_t vocab, uint32_t m,
+                       const uint32_t *penal_ids_dev, uint32_t n_penal, uint32_t serial,
+                       uint32_t *scratch, uint32_t *out, hipStream_t stream);
+
+}  // namespace eff

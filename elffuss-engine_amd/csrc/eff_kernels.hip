@@ -1,0 +1,960 @@
+// gfx950 kernels of the quantized matrix-product path.
+//
+// Work unit. Every kernel walks a row of W in units of 32 weights: one Q8_0
+// block, or one eighth of a 256-weight super-block. A unit is two runs of 16
+// weights ("halves" A and B) at k offsets (o0, o1) inside its block, each half
+// with one scale and one offset:
+//     sum_i w_i x_i = sA * sum_A u_i x_i + sB * sum_B u_i x_i - mA * sum_A x_i - mB * sum_B x_i
+// where u_i is a small unsigned integer taken from the block bytes. The unit
+// split follows the block layout so that the bytes of a unit are contiguous:
+//   Q8_0     one block; u = q + 128
+//   Q4_K     16 qs bytes: low nibbles = sub-block 2j, high nibbles = 2j+1
+//   Q6_K     16 ql bytes + the 16 qh bytes that complete them (two groups of 32)
+//   Q2_K     16 qs bytes at two of the four bit-shifts (two sub-blocks of 16)
+//   IQ2_XXS  one 32-weight group (4 grid entries, signs folded into u = ±g + 128)
+// The decoders follow the reference's DECODERS (kernels.wgsl.js:154-396); the
+// f32 dequantization (dequant_unit) reproduces their operation order exactly.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/elffuss_amd.h"
+#include "eff_formats.h"
+#include "eff_kernels.h"
+
+namespace eff {
+
+__constant__ uint64_t c_iq2xxs_grid[256] = {
+#include "iq2xxs_grid.inc"
+};
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Loads. Blocks start at even byte offsets; 4-byte words are read aligned and
+// re-assembled with v_alignbyte. A read may touch up to 4 bytes past the end
+// of a block (the reference's loader leaves that slack, model.js:248-254).
+__device__ __forceinline__ uint32_t ld32(const uint8_t *p) {
+  return __builtin_nontemporal_load((const uint32_t *)p);
+}
+
+__device__ __forceinline__ uint32_t ld_u16_a2(const uint8_t *p) {
+  uintptr_t a = (uintptr_t)p;
+  uint32_t w = __builtin_nontemporal_load((const uint32_t *)(a & ~(uintptr_t)3));
+  return (a & 2) ? (w >> 16) : (w & 0xFFFFu);
+}
+
+template <int N>
+__device__ __forceinline__ void ld_words_a2(const uint8_t *p, uint32_t *out) {
+  uintptr_t a = (uintptr_t)p;
+  const uint32_t *w = (const uint32_t *)(a & ~(uintptr_t)3);
+  uint32_t sh = (uint32_t)(a & 3);
+  uint32_t v[N + 1];
+#pragma unroll
+  for (int i = 0; i <= N; ++i) v[i] = __builtin_nontemporal_load(w + i);
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], sh);
+}
+
+__device__ __forceinline__ float h2f(uint32_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+  return (float)v;
+}
+
+__device__ __forceinline__ float ubyte(uint32_t w, int c) { return (float)((w >> (8 * c)) & 0xFFu); }
+
+// ---------------------------------------------------------------------------
+// Per-type raw unit data.
+template <int TYPE> struct Raw;
+
+template <> struct Raw<Q8_0> {
+  uint32_t s, v[8];
+};
+template <> struct Raw<Q8_0R> {
+  uint32_t v[8], s;
+};
+template <> struct Raw<Q4_K> {
+  uint32_t hdr[4], qs[4], sub;
+};
+template <> struct Raw<Q6_K> {
+  uint32_t ql[4], qh[4], sc, d, sub;
+};
+template <> struct Raw<Q2_K> {
+  uint32_t qs[4], sc, dd, sub;
+};
+template <> struct Raw<IQ2_XXS> {
+  uint32_t a0, a1, d;
+};
+
+template <int TYPE> constexpr uint32_t units_per_block() { return (TYPE == Q8_0 || TYPE == Q8_0R) ? 1u : 8u; }
+template <int TYPE> constexpr uint32_t block_elems() { return (TYPE == Q8_0 || TYPE == Q8_0R) ? 32u : 256u; }
+template <int TYPE> constexpr uint32_t block_bytes() {
+  return TYPE == Q8_0 ? 34u : TYPE == Q8_0R ? 34u : TYPE == Q4_K ? 144u : TYPE == Q6_K ? 210u
+       : TYPE == Q2_K ? 84u : 66u;
+}
+
+// k offsets of the two 16-weight halves of unit `sub` inside its block.
+template <int TYPE>
+__device__ __forceinline__ void unit_runs(uint32_t sub, uint32_t &o0, uint32_t &o1) {
+  if constexpr (TYPE == Q8_0 || TYPE == Q8_0R) {
+    o0 = 0; o1 = 16;
+  } else if constexpr (TYPE == Q4_K) {
+    // qs bytes 16*sub..: j = sub>>1, h = sub&1 -> weights 64j+16h (+32 for high nibbles)
+    o0 = 64u * (sub >> 1) + 16u * (sub & 1u); o1 = o0 + 32u;
+  } else if constexpr (TYPE == Q6_K) {
+    // ql bytes 16*sub..: n = sub>>2, gp = (sub>>1)&1, h = sub&1
+    o0 = 128u * (sub >> 2) + 32u * ((sub >> 1) & 1u) + 16u * (sub & 1u); o1 = o0 + 64u;
+  } else if constexpr (TYPE == Q2_K) {
+    // qs chunk c = sub>>1 (n = c>>1, half = c&1), shifts j = 2jp, 2jp+1 with jp = sub&1
+    uint32_t c = sub >> 1;
+    o0 = 128u * (c >> 1) + 64u * (sub & 1u) + 16u * (c & 1u); o1 = o0 + 32u;
+  } else {
+    o0 = 32u * sub; o1 = o0 + 16u;
+  }
+}
+
+// Issue the loads of unit `sub` of block `bi` (bp = its first byte in the GGUF layouts).
+template <int TYPE>
+__device__ __forceinline__ void load_raw(Raw<TYPE> &r, const uint8_t *base, uint64_t bi, uint32_t sub,
+                                         uint64_t scales_off) {
+  if constexpr (TYPE == Q8_0) {
+    const uint8_t *bp = base + bi * 34u;
+    r.s = ld_u16_a2(bp);
+    ld_words_a2<8>(bp + 2, r.v);
+  } else if constexpr (TYPE == Q8_0R) {
+    const u32x4 *q = (const u32x4 *)(base + bi * 32u);
+    u32x4 a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
+    r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
+    r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
+    r.s = ld_u16_a2(base + scales_off + bi * 2u);
+  } else if constexpr (TYPE == Q4_K) {
+    const uint8_t *bp = base + bi * 144u;
+    u32x4 h = __builtin_nontemporal_load((const u32x4 *)bp);
+    u32x4 q = __builtin_nontemporal_load((const u32x4 *)(bp + 16u + 16u * sub));
+    r.hdr[0] = h.x; r.hdr[1] = h.y; r.hdr[2] = h.z; r.hdr[3] = h.w;
+    r.qs[0] = q.x; r.qs[1] = q.y; r.qs[2] = q.z; r.qs[3] = q.w;
+    r.sub = sub;
+  } else if constexpr (TYPE == Q6_K) {
+    const uint8_t *bp = base + bi * 210u;
+    uint32_t n = sub >> 2, gp = (sub >> 1) & 1u, h = sub & 1u;
+    ld_words_a2<4>(bp + 16u * sub, r.ql);
+    ld_words_a2<4>(bp + 128u + 32u * n + 16u * h, r.qh);
+    // scales of groups gp and gp+2 at bytes 192 + 8n + 2g + h
+    const uint8_t *sp = bp + 192u + 8u * n + 2u * gp + h;
+    r.sc = (uint32_t)sp[0] | ((uint32_t)sp[4] << 8);
+    r.d = ld_u16_a2(bp + 208u);
+    r.sub = sub;
+  } else if constexpr (TYPE == Q2_K) {
+    const uint8_t *bp = base + bi * 84u;
+    uint32_t c = sub >> 1, jp = sub & 1u;
+    const uint8_t *qp = bp + 16u + 16u * c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.qs[i] = ld32(qp + 4 * i);
+    r.sc = ld32(bp + 8u * (c >> 1) + 4u * jp);
+    r.dd = ld32(bp + 80u);
+    r.sub = sub;
+  } else {
+    const uint8_t *bp = base + bi * 66u;
+    uint32_t a[2];
+    ld_words_a2<2>(bp + 2u + 8u * sub, a);
+    r.a0 = a[0]; r.a1 = a[1];
+    r.d = ld_u16_a2(bp);
+  }
+}
+
+// 6-bit (scale, min) pair `idx` of a Q4_K block (SCALE_MIN_K4, kernels.wgsl.js:94-104).
+__device__ __forceinline__ void q4k_scale_min(const uint32_t *hdr, uint32_t idx, uint32_t &sc, uint32_t &m) {
+  // scale bytes s[0..11] are bytes 4..15 of the block = hdr[1..3]
+  auto s = [&](uint32_t i) -> uint32_t { return (hdr[1 + (i >> 2)] >> (8u * (i & 3u))) & 0xFFu; };
+  if (idx < 4) {
+    sc = s(idx) & 63u;
+    m = s(idx + 4) & 63u;
+  } else {
+    sc = (s(idx + 4) & 0xFu) | ((s(idx - 4) >> 6) << 4);
+    m = (s(idx + 4) >> 4) | ((s(idx) >> 6) << 4);
+  }
+}
+
+// Unsigned values u of quad q (weights 4q..4q+3 of half A for q < 4, of half B
+// for q >= 4), one per byte. `grid` is the IQ2_XXS table in LDS (u32 pairs).
+template <int TYPE>
+__device__ __forceinline__ uint32_t quad(const Raw<TYPE> &r, int q, const uint32_t *grid) {
+  if constexpr (TYPE == Q8_0 || TYPE == Q8_0R) {
+    return r.v[q] ^ 0x80808080u;  // signed byte + 128
+  } else if constexpr (TYPE == Q4_K) {
+    return q < 4 ? (r.qs[q] & 0x0F0F0F0Fu) : ((r.qs[q - 4] >> 4) & 0x0F0F0F0Fu);
+  } else if constexpr (TYPE == Q6_K) {
+    uint32_t gp = (r.sub >> 1) & 1u;
+    if (q < 4) return (r.ql[q] & 0x0F0F0F0Fu) | (((r.qh[q] >> (2u * gp)) & 0x03030303u) << 4);
+    return ((r.ql[q - 4] >> 4) & 0x0F0F0F0Fu) | (((r.qh[q - 4] >> (2u * gp + 4u)) & 0x03030303u) << 4);
+  } else if constexpr (TYPE == Q2_K) {
+    uint32_t jp = r.sub & 1u;
+    return q < 4 ? ((r.qs[q] >> (4u * jp)) & 0x03030303u) : ((r.qs[q - 4] >> (4u * jp + 2u)) & 0x03030303u);
+  } else {
+    // entry l = q>>1 covers weights 8l..8l+7; this quad is its half (q&1)
+    uint32_t l = (uint32_t)q >> 1;
+    uint32_t gi = (r.a0 >> (8u * l)) & 0xFFu;
+    uint32_t bits = (r.a1 >> (7u * l)) & 127u;
+    uint32_t signs = bits | ((__builtin_popcount(bits) & 1u) << 7);  // even parity (kernels.wgsl.js:381-384)
+    uint32_t g = grid[2u * gi + (q & 1)];
+    uint32_t s4 = (signs >> (4u * (q & 1))) & 0xFu;
+    uint32_t m = ((s4 * 0x00204081u) & 0x01010101u) * 0xFFu;  // 0xFF in each negative byte
+    // +g -> g + 128 ; -g -> 128 - g, per byte, without carries between bytes
+    return (g ^ (m ^ 0x80808080u)) + (m & 0x01010101u);
+  }
+}
+
+// Scale and offset of the two halves: value_i = s * u_i - m.
+template <int TYPE>
+__device__ __forceinline__ void unit_scales(const Raw<TYPE> &r, float &sA, float &sB, float &mA, float &mB) {
+  if constexpr (TYPE == Q8_0 || TYPE == Q8_0R) {
+    float d = h2f(r.s);
+    sA = sB = d;
+    mA = mB = 128.f * d;
+  } else if constexpr (TYPE == Q4_K) {
+    float d = h2f(r.hdr[0] & 0xFFFFu), dmin = h2f(r.hdr[0] >> 16);
+    uint32_t j = r.sub >> 1, sc, m;
+    q4k_scale_min(r.hdr, 2u * j, sc, m);
+    sA = d * (float)sc; mA = dmin * (float)m;
+    q4k_scale_min(r.hdr, 2u * j + 1u, sc, m);
+    sB = d * (float)sc; mB = dmin * (float)m;
+  } else if constexpr (TYPE == Q6_K) {
+    float d = h2f(r.d);
+    sA = d * (float)(int8_t)(r.sc & 0xFFu);
+    sB = d * (float)(int8_t)(r.sc >> 8);
+    mA = 32.f * sA; mB = 32.f * sB;
+  } else if constexpr (TYPE == Q2_K) {
+    float d = h2f(r.dd & 0xFFFFu), dmin = h2f(r.dd >> 16);
+    uint32_t half = (r.sub >> 1) & 1u;
+    uint32_t scA = (r.sc >> (8u * half)) & 0xFFu, scB = (r.sc >> (8u * (half + 2u))) & 0xFFu;
+    sA = d * (float)(scA & 0xFu); mA = dmin * (float)(scA >> 4);
+    sB = d * (float)(scB & 0xFu); mB = dmin * (float)(scB >> 4);
+  } else {
+    float d = h2f(r.d);
+    float db = d * (0.5f + (float)(r.a1 >> 28)) * 0.25f;
+    sA = sB = db;
+    mA = mB = 128.f * db;
+  }
+}
+
+// Bit-exact f32 dequantization of one unit: out[0..15] = half A, out[16..31] =
+// half B, with the reference's operation order and no FMA contraction.
+template <int TYPE>
+__device__ __forceinline__ void dequant_unit(const Raw<TYPE> &r, const uint32_t *grid, float *out) {
+#pragma clang fp contract(off)
+  if constexpr (TYPE == Q8_0 || TYPE == Q8_0R) {
+    // f32(q) * d (kernels.wgsl.js:162-169, 857-865)
+    float d = h2f(r.s);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) out[i] = (float)(int8_t)((r.v[i >> 2] >> (8 * (i & 3))) & 0xFFu) * d;
+  } else if constexpr (TYPE == Q4_K) {
+    // d1 * q - m1 with d1 = d*sc, m1 = dmin*m (kernels.wgsl.js:233-249)
+    float d = h2f(r.hdr[0] & 0xFFFFu), dmin = h2f(r.hdr[0] >> 16);
+    uint32_t j = r.sub >> 1, sc, m;
+    q4k_scale_min(r.hdr, 2u * j, sc, m);
+    float d1 = d * (float)sc, m1 = dmin * (float)m;
+    q4k_scale_min(r.hdr, 2u * j + 1u, sc, m);
+    float d2 = d * (float)sc, m2 = dmin * (float)m;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      uint32_t b = (r.qs[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+      out[i] = d1 * (float)(b & 0xFu) - m1;
+      out[16 + i] = d2 * (float)(b >> 4) - m2;
+    }
+  } else if constexpr (TYPE == Q6_K) {
+    // (d * sc) * (q - 32) (kernels.wgsl.js:300-329)
+    float d = h2f(r.d);
+    float dA = d * (float)(int8_t)(r.sc & 0xFFu), dB = d * (float)(int8_t)(r.sc >> 8);
+    uint32_t gp = (r.sub >> 1) & 1u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      uint32_t l = (r.ql[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+      uint32_t h = (r.qh[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+      int qa = (int)((l & 0xFu) | (((h >> (2u * gp)) & 3u) << 4)) - 32;
+      int qb = (int)((l >> 4) | (((h >> (2u * gp + 4u)) & 3u) << 4)) - 32;
+      out[i] = dA * (float)qa;
+      out[16 + i] = dB * (float)qb;
+    }
+  } else if constexpr (TYPE == Q2_K) {
+    // dl * q - ml with dl = d*(sc&15), ml = dmin*(sc>>4) (kernels.wgsl.js:202-221)
+    float d = h2f(r.dd & 0xFFFFu), dmin = h2f(r.dd >> 16);
+    uint32_t half = (r.sub >> 1) & 1u, jp = r.sub & 1u;
+    uint32_t scA = (r.sc >> (8u * half)) & 0xFFu, scB = (r.sc >> (8u * (half + 2u))) & 0xFFu;
+    float dlA = d * (float)(scA & 0xFu), mlA = dmin * (float)(scA >> 4);
+    float dlB = d * (float)(scB & 0xFu), mlB = dmin * (float)(scB >> 4);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      uint32_t b = (r.qs[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+      out[i] = dlA * (float)((b >> (4u * jp)) & 3u) - mlA;
+      out[16 + i] = dlB * (float)((b >> (4u * jp + 2u)) & 3u) - mlB;
+    }
+  } else {
+    // db * g * sign with db = d * (0.5 + ls) * 0.25 (kernels.wgsl.js:374-395)
+    float d = h2f(r.d);
+    float db = d * (0.5f + (float)(r.a1 >> 28)) * 0.25f;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      uint32_t gi = (r.a0 >> (8u * l)) & 0xFFu;
+      uint32_t bits = (r.a1 >> (7u * l)) & 127u;
+      uint32_t signs = bits | ((__builtin_popcount(bits) & 1u) << 7);
+      uint32_t g0 = grid[2u * gi], g1 = grid[2u * gi + 1u];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        uint32_t gw = j < 4 ? g0 : g1;
+        float gv = (float)((gw >> (8 * (j & 3))) & 0xFFu);
+        float sg = (signs >> j) & 1u ? -1.0f : 1.0f;
+        out[8 * l + j] = db * gv * sg;
+      }
+    }
+  }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void stage_grid(uint32_t *grid) {
+  if constexpr (TYPE == IQ2_XXS) {
+    for (uint32_t i = threadIdx.x; i < 256; i += blockDim.x) {
+      uint64_t g = c_iq2xxs_grid[i];
+      grid[2 * i] = (uint32_t)g;
+      grid[2 * i + 1] = (uint32_t)(g >> 32);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dequantization (test hook): one thread per unit.
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ w, uint64_t scales_off,
+                                                 uint32_t n_blocks, float *__restrict__ out) {
+  __shared__ uint32_t grid[TYPE == IQ2_XXS ? 512 : 1];
+  stage_grid<TYPE>(grid);
+  if constexpr (TYPE == IQ2_XXS) __syncthreads();
+  uint64_t gu = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gu >= (uint64_t)n_blocks * units_per_block<TYPE>()) return;
+  uint64_t bi = gu / units_per_block<TYPE>();
+  uint32_t sub = (uint32_t)(gu % units_per_block<TYPE>());
+  Raw<TYPE> r;
+  load_raw<TYPE>(r, w, bi, sub, scales_off);
+  float v[32];
+  dequant_unit<TYPE>(r, grid, v);
+  uint32_t o0, o1;
+  unit_runs<TYPE>(sub, o0, o1);
+  float *dst = out + bi * block_elems<TYPE>();
+#pragma unroll
+  for (int i = 0; i < 16; i += 4) {
+    *(float4 *)(dst + o0 + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+    *(float4 *)(dst + o1 + i) = make_float4(v[16 + i], v[17 + i], v[18 + i], v[19 + i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV: Y[t][row] = sum_k W[row][k] X[t][k], 1..8 tokens, f32 accumulation.
+//
+// A workgroup is 4 waves. `ksplit` waves share R rows and split the units of
+// k between them; the 4/ksplit groups take consecutive row groups. x is staged
+// in LDS (f32, a 4-float pad every 32 floats so that lanes reading
+// consecutive units hit different banks) in passes of `kc` elements.
+__device__ __forceinline__ uint32_t xpad(uint32_t k) { return k + (k >> 5) * 4u; }
+
+template <int TYPE, int T, int R>
+__global__ __launch_bounds__(256) void k_gemv(WeightView wv, const float *__restrict__ x,
+                                              float *__restrict__ y, uint32_t kc, int ksplit) {
+  extern __shared__ float smem[];
+  const uint32_t kcp = xpad(kc);
+  float *xs = smem;
+  float *red = smem + T * kcp;
+  uint32_t *grid = (uint32_t *)(red + 4 * R * T);
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int groups = 4 / ksplit;
+  const int grp = wave / ksplit, ks = wave % ksplit;
+  const uint32_t row0 = (blockIdx.x * groups + grp) * R;
+  const uint32_t rows = wv.rows, k = wv.k;
+
+  stage_grid<TYPE>(grid);
+
+  uint32_t rowi[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) rowi[r] = min(row0 + (uint32_t)r, rows - 1u);
+
+  float acc[R][T];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[r][t] = 0.f;
+
+  constexpr uint32_t upb = units_per_block<TYPE>();
+  constexpr uint32_t E = block_elems<TYPE>();
+
+  for (uint32_t k0 = 0; k0 < k; k0 += kc) {
+    const uint32_t klen = min(kc, k - k0);
+    __syncthreads();
+    for (uint32_t i = (uint32_t)tid * 4u; i < klen * T; i += 1024u) {
+      uint32_t t = i / klen, kk = i - t * klen;
+      float4 v = *(const float4 *)(x + (uint64_t)t * k + k0 + kk);
+      *(float4 *)(xs + t * kcp + xpad(kk)) = v;
+    }
+    __syncthreads();
+    const uint32_t units = klen / 32u;
+    const uint32_t ub = units * (uint32_t)ks / (uint32_t)ksplit;
+    const uint32_t ue = units * (uint32_t)(ks + 1) / (uint32_t)ksplit;
+    for (uint32_t u = ub + (uint32_t)lane; u < ue; u += 64u) {
+      const uint32_t gu = k0 / 32u + u;
+      const uint32_t b = gu / upb, sub = gu % upb;
+      uint32_t o0, o1;
+      unit_runs<TYPE>(sub, o0, o1);
+      const uint32_t kl0 = b * E + o0 - k0, kl1 = b * E + o1 - k0;
+
+      Raw<TYPE> raw[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        load_raw<TYPE>(raw[r], wv.w, (uint64_t)rowi[r] * wv.bpr + b, sub, wv.scales_off);
+
+      float ra[R][T], rb[R][T], sxa[T], sxb[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        sxa[t] = sxb[t] = 0.f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) ra[r][t] = rb[r][t] = 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint32_t kl = q < 4 ? kl0 + 4u * q : kl1 + 4u * (q - 4);
+        float4 xv[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          xv[t] = *(const float4 *)(xs + t * kcp + xpad(kl));
+          float s = (xv[t].x + xv[t].y) + (xv[t].z + xv[t].w);
+          if (q < 4) sxa[t] += s; else sxb[t] += s;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint32_t qb = quad<TYPE>(raw[r], q, grid);
+          const float f0 = ubyte(qb, 0), f1 = ubyte(qb, 1), f2 = ubyte(qb, 2), f3 = ubyte(qb, 3);
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            float p = f0 * xv[t].x + f1 * xv[t].y + f2 * xv[t].z + f3 * xv[t].w;
+            if (q < 4) ra[r][t] += p; else rb[r][t] += p;
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float sA, sB, mA, mB;
+        unit_scales<TYPE>(raw[r], sA, sB, mA, mB);
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          acc[r][t] += (sA * ra[r][t] + sB * rb[r][t]) - (mA * sxa[t] + mB * sxb[t]);
+      }
+    }
+  }
+
+  // Reduce over the 64 lanes, then over the ksplit waves of the group.
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      float v = acc[r][t];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+      acc[r][t] = v;
+    }
+  if (ksplit == 1) {
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (row0 + r < rows)
+#pragma unroll
+          for (int t = 0; t < T; ++t) y[(uint64_t)t * rows + row0 + r] = acc[r][t];
+    }
+    return;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int t = 0; t < T; ++t) red[(wave * R + r) * T + t] = acc[r][t];
+  }
+  __syncthreads();
+  if (tid < groups * R * T) {
+    const int g = tid / (R * T), rt = tid % (R * T), r = rt / T, t = rt % T;
+    float v = 0.f;
+    for (int s = 0; s < ksplit; ++s) v += red[((g * ksplit + s) * R + r) * T + t];
+    const uint32_t row = (blockIdx.x * groups + g) * R + r;
+    if (row < rows) y[(uint64_t)t * rows + row] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GEMM: Y[t][row] = sum_k fp16(W[row][k]) fp16(X[t][k]), fp32 accumulation.
+// Workgroup tile 128 rows x 128 tokens, k steps of 256; 4 waves of 64x64, each
+// 2x2 MFMA 32x32x16 f16. The weight tile is dequantized (bit-exact f32, then
+// rounded to fp16) into LDS; x is rounded to fp16 into LDS.
+constexpr int GT = 128;         // tile rows / tokens
+constexpr int GK = 256;         // k step
+constexpr int GKP = GK + 8;     // padded LDS row (halves)
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_gemm(WeightView wv, const float *__restrict__ x,
+                                              float *__restrict__ y, uint32_t tokens) {
+  __shared__ _Float16 xs[GT * GKP];
+  __shared__ _Float16 ws[GT * GKP];
+  __shared__ uint32_t grid[TYPE == IQ2_XXS ? 512 : 1];
+  stage_grid<TYPE>(grid);
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint32_t n0 = blockIdx.x * GT, t0 = blockIdx.y * GT;
+  const uint32_t rows = wv.rows, k = wv.k;
+  const int wm = wave & 1, wn = wave >> 1;
+  constexpr uint32_t upb = units_per_block<TYPE>();
+  constexpr uint32_t E = block_elems<TYPE>();
+
+  float16v acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  for (uint32_t kb = 0; kb < k; kb += GK) {
+    const uint32_t klen = min((uint32_t)GK, k - kb);
+    __syncthreads();
+    // x tile -> fp16 (zero outside [tokens) x [k))
+    for (int i = tid; i < GT * (GK / 4); i += 256) {
+      const int t = i / (GK / 4), c = i % (GK / 4);
+      const uint32_t tok = t0 + t, kk = 4u * c;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (tok < tokens && kk < klen) v = *(const float4 *)(x + (uint64_t)tok * k + kb + kk);
+      half4 h4 = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+      *(half4 *)(xs + t * GKP + kk) = h4;
+    }
+    // weight tile: 128 rows x (256/32) units
+    const uint32_t units = klen / 32u;
+    for (int i = tid; i < GT * 8; i += 256) {
+      const int r = i / 8;
+      const uint32_t u = (uint32_t)(i % 8);
+      _Float16 *d = ws + r * GKP;
+      if (u >= units) {
+        const half8 z = {};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *(half8 *)(d + 32 * u + 8 * j) = z;
+        continue;
+      }
+      const uint32_t row = min(n0 + (uint32_t)r, rows - 1u);
+      const uint32_t gu = kb / 32u + u;
+      const uint32_t b = gu / upb, sub = gu % upb;
+      Raw<TYPE> raw;
+      load_raw<TYPE>(raw, wv.w, (uint64_t)row * wv.bpr + b, sub, wv.scales_off);
+      float v[32];
+      dequant_unit<TYPE>(raw, grid, v);
+      uint32_t o0, o1;
+      unit_runs<TYPE>(sub, o0, o1);
+      const uint32_t c0 = b * E + o0 - kb, c1 = b * E + o1 - kb;
+#pragma unroll
+      for (int j = 0; j < 16; j += 8) {
+        half8 ha, hb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ha[e] = (_Float16)v[j + e];
+          hb[e] = (_Float16)v[16 + j + e];
+        }
+        *(half8 *)(d + c0 + j) = ha;
+        *(half8 *)(d + c1 + j) = hb;
+      }
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int kk = 0; kk < GK; kk += 16) {
+      half8 a[2], bfr[2];
+      const int kq = kk + 8 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        a[i] = *(const half8 *)(xs + (64 * wm + 32 * i + (lane & 31)) * GKP + kq);
+        bfr[i] = *(const half8 *)(ws + (64 * wn + 32 * i + (lane & 31)) * GKP + kq);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // D[tok][row]: lane holds column (row) lane%32 and rows (tokens)
+  // 8*(v/4) + 4*(lane/32) + v%4 of each 32x32 tile.
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t row = n0 + 64 * wn + 32 * j + (lane & 31);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const uint32_t tok = t0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (row < rows && tok < tokens) y[(uint64_t)tok * rows + row] = acc[i][j][v];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Top-k. Order key of an f32 bit pattern: -0 counts as +0, positives get the
+// sign bit set, negatives are inverted, so u32 order = f32 order
+// (kernels.topk.wgsl.js:75-82). Elements are compared by the 64-bit composite
+// (key << 32 | ~index): larger composite = larger value, ties to lower index.
+__device__ __forceinline__ uint32_t order_key(uint32_t bits) {
+  uint32_t b = bits == 0x80000000u ? 0u : bits;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ bool is_nan_bits(uint32_t bits) { return (bits & 0x7FFFFFFFu) > 0x7F800000u; }
+
+struct TopkPenal {
+  uint32_t ids[128];
+};
+
+// Radix select, 8-bit digits from the top: after it, the `need` largest
+// composites among the candidates are exactly those with (c & mask) >= prefix.
+// Every thread calls it with its own candidates (vals[0..n), valid flags).
+template <int N>
+__device__ void radix_select(const uint64_t *vals, const bool *valid, uint32_t need, uint32_t *hist,
+                             uint32_t *scan, uint64_t &prefix_out, uint64_t &mask_out, uint32_t *shared_state) {
+  const int tid = threadIdx.x;
+  uint64_t prefix = 0, mask = 0;
+  // shared_state: [0] need, [1] digit, [2] done
+  if (tid == 0) { shared_state[0] = need; shared_state[2] = need == 0u; }
+  __syncthreads();
+  for (int round = 0; round < 8; ++round) {
+    if (shared_state[2]) break;
+    const int shift = 56 - 8 * round;
+    hist[tid] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < N; ++e)
+      if (valid[e] && (vals[e] & mask) == prefix) atomicAdd(&hist[(uint32_t)(vals[e] >> shift) & 255u], 1u);
+    __syncthreads();
+    // suffix sums: scan[d] = sum of hist[d..255]
+    const uint32_t h = hist[tid];
+    uint32_t v = h;
+    // inclusive suffix scan within the wave (lanes in reverse digit order)
+    const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      uint32_t o = __shfl_down(v, off, 64);
+      if (lane + off < 64) v += o;
+    }
+    if (lane == 0) scan[256 + wave] = v;  // wave total
+    __syncthreads();
+    uint32_t above = 0;
+    for (int w = wave + 1; w < 4; ++w) above += scan[256 + w];
+    v += above;            // count of candidates with digit >= tid
+    const uint32_t nd = shared_state[0];
+    const uint32_t gt = v - h;  // count with digit > tid
+    __syncthreads();
+    if (gt < nd && v >= nd) {
+      shared_state[1] = (uint32_t)tid;
+      shared_state[0] = nd - gt;
+      shared_state[2] = (h == nd - gt) ? 1u : 0u;
+    }
+    __syncthreads();
+    prefix |= (uint64_t)shared_state[1] << shift;
+    mask |= (uint64_t)255u << shift;
+  }
+  prefix_out = prefix;
+  mask_out = mask;
+}
+
+constexpr int TK_E = kTopkChunk / 256;  // logits per thread
+
+__global__ __launch_bounds__(256) void k_topk_chunks(const uint32_t *__restrict__ logits, uint32_t base,
+                                                     uint32_t vocab, uint32_t m, uint32_t *__restrict__ scratch) {
+  __shared__ uint32_t hist[256], scan[260], st[4], flag, nout;
+  const int tid = threadIdx.x;
+  const uint32_t g = blockIdx.x, ini = g * kTopkChunk;
+  if (tid == 0) { flag = 0; nout = 0; }
+  uint64_t c[TK_E];
+  bool valid[TK_E];
+  uint32_t bits[TK_E];
+  bool nan = false;
+  uint32_t nvalid = 0;
+#pragma unroll
+  for (int e = 0; e < TK_E; ++e) {
+    const uint32_t j = ini + (uint32_t)e * 256u + (uint32_t)tid;
+    valid[e] = j < vocab;
+    bits[e] = valid[e] ? logits[base + j] : 0u;
+    c[e] = ((uint64_t)order_key(bits[e]) << 32) | (uint64_t)(~j);
+    if (valid[e] && is_nan_bits(bits[e])) nan = true;
+  }
+  nvalid = vocab > ini ? min(kTopkChunk, vocab - ini) : 0u;
+  __syncthreads();
+  if (nan) atomicOr(&flag, 2u);
+  uint64_t prefix, mask;
+  radix_select<TK_E>(c, valid, min(m, nvalid), hist, scan, prefix, mask, st);
+  uint32_t *hdr = scratch + 2u * g;
+  uint32_t *pairs = scratch + 2u * gridDim.x + (uint64_t)g * 2u * kTopkChunkCap;
+  const uint32_t need = min(m, nvalid);
+#pragma unroll
+  for (int e = 0; e < TK_E; ++e) {
+    if (need && valid[e] && (c[e] & mask) >= prefix) {
+      const uint32_t s = atomicAdd(&nout, 1u);
+      if (s < kTopkChunkCap) {
+        pairs[2 * s] = ini + (uint32_t)e * 256u + (uint32_t)tid;
+        pairs[2 * s + 1] = bits[e];
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    hdr[0] = min(nout, kTopkChunkCap);
+    hdr[1] = flag | (nout > kTopkChunkCap ? 1u : 0u);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_topk_final(const uint32_t *__restrict__ logits, uint32_t base,
+                                                    uint32_t vocab, uint32_t m, TopkPenal penal, uint32_t n_penal,
+                                                    uint32_t serial, uint32_t chunks,
+                                                    const uint32_t *__restrict__ scratch, uint32_t *__restrict__ out) {
+  __shared__ uint32_t hist[256], scan[260], st[4], flags, nsel;
+  __shared__ uint64_t sel_c[EFF_TOPK_CAP];
+  __shared__ uint32_t sel_b[EFF_TOPK_CAP];
+  const int tid = threadIdx.x;
+  if (tid == 0) { flags = 0; nsel = 0; }
+  __syncthreads();
+  for (uint32_t g = tid; g < chunks; g += 256) {
+    const uint32_t f = scratch[2 * g + 1];
+    if (f) atomicOr(&flags, f);
+  }
+  // penalised ids: their raw logits (the penalty itself is applied by the sampler)
+  if ((uint32_t)tid < n_penal && tid < EFF_TOPK_P_MAX) {
+    const uint32_t id = penal.ids[tid];
+    out[EFF_TOPK_HEADER + tid] = id < vocab ? logits[base + id] : 0u;
+  } else if (tid < EFF_TOPK_P_MAX) {
+    out[EFF_TOPK_HEADER + tid] = 0u;
+  }
+  const uint32_t *pairs = scratch + 2u * chunks;
+  uint64_t prefix = 0, mask = 0;
+  uint32_t total = 0;
+  for (uint32_t g = 0; g < chunks; ++g) total += scratch[2 * g];
+  const uint32_t need = min(m, total);
+  // Candidates are visited in passes of 256 x 4 slots; the select needs them
+  // all at once, so they are gathered per pass into registers when they fit
+  // (chunks * cap <= 4096 slots), else streamed over several selects.
+  const uint32_t slots = chunks * kTopkChunkCap;
+  if (slots <= 4096u) {
+    uint64_t c[16];
+    bool valid[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t sidx = (uint32_t)e * 256u + (uint32_t)tid;
+      const uint32_t g = sidx / kTopkChunkCap, s = sidx % kTopkChunkCap;
+      valid[e] = sidx < slots && s < scratch[2 * g];
+      uint32_t id = 0, b = 0;
+      if (valid[e]) { id = pairs[2 * (uint64_t)sidx]; b = pairs[2 * (uint64_t)sidx + 1]; }
+      c[e] = ((uint64_t)order_key(b) << 32) | (uint64_t)(~id);
+    }
+    radix_select<16>(c, valid, need, hist, scan, prefix, mask, st);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      if (need && valid[e] && (c[e] & mask) >= prefix) {
+        const uint32_t q = atomicAdd(&nsel, 1u);
+        if (q < EFF_TOPK_CAP) {
+          sel_c[q] = c[e];
+          sel_b[q] = pairs[2 * (uint64_t)((uint32_t)e * 256u + (uint32_t)tid) + 1];
+        }
+      }
+    }
+  } else {
+    // Large vocabularies: stream the candidate slots; each round re-reads them.
+    uint64_t pre = 0, msk = 0;
+    if (tid == 0) { st[0] = need; st[2] = need == 0u; }
+    __syncthreads();
+    for (int round = 0; round < 8; ++round) {
+      if (st[2]) break;
+      const int shift = 56 - 8 * round;
+      hist[tid] = 0;
+      __syncthreads();
+      for (uint32_t sidx = tid; sidx < slots; sidx += 256) {
+        const uint32_t g = sidx / kTopkChunkCap, s = sidx % kTopkChunkCap;
+        if (s >= scratch[2 * g]) continue;
+        const uint64_t cc = ((uint64_t)order_key(pairs[2 * (uint64_t)sidx + 1]) << 32) | (uint64_t)(~pairs[2 * (uint64_t)sidx]);
+        if ((cc & msk) == pre) atomicAdd(&hist[(uint32_t)(cc >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        uint32_t nd = st[0], acc = 0;
+        for (int d = 255; d >= 0; --d) {
+          if (acc + hist[d] >= nd) {
+            st[1] = (uint32_t)d;
+            st[0] = nd - acc;
+            st[2] = hist[d] == nd - acc;
+            break;
+          }
+          acc += hist[d];
+        }
+      }
+      __syncthreads();
+      pre |= (uint64_t)st[1] << shift;
+      msk |= (uint64_t)255u << shift;
+    }
+    for (uint32_t sidx = tid; sidx < slots; sidx += 256) {
+      const uint32_t g = sidx / kTopkChunkCap, s = sidx % kTopkChunkCap;
+      if (!need || s >= scratch[2 * g]) continue;
+      const uint32_t b = pairs[2 * (uint64_t)sidx + 1];
+      const uint64_t cc = ((uint64_t)order_key(b) << 32) | (uint64_t)(~pairs[2 * (uint64_t)sidx]);
+      if ((cc & msk) >= pre) {
+        const uint32_t q = atomicAdd(&nsel, 1u);
+        if (q < EFF_TOPK_CAP) { sel_c[q] = cc; sel_b[q] = b; }
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t n = min(nsel, (uint32_t)EFF_TOPK_CAP);
+  uint32_t *outp = out + EFF_TOPK_HEADER + EFF_TOPK_P_MAX;
+  // rank = number of selected composites larger than this one (all distinct)
+  for (uint32_t i = tid; i < EFF_TOPK_CAP; i += 256) {
+    if (i < n) {
+      const uint64_t ci = sel_c[i];
+      uint32_t rank = 0;
+      for (uint32_t j = 0; j < n; ++j) rank += sel_c[j] > ci ? 1u : 0u;
+      outp[2 * rank] = ~(uint32_t)ci;
+      outp[2 * rank + 1] = sel_b[i];
+    } else {
+      outp[2 * i] = 0u;
+      outp[2 * i + 1] = 0u;
+    }
+  }
+  if (tid == 0) {
+    out[0] = n;
+    out[1] = flags | (nsel > EFF_TOPK_CAP ? 4u : 0u);
+    out[2] = n_penal;
+    out[3] = chunks;
+    out[4] = serial;
+    out[5] = out[6] = out[7] = 0u;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launchers.
+
+GemvPlan plan_gemv(const WeightView &wv, uint32_t tokens) {
+  GemvPlan p{};
+  p.rows_per_wave = tokens <= 2 ? 2 : 1;
+  // x budget in LDS: 48 KiB including the pad of 4 floats every 32
+  uint32_t kc = (uint32_t)(48u * 1024u / (4u * tokens) * 32u / 36u);
+  kc = kc / 256u * 256u;
+  if (kc == 0) kc = 256;
+  p.kc = wv.k <= kc ? wv.k : kc;
+  const uint32_t units = p.kc / 32u;
+  int ks = 1;
+  auto grid_for = [&](int s) {
+    uint32_t per = (uint32_t)p.rows_per_wave * (uint32_t)(4 / s);
+    return (wv.rows + per - 1) / per;
+  };
+  while (ks < 4 && grid_for(ks) < 1024u && units / (uint32_t)(2 * ks) >= 64u) ks *= 2;
+  p.ksplit = ks;
+  p.grid = grid_for(ks);
+  p.lds_bytes = sizeof(float) * ((size_t)tokens * (p.kc + p.kc / 8u) + 4u * p.rows_per_wave * tokens) +
+                (wv.type == IQ2_XXS ? 2048 : 0);
+  return p;
+}
+
+template <int TYPE, int T, int R>
+static hipError_t gemv_go(const WeightView &wv, const float *x, float *y, const GemvPlan &p, hipStream_t s) {
+  hipLaunchKernelGGL((k_gemv<TYPE, T, R>), dim3(p.grid), dim3(256), p.lds_bytes, s, wv, x, y, p.kc, p.ksplit);
+  return hipGetLastError();
+}
+
+template <int TYPE, int T>
+static hipError_t gemv_r(const WeightView &wv, const float *x, float *y, const GemvPlan &p, hipStream_t s) {
+  if (p.rows_per_wave == 2) return gemv_go<TYPE, T, 2>(wv, x, y, p, s);
+  return gemv_go<TYPE, T, 1>(wv, x, y, p, s);
+}
+
+template <int TYPE>
+static hipError_t gemv_t(const WeightView &wv, const float *x, float *y, uint32_t tokens, const GemvPlan &p,
+                         hipStream_t s) {
+  switch (tokens) {
+    case 1: return gemv_go<TYPE, 1, 2>(wv, x, y, p, s);
+    case 2: return gemv_go<TYPE, 2, 2>(wv, x, y, p, s);
+    case 3: return gemv_go<TYPE, 3, 1>(wv, x, y, p, s);
+    case 4: return gemv_go<TYPE, 4, 1>(wv, x, y, p, s);
+    case 5: return gemv_go<TYPE, 5, 1>(wv, x, y, p, s);
+    case 6: return gemv_go<TYPE, 6, 1>(wv, x, y, p, s);
+    case 7: return gemv_go<TYPE, 7, 1>(wv, x, y, p, s);
+    case 8: return gemv_go<TYPE, 8, 1>(wv, x, y, p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemv(const WeightView &wv, const float *x, float *y, uint32_t tokens, const GemvPlan &p,
+                       hipStream_t s) {
+  switch (wv.type) {
+    case Q8_0: return gemv_t<Q8_0>(wv, x, y, tokens, p, s);
+    case Q8_0R: return gemv_t<Q8_0R>(wv, x, y, tokens, p, s);
+    case Q4_K: return gemv_t<Q4_K>(wv, x, y, tokens, p, s);
+    case Q6_K: return gemv_t<Q6_K>(wv, x, y, tokens, p, s);
+    case Q2_K: return gemv_t<Q2_K>(wv, x, y, tokens, p, s);
+    case IQ2_XXS: return gemv_t<IQ2_XXS>(wv, x, y, tokens, p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int TYPE>
+static hipError_t gemm_go(const WeightView &wv, const float *x, float *y, uint32_t tokens, hipStream_t s) {
+  dim3 grid((wv.rows + GT - 1) / GT, (tokens + GT - 1) / GT);
+  hipLaunchKernelGGL((k_gemm<TYPE>), grid, dim3(256), 0, s, wv, x, y, tokens);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, hipStream_t s) {
+  switch (wv.type) {
+    case Q8_0: return gemm_go<Q8_0>(wv, x, y, tokens, s);
+    case Q8_0R: return gemm_go<Q8_0R>(wv, x, y, tokens, s);
+    case Q4_K: return gemm_go<Q4_K>(wv, x, y, tokens, s);
+    case Q6_K: return gemm_go<Q6_K>(wv, x, y, tokens, s);
+    case Q2_K: return gemm_go<Q2_K>(wv, x, y, tokens, s);
+    case IQ2_XXS: return gemm_go<IQ2_XXS>(wv, x, y, tokens, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int TYPE>
+static hipError_t dequant_go(const uint8_t *w, uint64_t scales_off, uint32_t n_blocks, float *out, hipStream_t s) {
+  uint64_t units = (uint64_t)n_blocks * units_per_block<TYPE>();
+  uint32_t grid = (uint32_t)((units + 255) / 256);
+  hipLaunchKernelGGL((k_dequant<TYPE>), dim3(grid), dim3(256), 0, s, w, scales_off, n_blocks, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant(const uint8_t *w, int type, uint64_t scales_off, uint32_t n_blocks, float *out,
+                          hipStream_t s) {
+  switch (type) {
+    case Q8_0: return dequant_go<Q8_0>(w, scales_off, n_blocks, out, s);
+    case Q8_0R: return dequant_go<Q8_0R>(w, scales_off, n_blocks, out, s);
+    case Q4_K: return dequant_go<Q4_K>(w, scales_off, n_blocks, out, s);
+    case Q6_K: return dequant_go<Q6_K>(w, scales_off, n_blocks, out, s);
+    case Q2_K: return dequant_go<Q2_K>(w, scales_off, n_blocks, out, s);
+    case IQ2_XXS: return dequant_go<IQ2_XXS>(w, scales_off, n_blocks, out, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+size_t topk_scratch_bytes(uint32_t vocab) {
+  uint32_t chunks = (vocab + kTopkChunk - 1) / kTopkChunk;
+  return sizeof(uint32_t) * ((size_t)2 * chunks + (size_t)2 * chunks * kTopkChunkCap);
+}
+
+hipError_t launch_topk(const uint32_t *logits, uint32_t base, uint32_t vocab, uint32_t m,
+                       const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, uint32_t *scratch,
+                       uint32_t *out, hipStream_t s) {
+  const uint32_t chunks = (vocab + kTopkChunk - 1) / kTopkChunk;
+  TopkPenal pen{};
+  for (uint32_t i = 0; i < n_penal && i < 128; ++i) pen.ids[i] = penal_ids[i];
+  hipLaunchKernelGGL(k_topk_chunks, dim3(chunks), dim3(256), 0, s, logits, base, vocab, m, scratch);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_topk_final, dim3(1), dim3(256), 0, s, logits, base, vocab, m, pen, n_penal, serial,
+                     chunks, (const uint32_t *)scratch, out);
+  return hipGetLastError();
+}
+
+}  // namespace eff

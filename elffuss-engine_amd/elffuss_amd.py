@@ -1,0 +1,306 @@
+"""Python binding of libelffuss_amd.so (the C ABI in include/elffuss_amd.h).
+
+The binding is a thin ctypes layer: device buffers stay opaque `Buffer`
+objects, every operation is enqueued on the context's HIP stream, and errors
+come back as exceptions carrying the library's message. `NotApplicable` is the
+reference's `null` ("this fast path does not apply", ops.gemv.js:13-21).
+
+There is no fallback: if the shared library is missing or no GPU is present,
+loading or opening a context raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libelffuss_amd.so")
+
+OK, NOT_APPLICABLE = 0, 1
+E_INVALID, E_TYPE, E_SHAPE, E_MARK, E_BOUNDS, E_DEVICE, E_NOMEM = -1, -2, -3, -4, -5, -6, -7
+Q8_0, Q2_K, Q4_K, Q6_K, IQ2_XXS, Q8_0R = 8, 10, 12, 14, 16, 264
+TYPES = {"Q8_0": Q8_0, "Q2_K": Q2_K, "Q4_K": Q4_K, "Q6_K": Q6_K, "IQ2_XXS": IQ2_XXS, "Q8_0R": Q8_0R}
+OPT_GEMV_MAX_TOKENS, OPT_GEMM_MIN_TOKENS = 1, 2
+TOPK_HEADER, TOPK_P_MAX, TOPK_CAP, TOPK_M_MAX = 8, 128, 256, 192
+
+ERRORS = {E_INVALID: "invalid argument", E_TYPE: "unsupported type", E_SHAPE: "shape",
+          E_MARK: "repack mark", E_BOUNDS: "bounds", E_DEVICE: "device", E_NOMEM: "out of memory"}
+
+
+class EffError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"[{ERRORS.get(code, code)}] {msg}")
+        self.code = code
+
+
+class NotApplicable(Exception):
+    """The requested fast path does not apply (the reference returns null)."""
+
+
+class Stats(ctypes.Structure):
+    _fields_ = [("gemv", ctypes.c_uint64), ("gemm", ctypes.c_uint64), ("skinny", ctypes.c_uint64),
+                ("dequant", ctypes.c_uint64), ("topk", ctypes.c_uint64), ("not_applicable", ctypes.c_uint64)]
+
+
+_lib = None
+
+
+def lib():
+    """Load the shared library (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built: run `make -C elffuss-engine_amd` (or __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    p, u32, u64, i32, i64, sz = (ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int,
+                                 ctypes.c_int64, ctypes.c_size_t)
+    sig = {
+        "eff_type_from_name": ([ctypes.c_char_p], i32),
+        "eff_type_name": ([i32], ctypes.c_char_p),
+        "eff_type_geometry": ([i32, ctypes.POINTER(u32), ctypes.POINTER(u32)], i32),
+        "eff_init": ([i32, ctypes.POINTER(p)], i32),
+        "eff_shutdown": ([p], i32),
+        "eff_last_error": ([p], ctypes.c_char_p),
+        "eff_stream": ([p], p),
+        "eff_set_stream": ([p, p], i32),
+        "eff_sync": ([p], i32),
+        "eff_set_option": ([p, i32, i64], i32),
+        "eff_get_stats": ([p, ctypes.POINTER(Stats)], i32),
+        "eff_buf_alloc": ([p, sz, ctypes.POINTER(p)], i32),
+        "eff_buf_wrap": ([p, p, sz, ctypes.POINTER(p)], i32),
+        "eff_buf_free": ([p, p], i32),
+        "eff_buf_size": ([p], sz),
+        "eff_buf_device_ptr": ([p], p),
+        "eff_buf_write": ([p, p, sz, p, sz], i32),
+        "eff_buf_read": ([p, p, sz, p, sz], i32),
+        "eff_buf_copy": ([p, p, sz, p, sz, sz], i32),
+        "eff_bytes_reordered": ([i32, u32], sz),
+        "eff_bytes_buffer_r": ([i32, u32], sz),
+        "eff_blocks_from_buffer": ([i32, sz], u32),
+        "eff_scales_from": ([i32, u32], u32),
+        "eff_buf_mark_r": ([p, i32, u32], i32),
+        "eff_buf_blocks_r": ([p, ctypes.POINTER(u32)], i32),
+        "eff_repack": ([i32, p, u32, p, sz], i32),
+        "eff_unrepack": ([i32, p, sz, u32, p], i32),
+        "eff_quantize": ([i32, p, sz, p, sz], i32),
+        "eff_fill_normal": ([u32, ctypes.c_float, p, sz], i32),
+        "eff_qmatmul": ([p, i32, p, p, p, u32, u32, u32], i32),
+        "eff_qgemv": ([p, i32, p, p, p, u32, u32, u32], i32),
+        "eff_qgemm": ([p, i32, p, p, p, u32, u32, u32], i32),
+        "eff_dequant": ([p, i32, p, p, u32], i32),
+        "eff_topk": ([p, p, u32, u32, u32, p, u32, u32, p], i32),
+        "eff_topk_out_bytes": ([], sz),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
+    _lib = L
+    return L
+
+
+EXPORTED = ("eff_type_from_name eff_type_name eff_type_geometry eff_init eff_shutdown eff_last_error "
+            "eff_stream eff_set_stream eff_sync eff_set_option eff_get_stats eff_buf_alloc eff_buf_wrap "
+            "eff_buf_free eff_buf_size eff_buf_device_ptr eff_buf_write eff_buf_read eff_buf_copy "
+            "eff_bytes_reordered eff_bytes_buffer_r eff_blocks_from_buffer eff_scales_from eff_buf_mark_r "
+            "eff_buf_blocks_r eff_repack eff_unrepack eff_quantize eff_fill_normal eff_qmatmul eff_qgemv "
+            "eff_qgemm eff_dequant eff_topk eff_topk_out_bytes").split()
+
+
+def type_code(t):
+    if isinstance(t, str):
+        if t not in TYPES:
+            raise EffError(E_TYPE, f"unsupported quantization type «{t}»")
+        return TYPES[t]
+    return int(t)
+
+
+def geometry(t):
+    e, b = ctypes.c_uint32(), ctypes.c_uint32()
+    rc = lib().eff_type_geometry(type_code(t), ctypes.byref(e), ctypes.byref(b))
+    if rc:
+        raise EffError(rc, f"unknown type {t}")
+    return e.value, b.value
+
+
+# ---- host data preparation (no device needed) ------------------------------
+
+def fill_normal(seed, sigma, n):
+    out = np.empty(n, dtype=np.float32)
+    rc = lib().eff_fill_normal(seed & 0xFFFFFFFF, sigma, out.ctypes.data, n)
+    if rc:
+        raise EffError(rc, "fill_normal")
+    return out
+
+
+def quantize(t, x):
+    t = type_code(t)
+    xs = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    e, b = geometry(t)
+    out = np.empty(xs.size // e * b, dtype=np.uint8)
+    rc = lib().eff_quantize(t, xs.ctypes.data, xs.size, out.ctypes.data, out.size)
+    if rc:
+        raise EffError(rc, f"quantize {t}")
+    return out
+
+
+def repack(src, n_blocks):
+    s = np.ascontiguousarray(src, dtype=np.uint8)
+    out = np.empty(lib().eff_bytes_buffer_r(Q8_0R, n_blocks), dtype=np.uint8)
+    rc = lib().eff_repack(Q8_0R, s.ctypes.data, n_blocks, out.ctypes.data, out.size)
+    if rc:
+        raise EffError(rc, "repack")
+    return out
+
+
+def unrepack(src, n_blocks):
+    s = np.ascontiguousarray(src, dtype=np.uint8)
+    out = np.empty(34 * n_blocks, dtype=np.uint8)
+    rc = lib().eff_unrepack(Q8_0R, s.ctypes.data, s.size, n_blocks, out.ctypes.data)
+    if rc:
+        raise EffError(rc, "unrepack")
+    return out
+
+
+def bytes_buffer_r(n):
+    return lib().eff_bytes_buffer_r(Q8_0R, n)
+
+
+def bytes_reordered(n):
+    return lib().eff_bytes_reordered(Q8_0R, n)
+
+
+def blocks_from_buffer(nbytes):
+    return lib().eff_blocks_from_buffer(Q8_0R, nbytes)
+
+
+# ---- device ------------------------------------------------------------------
+
+class Buffer:
+    def __init__(self, ctx, handle, size):
+        self.ctx, self.handle, self.size = ctx, handle, size
+
+    @property
+    def ptr(self):
+        return lib().eff_buf_device_ptr(self.handle)
+
+    def write(self, arr, offset=0):
+        a = np.ascontiguousarray(arr)
+        self.ctx._check(lib().eff_buf_write(self.ctx.h, self.handle, offset, a.ctypes.data, a.nbytes))
+
+    def read(self, dtype=np.uint8, count=None, offset=0):
+        dt = np.dtype(dtype)
+        n = (self.size - offset) // dt.itemsize if count is None else count
+        out = np.empty(n, dtype=dt)
+        self.ctx._check(lib().eff_buf_read(self.ctx.h, self.handle, offset, out.ctypes.data, out.nbytes))
+        return out
+
+    def mark_r(self, n_blocks):
+        rc = lib().eff_buf_mark_r(self.handle, Q8_0R, n_blocks)
+        if rc:
+            raise EffError(rc, f"mark_r: buffer of {self.size} bytes for {n_blocks} blocks")
+
+    def blocks_r(self):
+        n = ctypes.c_uint32()
+        rc = lib().eff_buf_blocks_r(self.handle, ctypes.byref(n))
+        if rc:
+            raise EffError(rc, "buffer carries no repack mark")
+        return n.value
+
+    def free(self):
+        if self.handle:
+            lib().eff_buf_free(self.ctx.h, self.handle)
+            self.handle = None
+
+
+class Context:
+    """One HIP device context and its stream (eff_init)."""
+
+    def __init__(self, device=0):
+        h = ctypes.c_void_p()
+        rc = lib().eff_init(device, ctypes.byref(h))
+        if rc:
+            raise EffError(rc, f"eff_init(device={device}) failed: no usable HIP device")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().eff_shutdown(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _check(self, rc):
+        if rc == NOT_APPLICABLE:
+            raise NotApplicable()
+        if rc:
+            raise EffError(rc, lib().eff_last_error(self.h).decode())
+        return rc
+
+    @property
+    def stream(self):
+        return lib().eff_stream(self.h)
+
+    def set_stream(self, stream_ptr):
+        self._check(lib().eff_set_stream(self.h, stream_ptr))
+
+    def sync(self):
+        self._check(lib().eff_sync(self.h))
+
+    def set_option(self, opt, value):
+        self._check(lib().eff_set_option(self.h, opt, value))
+
+    def stats(self):
+        s = Stats()
+        self._check(lib().eff_get_stats(self.h, ctypes.byref(s)))
+        return {f: getattr(s, f) for f, _ in Stats._fields_}
+
+    def alloc(self, nbytes):
+        h = ctypes.c_void_p()
+        self._check(lib().eff_buf_alloc(self.h, nbytes, ctypes.byref(h)))
+        return Buffer(self, h, nbytes)
+
+    def upload(self, arr):
+        a = np.ascontiguousarray(arr)
+        b = self.alloc(max(a.nbytes, 1))
+        if a.nbytes:
+            b.write(a)
+        return b
+
+    def copy(self, dst, src, n, dst_offset=0, src_offset=0):
+        self._check(lib().eff_buf_copy(self.h, dst.handle, dst_offset, src.handle, src_offset, n))
+
+    def qmatmul(self, t, w, x, y, rows, k, tokens=1):
+        self._check(lib().eff_qmatmul(self.h, type_code(t), w.handle, x.handle, y.handle, rows, k, tokens))
+
+    def qgemv(self, t, w, x, y, rows, k, tokens=1):
+        self._check(lib().eff_qgemv(self.h, type_code(t), w.handle, x.handle, y.handle, rows, k, tokens))
+
+    def qgemm(self, t, w, x, y, rows, k, tokens):
+        self._check(lib().eff_qgemm(self.h, type_code(t), w.handle, x.handle, y.handle, rows, k, tokens))
+
+    def dequant(self, t, w, out, n_blocks):
+        self._check(lib().eff_dequant(self.h, type_code(t), w.handle, out.handle, n_blocks))
+
+    def topk(self, logits, base, vocab, m, penal_ids=(), serial=1, out=None):
+        ids = np.ascontiguousarray(np.asarray(penal_ids, dtype=np.uint32))
+        if out is None:
+            out = self.alloc(lib().eff_topk_out_bytes())
+        self._check(lib().eff_topk(self.h, logits.handle, base, vocab, m,
+                                   ids.ctypes.data if ids.size else None, ids.size, serial, out.handle))
+        return out
+
+
+def parse_topk(u):
+    """Split the top-k output record (kernels.topk.wgsl.js:50-59 layout)."""
+    u = np.asarray(u, dtype=np.uint32)
+    n = int(u[0])
+    pairs = u[TOPK_HEADER + TOPK_P_MAX:].reshape(-1, 2)
+    return {"n": n, "flags": int(u[1]), "n_penal": int(u[2]), "chunks": int(u[3]), "serial": int(u[4]),
+            "penal_bits": u[TOPK_HEADER:TOPK_HEADER + int(u[2])].copy(),
+            "ids": pairs[:n, 0].copy(), "bits": pairs[:n, 1].copy()}

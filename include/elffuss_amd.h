@@ -1,0 +1,232 @@
+/*
+ * elffuss_amd.h — C ABI of the MI355X (gfx950) quantized matrix-product path.
+ *
+ * This is the drop-in boundary for Elffuss Engine's quantized GEMV/GEMM hot
+ * path. A host binding (N-API addon for the JavaScript engine, ctypes for
+ * Python) calls these functions with plain pointers and sizes. Device memory
+ * is held in opaque buffers; every launch is enqueued on the context's HIP
+ * stream and returns without waiting, as the reference records dispatches into
+ * an open compute pass and returns (ops.js:667-710). Only eff_buf_read and
+ * eff_sync wait for the device (device.js:165-200, readback).
+ *
+ * Return codes follow the reference's error conventions:
+ *   EFF_OK              success;
+ *   EFF_NOT_APPLICABLE  "this fast path does not apply, caller falls back",
+ *                       the reference's `null` (ops.gemv.js:13-21, ops.gemm2.js:5-8);
+ *   negative            contract violation or device failure, the reference's
+ *                       thrown Error; eff_last_error() gives the message.
+ *
+ * Types are ggml type codes (gguf.js:51-64) plus the internal repacked type
+ * Q8_0R (kernels.bloques.wgsl.js:86-89), which never appears in a GGUF file.
+ */
+#ifndef ELFFUSS_AMD_H
+#define ELFFUSS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------- */
+#define EFF_OK              0
+#define EFF_NOT_APPLICABLE  1
+#define EFF_E_INVALID      (-1)  /* bad argument (null pointer, zero size, ...) */
+#define EFF_E_TYPE         (-2)  /* unknown or unsupported type (ops.js:767-771) */
+#define EFF_E_SHAPE        (-3)  /* k not a multiple of the block (ops.js:850-852) */
+#define EFF_E_MARK         (-4)  /* repacked buffer unmarked, wrong type or call beyond the tensor (repack.js:268-286) */
+#define EFF_E_BOUNDS       (-5)  /* a buffer is too small for the call */
+#define EFF_E_DEVICE       (-6)  /* HIP runtime error */
+#define EFF_E_NOMEM        (-7)  /* device allocation failed */
+
+/* ---- types (ggml codes; gguf.js:51-64) ---------------------------------- */
+#define EFF_TYPE_Q8_0      8
+#define EFF_TYPE_Q2_K      10
+#define EFF_TYPE_Q4_K      12
+#define EFF_TYPE_Q6_K      14
+#define EFF_TYPE_IQ2_XXS   16
+#define EFF_TYPE_Q8_0R     264   /* Q8_0 repacked at load (kernels.bloques.wgsl.js:19-35) */
+
+/* ---- options (the reference's globalThis.__ELFFUSS_* switches, ops.js:827-1101) */
+#define EFF_OPT_GEMV_MAX_TOKENS  1  /* tokens <= this go to the GEMV kernels (default 8) */
+#define EFF_OPT_GEMM_MIN_TOKENS  2  /* tokens >= this go to the fp16 MFMA GEMM (default 64; __ELFFUSS_DRIFT_DESDE) */
+
+/* ---- top-k output layout (kernels.topk.wgsl.js:40-60) ------------------- */
+#define EFF_TOPK_M_MAX     192   /* largest M = K' + |S| accepted (TOPK_M_MAX) */
+#define EFF_TOPK_P_MAX     128   /* penalised ids (TOPK_P_MAX) */
+#define EFF_TOPK_CAP       256   /* candidate pairs in the output (TOPK_CAP) */
+#define EFF_TOPK_HEADER    8     /* u32 header words (TOPK_CABECERA) */
+#define EFF_TOPK_N_MAX     (1u << 24)  /* vocabulary limit (TOPK_N_MAX) */
+
+typedef struct eff_ctx eff_ctx;
+typedef struct eff_buf eff_buf;
+
+/* Dispatch counters: lets a caller assert that a fast path really ran
+ * (ops.gemv.js:92-95 `hechos`, ops.topk.js:36-40 `estadisticasTopK`). */
+typedef struct eff_stats {
+  uint64_t gemv;        /* GEMV launches (tokens <= GEMV max) */
+  uint64_t gemm;        /* fp16 MFMA GEMM launches */
+  uint64_t skinny;      /* GEMV launches over token groups (GEMV max < tokens < GEMM min) */
+  uint64_t dequant;     /* dequant launches */
+  uint64_t topk;        /* top-k launches (chunk + final pair) */
+  uint64_t not_applicable;  /* calls answered EFF_NOT_APPLICABLE */
+} eff_stats;
+
+/* ---- types and geometry -------------------------------------------------- */
+
+/* Type code for a ggml type name ("Q8_0", "Q8_0R", "Q4_K", "Q6_K", "Q2_K",
+ * "IQ2_XXS"); EFF_E_TYPE otherwise. Replaces quantInfo/QUANT_TYPES
+ * (kernels.wgsl.js:886-895). */
+int eff_type_from_name(const char *name);
+
+/* Name of a type code, or NULL. */
+const char *eff_type_name(int type);
+
+/* Elements and bytes per block (gguf.js:51-64; kernels.wgsl.js QUANT_TYPES).
+ * For Q8_0R block_bytes is the average 34, not a stride (kernels.wgsl.js:846-850). */
+int eff_type_geometry(int type, uint32_t *block_elems, uint32_t *block_bytes);
+
+/* ---- context -------------------------------------------------------------- */
+
+/* Open a context on HIP device `device` with its own stream (default priority).
+ * Replaces requestDevice + createOps (device.js:66-139, ops.js:1604-1633). */
+int eff_init(int device, eff_ctx **out);
+
+/* Release the context, its stream (if owned) and its scratch memory. */
+int eff_shutdown(eff_ctx *ctx);
+
+/* Message of the last error on this context ("" if none). */
+const char *eff_last_error(const eff_ctx *ctx);
+
+/* The hipStream_t launches are enqueued on. */
+void *eff_stream(eff_ctx *ctx);
+
+/* Enqueue on a caller-owned hipStream_t from now on (NULL: back to the
+ * context's own stream). The caller keeps ownership. */
+int eff_set_stream(eff_ctx *ctx, void *hip_stream);
+
+/* Wait for everything enqueued on the context's stream. */
+int eff_sync(eff_ctx *ctx);
+
+/* Set an option (EFF_OPT_*). Mirrors the __ELFFUSS_* switches read per call. */
+int eff_set_option(eff_ctx *ctx, int option, int64_t value);
+
+/* Dispatch counters since eff_init. */
+int eff_get_stats(const eff_ctx *ctx, eff_stats *out);
+
+/* ---- device buffers ------------------------------------------------------ */
+
+/* Allocate `bytes` of device memory (plus hidden read slack; the reference's
+ * loader leaves 4 bytes after every tensor, model.js:248-254). Contents are
+ * zero. Replaces ctx.alloc/createBuffer (ops.js:233-281). */
+int eff_buf_alloc(eff_ctx *ctx, size_t bytes, eff_buf **out);
+
+/* Wrap caller-owned device memory of `bytes` bytes (not freed by
+ * eff_buf_free). The caller must leave at least 16 readable bytes after it. */
+int eff_buf_wrap(eff_ctx *ctx, void *device_ptr, size_t bytes, eff_buf **out);
+
+int eff_buf_free(eff_ctx *ctx, eff_buf *buf);
+size_t eff_buf_size(const eff_buf *buf);
+void *eff_buf_device_ptr(const eff_buf *buf);
+
+/* Host -> device, enqueued on the stream (queue.writeBuffer). `src` is copied
+ * before return. */
+int eff_buf_write(eff_ctx *ctx, eff_buf *buf, size_t offset, const void *src, size_t n);
+
+/* Device -> host; waits for prior work (readback, device.js:165-200). */
+int eff_buf_read(eff_ctx *ctx, eff_buf *buf, size_t offset, void *dst, size_t n);
+
+/* Device -> device copy, enqueued. */
+int eff_buf_copy(eff_ctx *ctx, eff_buf *dst, size_t dst_offset, eff_buf *src,
+                 size_t src_offset, size_t n);
+
+/* ---- repacked layout (Q8_0R) -------------------------------------------- */
+
+/* Bytes of the Q8_0R format of n blocks: 34n rounded up to 4
+ * (bytesReordenado, kernels.bloques.wgsl.js:111-113). */
+size_t eff_bytes_reordered(int type_r, uint32_t n_blocks);
+
+/* Bytes of a Q8_0R buffer for n blocks: 34n rounded up to 16
+ * (bytesBufferR, kernels.bloques.wgsl.js:115-120). */
+size_t eff_bytes_buffer_r(int type_r, uint32_t n_blocks);
+
+/* Blocks a Q8_0R buffer of `bytes` bytes holds: floor(2L/17), L = bytes/4
+ * (bloquesDeBuffer, kernels.bloques.wgsl.js:128-135). */
+uint32_t eff_blocks_from_buffer(int type_r, size_t bytes);
+
+/* First u32 word of the scale region of a tensor of n blocks: 8n
+ * (escalasDesde, kernels.bloques.wgsl.js:122-125). */
+uint32_t eff_scales_from(int type_r, uint32_t n_blocks);
+
+/* Mark `buf` as holding a Q8_0R tensor of n blocks; its size must equal
+ * eff_bytes_buffer_r (marcaBufferR, repack.js:241-251). */
+int eff_buf_mark_r(eff_buf *buf, int type_r, uint32_t n_blocks);
+
+/* Blocks recorded by the mark, EFF_E_MARK if unmarked (bloquesR, repack.js:256-259). */
+int eff_buf_blocks_r(const eff_buf *buf, uint32_t *n_blocks);
+
+/* Host repack of n GGUF Q8_0 blocks into Q8_0R (reordena, repack.js:187-199).
+ * `dst_bytes` >= eff_bytes_reordered; bytes after the scales are zeroed. */
+int eff_repack(int type_r, const void *src, uint32_t n_blocks, void *dst, size_t dst_bytes);
+
+/* Inverse: Q8_0R back to GGUF blocks, 34n bytes (vuelveAlGGUF, repack.js:204-219). */
+int eff_unrepack(int type_r, const void *src, size_t src_bytes, uint32_t n_blocks, void *dst);
+
+/* ---- host data preparation ---------------------------------------------- */
+
+/* Quantize n floats (n a multiple of the block) into GGUF blocks. Q8_0 follows
+ * the reference's quantizer (cpu.js:273-287, aF16 cpu.js:84-99). Q4_K, Q6_K,
+ * Q2_K and IQ2_XXS have no quantizer in the reference (it only reads them);
+ * these are this library's own, producing valid blocks of the GGUF layout.
+ * Uses all host threads. */
+int eff_quantize(int type, const float *src, size_t n, void *dst, size_t dst_bytes);
+
+/* Deterministic N(0, sigma) floats: uniforms from the mulberry32 hash of
+ * sample.js:36-41 at counters seed+2i, seed+2i+1, Box-Muller in double,
+ * rounded to float. Element i depends only on (seed, i). */
+int eff_fill_normal(uint32_t seed, float sigma, float *dst, size_t n);
+
+/* ---- operations (enqueued on the context's stream) ---------------------- */
+
+/* Y[tokens][rows] = W (rows x k, quantized) . X[tokens][k]; X and Y are f32.
+ * Router of quant.matmul (ops.js:827-1101): tokens <= GEMV max -> GEMV;
+ * tokens >= GEMM min -> fp16 MFMA GEMM; in between -> GEMV over token groups.
+ * EFF_E_SHAPE if k % block_elems != 0. */
+int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
+                uint32_t rows, uint32_t k, uint32_t tokens);
+
+/* The decode GEMV alone (quant.gemv.matmul, ops.gemv.js:148-164): f32
+ * accumulation, 1..GEMV max tokens. EFF_NOT_APPLICABLE outside that range. */
+int eff_qgemv(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
+              uint32_t rows, uint32_t k, uint32_t tokens);
+
+/* The prefill GEMM alone (quant.gemm2.matmul, ops.gemm2.js:266-280): x and
+ * the dequantized weights rounded to fp16, MFMA with fp32 accumulation.
+ * EFF_NOT_APPLICABLE when tokens < GEMM min (planGemm2 returning null). */
+int eff_qgemm(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
+              uint32_t rows, uint32_t k, uint32_t tokens);
+
+/* Dequantize n_blocks blocks to f32, bit-exact with the reference decoders
+ * (quant.dequant, ops.js:813-823; dequantShader, kernels.wgsl.js:903-922). */
+int eff_dequant(eff_ctx *ctx, int type, eff_buf *w, eff_buf *out, uint32_t n_blocks);
+
+/* Exact top-m of logits[base .. base+vocab) ordered by (f32 value desc with
+ * -0 == +0, index asc), plus the raw logits of the penalised ids. Writes the
+ * reference's output record into `out` (kernels.topk.wgsl.js:50-59):
+ *   u32[0] candidates, [1] flags (2 = NaN seen, 1|4 = overflow), [2] n_penal,
+ *   [3] chunks, [4] serial, [5..7] 0, then EFF_TOPK_P_MAX penalised-logit bit
+ *   patterns, then EFF_TOPK_CAP (id, bits) pairs.
+ * Pairs are written sorted by (value desc, index asc). Replaces
+ * createTopKGPU().candidatos (ops.topk.js:99-165). */
+int eff_topk(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint32_t m,
+             const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, eff_buf *out);
+
+/* Size in bytes of the top-k output record (topkBytesSalida). */
+size_t eff_topk_out_bytes(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ELFFUSS_AMD_H */

@@ -1,0 +1,80 @@
+"""The BASELINE.json configurations at their full sizes, through the C ABI,
+against the oracle (whole outputs for GEMV, contiguous row slices for the
+large GEMMs) and, for C4, the top-40 of the GPU's own logits bit-exact."""
+import numpy as np
+import pytest
+
+from test_gpu_parity import check_close, make_weights, oracle_type, upload_w
+
+pytestmark = pytest.mark.gpu
+
+
+def run(ctx, eff, tname, rows, k, tokens, seed, force=None):
+    t, data, gguf, n = make_weights(eff, tname, rows, k, seed)
+    x = eff.fill_normal(seed + 1, 1.0, tokens * k)
+    wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    if force == "gemm":
+        ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+    else:
+        ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+    y = yb.read(np.float32).reshape(tokens, rows)
+    for b in (wb, xb, yb):
+        b.free()
+    return gguf, x, y
+
+
+def row_slice(eff, tname, gguf, k, r0, r1):
+    base = "Q8_0" if tname == "Q8_0R" else tname
+    e, bb = eff.geometry(base)
+    rb = k // e * bb
+    return gguf[r0 * rb: r1 * rb]
+
+
+@pytest.mark.parametrize("tname", ["Q8_0", "Q8_0R"])
+def test_c1_q8_0_gemv_8192x2048(ctx, eff, orc, tname):
+    gguf, x, y = run(ctx, eff, tname, 8192, 2048, 1, 101)
+    check_close(y, orc.gemv_f64(orc.Q8_0, gguf, 8192, 2048, x, 1), f"C1 {tname}")
+
+
+def test_c2_q4_k_gemv_2048x8192(ctx, eff, orc):
+    gguf, x, y = run(ctx, eff, "Q4_K", 2048, 8192, 1, 202)
+    check_close(y, orc.gemv_f64(orc.Q4_K, gguf, 2048, 8192, x, 1), "C2 Q4_K")
+
+
+@pytest.mark.parametrize("tokens", [512, 2048])
+def test_c3_q8_0_gemm(ctx, eff, orc, tokens):
+    rows, k = 8192, 2048
+    gguf, x, y = run(ctx, eff, "Q8_0", rows, k, tokens, 303)
+    for r0, r1 in ((0, 96), (rows - 160, rows)):
+        ref = orc.gemm_f16(orc.Q8_0, row_slice(eff, "Q8_0", gguf, k, r0, r1), r1 - r0, k, x, tokens)
+        check_close(y[:, r0:r1], ref, f"C3 M={tokens} rows {r0}:{r1}")
+
+
+def test_c4_q6_k_head_and_top40(ctx, eff, orc):
+    rows, k = 65536, 2048
+    t, data, gguf, n = make_weights(eff, "Q6_K", rows, k, 404)
+    x = eff.fill_normal(405, 1.0, k)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(rows * 4)
+    ctx.qmatmul(t, wb, xb, yb, rows, k, 1)
+    out = ctx.topk(yb, 0, rows, 40, penal_ids=[3, 77], serial=9)
+    y = yb.read(np.float32)
+    r = eff.parse_topk(out.read(np.uint32))
+    check_close(y[None, :], orc.gemv_f64(orc.Q6_K, gguf, rows, k, x, 1), "C4 Q6_K logits")
+    ids, bits, nan = orc.topk(y.view(np.uint32), 40)
+    assert not nan and r["flags"] == 0 and r["n"] == 40 and r["serial"] == 9
+    assert np.array_equal(r["ids"], ids) and np.array_equal(r["bits"], bits)
+    assert np.array_equal(r["penal_bits"], y.view(np.uint32)[[3, 77]])
+
+
+@pytest.mark.parametrize("tname", ["Q2_K", "IQ2_XXS"])
+@pytest.mark.parametrize("tokens", [1, 8, 32, 128])
+def test_c5_low_bit_sweep(ctx, eff, orc, tname, tokens):
+    rows, k = 8192, 2048
+    gguf, x, y = run(ctx, eff, tname, rows, k, tokens, 505 + tokens)
+    ot = oracle_type(orc, tname)
+    if tokens < 64:
+        check_close(y, orc.gemv_f64(ot, gguf, rows, k, x, tokens), f"C5 {tname} M={tokens}")
+    else:
+        for r0, r1 in ((0, 256), (rows - 256, rows)):
+            ref = orc.gemm_f16(ot, row_slice(eff, tname, gguf, k, r0, r1), r1 - r0, k, x, tokens)
+            check_close(y[:, r0:r1], ref, f"C5 {tname} M={tokens} rows {r0}:{r1}")

@@ -1,0 +1,244 @@
+"""GPU parity: the HIP path through the C ABI against the pinned oracle.
+
+Bars:
+  * dequantization, repack and top-k: bit-exact;
+  * GEMV (f32 activations): against the f64 oracle, relative L2 <= 1e-4 and,
+    per token, max |delta| <= 1e-3 * ||y_ref[token]||_2;
+  * GEMM (x and dequantized W rounded to fp16, the reference's DRIFT/GEMM2
+    rounding points): the same two bounds against the fp16-rounded oracle.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TYPES = ["Q8_0", "Q8_0R", "Q4_K", "Q6_K", "Q2_K", "IQ2_XXS"]
+REL_L2 = 1e-4
+ROW_FRAC = 1e-3
+
+
+def check_close(y, ref, what):
+    y = np.asarray(y, np.float64).reshape(ref.shape)
+    d = y - ref
+    rel = np.linalg.norm(d) / max(np.linalg.norm(ref), 1e-30)
+    row_norm = np.linalg.norm(ref, axis=1)
+    worst = np.max(np.abs(d), axis=1) / np.maximum(row_norm, 1e-30)
+    print(f"{what}: rel_l2={rel:.2e} max_row_frac={worst.max():.2e}", flush=True)
+    assert rel <= REL_L2, f"{what}: relative L2 {rel:.3e} > {REL_L2}"
+    assert np.all(worst <= ROW_FRAC), f"{what}: max|d| / ||row|| {worst.max():.3e} > {ROW_FRAC}"
+
+
+def make_weights(eff, tname, rows, k, seed):
+    """(type code for the op, bytes to upload, GGUF bytes, n_blocks)."""
+    base = "Q8_0" if tname == "Q8_0R" else tname
+    w = eff.quantize(base, eff.fill_normal(seed, 0.02, rows * k))
+    e, _ = eff.geometry(base)
+    n = rows * k // e
+    if tname == "Q8_0R":
+        return eff.Q8_0R, eff.repack(w, n), w, n
+    return eff.TYPES[tname], w, w, n
+
+
+def upload_w(ctx, eff, tname, data, n):
+    b = ctx.upload(data)
+    if tname == "Q8_0R":
+        b.mark_r(n)
+    return b
+
+
+def oracle_type(orc, tname):
+    return orc.Q8_0 if tname == "Q8_0R" else orc.NAMES[tname]
+
+
+# ---- dequantization --------------------------------------------------------------
+
+@pytest.mark.parametrize("tname", TYPES)
+@pytest.mark.parametrize("nrows", [1, 7, 1000])
+def test_dequant_bit_exact(ctx, eff, orc, tname, nrows):
+    k = 256
+    t, data, gguf, n = make_weights(eff, tname, nrows, k, 3 + nrows)
+    wb = upload_w(ctx, eff, tname, data, n)
+    out = ctx.alloc(nrows * k * 4)
+    ctx.dequant(t, wb, out, n)
+    got = out.read(np.uint32)
+    want = orc.dequant(oracle_type(orc, tname), gguf, n).view(np.uint32)
+    assert np.array_equal(got, want)
+    wb.free(); out.free()
+
+
+def test_dequant_q8_0r_partial_call_uses_tensor_scales(ctx, eff, orc):
+    """A call over fewer blocks than the tensor still finds the scales at 32N
+    (the output head is called with the tokenizer's vocabulary, repack.js:254-259)."""
+    t, data, gguf, n = make_weights(eff, "Q8_0R", 40, 256, 9)
+    wb = upload_w(ctx, eff, "Q8_0R", data, n)
+    out = ctx.alloc(100 * 32 * 4)
+    ctx.dequant(t, wb, out, 100)
+    assert np.array_equal(out.read(np.uint32), orc.dequant(orc.Q8_0, gguf, 100).view(np.uint32))
+
+
+# ---- GEMV ----------------------------------------------------------------------
+
+@pytest.mark.parametrize("tname", TYPES)
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4, 5, 8])
+def test_gemv_vs_f64_oracle(ctx, eff, orc, tname, tokens):
+    rows, k = 77, 2048      # rows not a multiple of the rows per wave; k spans two x passes at 8 tokens
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 20 + tokens)
+    x = eff.fill_normal(1000 + tokens, 1.0, tokens * k)
+    wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    ctx.qgemv(t, wb, xb, yb, rows, k, tokens)
+    ref = orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens)
+    check_close(yb.read(np.float32), ref, f"gemv {tname} T={tokens}")
+    for b in (wb, xb, yb):
+        b.free()
+
+
+@pytest.mark.parametrize("k", [32, 96, 256, 8192, 16384])
+def test_gemv_k_edge_cases(ctx, eff, orc, k):
+    for tname in (["Q8_0", "Q8_0R"] if k % 256 else TYPES):
+        rows = 5
+        t, data, gguf, n = make_weights(eff, tname, rows, k, k)
+        x = eff.fill_normal(k + 1, 1.0, k)
+        wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x), ctx.alloc(rows * 4)
+        ctx.qgemv(t, wb, xb, yb, rows, k, 1)
+        check_close(yb.read(np.float32), orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, 1),
+                    f"gemv {tname} k={k}")
+
+
+def test_q8_0r_gemv_bit_identical_to_q8_0(ctx, eff):
+    """Repacked and GGUF layouts give the same bits (kernels.wgsl.js:831-839)."""
+    rows, k = 300, 2048
+    _, data_r, gguf, n = make_weights(eff, "Q8_0R", rows, k, 5)
+    x = eff.fill_normal(6, 1.0, 2 * k)
+    a, b = ctx.upload(gguf), upload_w(ctx, eff, "Q8_0R", data_r, n)
+    xb, ya, yb = ctx.upload(x), ctx.alloc(2 * rows * 4), ctx.alloc(2 * rows * 4)
+    ctx.qgemv(eff.Q8_0, a, xb, ya, rows, k, 2)
+    ctx.qgemv(eff.Q8_0R, b, xb, yb, rows, k, 2)
+    assert np.array_equal(ya.read(np.uint32), yb.read(np.uint32))
+
+
+# ---- GEMM --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("tname", TYPES)
+@pytest.mark.parametrize("tokens", [64, 100, 200])
+def test_gemm_vs_fp16_oracle(ctx, eff, orc, tname, tokens):
+    rows, k = 130, 512
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 40 + tokens)
+    x = eff.fill_normal(2000 + tokens, 1.0, tokens * k)
+    wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+    ref = orc.gemm_f16(oracle_type(orc, tname), gguf, rows, k, x, tokens)
+    check_close(yb.read(np.float32), ref, f"gemm {tname} M={tokens}")
+    for b in (wb, xb, yb):
+        b.free()
+
+
+def test_gemm_q8_0_k_not_multiple_of_step(ctx, eff, orc):
+    rows, k, tokens = 64, 96, 70
+    t, data, gguf, n = make_weights(eff, "Q8_0", rows, k, 71)
+    x = eff.fill_normal(72, 1.0, tokens * k)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+    check_close(yb.read(np.float32), orc.gemm_f16(orc.Q8_0, gguf, rows, k, x, tokens), "gemm Q8_0 k=96")
+
+
+# ---- router, NOT_APPLICABLE and errors -----------------------------------------------
+
+def test_router_paths_and_stats(ctx, eff, orc):
+    rows, k = 96, 512
+    t, data, gguf, n = make_weights(eff, "Q4_K", rows, k, 90)
+    wb = ctx.upload(data)
+    before = ctx.stats()
+    for tokens, oracle_fn in ((1, orc.gemv_f64), (9, orc.gemv_f64), (33, orc.gemv_f64), (64, orc.gemm_f16)):
+        x = eff.fill_normal(91 + tokens, 1.0, tokens * k)
+        xb, yb = ctx.upload(x), ctx.alloc(tokens * rows * 4)
+        ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+        check_close(yb.read(np.float32), oracle_fn(orc.Q4_K, gguf, rows, k, x, tokens), f"matmul T={tokens}")
+    after = ctx.stats()
+    assert after["gemv"] - before["gemv"] == 1
+    assert after["skinny"] - before["skinny"] == 2 + 5
+    assert after["gemm"] - before["gemm"] == 1
+
+
+def test_not_applicable_and_errors(ctx, eff):
+    rows, k = 8, 256
+    t, data, gguf, n = make_weights(eff, "Q4_K", rows, k, 1)
+    wb, xb, yb = ctx.upload(data), ctx.alloc(64 * k * 4), ctx.alloc(64 * rows * 4)
+    with pytest.raises(eff.NotApplicable):
+        ctx.qgemv(t, wb, xb, yb, rows, k, 9)
+    with pytest.raises(eff.NotApplicable):
+        ctx.qgemm(t, wb, xb, yb, rows, k, 32)
+    with pytest.raises(eff.EffError) as e:
+        ctx.qmatmul(t, wb, xb, yb, rows, 300, 1)
+    assert e.value.code == eff.E_SHAPE and "300" in str(e.value)
+    with pytest.raises(eff.EffError) as e:
+        ctx.qmatmul(99, wb, xb, yb, rows, k, 1)
+    assert e.value.code == eff.E_TYPE
+    with pytest.raises(eff.EffError) as e:
+        ctx.qmatmul(t, wb, xb, yb, rows * 4, k, 1)      # W too small for the call
+    assert e.value.code == eff.E_BOUNDS
+    # Q8_0R: unmarked buffer, and a call beyond the marked tensor
+    _, data_r, _, nr = make_weights(eff, "Q8_0R", rows, k, 2)
+    rb = ctx.upload(data_r)
+    with pytest.raises(eff.EffError) as e:
+        ctx.qmatmul(eff.Q8_0R, rb, xb, yb, rows, k, 1)
+    assert e.value.code == eff.E_MARK
+    rb.mark_r(nr)
+    assert rb.blocks_r() == nr
+    ctx.qmatmul(eff.Q8_0R, rb, xb, yb, rows, k, 1)
+    with pytest.raises(eff.EffError) as e:
+        ctx.qmatmul(eff.Q8_0R, rb, xb, yb, rows + 1, k, 1)
+    assert e.value.code == eff.E_MARK
+    with pytest.raises(eff.EffError):
+        ctx.alloc(1000).mark_r(64)                      # wrong size for 64 blocks
+    # options
+    ctx.set_option(eff.OPT_GEMM_MIN_TOKENS, 16)
+    try:
+        ctx.qgemm(t, wb, xb, yb, rows, k, 32)
+    finally:
+        ctx.set_option(eff.OPT_GEMM_MIN_TOKENS, 64)
+    with pytest.raises(eff.EffError):
+        ctx.set_option(eff.OPT_GEMV_MAX_TOKENS, 9)
+
+
+# ---- top-k ---------------------------------------------------------------------------
+
+def run_topk(ctx, eff, vals, m, base=0, penal=(), serial=7):
+    buf = np.zeros(base + vals.size, np.float32)
+    buf[base:] = vals
+    lb = ctx.upload(buf)
+    out = ctx.topk(lb, base, vals.size, m, penal, serial)
+    return eff.parse_topk(out.read(np.uint32))
+
+
+@pytest.mark.parametrize("vocab,m", [(1, 1), (100, 40), (4096, 40), (4097, 40), (65536, 40),
+                                     (70000, 192), (10, 40), (200000, 7)])
+def test_topk_bit_exact(ctx, eff, orc, vocab, m):
+    rng = np.random.default_rng(vocab + m)
+    vals = rng.normal(0, 3, vocab).astype(np.float32)
+    vals[rng.integers(0, vocab, max(1, vocab // 8))] = 2.5      # ties, broken by index
+    if vocab > 3:
+        vals[1], vals[2] = -0.0, 0.0
+    r = run_topk(ctx, eff, vals, m, base=3, penal=[0, vocab - 1, vocab + 5], serial=42)
+    ids, bits, nan = orc.topk(vals.view(np.uint32), m)
+    assert r["n"] == len(ids) and r["flags"] == 0 and r["serial"] == 42
+    assert r["chunks"] == (vocab + 4095) // 4096
+    assert np.array_equal(r["ids"], ids) and np.array_equal(r["bits"], bits)
+    assert np.array_equal(r["penal_bits"], np.array([vals.view(np.uint32)[0], vals.view(np.uint32)[-1], 0], np.uint32))
+
+
+def test_topk_flags_nan_and_limits(ctx, eff):
+    vals = np.arange(5000, dtype=np.float32)
+    vals[1234] = np.nan
+    r = run_topk(ctx, eff, vals, 40)
+    assert r["flags"] & 2
+    lb = ctx.upload(vals)
+    with pytest.raises(eff.NotApplicable):
+        ctx.topk(lb, 0, vals.size, 193)
+    with pytest.raises(eff.NotApplicable):
+        ctx.topk(lb, 0, vals.size, 40, penal_ids=list(range(129)))
+
+
+def test_topk_all_equal(ctx, eff):
+    vals = np.full(9000, 1.5, np.float32)
+    r = run_topk(ctx, eff, vals, 40)
+    assert list(r["ids"]) == list(range(40))
