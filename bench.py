@@ -146,6 +146,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--only", default="", help="run only sweep entries whose name contains this text")
+    ap.add_argument("--no-head", action="store_true", help="skip the headline measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path is single-GPU by design (got --gpus {args.gpus}); "
@@ -159,10 +161,12 @@ def main():
     torch.cuda.init()
 
     # Headline: configs[1]
-    head = Config(eff, ctx, "Q4_K", 2048, 8192, 1, 202)
-    ms = time_steps(torch, ctx, head, args.steps, args.warmup)
-    gbs = head.bytes / (ms * 1e-3) / 1e9
-    head.free()
+    ms, gbs = float("nan"), float("nan")
+    if not args.no_head:
+        head = Config(eff, ctx, "Q4_K", 2048, 8192, 1, 202)
+        ms = time_steps(torch, ctx, head, args.steps, args.warmup)
+        gbs = head.bytes / (ms * 1e-3) / 1e9
+        head.free()
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
@@ -180,10 +184,12 @@ def main():
             for m in (1, 8, 32, 128):
                 plan.append(("C5", tn, 8192, 2048, m, 0))
         for tag, tn, rows, k, m, tk in plan:
+            key = f"{tag} {tn} N={rows} K={k} M={m}" + (" +top40" if tk else "")
+            if args.only and args.only not in key:
+                continue
             cfg = Config(eff, ctx, tn, rows, k, m, 300 + rows + m, topk=tk)
             steps = 40 if cfg.gemm else 100
             t_ms = time_steps(torch, ctx, cfg, steps, 5)
-            key = f"{tag} {tn} N={rows} K={k} M={m}" + (" +top40" if tk else "")
             gb = cfg.bytes / (t_ms * 1e-3) / 1e9
             tf = cfg.flops / (t_ms * 1e-3) / 1e12
             hbm_t = cfg.bytes / (HBM_PEAK_GBS * 1e9)

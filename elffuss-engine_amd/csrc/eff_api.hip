@@ -28,6 +28,8 @@ struct eff_ctx {
   eff_stats stats{};
   void *topk_scratch = nullptr;
   size_t topk_scratch_bytes = 0;
+  void *xh_scratch = nullptr;       // fp16 copy of the GEMM activations
+  size_t xh_scratch_bytes = 0;
 };
 
 struct eff_buf {
@@ -88,6 +90,7 @@ int weight_view(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint
   wv.bpr = bpr;
   wv.row_bytes = (uint64_t)bpr * g.bytes;
   wv.scales_off = 0;
+  wv.w_bytes = w->size + (w->owned ? kSlack : 16);  // wrapped buffers guarantee 16 readable bytes
   if (type == EFF_TYPE_Q8_0R) {
     if (w->mark_type != EFF_TYPE_Q8_0R)
       return fail(ctx, EFF_E_MARK, "%s Q8_0R: the buffer does not carry the mark of a repacked tensor "
@@ -118,8 +121,25 @@ int run_gemv(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint3
   return EFF_OK;
 }
 
+// Grow a context-owned scratch buffer (outside of any graph capture: the
+// first call of a shape must be eager).
+int grow(eff_ctx *ctx, void **p, size_t *have, size_t need, const char *what) {
+  if (need <= *have) return EFF_OK;
+  if (*p) {
+    EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    (void)hipFree(*p);
+    *p = nullptr;
+    *have = 0;
+  }
+  if (hipMalloc(p, need) != hipSuccess) return fail(ctx, EFF_E_NOMEM, "%s scratch of %zu bytes", what, need);
+  *have = need;
+  return EFF_OK;
+}
+
 int run_gemm(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
-  hipError_t e = launch_gemm(wv, x, y, tokens, ctx->stream);
+  int rc = grow(ctx, &ctx->xh_scratch, &ctx->xh_scratch_bytes, (size_t)2 * tokens * wv.k + 256, "gemm x");
+  if (rc) return rc;
+  hipError_t e = launch_gemm(wv, x, y, tokens, ctx->xh_scratch, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
   return EFF_OK;
 }
@@ -149,6 +169,7 @@ int eff_shutdown(eff_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->topk_scratch) (void)hipFree(ctx->topk_scratch);
+  if (ctx->xh_scratch) (void)hipFree(ctx->xh_scratch);
   if (ctx->own) (void)hipStreamDestroy(ctx->own);
   delete ctx;
   return EFF_OK;
@@ -364,7 +385,12 @@ int eff_dequant(eff_ctx *ctx, int type, eff_buf *w, eff_buf *out, uint32_t n_blo
   if ((uint64_t)n_blocks * g.elems * 4 > out->size) return fail(ctx, EFF_E_BOUNDS, "dequant: output buffer too small");
   int rc = use_device(ctx);
   if (rc) return rc;
-  hipError_t e = launch_dequant((const uint8_t *)w->ptr, type, scales_off, n_blocks, (float *)out->ptr, ctx->stream);
+  WeightView wv{};
+  wv.w = (const uint8_t *)w->ptr;
+  wv.type = type;
+  wv.scales_off = scales_off;
+  wv.w_bytes = w->size + (w->owned ? kSlack : 16);  // wrapped buffers guarantee 16 readable bytes
+  hipError_t e = launch_dequant(wv, n_blocks, (float *)out->ptr, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "dequant launch");
   ++ctx->stats.dequant;
   return EFF_OK;

@@ -14,15 +14,17 @@ struct WeightView {
   uint32_t rows, k, bpr;  // bpr = k / block_elems
   uint64_t row_bytes;     // bpr * block_bytes (GGUF layouts)
   uint64_t scales_off;    // Q8_0R: byte offset of the scale region (32 * N of the tensor)
+  uint64_t w_bytes;       // readable bytes from w (loads past it return 0)
 };
 
 // GEMV shape chosen by the host (see plan_gemv).
 struct GemvPlan {
   int rows_per_wave;  // R
-  int ksplit;         // waves of a workgroup that share rows and split k (1, 2, 4)
-  uint32_t kc;        // k elements of x staged in LDS per pass
+  int ksplit;         // S: waves of a workgroup splitting k (1, 2, 4); the tile has 4/S * R rows
+  uint32_t kc;        // k elements per slice
+  uint32_t tiles;     // row tiles
   uint32_t grid;      // workgroups
-  size_t lds_bytes;   // dynamic LDS
+  size_t lds_bytes;   // dynamic LDS (unused)
 };
 
 GemvPlan plan_gemv(const WeightView &wv, uint32_t tokens);
@@ -30,11 +32,11 @@ GemvPlan plan_gemv(const WeightView &wv, uint32_t tokens);
 hipError_t launch_gemv(const WeightView &wv, const float *x, float *y, uint32_t tokens,
                        const GemvPlan &p, hipStream_t stream);
 
-hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens,
+// x is first rounded to fp16 into `xh_scratch` (tokens * k halves).
+hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *xh_scratch,
                        hipStream_t stream);
 
-hipError_t launch_dequant(const uint8_t *w, int type, uint64_t scales_off, uint32_t n_blocks,
-                          float *out, hipStream_t stream);
+hipError_t launch_dequant(const WeightView &wv, uint32_t n_blocks, float *out, hipStream_t stream);
 
 // Top-k scratch: per chunk 2 u32 (count, flags) + 2 * kTopkChunkCap u32 (id, bits).
 constexpr uint32_t kTopkChunk = 4096;     // logits per chunk workgroup

@@ -33,29 +33,74 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
-// Loads. Blocks start at even byte offsets; 4-byte words are read aligned and
-// re-assembled with v_alignbyte. A read may touch up to 4 bytes past the end
-// of a block (the reference's loader leaves that slack, model.js:248-254).
-__device__ __forceinline__ uint32_t ld32(const uint8_t *p) {
-  return __builtin_nontemporal_load((const uint32_t *)p);
+// Loads go through buffer resources: a base address in SGPRs, 32-bit byte
+// offsets per lane with immediate displacements, and a byte count past which
+// reads return 0 (so no read can leave the buffer). Blocks start at even byte
+// offsets; 4-byte words are read aligned and re-assembled with v_alignbyte.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcFlags = 0x00020000;  // dword 3 of the buffer descriptor (gfx9 family)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint64_t bytes) {
+  const uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)n, kRsrcFlags);
 }
 
-__device__ __forceinline__ uint32_t ld_u16_a2(const uint8_t *p) {
-  uintptr_t a = (uintptr_t)p;
-  uint32_t w = __builtin_nontemporal_load((const uint32_t *)(a & ~(uintptr_t)3));
-  return (a & 2) ? (w >> 16) : (w & 0xFFFFu);
+__device__ __forceinline__ uint32_t ld32(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t ld_u16_a2(rsrc_t r, uint32_t off) {
+  const uint32_t w = ld32(r, off & ~3u);
+  return (off & 2u) ? (w >> 16) : (w & 0xFFFFu);
 }
 
 template <int N>
-__device__ __forceinline__ void ld_words_a2(const uint8_t *p, uint32_t *out) {
-  uintptr_t a = (uintptr_t)p;
-  const uint32_t *w = (const uint32_t *)(a & ~(uintptr_t)3);
-  uint32_t sh = (uint32_t)(a & 3);
+__device__ __forceinline__ void ld_words_a2(rsrc_t r, uint32_t off, uint32_t *out) {
+  const uint32_t base = off & ~3u, sh = off & 3u;
   uint32_t v[N + 1];
 #pragma unroll
-  for (int i = 0; i <= N; ++i) v[i] = __builtin_nontemporal_load(w + i);
+  for (int i = 0; i <= N; ++i) v[i] = ld32(r, base + 4u * i);
 #pragma unroll
   for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], sh);
+}
+
+// Where the blocks of a weight tile live: `q` covers the GGUF blocks (or the
+// Q8_0R quants) from the tile's first block on, `s` the Q8_0R scales.
+struct BufSrc {
+  rsrc_t q, s;
+};
+
+__device__ __forceinline__ BufSrc make_src(const WeightView &wv, uint64_t first_block) {
+  BufSrc src;
+  if (wv.type == Q8_0R) {
+    const uint64_t qo = 32ull * first_block, so = wv.scales_off + 2ull * first_block;
+    src.q = make_rsrc(wv.w + qo, wv.w_bytes > qo ? wv.w_bytes - qo : 0);
+    src.s = make_rsrc(wv.w + so, wv.w_bytes > so ? wv.w_bytes - so : 0);
+  } else {
+    const uint64_t bo = first_block * geometry(wv.type).bytes;
+    src.q = make_rsrc(wv.w + bo, wv.w_bytes > bo ? wv.w_bytes - bo : 0);
+    src.s = src.q;
+  }
+  return src;
+}
+
+// Sum over each 16-lane row with DPP; every lane of the row gets the sum.
+__device__ __forceinline__ float dpp_row_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  return v;
+}
+
+// Sum over the 64 lanes of the wave (wave-uniform result).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = dpp_row_sum(v);
+  const int iv = __builtin_bit_cast(int, v);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48)));
 }
 
 __device__ __forceinline__ float h2f(uint32_t h) {
@@ -115,52 +160,53 @@ __device__ __forceinline__ void unit_runs(uint32_t sub, uint32_t &o0, uint32_t &
   }
 }
 
-// Issue the loads of unit `sub` of block `bi` (bp = its first byte in the GGUF layouts).
+// Issue the loads of unit `sub` of block `bi` (counted from the first block of `src`).
 template <int TYPE>
-__device__ __forceinline__ void load_raw(Raw<TYPE> &r, const uint8_t *base, uint64_t bi, uint32_t sub,
-                                         uint64_t scales_off) {
+__device__ __forceinline__ void load_raw(Raw<TYPE> &r, const BufSrc &src, uint32_t bi, uint32_t sub) {
   if constexpr (TYPE == Q8_0) {
-    const uint8_t *bp = base + bi * 34u;
-    r.s = ld_u16_a2(bp);
-    ld_words_a2<8>(bp + 2, r.v);
+    const uint32_t bp = bi * 34u;
+    r.s = ld_u16_a2(src.q, bp);
+    ld_words_a2<8>(src.q, bp + 2u, r.v);
   } else if constexpr (TYPE == Q8_0R) {
-    const u32x4 *q = (const u32x4 *)(base + bi * 32u);
-    u32x4 a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    const u32x4v a = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)(bi * 32u), 0, 0);
+    const u32x4v b = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)(bi * 32u + 16u), 0, 0);
     r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
     r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
-    r.s = ld_u16_a2(base + scales_off + bi * 2u);
+    r.s = ld_u16_a2(src.s, bi * 2u);
   } else if constexpr (TYPE == Q4_K) {
-    const uint8_t *bp = base + bi * 144u;
-    u32x4 h = __builtin_nontemporal_load((const u32x4 *)bp);
-    u32x4 q = __builtin_nontemporal_load((const u32x4 *)(bp + 16u + 16u * sub));
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    const uint32_t bp = bi * 144u;
+    const u32x4v h = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)bp, 0, 0);
+    const u32x4v q = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)(bp + 16u + 16u * sub), 0, 0);
     r.hdr[0] = h.x; r.hdr[1] = h.y; r.hdr[2] = h.z; r.hdr[3] = h.w;
     r.qs[0] = q.x; r.qs[1] = q.y; r.qs[2] = q.z; r.qs[3] = q.w;
     r.sub = sub;
   } else if constexpr (TYPE == Q6_K) {
-    const uint8_t *bp = base + bi * 210u;
-    uint32_t n = sub >> 2, gp = (sub >> 1) & 1u, h = sub & 1u;
-    ld_words_a2<4>(bp + 16u * sub, r.ql);
-    ld_words_a2<4>(bp + 128u + 32u * n + 16u * h, r.qh);
+    const uint32_t bp = bi * 210u;
+    const uint32_t n = sub >> 2, gp = (sub >> 1) & 1u, h = sub & 1u;
+    ld_words_a2<4>(src.q, bp + 16u * sub, r.ql);
+    ld_words_a2<4>(src.q, bp + 128u + 32u * n + 16u * h, r.qh);
     // scales of groups gp and gp+2 at bytes 192 + 8n + 2g + h
-    const uint8_t *sp = bp + 192u + 8u * n + 2u * gp + h;
-    r.sc = (uint32_t)sp[0] | ((uint32_t)sp[4] << 8);
-    r.d = ld_u16_a2(bp + 208u);
+    const uint32_t so = bp + 192u + 8u * n + 2u * gp + h;
+    r.sc = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(src.q, (int)so, 0, 0) |
+           ((uint32_t)__builtin_amdgcn_raw_buffer_load_b8(src.q, (int)(so + 4u), 0, 0) << 8);
+    r.d = ld_u16_a2(src.q, bp + 208u);
     r.sub = sub;
   } else if constexpr (TYPE == Q2_K) {
-    const uint8_t *bp = base + bi * 84u;
-    uint32_t c = sub >> 1, jp = sub & 1u;
-    const uint8_t *qp = bp + 16u + 16u * c;
+    const uint32_t bp = bi * 84u;
+    const uint32_t c = sub >> 1, jp = sub & 1u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r.qs[i] = ld32(qp + 4 * i);
-    r.sc = ld32(bp + 8u * (c >> 1) + 4u * jp);
-    r.dd = ld32(bp + 80u);
+    for (int i = 0; i < 4; ++i) r.qs[i] = ld32(src.q, bp + 16u + 16u * c + 4u * i);
+    r.sc = ld32(src.q, bp + 8u * (c >> 1) + 4u * jp);
+    r.dd = ld32(src.q, bp + 80u);
     r.sub = sub;
   } else {
-    const uint8_t *bp = base + bi * 66u;
+    const uint32_t bp = bi * 66u;
     uint32_t a[2];
-    ld_words_a2<2>(bp + 2u + 8u * sub, a);
+    ld_words_a2<2>(src.q, bp + 2u + 8u * sub, a);
     r.a0 = a[0]; r.a1 = a[1];
-    r.d = ld_u16_a2(bp);
+    r.d = ld_u16_a2(src.q, bp);
   }
 }
 
@@ -325,17 +371,19 @@ __device__ __forceinline__ void stage_grid(uint32_t *grid) {
 // ---------------------------------------------------------------------------
 // Dequantization (test hook): one thread per unit.
 template <int TYPE>
-__global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ w, uint64_t scales_off,
-                                                 uint32_t n_blocks, float *__restrict__ out) {
+__global__ __launch_bounds__(256) void k_dequant(WeightView wv, uint32_t n_blocks, float *__restrict__ out) {
   __shared__ uint32_t grid[TYPE == IQ2_XXS ? 512 : 1];
   stage_grid<TYPE>(grid);
   if constexpr (TYPE == IQ2_XXS) __syncthreads();
+  constexpr uint32_t upb = units_per_block<TYPE>();
+  const uint64_t first = (uint64_t)blockIdx.x * 256u / upb;   // first block of this workgroup
+  const BufSrc src = make_src(wv, first);
   uint64_t gu = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gu >= (uint64_t)n_blocks * units_per_block<TYPE>()) return;
-  uint64_t bi = gu / units_per_block<TYPE>();
-  uint32_t sub = (uint32_t)(gu % units_per_block<TYPE>());
+  if (gu >= (uint64_t)n_blocks * upb) return;
+  uint64_t bi = gu / upb;
+  uint32_t sub = (uint32_t)(gu % upb);
   Raw<TYPE> r;
-  load_raw<TYPE>(r, w, bi, sub, scales_off);
+  load_raw<TYPE>(r, src, (uint32_t)(bi - first), sub);
   float v[32];
   dequant_unit<TYPE>(r, grid, v);
   uint32_t o0, o1;
@@ -351,32 +399,32 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ w, 
 // ---------------------------------------------------------------------------
 // GEMV: Y[t][row] = sum_k W[row][k] X[t][k], 1..8 tokens, f32 accumulation.
 //
-// A workgroup is 4 waves. `ksplit` waves share R rows and split the units of
-// k between them; the 4/ksplit groups take consecutive row groups. x is staged
-// in LDS (f32, a 4-float pad every 32 floats so that lanes reading
-// consecutive units hit different banks) in passes of `kc` elements.
-__device__ __forceinline__ uint32_t xpad(uint32_t k) { return k + (k >> 5) * 4u; }
-
+// A workgroup is 4 waves arranged as G = 4/S row groups x S slices of k. Each
+// wave owns R rows of its group and one slice of k; its lanes walk the units
+// of the slice, so each x value is loaded once per R rows (from the L1/L2
+// cache: x is small and read by every workgroup). The weight loads of a unit
+// are issued first. Slices of one row group are added in slice order through
+// LDS, so the result does not depend on scheduling.
 template <int TYPE, int T, int R>
 __global__ __launch_bounds__(256) void k_gemv(WeightView wv, const float *__restrict__ x,
-                                              float *__restrict__ y, uint32_t kc, int ksplit) {
-  extern __shared__ float smem[];
-  const uint32_t kcp = xpad(kc);
-  float *xs = smem;
-  float *red = smem + T * kcp;
-  uint32_t *grid = (uint32_t *)(red + 4 * R * T);
-
+                                              float *__restrict__ y, int S) {
+  __shared__ uint32_t grid[TYPE == IQ2_XXS ? 512 : 1];
+  __shared__ float red[4 * R * T];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int groups = 4 / ksplit;
-  const int grp = wave / ksplit, ks = wave % ksplit;
-  const uint32_t row0 = (blockIdx.x * groups + grp) * R;
+  const int G = 4 / S, g = wave / S, sl = wave % S;
   const uint32_t rows = wv.rows, k = wv.k;
+  const uint32_t trow0 = blockIdx.x * (uint32_t)(G * R);     // first row of the tile
+  const uint32_t row0 = trow0 + (uint32_t)(g * R);          // first row of this wave
 
-  stage_grid<TYPE>(grid);
+  if constexpr (TYPE == IQ2_XXS) {
+    stage_grid<TYPE>(grid);
+    __syncthreads();
+  }
+  const BufSrc src = make_src(wv, (uint64_t)trow0 * wv.bpr);
 
-  uint32_t rowi[R];
+  uint32_t lrow[R];  // row of the tile (clamped into the matrix)
 #pragma unroll
-  for (int r = 0; r < R; ++r) rowi[r] = min(row0 + (uint32_t)r, rows - 1u);
+  for (int r = 0; r < R; ++r) lrow[r] = min(row0 + (uint32_t)r, rows - 1u) - trow0;
 
   float acc[R][T];
 #pragma unroll
@@ -386,81 +434,106 @@ __global__ __launch_bounds__(256) void k_gemv(WeightView wv, const float *__rest
 
   constexpr uint32_t upb = units_per_block<TYPE>();
   constexpr uint32_t E = block_elems<TYPE>();
+  const uint32_t units = k / 32u;
+  const uint32_t ub = units / (uint32_t)S * (uint32_t)sl, ue = units / (uint32_t)S * (uint32_t)(sl + 1);
 
-  for (uint32_t k0 = 0; k0 < k; k0 += kc) {
-    const uint32_t klen = min(kc, k - k0);
-    __syncthreads();
-    for (uint32_t i = (uint32_t)tid * 4u; i < klen * T; i += 1024u) {
-      uint32_t t = i / klen, kk = i - t * klen;
-      float4 v = *(const float4 *)(x + (uint64_t)t * k + k0 + kk);
-      *(float4 *)(xs + t * kcp + xpad(kk)) = v;
-    }
-    __syncthreads();
-    const uint32_t units = klen / 32u;
-    const uint32_t ub = units * (uint32_t)ks / (uint32_t)ksplit;
-    const uint32_t ue = units * (uint32_t)(ks + 1) / (uint32_t)ksplit;
-    for (uint32_t u = ub + (uint32_t)lane; u < ue; u += 64u) {
-      const uint32_t gu = k0 / 32u + u;
-      const uint32_t b = gu / upb, sub = gu % upb;
-      uint32_t o0, o1;
-      unit_runs<TYPE>(sub, o0, o1);
-      const uint32_t kl0 = b * E + o0 - k0, kl1 = b * E + o1 - k0;
+  for (uint32_t gu = ub + (uint32_t)lane; gu < ue; gu += 64u) {
+    const uint32_t b = gu / upb, sub = gu % upb;
+    uint32_t o0, o1;
+    unit_runs<TYPE>(sub, o0, o1);
+    const uint32_t k0 = b * E + o0, k1 = b * E + o1;
 
-      Raw<TYPE> raw[R];
+    Raw<TYPE> raw[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r)
-        load_raw<TYPE>(raw[r], wv.w, (uint64_t)rowi[r] * wv.bpr + b, sub, wv.scales_off);
+    for (int r = 0; r < R; ++r) load_raw<TYPE>(raw[r], src, lrow[r] * wv.bpr + b, sub);
 
-      float ra[R][T], rb[R][T], sxa[T], sxb[T];
+    if constexpr (T <= 2) {
+      // Scales factored out of the unit: value = s*u - m per half.
+      float4 xa[T][4], xb[T][4];
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          xa[t][q] = *(const float4 *)(x + (uint64_t)t * k + k0 + 4 * q);
+          xb[t][q] = *(const float4 *)(x + (uint64_t)t * k + k1 + 4 * q);
+        }
+      float sxa[T], sxb[T];
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        sxa[t] = sxb[t] = 0.f;
+        float a = 0.f, bb = 0.f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) ra[r][t] = rb[r][t] = 0.f;
+        for (int q = 0; q < 4; ++q) {
+          a += (xa[t][q].x + xa[t][q].y) + (xa[t][q].z + xa[t][q].w);
+          bb += (xb[t][q].x + xb[t][q].y) + (xb[t][q].z + xb[t][q].w);
+        }
+        sxa[t] = a; sxb[t] = bb;
       }
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const uint32_t kl = q < 4 ? kl0 + 4u * q : kl1 + 4u * (q - 4);
-        float4 xv[T];
+      for (int r = 0; r < R; ++r) {
+        float ra[T], rb[T];
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-          xv[t] = *(const float4 *)(xs + t * kcp + xpad(kl));
-          float s = (xv[t].x + xv[t].y) + (xv[t].z + xv[t].w);
-          if (q < 4) sxa[t] += s; else sxb[t] += s;
-        }
+        for (int t = 0; t < T; ++t) ra[t] = rb[t] = 0.f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int q = 0; q < 8; ++q) {
           const uint32_t qb = quad<TYPE>(raw[r], q, grid);
           const float f0 = ubyte(qb, 0), f1 = ubyte(qb, 1), f2 = ubyte(qb, 2), f3 = ubyte(qb, 3);
 #pragma unroll
           for (int t = 0; t < T; ++t) {
-            float p = f0 * xv[t].x + f1 * xv[t].y + f2 * xv[t].z + f3 * xv[t].w;
-            if (q < 4) ra[r][t] += p; else rb[r][t] += p;
+            const float4 xv = q < 4 ? xa[t][q] : xb[t][q - 4];
+            float &a = q < 4 ? ra[t] : rb[t];
+            a = __builtin_fmaf(f0, xv.x, a);
+            a = __builtin_fmaf(f1, xv.y, a);
+            a = __builtin_fmaf(f2, xv.z, a);
+            a = __builtin_fmaf(f3, xv.w, a);
           }
         }
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
         float sA, sB, mA, mB;
         unit_scales<TYPE>(raw[r], sA, sB, mA, mB);
 #pragma unroll
-        for (int t = 0; t < T; ++t)
-          acc[r][t] += (sA * ra[r][t] + sB * rb[r][t]) - (mA * sxa[t] + mB * sxb[t]);
+        for (int t = 0; t < T; ++t) {
+          float v = acc[r][t];
+          v = __builtin_fmaf(sA, ra[t], v);
+          v = __builtin_fmaf(sB, rb[t], v);
+          v = __builtin_fmaf(-mA, sxa[t], v);
+          acc[r][t] = __builtin_fmaf(-mB, sxb[t], v);
+        }
+      }
+    } else {
+      // Many tokens: each weight is formed once (s*u - m) and used T times.
+      float sA[R], sB[R], mA[R], mB[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) unit_scales<TYPE>(raw[r], sA[r], sB[r], mA[r], mB[r]);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint32_t kq = q < 4 ? k0 + 4 * q : k1 + 4 * (q - 4);
+        float4 xv[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) xv[t] = *(const float4 *)(x + (uint64_t)t * k + kq);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint32_t qb = quad<TYPE>(raw[r], q, grid);
+          const float s = q < 4 ? sA[r] : sB[r], m = q < 4 ? mA[r] : mB[r];
+          const float w0 = __builtin_fmaf(s, ubyte(qb, 0), -m), w1 = __builtin_fmaf(s, ubyte(qb, 1), -m);
+          const float w2 = __builtin_fmaf(s, ubyte(qb, 2), -m), w3 = __builtin_fmaf(s, ubyte(qb, 3), -m);
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            float a = acc[r][t];
+            a = __builtin_fmaf(w0, xv[t].x, a);
+            a = __builtin_fmaf(w1, xv[t].y, a);
+            a = __builtin_fmaf(w2, xv[t].z, a);
+            acc[r][t] = __builtin_fmaf(w3, xv[t].w, a);
+          }
+        }
       }
     }
   }
 
-  // Reduce over the 64 lanes, then over the ksplit waves of the group.
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-      float v = acc[r][t];
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-      acc[r][t] = v;
-    }
-  if (ksplit == 1) {
+    for (int t = 0; t < T; ++t) acc[r][t] = wave_sum(acc[r][t]);
+
+  if (S == 1) {
     if (lane == 0) {
 #pragma unroll
       for (int r = 0; r < R; ++r)
@@ -477,38 +550,160 @@ __global__ __launch_bounds__(256) void k_gemv(WeightView wv, const float *__rest
       for (int t = 0; t < T; ++t) red[(wave * R + r) * T + t] = acc[r][t];
   }
   __syncthreads();
-  if (tid < groups * R * T) {
-    const int g = tid / (R * T), rt = tid % (R * T), r = rt / T, t = rt % T;
+  if (tid < G * R * T) {
+    const int gg = tid / (R * T), rt = tid % (R * T), r = rt / T, t = rt % T;
     float v = 0.f;
-    for (int s = 0; s < ksplit; ++s) v += red[((g * ksplit + s) * R + r) * T + t];
-    const uint32_t row = (blockIdx.x * groups + g) * R + r;
+    for (int q = 0; q < S; ++q) v += red[((gg * S + q) * R + r) * T + t];
+    const uint32_t row = trow0 + (uint32_t)(gg * R + r);
     if (row < rows) y[(uint64_t)t * rows + row] = v;
   }
 }
 
 // ---------------------------------------------------------------------------
 // GEMM: Y[t][row] = sum_k fp16(W[row][k]) fp16(X[t][k]), fp32 accumulation.
-// Workgroup tile 128 rows x 128 tokens, k steps of 256; 4 waves of 64x64, each
-// 2x2 MFMA 32x32x16 f16. The weight tile is dequantized (bit-exact f32, then
-// rounded to fp16) into LDS; x is rounded to fp16 into LDS.
-constexpr int GT = 128;         // tile rows / tokens
-constexpr int GK = 256;         // k step
+//
+// x is rounded to fp16 once by k_x_to_f16. A workgroup computes a tile of
+// 128 rows x 128 tokens in k steps of 128, with 4 waves of 64 x 64 (2 x 2
+// MFMA 32x32x16 f16 each). LDS holds two stages; the global loads of step
+// i+1 (raw weight units and fp16 x) are issued before the MFMAs of step i,
+// and decoded into the other stage afterwards, so one barrier per step.
+// Weights are dequantized to fp16: Q8_0/Q8_0R with packed fp16 arithmetic
+// (q exact, then one rounding of q*d, i.e. fp16(d*q)), the other types as
+// the bit-exact f32 value rounded to fp16.
+constexpr int GT = 128;         // tile rows = tile tokens
+constexpr int GK = 128;         // k step
 constexpr int GKP = GK + 8;     // padded LDS row (halves)
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__global__ __launch_bounds__(256) void k_x_to_f16(const float *__restrict__ x, _Float16 *__restrict__ xh,
+                                                  uint64_t n4) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (i >= n4) return;
+  const float4 v = *(const float4 *)(x + 4 * i);
+  const half4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+  *(half4 *)(xh + 4 * i) = h;
+}
+
+// 32 fp16 weights of a unit: out[0..15] half A, out[16..31] half B.
+template <int TYPE>
+__device__ __forceinline__ void unit_f16(const Raw<TYPE> &r, const uint32_t *grid, half8 *out) {
+  if constexpr (TYPE == Q8_0 || TYPE == Q8_0R) {
+    // q+128 as a byte -> fp16 1024+(q+128) by placing 0x64 above it, minus
+    // 1152 (exact), times d (one rounding).
+    const uint32_t magic = 0x64646464u;
+    const half2v d2 = {__builtin_bit_cast(_Float16, (uint16_t)r.s), __builtin_bit_cast(_Float16, (uint16_t)r.s)};
+    const half2v off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      half8 h;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t u = r.v[2 * i + j] ^ 0x80808080u;
+        const half2v lo = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(magic, u, 0x04010400u));
+        const half2v hi = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(magic, u, 0x04030402u));
+        const half2v a = (lo + off) * d2, b = (hi + off) * d2;
+        h[4 * j] = a.x; h[4 * j + 1] = a.y; h[4 * j + 2] = b.x; h[4 * j + 3] = b.y;
+      }
+      out[i] = h;
+    }
+  } else {
+    float v[32];
+    dequant_unit<TYPE>(r, grid, v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      half8 h;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = (_Float16)v[8 * i + j];
+      out[i] = h;
+    }
+  }
+}
 
 template <int TYPE>
-__global__ __launch_bounds__(256) void k_gemm(WeightView wv, const float *__restrict__ x,
-                                              float *__restrict__ y, uint32_t tokens) {
-  __shared__ _Float16 xs[GT * GKP];
-  __shared__ _Float16 ws[GT * GKP];
+__global__ __launch_bounds__(256) void k_gemm(WeightView wv, const _Float16 *__restrict__ xh,
+                                              float *__restrict__ y, uint32_t tokens, uint32_t row_tiles,
+                                              uint32_t tok_tiles) {
+  __shared__ _Float16 xs[2][GT * GKP];
+  __shared__ _Float16 ws[2][GT * GKP];
   __shared__ uint32_t grid[TYPE == IQ2_XXS ? 512 : 1];
   stage_grid<TYPE>(grid);
 
+  // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs;
+  // give each XCD a contiguous run of tiles, token tiles fastest, so the
+  // tiles sharing a weight slice share that XCD's L2.
+  const uint32_t ntiles = row_tiles * tok_tiles;
+  const uint32_t per_xcd = (ntiles + 7) / 8;
+  uint32_t lin = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (ntiles % 8 != 0 || lin >= ntiles) lin = blockIdx.x;  // uneven split: keep the plain order
+  const uint32_t n0 = (lin / tok_tiles) * GT, t0 = (lin % tok_tiles) * GT;
+
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const uint32_t n0 = blockIdx.x * GT, t0 = blockIdx.y * GT;
   const uint32_t rows = wv.rows, k = wv.k;
   const int wm = wave & 1, wn = wave >> 1;
   constexpr uint32_t upb = units_per_block<TYPE>();
   constexpr uint32_t E = block_elems<TYPE>();
+  const BufSrc src = make_src(wv, (uint64_t)n0 * wv.bpr);
+
+  // Work of each thread per step: 2 weight units (128 rows x 4 units) and
+  // 8 x chunks of 8 halves (128 tokens x 16 chunks).
+  constexpr int UNITS = GT * (GK / 32) / 256;
+  constexpr int XCH = GT * (GK / 8) / 256;
+  Raw<TYPE> raw[UNITS];
+  half8 xr[XCH];
+
+  auto load_step = [&](uint32_t kb) {
+    const uint32_t klen = min((uint32_t)GK, k - kb);
+#pragma unroll
+    for (int i = 0; i < UNITS; ++i) {
+      const int id = tid + 256 * i;
+      const int r = id / (GK / 32);
+      const uint32_t u = (uint32_t)(id % (GK / 32));
+      const uint32_t lrow = min(n0 + (uint32_t)r, rows - 1u) - n0;
+      const uint32_t gu = kb / 32u + min(u, klen / 32u - 1u);
+      load_raw<TYPE>(raw[i], src, lrow * wv.bpr + gu / upb, gu % upb);
+    }
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int id = tid + 256 * i;
+      const uint32_t t = (uint32_t)(id / (GK / 8)), c = (uint32_t)(id % (GK / 8));
+      const uint32_t tok = t0 + t, kk = 8u * c;
+      half8 h = {};
+      if (tok < tokens && kk < klen) h = *(const half8 *)(xh + (uint64_t)tok * k + kb + kk);
+      xr[i] = h;
+    }
+  };
+  auto store_step = [&](int buf, uint32_t kb) {
+    const uint32_t klen = min((uint32_t)GK, k - kb);
+#pragma unroll
+    for (int i = 0; i < UNITS; ++i) {
+      const int id = tid + 256 * i;
+      const int r = id / (GK / 32);
+      const uint32_t u = (uint32_t)(id % (GK / 32));
+      _Float16 *d = ws[buf] + r * GKP;
+      if (u >= klen / 32u) {
+        const half8 z = {};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *(half8 *)(d + 32 * u + 8 * j) = z;
+        continue;
+      }
+      const uint32_t gu = kb / 32u + u;
+      uint32_t o0, o1;
+      unit_runs<TYPE>(gu % upb, o0, o1);
+      const uint32_t c0 = (gu / upb) * E + o0 - kb, c1 = (gu / upb) * E + o1 - kb;
+      half8 h[4];
+      unit_f16<TYPE>(raw[i], grid, h);
+      *(half8 *)(d + c0) = h[0];
+      *(half8 *)(d + c0 + 8) = h[1];
+      *(half8 *)(d + c1) = h[2];
+      *(half8 *)(d + c1 + 8) = h[3];
+    }
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int id = tid + 256 * i;
+      const int t = id / (GK / 8), c = id % (GK / 8);
+      *(half8 *)(xs[buf] + t * GKP + 8 * c) = xr[i];
+    }
+  };
 
   float16v acc[2][2];
 #pragma unroll
@@ -518,61 +713,24 @@ __global__ __launch_bounds__(256) void k_gemm(WeightView wv, const float *__rest
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  for (uint32_t kb = 0; kb < k; kb += GK) {
-    const uint32_t klen = min((uint32_t)GK, k - kb);
-    __syncthreads();
-    // x tile -> fp16 (zero outside [tokens) x [k))
-    for (int i = tid; i < GT * (GK / 4); i += 256) {
-      const int t = i / (GK / 4), c = i % (GK / 4);
-      const uint32_t tok = t0 + t, kk = 4u * c;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (tok < tokens && kk < klen) v = *(const float4 *)(x + (uint64_t)tok * k + kb + kk);
-      half4 h4 = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
-      *(half4 *)(xs + t * GKP + kk) = h4;
-    }
-    // weight tile: 128 rows x (256/32) units
-    const uint32_t units = klen / 32u;
-    for (int i = tid; i < GT * 8; i += 256) {
-      const int r = i / 8;
-      const uint32_t u = (uint32_t)(i % 8);
-      _Float16 *d = ws + r * GKP;
-      if (u >= units) {
-        const half8 z = {};
+  const uint32_t steps = (k + GK - 1) / GK;
+  if constexpr (TYPE == IQ2_XXS) __syncthreads();  // grid staged
+  load_step(0);
+  store_step(0, 0);
+  __syncthreads();
+  for (uint32_t st = 0; st < steps; ++st) {
+    const int buf = st & 1;
+    const bool more = st + 1 < steps;
+    if (more) load_step((st + 1) * GK);
+    const _Float16 *xa = xs[buf], *wa = ws[buf];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) *(half8 *)(d + 32 * u + 8 * j) = z;
-        continue;
-      }
-      const uint32_t row = min(n0 + (uint32_t)r, rows - 1u);
-      const uint32_t gu = kb / 32u + u;
-      const uint32_t b = gu / upb, sub = gu % upb;
-      Raw<TYPE> raw;
-      load_raw<TYPE>(raw, wv.w, (uint64_t)row * wv.bpr + b, sub, wv.scales_off);
-      float v[32];
-      dequant_unit<TYPE>(raw, grid, v);
-      uint32_t o0, o1;
-      unit_runs<TYPE>(sub, o0, o1);
-      const uint32_t c0 = b * E + o0 - kb, c1 = b * E + o1 - kb;
-#pragma unroll
-      for (int j = 0; j < 16; j += 8) {
-        half8 ha, hb;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          ha[e] = (_Float16)v[j + e];
-          hb[e] = (_Float16)v[16 + j + e];
-        }
-        *(half8 *)(d + c0 + j) = ha;
-        *(half8 *)(d + c1 + j) = hb;
-      }
-    }
-    __syncthreads();
-#pragma unroll 4
     for (int kk = 0; kk < GK; kk += 16) {
       half8 a[2], bfr[2];
       const int kq = kk + 8 * (lane >> 5);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        a[i] = *(const half8 *)(xs + (64 * wm + 32 * i + (lane & 31)) * GKP + kq);
-        bfr[i] = *(const half8 *)(ws + (64 * wn + 32 * i + (lane & 31)) * GKP + kq);
+        a[i] = *(const half8 *)(xa + (64 * wm + 32 * i + (lane & 31)) * GKP + kq);
+        bfr[i] = *(const half8 *)(wa + (64 * wn + 32 * i + (lane & 31)) * GKP + kq);
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -580,6 +738,8 @@ __global__ __launch_bounds__(256) void k_gemm(WeightView wv, const float *__rest
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bfr[j], acc[i][j], 0, 0, 0);
     }
+    if (more) store_step(buf ^ 1, (st + 1) * GK);
+    __syncthreads();
   }
 
   // D[tok][row]: lane holds column (row) lane%32 and rows (tokens)
@@ -837,50 +997,42 @@ __global__ __launch_bounds__(256) void k_topk_final(const uint32_t *__restrict__
 
 GemvPlan plan_gemv(const WeightView &wv, uint32_t tokens) {
   GemvPlan p{};
-  p.rows_per_wave = tokens <= 2 ? 2 : 1;
-  // x budget in LDS: 48 KiB including the pad of 4 floats every 32
-  uint32_t kc = (uint32_t)(48u * 1024u / (4u * tokens) * 32u / 36u);
-  kc = kc / 256u * 256u;
-  if (kc == 0) kc = 256;
-  p.kc = wv.k <= kc ? wv.k : kc;
-  const uint32_t units = p.kc / 32u;
-  int ks = 1;
-  auto grid_for = [&](int s) {
-    uint32_t per = (uint32_t)p.rows_per_wave * (uint32_t)(4 / s);
-    return (wv.rows + per - 1) / per;
-  };
-  while (ks < 4 && grid_for(ks) < 1024u && units / (uint32_t)(2 * ks) >= 64u) ks *= 2;
-  p.ksplit = ks;
-  p.grid = grid_for(ks);
-  p.lds_bytes = sizeof(float) * ((size_t)tokens * (p.kc + p.kc / 8u) + 4u * p.rows_per_wave * tokens) +
-                (wv.type == IQ2_XXS ? 2048 : 0);
+  p.rows_per_wave = 4;
+  const uint32_t E = geometry(wv.type).elems;
+  // Split k over the 4 waves while row tiles alone give fewer than 512
+  // workgroups, keeping every slice a whole number of blocks and at least 64
+  // units (one per lane).
+  int S = 1;
+  auto tiles = [&](int s) { uint32_t per = (uint32_t)(4 / s) * (uint32_t)p.rows_per_wave; return (wv.rows + per - 1) / per; };
+  while (S < 4 && tiles(S) < 512u && wv.k % (uint32_t)(2 * S) == 0 && (wv.k / (uint32_t)(2 * S)) % E == 0 &&
+         wv.k / (uint32_t)(2 * S) >= 2048u)
+    S *= 2;
+  p.ksplit = S;
+  p.kc = wv.k / (uint32_t)S;
+  p.tiles = tiles(S);
+  p.grid = p.tiles;
+  p.lds_bytes = 0;
   return p;
 }
 
-template <int TYPE, int T, int R>
-static hipError_t gemv_go(const WeightView &wv, const float *x, float *y, const GemvPlan &p, hipStream_t s) {
-  hipLaunchKernelGGL((k_gemv<TYPE, T, R>), dim3(p.grid), dim3(256), p.lds_bytes, s, wv, x, y, p.kc, p.ksplit);
-  return hipGetLastError();
-}
-
 template <int TYPE, int T>
-static hipError_t gemv_r(const WeightView &wv, const float *x, float *y, const GemvPlan &p, hipStream_t s) {
-  if (p.rows_per_wave == 2) return gemv_go<TYPE, T, 2>(wv, x, y, p, s);
-  return gemv_go<TYPE, T, 1>(wv, x, y, p, s);
+static hipError_t gemv_go(const WeightView &wv, const float *x, float *y, const GemvPlan &p, hipStream_t s) {
+  hipLaunchKernelGGL((k_gemv<TYPE, T, 4>), dim3(p.grid), dim3(256), 0, s, wv, x, y, p.ksplit);
+  return hipGetLastError();
 }
 
 template <int TYPE>
 static hipError_t gemv_t(const WeightView &wv, const float *x, float *y, uint32_t tokens, const GemvPlan &p,
                          hipStream_t s) {
   switch (tokens) {
-    case 1: return gemv_go<TYPE, 1, 2>(wv, x, y, p, s);
-    case 2: return gemv_go<TYPE, 2, 2>(wv, x, y, p, s);
-    case 3: return gemv_go<TYPE, 3, 1>(wv, x, y, p, s);
-    case 4: return gemv_go<TYPE, 4, 1>(wv, x, y, p, s);
-    case 5: return gemv_go<TYPE, 5, 1>(wv, x, y, p, s);
-    case 6: return gemv_go<TYPE, 6, 1>(wv, x, y, p, s);
-    case 7: return gemv_go<TYPE, 7, 1>(wv, x, y, p, s);
-    case 8: return gemv_go<TYPE, 8, 1>(wv, x, y, p, s);
+    case 1: return gemv_go<TYPE, 1>(wv, x, y, p, s);
+    case 2: return gemv_go<TYPE, 2>(wv, x, y, p, s);
+    case 3: return gemv_go<TYPE, 3>(wv, x, y, p, s);
+    case 4: return gemv_go<TYPE, 4>(wv, x, y, p, s);
+    case 5: return gemv_go<TYPE, 5>(wv, x, y, p, s);
+    case 6: return gemv_go<TYPE, 6>(wv, x, y, p, s);
+    case 7: return gemv_go<TYPE, 7>(wv, x, y, p, s);
+    case 8: return gemv_go<TYPE, 8>(wv, x, y, p, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -899,41 +1051,47 @@ hipError_t launch_gemv(const WeightView &wv, const float *x, float *y, uint32_t 
 }
 
 template <int TYPE>
-static hipError_t gemm_go(const WeightView &wv, const float *x, float *y, uint32_t tokens, hipStream_t s) {
-  dim3 grid((wv.rows + GT - 1) / GT, (tokens + GT - 1) / GT);
-  hipLaunchKernelGGL((k_gemm<TYPE>), grid, dim3(256), 0, s, wv, x, y, tokens);
+static hipError_t gemm_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
+  const uint32_t row_tiles = (wv.rows + GT - 1) / GT, tok_tiles = (tokens + GT - 1) / GT;
+  hipLaunchKernelGGL((k_gemm<TYPE>), dim3(row_tiles * tok_tiles), dim3(256), 0, s, wv, xh, y, tokens, row_tiles,
+                     tok_tiles);
   return hipGetLastError();
 }
 
-hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, hipStream_t s) {
+hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *xh_scratch,
+                       hipStream_t s) {
+  const uint64_t n4 = (uint64_t)tokens * wv.k / 4;
+  _Float16 *xh = (_Float16 *)xh_scratch;
+  hipLaunchKernelGGL(k_x_to_f16, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, s, x, xh, n4);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   switch (wv.type) {
-    case Q8_0: return gemm_go<Q8_0>(wv, x, y, tokens, s);
-    case Q8_0R: return gemm_go<Q8_0R>(wv, x, y, tokens, s);
-    case Q4_K: return gemm_go<Q4_K>(wv, x, y, tokens, s);
-    case Q6_K: return gemm_go<Q6_K>(wv, x, y, tokens, s);
-    case Q2_K: return gemm_go<Q2_K>(wv, x, y, tokens, s);
-    case IQ2_XXS: return gemm_go<IQ2_XXS>(wv, x, y, tokens, s);
+    case Q8_0: return gemm_go<Q8_0>(wv, xh, y, tokens, s);
+    case Q8_0R: return gemm_go<Q8_0R>(wv, xh, y, tokens, s);
+    case Q4_K: return gemm_go<Q4_K>(wv, xh, y, tokens, s);
+    case Q6_K: return gemm_go<Q6_K>(wv, xh, y, tokens, s);
+    case Q2_K: return gemm_go<Q2_K>(wv, xh, y, tokens, s);
+    case IQ2_XXS: return gemm_go<IQ2_XXS>(wv, xh, y, tokens, s);
     default: return hipErrorInvalidValue;
   }
 }
 
 template <int TYPE>
-static hipError_t dequant_go(const uint8_t *w, uint64_t scales_off, uint32_t n_blocks, float *out, hipStream_t s) {
+static hipError_t dequant_go(const WeightView &wv, uint32_t n_blocks, float *out, hipStream_t s) {
   uint64_t units = (uint64_t)n_blocks * units_per_block<TYPE>();
   uint32_t grid = (uint32_t)((units + 255) / 256);
-  hipLaunchKernelGGL((k_dequant<TYPE>), dim3(grid), dim3(256), 0, s, w, scales_off, n_blocks, out);
+  hipLaunchKernelGGL((k_dequant<TYPE>), dim3(grid), dim3(256), 0, s, wv, n_blocks, out);
   return hipGetLastError();
 }
 
-hipError_t launch_dequant(const uint8_t *w, int type, uint64_t scales_off, uint32_t n_blocks, float *out,
-                          hipStream_t s) {
-  switch (type) {
-    case Q8_0: return dequant_go<Q8_0>(w, scales_off, n_blocks, out, s);
-    case Q8_0R: return dequant_go<Q8_0R>(w, scales_off, n_blocks, out, s);
-    case Q4_K: return dequant_go<Q4_K>(w, scales_off, n_blocks, out, s);
-    case Q6_K: return dequant_go<Q6_K>(w, scales_off, n_blocks, out, s);
-    case Q2_K: return dequant_go<Q2_K>(w, scales_off, n_blocks, out, s);
-    case IQ2_XXS: return dequant_go<IQ2_XXS>(w, scales_off, n_blocks, out, s);
+hipError_t launch_dequant(const WeightView &wv, uint32_t n_blocks, float *out, hipStream_t s) {
+  switch (wv.type) {
+    case Q8_0: return dequant_go<Q8_0>(wv, n_blocks, out, s);
+    case Q8_0R: return dequant_go<Q8_0R>(wv, n_blocks, out, s);
+    case Q4_K: return dequant_go<Q4_K>(wv, n_blocks, out, s);
+    case Q6_K: return dequant_go<Q6_K>(wv, n_blocks, out, s);
+    case Q2_K: return dequant_go<Q2_K>(wv, n_blocks, out, s);
+    case IQ2_XXS: return dequant_go<IQ2_XXS>(wv, n_blocks, out, s);
     default: return hipErrorInvalidValue;
   }
 }
