@@ -152,9 +152,9 @@ __device__ __forceinline__ void unit_runs(uint32_t sub, uint32_t &o0, uint32_t &
     // ql bytes 16*sub..: n = sub>>2, gp = (sub>>1)&1, h = sub&1
     o0 = 128u * (sub >> 2) + 32u * ((sub >> 1) & 1u) + 16u * (sub & 1u); o1 = o0 + 64u;
   } else if constexpr (TYPE == Q2_K) {
-    // qs chunk c = sub>>1 (n = c>>1, half = c&1), shifts j = 2jp, 2jp+1 with jp = sub&1
-    uint32_t c = sub >> 1;
-    o0 = 128u * (c >> 1) + 64u * (sub & 1u) + 16u * (c & 1u); o1 = o0 + 32u;
+    // sub = 4n + 2jp + half: qs chunk c = 2n + half at bit shifts j = 2jp, 2jp+1;
+    // consecutive pairs of units cover 64 consecutive weights
+    o0 = 128u * (sub >> 2) + 64u * ((sub >> 1) & 1u) + 16u * (sub & 1u); o1 = o0 + 32u;
   } else {
     o0 = 32u * sub; o1 = o0 + 16u;
   }
@@ -195,10 +195,10 @@ __device__ __forceinline__ void load_raw(Raw<TYPE> &r, const BufSrc &src, uint32
     r.sub = sub;
   } else if constexpr (TYPE == Q2_K) {
     const uint32_t bp = bi * 84u;
-    const uint32_t c = sub >> 1, jp = sub & 1u;
+    const uint32_t n = sub >> 2, jp = (sub >> 1) & 1u, c = 2u * n + (sub & 1u);
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.qs[i] = ld32(src.q, bp + 16u + 16u * c + 4u * i);
-    r.sc = ld32(src.q, bp + 8u * (c >> 1) + 4u * jp);
+    r.sc = ld32(src.q, bp + 8u * n + 4u * jp);
     r.dd = ld32(src.q, bp + 80u);
     r.sub = sub;
   } else {
@@ -211,15 +211,19 @@ __device__ __forceinline__ void load_raw(Raw<TYPE> &r, const BufSrc &src, uint32
 }
 
 // 6-bit (scale, min) pair `idx` of a Q4_K block (SCALE_MIN_K4, kernels.wgsl.js:94-104).
-__device__ __forceinline__ void q4k_scale_min(const uint32_t *hdr, uint32_t idx, uint32_t &sc, uint32_t &m) {
-  // scale bytes s[0..11] are bytes 4..15 of the block = hdr[1..3]
-  auto s = [&](uint32_t i) -> uint32_t { return (hdr[1 + (i >> 2)] >> (8u * (i & 3u))) & 0xFFu; };
+// s1, s2, s3 are the block's scale bytes 0-3, 4-7 and 8-11 as little-endian words.
+__device__ __forceinline__ void q4k_scale_min(uint32_t s1, uint32_t s2, uint32_t s3, uint32_t idx, uint32_t &sc,
+                                              uint32_t &m) {
+  const uint32_t sh = 8u * (idx & 3u);
   if (idx < 4) {
-    sc = s(idx) & 63u;
-    m = s(idx + 4) & 63u;
+    sc = (s1 >> sh) & 63u;
+    m = (s2 >> sh) & 63u;
   } else {
-    sc = (s(idx + 4) & 0xFu) | ((s(idx - 4) >> 6) << 4);
-    m = (s(idx + 4) >> 4) | ((s(idx) >> 6) << 4);
+    const uint32_t a = (s3 >> sh) & 0xFFu;   // byte idx + 4
+    const uint32_t b = (s1 >> sh) & 0xFFu;   // byte idx - 4
+    const uint32_t c = (s2 >> sh) & 0xFFu;   // byte idx
+    sc = (a & 0xFu) | ((b >> 6) << 4);
+    m = (a >> 4) | ((c >> 6) << 4);
   }
 }
 
@@ -236,7 +240,7 @@ __device__ __forceinline__ uint32_t quad(const Raw<TYPE> &r, int q, const uint32
     if (q < 4) return (r.ql[q] & 0x0F0F0F0Fu) | (((r.qh[q] >> (2u * gp)) & 0x03030303u) << 4);
     return ((r.ql[q - 4] >> 4) & 0x0F0F0F0Fu) | (((r.qh[q - 4] >> (2u * gp + 4u)) & 0x03030303u) << 4);
   } else if constexpr (TYPE == Q2_K) {
-    uint32_t jp = r.sub & 1u;
+    uint32_t jp = (r.sub >> 1) & 1u;
     return q < 4 ? ((r.qs[q] >> (4u * jp)) & 0x03030303u) : ((r.qs[q - 4] >> (4u * jp + 2u)) & 0x03030303u);
   } else {
     // entry l = q>>1 covers weights 8l..8l+7; this quad is its half (q&1)
@@ -262,9 +266,9 @@ __device__ __forceinline__ void unit_scales(const Raw<TYPE> &r, float &sA, float
   } else if constexpr (TYPE == Q4_K) {
     float d = h2f(r.hdr[0] & 0xFFFFu), dmin = h2f(r.hdr[0] >> 16);
     uint32_t j = r.sub >> 1, sc, m;
-    q4k_scale_min(r.hdr, 2u * j, sc, m);
+    q4k_scale_min(r.hdr[1], r.hdr[2], r.hdr[3], 2u * j, sc, m);
     sA = d * (float)sc; mA = dmin * (float)m;
-    q4k_scale_min(r.hdr, 2u * j + 1u, sc, m);
+    q4k_scale_min(r.hdr[1], r.hdr[2], r.hdr[3], 2u * j + 1u, sc, m);
     sB = d * (float)sc; mB = dmin * (float)m;
   } else if constexpr (TYPE == Q6_K) {
     float d = h2f(r.d);
@@ -273,7 +277,7 @@ __device__ __forceinline__ void unit_scales(const Raw<TYPE> &r, float &sA, float
     mA = 32.f * sA; mB = 32.f * sB;
   } else if constexpr (TYPE == Q2_K) {
     float d = h2f(r.dd & 0xFFFFu), dmin = h2f(r.dd >> 16);
-    uint32_t half = (r.sub >> 1) & 1u;
+    uint32_t half = r.sub & 1u;
     uint32_t scA = (r.sc >> (8u * half)) & 0xFFu, scB = (r.sc >> (8u * (half + 2u))) & 0xFFu;
     sA = d * (float)(scA & 0xFu); mA = dmin * (float)(scA >> 4);
     sB = d * (float)(scB & 0xFu); mB = dmin * (float)(scB >> 4);
@@ -299,9 +303,9 @@ __device__ __forceinline__ void dequant_unit(const Raw<TYPE> &r, const uint32_t 
     // d1 * q - m1 with d1 = d*sc, m1 = dmin*m (kernels.wgsl.js:233-249)
     float d = h2f(r.hdr[0] & 0xFFFFu), dmin = h2f(r.hdr[0] >> 16);
     uint32_t j = r.sub >> 1, sc, m;
-    q4k_scale_min(r.hdr, 2u * j, sc, m);
+    q4k_scale_min(r.hdr[1], r.hdr[2], r.hdr[3], 2u * j, sc, m);
     float d1 = d * (float)sc, m1 = dmin * (float)m;
-    q4k_scale_min(r.hdr, 2u * j + 1u, sc, m);
+    q4k_scale_min(r.hdr[1], r.hdr[2], r.hdr[3], 2u * j + 1u, sc, m);
     float d2 = d * (float)sc, m2 = dmin * (float)m;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -326,7 +330,7 @@ __device__ __forceinline__ void dequant_unit(const Raw<TYPE> &r, const uint32_t 
   } else if constexpr (TYPE == Q2_K) {
     // dl * q - ml with dl = d*(sc&15), ml = dmin*(sc>>4) (kernels.wgsl.js:202-221)
     float d = h2f(r.dd & 0xFFFFu), dmin = h2f(r.dd >> 16);
-    uint32_t half = (r.sub >> 1) & 1u, jp = r.sub & 1u;
+    uint32_t half = r.sub & 1u, jp = (r.sub >> 1) & 1u;
     uint32_t scA = (r.sc >> (8u * half)) & 0xFFu, scB = (r.sc >> (8u * (half + 2u))) & 0xFFu;
     float dlA = d * (float)(scA & 0xFu), mlA = dmin * (float)(scA >> 4);
     float dlB = d * (float)(scB & 0xFu), mlB = dmin * (float)(scB >> 4);
@@ -570,10 +574,10 @@ __global__ __launch_bounds__(256) void k_gemv(WeightView wv, const float *__rest
 // Weights are dequantized to fp16: Q8_0/Q8_0R with packed fp16 arithmetic
 // (q exact, then one rounding of q*d, i.e. fp16(d*q)), the other types as
 // the bit-exact f32 value rounded to fp16.
-constexpr int GT = 128;         // tile rows = tile tokens
-constexpr int GK = 128;         // k step
-constexpr int GKP = GK + 8;     // padded LDS row (halves)
+constexpr int GBM = 128;        // tile tokens
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+template <int TYPE> constexpr int gemm_bk() { return TYPE == Q6_K ? 128 : 64; }
 
 __global__ __launch_bounds__(256) void k_x_to_f16(const float *__restrict__ x, _Float16 *__restrict__ xh,
                                                   uint64_t n4) {
@@ -619,12 +623,19 @@ __device__ __forceinline__ void unit_f16(const Raw<TYPE> &r, const uint32_t *gri
   }
 }
 
-template <int TYPE>
+// Tile: GBM = 128 tokens x BN rows. The 4 waves form a WM x WN grid (WM*WN =
+// 4); each wave computes FM x FN MFMA 32x32 fragments.
+template <int TYPE, int BN, int WN>
 __global__ __launch_bounds__(256) void k_gemm(WeightView wv, const _Float16 *__restrict__ xh,
                                               float *__restrict__ y, uint32_t tokens, uint32_t row_tiles,
                                               uint32_t tok_tiles) {
-  __shared__ _Float16 xs[2][GT * GKP];
-  __shared__ _Float16 ws[2][GT * GKP];
+  constexpr int BK = gemm_bk<TYPE>();
+  constexpr int BKP = BK + 8;                 // padded LDS row (halves)
+  constexpr int WM = 4 / WN;
+  constexpr int FM = GBM / WM / 32, FN = BN / WN / 32;
+  static_assert(FM >= 1 && FN >= 1, "tile");
+  __shared__ _Float16 xs[2][GBM * BKP];
+  __shared__ _Float16 ws[2][BN * BKP];
   __shared__ uint32_t grid[TYPE == IQ2_XXS ? 512 : 1];
   stage_grid<TYPE>(grid);
 
@@ -632,32 +643,35 @@ __global__ __launch_bounds__(256) void k_gemm(WeightView wv, const _Float16 *__r
   // give each XCD a contiguous run of tiles, token tiles fastest, so the
   // tiles sharing a weight slice share that XCD's L2.
   const uint32_t ntiles = row_tiles * tok_tiles;
-  const uint32_t per_xcd = (ntiles + 7) / 8;
-  uint32_t lin = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-  if (ntiles % 8 != 0 || lin >= ntiles) lin = blockIdx.x;  // uneven split: keep the plain order
-  const uint32_t n0 = (lin / tok_tiles) * GT, t0 = (lin % tok_tiles) * GT;
+  uint32_t lin = blockIdx.x;
+  if (ntiles % 8 == 0) lin = (blockIdx.x % 8) * (ntiles / 8) + blockIdx.x / 8;
+  const uint32_t n0 = (lin / tok_tiles) * BN, t0 = (lin % tok_tiles) * GBM;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const uint32_t rows = wv.rows, k = wv.k;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % WM, wn = wave / WM;
   constexpr uint32_t upb = units_per_block<TYPE>();
   constexpr uint32_t E = block_elems<TYPE>();
   const BufSrc src = make_src(wv, (uint64_t)n0 * wv.bpr);
+  // fp16 x of this token tile; rows past `tokens` read as 0
+  const uint64_t xoff = (uint64_t)t0 * k;
+  const uint64_t xbytes = tokens > t0 ? (uint64_t)(tokens - t0) * k * 2u : 0;
+  const rsrc_t xsrc = make_rsrc(xh + xoff, xbytes);
 
-  // Work of each thread per step: 2 weight units (128 rows x 4 units) and
-  // 8 x chunks of 8 halves (128 tokens x 16 chunks).
-  constexpr int UNITS = GT * (GK / 32) / 256;
-  constexpr int XCH = GT * (GK / 8) / 256;
+  constexpr int UNITS_ALL = BN * (BK / 32);                   // weight units per step
+  constexpr int UNITS = (UNITS_ALL + 255) / 256;
+  constexpr int XCH = GBM * (BK / 8) / 256;                    // 8-half x chunks per thread
   Raw<TYPE> raw[UNITS];
   half8 xr[XCH];
 
   auto load_step = [&](uint32_t kb) {
-    const uint32_t klen = min((uint32_t)GK, k - kb);
+    const uint32_t klen = min((uint32_t)BK, k - kb);
 #pragma unroll
     for (int i = 0; i < UNITS; ++i) {
       const int id = tid + 256 * i;
-      const int r = id / (GK / 32);
-      const uint32_t u = (uint32_t)(id % (GK / 32));
+      if (UNITS_ALL % 256 != 0 && id >= UNITS_ALL) break;
+      const int r = id / (BK / 32);
+      const uint32_t u = (uint32_t)(id % (BK / 32));
       const uint32_t lrow = min(n0 + (uint32_t)r, rows - 1u) - n0;
       const uint32_t gu = kb / 32u + min(u, klen / 32u - 1u);
       load_raw<TYPE>(raw[i], src, lrow * wv.bpr + gu / upb, gu % upb);
@@ -665,21 +679,23 @@ __global__ __launch_bounds__(256) void k_gemm(WeightView wv, const _Float16 *__r
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
       const int id = tid + 256 * i;
-      const uint32_t t = (uint32_t)(id / (GK / 8)), c = (uint32_t)(id % (GK / 8));
-      const uint32_t tok = t0 + t, kk = 8u * c;
-      half8 h = {};
-      if (tok < tokens && kk < klen) h = *(const half8 *)(xh + (uint64_t)tok * k + kb + kk);
-      xr[i] = h;
+      const uint32_t t = (uint32_t)(id / (BK / 8)), c = (uint32_t)(id % (BK / 8));
+      const uint32_t kk = 8u * c;
+      // past k: an offset beyond the descriptor, which reads 0
+      const uint32_t off = kk < klen ? (t * k + kb + kk) * 2u : 0xFFFFFFF0u;
+      typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+      xr[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)off, 0, 0));
     }
   };
   auto store_step = [&](int buf, uint32_t kb) {
-    const uint32_t klen = min((uint32_t)GK, k - kb);
+    const uint32_t klen = min((uint32_t)BK, k - kb);
 #pragma unroll
     for (int i = 0; i < UNITS; ++i) {
       const int id = tid + 256 * i;
-      const int r = id / (GK / 32);
-      const uint32_t u = (uint32_t)(id % (GK / 32));
-      _Float16 *d = ws[buf] + r * GKP;
+      if (UNITS_ALL % 256 != 0 && id >= UNITS_ALL) break;
+      const int r = id / (BK / 32);
+      const uint32_t u = (uint32_t)(id % (BK / 32));
+      _Float16 *d = ws[buf] + r * BKP;
       if (u >= klen / 32u) {
         const half8 z = {};
 #pragma unroll
@@ -700,20 +716,20 @@ __global__ __launch_bounds__(256) void k_gemm(WeightView wv, const _Float16 *__r
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
       const int id = tid + 256 * i;
-      const int t = id / (GK / 8), c = id % (GK / 8);
-      *(half8 *)(xs[buf] + t * GKP + 8 * c) = xr[i];
+      const int t = id / (BK / 8), c = id % (BK / 8);
+      *(half8 *)(xs[buf] + t * BKP + 8 * c) = xr[i];
     }
   };
 
-  float16v acc[2][2];
+  float16v acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  const uint32_t steps = (k + GK - 1) / GK;
+  const uint32_t steps = (k + BK - 1) / BK;
   if constexpr (TYPE == IQ2_XXS) __syncthreads();  // grid staged
   load_step(0);
   store_step(0, 0);
@@ -721,37 +737,36 @@ __global__ __launch_bounds__(256) void k_gemm(WeightView wv, const _Float16 *__r
   for (uint32_t st = 0; st < steps; ++st) {
     const int buf = st & 1;
     const bool more = st + 1 < steps;
-    if (more) load_step((st + 1) * GK);
+    if (more) load_step((st + 1) * BK);
     const _Float16 *xa = xs[buf], *wa = ws[buf];
 #pragma unroll
-    for (int kk = 0; kk < GK; kk += 16) {
-      half8 a[2], bfr[2];
+    for (int kk = 0; kk < BK; kk += 16) {
+      half8 a[FM], bfr[FN];
       const int kq = kk + 8 * (lane >> 5);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        a[i] = *(const half8 *)(xa + (64 * wm + 32 * i + (lane & 31)) * GKP + kq);
-        bfr[i] = *(const half8 *)(wa + (64 * wn + 32 * i + (lane & 31)) * GKP + kq);
-      }
+      for (int i = 0; i < FM; ++i) a[i] = *(const half8 *)(xa + ((wm * FM + i) * 32 + (lane & 31)) * BKP + kq);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < FN; ++j) bfr[j] = *(const half8 *)(wa + ((wn * FN + j) * 32 + (lane & 31)) * BKP + kq);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bfr[j], acc[i][j], 0, 0, 0);
     }
-    if (more) store_step(buf ^ 1, (st + 1) * GK);
+    if (more) store_step(buf ^ 1, (st + 1) * BK);
     __syncthreads();
   }
 
   // D[tok][row]: lane holds column (row) lane%32 and rows (tokens)
-  // 8*(v/4) + 4*(lane/32) + v%4 of each 32x32 tile.
+  // 8*(v/4) + 4*(lane/32) + v%4 of each 32x32 fragment.
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t row = n0 + 64 * wn + 32 * j + (lane & 31);
+    for (int j = 0; j < FN; ++j) {
+      const uint32_t row = n0 + (wn * FN + j) * 32 + (lane & 31);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const uint32_t tok = t0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const uint32_t tok = t0 + (wm * FM + i) * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         if (row < rows && tok < tokens) y[(uint64_t)tok * rows + row] = acc[i][j][v];
       }
     }
@@ -1052,9 +1067,19 @@ hipError_t launch_gemv(const WeightView &wv, const float *x, float *y, uint32_t 
 
 template <int TYPE>
 static hipError_t gemm_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
-  const uint32_t row_tiles = (wv.rows + GT - 1) / GT, tok_tiles = (tokens + GT - 1) / GT;
-  hipLaunchKernelGGL((k_gemm<TYPE>), dim3(row_tiles * tok_tiles), dim3(256), 0, s, wv, xh, y, tokens, row_tiles,
-                     tok_tiles);
+  const uint32_t tok_tiles = (tokens + GBM - 1) / GBM;
+  // Wide tiles (128 rows) when they give at least one workgroup per CU,
+  // else narrow tiles (32 rows) to spread small problems over the GPU.
+  const uint32_t wide = (wv.rows + 127) / 128 * tok_tiles;
+  if (wide >= 256) {
+    const uint32_t row_tiles = (wv.rows + 127) / 128;
+    hipLaunchKernelGGL((k_gemm<TYPE, 128, 2>), dim3(row_tiles * tok_tiles), dim3(256), 0, s, wv, xh, y, tokens,
+                       row_tiles, tok_tiles);
+  } else {
+    const uint32_t row_tiles = (wv.rows + 31) / 32;
+    hipLaunchKernelGGL((k_gemm<TYPE, 32, 1>), dim3(row_tiles * tok_tiles), dim3(256), 0, s, wv, xh, y, tokens,
+                       row_tiles, tok_tiles);
+  }
   return hipGetLastError();
 }
 
