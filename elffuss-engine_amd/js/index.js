@@ -1,0 +1,349 @@
+'use strict';
+// JavaScript host of the MI355X quantized matrix-product path: the operator
+// objects of Elffuss Engine (createQuantOps, createGemvOps, createGemm2Ops,
+// createTopKGPU) and the repack helpers of repack.js / kernels.bloques.wgsl.js,
+// with the same call shapes, over the N-API addon (elffuss_amd.node) and the
+// C ABI of include/elffuss_amd.h. A drop-in for device.js's WebGPU buffers
+// and dispatches on this path only.
+//
+// Semantics kept from the reference:
+//   * operations record work and return without waiting (ops.js:667-710); the
+//     Promises they return resolve once the launch is enqueued, and only
+//     readback() waits for the device (device.js:165-200);
+//   * a fast path that does not apply returns null and the caller falls back
+//     (ops.gemv.js:13-21, ops.gemm2.js:5-8);
+//   * contract violations throw an Error (ops.js:767-771, 850-852;
+//     repack.js:268-286) — here with the library's message and a `code`.
+// Written for Node >= 12 (ES2019, CommonJS).
+
+const path = require('path');
+
+const native = require(path.join(__dirname, 'elffuss_amd.node'));
+
+const STATUS = { NOT_APPLICABLE: 1, E_INVALID: -1, E_TYPE: -2, E_SHAPE: -3, E_MARK: -4, E_BOUNDS: -5, E_DEVICE: -6 };
+const OPT = { GEMV_MAX_TOKENS: 1, GEMM_MIN_TOKENS: 2 };
+const TOPK = { M_MAX: 192, P_MAX: 128, CAP: 256, CABECERA: 8, N_MAX: 1 << 24, POR_TROZO: 4096 };
+
+// ---- types (gguf.js:51-64, kernels.wgsl.js QUANT_TYPES) --------------------
+const TYPE_NAMES = ['Q8_0', 'Q8_0R', 'Q4_K', 'Q6_K', 'Q2_K', 'IQ2_XXS'];
+const QUANT_TYPES = {};
+for (const name of TYPE_NAMES) {
+  const code = native.typeFromName(name);
+  const g = native.geometry(code);
+  QUANT_TYPES[name] = { name, code, blockElems: g.blockElems, blockBytes: g.blockBytes,
+    table: name === 'IQ2_XXS' ? 'IQ2XXS' : null };
+}
+
+function quantInfo(type) {
+  const i = QUANT_TYPES[type];
+  if (!i) {
+    const e = new Error(`tipo de cuantización no soportado: «${type}»`);
+    e.code = STATUS.E_TYPE;
+    throw e;
+  }
+  return i;
+}
+
+// ---- device and buffers (device.js / ops.js ctx) ----------------------------
+
+class DeviceBuffer {
+  constructor(device, size, label) {
+    this.device = device;
+    this.size = size;
+    this.label = label || '';
+    this._h = native.bufAlloc(device._ctx, size);
+    this._alive = true;
+  }
+  destroy() {
+    if (this._alive) {
+      native.bufFree(this.device._ctx, this._h);
+      this._alive = false;
+    }
+  }
+}
+
+// The HIP device context standing in for requestDevice() (device.js:66-139).
+function requestDevice(opts) {
+  const o = opts || {};
+  const ctx = native.init(o.device || 0);
+  const device = {
+    _ctx: ctx,
+    features: new Set(['shader-f16']),
+    limits: { maxStorageBufferBindingSize: 2 ** 32, maxComputeWorkgroupStorageSize: 163840 },
+    createBuffer(desc) {
+      return new DeviceBuffer(device, desc.size, desc.label);
+    },
+    queue: {
+      // queue.writeBuffer(buffer, offset, data[, dataOffset, size])
+      writeBuffer(buf, offset, data, dataOffset, size) {
+        let view = data;
+        if (dataOffset !== undefined || size !== undefined) {
+          const bytes = ArrayBuffer.isView(data)
+            ? new Uint8Array(data.buffer, data.byteOffset, data.byteLength) : new Uint8Array(data);
+          const el = ArrayBuffer.isView(data) && data.BYTES_PER_ELEMENT ? data.BYTES_PER_ELEMENT : 1;
+          const start = (dataOffset || 0) * el;
+          const len = size !== undefined ? size * el : bytes.byteLength - start;
+          view = bytes.subarray(start, start + len);
+        }
+        native.bufWrite(ctx, buf._h, offset, view);
+      },
+      onSubmittedWorkDone() {
+        native.sync(ctx);
+        return Promise.resolve();
+      },
+    },
+    setOption(option, value) {
+      native.setOption(ctx, option, value);
+    },
+    stats() {
+      return native.stats(ctx);
+    },
+    destroy() {
+      native.shutdown(ctx);
+    },
+  };
+  return Promise.resolve(device);
+}
+
+// Device -> host copy; waits for the work enqueued before it (device.js:165).
+function readback(device, buf, offset, size) {
+  const off = offset || 0;
+  const n = size === undefined ? buf.size - off : size;
+  return native.bufReadAsync(device._ctx, buf._h, off, n);
+}
+
+// The ops context: allocations live until recycle() (ops.js:233-307).
+function createContext(device) {
+  const scratch = [];
+  return {
+    device,
+    scratch,
+    alloc(bytes, label) {
+      const b = device.createBuffer({ size: Math.max(4, Math.ceil(bytes / 256) * 256), label });
+      scratch.push(b);
+      return b;
+    },
+    recycle() {
+      for (const b of scratch.splice(0)) b.destroy();
+    },
+  };
+}
+
+// ---- repacked layout (repack.js, kernels.bloques.wgsl.js) ---------------------
+
+const TIPOS_R = new Set(['Q8_0R']);
+const TIPO_R = Object.freeze({ Q8_0: 'Q8_0R' });
+const TIPO_GGUF = Object.freeze({ Q8_0R: 'Q8_0' });
+const R_CODE = QUANT_TYPES.Q8_0R.code;
+
+function checkR(tipo, what) {
+  if (tipo !== 'Q8_0R' && tipo !== 'Q8_0') throw new Error(`${what}: tipo sin formato reordenado: «${tipo}»`);
+}
+function bytesReordenado(tipo, nBloques) { checkR(tipo, 'bytesReordenado'); return native.bufferMath(0, R_CODE, nBloques); }
+function bytesBufferR(tipo, nBloques) { checkR(tipo, 'bytesBufferR'); return native.bufferMath(1, R_CODE, nBloques); }
+function bloquesDeBuffer(tipo, bytes) { checkR(tipo, 'bloquesDeBuffer'); return native.bufferMath(2, R_CODE, bytes); }
+function escalasDesde(tipo, nBloques) { checkR(tipo, 'escalasDesde'); return native.bufferMath(3, R_CODE, nBloques); }
+
+// reordena (repack.js:187-199): Q8_0 GGUF bytes -> Q8_0R, into `dst` if given.
+function reordena(tipo, src, nBloques, dst) {
+  checkR(tipo, 'reordena');
+  const need = bytesReordenado(tipo, nBloques);
+  if (dst && dst.byteLength < need) throw new Error(`reordena: el destino mide ${dst.byteLength} y hacen falta ${need}`);
+  const out = native.repack(R_CODE, src, nBloques, dst ? dst.byteLength : bytesBufferR(tipo, nBloques));
+  if (dst) { new Uint8Array(dst.buffer, dst.byteOffset, dst.byteLength).set(out); return dst; }
+  return out;
+}
+
+// vuelveAlGGUF (repack.js:204-219).
+function vuelveAlGGUF(tipo, src, nBloques) {
+  checkR(tipo, 'vuelveAlGGUF');
+  return native.unrepack(R_CODE, src, nBloques);
+}
+
+// marcaBufferR (repack.js:241-251): the mark lives with the device buffer.
+function marcaBufferR(buf, tipoR, nBloques) {
+  if (!TIPOS_R.has(tipoR)) throw new Error(`marcaBufferR: «${tipoR}» no es un tipo reordenado`);
+  if (!(nBloques > 0) || nBloques % 1 !== 0) throw new Error(`marcaBufferR: número de bloques inválido: ${nBloques}`);
+  const esperado = bytesBufferR(tipoR, nBloques);
+  if (buf.size !== esperado || native.bufMarkR(buf._h, R_CODE, nBloques) !== 0) {
+    throw new Error(`marcaBufferR: «${buf.label || '?'}» mide ${buf.size} bytes y un ${tipoR} de ` +
+      `${nBloques} bloques tiene que medir ${esperado}`);
+  }
+  return buf;
+}
+
+// bloquesR (repack.js:256-259).
+function bloquesR(buf) {
+  return native.bufBlocksR(buf._h);
+}
+
+// compruebaBufferR (repack.js:268-286).
+function compruebaBufferR(tipo, buf, opts, que) {
+  const o = opts || {};
+  const bloques = o.bloques || 0, porFila = o.porFila || 0;
+  const q = que || 'lector';
+  const n = bloquesR(buf);
+  if (n === undefined) {
+    throw new Error(`${q} ${tipo}: el buffer «${buf.label || '?'}» no lleva la marca de un tensor reordenado`);
+  }
+  if (!TIPOS_R.has(tipo)) throw new Error(`${q}: el buffer «${buf.label || '?'}» guarda un Q8_0R y se iba a leer como ${tipo}`);
+  if (bloques > n) throw new Error(`${q} ${tipo}: la llamada lee ${bloques} bloques y el tensor de «${buf.label || '?'}» tiene ${n}`);
+  if (porFila > 0 && n % porFila !== 0) throw new Error(`${q} ${tipo}: el tensor (${n} bloques) no son filas enteras de ${porFila} bloques`);
+  return n;
+}
+
+// creaBufferR (repack.js:293-306).
+function creaBufferR(device, t, tipoR) {
+  const nBloques = t.nElements / 32;
+  const buf = device.createBuffer({ size: bytesBufferR(tipoR, nBloques), label: t.name });
+  return marcaBufferR(buf, tipoR, nBloques);
+}
+
+// ---- operators ---------------------------------------------------------------
+
+// createGemvOps (ops.gemv.js:44-221): the decode GEMV, null when it does not apply.
+function createGemvOps(device, deps) {
+  const ctx = deps.ctx;
+  const hechos = { matmul: 0 };
+  return {
+    matmul(tipo, wBuf, xBuf, rows, k, tokens) {
+      const t = tokens === undefined ? 1 : tokens;
+      const i = QUANT_TYPES[tipo];
+      if (!i || !(t >= 1) || k % i.blockElems !== 0) return Promise.resolve(null);
+      const y = ctx.alloc(rows * t * 4, 'matmul.y');
+      const r = native.qgemv(device._ctx, i.code, wBuf._h, xBuf._h, y._h, rows, k, t);
+      if (r === null) return Promise.resolve(null);
+      hechos.matmul++;
+      return Promise.resolve(y);
+    },
+    despachados() { return Object.assign({}, hechos); },
+    rechazados() { return []; },
+  };
+}
+
+// createGemm2Ops (ops.gemm2.js:259-303): the prefill GEMM, null when it does not apply.
+function createGemm2Ops(ctx) {
+  const device = ctx.device;
+  return {
+    plan(type, rows, k, tokens) {
+      const i = QUANT_TYPES[type];
+      const min = 64;
+      if (!i || k % 32 !== 0 || !(tokens >= min)) return null;
+      return { via: 'mfma-f16', type, bpr: k / i.blockElems };
+    },
+    olvida() {},
+    matmul(type, wBuf, xBuf, rows, k, tokens) {
+      const i = QUANT_TYPES[type];
+      if (!i) return Promise.resolve(null);
+      const y = ctx.alloc(rows * tokens * 4, 'matmul.y');
+      const r = native.qgemm(device._ctx, i.code, wBuf._h, xBuf._h, y._h, rows, k, tokens);
+      return Promise.resolve(r === null ? null : y);
+    },
+    reproducible(type, rows, k, lote) { return this.plan(type, rows, k, lote) !== null; },
+    // The last-layer tail: one token computed with the plan of the whole batch.
+    cola(type, wBuf, x1, rows, k, lote) {
+      if (!this.reproducible(type, rows, k, lote)) return Promise.resolve(null);
+      const i = QUANT_TYPES[type];
+      device.setOption(OPT.GEMM_MIN_TOKENS, 1);
+      try {
+        const y = ctx.alloc(rows * 4, 'matmul.y');
+        native.qgemm(device._ctx, i.code, wBuf._h, x1._h, y._h, rows, k, 1);
+        return Promise.resolve(y);
+      } finally {
+        device.setOption(OPT.GEMM_MIN_TOKENS, 64);
+      }
+    },
+  };
+}
+
+// createQuantOps (ops.js:748-1142).
+function createQuantOps(device, opts) {
+  const o = opts || {};
+  const ctx = o.ctx || createContext(device);
+  const gemv = createGemvOps(device, { ctx });
+  const gemm2 = createGemm2Ops(ctx);
+  return {
+    // Whole tensor -> f32, bit-exact with the reference decoders (ops.js:813-823).
+    dequant(type, wBuf, nBlocks) {
+      const i = quantInfo(type);
+      if (TIPOS_R.has(type)) compruebaBufferR(type, wBuf, { bloques: nBlocks }, 'dequant');
+      const out = ctx.alloc(nBlocks * i.blockElems * 4, 'dequant.out');
+      native.dequant(device._ctx, i.code, wBuf._h, out._h, nBlocks);
+      return Promise.resolve(out);
+    },
+    // Y[tokens][rows] = W . X (ops.js:827-1101); throws when k is not a
+    // multiple of the block, or for an unmarked repacked buffer.
+    matmul(type, wBuf, xBuf, rows, k, tokens) {
+      const t = tokens === undefined ? 1 : tokens;
+      const i = quantInfo(type);
+      if (k % i.blockElems !== 0) throw new Error(`matmul ${type}: k=${k} no es múltiplo de ${i.blockElems}`);
+      if (TIPOS_R.has(type)) compruebaBufferR(type, wBuf, { bloques: rows * (k / i.blockElems) }, 'matmul');
+      const y = ctx.alloc(rows * t * 4, 'matmul.y');
+      native.qmatmul(device._ctx, i.code, wBuf._h, xBuf._h, y._h, rows, k, t);
+      return Promise.resolve(y);
+    },
+    // The IQ2_XXS grid is part of the library (no upload needed).
+    prepare(types) {
+      for (const t of new Set(types)) quantInfo(t);
+      return Promise.resolve();
+    },
+    upload(array, label) {
+      const buf = ctx.alloc(array.byteLength, label || 'x');
+      device.queue.writeBuffer(buf, 0, array);
+      return buf;
+    },
+    ctx,
+    gemv,
+    gemm2,
+  };
+}
+
+// createTopKGPU (ops.topk.js:42-190): candidatos() returns the exact top-M by
+// (value desc, index asc) of one logits vector plus the raw logits of the
+// penalised ids, or null when the device result must not be used.
+const estadisticasTopK = { gpu: 0, respaldo: 0, motivos: {} };
+
+function createTopKGPU(device, ctx) {
+  const out = device.createBuffer({ size: native.topkOutBytes(), label: 'topk.out' });
+  let serie = 0;
+  const stats = { gpu: 0, respaldo: 0, motivos: {} };
+  const respaldo = (motivo) => {
+    for (const s of [stats, estadisticasTopK]) {
+      s.respaldo++;
+      s.motivos[motivo] = (s.motivos[motivo] || 0) + 1;
+    }
+    return null;
+  };
+  async function candidatos(logits, base, vocab, plan) {
+    if (vocab >= TOPK.N_MAX) return respaldo('vocabulario');
+    serie = ((serie + 1) >>> 0) || 1;
+    const esta = serie;
+    const S = plan.S || new Uint32Array(0);
+    const r = native.topk(device._ctx, logits._h, base, vocab, plan.M, S, esta, out._h);
+    if (r === null) return respaldo('no aplica');
+    const u = new Uint32Array(await readback(device, out, 0, out.size));
+    if (u[4] !== esta) return respaldo('serie');
+    if (u[1] !== 0) return respaldo(u[1] & 2 ? 'NaN' : 'no cupo');
+    const n = u[0];
+    const ini = TOPK.CABECERA + TOPK.P_MAX;
+    const ids = new Uint32Array(n), bits = new Uint32Array(n);
+    for (let q = 0; q < n; q++) { ids[q] = u[ini + 2 * q]; bits[q] = u[ini + 2 * q + 1]; }
+    stats.gpu++; estadisticasTopK.gpu++;
+    return { ids, bits, bitsS: u.slice(TOPK.CABECERA, TOPK.CABECERA + S.length) };
+  }
+  return {
+    stats,
+    candidatos,
+    destroy() { out.destroy(); },
+  };
+}
+
+module.exports = {
+  native, STATUS, OPT, TOPK, QUANT_TYPES, quantInfo,
+  requestDevice, readback, createContext,
+  createQuantOps, createGemvOps, createGemm2Ops, createTopKGPU, estadisticasTopK,
+  TIPOS_R, TIPO_R, TIPO_GGUF, bytesReordenado, bytesBufferR, bloquesDeBuffer, escalasDesde,
+  reordena, vuelveAlGGUF, marcaBufferR, bloquesR, compruebaBufferR, creaBufferR,
+  quantize: (type, f32) => native.quantize(quantInfo(type).code, f32),
+  fillNormal: (seed, sigma, n) => native.fillNormal(seed, sigma, n),
+};

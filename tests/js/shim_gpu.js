@@ -1,0 +1,63 @@
+'use strict';
+// GPU run of the JavaScript host: reads a case written by tests/test_gpu_js.py,
+// runs the operators through the addon exactly as the engine would call them,
+// and writes the results back for the Python side to check against the oracle.
+const assert = require('assert');
+const fs = require('fs');
+const path = require('path');
+const eff = require(path.join(__dirname, '..', '..', 'elffuss-engine_amd', 'js', 'index.js'));
+
+async function main() {
+  const dir = process.argv[2];
+  const meta = JSON.parse(fs.readFileSync(path.join(dir, 'meta.json'), 'utf8'));
+  const device = await eff.requestDevice();
+  const ops = eff.createQuantOps(device);
+  const out = {};
+  const rd = async (buf, n) => new Float32Array(await eff.readback(device, buf, 0, n * 4));
+  for (const c of meta.cases) {
+    const w = fs.readFileSync(path.join(dir, c.w));
+    const x = new Float32Array(fs.readFileSync(path.join(dir, c.x)).buffer.slice(0));
+    let wBuf;
+    if (c.type === 'Q8_0R') {
+      const n = c.rows * c.k / 32;
+      wBuf = device.createBuffer({ size: eff.bytesBufferR('Q8_0R', n), label: 'w' });
+      device.queue.writeBuffer(wBuf, 0, eff.reordena('Q8_0', w, n));
+      assert.throws(() => eff.compruebaBufferR('Q8_0R', wBuf, {}, 'matmul'), /marca/);
+      eff.marcaBufferR(wBuf, 'Q8_0R', n);
+      assert.strictEqual(eff.bloquesR(wBuf), n);
+    } else {
+      wBuf = ops.upload(w, 'w');
+    }
+    const xBuf = ops.upload(x, 'x');
+    const y = await ops.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens);
+    out[c.name] = Array.from(await rd(y, c.rows * c.tokens));
+    if (c.tokens <= 8) {
+      const yg = await ops.gemv.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens);
+      out[c.name + ':gemv'] = Array.from(await rd(yg, c.rows * c.tokens));
+    } else {
+      assert.strictEqual(await ops.gemv.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens), null);
+    }
+    if (c.tokens >= 64) {
+      const ym = await ops.gemm2.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens);
+      out[c.name + ':gemm2'] = Array.from(await rd(ym, c.rows * c.tokens));
+    } else {
+      assert.strictEqual(await ops.gemm2.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens), null);
+    }
+    const nb = c.rows * c.k / eff.QUANT_TYPES[c.type].blockElems;
+    const dq = await ops.dequant(c.type, wBuf, nb);
+    out[c.name + ':dequant'] = Array.from(new Uint32Array(await eff.readback(device, dq, 0, nb * eff.QUANT_TYPES[c.type].blockElems * 4)));
+    assert.throws(() => ops.matmul(c.type, wBuf, xBuf, c.rows, c.k + 1, 1), /múltiplo/);
+    ops.ctx.recycle();
+  }
+  // top-k over a logits vector, candidates through createTopKGPU
+  const logits = new Float32Array(fs.readFileSync(path.join(dir, meta.topk.logits)).buffer.slice(0));
+  const lb = ops.upload(logits, 'logits');
+  const tk = eff.createTopKGPU(device, ops.ctx);
+  const c = await tk.candidatos(lb, 0, logits.length, { M: meta.topk.m, S: Uint32Array.from(meta.topk.S) });
+  out.topk = { ids: Array.from(c.ids), bits: Array.from(c.bits), bitsS: Array.from(c.bitsS) };
+  out.stats = device.stats();
+  fs.writeFileSync(path.join(dir, 'out.json'), JSON.stringify(out));
+  device.destroy();
+  console.log('shim_gpu ok');
+}
+main().catch((e) => { console.error(e); process.exit(1); });

@@ -1,0 +1,57 @@
+"""The JavaScript host on the GPU: tests/js/shim_gpu.js drives createQuantOps,
+gemv, gemm2, dequant, the Q8_0R marks and createTopKGPU through the N-API
+addon; its outputs are checked here against the oracle."""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from test_gpu_parity import check_close
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
+def test_js_shim_gpu(eff, orc, tmp_path):
+    cases = []
+    spec = [("q4k_t1", "Q4_K", 96, 2048, 1), ("q8r_t3", "Q8_0R", 64, 1024, 3), ("q6k_t2", "Q6_K", 40, 512, 2),
+            ("iq2_t9", "IQ2_XXS", 48, 512, 9), ("q2k_t64", "Q2_K", 64, 512, 64)]
+    data = {}
+    for i, (name, t, rows, k, tokens) in enumerate(spec):
+        base = "Q8_0" if t == "Q8_0R" else t
+        w = eff.quantize(base, eff.fill_normal(70 + i, 0.02, rows * k))
+        x = eff.fill_normal(80 + i, 1.0, tokens * k)
+        w.tofile(tmp_path / f"{name}.w")
+        x.tofile(tmp_path / f"{name}.x")
+        data[name] = (base, w, x, rows, k, tokens)
+        cases.append({"name": name, "type": t, "rows": rows, "k": k, "tokens": tokens,
+                      "w": f"{name}.w", "x": f"{name}.x"})
+    logits = eff.fill_normal(99, 3.0, 70000)
+    logits[100:140] = 2.5
+    logits.tofile(tmp_path / "logits.bin")
+    meta = {"cases": cases, "topk": {"logits": "logits.bin", "m": 40, "S": [5, 69999]}}
+    (tmp_path / "meta.json").write_text(json.dumps(meta))
+    r = subprocess.run(["node", os.path.join(HERE, "js", "shim_gpu.js"), str(tmp_path)], capture_output=True,
+                       text=True, timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stderr
+    out = json.loads((tmp_path / "out.json").read_text())
+    for name, (base, w, x, rows, k, tokens) in data.items():
+        ot = orc.NAMES[base]
+        ref = (orc.gemm_f16 if tokens >= 64 else orc.gemv_f64)(ot, w, rows, k, x, tokens)
+        check_close(np.array(out[name], np.float32), ref, f"js matmul {name}")
+        if tokens <= 8:
+            check_close(np.array(out[name + ":gemv"], np.float32), ref, f"js gemv {name}")
+        if tokens >= 64:
+            check_close(np.array(out[name + ":gemm2"], np.float32), ref, f"js gemm2 {name}")
+        e, _ = eff.geometry(base)
+        assert np.array_equal(np.array(out[name + ":dequant"], np.uint32),
+                              orc.dequant(ot, w, rows * k // e).view(np.uint32))
+    ids, bits, _ = orc.topk(logits.view(np.uint32), 40)
+    assert out["topk"]["ids"] == ids.tolist() and out["topk"]["bits"] == bits.tolist()
+    assert out["topk"]["bitsS"] == logits.view(np.uint32)[[5, 69999]].tolist()
+    assert out["stats"]["topk"] == 1 and out["stats"]["gemm"] >= 2
