@@ -148,6 +148,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--only", default="", help="run only sweep entries whose name contains this text")
     ap.add_argument("--no-head", action="store_true", help="skip the headline measurement")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="also run 5 device-to-device copies of MIB MiB (calibration of the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path is single-GPU by design (got --gpus {args.gpus}); "
@@ -167,6 +169,15 @@ def main():
         ms = time_steps(torch, ctx, head, args.steps, args.warmup)
         gbs = head.bytes / (ms * 1e-3) / 1e9
         head.free()
+
+    if args.copy_probe:
+        nbytes = args.copy_probe << 20
+        src, dst = ctx.alloc(nbytes), ctx.alloc(nbytes)
+        for _ in range(5):
+            ctx.copy(dst, src, nbytes)
+        ctx.sync()
+        src.free()
+        dst.free()
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
