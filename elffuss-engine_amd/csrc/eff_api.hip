@@ -25,6 +25,7 @@ struct eff_ctx {
   std::string error;
   int64_t gemv_max_tokens = 8;
   int64_t gemm_min_tokens = 64;
+  int64_t gemv_kernel = 0;
   eff_stats stats{};
   void *topk_scratch = nullptr;
   size_t topk_scratch_bytes = 0;
@@ -115,8 +116,14 @@ int weight_view(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint
 }
 
 int run_gemv(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
-  GemvPlan p = plan_gemv(wv, tokens);
-  hipError_t e = launch_gemv(wv, x, y, tokens, p, ctx->stream);
+  GemvPlan p;
+  hipError_t e;
+  if (ctx->gemv_kernel == 0 && gemv_mx_plan(wv, tokens, p)) {
+    e = launch_gemv_mx(wv, x, y, tokens, p, ctx->stream);
+  } else {
+    p = plan_gemv(wv, tokens);
+    e = launch_gemv(wv, x, y, tokens, p, ctx->stream);
+  }
   if (e != hipSuccess) return hip_fail(ctx, e, "gemv launch");
   return EFF_OK;
 }
@@ -203,6 +210,10 @@ int eff_set_option(eff_ctx *ctx, int option, int64_t value) {
     case EFF_OPT_GEMM_MIN_TOKENS:
       if (value < 1) return fail(ctx, EFF_E_INVALID, "GEMM min tokens must be >= 1, got %lld", (long long)value);
       ctx->gemm_min_tokens = value;
+      return EFF_OK;
+    case EFF_OPT_GEMV_KERNEL:
+      if (value < 0 || value > 1) return fail(ctx, EFF_E_INVALID, "GEMV kernel must be 0 or 1, got %lld", (long long)value);
+      ctx->gemv_kernel = value;
       return EFF_OK;
     default: return fail(ctx, EFF_E_INVALID, "unknown option %d", option);
   }

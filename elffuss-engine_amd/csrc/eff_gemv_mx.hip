@@ -1,0 +1,775 @@
+// GEMV on the matrix cores: Y[t][row] = sum_k W[row][k] X[t][k] for 1..8
+// tokens, with the weights kept as the signed 8-bit integers of their blocks
+// and x split into three signed 8-bit digit planes.
+//
+// x digits. For each group of 32 consecutive x values of a token, with
+// max|x| < 2^E, x is rounded to xi = round(x * 2^(21-E)) (|xi| <= 2^21) and
+// written xi = d2*65536 + d1*256 + d0 with d0, d1 in [-128, 127] and
+// |d2| <= 32: 22 significant bits relative to the group maximum. The group
+// factor p = 2^(E-21) and the f32 sums of x over each 16 values stay beside
+// the digits in LDS. A workgroup prepares the digits of the whole x once.
+//
+// Weights. Every type is read in tasks of 64 weights of one row, made of 4
+// runs of 16 consecutive k; each run has its own scale (Q6_K, Q2_K) or two
+// runs share one (Q8_0, Q4_K, IQ2_XXS). value = s * u - m with u a signed
+// 8-bit integer taken from the block bytes:
+//   Q8_0, Q8_0R  u = q                     s = d               m = 0
+//   Q4_K         u = 4-bit q               s = d * sc          m = dmin * mn
+//   Q6_K         u = ql | qh << 4 (0..63)  s = d * sc          m = 32 * d * sc
+//   Q2_K         u = 2-bit q               s = d * (sc & 15)   m = dmin * (sc >> 4)
+//   IQ2_XXS      u = +-grid byte           s = d*(0.5+ls)/4    m = 0
+// (the block decoders of kernels.wgsl.js:154-396, in integer form).
+//
+// MFMA. v_mfma_i32_4x4x4_16b_i8 computes 16 independent 4x4x4 products. Lane
+// l = 4b + c holds, for block b, row c of A (4 x values of digit plane c; row
+// 3 is filler whose output is not used) and column c of B (4 weights of row c
+// of W). Its D is then the three exact integer sums sum(u * d_i) over those
+// 4 k for its own row. A wave covers 4 rows of W (c) x 16 tasks (b); the 16
+// MFMAs of a task accumulate per scale group in D, and each group is folded
+// into the lane's f32 sum:  acc += s * p * (D2*65536 + D1*256 + D0) - m * sum(x).
+// The 16 task slots of a row are added with DPP at the end, and the k slices
+// of a workgroup in a fixed order through LDS.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/elffuss_amd.h"
+#include "eff_device.h"
+#include "eff_formats.h"
+#include "eff_kernels.h"
+
+namespace eff {
+
+static __constant__ uint64_t c_grid_mx[256] = {
+#include "iq2xxs_grid.inc"
+};
+
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+namespace {
+
+constexpr int kMxTables = 3072;  // IQ2_XXS grid (256 x 8 B) + sign masks (128 x 8 B), LDS bytes
+
+__device__ __forceinline__ float ub(uint32_t w, int c) { return (float)((w >> (8 * c)) & 0xFFu); }
+
+// ---------------------------------------------------------------------------
+// Tasks: the bytes of 64 weights of one row, their int8 form (B[16], one
+// dword per MFMA; MFMAs 4r..4r+3 are run r) and their scales.
+//
+// A wave stages, per pass, the bytes of its 4 rows that hold 16 consecutive
+// tasks (RB bytes per row) into LDS with coalesced 16-byte loads, then every
+// lane reads its task from there. `tbyte(ti)` is the offset of task ti's
+// first byte in its row (ti a multiple of 4 starts a block), `ALIGN` the
+// alignment that row and pass offsets always have, `read(p, b)` takes the
+// LDS address of the pass region of the lane's row and the task slot b.
+template <int TYPE> struct Task;
+
+// LDS reads at 4-byte and at 2-byte aligned addresses.
+__device__ __forceinline__ uint32_t lds32(const uint8_t *p) { return *(const uint32_t *)p; }
+// (Alignment is taken off the pointer by pointer arithmetic, so that the
+// compiler keeps the LDS address space and emits ds_read, not flat loads.)
+__device__ __forceinline__ void lds16_a2(const uint8_t *p, uint32_t *out) {
+  const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
+  const uint8_t *q = p - sh;
+  uint32_t v[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) v[i] = lds32(q + 4 * i);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], sh);
+}
+__device__ __forceinline__ uint32_t lds16b_a2(const uint8_t *p) {
+  const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
+  const uint32_t w = lds32(p - sh);
+  return sh ? (w >> 16) : (w & 0xFFFFu);
+}
+
+template <> struct Task<Q8_0> {
+  static constexpr int G = 2;  // scale groups (2 runs each)
+  static constexpr uint32_t RB = 1088, ALIGN = 4;
+  __device__ static uint32_t tbyte(uint32_t ti) { return 68u * ti; }
+  uint32_t w[17];              // two blocks, 68 bytes from a 4-aligned offset
+  __device__ void read(const uint8_t *p, uint32_t b) {
+#pragma unroll
+    for (int i = 0; i < 17; ++i) w[i] = lds32(p + 68u * b + 4u * i);
+  }
+  __device__ void decode(uint32_t *B, const uint32_t *) const {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) B[j] = __builtin_amdgcn_alignbyte(w[j + 1], w[j], 2);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) B[8 + j] = w[9 + j];
+  }
+  __device__ void scales(uint32_t, float *sa, float *sb, float &fa, float &fb) const {
+    sa[0] = h2f(w[0] & 0xFFFFu);
+    sa[1] = h2f(w[8] >> 16);
+    sb[0] = sb[1] = 0.f;
+    fa = 1.f;
+    fb = 0.f;
+  }
+  __device__ static uint32_t run_k(uint32_t ti, int r) { return 64u * ti + 16u * (uint32_t)r; }
+};
+
+// Quants and scales live in two regions; the scales (2 bytes per block) are
+// staged as a second region of 64 bytes per row and pass.
+template <> struct Task<Q8_0R> {
+  static constexpr int G = 2;
+  static constexpr uint32_t RB = 1024, ALIGN = 16, RB2 = 64, ALIGN2 = 4;
+  __device__ static uint32_t tbyte(uint32_t ti) { return 64u * ti; }
+  __device__ static uint32_t tbyte2(uint32_t ti) { return 4u * ti; }
+  uint32_t q[16], s;
+  __device__ void read(const uint8_t *p, uint32_t b) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 v = *(const u32x4 *)(p + 64u * b + 16u * i);
+      q[4 * i] = v.x; q[4 * i + 1] = v.y; q[4 * i + 2] = v.z; q[4 * i + 3] = v.w;
+    }
+  }
+  __device__ void read2(const uint8_t *p, uint32_t b) { s = lds32(p + 4u * b); }
+  __device__ void decode(uint32_t *B, const uint32_t *) const {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) B[j] = q[j];
+  }
+  __device__ void scales(uint32_t, float *sa, float *sb, float &fa, float &fb) const {
+    sa[0] = h2f(s & 0xFFFFu);
+    sa[1] = h2f(s >> 16);
+    sb[0] = sb[1] = 0.f;
+    fa = 1.f;
+    fb = 0.f;
+  }
+  __device__ static uint32_t run_k(uint32_t ti, int r) { return 64u * ti + 16u * (uint32_t)r; }
+};
+
+// Task = sub-block pair p = ti % 4 of block ti / 4: qs bytes 32p..32p+31, low
+// nibbles = sub-block 2p (runs 0, 1), high nibbles = 2p+1 (runs 2, 3).
+template <> struct Task<Q4_K> {
+  static constexpr int G = 2;
+  static constexpr uint32_t RB = 576, ALIGN = 16;
+  __device__ static uint32_t tbyte(uint32_t ti) { return 144u * (ti >> 2); }
+  uint32_t h[4], qs[8];
+  __device__ void read(const uint8_t *p, uint32_t b) {
+    const uint8_t *blk = p + 144u * (b >> 2);
+    const u32x4 a = *(const u32x4 *)blk;
+    const u32x4 c = *(const u32x4 *)(blk + 16u + 32u * (b & 3u));
+    const u32x4 d = *(const u32x4 *)(blk + 32u + 32u * (b & 3u));
+    h[0] = a.x; h[1] = a.y; h[2] = a.z; h[3] = a.w;
+    qs[0] = c.x; qs[1] = c.y; qs[2] = c.z; qs[3] = c.w; qs[4] = d.x; qs[5] = d.y; qs[6] = d.z; qs[7] = d.w;
+  }
+  __device__ void decode(uint32_t *B, const uint32_t *) const {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      B[j] = qs[j] & 0x0F0F0F0Fu;
+      B[8 + j] = (qs[j] >> 4) & 0x0F0F0F0Fu;
+    }
+  }
+  // 6-bit (scale, min) pairs 2p and 2p+1 (SCALE_MIN_K4, kernels.wgsl.js:94-104),
+  // extracted for 4 pairs at a time as packed bytes.
+  __device__ void scales(uint32_t ti, float *sa, float *sb, float &fa, float &fb) const {
+    const uint32_t p = ti & 3u;
+    const uint32_t sc_lo = h[1] & 0x3F3F3F3Fu, mn_lo = h[2] & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (h[3] & 0x0F0F0F0Fu) | ((h[1] >> 2) & 0x30303030u);
+    const uint32_t mn_hi = ((h[3] >> 4) & 0x0F0F0F0Fu) | ((h[2] >> 2) & 0x30303030u);
+    uint32_t sc = p < 2u ? sc_lo : sc_hi, mn = p < 2u ? mn_lo : mn_hi;
+    const uint32_t sh = 16u * (p & 1u);
+    sc >>= sh;
+    mn >>= sh;
+    sa[0] = ub(sc, 0); sa[1] = ub(sc, 1);
+    sb[0] = ub(mn, 0); sb[1] = ub(mn, 1);
+    fa = h2f(h[0] & 0xFFFFu);
+    fb = h2f(h[0] >> 16);
+  }
+  __device__ static uint32_t run_k(uint32_t ti, int r) { return 64u * ti + 16u * (uint32_t)r; }
+};
+
+// Task = (block ti/4, half n = (ti>>1)&1, l-range h = ti&1): weights
+// 128n + 32g + 16h + i, g = 0..3 (run g), from ql bytes 64n + 32(g&1) + 16h + i
+// (nibble g>>1), qh bytes 32n + 16h + i (bits 2g), scale 8n + 2g + h.
+template <> struct Task<Q6_K> {
+  static constexpr int G = 4;
+  static constexpr uint32_t RB = 840, ALIGN = 2;
+  __device__ static uint32_t tbyte(uint32_t ti) { return 210u * (ti >> 2); }
+  uint32_t p0[4], p1[4], qh[4], sc0, sc1, d;
+  __device__ void read(const uint8_t *p, uint32_t b) {
+    const uint8_t *blk = p + 210u * (b >> 2);
+    const uint32_t n = (b >> 1) & 1u, h = b & 1u;
+    lds16_a2(blk + 64u * n + 16u * h, p0);
+    lds16_a2(blk + 64u * n + 32u + 16u * h, p1);
+    lds16_a2(blk + 128u + 32u * n + 16u * h, qh);
+    const uint8_t *so = blk + 192u + 8u * n;
+    const uint32_t sh = (uint32_t)((uintptr_t)so & 3u);
+    const uint8_t *sq = so - sh;
+    const uint32_t a = lds32(sq), bb = lds32(sq + 4), c = lds32(sq + 8);
+    sc0 = __builtin_amdgcn_alignbyte(bb, a, sh);
+    sc1 = __builtin_amdgcn_alignbyte(c, bb, sh);
+    d = lds16b_a2(blk + 208u);
+  }
+  __device__ void decode(uint32_t *B, const uint32_t *) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      B[i] = (p0[i] & 0x0F0F0F0Fu) | ((qh[i] << 4) & 0x30303030u);
+      B[4 + i] = (p1[i] & 0x0F0F0F0Fu) | ((qh[i] << 2) & 0x30303030u);
+      B[8 + i] = ((p0[i] >> 4) & 0x0F0F0F0Fu) | (qh[i] & 0x30303030u);
+      B[12 + i] = ((p1[i] >> 4) & 0x0F0F0F0Fu) | ((qh[i] >> 2) & 0x30303030u);
+    }
+  }
+  __device__ void scales(uint32_t ti, float *sa, float *sb, float &fa, float &fb) const {
+    const uint32_t h8 = 8u * (ti & 1u);
+    sa[0] = (float)(int)__builtin_amdgcn_sbfe((int)sc0, h8, 8);
+    sa[1] = (float)(int)__builtin_amdgcn_sbfe((int)sc0, h8 + 16u, 8);
+    sa[2] = (float)(int)__builtin_amdgcn_sbfe((int)sc1, h8, 8);
+    sa[3] = (float)(int)__builtin_amdgcn_sbfe((int)sc1, h8 + 16u, 8);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) sb[g] = sa[g];
+    fa = h2f(d);
+    fb = 32.f * fa;
+  }
+  __device__ static uint32_t run_k(uint32_t ti, int r) {
+    return 256u * (ti >> 2) + 128u * ((ti >> 1) & 1u) + 32u * (uint32_t)r + 16u * (ti & 1u);
+  }
+};
+
+// Task = (block ti/4, n, h) as Q6_K: qs bytes 32n + 16h + i at bit shift 2g,
+// scale byte 8n + 2g + h.
+template <> struct Task<Q2_K> {
+  static constexpr int G = 4;
+  static constexpr uint32_t RB = 336, ALIGN = 4;
+  __device__ static uint32_t tbyte(uint32_t ti) { return 84u * (ti >> 2); }
+  uint32_t qs[4], sc0, sc1, dd;
+  __device__ void read(const uint8_t *p, uint32_t b) {
+    const uint8_t *blk = p + 84u * (b >> 2);
+    const uint32_t n = (b >> 1) & 1u, h = b & 1u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qs[i] = lds32(blk + 16u + 32u * n + 16u * h + 4u * i);
+    sc0 = lds32(blk + 8u * n);
+    sc1 = lds32(blk + 8u * n + 4u);
+    dd = lds32(blk + 80u);
+  }
+  __device__ void decode(uint32_t *B, const uint32_t *) const {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) B[4 * g + i] = (qs[i] >> (2 * g)) & 0x03030303u;
+  }
+  __device__ void scales(uint32_t ti, float *sa, float *sb, float &fa, float &fb) const {
+    const uint32_t h8 = 8u * (ti & 1u);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t v = ((g < 2 ? sc0 : sc1) >> (h8 + 16u * (g & 1))) & 0xFFu;
+      sa[g] = (float)(v & 15u);
+      sb[g] = (float)(v >> 4);
+    }
+    fa = h2f(dd & 0xFFFFu);
+    fb = h2f(dd >> 16);
+  }
+  __device__ static uint32_t run_k(uint32_t ti, int r) {
+    return 256u * (ti >> 2) + 128u * ((ti >> 1) & 1u) + 32u * (uint32_t)r + 16u * (ti & 1u);
+  }
+};
+
+// Task = 32-weight groups 2(ti%4) and 2(ti%4)+1 of block ti/4: per group a
+// word of 4 grid indices (8 weights each) and a word of 4 x 7 sign bits and
+// the 4-bit scale (kernels.wgsl.js:374-395). The grid entries and the sign
+// masks (parity bit added) come from LDS tables.
+template <> struct Task<IQ2_XXS> {
+  static constexpr int G = 2;
+  static constexpr uint32_t RB = 264, ALIGN = 2;
+  __device__ static uint32_t tbyte(uint32_t ti) { return 66u * (ti >> 2); }
+  uint32_t q[4], d;
+  __device__ void read(const uint8_t *p, uint32_t b) {
+    const uint8_t *blk = p + 66u * (b >> 2);
+    lds16_a2(blk + 2u + 16u * (b & 3u), q);
+    d = lds16b_a2(blk);
+  }
+  __device__ void decode(uint32_t *B, const uint32_t *tab) const {
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t gi = (q[2 * gg] >> (8 * e)) & 0xFFu, sg = (q[2 * gg + 1] >> (7 * e)) & 127u;
+        const uint2 g = *(const uint2 *)(tab + 2u * gi);
+        const uint2 m = *(const uint2 *)(tab + 512u + 2u * sg);
+        // bytes with a set mask are negated: ~g + 1 (grid bytes are never 0)
+        B[8 * gg + 2 * e] = (g.x ^ m.x) + (m.x & 0x01010101u);
+        B[8 * gg + 2 * e + 1] = (g.y ^ m.y) + (m.y & 0x01010101u);
+      }
+  }
+  __device__ void scales(uint32_t, float *sa, float *sb, float &fa, float &fb) const {
+    sa[0] = 0.5f + (float)(q[1] >> 28);
+    sa[1] = 0.5f + (float)(q[3] >> 28);
+    sb[0] = sb[1] = 0.f;
+    fa = 0.25f * h2f(d);
+    fb = 0.f;
+  }
+  __device__ static uint32_t run_k(uint32_t ti, int r) { return 64u * ti + 16u * (uint32_t)r; }
+};
+
+// Staging geometry: chunks of 16 bytes per row and pass (covering the region
+// from its 16-byte aligned start), direct-to-LDS loads per stage (64 chunks
+// each) and the stage size in LDS.
+template <uint32_t RB, uint32_t ALIGN> struct Stage {
+  static constexpr uint32_t CPR = (RB + (16u - ALIGN) + 15u) / 16u;
+  static constexpr uint32_t LOADS = (4u * CPR + 63u) / 64u;
+  static constexpr uint32_t BYTES = LOADS * 1024u;
+};
+
+template <int TYPE> struct Stage2 {
+  static constexpr uint32_t LOADS = 0, BYTES = 0, CPR = 1;
+};
+template <> struct Stage2<Q8_0R> : Stage<Task<Q8_0R>::RB2, Task<Q8_0R>::ALIGN2> {};
+
+// ---------------------------------------------------------------------------
+// x -> digit planes. One thread per 8 consecutive values ("octet"); the 4
+// threads of a quad cover one 32-value group. LDS per token: digits
+// [k/16][plane][16 B] (3 B per value), then per 32-value group
+// {p, sum x[0..15], sum x[16..31], -}.
+//
+// Vector loads return in issue order, so the first kXr octets of every thread
+// are loaded before the weights and converted while the weights are in
+// flight; any further octets are loaded and converted afterwards.
+constexpr uint32_t kXr = 4;
+
+struct XOct {
+  float4 a, b;
+};
+
+__device__ __forceinline__ void x_load(const float *__restrict__ x, uint32_t k, uint32_t o, XOct &v) {
+  const uint32_t opt = k / 8u, t = o / opt, ko = 8u * (o % opt);
+  v.a = *(const float4 *)(x + (uint64_t)t * k + ko);
+  v.b = *(const float4 *)(x + (uint64_t)t * k + ko + 4u);
+}
+
+__device__ __forceinline__ void x_store(const XOct &v, uint32_t k, uint32_t T, uint32_t o, uint8_t *lds) {
+  const uint32_t opt = k / 8u, t = o / opt, ko = 8u * (o % opt);
+  const float4 a = v.a, b = v.b;
+  float m = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                  fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+  // the quad's maximum (quad_perm [1,0,3,2] then [2,3,0,1])
+  m = fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, m), 0xB1, 0xF, 0xF, false)));
+  m = fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, m), 0x4E, 0xF, 0xF, false)));
+  // max < 2^E with E = e - 126 (e = biased exponent of m, at least 21 so that
+  // p stays a normal number); a group holding an infinity gets p = NaN (a NaN
+  // reaches the result through the group sums).
+  const uint32_t eb = (__builtin_bit_cast(uint32_t, m) >> 23) & 0xFFu;
+  const uint32_t e = eb < 21u ? 21u : (eb > 254u ? 254u : eb);
+  const float scale = __builtin_bit_cast(float, (274u - e) << 23);  // 2^(21 - E)
+  const float p = eb == 255u ? __builtin_bit_cast(float, 0x7FC00000u) : __builtin_bit_cast(float, (e - 20u) << 23);
+  // round(x * scale) + 0x808080 through the f32 magic 1.5 * 2^23: the three
+  // low bytes are the digits + 128
+  const float v8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t e8[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    e8[i] = __builtin_bit_cast(uint32_t, __builtin_fmaf(v8[i], scale, 12582912.0f)) - 0x4ABF7F80u;
+  uint32_t pl[3][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t *q = e8 + 4 * h;
+    const uint32_t l01 = __builtin_amdgcn_perm(q[1], q[0], 0x05010400u);  // e0.b0 e1.b0 e0.b1 e1.b1
+    const uint32_t l23 = __builtin_amdgcn_perm(q[3], q[2], 0x05010400u);
+    const uint32_t h01 = __builtin_amdgcn_perm(q[1], q[0], 0x07030602u);  // e0.b2 e1.b2 e0.b3 e1.b3
+    const uint32_t h23 = __builtin_amdgcn_perm(q[3], q[2], 0x07030602u);
+    pl[0][h] = __builtin_amdgcn_perm(l23, l01, 0x05040100u) ^ 0x80808080u;
+    pl[1][h] = __builtin_amdgcn_perm(l23, l01, 0x07060302u) ^ 0x80808080u;
+    pl[2][h] = __builtin_amdgcn_perm(h23, h01, 0x05040100u) ^ 0x80808080u;
+  }
+  uint8_t *dig = lds + (uint64_t)t * k * 3u + (ko / 16u) * 48u + 8u * ((ko / 8u) & 1u);
+#pragma unroll
+  for (int d = 0; d < 3; ++d) *(uint2 *)(dig + 16 * d) = make_uint2(pl[d][0], pl[d][1]);
+  // sums over 16 values: this octet + its neighbour in the quad
+  float s = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+  s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0xB1, 0xF, 0xF, false));
+  float *meta = (float *)(lds + (uint64_t)T * k * 3u) + (uint64_t)t * (k / 8u) + 4u * (ko / 32u);
+  const uint32_t q4 = (ko / 8u) & 3u;
+  if (q4 == 0u) meta[1] = s;
+  if (q4 == 2u) meta[2] = s;
+  if (q4 == 1u) meta[0] = p;
+}
+
+// IQ2_XXS tables in LDS: the grid (256 x 8 bytes) and, for each 7-bit sign
+// field, the byte masks of its 8 signs (parity bit added, kernels.wgsl.js:381-384).
+__device__ __forceinline__ void mx_tables(uint32_t *tab, uint64_t g, uint32_t tid) {
+  tab[2 * tid] = (uint32_t)g;
+  tab[2 * tid + 1] = (uint32_t)(g >> 32);
+  if (tid < 128u) {
+    const uint32_t s8 = tid | ((uint32_t)(__builtin_popcount(tid) & 1) << 7);
+    uint32_t m0 = 0, m1 = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      m0 |= ((s8 >> j) & 1u) ? (0xFFu << (8 * j)) : 0u;
+      m1 |= ((s8 >> (4 + j)) & 1u) ? (0xFFu << (8 * j)) : 0u;
+    }
+    tab[512 + 2 * tid] = m0;
+    tab[512 + 2 * tid + 1] = m1;
+  }
+}
+
+// Sum over the 16 lanes 4b + c of one c (DPP row rotations, then across the
+// 4 rows of 16 lanes); every lane gets the total of its c.
+__device__ __forceinline__ float slot_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// A workgroup is NW waves = (NW/S) row quads x S slices of k; a tile is its
+// 4*NW/S rows. With S = 1 the workgroups are persistent: workgroup i takes
+// tiles i, i + grid, ... and each wave streams through the passes of its row
+// quad in every tile. With S > 1 there is one tile per workgroup and the
+// slices are added in a fixed order through LDS.
+//
+// A pass is 16 tasks of the wave's 4 rows. Its bytes (4 rows x RB) are
+// fetched with coalesced 16-byte loads (lane i takes chunks i, i+64, ...) two
+// passes ahead into registers, and written to the wave's LDS stage just before
+// the pass is computed; each lane then reads its own task from the stage.
+template <int TYPE, int T, int NW>
+__global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float *__restrict__ x,
+                                                     float *__restrict__ y, int S) {
+  using TK = Task<TYPE>;
+  using ST = Stage<TK::RB, TK::ALIGN>;
+  using ST2 = Stage2<TYPE>;
+  constexpr bool kTab = TYPE == IQ2_XXS;
+  constexpr uint32_t NT = NW * 64u, SBT = ST::BYTES + ST2::BYTES;
+  constexpr uint32_t L2N = ST2::LOADS > 0 ? ST2::LOADS : 1u;
+  extern __shared__ __align__(16) uint8_t lds[];
+  uint32_t *tab = (uint32_t *)lds;
+  uint8_t *xl = lds + (kTab ? kMxTables : 0);
+
+  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, b = lane >> 2, c = lane & 3u;
+  const uint32_t rows = wv.rows, k = wv.k;
+  const uint32_t G4 = (uint32_t)NW / (uint32_t)S, gq = wave / (uint32_t)S, sl = wave % (uint32_t)S;
+  const uint32_t RPT = 4u * G4, tiles = (rows + RPT - 1u) / RPT;
+  const BufSrc src = make_src(wv, 0);
+  const uint32_t xbytes = (uint32_t)T * k * 3u + (uint32_t)T * (k / 8u) * 4u;
+  uint8_t *const stg = xl + xbytes + wave * SBT;
+  float *red = (float *)(xl + xbytes + (uint32_t)NW * SBT);
+
+  const uint32_t ntask = k / 64u / (uint32_t)S, t0 = sl * ntask;
+  const uint32_t passes = (ntask + 15u) / 16u;
+  const uint32_t my_tiles = (tiles - 1u - blockIdx.x) / gridDim.x + 1u, nitems = my_tiles * passes;
+  // bytes of a row: GGUF blocks, or the quants of Q8_0R (its scales: 2 per block)
+  const uint32_t rbytes = TYPE == Q8_0R ? 32u * wv.bpr : (uint32_t)wv.row_bytes, sbytes = 2u * wv.bpr;
+  auto row_of = [&](uint32_t tile, uint32_t r) { return min(tile * RPT + 4u * gq + r, rows - 1u); };
+
+  // This lane's chunks: chunk q = lane + 64j is chunk q % CPR of row q / CPR.
+  uint32_t s_r[ST::LOADS], s_ch[ST::LOADS];
+#pragma unroll
+  for (uint32_t j = 0; j < ST::LOADS; ++j) {
+    const uint32_t q = lane + 64u * j, r = q / ST::CPR;
+    s_r[j] = min(r, 3u);
+    s_ch[j] = 16u * (r > 3u ? 0u : q - r * ST::CPR);
+  }
+  uint32_t s2_r = 0, s2_ch = 0;
+  if constexpr (ST2::LOADS > 0) {
+    const uint32_t r = lane / ST2::CPR;
+    s2_r = min(r, 3u);
+    s2_ch = 16u * (r > 3u ? 0u : lane - r * ST2::CPR);
+  }
+  struct Regs {
+    u32x4 q[ST::LOADS], s[L2N];
+  };
+  auto fetch = [&](uint32_t tile, uint32_t ps, Regs &R) {
+    const uint32_t roff = TK::tbyte(t0 + 16u * ps);
+#pragma unroll
+    for (uint32_t j = 0; j < ST::LOADS; ++j) {
+      const uint32_t o = row_of(tile, s_r[j]) * rbytes + roff;
+      R.q[j] = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)((o & ~15u) + s_ch[j]), 0, 0);
+    }
+    if constexpr (ST2::LOADS > 0) {
+      const uint32_t o = row_of(tile, s2_r) * sbytes + Task<Q8_0R>::tbyte2(t0 + 16u * ps);
+      R.s[0] = __builtin_amdgcn_raw_buffer_load_b128(src.s, (int)((o & ~15u) + s2_ch), 0, 0);
+    }
+  };
+  auto put = [&](const Regs &R) {
+#pragma unroll
+    for (uint32_t j = 0; j < ST::LOADS; ++j) *(u32x4 *)(stg + 1024u * j + 16u * lane) = R.q[j];
+    if constexpr (ST2::LOADS > 0) *(u32x4 *)(stg + ST::BYTES + 16u * lane) = R.s[0];
+  };
+  // Fetch cursor, two items ahead of the compute cursor; it stops on the last
+  // item (fetched again), so the number of loads in flight never changes.
+  uint32_t f_tile = blockIdx.x, f_ps = 0, f_n = 0;
+  auto fetch_next = [&](Regs &R) {
+    fetch(f_tile, f_ps, R);
+    if (f_n + 1u < nitems) {
+      ++f_n;
+      if (++f_ps == passes) {
+        f_ps = 0;
+        f_tile += gridDim.x;
+      }
+    }
+  };
+
+  // x (and the IQ2_XXS grid) first, then the weights of the first two items
+  const uint32_t noct = (uint32_t)T * (k / 8u);
+  XOct xo[kXr];
+#pragma unroll
+  for (uint32_t i = 0; i < kXr; ++i)
+    if (tid + NT * i < noct) x_load(x, k, tid + NT * i, xo[i]);
+  uint64_t gent = 0;
+  if constexpr (kTab) gent = c_grid_mx[tid & 255u];
+  __asm__ volatile("" ::: "memory");  // keep these loads ahead of the weights
+
+  Regs RA, RB;
+  fetch_next(RA);
+  fetch_next(RB);
+
+  if constexpr (kTab) {
+    if (tid < 256u) mx_tables(tab, gent, tid);
+  }
+#pragma unroll
+  for (uint32_t i = 0; i < kXr; ++i)
+    if (tid + NT * i < noct) x_store(xo[i], k, (uint32_t)T, tid + NT * i, xl);
+  for (uint32_t o = tid + NT * kXr; o < noct; o += NT) {
+    XOct v;
+    x_load(x, k, o, v);
+    x_store(v, k, (uint32_t)T, o, xl);
+  }
+  __syncthreads();
+
+  const uint8_t *dig = xl;
+  const float *meta = (const float *)(xl + (uint64_t)T * k * 3u);
+  const uint32_t cd = c < 3u ? c : 0u;
+
+  float acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = 0.f;
+
+  constexpr int G = TK::G, RPG = 4 / G;  // runs per scale group
+  auto compute = [&](uint32_t tile, uint32_t ps) {
+    const uint32_t slot = 16u * ps + b;
+    const bool active = slot < ntask;
+    const uint32_t ti = t0 + 16u * ps + b;
+    const uint32_t roff = TK::tbyte(t0 + 16u * ps);
+    const uint32_t myrow = row_of(tile, c);
+    TK w;
+    w.read(stg + c * (ST::CPR * 16u) + ((myrow * rbytes + roff) & 15u), b);
+    if constexpr (ST2::LOADS > 0) {
+      const uint32_t roff2 = Task<Q8_0R>::tbyte2(t0 + 16u * ps);
+      w.read2(stg + ST::BYTES + c * (ST2::CPR * 16u) + ((myrow * sbytes + roff2) & 15u), b);
+    }
+    uint32_t B[16];
+    w.decode(B, tab);
+    float sa[G], sb[G], fa, fb;
+    w.scales(ti, sa, sb, fa, fb);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint8_t *dt = dig + (uint64_t)t * k * 3u;
+      const float *mt = meta + (uint64_t)t * (k / 8u);
+      float av = 0.f, bv = 0.f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        int4v D = {0, 0, 0, 0};
+        float pg = 0.f, xg = 0.f;
+#pragma unroll
+        for (int rr = 0; rr < RPG; ++rr) {
+          const int r = g * RPG + rr;
+          const uint32_t ks = active ? TK::run_k(ti, r) : 0u;
+          const u32x4 A = *(const u32x4 *)(dt + (ks / 16u) * 48u + 16u * cd);
+          const float4 M = *(const float4 *)(mt + 4u * (ks / 32u));
+          pg = M.x;
+          xg += ((ks / 16u) & 1u) ? M.z : M.y;
+          D = __builtin_amdgcn_mfma_i32_4x4x4i8((int)A.x, (int)B[4 * r], D, 0, 0, 0);
+          D = __builtin_amdgcn_mfma_i32_4x4x4i8((int)A.y, (int)B[4 * r + 1], D, 0, 0, 0);
+          D = __builtin_amdgcn_mfma_i32_4x4x4i8((int)A.z, (int)B[4 * r + 2], D, 0, 0, 0);
+          D = __builtin_amdgcn_mfma_i32_4x4x4i8((int)A.w, (int)B[4 * r + 3], D, 0, 0, 0);
+        }
+        const float f = __builtin_fmaf((float)(D.z * 256 + D.y), 256.f, (float)D.x);
+        av = __builtin_fmaf(sa[g], pg * f, av);
+        bv = __builtin_fmaf(sb[g], xg, bv);
+      }
+      const float v = __builtin_fmaf(fa, av, -fb * bv);
+      acc[t] += active ? v : 0.f;
+    }
+  };
+  // End of a tile: the 16 task slots of each row are added; S = 1 writes y,
+  // S > 1 (one tile per workgroup) adds the slices through LDS.
+  auto finish = [&](uint32_t tile) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = slot_sum(acc[t]);
+    if (S == 1) {
+      const uint32_t r = tile * RPT + 4u * gq + c;
+      if (b == 0u && r < rows) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) y[(uint64_t)t * rows + r] = acc[t];
+      }
+    } else {
+      if (b == 0u) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) red[(wave * 4u + c) * (uint32_t)T + t] = acc[t];
+      }
+      __syncthreads();
+      if (tid < RPT * (uint32_t)T) {
+        const uint32_t rq = tid / (4u * (uint32_t)T), rc = (tid / (uint32_t)T) % 4u, t = tid % (uint32_t)T;
+        float v = 0.f;
+        for (uint32_t q = 0; q < (uint32_t)S; ++q) v += red[((rq * (uint32_t)S + q) * 4u + rc) * (uint32_t)T + t];
+        const uint32_t r = tile * RPT + 4u * rq + rc;
+        if (r < rows) y[(uint64_t)t * rows + r] = v;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = 0.f;
+  };
+  uint32_t c_tile = blockIdx.x, c_ps = 0;
+  auto step = [&](Regs &R) {
+    put(R);
+    compute(c_tile, c_ps);
+    if (++c_ps == passes) {
+      finish(c_tile);
+      c_ps = 0;
+      c_tile += gridDim.x;
+    }
+  };
+
+  for (uint32_t n = 0; n < nitems; n += 2u) {
+    step(RA);
+    fetch_next(RA);
+    if (n + 1u < nitems) step(RB);
+    fetch_next(RB);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+
+namespace {
+
+template <int TYPE> constexpr size_t stage_bytes() {
+  return (size_t)Stage<Task<TYPE>::RB, Task<TYPE>::ALIGN>::BYTES + Stage2<TYPE>::BYTES;
+}
+
+size_t stage_bytes_of(int type) {
+  switch (type) {
+    case Q8_0: return stage_bytes<Q8_0>();
+    case Q8_0R: return stage_bytes<Q8_0R>();
+    case Q4_K: return stage_bytes<Q4_K>();
+    case Q6_K: return stage_bytes<Q6_K>();
+    case Q2_K: return stage_bytes<Q2_K>();
+    case IQ2_XXS: return stage_bytes<IQ2_XXS>();
+    default: return 0;
+  }
+}
+
+// LDS: IQ2_XXS tables, x digits, one weight stage per wave, slice sums.
+size_t mx_lds_bytes(const WeightView &wv, uint32_t tokens, int nw) {
+  return (wv.type == IQ2_XXS ? (size_t)kMxTables : 0) + (size_t)tokens * wv.k * 3u +
+         (size_t)tokens * (wv.k / 8u) * 4u + (size_t)nw * stage_bytes_of(wv.type) + (size_t)nw * 4u * tokens * 4u;
+}
+
+int g_force_nw = 0, g_force_s = 0;
+
+}  // namespace
+
+void gemv_mx_override(int nw, int s) {
+  g_force_nw = nw;
+  g_force_s = s;
+}
+
+bool gemv_mx_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p) {
+  if (tokens < 1 || tokens > 8 || wv.k % 64u) return false;
+  if (wv.w_bytes >= (1ull << 32)) return false;  // byte offsets are 32-bit
+  const bool kq = wv.type != Q8_0 && wv.type != Q8_0R;
+  // a slice holds whole passes' worth of blocks: k % (256 S) for the K types
+  auto slice_ok = [&](int s) { return wv.k % ((kq ? 256u : 64u) * (uint32_t)s) == 0; };
+  struct Cand { int nw, s; };
+  const Cand cands[] = {{8, 1}, {4, 1}, {8, 2}, {4, 2}, {8, 4}, {4, 4}};
+  // The most rows per workgroup (x digits are prepared once for them) that
+  // still give one workgroup per CU; failing that, the most workgroups.
+  int best = -1;
+  uint32_t best_rows = 0;
+  bool best_enough = false;
+  for (int i = 0; i < 6; ++i) {
+    const Cand &cd = cands[i];
+    if (g_force_nw && (cd.nw != g_force_nw || cd.s != g_force_s)) continue;
+    if (!slice_ok(cd.s) || mx_lds_bytes(wv, tokens, cd.nw) > kMxMaxLds) continue;
+    const uint32_t per = 4u * (uint32_t)(cd.nw / cd.s);
+    const bool enough = (wv.rows + per - 1u) / per >= 256u;
+    const bool better = best < 0 || (enough && !best_enough) ||
+                        (enough && best_enough && per > best_rows) || (!enough && !best_enough && per < best_rows);
+    if (better) {
+      best = i;
+      best_rows = per;
+      best_enough = enough;
+    }
+  }
+  if (best < 0) return false;
+  p = GemvPlan{};
+  p.rows_per_wave = 4;
+  p.ksplit = cands[best].s;
+  p.waves = cands[best].nw;
+  p.kc = wv.k / (uint32_t)p.ksplit;
+  p.tiles = (wv.rows + best_rows - 1u) / best_rows;
+  p.grid = p.tiles;
+  p.lds_bytes = mx_lds_bytes(wv, tokens, p.waves);
+  return true;
+}
+
+// Workgroups resident at once on the current device for this kernel and LDS
+// size (persistent grids are sized to it).
+template <int TYPE, int T, int NW>
+static hipError_t mx_resident(size_t lds, uint32_t &out) {
+  static bool attr = false;
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_mx<TYPE, T, NW>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMxMaxLds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  int dev = 0, cus = 0, per = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess)
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_gemv_mx<TYPE, T, NW>, NW * 64, lds);
+  if (e != hipSuccess) return e;
+  out = (uint32_t)(cus > 0 ? cus : 1) * (uint32_t)(per > 0 ? per : 1);
+  return hipSuccess;
+}
+
+template <int TYPE, int T, int NW>
+static hipError_t mx_launch(const WeightView &wv, const float *x, float *y, const GemvPlan &p, hipStream_t s) {
+  uint32_t grid = p.tiles;
+  if (p.ksplit == 1) {
+    uint32_t res = 0;
+    const hipError_t e = mx_resident<TYPE, T, NW>(p.lds_bytes, res);
+    if (e != hipSuccess) return e;
+    grid = grid < res ? grid : res;
+  }
+  hipLaunchKernelGGL((k_gemv_mx<TYPE, T, NW>), dim3(grid), dim3(NW * 64), p.lds_bytes, s, wv, x, y, p.ksplit);
+  return hipGetLastError();
+}
+
+template <int TYPE, int T>
+static hipError_t mx_go(const WeightView &wv, const float *x, float *y, const GemvPlan &p, hipStream_t s) {
+  return p.waves == 8 ? mx_launch<TYPE, T, 8>(wv, x, y, p, s) : mx_launch<TYPE, T, 4>(wv, x, y, p, s);
+}
+
+template <int TYPE>
+static hipError_t mx_t(const WeightView &wv, const float *x, float *y, uint32_t tokens, const GemvPlan &p,
+                       hipStream_t s) {
+  switch (tokens) {
+    case 1: return mx_go<TYPE, 1>(wv, x, y, p, s);
+    case 2: return mx_go<TYPE, 2>(wv, x, y, p, s);
+    case 3: return mx_go<TYPE, 3>(wv, x, y, p, s);
+    case 4: return mx_go<TYPE, 4>(wv, x, y, p, s);
+    case 5: return mx_go<TYPE, 5>(wv, x, y, p, s);
+    case 6: return mx_go<TYPE, 6>(wv, x, y, p, s);
+    case 7: return mx_go<TYPE, 7>(wv, x, y, p, s);
+    case 8: return mx_go<TYPE, 8>(wv, x, y, p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemv_mx(const WeightView &wv, const float *x, float *y, uint32_t tokens, const GemvPlan &p,
+                          hipStream_t s) {
+  switch (wv.type) {
+    case Q8_0: return mx_t<Q8_0>(wv, x, y, tokens, p, s);
+    case Q8_0R: return mx_t<Q8_0R>(wv, x, y, tokens, p, s);
+    case Q4_K: return mx_t<Q4_K>(wv, x, y, tokens, p, s);
+    case Q6_K: return mx_t<Q6_K>(wv, x, y, tokens, p, s);
+    case Q2_K: return mx_t<Q2_K>(wv, x, y, tokens, p, s);
+    case IQ2_XXS: return mx_t<IQ2_XXS>(wv, x, y, tokens, p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace eff

@@ -20,7 +20,8 @@ struct WeightView {
 // GEMV shape chosen by the host (see plan_gemv).
 struct GemvPlan {
   int rows_per_wave;  // R
-  int ksplit;         // S: waves of a workgroup splitting k (1, 2, 4); the tile has 4/S * R rows
+  int ksplit;         // S: waves of a workgroup splitting k (1, 2, 4); the tile has waves/S * R rows
+  int waves;          // waves per workgroup (4, or 8 for the matrix-core GEMV)
   uint32_t kc;        // k elements per slice
   uint32_t tiles;     // row tiles
   uint32_t grid;      // workgroups
@@ -31,6 +32,16 @@ GemvPlan plan_gemv(const WeightView &wv, uint32_t tokens);
 
 hipError_t launch_gemv(const WeightView &wv, const float *x, float *y, uint32_t tokens,
                        const GemvPlan &p, hipStream_t stream);
+
+// Matrix-core GEMV (int8 MFMA over x digit planes, eff_gemv_mx.hip). Needs
+// k % 64 == 0, 1..8 tokens and the x digits of one workgroup within kMxMaxLds;
+// returns false (and the f32 kernel is used) otherwise.
+constexpr size_t kMxMaxLds = 160 * 1024;
+bool gemv_mx_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p);
+// Tuning hook: restrict the plan to (waves, k slices); (0, 0) restores the automatic choice.
+void gemv_mx_override(int waves, int ksplit);
+hipError_t launch_gemv_mx(const WeightView &wv, const float *x, float *y, uint32_t tokens,
+                          const GemvPlan &p, hipStream_t stream);
 
 // x is first rounded to fp16 into `xh_scratch` (tokens * k halves).
 hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *xh_scratch,

@@ -18,6 +18,7 @@
 #include <stdint.h>
 
 #include "../../include/elffuss_amd.h"
+#include "eff_device.h"
 #include "eff_formats.h"
 #include "eff_kernels.h"
 
@@ -26,87 +27,6 @@ namespace eff {
 __constant__ uint64_t c_iq2xxs_grid[256] = {
 #include "iq2xxs_grid.inc"
 };
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-typedef float float16v __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// ---------------------------------------------------------------------------
-// Loads go through buffer resources: a base address in SGPRs, 32-bit byte
-// offsets per lane with immediate displacements, and a byte count past which
-// reads return 0 (so no read can leave the buffer). Blocks start at even byte
-// offsets; 4-byte words are read aligned and re-assembled with v_alignbyte.
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr int kRsrcFlags = 0x00020000;  // dword 3 of the buffer descriptor (gfx9 family)
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint64_t bytes) {
-  const uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)bytes;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)n, kRsrcFlags);
-}
-
-__device__ __forceinline__ uint32_t ld32(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
-}
-
-__device__ __forceinline__ uint32_t ld_u16_a2(rsrc_t r, uint32_t off) {
-  const uint32_t w = ld32(r, off & ~3u);
-  return (off & 2u) ? (w >> 16) : (w & 0xFFFFu);
-}
-
-template <int N>
-__device__ __forceinline__ void ld_words_a2(rsrc_t r, uint32_t off, uint32_t *out) {
-  const uint32_t base = off & ~3u, sh = off & 3u;
-  uint32_t v[N + 1];
-#pragma unroll
-  for (int i = 0; i <= N; ++i) v[i] = ld32(r, base + 4u * i);
-#pragma unroll
-  for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], sh);
-}
-
-// Where the blocks of a weight tile live: `q` covers the GGUF blocks (or the
-// Q8_0R quants) from the tile's first block on, `s` the Q8_0R scales.
-struct BufSrc {
-  rsrc_t q, s;
-};
-
-__device__ __forceinline__ BufSrc make_src(const WeightView &wv, uint64_t first_block) {
-  BufSrc src;
-  if (wv.type == Q8_0R) {
-    const uint64_t qo = 32ull * first_block, so = wv.scales_off + 2ull * first_block;
-    src.q = make_rsrc(wv.w + qo, wv.w_bytes > qo ? wv.w_bytes - qo : 0);
-    src.s = make_rsrc(wv.w + so, wv.w_bytes > so ? wv.w_bytes - so : 0);
-  } else {
-    const uint64_t bo = first_block * geometry(wv.type).bytes;
-    src.q = make_rsrc(wv.w + bo, wv.w_bytes > bo ? wv.w_bytes - bo : 0);
-    src.s = src.q;
-  }
-  return src;
-}
-
-// Sum over each 16-lane row with DPP; every lane of the row gets the sum.
-__device__ __forceinline__ float dpp_row_sum(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
-  return v;
-}
-
-// Sum over the 64 lanes of the wave (wave-uniform result).
-__device__ __forceinline__ float wave_sum(float v) {
-  v = dpp_row_sum(v);
-  const int iv = __builtin_bit_cast(int, v);
-  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0)) +
-          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16))) +
-         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32)) +
-          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48)));
-}
-
-__device__ __forceinline__ float h2f(uint32_t h) {
-  _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
-  return (float)v;
-}
 
 __device__ __forceinline__ float ubyte(uint32_t w, int c) { return (float)((w >> (8 * c)) & 0xFFu); }
 

@@ -21,7 +21,7 @@ const path = require('path');
 const native = require(path.join(__dirname, 'elffuss_amd.node'));
 
 const STATUS = { NOT_APPLICABLE: 1, E_INVALID: -1, E_TYPE: -2, E_SHAPE: -3, E_MARK: -4, E_BOUNDS: -5, E_DEVICE: -6 };
-const OPT = { GEMV_MAX_TOKENS: 1, GEMM_MIN_TOKENS: 2 };
+const OPT = { GEMV_MAX_TOKENS: 1, GEMM_MIN_TOKENS: 2, GEMV_KERNEL: 3 };
 const TOPK = { M_MAX: 192, P_MAX: 128, CAP: 256, CABECERA: 8, N_MAX: 1 << 24, POR_TROZO: 4096 };
 
 // ---- types (gguf.js:51-64, kernels.wgsl.js QUANT_TYPES) --------------------

@@ -51,6 +51,7 @@ extern "C" {
 /* ---- options (the reference's globalThis.__ELFFUSS_* switches, ops.js:827-1101) */
 #define EFF_OPT_GEMV_MAX_TOKENS  1  /* tokens <= this go to the GEMV kernels (default 8) */
 #define EFF_OPT_GEMM_MIN_TOKENS  2  /* tokens >= this go to the fp16 MFMA GEMM (default 64; __ELFFUSS_DRIFT_DESDE) */
+#define EFF_OPT_GEMV_KERNEL      3  /* 0: int8 matrix-core GEMV where it applies (default), 1: f32 vector GEMV */
 
 /* ---- top-k output layout (kernels.topk.wgsl.js:40-60) ------------------- */
 #define EFF_TOPK_M_MAX     192   /* largest M = K' + |S| accepted (TOPK_M_MAX) */

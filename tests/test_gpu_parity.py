@@ -78,22 +78,32 @@ def test_dequant_q8_0r_partial_call_uses_tensor_scales(ctx, eff, orc):
 
 # ---- GEMV ----------------------------------------------------------------------
 
+@pytest.fixture(params=["mx", "f32"])
+def gemv_kernel(request, ctx, eff):
+    """Both GEMV kernels: the int8 matrix-core one (default) and the f32 vector one."""
+    ctx.set_option(eff.OPT_GEMV_KERNEL, 0 if request.param == "mx" else 1)
+    yield request.param
+    ctx.set_option(eff.OPT_GEMV_KERNEL, 0)
+
+
 @pytest.mark.parametrize("tname", TYPES)
 @pytest.mark.parametrize("tokens", [1, 2, 3, 4, 5, 8])
-def test_gemv_vs_f64_oracle(ctx, eff, orc, tname, tokens):
-    rows, k = 77, 2048      # rows not a multiple of the rows per wave; k spans two x passes at 8 tokens
+def test_gemv_vs_f64_oracle(ctx, eff, orc, gemv_kernel, tname, tokens):
+    rows, k = 77, 2048      # rows not a multiple of the rows per wave; k split over two waves
     t, data, gguf, n = make_weights(eff, tname, rows, k, 20 + tokens)
     x = eff.fill_normal(1000 + tokens, 1.0, tokens * k)
     wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x), ctx.alloc(tokens * rows * 4)
     ctx.qgemv(t, wb, xb, yb, rows, k, tokens)
     ref = orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens)
-    check_close(yb.read(np.float32), ref, f"gemv {tname} T={tokens}")
+    check_close(yb.read(np.float32), ref, f"gemv[{gemv_kernel}] {tname} T={tokens}")
     for b in (wb, xb, yb):
         b.free()
 
 
-@pytest.mark.parametrize("k", [32, 96, 256, 8192, 16384])
-def test_gemv_k_edge_cases(ctx, eff, orc, k):
+@pytest.mark.parametrize("k", [32, 96, 192, 256, 768, 8192, 16384])
+def test_gemv_k_edge_cases(ctx, eff, orc, gemv_kernel, k):
+    """k = 32, 96: not a whole number of 64-weight tasks (f32 kernel); 192, 768:
+    a pass of tasks partly beyond k; 8192, 16384: the largest per-wave slices."""
     for tname in (["Q8_0", "Q8_0R"] if k % 256 else TYPES):
         rows = 5
         t, data, gguf, n = make_weights(eff, tname, rows, k, k)
@@ -101,7 +111,44 @@ def test_gemv_k_edge_cases(ctx, eff, orc, k):
         wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x), ctx.alloc(rows * 4)
         ctx.qgemv(t, wb, xb, yb, rows, k, 1)
         check_close(yb.read(np.float32), orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, 1),
-                    f"gemv {tname} k={k}")
+                    f"gemv[{gemv_kernel}] {tname} k={k}")
+
+
+@pytest.mark.parametrize("tname", TYPES)
+def test_gemv_x_dynamic_range(ctx, eff, orc, gemv_kernel, tname):
+    """x digits are exact to 22 bits of each 32-value group's maximum: groups of
+    zeros, of tiny (1e-30) and huge (1e30) values, outliers next to small values,
+    and subnormals keep the f64 bounds."""
+    rows, k, tokens = 40, 2048, 3
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 77)
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 1, (tokens, k)).astype(np.float32)
+    x[0, :32] = 0.0
+    x[0, 32:64] *= 1e-30
+    x[0, 64:96] *= 1e30
+    x[1, ::37] *= 1e4                                   # outliers among ordinary values
+    x[1, 96:128] = np.float32(1e-40)                    # subnormal group
+    x[2, :] *= 1e-3
+    x = x.reshape(-1)
+    wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    ctx.qgemv(t, wb, xb, yb, rows, k, tokens)
+    ref = orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens)
+    check_close(yb.read(np.float32), ref, f"gemv[{gemv_kernel}] {tname} x range")
+
+
+@pytest.mark.parametrize("tname", ["Q8_0", "Q4_K", "IQ2_XXS"])
+def test_gemv_non_finite_x(ctx, eff, gemv_kernel, tname):
+    """A NaN or an infinity in x makes every output of its token non-finite (as
+    an f32 dot product does); the other tokens are unaffected."""
+    rows, k, tokens = 20, 512, 3
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 78)
+    x = eff.fill_normal(79, 1.0, tokens * k).reshape(tokens, k)
+    x[0, 100] = np.nan
+    x[1, 300] = np.inf
+    wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x.reshape(-1)), ctx.alloc(tokens * rows * 4)
+    ctx.qgemv(t, wb, xb, yb, rows, k, tokens)
+    y = yb.read(np.float32).reshape(tokens, rows)
+    assert np.all(~np.isfinite(y[0])) and np.all(~np.isfinite(y[1])) and np.all(np.isfinite(y[2]))
 
 
 def test_q8_0r_gemv_bit_identical_to_q8_0(ctx, eff):
