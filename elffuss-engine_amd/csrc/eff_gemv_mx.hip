@@ -84,6 +84,7 @@ __device__ __forceinline__ uint32_t lds16b_a2(const uint8_t *p) {
 
 template <> struct Task<Q8_0> {
   static constexpr int G = 2;  // scale groups (2 runs each)
+  static constexpr uint32_t RUN = 16u;  // k distance between runs
   static constexpr uint32_t RB = 1088, ALIGN = 4;
   __device__ static uint32_t tbyte(uint32_t ti) { return 68u * ti; }
   uint32_t w[17];              // two blocks, 68 bytes from a 4-aligned offset
@@ -111,6 +112,7 @@ template <> struct Task<Q8_0> {
 // staged as a second region of 64 bytes per row and pass.
 template <> struct Task<Q8_0R> {
   static constexpr int G = 2;
+  static constexpr uint32_t RUN = 16u;  // k distance between runs
   static constexpr uint32_t RB = 1024, ALIGN = 16, RB2 = 64, ALIGN2 = 4;
   __device__ static uint32_t tbyte(uint32_t ti) { return 64u * ti; }
   __device__ static uint32_t tbyte2(uint32_t ti) { return 4u * ti; }
@@ -141,6 +143,7 @@ template <> struct Task<Q8_0R> {
 // nibbles = sub-block 2p (runs 0, 1), high nibbles = 2p+1 (runs 2, 3).
 template <> struct Task<Q4_K> {
   static constexpr int G = 2;
+  static constexpr uint32_t RUN = 16u;  // k distance between runs
   static constexpr uint32_t RB = 576, ALIGN = 16;
   __device__ static uint32_t tbyte(uint32_t ti) { return 144u * (ti >> 2); }
   uint32_t h[4], qs[8];
@@ -183,6 +186,7 @@ template <> struct Task<Q4_K> {
 // (nibble g>>1), qh bytes 32n + 16h + i (bits 2g), scale 8n + 2g + h.
 template <> struct Task<Q6_K> {
   static constexpr int G = 4;
+  static constexpr uint32_t RUN = 32u;  // k distance between runs
   static constexpr uint32_t RB = 840, ALIGN = 2;
   __device__ static uint32_t tbyte(uint32_t ti) { return 210u * (ti >> 2); }
   uint32_t p0[4], p1[4], qh[4], sc0, sc1, d;
@@ -229,6 +233,7 @@ template <> struct Task<Q6_K> {
 // scale byte 8n + 2g + h.
 template <> struct Task<Q2_K> {
   static constexpr int G = 4;
+  static constexpr uint32_t RUN = 32u;  // k distance between runs
   static constexpr uint32_t RB = 336, ALIGN = 4;
   __device__ static uint32_t tbyte(uint32_t ti) { return 84u * (ti >> 2); }
   uint32_t qs[4], sc0, sc1, dd;
@@ -269,6 +274,7 @@ template <> struct Task<Q2_K> {
 // masks (parity bit added) come from LDS tables.
 template <> struct Task<IQ2_XXS> {
   static constexpr int G = 2;
+  static constexpr uint32_t RUN = 16u;  // k distance between runs
   static constexpr uint32_t RB = 264, ALIGN = 2;
   __device__ static uint32_t tbyte(uint32_t ti) { return 66u * (ti >> 2); }
   uint32_t q[4], d;
@@ -301,10 +307,11 @@ template <> struct Task<IQ2_XXS> {
 };
 
 // Staging geometry: chunks of 16 bytes per row and pass (covering the region
-// from its 16-byte aligned start), direct-to-LDS loads per stage (64 chunks
-// each) and the stage size in LDS.
+// from its 4-byte aligned start), 16-byte loads per lane and stage, and the
+// stage size in LDS.
 template <uint32_t RB, uint32_t ALIGN> struct Stage {
-  static constexpr uint32_t CPR = (RB + (16u - ALIGN) + 15u) / 16u;
+  // regions start at 4-byte aligned offsets (floored by 2 bytes for ALIGN 2)
+  static constexpr uint32_t CPR = (RB + (ALIGN < 4u ? 2u : 0u) + 15u) / 16u;
   static constexpr uint32_t LOADS = (4u * CPR + 63u) / 64u;
   static constexpr uint32_t BYTES = LOADS * 1024u;
 };
@@ -436,7 +443,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
   uint32_t *tab = (uint32_t *)lds;
   uint8_t *xl = lds + (kTab ? kMxTables : 0);
 
-  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, b = lane >> 2, c = lane & 3u;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, b = lane >> 2, c = lane & 3u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar registers)
   const uint32_t rows = wv.rows, k = wv.k;
   const uint32_t G4 = (uint32_t)NW / (uint32_t)S, gq = wave / (uint32_t)S, sl = wave % (uint32_t)S;
   const uint32_t RPT = 4u * G4, tiles = (rows + RPT - 1u) / RPT;
@@ -452,7 +460,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
   const uint32_t rbytes = TYPE == Q8_0R ? 32u * wv.bpr : (uint32_t)wv.row_bytes, sbytes = 2u * wv.bpr;
   auto row_of = [&](uint32_t tile, uint32_t r) { return min(tile * RPT + 4u * gq + r, rows - 1u); };
 
-  // This lane's chunks: chunk q = lane + 64j is chunk q % CPR of row q / CPR.
+  // This lane's chunks: chunk q = lane + 64j is chunk q % CPR of row q / CPR,
+  // stored at byte 16q of the stage.
   uint32_t s_r[ST::LOADS], s_ch[ST::LOADS];
 #pragma unroll
   for (uint32_t j = 0; j < ST::LOADS; ++j) {
@@ -466,20 +475,28 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
     s2_r = min(r, 3u);
     s2_ch = 16u * (r > 3u ? 0u : lane - r * ST2::CPR);
   }
+  // Per-lane load offsets of the fetch tile (the pass offset comes on top, in
+  // the scalar offset of the load when the region start is 4-byte aligned).
+  uint32_t vo[ST::LOADS], vo2 = 0;
+  auto set_tile = [&](uint32_t tile) {
+#pragma unroll
+    for (uint32_t j = 0; j < ST::LOADS; ++j) vo[j] = row_of(tile, s_r[j]) * rbytes + (TK::ALIGN >= 4u ? s_ch[j] : 0u);
+    if constexpr (ST2::LOADS > 0) vo2 = row_of(tile, s2_r) * sbytes + s2_ch;
+  };
   struct Regs {
     u32x4 q[ST::LOADS], s[L2N];
   };
-  auto fetch = [&](uint32_t tile, uint32_t ps, Regs &R) {
+  auto fetch = [&](uint32_t ps, Regs &R) {
     const uint32_t roff = TK::tbyte(t0 + 16u * ps);
 #pragma unroll
     for (uint32_t j = 0; j < ST::LOADS; ++j) {
-      const uint32_t o = row_of(tile, s_r[j]) * rbytes + roff;
-      R.q[j] = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)((o & ~15u) + s_ch[j]), 0, 0);
+      if constexpr (TK::ALIGN >= 4u)
+        R.q[j] = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)vo[j], (int)roff, 0);
+      else
+        R.q[j] = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)(((vo[j] + roff) & ~3u) + s_ch[j]), 0, 0);
     }
-    if constexpr (ST2::LOADS > 0) {
-      const uint32_t o = row_of(tile, s2_r) * sbytes + Task<Q8_0R>::tbyte2(t0 + 16u * ps);
-      R.s[0] = __builtin_amdgcn_raw_buffer_load_b128(src.s, (int)((o & ~15u) + s2_ch), 0, 0);
-    }
+    if constexpr (ST2::LOADS > 0)
+      R.s[0] = __builtin_amdgcn_raw_buffer_load_b128(src.s, (int)vo2, (int)Task<Q8_0R>::tbyte2(t0 + 16u * ps), 0);
   };
   auto put = [&](const Regs &R) {
 #pragma unroll
@@ -489,13 +506,15 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
   // Fetch cursor, two items ahead of the compute cursor; it stops on the last
   // item (fetched again), so the number of loads in flight never changes.
   uint32_t f_tile = blockIdx.x, f_ps = 0, f_n = 0;
+  set_tile(f_tile);
   auto fetch_next = [&](Regs &R) {
-    fetch(f_tile, f_ps, R);
+    fetch(f_ps, R);
     if (f_n + 1u < nitems) {
       ++f_n;
       if (++f_ps == passes) {
         f_ps = 0;
         f_tile += gridDim.x;
+        set_tile(f_tile);
       }
     }
   };
@@ -541,34 +560,36 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
     const bool active = slot < ntask;
     const uint32_t ti = t0 + 16u * ps + b;
     const uint32_t roff = TK::tbyte(t0 + 16u * ps);
-    const uint32_t myrow = row_of(tile, c);
     TK w;
-    w.read(stg + c * (ST::CPR * 16u) + ((myrow * rbytes + roff) & 15u), b);
-    if constexpr (ST2::LOADS > 0) {
-      const uint32_t roff2 = Task<Q8_0R>::tbyte2(t0 + 16u * ps);
-      w.read2(stg + ST::BYTES + c * (ST2::CPR * 16u) + ((myrow * sbytes + roff2) & 15u), b);
+    if constexpr (TK::ALIGN >= 4u) {
+      w.read(stg + c * (ST::CPR * 16u), b);
+    } else {
+      w.read(stg + c * (ST::CPR * 16u) + ((row_of(tile, c) * rbytes + roff) & 3u), b);
     }
+    if constexpr (ST2::LOADS > 0) w.read2(stg + ST::BYTES + c * (ST2::CPR * 16u), b);
     uint32_t B[16];
     w.decode(B, tab);
     float sa[G], sb[G], fa, fb;
     w.scales(ti, sa, sb, fa, fb);
+    // x digits and group data of the task's first run; the other runs sit at
+    // fixed distances (RUN apart in k)
+    const uint32_t kb = active ? TK::run_k(ti, 0) : 0u;
+    const bool xh = ((kb / 16u) & 1u) != 0u;  // runs of 16-weight groups: which half of the 32-group
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const uint8_t *dt = dig + (uint64_t)t * k * 3u;
-      const float *mt = meta + (uint64_t)t * (k / 8u);
+      const uint8_t *dA = dig + (uint64_t)t * k * 3u + (kb / 16u) * 48u + 16u * cd;
+      const float *mA = meta + (uint64_t)t * (k / 8u) + 4u * (kb / 32u);
       float av = 0.f, bv = 0.f;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         int4v D = {0, 0, 0, 0};
-        float pg = 0.f, xg = 0.f;
+        const float4 M = *(const float4 *)(mA + 4u * ((uint32_t)(g * RPG) * TK::RUN / 32u));
+        const float pg = M.x;
+        const float xg = RPG == 2 ? M.y + M.z : (xh ? M.z : M.y);
 #pragma unroll
         for (int rr = 0; rr < RPG; ++rr) {
           const int r = g * RPG + rr;
-          const uint32_t ks = active ? TK::run_k(ti, r) : 0u;
-          const u32x4 A = *(const u32x4 *)(dt + (ks / 16u) * 48u + 16u * cd);
-          const float4 M = *(const float4 *)(mt + 4u * (ks / 32u));
-          pg = M.x;
-          xg += ((ks / 16u) & 1u) ? M.z : M.y;
+          const u32x4 A = *(const u32x4 *)(dA + ((uint32_t)r * TK::RUN / 16u) * 48u);
           D = __builtin_amdgcn_mfma_i32_4x4x4i8((int)A.x, (int)B[4 * r], D, 0, 0, 0);
           D = __builtin_amdgcn_mfma_i32_4x4x4i8((int)A.y, (int)B[4 * r + 1], D, 0, 0, 0);
           D = __builtin_amdgcn_mfma_i32_4x4x4i8((int)A.z, (int)B[4 * r + 2], D, 0, 0, 0);
@@ -611,21 +632,26 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
     for (int t = 0; t < T; ++t) acc[t] = 0.f;
   };
   uint32_t c_tile = blockIdx.x, c_ps = 0;
-  auto step = [&](Regs &R) {
+  // the registers of a pass are free once written to the stage: the fetch two
+  // items ahead goes out before the pass is computed
+  auto step = [&](Regs &R, bool run) {
     put(R);
-    compute(c_tile, c_ps);
-    if (++c_ps == passes) {
-      finish(c_tile);
-      c_ps = 0;
-      c_tile += gridDim.x;
+    fetch_next(R);
+    if (run) {
+      compute(c_tile, c_ps);
+      if (++c_ps == passes) {
+        finish(c_tile);
+        c_ps = 0;
+        c_tile += gridDim.x;
+      }
     }
   };
 
+  // (the second fetch of an iteration is issued even without a second item,
+  // so the loads in flight are the same on every path)
   for (uint32_t n = 0; n < nitems; n += 2u) {
-    step(RA);
-    fetch_next(RA);
-    if (n + 1u < nitems) step(RB);
-    fetch_next(RB);
+    step(RA, true);
+    step(RB, n + 1u < nitems);
   }
 }
 
@@ -672,7 +698,8 @@ bool gemv_mx_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p) {
   // a slice holds whole passes' worth of blocks: k % (256 S) for the K types
   auto slice_ok = [&](int s) { return wv.k % ((kq ? 256u : 64u) * (uint32_t)s) == 0; };
   struct Cand { int nw, s; };
-  const Cand cands[] = {{8, 1}, {4, 1}, {8, 2}, {4, 2}, {8, 4}, {4, 4}};
+  // for equal rows per workgroup the wider workgroup (more waves per CU) comes first
+  const Cand cands[] = {{8, 1}, {8, 2}, {4, 1}, {8, 4}, {4, 2}, {4, 4}};
   // The most rows per workgroup (x digits are prepared once for them) that
   // still give one workgroup per CU; failing that, the most workgroups.
   int best = -1;
