@@ -494,7 +494,6 @@ __global__ __launch_bounds__(256) void k_gemv(WeightView wv, const float *__rest
 // Weights are dequantized to fp16: Q8_0/Q8_0R with packed fp16 arithmetic
 // (q exact, then one rounding of q*d, i.e. fp16(d*q)), the other types as
 // the bit-exact f32 value rounded to fp16.
-constexpr int GBM = 128;        // tile tokens
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 template <int TYPE> constexpr int gemm_bk() { return TYPE == Q6_K ? 128 : 64; }
@@ -543,33 +542,38 @@ __device__ __forceinline__ void unit_f16(const Raw<TYPE> &r, const uint32_t *gri
   }
 }
 
-// Tile: GBM = 128 tokens x BN rows. The 4 waves form a WM x WN grid (WM*WN =
-// 4); each wave computes FM x FN MFMA 32x32 fragments.
-template <int TYPE, int BN, int WN>
-__global__ __launch_bounds__(256) void k_gemm(WeightView wv, const _Float16 *__restrict__ xh,
-                                              float *__restrict__ y, uint32_t tokens, uint32_t row_tiles,
-                                              uint32_t tok_tiles) {
-  constexpr int BK = gemm_bk<TYPE>();
+// Tile: BM tokens x BN rows in k steps of BK. The NW = WM x WN x WK waves:
+// each wave computes FM x FN MFMA 32x32x16 fragments of (BM/WM) x (BN/WN)
+// over its share (1/WK) of every k step; with WK > 1 the shares are added
+// through LDS at the end. Operands are staged in LDS as fp16 (two stages);
+// the global loads of step s+2 are issued while step s is computed, from two
+// register sets. Tiles are dealt so that the workgroups of one XCD cover a
+// contiguous run of row tiles with all their token tiles: the x and W slices
+// of a k step are then shared through that XCD's L2.
+template <int TYPE, int BM, int BN, int BK, int WM, int WN, int WK>
+__global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const _Float16 *__restrict__ xh,
+                                                           float *__restrict__ y, uint32_t tokens,
+                                                           uint32_t row_tiles, uint32_t tok_tiles) {
+  constexpr int NW = WM * WN * WK, NT = NW * 64;
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   constexpr int BKP = BK + 8;                 // padded LDS row (halves)
-  constexpr int WM = 4 / WN;
-  constexpr int FM = GBM / WM / 32, FN = BN / WN / 32;
-  static_assert(FM >= 1 && FN >= 1, "tile");
-  __shared__ _Float16 xs[2][GBM * BKP];
-  __shared__ _Float16 ws[2][BN * BKP];
-  __shared__ uint32_t grid[TYPE == IQ2_XXS ? 512 : 1];
+  constexpr int FM = BM / WM / 32, FN = BN / WN / 32, KS = BK / 16 / WK;
+  static_assert(FM >= 1 && FN >= 1 && KS >= 1, "tile");
+  extern __shared__ __align__(16) uint8_t gsm[];
+  _Float16 *const xs0 = (_Float16 *)gsm, *const xs1 = xs0 + BM * BKP;
+  _Float16 *const ws0 = xs1 + BM * BKP, *const ws1 = ws0 + BN * BKP;
+  constexpr size_t kStages = (size_t)2 * (BM + BN) * BKP * 2, kRed = WK > 1 ? (size_t)BM * BN * 4 : 0;
+  uint32_t *const grid = (uint32_t *)(gsm + (kStages > kRed ? kStages : kRed));
   stage_grid<TYPE>(grid);
 
-  // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs;
-  // give each XCD a contiguous run of tiles, token tiles fastest, so the
-  // tiles sharing a weight slice share that XCD's L2.
   const uint32_t ntiles = row_tiles * tok_tiles;
   uint32_t lin = blockIdx.x;
   if (ntiles % 8 == 0) lin = (blockIdx.x % 8) * (ntiles / 8) + blockIdx.x / 8;
-  const uint32_t n0 = (lin / tok_tiles) * BN, t0 = (lin % tok_tiles) * GBM;
+  const uint32_t n0 = (lin / tok_tiles) * BN, t0 = (lin % tok_tiles) * BM;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const uint32_t rows = wv.rows, k = wv.k;
-  const int wm = wave % WM, wn = wave / WM;
+  const int wk = wave % WK, wn = (wave / WK) % WN, wm = wave / (WK * WN);
   constexpr uint32_t upb = units_per_block<TYPE>();
   constexpr uint32_t E = block_elems<TYPE>();
   const BufSrc src = make_src(wv, (uint64_t)n0 * wv.bpr);
@@ -579,43 +583,45 @@ __global__ __launch_bounds__(256) void k_gemm(WeightView wv, const _Float16 *__r
   const rsrc_t xsrc = make_rsrc(xh + xoff, xbytes);
 
   constexpr int UNITS_ALL = BN * (BK / 32);                   // weight units per step
-  constexpr int UNITS = (UNITS_ALL + 255) / 256;
-  constexpr int XCH = GBM * (BK / 8) / 256;                    // 8-half x chunks per thread
-  Raw<TYPE> raw[UNITS];
-  half8 xr[XCH];
+  constexpr int UNITS = (UNITS_ALL + NT - 1) / NT;
+  constexpr int XCH = BM * (BK / 8) / NT;                     // 8-half x chunks per thread
+  static_assert(XCH * NT == BM * (BK / 8), "x chunks");
+  struct Regs {
+    Raw<TYPE> raw[UNITS];
+    half8 xr[XCH];
+  };
 
-  auto load_step = [&](uint32_t kb) {
+  auto load_step = [&](uint32_t kb, Regs &R) {
     const uint32_t klen = min((uint32_t)BK, k - kb);
 #pragma unroll
     for (int i = 0; i < UNITS; ++i) {
-      const int id = tid + 256 * i;
-      if (UNITS_ALL % 256 != 0 && id >= UNITS_ALL) break;
+      const int id = tid + NT * i;
+      if (UNITS_ALL % NT != 0 && id >= UNITS_ALL) break;
       const int r = id / (BK / 32);
       const uint32_t u = (uint32_t)(id % (BK / 32));
       const uint32_t lrow = min(n0 + (uint32_t)r, rows - 1u) - n0;
       const uint32_t gu = kb / 32u + min(u, klen / 32u - 1u);
-      load_raw<TYPE>(raw[i], src, lrow * wv.bpr + gu / upb, gu % upb);
+      load_raw<TYPE>(R.raw[i], src, lrow * wv.bpr + gu / upb, gu % upb);
     }
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
-      const int id = tid + 256 * i;
+      const int id = tid + NT * i;
       const uint32_t t = (uint32_t)(id / (BK / 8)), c = (uint32_t)(id % (BK / 8));
       const uint32_t kk = 8u * c;
       // past k: an offset beyond the descriptor, which reads 0
       const uint32_t off = kk < klen ? (t * k + kb + kk) * 2u : 0xFFFFFFF0u;
-      typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-      xr[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)off, 0, 0));
+      R.xr[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)off, 0, 0));
     }
   };
-  auto store_step = [&](int buf, uint32_t kb) {
+  auto store_step = [&](uint32_t kb, const Regs &R, _Float16 *xs, _Float16 *ws) {
     const uint32_t klen = min((uint32_t)BK, k - kb);
 #pragma unroll
     for (int i = 0; i < UNITS; ++i) {
-      const int id = tid + 256 * i;
-      if (UNITS_ALL % 256 != 0 && id >= UNITS_ALL) break;
+      const int id = tid + NT * i;
+      if (UNITS_ALL % NT != 0 && id >= UNITS_ALL) break;
       const int r = id / (BK / 32);
       const uint32_t u = (uint32_t)(id % (BK / 32));
-      _Float16 *d = ws[buf] + r * BKP;
+      _Float16 *d = ws + r * BKP;
       if (u >= klen / 32u) {
         const half8 z = {};
 #pragma unroll
@@ -627,7 +633,7 @@ __global__ __launch_bounds__(256) void k_gemm(WeightView wv, const _Float16 *__r
       unit_runs<TYPE>(gu % upb, o0, o1);
       const uint32_t c0 = (gu / upb) * E + o0 - kb, c1 = (gu / upb) * E + o1 - kb;
       half8 h[4];
-      unit_f16<TYPE>(raw[i], grid, h);
+      unit_f16<TYPE>(R.raw[i], grid, h);
       *(half8 *)(d + c0) = h[0];
       *(half8 *)(d + c0 + 8) = h[1];
       *(half8 *)(d + c1) = h[2];
@@ -635,9 +641,9 @@ __global__ __launch_bounds__(256) void k_gemm(WeightView wv, const _Float16 *__r
     }
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
-      const int id = tid + 256 * i;
+      const int id = tid + NT * i;
       const int t = id / (BK / 8), c = id % (BK / 8);
-      *(half8 *)(xs[buf] + t * BKP + 8 * c) = xr[i];
+      *(half8 *)(xs + t * BKP + 8 * c) = R.xr[i];
     }
   };
 
@@ -649,32 +655,78 @@ __global__ __launch_bounds__(256) void k_gemm(WeightView wv, const _Float16 *__r
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  const uint32_t steps = (k + BK - 1) / BK;
-  if constexpr (TYPE == IQ2_XXS) __syncthreads();  // grid staged
-  load_step(0);
-  store_step(0, 0);
-  __syncthreads();
-  for (uint32_t st = 0; st < steps; ++st) {
-    const int buf = st & 1;
-    const bool more = st + 1 < steps;
-    if (more) load_step((st + 1) * BK);
-    const _Float16 *xa = xs[buf], *wa = ws[buf];
+  // Fragments of 16-k substep ks; the next substep's are read while the
+  // current one's MFMAs run (two register sets).
+  auto frag = [&](const _Float16 *xa, const _Float16 *wa, int ks, half8 *a, half8 *bfr) {
+    const int kq = (wk * KS + ks) * 16 + 8 * (lane >> 5);
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      half8 a[FM], bfr[FN];
-      const int kq = kk + 8 * (lane >> 5);
+    for (int i = 0; i < FM; ++i) a[i] = *(const half8 *)(xa + ((wm * FM + i) * 32 + (lane & 31)) * BKP + kq);
 #pragma unroll
-      for (int i = 0; i < FM; ++i) a[i] = *(const half8 *)(xa + ((wm * FM + i) * 32 + (lane & 31)) * BKP + kq);
+    for (int j = 0; j < FN; ++j) bfr[j] = *(const half8 *)(wa + ((wn * FN + j) * 32 + (lane & 31)) * BKP + kq);
+  };
+  auto mma = [&](const _Float16 *xa, const _Float16 *wa) {
+    half8 a[2][FM], bfr[2][FN];
+    frag(xa, wa, 0, a[0], bfr[0]);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bfr[j] = *(const half8 *)(wa + ((wn * FN + j) * 32 + (lane & 31)) * BKP + kq);
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) frag(xa, wa, ks + 1, a[(ks + 1) & 1], bfr[(ks + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the MFMAs
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bfr[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks & 1][i], bfr[ks & 1][j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (more) store_step(buf ^ 1, (st + 1) * BK);
+  };
+
+  const uint32_t steps = (k + BK - 1) / BK, last = steps - 1u;
+  if constexpr (TYPE == IQ2_XXS) __syncthreads();  // grid staged
+  // Loads are never skipped (past the last step they repeat it), so the wait
+  // before each store covers exactly the older register set.
+  Regs RA, RB;
+  load_step(0, RA);
+  load_step(min(1u, last) * BK, RB);
+  store_step(0, RA, xs0, ws0);
+  load_step(min(2u, last) * BK, RA);
+  __syncthreads();
+  for (uint32_t st = 0; st < steps; st += 2) {
+    mma(xs0, ws0);
+    if (st + 1 < steps) store_step((st + 1) * BK, RB, xs1, ws1);
+    load_step(min(st + 3, last) * BK, RB);
     __syncthreads();
+    if (st + 1 < steps) mma(xs1, ws1);
+    if (st + 2 < steps) store_step((st + 2) * BK, RA, xs0, ws0);
+    load_step(min(st + 4, last) * BK, RA);
+    __syncthreads();
+  }
+
+  // k shares of the same fragments are added through LDS (the stages are free)
+  if constexpr (WK > 1) {
+    float *red = (float *)gsm;
+    const int pair = wm * WN + wn;
+    for (int q = 1; q < WK; ++q) {
+      if (wk == q) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              red[(((pair * FM + i) * FN + j) * 16 + v) * 64 + lane] = acc[i][j][v];
+      }
+      __syncthreads();
+      if (wk == 0) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] += red[(((pair * FM + i) * FN + j) * 16 + v) * 64 + lane];
+      }
+      __syncthreads();
+    }
+    if (wk != 0) return;
   }
 
   // D[tok][row]: lane holds column (row) lane%32 and rows (tokens)
@@ -985,22 +1037,39 @@ hipError_t launch_gemv(const WeightView &wv, const float *x, float *y, uint32_t 
   }
 }
 
+template <int TYPE, int BM, int BN, int BK, int WM, int WN, int WK>
+static hipError_t gemm_cfg(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
+  // two operand stages, or the fragments of the k shares at the end (BM * BN
+  // floats, in the same space), whichever is larger; then the IQ2_XXS grid
+  constexpr size_t stages = (size_t)2 * (BM + BN) * (BK + 8) * 2, red = WK > 1 ? (size_t)BM * BN * 4 : 0;
+  constexpr size_t lds = (stages > red ? stages : red) + (TYPE == IQ2_XXS ? 2048 : 0);
+  static_assert(lds <= 160 * 1024, "LDS");
+  static bool attr = false;
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<TYPE, BM, BN, BK, WM, WN, WK>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  const uint32_t tok_tiles = (tokens + BM - 1) / BM, row_tiles = (wv.rows + BN - 1) / BN;
+  hipLaunchKernelGGL((k_gemm<TYPE, BM, BN, BK, WM, WN, WK>), dim3(row_tiles * tok_tiles), dim3(WM * WN * WK * 64), lds,
+                     s, wv, xh, y, tokens, row_tiles, tok_tiles);
+  return hipGetLastError();
+}
+
+// Tile by size, 8 waves (two per SIMD, so one wave's loads and dequantization
+// overlap the other's MFMAs): 256 x 128 tokens x rows for >= 1024 tokens
+// (k steps of 64; Q6_K units need steps of 128), 128 x 128 from 256 tokens,
+// else 128 tokens x 32 rows (small token counts are bound by the weight
+// bytes; narrow tiles spread them over the CUs). The waves that share a
+// fragment split each k step and are added at the end.
 template <int TYPE>
 static hipError_t gemm_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
-  const uint32_t tok_tiles = (tokens + GBM - 1) / GBM;
-  // Wide tiles (128 rows) when they give at least one workgroup per CU,
-  // else narrow tiles (32 rows) to spread small problems over the GPU.
-  const uint32_t wide = (wv.rows + 127) / 128 * tok_tiles;
-  if (wide >= 256) {
-    const uint32_t row_tiles = (wv.rows + 127) / 128;
-    hipLaunchKernelGGL((k_gemm<TYPE, 128, 2>), dim3(row_tiles * tok_tiles), dim3(256), 0, s, wv, xh, y, tokens,
-                       row_tiles, tok_tiles);
-  } else {
-    const uint32_t row_tiles = (wv.rows + 31) / 32;
-    hipLaunchKernelGGL((k_gemm<TYPE, 32, 1>), dim3(row_tiles * tok_tiles), dim3(256), 0, s, wv, xh, y, tokens,
-                       row_tiles, tok_tiles);
+  if constexpr (TYPE != Q6_K) {
+    if (tokens >= 1024) return gemm_cfg<TYPE, 256, 128, 64, 2, 2, 2>(wv, xh, y, tokens, s);
   }
-  return hipGetLastError();
+  if (tokens >= 256) return gemm_cfg<TYPE, 128, 128, 128, 1, 2, 4>(wv, xh, y, tokens, s);
+  return gemm_cfg<TYPE, 128, 32, 128, 1, 1, 8>(wv, xh, y, tokens, s);
 }
 
 hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *xh_scratch,

@@ -166,8 +166,11 @@ def test_q8_0r_gemv_bit_identical_to_q8_0(ctx, eff):
 # ---- GEMM --------------------------------------------------------------------------
 
 @pytest.mark.parametrize("tname", TYPES)
-@pytest.mark.parametrize("tokens", [64, 100, 200])
+@pytest.mark.parametrize("tokens", [64, 100, 200, 300, 1100])
 def test_gemm_vs_fp16_oracle(ctx, eff, orc, tname, tokens):
+    """Every tile configuration: 128 x 32 (< 256 tokens), 128 x 128 with a
+    k split (>= 256), 256 x 128 (>= 1024; Q6_K stays on 128 x 128); rows and
+    tokens not multiples of the tiles."""
     rows, k = 130, 512
     t, data, gguf, n = make_weights(eff, tname, rows, k, 40 + tokens)
     x = eff.fill_normal(2000 + tokens, 1.0, tokens * k)
