@@ -542,27 +542,31 @@ __device__ __forceinline__ void unit_f16(const Raw<TYPE> &r, const uint32_t *gri
   }
 }
 
-// Tile: BM tokens x BN rows in k steps of BK. The NW = WM x WN x WK waves:
-// each wave computes FM x FN MFMA 32x32x16 fragments of (BM/WM) x (BN/WN)
-// over its share (1/WK) of every k step; with WK > 1 the shares are added
-// through LDS at the end. Operands are staged in LDS as fp16 (two stages);
-// the global loads of step s+2 are issued while step s is computed, from two
-// register sets. Tiles are dealt so that the workgroups of one XCD cover a
-// contiguous run of row tiles with all their token tiles: the x and W slices
-// of a k step are then shared through that XCD's L2.
-template <int TYPE, int BM, int BN, int BK, int WM, int WN, int WK>
-__global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const _Float16 *__restrict__ xh,
-                                                           float *__restrict__ y, uint32_t tokens,
-                                                           uint32_t row_tiles, uint32_t tok_tiles) {
-  constexpr int NW = WM * WN * WK, NT = NW * 64;
-  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+// Tile: BM tokens x BN rows in k steps of BK, 8 waves in two roles:
+//  * 4 producer waves load the x and W bytes of step s+3 into registers (three
+//    register sets: loads have three steps to arrive) and write step s+1 into
+//    LDS as fp16 (W dequantized);
+//  * 4 MFMA waves, CM x CN x CK, compute step s from LDS: each owns FM x FN
+//    32x32x16 fragments of (BM/CM) x (BN/CN) over 1/CK of every k step (CK > 1:
+//    the shares are added through LDS at the end).
+// One producer and one MFMA wave share each SIMD, so dequantization and loads
+// overlap the MFMAs; one barrier per step hands a stage over. Tiles are dealt
+// so that the workgroups of one XCD cover a contiguous run of row tiles with
+// all their token tiles: the x and W slices of a k step are shared through
+// that XCD's L2.
+template <int TYPE, int BM, int BN, int BK, int CM, int CN, int CK>
+__global__ __launch_bounds__(512) void k_gemm(WeightView wv, const _Float16 *__restrict__ xh,
+                                              float *__restrict__ y, uint32_t tokens, uint32_t row_tiles,
+                                              uint32_t tok_tiles) {
+  static_assert(CM * CN * CK == 4, "4 MFMA waves");
+  constexpr int PT = 256;                     // producer threads
   constexpr int BKP = BK + 8;                 // padded LDS row (halves)
-  constexpr int FM = BM / WM / 32, FN = BN / WN / 32, KS = BK / 16 / WK;
+  constexpr int FM = BM / CM / 32, FN = BN / CN / 32, KS = BK / 16 / CK;
   static_assert(FM >= 1 && FN >= 1 && KS >= 1, "tile");
   extern __shared__ __align__(16) uint8_t gsm[];
   _Float16 *const xs0 = (_Float16 *)gsm, *const xs1 = xs0 + BM * BKP;
   _Float16 *const ws0 = xs1 + BM * BKP, *const ws1 = ws0 + BN * BKP;
-  constexpr size_t kStages = (size_t)2 * (BM + BN) * BKP * 2, kRed = WK > 1 ? (size_t)BM * BN * 4 : 0;
+  constexpr size_t kStages = (size_t)2 * (BM + BN) * BKP * 2, kRed = CK > 1 ? (size_t)BM * BN * 4 : 0;
   uint32_t *const grid = (uint32_t *)(gsm + (kStages > kRed ? kStages : kRed));
   stage_grid<TYPE>(grid);
 
@@ -571,9 +575,12 @@ __global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const
   if (ntiles % 8 == 0) lin = (blockIdx.x % 8) * (ntiles / 8) + blockIdx.x / 8;
   const uint32_t n0 = (lin / tok_tiles) * BN, t0 = (lin % tok_tiles) * BM;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool producer = wave >= 4;
+  const int ptid = tid - 256;                 // producer thread index
   const uint32_t rows = wv.rows, k = wv.k;
-  const int wk = wave % WK, wn = (wave / WK) % WN, wm = wave / (WK * WN);
+  const int ck = wave % CK, cn = (wave / CK) % CN, cm = (wave / (CK * CN)) % CM;
   constexpr uint32_t upb = units_per_block<TYPE>();
   constexpr uint32_t E = block_elems<TYPE>();
   const BufSrc src = make_src(wv, (uint64_t)n0 * wv.bpr);
@@ -583,9 +590,9 @@ __global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const
   const rsrc_t xsrc = make_rsrc(xh + xoff, xbytes);
 
   constexpr int UNITS_ALL = BN * (BK / 32);                   // weight units per step
-  constexpr int UNITS = (UNITS_ALL + NT - 1) / NT;
-  constexpr int XCH = BM * (BK / 8) / NT;                     // 8-half x chunks per thread
-  static_assert(XCH * NT == BM * (BK / 8), "x chunks");
+  constexpr int UNITS = (UNITS_ALL + PT - 1) / PT;
+  constexpr int XCH = BM * (BK / 8) / PT;                     // 8-half x chunks per producer thread
+  static_assert(XCH * PT == BM * (BK / 8), "x chunks");
   struct Regs {
     Raw<TYPE> raw[UNITS];
     half8 xr[XCH];
@@ -595,8 +602,8 @@ __global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const
     const uint32_t klen = min((uint32_t)BK, k - kb);
 #pragma unroll
     for (int i = 0; i < UNITS; ++i) {
-      const int id = tid + NT * i;
-      if (UNITS_ALL % NT != 0 && id >= UNITS_ALL) break;
+      const int id = ptid + PT * i;
+      if (UNITS_ALL % PT != 0 && id >= UNITS_ALL) break;
       const int r = id / (BK / 32);
       const uint32_t u = (uint32_t)(id % (BK / 32));
       const uint32_t lrow = min(n0 + (uint32_t)r, rows - 1u) - n0;
@@ -605,7 +612,7 @@ __global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const
     }
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
-      const int id = tid + NT * i;
+      const int id = ptid + PT * i;
       const uint32_t t = (uint32_t)(id / (BK / 8)), c = (uint32_t)(id % (BK / 8));
       const uint32_t kk = 8u * c;
       // past k: an offset beyond the descriptor, which reads 0
@@ -617,8 +624,8 @@ __global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const
     const uint32_t klen = min((uint32_t)BK, k - kb);
 #pragma unroll
     for (int i = 0; i < UNITS; ++i) {
-      const int id = tid + NT * i;
-      if (UNITS_ALL % NT != 0 && id >= UNITS_ALL) break;
+      const int id = ptid + PT * i;
+      if (UNITS_ALL % PT != 0 && id >= UNITS_ALL) break;
       const int r = id / (BK / 32);
       const uint32_t u = (uint32_t)(id % (BK / 32));
       _Float16 *d = ws + r * BKP;
@@ -641,7 +648,7 @@ __global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const
     }
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
-      const int id = tid + NT * i;
+      const int id = ptid + PT * i;
       const int t = id / (BK / 8), c = id % (BK / 8);
       *(half8 *)(xs + t * BKP + 8 * c) = R.xr[i];
     }
@@ -658,11 +665,11 @@ __global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const
   // Fragments of 16-k substep ks; the next substep's are read while the
   // current one's MFMAs run (two register sets).
   auto frag = [&](const _Float16 *xa, const _Float16 *wa, int ks, half8 *a, half8 *bfr) {
-    const int kq = (wk * KS + ks) * 16 + 8 * (lane >> 5);
+    const int kq = (ck * KS + ks) * 16 + 8 * (lane >> 5);
 #pragma unroll
-    for (int i = 0; i < FM; ++i) a[i] = *(const half8 *)(xa + ((wm * FM + i) * 32 + (lane & 31)) * BKP + kq);
+    for (int i = 0; i < FM; ++i) a[i] = *(const half8 *)(xa + ((cm * FM + i) * 32 + (lane & 31)) * BKP + kq);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) bfr[j] = *(const half8 *)(wa + ((wn * FN + j) * 32 + (lane & 31)) * BKP + kq);
+    for (int j = 0; j < FN; ++j) bfr[j] = *(const half8 *)(wa + ((cn * FN + j) * 32 + (lane & 31)) * BKP + kq);
   };
   auto mma = [&](const _Float16 *xa, const _Float16 *wa) {
     half8 a[2][FM], bfr[2][FN];
@@ -682,31 +689,42 @@ __global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const
 
   const uint32_t steps = (k + BK - 1) / BK, last = steps - 1u;
   if constexpr (TYPE == IQ2_XXS) __syncthreads();  // grid staged
-  // Loads are never skipped (past the last step they repeat it), so the wait
-  // before each store covers exactly the older register set.
-  Regs RA, RB;
-  load_step(0, RA);
-  load_step(min(1u, last) * BK, RB);
-  store_step(0, RA, xs0, ws0);
-  load_step(min(2u, last) * BK, RA);
-  __syncthreads();
-  for (uint32_t st = 0; st < steps; st += 2) {
-    mma(xs0, ws0);
-    if (st + 1 < steps) store_step((st + 1) * BK, RB, xs1, ws1);
-    load_step(min(st + 3, last) * BK, RB);
+  if (producer) {
+    // Producer: three register sets, loads never skipped (past the last step
+    // they repeat it), so each wait covers exactly the oldest set.
+    Regs R0, R1, R2;
+    load_step(0, R0);
+    load_step(min(1u, last) * BK, R1);
+    load_step(min(2u, last) * BK, R2);
+    store_step(0, R0, xs0, ws0);
+    load_step(min(3u, last) * BK, R0);
     __syncthreads();
-    if (st + 1 < steps) mma(xs1, ws1);
-    if (st + 2 < steps) store_step((st + 2) * BK, RA, xs0, ws0);
-    load_step(min(st + 4, last) * BK, RA);
+    for (uint32_t st = 0; st < steps; st += 3) {
+      // during step st: step st+1 goes to the other stage
+      if (st + 1 < steps) store_step((st + 1) * BK, R1, ((st + 1) & 1) ? xs1 : xs0, ((st + 1) & 1) ? ws1 : ws0);
+      load_step(min(st + 4, last) * BK, R1);
+      __syncthreads();
+      if (st + 2 < steps) store_step((st + 2) * BK, R2, ((st + 2) & 1) ? xs1 : xs0, ((st + 2) & 1) ? ws1 : ws0);
+      load_step(min(st + 5, last) * BK, R2);
+      if (st + 1 < steps) __syncthreads();
+      if (st + 3 < steps) store_step((st + 3) * BK, R0, ((st + 3) & 1) ? xs1 : xs0, ((st + 3) & 1) ? ws1 : ws0);
+      load_step(min(st + 6, last) * BK, R0);
+      if (st + 2 < steps) __syncthreads();
+    }
+  } else {
     __syncthreads();
+    for (uint32_t st = 0; st < steps; ++st) {
+      mma((st & 1) ? xs1 : xs0, (st & 1) ? ws1 : ws0);
+      __syncthreads();
+    }
   }
 
   // k shares of the same fragments are added through LDS (the stages are free)
-  if constexpr (WK > 1) {
+  if constexpr (CK > 1) {
     float *red = (float *)gsm;
-    const int pair = wm * WN + wn;
-    for (int q = 1; q < WK; ++q) {
-      if (wk == q) {
+    const int pair = cm * CN + cn;
+    for (int q = 1; q < CK; ++q) {
+      if (!producer && ck == q) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -716,7 +734,7 @@ __global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const
               red[(((pair * FM + i) * FN + j) * 16 + v) * 64 + lane] = acc[i][j][v];
       }
       __syncthreads();
-      if (wk == 0) {
+      if (!producer && ck == 0) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -726,8 +744,8 @@ __global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const
       }
       __syncthreads();
     }
-    if (wk != 0) return;
   }
+  if (producer || ck != 0) return;
 
   // D[tok][row]: lane holds column (row) lane%32 and rows (tokens)
   // 8*(v/4) + 4*(lane/32) + v%4 of each 32x32 fragment.
@@ -735,10 +753,10 @@ __global__ __launch_bounds__(WM * WN * WK * 64) void k_gemm(WeightView wv, const
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const uint32_t row = n0 + (wn * FN + j) * 32 + (lane & 31);
+      const uint32_t row = n0 + (cn * FN + j) * 32 + (lane & 31);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const uint32_t tok = t0 + (wm * FM + i) * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const uint32_t tok = t0 + (cm * FM + i) * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         if (row < rows && tok < tokens) y[(uint64_t)tok * rows + row] = acc[i][j][v];
       }
     }
@@ -1037,39 +1055,37 @@ hipError_t launch_gemv(const WeightView &wv, const float *x, float *y, uint32_t 
   }
 }
 
-template <int TYPE, int BM, int BN, int BK, int WM, int WN, int WK>
+template <int TYPE, int BM, int BN, int BK, int CM, int CN, int CK>
 static hipError_t gemm_cfg(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
   // two operand stages, or the fragments of the k shares at the end (BM * BN
   // floats, in the same space), whichever is larger; then the IQ2_XXS grid
-  constexpr size_t stages = (size_t)2 * (BM + BN) * (BK + 8) * 2, red = WK > 1 ? (size_t)BM * BN * 4 : 0;
+  constexpr size_t stages = (size_t)2 * (BM + BN) * (BK + 8) * 2, red = CK > 1 ? (size_t)BM * BN * 4 : 0;
   constexpr size_t lds = (stages > red ? stages : red) + (TYPE == IQ2_XXS ? 2048 : 0);
   static_assert(lds <= 160 * 1024, "LDS");
   static bool attr = false;
   if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<TYPE, BM, BN, BK, WM, WN, WK>,
+    const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<TYPE, BM, BN, BK, CM, CN, CK>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr = true;
   }
   const uint32_t tok_tiles = (tokens + BM - 1) / BM, row_tiles = (wv.rows + BN - 1) / BN;
-  hipLaunchKernelGGL((k_gemm<TYPE, BM, BN, BK, WM, WN, WK>), dim3(row_tiles * tok_tiles), dim3(WM * WN * WK * 64), lds,
-                     s, wv, xh, y, tokens, row_tiles, tok_tiles);
+  hipLaunchKernelGGL((k_gemm<TYPE, BM, BN, BK, CM, CN, CK>), dim3(row_tiles * tok_tiles), dim3(512), lds, s, wv, xh,
+                     y, tokens, row_tiles, tok_tiles);
   return hipGetLastError();
 }
 
-// Tile by size, 8 waves (two per SIMD, so one wave's loads and dequantization
-// overlap the other's MFMAs): 256 x 128 tokens x rows for >= 1024 tokens
-// (k steps of 64; Q6_K units need steps of 128), 128 x 128 from 256 tokens,
-// else 128 tokens x 32 rows (small token counts are bound by the weight
-// bytes; narrow tiles spread them over the CUs). The waves that share a
-// fragment split each k step and are added at the end.
+// Tile by size: 256 x 128 tokens x rows for >= 1024 tokens (k steps of 64;
+// Q6_K units need steps of 128), 128 x 128 from 256 tokens, else 128 tokens x
+// 32 rows (small token counts are bound by the weight bytes; narrow tiles
+// spread them over the CUs).
 template <int TYPE>
 static hipError_t gemm_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
   if constexpr (TYPE != Q6_K) {
-    if (tokens >= 1024) return gemm_cfg<TYPE, 256, 128, 64, 2, 2, 2>(wv, xh, y, tokens, s);
+    if (tokens >= 1024) return gemm_cfg<TYPE, 256, 128, 64, 2, 2, 1>(wv, xh, y, tokens, s);
   }
-  if (tokens >= 256) return gemm_cfg<TYPE, 128, 128, 128, 1, 2, 4>(wv, xh, y, tokens, s);
-  return gemm_cfg<TYPE, 128, 32, 128, 1, 1, 8>(wv, xh, y, tokens, s);
+  if (tokens >= 256) return gemm_cfg<TYPE, 128, 128, 128, 2, 1, 2>(wv, xh, y, tokens, s);
+  return gemm_cfg<TYPE, 128, 32, 128, 1, 1, 4>(wv, xh, y, tokens, s);
 }
 
 hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *xh_scratch,
