@@ -486,11 +486,8 @@ __global__ __launch_bounds__(256) void k_gemv(WeightView wv, const float *__rest
 // ---------------------------------------------------------------------------
 // GEMM: Y[t][row] = sum_k fp16(W[row][k]) fp16(X[t][k]), fp32 accumulation.
 //
-// x is rounded to fp16 once by k_x_to_f16. A workgroup computes a tile of
-// 128 rows x 128 tokens in k steps of 128, with 4 waves of 64 x 64 (2 x 2
-// MFMA 32x32x16 f16 each). LDS holds two stages; the global loads of step
-// i+1 (raw weight units and fp16 x) are issued before the MFMAs of step i,
-// and decoded into the other stage afterwards, so one barrier per step.
+// x is rounded to fp16 once by k_x_to_f16; the tile kernel (k_gemm, below)
+// stages fp16 x and dequantized fp16 W through LDS for the MFMAs.
 // Weights are dequantized to fp16: Q8_0/Q8_0R with packed fp16 arithmetic
 // (q exact, then one rounding of q*d, i.e. fp16(d*q)), the other types as
 // the bit-exact f32 value rounded to fp16.
