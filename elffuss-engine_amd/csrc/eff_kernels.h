@@ -43,9 +43,16 @@ void gemv_mx_override(int waves, int ksplit);
 hipError_t launch_gemv_mx(const WeightView &wv, const float *x, float *y, uint32_t tokens,
                           const GemvPlan &p, hipStream_t stream);
 
-// x is first rounded to fp16 into `xh_scratch` (tokens * k halves).
+// x is first rounded to fp16 into `xh_scratch`, gemm_x_bytes(...) bytes laid
+// out as [token tile][k step][token][k] (zero past the tokens and past k).
+size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t k);
 hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *xh_scratch,
                        hipStream_t stream);
+// 256 x 256 tile GEMM with direct-to-LDS staging (Q8_0, >= 1024 tokens); x
+// in the [token tile][k step][256][64] layout.
+bool gemm_big_applies(int type, uint32_t tokens, uint32_t k);
+hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens,
+                           hipStream_t stream);
 
 hipError_t launch_dequant(const WeightView &wv, uint32_t n_blocks, float *out, hipStream_t stream);
 

@@ -80,54 +80,120 @@ __device__ __forceinline__ void unit_runs(uint32_t sub, uint32_t &o0, uint32_t &
   }
 }
 
+// Loading a unit is split in two: issue_raw issues the loads and keeps the
+// words as loaded; finish_raw re-assembles them (v_alignbyte of 2-byte aligned
+// runs, 16-bit fields, byte pairs) into Raw. Callers that prefetch call
+// finish_raw only where the unit is used, so that no instruction between the
+// loads and that point waits for them.
+template <int TYPE> struct RawLd {
+  Raw<TYPE> r;  // Q4_K, Q2_K: the loads are the final form
+};
+template <> struct RawLd<Q8_0> {
+  uint32_t sw, w[9], bp;
+};
+template <> struct RawLd<Q8_0R> {
+  uint32_t v[8], sw, so;
+};
+template <> struct RawLd<Q6_K> {
+  uint32_t ql[5], qh[5], s0, s1, dw, bp, sub;
+};
+template <> struct RawLd<IQ2_XXS> {
+  uint32_t a[3], dw, bp;
+};
+
 // Issue the loads of unit `sub` of block `bi` (counted from the first block of `src`).
 template <int TYPE>
-__device__ __forceinline__ void load_raw(Raw<TYPE> &r, const BufSrc &src, uint32_t bi, uint32_t sub) {
+__device__ __forceinline__ void issue_raw(RawLd<TYPE> &l, const BufSrc &src, uint32_t bi, uint32_t sub) {
   if constexpr (TYPE == Q8_0) {
-    const uint32_t bp = bi * 34u;
-    r.s = ld_u16_a2(src.q, bp);
-    ld_words_a2<8>(src.q, bp + 2u, r.v);
+    const uint32_t bp = bi * 34u, qb = (bp + 2u) & ~3u;
+    l.sw = ld32(src.q, bp & ~3u);
+#pragma unroll
+    for (int i = 0; i < 9; ++i) l.w[i] = ld32(src.q, qb + 4u * i);
+    l.bp = bp;
   } else if constexpr (TYPE == Q8_0R) {
-    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-    const u32x4v a = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)(bi * 32u), 0, 0);
-    const u32x4v b = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)(bi * 32u + 16u), 0, 0);
-    r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
-    r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
-    r.s = ld_u16_a2(src.s, bi * 2u);
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)(bi * 32u), 0, 0);
+    const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)(bi * 32u + 16u), 0, 0);
+    l.v[0] = a.x; l.v[1] = a.y; l.v[2] = a.z; l.v[3] = a.w;
+    l.v[4] = b.x; l.v[5] = b.y; l.v[6] = b.z; l.v[7] = b.w;
+    l.so = bi * 2u;
+    l.sw = ld32(src.s, l.so & ~3u);
   } else if constexpr (TYPE == Q4_K) {
-    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
     const uint32_t bp = bi * 144u;
-    const u32x4v h = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)bp, 0, 0);
-    const u32x4v q = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)(bp + 16u + 16u * sub), 0, 0);
-    r.hdr[0] = h.x; r.hdr[1] = h.y; r.hdr[2] = h.z; r.hdr[3] = h.w;
-    r.qs[0] = q.x; r.qs[1] = q.y; r.qs[2] = q.z; r.qs[3] = q.w;
-    r.sub = sub;
+    const u32x4 h = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)bp, 0, 0);
+    const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)(bp + 16u + 16u * sub), 0, 0);
+    l.r.hdr[0] = h.x; l.r.hdr[1] = h.y; l.r.hdr[2] = h.z; l.r.hdr[3] = h.w;
+    l.r.qs[0] = q.x; l.r.qs[1] = q.y; l.r.qs[2] = q.z; l.r.qs[3] = q.w;
+    l.r.sub = sub;
   } else if constexpr (TYPE == Q6_K) {
     const uint32_t bp = bi * 210u;
     const uint32_t n = sub >> 2, gp = (sub >> 1) & 1u, h = sub & 1u;
-    ld_words_a2<4>(src.q, bp + 16u * sub, r.ql);
-    ld_words_a2<4>(src.q, bp + 128u + 32u * n + 16u * h, r.qh);
+    const uint32_t lo = bp + 16u * sub, ho = bp + 128u + 32u * n + 16u * h;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) l.ql[i] = ld32(src.q, (lo & ~3u) + 4u * i);
+#pragma unroll
+    for (int i = 0; i < 5; ++i) l.qh[i] = ld32(src.q, (ho & ~3u) + 4u * i);
     // scales of groups gp and gp+2 at bytes 192 + 8n + 2g + h
     const uint32_t so = bp + 192u + 8u * n + 2u * gp + h;
-    r.sc = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(src.q, (int)so, 0, 0) |
-           ((uint32_t)__builtin_amdgcn_raw_buffer_load_b8(src.q, (int)(so + 4u), 0, 0) << 8);
-    r.d = ld_u16_a2(src.q, bp + 208u);
-    r.sub = sub;
+    l.s0 = __builtin_amdgcn_raw_buffer_load_b8(src.q, (int)so, 0, 0);
+    l.s1 = __builtin_amdgcn_raw_buffer_load_b8(src.q, (int)(so + 4u), 0, 0);
+    l.dw = ld32(src.q, (bp + 208u) & ~3u);
+    l.bp = bp;
+    l.sub = sub;
   } else if constexpr (TYPE == Q2_K) {
     const uint32_t bp = bi * 84u;
     const uint32_t n = sub >> 2, jp = (sub >> 1) & 1u, c = 2u * n + (sub & 1u);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r.qs[i] = ld32(src.q, bp + 16u + 16u * c + 4u * i);
-    r.sc = ld32(src.q, bp + 8u * n + 4u * jp);
-    r.dd = ld32(src.q, bp + 80u);
-    r.sub = sub;
+    for (int i = 0; i < 4; ++i) l.r.qs[i] = ld32(src.q, bp + 16u + 16u * c + 4u * i);
+    l.r.sc = ld32(src.q, bp + 8u * n + 4u * jp);
+    l.r.dd = ld32(src.q, bp + 80u);
+    l.r.sub = sub;
   } else {
-    const uint32_t bp = bi * 66u;
-    uint32_t a[2];
-    ld_words_a2<2>(src.q, bp + 2u + 8u * sub, a);
-    r.a0 = a[0]; r.a1 = a[1];
-    r.d = ld_u16_a2(src.q, bp);
+    const uint32_t bp = bi * 66u, ao = bp + 2u + 8u * sub;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) l.a[i] = ld32(src.q, (ao & ~3u) + 4u * i);
+    l.dw = ld32(src.q, bp & ~3u);
+    l.bp = bp;
   }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void finish_raw(const RawLd<TYPE> &l, Raw<TYPE> &r) {
+  if constexpr (TYPE == Q8_0) {
+    const uint32_t sh = (l.bp + 2u) & 3u;
+    r.s = (l.bp & 2u) ? (l.sw >> 16) : (l.sw & 0xFFFFu);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r.v[i] = __builtin_amdgcn_alignbyte(l.w[i + 1], l.w[i], sh);
+  } else if constexpr (TYPE == Q8_0R) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r.v[i] = l.v[i];
+    r.s = (l.so & 2u) ? (l.sw >> 16) : (l.sw & 0xFFFFu);
+  } else if constexpr (TYPE == Q6_K) {
+    const uint32_t n = l.sub >> 2, h = l.sub & 1u;
+    const uint32_t shl = (l.bp + 16u * l.sub) & 3u, shh = (l.bp + 128u + 32u * n + 16u * h) & 3u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r.ql[i] = __builtin_amdgcn_alignbyte(l.ql[i + 1], l.ql[i], shl);
+      r.qh[i] = __builtin_amdgcn_alignbyte(l.qh[i + 1], l.qh[i], shh);
+    }
+    r.sc = l.s0 | (l.s1 << 8);
+    r.d = ((l.bp + 208u) & 2u) ? (l.dw >> 16) : (l.dw & 0xFFFFu);
+    r.sub = l.sub;
+  } else if constexpr (TYPE == IQ2_XXS) {
+    // the unit's words start at block offset + 2 + 8 sub: the same alignment as + 2
+    const uint32_t sh = (l.bp + 2u) & 3u;
+    r.a0 = __builtin_amdgcn_alignbyte(l.a[1], l.a[0], sh);
+    r.a1 = __builtin_amdgcn_alignbyte(l.a[2], l.a[1], sh);
+    r.d = (l.bp & 2u) ? (l.dw >> 16) : (l.dw & 0xFFFFu);
+  } else {
+    r = l.r;
+  }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void load_raw(Raw<TYPE> &r, const BufSrc &src, uint32_t bi, uint32_t sub) {
+  RawLd<TYPE> l;
+  issue_raw<TYPE>(l, src, bi, sub);
+  finish_raw<TYPE>(l, r);
 }
 
 // 6-bit (scale, min) pair `idx` of a Q4_K block (SCALE_MIN_K4, kernels.wgsl.js:94-104).
@@ -495,13 +561,28 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 template <int TYPE> constexpr int gemm_bk() { return TYPE == Q6_K ? 128 : 64; }
 
+// One thread per 8 halves of the output, laid out as [token tile][k step]
+// [BM tokens][BK k]: the x slice of one tile and k step is one contiguous
+// run of BM * BK halves. Tokens past `tokens` and k past `k` are zero.
 __global__ __launch_bounds__(256) void k_x_to_f16(const float *__restrict__ x, _Float16 *__restrict__ xh,
-                                                  uint64_t n4) {
-  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-  if (i >= n4) return;
-  const float4 v = *(const float4 *)(x + 4 * i);
-  const half4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
-  *(half4 *)(xh + 4 * i) = h;
+                                                  uint32_t tokens, uint32_t k, uint32_t bm_log2, uint32_t bk_log2,
+                                                  uint32_t steps, uint64_t n8) {
+  const uint64_t o = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (o >= n8) return;
+  const uint32_t per_blk = 1u << (bm_log2 + bk_log2 - 3u);   // half8 per (tile, step)
+  const uint64_t blk = o >> (bm_log2 + bk_log2 - 3u);
+  const uint32_t in = (uint32_t)(o & (per_blk - 1u));
+  const uint32_t t = in >> (bk_log2 - 3u), c = in & ((1u << (bk_log2 - 3u)) - 1u);
+  const uint32_t tile = (uint32_t)(blk / steps), st = (uint32_t)(blk % steps);
+  const uint32_t tok = (tile << bm_log2) + t, kk = (st << bk_log2) + 8u * c;
+  half8 h = {};
+  if (tok < tokens && kk < k) {   // k is a multiple of 32, so all 8 values exist
+    const float4 a = *(const float4 *)(x + (uint64_t)tok * k + kk);
+    const float4 b = *(const float4 *)(x + (uint64_t)tok * k + kk + 4);
+    h[0] = (_Float16)a.x; h[1] = (_Float16)a.y; h[2] = (_Float16)a.z; h[3] = (_Float16)a.w;
+    h[4] = (_Float16)b.x; h[5] = (_Float16)b.y; h[6] = (_Float16)b.z; h[7] = (_Float16)b.w;
+  }
+  *(half8 *)(xh + 8 * o) = h;
 }
 
 // 32 fp16 weights of a unit: out[0..15] half A, out[16..31] half B.
@@ -551,7 +632,7 @@ __device__ __forceinline__ void unit_f16(const Raw<TYPE> &r, const uint32_t *gri
 // so that the workgroups of one XCD cover a contiguous run of row tiles with
 // all their token tiles: the x and W slices of a k step are shared through
 // that XCD's L2.
-template <int TYPE, int BM, int BN, int BK, int CM, int CN, int CK>
+template <int TYPE, int BM, int BN, int BK, int CM, int CN, int CK, int NS>
 __global__ __launch_bounds__(512) void k_gemm(WeightView wv, const _Float16 *__restrict__ xh,
                                               float *__restrict__ y, uint32_t tokens, uint32_t row_tiles,
                                               uint32_t tok_tiles) {
@@ -581,17 +662,16 @@ __global__ __launch_bounds__(512) void k_gemm(WeightView wv, const _Float16 *__r
   constexpr uint32_t upb = units_per_block<TYPE>();
   constexpr uint32_t E = block_elems<TYPE>();
   const BufSrc src = make_src(wv, (uint64_t)n0 * wv.bpr);
-  // fp16 x of this token tile; rows past `tokens` read as 0
-  const uint64_t xoff = (uint64_t)t0 * k;
-  const uint64_t xbytes = tokens > t0 ? (uint64_t)(tokens - t0) * k * 2u : 0;
-  const rsrc_t xsrc = make_rsrc(xh + xoff, xbytes);
+  const uint32_t steps = (k + BK - 1) / BK, last = steps - 1u;
+  // fp16 x of this token tile: steps runs of BM x BK halves (zero-padded)
+  const rsrc_t xsrc = make_rsrc(xh + (uint64_t)(t0 / BM) * steps * BM * BK, (uint64_t)steps * BM * BK * 2u);
 
   constexpr int UNITS_ALL = BN * (BK / 32);                   // weight units per step
   constexpr int UNITS = (UNITS_ALL + PT - 1) / PT;
   constexpr int XCH = BM * (BK / 8) / PT;                     // 8-half x chunks per producer thread
   static_assert(XCH * PT == BM * (BK / 8), "x chunks");
   struct Regs {
-    Raw<TYPE> raw[UNITS];
+    RawLd<TYPE> raw[UNITS];
     half8 xr[XCH];
   };
 
@@ -605,15 +685,12 @@ __global__ __launch_bounds__(512) void k_gemm(WeightView wv, const _Float16 *__r
       const uint32_t u = (uint32_t)(id % (BK / 32));
       const uint32_t lrow = min(n0 + (uint32_t)r, rows - 1u) - n0;
       const uint32_t gu = kb / 32u + min(u, klen / 32u - 1u);
-      load_raw<TYPE>(R.raw[i], src, lrow * wv.bpr + gu / upb, gu % upb);
+      issue_raw<TYPE>(R.raw[i], src, lrow * wv.bpr + gu / upb, gu % upb);
     }
+    // contiguous: thread id takes halves 8 id .. 8 id + 7 of the step's run
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
-      const int id = ptid + PT * i;
-      const uint32_t t = (uint32_t)(id / (BK / 8)), c = (uint32_t)(id % (BK / 8));
-      const uint32_t kk = 8u * c;
-      // past k: an offset beyond the descriptor, which reads 0
-      const uint32_t off = kk < klen ? (t * k + kb + kk) * 2u : 0xFFFFFFF0u;
+      const uint32_t off = (kb / BK) * (uint32_t)(BM * BK * 2) + 16u * (uint32_t)(ptid + PT * i);
       R.xr[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)off, 0, 0));
     }
   };
@@ -636,8 +713,10 @@ __global__ __launch_bounds__(512) void k_gemm(WeightView wv, const _Float16 *__r
       uint32_t o0, o1;
       unit_runs<TYPE>(gu % upb, o0, o1);
       const uint32_t c0 = (gu / upb) * E + o0 - kb, c1 = (gu / upb) * E + o1 - kb;
+      Raw<TYPE> raw;
+      finish_raw<TYPE>(R.raw[i], raw);
       half8 h[4];
-      unit_f16<TYPE>(R.raw[i], grid, h);
+      unit_f16<TYPE>(raw, grid, h);
       *(half8 *)(d + c0) = h[0];
       *(half8 *)(d + c0 + 8) = h[1];
       *(half8 *)(d + c1) = h[2];
@@ -684,29 +763,26 @@ __global__ __launch_bounds__(512) void k_gemm(WeightView wv, const _Float16 *__r
     }
   };
 
-  const uint32_t steps = (k + BK - 1) / BK, last = steps - 1u;
   if constexpr (TYPE == IQ2_XXS) __syncthreads();  // grid staged
   if (producer) {
-    // Producer: three register sets, loads never skipped (past the last step
-    // they repeat it), so each wait covers exactly the oldest set.
-    Regs R0, R1, R2;
-    load_step(0, R0);
-    load_step(min(1u, last) * BK, R1);
-    load_step(min(2u, last) * BK, R2);
-    store_step(0, R0, xs0, ws0);
-    load_step(min(3u, last) * BK, R0);
+    // Producer: NS register sets, loads never skipped (past the last step
+    // they repeat it), so each wait covers exactly the oldest set; the loads
+    // of a step go out NS - 1 steps before it is written to LDS.
+    Regs R[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) load_step(min((uint32_t)j, last) * BK, R[j]);
+    store_step(0, R[0], xs0, ws0);
+    load_step(min((uint32_t)NS, last) * BK, R[0]);
     __syncthreads();
-    for (uint32_t st = 0; st < steps; st += 3) {
-      // during step st: step st+1 goes to the other stage
-      if (st + 1 < steps) store_step((st + 1) * BK, R1, ((st + 1) & 1) ? xs1 : xs0, ((st + 1) & 1) ? ws1 : ws0);
-      load_step(min(st + 4, last) * BK, R1);
-      __syncthreads();
-      if (st + 2 < steps) store_step((st + 2) * BK, R2, ((st + 2) & 1) ? xs1 : xs0, ((st + 2) & 1) ? ws1 : ws0);
-      load_step(min(st + 5, last) * BK, R2);
-      if (st + 1 < steps) __syncthreads();
-      if (st + 3 < steps) store_step((st + 3) * BK, R0, ((st + 3) & 1) ? xs1 : xs0, ((st + 3) & 1) ? ws1 : ws0);
-      load_step(min(st + 6, last) * BK, R0);
-      if (st + 2 < steps) __syncthreads();
+    for (uint32_t st = 0; st < steps; st += NS) {
+#pragma unroll
+      for (int j = 1; j <= NS; ++j) {
+        // during step st + j - 1: step st + j goes to the other stage
+        const uint32_t sj = st + (uint32_t)j;
+        if (sj < steps) store_step(sj * BK, R[j % NS], (sj & 1) ? xs1 : xs0, (sj & 1) ? ws1 : ws0);
+        load_step(min(sj + (uint32_t)NS, last) * BK, R[j % NS]);
+        if (sj - 1u < steps) __syncthreads();
+      }
     }
   } else {
     __syncthreads();
@@ -1084,22 +1160,33 @@ hipError_t launch_gemv(const WeightView &wv, const float *x, float *y, uint32_t 
   }
 }
 
+// Register sets of the producer waves: as many as fit beside the MFMA
+// waves' accumulators (both roles share one register allocation of 256).
+template <int TYPE, int BM, int BN, int BK>
+constexpr int gemm_sets() {
+  constexpr int units = (BN * (BK / 32) + 255) / 256, xwords = 4 * (BM * (BK / 8) / 256);
+  constexpr int set = xwords + units * (int)(sizeof(RawLd<TYPE>) / 4);
+  constexpr int ns = 180 / set;
+  return ns < 3 ? 3 : ns > 5 ? 5 : ns;
+}
+
 template <int TYPE, int BM, int BN, int BK, int CM, int CN, int CK>
 static hipError_t gemm_cfg(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
   // two operand stages, or the fragments of the k shares at the end (BM * BN
   // floats, in the same space), whichever is larger; then the IQ2_XXS grid
   constexpr size_t stages = (size_t)2 * (BM + BN) * (BK + 8) * 2, red = CK > 1 ? (size_t)BM * BN * 4 : 0;
   constexpr size_t lds = (stages > red ? stages : red) + (TYPE == IQ2_XXS ? 2048 : 0);
+  constexpr int NS = gemm_sets<TYPE, BM, BN, BK>();
   static_assert(lds <= 160 * 1024, "LDS");
   static bool attr = false;
   if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<TYPE, BM, BN, BK, CM, CN, CK>,
+    const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<TYPE, BM, BN, BK, CM, CN, CK, NS>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr = true;
   }
   const uint32_t tok_tiles = (tokens + BM - 1) / BM, row_tiles = (wv.rows + BN - 1) / BN;
-  hipLaunchKernelGGL((k_gemm<TYPE, BM, BN, BK, CM, CN, CK>), dim3(row_tiles * tok_tiles), dim3(512), lds, s, wv, xh,
+  hipLaunchKernelGGL((k_gemm<TYPE, BM, BN, BK, CM, CN, CK, NS>), dim3(row_tiles * tok_tiles), dim3(512), lds, s, wv, xh,
                      y, tokens, row_tiles, tok_tiles);
   return hipGetLastError();
 }
@@ -1108,22 +1195,42 @@ static hipError_t gemm_cfg(const WeightView &wv, const _Float16 *xh, float *y, u
 // Q6_K units need steps of 128), 128 x 128 from 256 tokens, else 128 tokens x
 // 32 rows (small token counts are bound by the weight bytes; narrow tiles
 // spread them over the CUs).
+static bool gemm_wide(int type, uint32_t tokens) { return type != Q6_K && tokens >= 1024; }
+
 template <int TYPE>
 static hipError_t gemm_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
   if constexpr (TYPE != Q6_K) {
-    if (tokens >= 1024) return gemm_cfg<TYPE, 256, 128, 64, 2, 2, 1>(wv, xh, y, tokens, s);
+    if (gemm_wide(TYPE, tokens)) return gemm_cfg<TYPE, 256, 128, 64, 2, 2, 1>(wv, xh, y, tokens, s);
   }
   if (tokens >= 256) return gemm_cfg<TYPE, 128, 128, 128, 2, 1, 2>(wv, xh, y, tokens, s);
   return gemm_cfg<TYPE, 128, 32, 128, 1, 1, 4>(wv, xh, y, tokens, s);
 }
 
+// Token tile and k step of the chosen configuration (log2), as the x layout needs them.
+static void gemm_x_tile(int type, uint32_t tokens, uint32_t &bm_log2, uint32_t &bk_log2) {
+  // (the 256 x 256 kernel uses the wide layout too)
+  if (gemm_wide(type, tokens)) { bm_log2 = 8; bk_log2 = 6; } else { bm_log2 = 7; bk_log2 = 7; }
+}
+
+size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t k) {
+  uint32_t bm, bk;
+  gemm_x_tile(type, tokens, bm, bk);
+  const uint64_t tiles = (tokens + (1u << bm) - 1) >> bm, steps = (k + (1u << bk) - 1) >> bk;
+  return (size_t)(tiles * steps) << (bm + bk + 1);
+}
+
 hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *xh_scratch,
                        hipStream_t s) {
-  const uint64_t n4 = (uint64_t)tokens * wv.k / 4;
+  uint32_t bm, bk;
+  gemm_x_tile(wv.type, tokens, bm, bk);
+  const uint32_t steps = (wv.k + (1u << bk) - 1) >> bk;
+  const uint64_t n8 = (uint64_t)gemm_x_bytes(wv.type, tokens, wv.k) / 16u;
   _Float16 *xh = (_Float16 *)xh_scratch;
-  hipLaunchKernelGGL(k_x_to_f16, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, s, x, xh, n4);
+  hipLaunchKernelGGL(k_x_to_f16, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, s, x, xh, tokens, wv.k, bm, bk,
+                     steps, n8);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (gemm_big_applies(wv.type, tokens, wv.k)) return launch_gemm_big(wv, xh, y, tokens, s);
   switch (wv.type) {
     case Q8_0: return gemm_go<Q8_0>(wv, xh, y, tokens, s);
     case Q8_0R: return gemm_go<Q8_0R>(wv, xh, y, tokens, s);
