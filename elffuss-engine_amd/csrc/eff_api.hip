@@ -144,7 +144,7 @@ int grow(eff_ctx *ctx, void **p, size_t *have, size_t need, const char *what) {
 }
 
 int run_gemm(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
-  int rc = grow(ctx, &ctx->xh_scratch, &ctx->xh_scratch_bytes, gemm_x_bytes(wv.type, tokens, wv.k), "gemm x");
+  int rc = grow(ctx, &ctx->xh_scratch, &ctx->xh_scratch_bytes, gemm_x_bytes(wv.type, tokens, wv.k, wv.rows), "gemm x");
   if (rc) return rc;
   hipError_t e = launch_gemm(wv, x, y, tokens, ctx->xh_scratch, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");

@@ -25,7 +25,7 @@
 //
 // The k order inside an MFMA is free as long as both operands follow it:
 // slot m (16 k) of a step takes, in lane half h, the 8 weights
-// 16 m + 8 h .. 16 m + 8 h + 7 of the step (block m / 2).
+// 16 h + 8 (m & 1) .. + 7 of block m / 2 of the step.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -38,16 +38,15 @@ namespace eff {
 
 namespace {
 
-constexpr uint32_t kBM = 256, kBN = 256, kBK = 64;
-constexpr uint32_t kXS = kBM * kBK * 2;   // x stage bytes (32 KB)
+constexpr uint32_t kBN = 256, kBK = 64;   // tile rows, k per step
 constexpr uint32_t kRB = 80;              // raw weight bytes per row and stage
 constexpr uint32_t kWS = kBN * kRB;       // weight stage bytes (20 KB)
-constexpr uint32_t kXDma = kXS / 4096;    // x loads per wave and step (64 lanes x 16 bytes)
-constexpr uint32_t kWDma = kWS / 4096;    // weight loads per wave and step
-constexpr uint32_t kDma = kXDma + kWDma;  // all loads per wave and step
-// waves along tokens x along rows, and 32 x 32 fragments per wave
-constexpr uint32_t kWM = 1, kWN = 4, kFM = kBM / 32 / kWM, kFN = kBN / 32 / kWN;
-static_assert(kWS % 4096 == 0 && kXS % 4096 == 0, "whole loads per wave");
+constexpr uint32_t kWG = kWS / 1024;      // weight loads per step (64 lanes x 16 bytes each)
+// waves along tokens x along rows (one wave per SIMD); 32 x 32 fragments
+// along rows per wave
+constexpr uint32_t kWM = 1, kWN = 4, kNW = kWM * kWN, kFN = kBN / 32 / kWN;
+constexpr uint32_t kWDma = (kWG + kNW - 1) / kNW;  // weight loads of a wave per step (at most)
+static_assert(kWS % 1024 == 0, "whole loads");
 
 // 16 bytes per lane from the buffer (voffset + soffset) into LDS at
 // lds + 16 * lane. Written as inline assembly so that the compiler, which
@@ -55,9 +54,10 @@ static_assert(kWS % 4096 == 0 && kXS % 4096 == 0, "whole loads per wave");
 // reads of the other stages; the waits are explicit (wait_vm).
 __device__ __forceinline__ void dma16(rsrc_t r, const uint8_t *lds, uint32_t voff, uint32_t soff) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
-               : "s"(m0), "v"(voff), "s"(r), "s"(soff)
+               : "s"(m0), "v"(voff), "s"(r), "s"(so)
                : "memory", "m0");
 }
 
@@ -70,9 +70,18 @@ __device__ __forceinline__ void wait_vm() {
 
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const uint32_t *)p; }
 
-__global__ __launch_bounds__(256) void k_gemm_q8(WeightView wv, const _Float16 *__restrict__ xh,
+// BM tokens per tile; KS workgroups split k (KS = 2: the two halves are
+// added into y, zeroed beforehand, with atomic adds, which give the same
+// bits in either order: 0 + a + b = a + b).
+template <uint32_t BM, uint32_t KS>
+__global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Float16 *__restrict__ xh,
                                                  float *__restrict__ y, uint32_t tokens, uint32_t row_tiles,
                                                  uint32_t tok_tiles) {
+  constexpr uint32_t kXS = BM * kBK * 2;   // x stage bytes
+  constexpr uint32_t kXDma = kXS / 1024 / kNW;  // x loads per wave and step
+  static_assert(kXS % (1024 * kNW) == 0, "x loads");
+  constexpr uint32_t kFM = BM / 32 / kWM;
+  static_assert(KS >= 1 && KS <= 2, "tile");
   // three stages, each x (kXS bytes) then W (kWS bytes); separate objects,
   // so that the compiler can tell loads into one stage from reads of another
   __shared__ __align__(16) uint8_t st0[kXS + kWS];
@@ -86,15 +95,20 @@ __global__ __launch_bounds__(256) void k_gemm_q8(WeightView wv, const _Float16 *
   // Tiles are dealt so that the workgroups of one XCD (blockIdx % 8) take a
   // contiguous run of tiles, token tiles fastest: they share x and W slices
   // through that XCD's L2.
-  const uint32_t ntiles = row_tiles * tok_tiles;
+  // (k halves slowest: the XCDs of one half share its x and W slices)
+  const uint32_t ntiles = row_tiles * tok_tiles * KS;
   uint32_t lin = blockIdx.x;
   if (ntiles % 8u == 0u) lin = (blockIdx.x % 8u) * (ntiles / 8u) + blockIdx.x / 8u;
-  const uint32_t n0 = (lin / tok_tiles) * kBN, tt = lin % tok_tiles, t0 = tt * kBM;
+  const uint32_t kq = lin / (row_tiles * tok_tiles);
+  lin %= row_tiles * tok_tiles;
+  const uint32_t n0 = (lin / tok_tiles) * kBN, tt = lin % tok_tiles, t0 = tt * BM;
   const uint32_t rows = wv.rows, k = wv.k;
-  const uint32_t steps = (k + kBK - 1u) / kBK, last = steps - 1u;
+  const uint32_t steps_all = (k + kBK - 1u) / kBK;
+  // this workgroup's steps: s0 .. s0 + steps - 1 (absolute step numbers)
+  const uint32_t s0 = kq * steps_all / KS, steps = (kq + 1u) * steps_all / KS - s0, last = steps - 1u;
 
   // Sources: x run of this token tile, weight rows from the tile's first row.
-  const rsrc_t xsrc = make_rsrc(xh + (uint64_t)tt * steps * (kBM * kBK), (uint64_t)steps * kXS);
+  const rsrc_t xsrc = make_rsrc(xh + (uint64_t)tt * steps_all * (BM * kBK), (uint64_t)steps_all * kXS);
   const BufSrc src = make_src(wv, (uint64_t)n0 * wv.bpr);
   const uint32_t rb = (uint32_t)wv.row_bytes;
   const uint32_t rmax = rows - 1u - n0;  // last valid row of the tile (rows past it repeat it)
@@ -103,27 +117,37 @@ __global__ __launch_bounds__(256) void k_gemm_q8(WeightView wv, const _Float16 *
   // 64 (8 w + j) + lane = 8 t + p of the stage, token t, stored chunk p,
   // holding x chunk c = p ^ (t & 7) (t & 7 = lane >> 3 here).
   const uint32_t xl = (lane >> 3) * 128u + (((lane & 7u) ^ (lane >> 3)) << 4);
-  // W: chunk q = 64 (5 w + j) + lane is chunk q % 5 of row q / 5.
+  // W: load j of wave w is load g = w + kNW j of the step (those with
+  // g < kWG); its chunk q = 64 g + lane is chunk q % 5 of row q / 5.
+  const uint32_t nwl = wave < kWG % kNW || kWG % kNW == 0 ? kWDma : kWDma - 1u;
   uint32_t wl[kWDma];
 #pragma unroll
   for (uint32_t j = 0; j < kWDma; ++j) {
-    const uint32_t q = 64u * (kWDma * wave + j) + lane, r = q / 5u;
+    const uint32_t q = 64u * min(wave + kNW * j, kWG - 1u) + lane, r = q / 5u;
     wl[j] = min(r, rmax) * rb + 16u * (q - 5u * r);
   }
   // The loads of one step, in four groups (issued one per k slot, so that
   // the texture unit, shared by the CU's waves, is busy all step long).
   auto issue_group = [&](int g, uint32_t s, const uint8_t *xs, const uint8_t *ws) {
 #pragma unroll
-    for (uint32_t i = 0; i < kDma; ++i) {
+    for (uint32_t i = 0; i < kXDma + kWDma; ++i) {
       if ((int)(i % 4u) != g) continue;
       if (i < kXDma) {
         const uint32_t slot = kXDma * wave + i;
-        dma16(xsrc, xs + 1024u * slot, xl + 1024u * slot, s * kXS);
+        dma16(xsrc, xs + 1024u * slot, xl + 1024u * slot, (s0 + s) * kXS);
       } else {
         const uint32_t j = i - kXDma;
-        dma16(src.q, ws + 1024u * (kWDma * wave + j), wl[j], s * 68u);
+        if (j < nwl) dma16(src.q, ws + 1024u * (wave + kNW * j), wl[j], (s0 + s) * 68u);
       }
     }
+  };
+  // wait until this wave's loads of the previous step are complete (the
+  // next step's may be outstanding)
+  auto wait_prev = [&]() {
+    if (kWG % kNW == 0 || nwl == kWDma)
+      wait_vm<kXDma + kWDma>();
+    else
+      wait_vm<kXDma + kWDma - 1>();
   };
   auto issue = [&](uint32_t s, const uint8_t *xs, const uint8_t *ws) {
 #pragma unroll
@@ -136,8 +160,8 @@ __global__ __launch_bounds__(256) void k_gemm_q8(WeightView wv, const _Float16 *
   const uint32_t abase = (kFM * 32u * wm + n) * 128u;
   uint32_t acol[4];
 #pragma unroll
-  for (uint32_t m = 0; m < 4; ++m) acol[m] = ((2u * m + h) ^ (n & 7u)) << 4;
-  const uint32_t bbase = (kFN * 32u * wn + n) * kRB + 8u * h;
+  for (uint32_t m = 0; m < 4; ++m) acol[m] = ((4u * (m >> 1) + 2u * h + (m & 1u)) ^ (n & 7u)) << 4;
+  const uint32_t brow = (kFN * 32u * wn + n) * kRB;
 
   float16v acc[kFM][kFN];
 #pragma unroll
@@ -150,119 +174,142 @@ __global__ __launch_bounds__(256) void k_gemm_q8(WeightView wv, const _Float16 *
   typedef _Float16 half2v __attribute__((ext_vector_type(2)));
   const half2v off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
 
-  // Operands of k slot m: A fragments from the x stage, B fragments decoded
-  // from the raw weights (quants of block m / 2 at bytes 34 (m/2) + 2 +
-  // 16 (m&1) + 8 h of the row: 2 past a multiple of 8 for block 0, re-aligned
-  // with v_alignbyte, which shifts by 0..3 bytes; on a 4-byte boundary for
-  // block 1).
+  // Operands. Slot m takes, in lane half h, the weights 16 h + 8 (m & 1) ..
+  // + 7 of block m / 2 (and the same k of x). A fragments come from the x
+  // stage; the B fragments of both slots of block u are decoded from the
+  // two 16-byte chunks at byte 32 u + 16 h of the row (read whole: 16-byte
+  // reads of 8 rows hit 8 different bank groups, as the 80-byte row stride
+  // is 5 chunks), in which the lane's 16 quants start 2 + 2 u bytes in
+  // (re-aligned with v_alignbyte, which shifts by 0..3 bytes, for block 0).
   auto load_a = [&](const uint8_t *xs, int m, half8 *a) {
 #pragma unroll
     for (int fi = 0; fi < (int)kFM; ++fi) a[fi] = *(const half8 *)(xs + abase + fi * 4096u + acol[m]);
   };
-  auto load_b = [&](const uint8_t *ws, int m, uint32_t (*q)[2]) {
-    const uint32_t c0 = 34u * (uint32_t)(m >> 1) + 2u + 16u * (uint32_t)(m & 1);
+  auto load_b = [&](const uint8_t *ws, int u, uint32_t (*q)[4]) {
 #pragma unroll
     for (int fj = 0; fj < (int)kFN; ++fj) {
-      const uint8_t *rp = ws + bbase + fj * (32u * kRB);
-      if ((m >> 1) == 0) {
-        const uint2 lo = *(const uint2 *)(rp + (c0 & ~7u));
-        const uint32_t hi = lds_u32(rp + (c0 & ~7u) + 8u);
-        q[fj][0] = __builtin_amdgcn_alignbyte(lo.y, lo.x, c0 & 3u);
-        q[fj][1] = __builtin_amdgcn_alignbyte(hi, lo.y, c0 & 3u);
+      const uint8_t *rp = ws + brow + fj * (32u * kRB) + 32u * (uint32_t)u + 16u * h;
+      const u32x4 c0 = *(const u32x4 *)rp, c1 = *(const u32x4 *)(rp + 16);
+      if (u == 0) {
+        q[fj][0] = __builtin_amdgcn_alignbyte(c0.y, c0.x, 2);
+        q[fj][1] = __builtin_amdgcn_alignbyte(c0.z, c0.y, 2);
+        q[fj][2] = __builtin_amdgcn_alignbyte(c0.w, c0.z, 2);
+        q[fj][3] = __builtin_amdgcn_alignbyte(c1.x, c0.w, 2);
       } else {
-        q[fj][0] = lds_u32(rp + c0);
-        q[fj][1] = lds_u32(rp + c0 + 4u);
+        q[fj][0] = c0.y; q[fj][1] = c0.z; q[fj][2] = c0.w; q[fj][3] = c1.x;
       }
     }
   };
-  auto decode = [&](const uint32_t (*q)[2], const half2v *d, half8 *b) {
-#pragma unroll
-    for (int fj = 0; fj < (int)kFN; ++fj) {
-      const uint32_t q0 = q[fj][0] ^ 0x80808080u, q1 = q[fj][1] ^ 0x80808080u;
-      const half2v e0 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, q0, 0x04010400u));
-      const half2v e1 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, q0, 0x04030402u));
-      const half2v e2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, q1, 0x04010400u));
-      const half2v e3 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, q1, 0x04030402u));
-      const half2v v0 = (e0 + off) * d[fj], v1 = (e1 + off) * d[fj], v2 = (e2 + off) * d[fj],
-                   v3 = (e3 + off) * d[fj];
-      b[fj] = half8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
-    }
+  // quants q0, q1 (8 signed bytes) -> fp16(d * q)
+  auto decode8 = [&](uint32_t q0, uint32_t q1, half2v d) {
+    q0 ^= 0x80808080u;
+    q1 ^= 0x80808080u;
+    const half2v e0 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, q0, 0x04010400u));
+    const half2v e1 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, q0, 0x04030402u));
+    const half2v e2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, q1, 0x04010400u));
+    const half2v e3 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, q1, 0x04030402u));
+    const half2v v0 = (e0 + off) * d, v1 = (e1 + off) * d, v2 = (e2 + off) * d, v3 = (e3 + off) * d;
+    return half8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
   };
 
-  // One step from stage (xs, ws), with the loads of a later step going to
-  // (xn, wn_) in four groups; `full` is false on a last step holding one
-  // block only (k % 64 == 32): the second block's weights are zero. The
-  // operands of slot m + 1 are read and decoded while the 16 MFMAs of slot m
-  // run.
-  auto compute = [&](const uint8_t *xs, const uint8_t *ws, bool full, uint32_t sn, const uint8_t *xn,
-                     const uint8_t *wn_) {
-    // block scales of the lane's 4 rows: byte 0 (block 0), byte 34 (block 1)
-    half2v d0[kFN], d1[kFN];
+  // Block scales of the lane's rows in stage ws: byte 0 (block 0) and byte
+  // 34 (block 1); `full` is false on a last step holding one block only
+  // (k % 64 == 32): the second block's weights are then zero.
+  half2v d0[kFN], d1[kFN];
+  auto scales = [&](const uint8_t *ws, bool full) {
 #pragma unroll
     for (int fj = 0; fj < (int)kFN; ++fj) {
-      const uint8_t *rp = ws + bbase - 8u * h + fj * (32u * kRB);
+      const uint8_t *rp = ws + brow + fj * (32u * kRB);
       const uint32_t w0 = lds_u32(rp), w1 = lds_u32(rp + 32);
       const _Float16 s0 = __builtin_bit_cast(_Float16, (uint16_t)(w0 & 0xFFFFu));
       const _Float16 s1 = full ? __builtin_bit_cast(_Float16, (uint16_t)(w1 >> 16)) : (_Float16)0.0f;
       d0[fj] = half2v{s0, s0};
       d1[fj] = half2v{s1, s1};
     }
-    half8 a[2][kFM], b[2][kFN];
-    uint32_t q[kFN][2];
-    load_a(xs, 0, a[0]);
-    load_b(ws, 0, q);
-    decode(q, d0, b[0]);
+  };
+  half8 a[2][kFM], bb[2][2][kFN];   // A per slot; B per block (both slots)
+  uint32_t q[kFN][4];
+  // operands of slot m (from stage st): A, and for an even slot the B of its block
+  auto operands = [&](const uint8_t *st, int m) {
+    load_a(st, m, a[m & 1]);
+    if ((m & 1) == 0) {
+      const int u = m >> 1;
+      load_b(st + kXS, u, q);
+#pragma unroll
+      for (int fj = 0; fj < (int)kFN; ++fj) {
+        const half2v d = u == 0 ? d0[fj] : d1[fj];
+        bb[u][0][fj] = decode8(q[fj][0], q[fj][1], d);
+        bb[u][1][fj] = decode8(q[fj][2], q[fj][3], d);
+      }
+    }
+  };
+
+  // the last step of k holds one block
+  const bool tail_half = (k % kBK) != 0u && s0 + steps == steps_all;
+  // Step s computes from stage cur; the operands of slot m + 1 are read and
+  // decoded while the 16 MFMAs of slot m run, and the loads of step s + 2
+  // go to stage tgt in four groups. Before the last slot's MFMAs, the wave
+  // waits for its loads of step s + 1 (at most the kDma loads of step s + 2
+  // may still be outstanding) and meets the others at a barrier: stage nxt
+  // is then complete, and every wave is done reading stage cur, which the
+  // loads of step s + 3 (issued during step s + 1) overwrite. Slot 0 of
+  // step s + 1 is then prepared during the last MFMAs of step s.
+  auto step = [&](uint32_t s, const uint8_t *cur, const uint8_t *nxt, const uint8_t *tgt) {
+    const uint32_t sn = min(s + 2u, last);
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      issue_group(m, sn, xn, wn_);
+      issue_group(m, sn, tgt, tgt + kXS);
       if (m < 3) {
-        load_a(xs, m + 1, a[(m + 1) & 1]);
-        load_b(ws, m + 1, q);
-        decode(q, (m + 1) >= 2 ? d1 : d0, b[(m + 1) & 1]);
+        operands(cur, m + 1);
+      } else {
+        wait_prev();
+        __builtin_amdgcn_s_barrier();
+        scales(nxt + kXS, !(tail_half && s + 1u == last));
+        operands(nxt, 0);
       }
 #pragma unroll
       for (int fi = 0; fi < (int)kFM; ++fi)
 #pragma unroll
         for (int fj = 0; fj < (int)kFN; ++fj)
-          acc[fi][fj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[m & 1][fi], b[m & 1][fj], acc[fi][fj], 0, 0, 0);
+          acc[fi][fj] =
+              __builtin_amdgcn_mfma_f32_32x32x16_f16(a[m & 1][fi], bb[m >> 1][m & 1][fj], acc[fi][fj], 0, 0, 0);
       // schedule: the next slot's LDS reads first, three MFMAs while they
-      // land, then its decode interleaved with the remaining MFMAs
-      if (m < 3) {
-        __builtin_amdgcn_sched_group_barrier(0x100, kFM + 2 * kFN, 0);  // LDS reads
-        __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);               // 3 MFMA
+      // land, then the decode of the next block (odd m) interleaved with
+      // the remaining MFMAs
+      if (m == 3)
+        __builtin_amdgcn_sched_group_barrier(0x100, kFM + 4 * kFN, 0);  // A, B and next scales
+      else if (m == 1)
+        __builtin_amdgcn_sched_group_barrier(0x100, kFM + 2 * kFN, 0);  // A and B
+      else
+        __builtin_amdgcn_sched_group_barrier(0x100, kFM, 0);            // A
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);                // 3 MFMA
 #pragma unroll
-        for (int i = 0; i < (int)(kFM * kFN) - 3; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x002, (16 * kFN + kFM * kFN - 4) / (kFM * kFN - 3), 0);  // VALU
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                            // 1 MFMA
-        }
+      for (int i = 0; i < (int)(kFM * kFN) - 3; ++i) {
+        if (m & 1)
+          __builtin_amdgcn_sched_group_barrier(0x002, (34 * kFN + kFM * kFN - 4) / (kFM * kFN - 3), 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                            // 1 MFMA
       }
     }
   };
 
-  const bool tail_half = (k % kBK) != 0u;  // the last step holds one block
-  // Step s: its loads (issued during step s - 2) are complete once at most
-  // the next step's kDma loads are outstanding; the barrier makes every
-  // wave's loads visible and frees the stage the loads of step s + 2 go to
-  // (read in step s - 1).
-  auto step = [&](uint32_t s, const uint8_t *xs, const uint8_t *ws, const uint8_t *xn, const uint8_t *wn_) {
-    wait_vm<kDma>();
-    __builtin_amdgcn_s_barrier();
-    compute(xs, ws, !(tail_half && s == last), min(s + 2u, last), xn, wn_);
-  };
-
   issue(0, st0, st0 + kXS);
   issue(min(1u, last), st1, st1 + kXS);
+  wait_prev();
+  __builtin_amdgcn_s_barrier();
+  scales(st0 + kXS, !(tail_half && last == 0u));
+  operands(st0, 0);
   // three steps per iteration, so that the stages are fixed objects; the
   // last one or two steps after the loop (no branch inside the loop: the
-  // accumulators stay in place)
+  // accumulators stay in place). After the last step, the reads of a
+  // following step see stale stage contents and are not used.
   uint32_t s = 0;
   for (; s + 3u <= steps; s += 3u) {
-    step(s, st0, st0 + kXS, st2, st2 + kXS);
-    step(s + 1u, st1, st1 + kXS, st0, st0 + kXS);
-    step(s + 2u, st2, st2 + kXS, st1, st1 + kXS);
+    step(s, st0, st1, st2);
+    step(s + 1u, st1, st2, st0);
+    step(s + 2u, st2, st0, st1);
   }
-  if (s < steps) step(s, st0, st0 + kXS, st2, st2 + kXS);
-  if (s + 1u < steps) step(s + 1u, st1, st1 + kXS, st0, st0 + kXS);
+  if (s < steps) step(s, st0, st1, st2);
+  if (s + 1u < steps) step(s + 1u, st1, st2, st0);
   wait_vm<0>();
 
   // D[tok][row]: lane holds row (column) n of each fragment and tokens
@@ -276,22 +323,48 @@ __global__ __launch_bounds__(256) void k_gemm_q8(WeightView wv, const _Float16 *
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const uint32_t tok = t0 + kFM * 32u * wm + 32u * fi + 8u * (v >> 2) + 4u * h + (v & 3);
-        if (tok < tokens) y[(uint64_t)tok * rows + row] = acc[fi][fj][v];
+        if (tok < tokens) {
+          if constexpr (KS == 1)
+            y[(uint64_t)tok * rows + row] = acc[fi][fj][v];
+          else
+            unsafeAtomicAdd(y + (uint64_t)tok * rows + row, acc[fi][fj][v]);
+        }
       }
   }
 }
 
-}  // namespace
 
-bool gemm_big_applies(int type, uint32_t tokens, uint32_t k) {
-  return type == Q8_0 && tokens >= 1024 && k % 32u == 0;
+__global__ __launch_bounds__(256) void k_zero(float4 *__restrict__ p, uint64_t n4) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (i < n4) p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
-hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
-  const uint32_t tok_tiles = (tokens + kBM - 1) / kBM, row_tiles = (wv.rows + kBN - 1) / kBN;
-  hipLaunchKernelGGL(k_gemm_q8, dim3(row_tiles * tok_tiles), dim3(256), 0, s, wv, xh, y, tokens, row_tiles,
-                     tok_tiles);
+template <uint32_t BM, uint32_t KS>
+hipError_t gemm_q8_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
+  const uint32_t tok_tiles = (tokens + BM - 1) / BM, row_tiles = (wv.rows + kBN - 1) / kBN;
+  if (KS > 1) {
+    // y is zeroed by a kernel (not a memset node) so that graph replays stay exact
+    const uint64_t n4 = (uint64_t)tokens * wv.rows / 4u;
+    hipLaunchKernelGGL(k_zero, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, s, (float4 *)y, n4);
+  }
+  hipLaunchKernelGGL((k_gemm_q8<BM, KS>), dim3(row_tiles * tok_tiles * KS), dim3(kNW * 64), 0, s, wv, xh, y, tokens,
+                     row_tiles, tok_tiles);
   return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows) {
+  return type == Q8_0 && tokens >= 256 && k % 32u == 0 && (tokens >= 1024 || ((uint64_t)tokens * rows) % 4u == 0);
+}
+
+uint32_t gemm_big_tile_log2(uint32_t tokens) { return tokens >= 1024 ? 8u : 7u; }
+
+hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
+  // >= 1024 tokens: 256-token tiles fill the GPU; below, 128-token tiles
+  // with k split in two
+  if (tokens >= 1024) return gemm_q8_go<256, 1>(wv, xh, y, tokens, s);
+  return gemm_q8_go<128, 1>(wv, xh, y, tokens, s);
 }
 
 }  // namespace eff

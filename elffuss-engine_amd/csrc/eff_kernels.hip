@@ -1207,14 +1207,21 @@ static hipError_t gemm_go(const WeightView &wv, const _Float16 *xh, float *y, ui
 }
 
 // Token tile and k step of the chosen configuration (log2), as the x layout needs them.
-static void gemm_x_tile(int type, uint32_t tokens, uint32_t &bm_log2, uint32_t &bk_log2) {
-  // (the 256 x 256 kernel uses the wide layout too)
-  if (gemm_wide(type, tokens)) { bm_log2 = 8; bk_log2 = 6; } else { bm_log2 = 7; bk_log2 = 7; }
+static void gemm_x_tile(int type, uint32_t tokens, uint32_t k, uint32_t rows, uint32_t &bm_log2,
+                        uint32_t &bk_log2) {
+  if (gemm_big_applies(type, tokens, k, rows)) {
+    bm_log2 = gemm_big_tile_log2(tokens);
+    bk_log2 = 6;
+  } else if (gemm_wide(type, tokens)) {
+    bm_log2 = 8; bk_log2 = 6;
+  } else {
+    bm_log2 = 7; bk_log2 = 7;
+  }
 }
 
-size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t k) {
+size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t k, uint32_t rows) {
   uint32_t bm, bk;
-  gemm_x_tile(type, tokens, bm, bk);
+  gemm_x_tile(type, tokens, k, rows, bm, bk);
   const uint64_t tiles = (tokens + (1u << bm) - 1) >> bm, steps = (k + (1u << bk) - 1) >> bk;
   return (size_t)(tiles * steps) << (bm + bk + 1);
 }
@@ -1222,15 +1229,15 @@ size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t k) {
 hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *xh_scratch,
                        hipStream_t s) {
   uint32_t bm, bk;
-  gemm_x_tile(wv.type, tokens, bm, bk);
+  gemm_x_tile(wv.type, tokens, wv.k, wv.rows, bm, bk);
   const uint32_t steps = (wv.k + (1u << bk) - 1) >> bk;
-  const uint64_t n8 = (uint64_t)gemm_x_bytes(wv.type, tokens, wv.k) / 16u;
+  const uint64_t n8 = (uint64_t)gemm_x_bytes(wv.type, tokens, wv.k, wv.rows) / 16u;
   _Float16 *xh = (_Float16 *)xh_scratch;
   hipLaunchKernelGGL(k_x_to_f16, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, s, x, xh, tokens, wv.k, bm, bk,
                      steps, n8);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (gemm_big_applies(wv.type, tokens, wv.k)) return launch_gemm_big(wv, xh, y, tokens, s);
+  if (gemm_big_applies(wv.type, tokens, wv.k, wv.rows)) return launch_gemm_big(wv, xh, y, tokens, s);
   switch (wv.type) {
     case Q8_0: return gemm_go<Q8_0>(wv, xh, y, tokens, s);
     case Q8_0R: return gemm_go<Q8_0R>(wv, xh, y, tokens, s);
