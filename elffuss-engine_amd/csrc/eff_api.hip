@@ -118,7 +118,9 @@ int weight_view(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint
 int run_gemv(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
   GemvPlan p;
   hipError_t e;
-  if (ctx->gemv_kernel == 0 && gemv_mx_plan(wv, tokens, p)) {
+  if (ctx->gemv_kernel == 0 && gemv_mt_plan(wv, tokens, p)) {
+    e = launch_gemv_mt(wv, x, y, tokens, p, ctx->stream);
+  } else if (ctx->gemv_kernel == 0 && gemv_mx_plan(wv, tokens, p)) {
     e = launch_gemv_mx(wv, x, y, tokens, p, ctx->stream);
   } else {
     p = plan_gemv(wv, tokens);
@@ -367,10 +369,13 @@ int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint
     if (!rc) ++ctx->stats.gemm;
     return rc;
   }
-  // Between the two: the f32 GEMV over groups of up to 8 tokens. Y is
-  // token-major, so each group writes a contiguous slice.
-  for (uint32_t t0 = 0; t0 < tokens; t0 += 8) {
-    const uint32_t tn = tokens - t0 < 8 ? tokens - t0 : 8;
+  // Between the two: the GEMV over groups of tokens (16 per launch for the
+  // multi-token matrix-core kernel, else 8). Y is token-major, so each group
+  // writes a contiguous slice.
+  GemvPlan p16;
+  const uint32_t grp = ctx->gemv_kernel == 0 && gemv_mt_plan(wv, 16, p16) ? 16u : 8u;
+  for (uint32_t t0 = 0; t0 < tokens; t0 += grp) {
+    const uint32_t tn = tokens - t0 < grp ? tokens - t0 : grp;
     rc = run_gemv(ctx, wv, xp + (uint64_t)t0 * k, yp + (uint64_t)t0 * rows, tn);
     if (rc) return rc;
     ++ctx->stats.skinny;

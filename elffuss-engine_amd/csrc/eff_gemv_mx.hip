@@ -342,7 +342,10 @@ __device__ __forceinline__ void x_load(const float *__restrict__ x, uint32_t k, 
   v.b = *(const float4 *)(x + (uint64_t)t * k + ko + 4u);
 }
 
-__device__ __forceinline__ void x_store(const XOct &v, uint32_t k, uint32_t T, uint32_t o, uint8_t *lds) {
+// dstride: bytes of digits per token (3 k, or padded); mstride: floats of
+// group data per token (k / 8, or padded); meta: the group data area.
+__device__ __forceinline__ void x_store(const XOct &v, uint32_t k, uint32_t o, uint8_t *lds, uint32_t dstride,
+                                        float *metab, uint32_t mstride) {
   const uint32_t opt = k / 8u, t = o / opt, ko = 8u * (o % opt);
   const float4 a = v.a, b = v.b;
   float m = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
@@ -376,13 +379,13 @@ __device__ __forceinline__ void x_store(const XOct &v, uint32_t k, uint32_t T, u
     pl[1][h] = __builtin_amdgcn_perm(l23, l01, 0x07060302u) ^ 0x80808080u;
     pl[2][h] = __builtin_amdgcn_perm(h23, h01, 0x05040100u) ^ 0x80808080u;
   }
-  uint8_t *dig = lds + (uint64_t)t * k * 3u + (ko / 16u) * 48u + 8u * ((ko / 8u) & 1u);
+  uint8_t *dig = lds + (uint64_t)t * dstride + (ko / 16u) * 48u + 8u * ((ko / 8u) & 1u);
 #pragma unroll
   for (int d = 0; d < 3; ++d) *(uint2 *)(dig + 16 * d) = make_uint2(pl[d][0], pl[d][1]);
   // sums over 16 values: this octet + its neighbour in the quad
   float s = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
   s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0xB1, 0xF, 0xF, false));
-  float *meta = (float *)(lds + (uint64_t)T * k * 3u) + (uint64_t)t * (k / 8u) + 4u * (ko / 32u);
+  float *meta = metab + (uint64_t)t * mstride + 4u * (ko / 32u);
   const uint32_t q4 = (ko / 8u) & 3u;
   if (q4 == 0u) meta[1] = s;
   if (q4 == 2u) meta[2] = s;
@@ -538,11 +541,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
   }
 #pragma unroll
   for (uint32_t i = 0; i < kXr; ++i)
-    if (tid + NT * i < noct) x_store(xo[i], k, (uint32_t)T, tid + NT * i, xl);
+    if (tid + NT * i < noct) x_store(xo[i], k, tid + NT * i, xl, k * 3u, (float *)(xl + (uint64_t)T * k * 3u), k / 8u);
   for (uint32_t o = tid + NT * kXr; o < noct; o += NT) {
     XOct v;
     x_load(x, k, o, v);
-    x_store(v, k, (uint32_t)T, o, xl);
+    x_store(v, k, o, xl, k * 3u, (float *)(xl + (uint64_t)T * k * 3u), k / 8u);
   }
   __syncthreads();
 
@@ -652,6 +655,353 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
   for (uint32_t n = 0; n < nitems; n += 2u) {
     step(RA, true);
     step(RB, n + 1u < nitems);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Multi-token GEMV: 4 to 16 tokens per launch on v_mfma_i32_16x16x32_i8.
+//
+// One MFMA multiplies 16 rows of W (B: 32 k x 16 rows of int8 weights u) by
+// 4 tokens x 4 digit planes of x (A: 16 x 32 k, row 4 t + plane; plane 3 is
+// zero): lane l supplies B row l % 16 at k 8 (l / 16) .. + 7 and A row l % 16
+// at the same k, and receives D for token l / 16 of the group, planes 0..3,
+// row l % 16. The weights of a 32-k group are decoded once for all tokens,
+// and each lane folds D into its (token, row) sum as the 4-row kernel does:
+//   acc += s * p * ((D2 * 256 + D1) * 256 + D0) - m * sum(x).
+// Types whose scales cover 16 weights (Q2_K, Q6_K) take two MFMAs per group,
+// each with the other half's weights zeroed.
+//
+// A wave owns 16 rows and a slice of k; a workgroup is NW waves = (NW / S)
+// row tiles x S slices, the slices added in a fixed order through LDS. k is
+// walked in passes of 256: the 16 rows' bytes of a pass are fetched with
+// coalesced 16-byte loads two passes ahead, written to the wave's LDS stage,
+// and each lane reads its 8 weights of every group from there.
+template <int TYPE> struct MtW;
+
+template <int TYPE> constexpr uint32_t mt_block_elems() { return TYPE == Q8_0 ? 32u : 256u; }
+template <int TYPE> constexpr uint32_t mt_block_bytes() {
+  return TYPE == Q8_0 ? 34u : TYPE == Q4_K ? 144u : TYPE == Q6_K ? 210u : TYPE == Q2_K ? 84u : 66u;
+}
+
+// 6-bit (scale, min) pair j of a Q4_K block from its scale words (bytes 4-7,
+// 8-11, 12-15 of the block), as SCALE_MIN_K4 (kernels.wgsl.js:94-104)
+__device__ __forceinline__ void mt_q4k_sm(uint32_t s1, uint32_t s2, uint32_t s3, uint32_t j, uint32_t &sc,
+                                          uint32_t &mn) {
+  const uint32_t sh = 8u * (j & 3u);
+  if (j < 4u) {
+    sc = (s1 >> sh) & 63u;
+    mn = (s2 >> sh) & 63u;
+  } else {
+    const uint32_t a = (s3 >> sh) & 0xFFu, b = (s1 >> sh) & 0xFFu, c = (s2 >> sh) & 0xFFu;
+    sc = (a & 0xFu) | ((b >> 6) << 4);
+    mn = (a >> 4) | ((c >> 6) << 4);
+  }
+}
+
+// 8 bytes at a 2-byte aligned LDS address
+__device__ __forceinline__ uint2 lds8_a2(const uint8_t *p) {
+  const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
+  const uint8_t *q = p - sh;
+  const uint32_t v0 = lds32(q), v1 = lds32(q + 4), v2 = lds32(q + 8);
+  return make_uint2(__builtin_amdgcn_alignbyte(v1, v0, sh), __builtin_amdgcn_alignbyte(v2, v1, sh));
+}
+__device__ __forceinline__ float lds_h2f(const uint8_t *p) {
+  const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
+  const uint32_t w = lds32(p - sh);
+  return h2f(sh ? (w >> 16) : (w & 0xFFFFu));
+}
+
+// Per type: pass bytes per row (RB, 256 k), alignment of the pass start
+// (ALIGN), scale groups per 32 k (SUB), and the decode of group g of a pass:
+// the lane's 8 weights (kq = k / 8 inside the group) and the scales s, m of
+// each 16- or 32-weight part, value = s u - m.
+template <> struct MtW<Q8_0> {
+  static constexpr uint32_t RB = 272, ALIGN = 4, SUB = 1;
+  __device__ static void dec(const uint8_t *r, uint32_t g, uint32_t kq, const uint32_t *, uint2 &u, float *s,
+                             float *m) {
+    u = lds8_a2(r + 34u * g + 2u + 8u * kq);
+    s[0] = lds_h2f(r + 34u * g);
+    m[0] = 0.f;
+  }
+};
+template <> struct MtW<Q4_K> {
+  static constexpr uint32_t RB = 144, ALIGN = 16, SUB = 1;
+  __device__ static void dec(const uint8_t *r, uint32_t g, uint32_t kq, const uint32_t *, uint2 &u, float *s,
+                             float *m) {
+    const uint2 w = *(const uint2 *)(r + 16u + 32u * (g >> 1) + 8u * kq);
+    const uint32_t sh = 4u * (g & 1u);
+    u = make_uint2((w.x >> sh) & 0x0F0F0F0Fu, (w.y >> sh) & 0x0F0F0F0Fu);
+    const uint4 hd = *(const uint4 *)r;
+    uint32_t sc, mn;
+    mt_q4k_sm(hd.y, hd.z, hd.w, g, sc, mn);
+    s[0] = h2f(hd.x & 0xFFFFu) * (float)sc;
+    m[0] = h2f(hd.x >> 16) * (float)mn;
+  }
+};
+template <> struct MtW<Q6_K> {
+  static constexpr uint32_t RB = 210, ALIGN = 2, SUB = 2;
+  __device__ static void dec(const uint8_t *r, uint32_t g, uint32_t kq, const uint32_t *, uint2 &u, float *s,
+                             float *m) {
+    // weight 32 g + l: ql byte 64 n + 32 (g & 1) + l (nibble (g & 3) >> 1),
+    // qh byte 32 n + l (bits 2 (g & 3)), n = g >> 2; u = q in 0..63, m = 32 s
+    const uint32_t n = g >> 2, gg = g & 3u;
+    const uint2 ql = lds8_a2(r + 64u * n + 32u * (g & 1u) + 8u * kq);
+    const uint2 qh = lds8_a2(r + 128u + 32u * n + 8u * kq);
+    const uint32_t ls = 4u * (gg >> 1), hs = 2u * gg;
+    u.x = ((ql.x >> ls) & 0x0F0F0F0Fu) | (((qh.x >> hs) & 0x03030303u) << 4);
+    u.y = ((ql.y >> ls) & 0x0F0F0F0Fu) | (((qh.y >> hs) & 0x03030303u) << 4);
+    const float d = lds_h2f(r + 208u);
+    const uint8_t *sc = r + 192u + 2u * g;  // int8 scales of weights 32 g .. + 15, + 16 .. + 31
+    const uint32_t sh = (uint32_t)((uintptr_t)sc & 3u);
+    const uint32_t sw = lds32(sc - sh) >> (8u * sh);
+    s[0] = d * (float)(int8_t)(sw & 0xFFu);
+    s[1] = d * (float)(int8_t)((sw >> 8) & 0xFFu);
+    m[0] = 32.f * s[0];
+    m[1] = 32.f * s[1];
+  }
+};
+template <> struct MtW<Q2_K> {
+  // The 4-bit scale of each 16 is folded into the weights (u sc <= 45 fits a
+  // signed byte): one MFMA per group, s = d, and the mins of both halves.
+  static constexpr uint32_t RB = 84, ALIGN = 4, SUB = 1;
+  __device__ static void dec(const uint8_t *r, uint32_t g, uint32_t kq, const uint32_t *, uint2 &u, float *s,
+                             float *m) {
+    // weight 32 g + l: qs byte 32 (g >> 2) + l, bits 2 (g & 3); scale byte 2 g (+1)
+    const uint2 w = *(const uint2 *)(r + 16u + 32u * (g >> 2) + 8u * kq);
+    const uint32_t sh = 2u * (g & 3u);
+    const uint32_t dd = lds32(r + 80u);
+    const uint32_t sc = lds32(r + 4u * (g >> 1)) >> (16u * (g & 1u));
+    const uint32_t mine = kq < 2u ? (sc & 0xFu) : ((sc >> 8) & 0xFu);
+    const uint32_t a = (w.x >> sh) & 0x03030303u, b = (w.y >> sh) & 0x03030303u;
+    // u * sc per byte from the two bits of u (no carries: each product < 64)
+    u.x = (a & 0x01010101u) * mine + ((a >> 1) & 0x01010101u) * (2u * mine);
+    u.y = (b & 0x01010101u) * mine + ((b >> 1) & 0x01010101u) * (2u * mine);
+    const float dmin = h2f(dd >> 16);
+    s[0] = h2f(dd & 0xFFFFu);
+    m[0] = dmin * (float)((sc >> 4) & 0xFu);
+    m[1] = dmin * (float)((sc >> 12) & 0xFu);
+  }
+};
+template <> struct MtW<IQ2_XXS> {
+  static constexpr uint32_t RB = 66, ALIGN = 2, SUB = 1;
+  __device__ static void dec(const uint8_t *r, uint32_t g, uint32_t kq, const uint32_t *tab, uint2 &u, float *s,
+                             float *m) {
+    // group g: grid indices (a0) and 4 x 7 sign bits + 4-bit scale (a1) at 2 + 8 g
+    const uint2 a = lds8_a2(r + 2u + 8u * g);
+    const uint32_t gi = (a.x >> (8u * kq)) & 0xFFu, sg = (a.y >> (7u * kq)) & 127u;
+    const uint32_t g0 = tab[2u * gi], g1 = tab[2u * gi + 1u];
+    const uint32_t m0 = tab[512u + 2u * sg], m1 = tab[512u + 2u * sg + 1u];
+    // +g or -g per byte (two's complement, no carries between bytes)
+    u.x = (g0 ^ m0) + (m0 & 0x01010101u);
+    u.y = (g1 ^ m1) + (m1 & 0x01010101u);
+    s[0] = lds_h2f(r) * (0.5f + (float)(a.y >> 28)) * 0.25f;
+    m[0] = 0.f;
+  }
+};
+
+template <int TYPE> struct MtStage {
+  using W = MtW<TYPE>;
+  // a pass region of a row, staged from its 4-byte aligned start (+2 bytes
+  // for 2-byte aligned types), in 16-byte chunks
+  static constexpr uint32_t CPR = (W::RB + (W::ALIGN < 4 ? 2u : 0u) + 15u) / 16u;
+  static constexpr uint32_t LOADS = (16u * CPR + 63u) / 64u;
+  static constexpr uint32_t BYTES = 16u * CPR * 16u;
+};
+
+template <int TYPE, int TG, int NW>
+__global__ __launch_bounds__(NW * 64) void k_gemv_mt(WeightView wv, const float *__restrict__ x,
+                                                     float *__restrict__ y, uint32_t tokens, int S) {
+  using W = MtW<TYPE>;
+  using ST = MtStage<TYPE>;
+  constexpr bool kTab = TYPE == IQ2_XXS;
+  constexpr uint32_t T = 4u * TG, NT = NW * 64u;
+  extern __shared__ __align__(16) uint8_t lds[];
+  uint32_t *tab = (uint32_t *)lds;
+  uint8_t *xl = lds + (kTab ? kMxTables : 0);
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t rows = wv.rows, k = wv.k;
+  const uint32_t RT = (uint32_t)NW / (uint32_t)S, rt = wave / (uint32_t)S, sl = wave % (uint32_t)S;
+  const uint32_t r0 = (blockIdx.x * RT + rt) * 16u;  // first row of the wave
+  const uint32_t ks = k / (uint32_t)S, k0 = sl * ks, passes = ks / 256u;
+  // per token: digits 3 k bytes + 32, group data k / 8 floats + 4 (the
+  // padding spreads the 4 tokens of an MFMA over different LDS banks)
+  const uint32_t dstr = 3u * k + 32u, mstr = k / 8u + 4u;
+  const uint32_t xbytes = T * dstr + T * mstr * 4u;
+  float *const metab = (float *)(xl + T * dstr);
+  uint8_t *stg = xl + xbytes + 16u + wave * ST::BYTES;
+  float *red = (float *)(xl + xbytes + 16u + (uint32_t)NW * ST::BYTES);
+  const BufSrc src = make_src(wv, 0);
+  const uint32_t rbytes = (uint32_t)wv.row_bytes;
+
+  // Lane chunks: chunk q = lane + 64 j is chunk q % CPR of row q / CPR
+  // (rows past the matrix repeat its last row); a pass region is staged from
+  // the 4-byte floor of its start.
+  uint32_t vr[ST::LOADS], vc[ST::LOADS];
+  bool vok[ST::LOADS];
+#pragma unroll
+  for (uint32_t j = 0; j < ST::LOADS; ++j) {
+    const uint32_t q = lane + 64u * j, r = min(q / ST::CPR, 15u);
+    vok[j] = q < 16u * ST::CPR;
+    vr[j] = min(r0 + r, rows - 1u) * rbytes;
+    vc[j] = 16u * (q - r * ST::CPR);
+  }
+  // pass start inside a row (first block of the pass)
+  auto pstart = [&](uint32_t ps) { return (k0 + 256u * ps) / mt_block_elems<TYPE>() * mt_block_bytes<TYPE>(); };
+  struct Regs {
+    u32x4 q[ST::LOADS];
+  };
+  auto fetch = [&](uint32_t ps, Regs &R) {
+    const uint32_t po = pstart(min(ps, passes - 1u));
+#pragma unroll
+    for (uint32_t j = 0; j < ST::LOADS; ++j)
+      R.q[j] = __builtin_amdgcn_raw_buffer_load_b128(src.q, (int)(((vr[j] + po) & ~3u) + vc[j]), 0, 0);
+  };
+  auto put = [&](const Regs &R) {
+#pragma unroll
+    for (uint32_t j = 0; j < ST::LOADS; ++j)
+      if (vok[j]) *(u32x4 *)(stg + 1024u * j + 16u * lane) = R.q[j];
+  };
+
+  // x (and the IQ2_XXS tables) first, then the weights of the first two passes
+  const uint32_t noct = tokens * (k / 8u), ntot = T * (k / 8u);
+  XOct xo[kXr];
+#pragma unroll
+  for (uint32_t i = 0; i < kXr; ++i)
+    if (tid + NT * i < noct) x_load(x, k, tid + NT * i, xo[i]);
+  uint64_t gent = 0;
+  if constexpr (kTab) gent = c_grid_mx[tid & 255u];
+  __asm__ volatile("" ::: "memory");
+  Regs RA, RB;
+  fetch(0, RA);
+  fetch(1, RB);
+  if constexpr (kTab) {
+    if (tid < 256u) mx_tables(tab, gent, tid);
+  }
+#pragma unroll
+  for (uint32_t i = 0; i < kXr; ++i)
+    if (tid + NT * i < noct) x_store(xo[i], k, tid + NT * i, xl, dstr, metab, mstr);
+  for (uint32_t o = tid + NT * kXr; o < noct; o += NT) {
+    XOct v;
+    x_load(x, k, o, v);
+    x_store(v, k, o, xl, dstr, metab, mstr);
+  }
+  if (tid < 4u) ((uint32_t *)(xl + xbytes))[tid] = 0u;  // the zero plane
+  // tokens past `tokens`: zero digits and group data
+  for (uint32_t o = noct + tid; o < ntot; o += NT) {
+    const uint32_t opt = k / 8u, t = o / opt, ko = 8u * (o % opt);
+    uint8_t *dig = xl + (uint64_t)t * dstr + (ko / 16u) * 48u + 8u * ((ko / 8u) & 1u);
+#pragma unroll
+    for (int d = 0; d < 3; ++d) *(uint2 *)(dig + 16 * d) = make_uint2(0u, 0u);
+    if ((ko & 31u) == 0u) *(float4 *)(metab + (uint64_t)t * mstr + ko / 8u) = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  __syncthreads();
+
+  const uint32_t n = lane & 15u, kq = lane >> 4;
+  // A row of the lane: token (lane % 16) / 4 of each group, plane lane % 4;
+  // plane 3 reads a zeroed 16 bytes (its address does not advance)
+  const uint32_t at = (lane & 15u) >> 2, ap = lane & 3u;
+  const uint32_t amul = ap < 3u ? 1u : 0u;
+  const uint32_t abase = ap < 3u ? at * dstr + 16u * ap + 8u * (kq & 1u) + 48u * (kq >> 1) : xbytes;
+  const float *meta = metab;
+  const uint32_t rowb = min(r0 + n, rows - 1u) * rbytes;  // this lane's row (B operand)
+  float acc[TG];
+#pragma unroll
+  for (int t = 0; t < TG; ++t) acc[t] = 0.f;
+
+  // Two groups at a time: both decodes and all their MFMAs are issued before
+  // the first fold reads an MFMA result.
+  auto compute = [&](uint32_t ps) {
+    const uint8_t *rr = stg + n * (ST::CPR * 16u) + (W::ALIGN < 4 ? ((rowb + pstart(ps)) & 3u) : 0u);
+    const uint32_t kp = k0 + 256u * ps;
+#pragma unroll
+    for (uint32_t g0 = 0; g0 < 8u; g0 += 2u) {
+      uint2 u[2];
+      float s[2][2], m[2][2];
+      long A[2][TG];
+      float4 M[2][TG];
+      int4v D[2][TG][W::SUB];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t g = g0 + (uint32_t)j, kg = kp + 32u * g;
+        W::dec(rr, g, kq, tab, u[j], s[j], m[j]);
+#pragma unroll
+        for (int tg = 0; tg < TG; ++tg) {
+          // A: 8 digits of plane ap of token 4 tg + at
+          const uint2 av = *(const uint2 *)(xl + abase + amul * (4u * (uint32_t)tg * dstr + (kg / 16u) * 48u));
+          A[j][tg] = (long)(((uint64_t)av.y << 32) | av.x);
+          M[j][tg] = *(const float4 *)(meta + (uint64_t)(4u * tg + kq) * mstr + 4u * (kg / 32u));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint64_t b64 = ((uint64_t)u[j].y << 32) | u[j].x;
+#pragma unroll
+        for (int tg = 0; tg < TG; ++tg) {
+          if constexpr (W::SUB == 1) {
+            D[j][tg][0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[j][tg], (long)b64, int4v{0, 0, 0, 0}, 0, 0, 0);
+          } else {
+            // the weights of the other 16 are zeroed (kq < 2: k 0..15)
+            const long Blo = (long)(kq < 2u ? b64 : 0ull), Bhi = (long)(kq < 2u ? 0ull : b64);
+            D[j][tg][0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[j][tg], Blo, int4v{0, 0, 0, 0}, 0, 0, 0);
+            D[j][tg][W::SUB - 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[j][tg], Bhi, int4v{0, 0, 0, 0}, 0, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int tg = 0; tg < TG; ++tg) {
+          const float4 Mv = M[j][tg];
+#pragma unroll
+          for (int h = 0; h < (int)W::SUB; ++h) {
+            const int4v Dv = D[j][tg][h];
+            const float f = __builtin_fmaf((float)(Dv.z * 256 + Dv.y), 256.f, (float)Dv.x);
+            acc[tg] = __builtin_fmaf(s[j][h] * Mv.x, f, acc[tg]);
+          }
+          if (TYPE == Q4_K) acc[tg] = __builtin_fmaf(-m[j][0], Mv.y + Mv.z, acc[tg]);
+          if (TYPE == Q2_K || TYPE == Q6_K)
+            acc[tg] = __builtin_fmaf(-m[j][1], Mv.z, __builtin_fmaf(-m[j][0], Mv.y, acc[tg]));
+        }
+    }
+  };
+
+  // passes: the registers of a pass are free once written to the stage; the
+  // fetch two passes ahead goes out before the pass is computed (past the
+  // last pass it repeats the last one, so the loads in flight never change)
+  for (uint32_t ps = 0; ps < passes; ps += 2u) {
+    put(RA);
+    fetch(ps + 2u, RA);
+    compute(ps);
+    if (ps + 1u < passes) {
+      put(RB);
+      fetch(ps + 3u, RB);
+      compute(ps + 1u);
+    }
+  }
+
+  // slices of a row tile added in slice order; lane (kq, n) holds token
+  // 4 tg + kq, row n
+  if (S > 1) {
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg) red[(wave * (uint32_t)TG + tg) * 64u + lane] = acc[tg];
+    __syncthreads();
+    if (sl != 0u) return;
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg) {
+      float v = 0.f;
+      for (uint32_t q = 0; q < (uint32_t)S; ++q) v += red[((wave + q) * (uint32_t)TG + tg) * 64u + lane];
+      acc[tg] = v;
+    }
+  }
+  const uint32_t row = r0 + n;
+  if (row < rows) {
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg) {
+      const uint32_t t = 4u * tg + kq;
+      if (t < tokens) y[(uint64_t)t * rows + row] = acc[tg];
+    }
   }
 }
 
@@ -782,6 +1132,114 @@ static hipError_t mx_t(const WeightView &wv, const float *x, float *y, uint32_t 
     case 6: return mx_go<TYPE, 6>(wv, x, y, p, s);
     case 7: return mx_go<TYPE, 7>(wv, x, y, p, s);
     case 8: return mx_go<TYPE, 8>(wv, x, y, p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Multi-token GEMV host side.
+namespace {
+
+template <int TYPE> constexpr size_t mt_stage_bytes() { return MtStage<TYPE>::BYTES; }
+
+size_t mt_stage_of(int type) {
+  switch (type) {
+    case Q8_0: return mt_stage_bytes<Q8_0>();
+    case Q4_K: return mt_stage_bytes<Q4_K>();
+    case Q6_K: return mt_stage_bytes<Q6_K>();
+    case Q2_K: return mt_stage_bytes<Q2_K>();
+    case IQ2_XXS: return mt_stage_bytes<IQ2_XXS>();
+    default: return 0;
+  }
+}
+
+// LDS: IQ2_XXS tables, x digits of 4 TG tokens, one stage per wave, slice sums.
+size_t mt_lds_bytes(const WeightView &wv, uint32_t tg, int nw) {
+  const size_t t = 4u * tg;
+  return (wv.type == IQ2_XXS ? (size_t)kMxTables : 0) + t * (3u * wv.k + 32u) + t * (wv.k / 8u + 4u) * 4u + 16u +
+         (size_t)nw * mt_stage_of(wv.type) + (size_t)nw * tg * 64u * 4u;
+}
+
+}  // namespace
+
+bool gemv_mt_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p) {
+  if (tokens < 4 || tokens > 16) return false;
+  if (wv.type != Q8_0 && wv.type != Q4_K && wv.type != Q6_K && wv.type != Q2_K && wv.type != IQ2_XXS) return false;
+  if (wv.k % 256u || wv.w_bytes >= (1ull << 32)) return false;
+  const uint32_t tg = (tokens + 3u) / 4u, tiles = (wv.rows + 15u) / 16u;
+  struct Cand { int nw, s; };
+  // for equal rows per workgroup the wider workgroup comes first
+  const Cand cands[] = {{8, 1}, {8, 2}, {4, 1}, {8, 4}, {4, 2}, {8, 8}, {4, 4}};
+  int best = -1;
+  uint32_t best_rt = 0;
+  bool best_enough = false;
+  for (int i = 0; i < 7; ++i) {
+    const Cand &cd = cands[i];
+    if (g_force_nw && (cd.nw != g_force_nw || cd.s != g_force_s)) continue;
+    if (wv.k % (256u * (uint32_t)cd.s) || mt_lds_bytes(wv, tg, cd.nw) > kMxMaxLds) continue;
+    const uint32_t rt = (uint32_t)(cd.nw / cd.s);
+    const bool enough = (tiles + rt - 1u) / rt >= 256u;
+    const bool better = best < 0 || (enough && !best_enough) || (enough && best_enough && rt > best_rt) ||
+                        (!enough && !best_enough && rt < best_rt);
+    if (better) {
+      best = i;
+      best_rt = rt;
+      best_enough = enough;
+    }
+  }
+  if (best < 0) return false;
+  p = GemvPlan{};
+  p.rows_per_wave = 16;
+  p.ksplit = cands[best].s;
+  p.waves = cands[best].nw;
+  p.kc = wv.k / (uint32_t)p.ksplit;
+  p.tiles = (tiles + best_rt - 1u) / best_rt;
+  p.grid = p.tiles;
+  p.lds_bytes = mt_lds_bytes(wv, tg, p.waves);
+  return true;
+}
+
+template <int TYPE, int TG, int NW>
+static hipError_t mt_launch(const WeightView &wv, const float *x, float *y, uint32_t tokens, const GemvPlan &p,
+                            hipStream_t s) {
+  static bool attr = false;
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_mt<TYPE, TG, NW>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMxMaxLds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  hipLaunchKernelGGL((k_gemv_mt<TYPE, TG, NW>), dim3(p.grid), dim3(NW * 64), p.lds_bytes, s, wv, x, y, tokens,
+                     p.ksplit);
+  return hipGetLastError();
+}
+
+template <int TYPE, int TG>
+static hipError_t mt_go(const WeightView &wv, const float *x, float *y, uint32_t tokens, const GemvPlan &p,
+                        hipStream_t s) {
+  return p.waves == 8 ? mt_launch<TYPE, TG, 8>(wv, x, y, tokens, p, s) : mt_launch<TYPE, TG, 4>(wv, x, y, tokens, p, s);
+}
+
+template <int TYPE>
+static hipError_t mt_t(const WeightView &wv, const float *x, float *y, uint32_t tokens, const GemvPlan &p,
+                       hipStream_t s) {
+  switch ((tokens + 3u) / 4u) {
+    case 1: return mt_go<TYPE, 1>(wv, x, y, tokens, p, s);
+    case 2: return mt_go<TYPE, 2>(wv, x, y, tokens, p, s);
+    case 3: return mt_go<TYPE, 3>(wv, x, y, tokens, p, s);
+    case 4: return mt_go<TYPE, 4>(wv, x, y, tokens, p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemv_mt(const WeightView &wv, const float *x, float *y, uint32_t tokens, const GemvPlan &p,
+                          hipStream_t s) {
+  switch (wv.type) {
+    case Q8_0: return mt_t<Q8_0>(wv, x, y, tokens, p, s);
+    case Q4_K: return mt_t<Q4_K>(wv, x, y, tokens, p, s);
+    case Q6_K: return mt_t<Q6_K>(wv, x, y, tokens, p, s);
+    case Q2_K: return mt_t<Q2_K>(wv, x, y, tokens, p, s);
+    case IQ2_XXS: return mt_t<IQ2_XXS>(wv, x, y, tokens, p, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -42,6 +42,11 @@ bool gemv_mx_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p);
 void gemv_mx_override(int waves, int ksplit);
 hipError_t launch_gemv_mx(const WeightView &wv, const float *x, float *y, uint32_t tokens,
                           const GemvPlan &p, hipStream_t stream);
+// Multi-token matrix-core GEMV (16 rows x 4 tokens per MFMA): 4..16 tokens
+// per launch, Q8_0/Q4_K/Q6_K/Q2_K/IQ2_XXS, k % 256 == 0.
+bool gemv_mt_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p);
+hipError_t launch_gemv_mt(const WeightView &wv, const float *x, float *y, uint32_t tokens,
+                          const GemvPlan &p, hipStream_t stream);
 
 // x is first rounded to fp16 into `xh_scratch`, gemm_x_bytes(...) bytes laid
 // out as [token tile][k step][token][k] (zero past the tokens and past k).

@@ -205,7 +205,8 @@ def test_router_paths_and_stats(ctx, eff, orc):
         check_close(yb.read(np.float32), oracle_fn(orc.Q4_K, gguf, rows, k, x, tokens), f"matmul T={tokens}")
     after = ctx.stats()
     assert after["gemv"] - before["gemv"] == 1
-    assert after["skinny"] - before["skinny"] == 2 + 5
+    # 9..63 tokens: groups of 16 on the multi-token matrix-core GEMV (Q4_K, k % 256 == 0)
+    assert after["skinny"] - before["skinny"] == 1 + 3
     assert after["gemm"] - before["gemm"] == 1
 
 
