@@ -199,6 +199,13 @@ def main():
             if args.only and args.only not in key:
                 continue
             cfg = Config(eff, ctx, tn, rows, k, m, 300 + rows + m, topk=tk)
+            # the router's choice for this shape, from its launch counters
+            before = ctx.stats()
+            cfg.step(ctx, 0)
+            after = ctx.stats()
+            groups = after["skinny"] - before["skinny"]
+            path = "gemm" if after["gemm"] > before["gemm"] else (
+                f"gemv x {groups} token groups" if groups else "gemv")
             steps = 40 if cfg.gemm else 100
             t_ms = time_steps(torch, ctx, cfg, steps, 5)
             gb = cfg.bytes / (t_ms * 1e-3) / 1e9
@@ -209,7 +216,7 @@ def main():
             sweep[key] = {"us": round(t_ms * 1e3, 2), "GB/s": round(gb, 1), "TFLOP/s": round(tf, 2),
                           "bound": bound,
                           "roofline_frac": round((mfma_t if bound == "mfma" else hbm_t) / (t_ms * 1e-3), 4),
-                          "path": "gemm" if cfg.gemm else ("gemv" if m <= 8 else "gemv x groups of 8")}
+                          "path": path}
             cfg.free()
             print(f"# {key}: {sweep[key]}", file=sys.stderr, flush=True)
 

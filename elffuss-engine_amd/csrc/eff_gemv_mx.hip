@@ -336,17 +336,33 @@ struct XOct {
   float4 a, b;
 };
 
+// Token t and k offset ko of octet o, for at most TMAX tokens (compares
+// instead of a division by k / 8).
+template <uint32_t TMAX>
+__device__ __forceinline__ void oct_pos(uint32_t k, uint32_t o, uint32_t &t, uint32_t &ko) {
+  const uint32_t opt = k / 8u;
+  uint32_t n = 0;
+#pragma unroll
+  for (uint32_t i = 1; i < TMAX; ++i) n += o >= i * opt ? 1u : 0u;
+  t = n;
+  ko = 8u * (o - n * opt);
+}
+
+template <uint32_t TMAX>
 __device__ __forceinline__ void x_load(const float *__restrict__ x, uint32_t k, uint32_t o, XOct &v) {
-  const uint32_t opt = k / 8u, t = o / opt, ko = 8u * (o % opt);
+  uint32_t t, ko;
+  oct_pos<TMAX>(k, o, t, ko);
   v.a = *(const float4 *)(x + (uint64_t)t * k + ko);
   v.b = *(const float4 *)(x + (uint64_t)t * k + ko + 4u);
 }
 
 // dstride: bytes of digits per token (3 k, or padded); mstride: floats of
 // group data per token (k / 8, or padded); meta: the group data area.
+template <uint32_t TMAX>
 __device__ __forceinline__ void x_store(const XOct &v, uint32_t k, uint32_t o, uint8_t *lds, uint32_t dstride,
                                         float *metab, uint32_t mstride) {
-  const uint32_t opt = k / 8u, t = o / opt, ko = 8u * (o % opt);
+  uint32_t t, ko;
+  oct_pos<TMAX>(k, o, t, ko);
   const float4 a = v.a, b = v.b;
   float m = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
                   fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
@@ -433,9 +449,18 @@ __device__ __forceinline__ float slot_sum(float v) {
 // fetched with coalesced 16-byte loads (lane i takes chunks i, i+64, ...) two
 // passes ahead into registers, and written to the wave's LDS stage just before
 // the pass is computed; each lane then reads its own task from the stage.
+// Launch geometry, computed on the host so that the kernel's prologue (which
+// every workgroup runs before its first load) has no integer divisions.
+struct MxGeo {
+  uint32_t s_log2;  // S = 2^s_log2 k slices per row quad
+  uint32_t ntask;   // 64-weight tasks per slice (k / 64 / S)
+  uint32_t passes;  // passes of 16 tasks per slice
+  uint32_t tq, tr;  // row tiles = tq * grid + tr
+};
+
 template <int TYPE, int T, int NW>
 __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float *__restrict__ x,
-                                                     float *__restrict__ y, int S) {
+                                                     float *__restrict__ y, MxGeo geo) {
   using TK = Task<TYPE>;
   using ST = Stage<TK::RB, TK::ALIGN>;
   using ST2 = Stage2<TYPE>;
@@ -446,19 +471,23 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
   uint32_t *tab = (uint32_t *)lds;
   uint8_t *xl = lds + (kTab ? kMxTables : 0);
 
+  // all kernel arguments in scalar registers at once: one round trip to the
+  // argument buffer instead of one per use
+  __asm__ volatile("" ::"s"(wv.w), "s"(wv.rows), "s"(wv.k), "s"(wv.bpr), "s"(wv.row_bytes), "s"(wv.w_bytes),
+                   "s"(wv.scales_off), "s"(x), "s"(y), "s"(geo.s_log2), "s"(geo.ntask), "s"(geo.passes), "s"(geo.tq),
+                   "s"(geo.tr));
   const uint32_t tid = threadIdx.x, lane = tid & 63u, b = lane >> 2, c = lane & 3u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar registers)
   const uint32_t rows = wv.rows, k = wv.k;
-  const uint32_t G4 = (uint32_t)NW / (uint32_t)S, gq = wave / (uint32_t)S, sl = wave % (uint32_t)S;
-  const uint32_t RPT = 4u * G4, tiles = (rows + RPT - 1u) / RPT;
+  const uint32_t S = 1u << geo.s_log2, G4 = (uint32_t)NW >> geo.s_log2;
+  const uint32_t gq = wave >> geo.s_log2, sl = wave & (S - 1u), RPT = 4u * G4;
   const BufSrc src = make_src(wv, 0);
   const uint32_t xbytes = (uint32_t)T * k * 3u + (uint32_t)T * (k / 8u) * 4u;
   uint8_t *const stg = xl + xbytes + wave * SBT;
   float *red = (float *)(xl + xbytes + (uint32_t)NW * SBT);
 
-  const uint32_t ntask = k / 64u / (uint32_t)S, t0 = sl * ntask;
-  const uint32_t passes = (ntask + 15u) / 16u;
-  const uint32_t my_tiles = (tiles - 1u - blockIdx.x) / gridDim.x + 1u, nitems = my_tiles * passes;
+  const uint32_t ntask = geo.ntask, t0 = sl * ntask, passes = geo.passes;
+  const uint32_t my_tiles = geo.tq + (blockIdx.x < geo.tr ? 1u : 0u), nitems = my_tiles * passes;
   // bytes of a row: GGUF blocks, or the quants of Q8_0R (its scales: 2 per block)
   const uint32_t rbytes = TYPE == Q8_0R ? 32u * wv.bpr : (uint32_t)wv.row_bytes, sbytes = 2u * wv.bpr;
   auto row_of = [&](uint32_t tile, uint32_t r) { return min(tile * RPT + 4u * gq + r, rows - 1u); };
@@ -527,7 +556,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
   XOct xo[kXr];
 #pragma unroll
   for (uint32_t i = 0; i < kXr; ++i)
-    if (tid + NT * i < noct) x_load(x, k, tid + NT * i, xo[i]);
+    if (tid + NT * i < noct) x_load<(uint32_t)T>(x, k, tid + NT * i, xo[i]);
   uint64_t gent = 0;
   if constexpr (kTab) gent = c_grid_mx[tid & 255u];
   __asm__ volatile("" ::: "memory");  // keep these loads ahead of the weights
@@ -541,11 +570,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
   }
 #pragma unroll
   for (uint32_t i = 0; i < kXr; ++i)
-    if (tid + NT * i < noct) x_store(xo[i], k, tid + NT * i, xl, k * 3u, (float *)(xl + (uint64_t)T * k * 3u), k / 8u);
+    if (tid + NT * i < noct) x_store<(uint32_t)T>(xo[i], k, tid + NT * i, xl, k * 3u, (float *)(xl + (uint64_t)T * k * 3u), k / 8u);
   for (uint32_t o = tid + NT * kXr; o < noct; o += NT) {
     XOct v;
-    x_load(x, k, o, v);
-    x_store(v, k, o, xl, k * 3u, (float *)(xl + (uint64_t)T * k * 3u), k / 8u);
+    x_load<(uint32_t)T>(x, k, o, v);
+    x_store<(uint32_t)T>(v, k, o, xl, k * 3u, (float *)(xl + (uint64_t)T * k * 3u), k / 8u);
   }
   __syncthreads();
 
@@ -810,7 +839,7 @@ template <int TYPE> struct MtStage {
 
 template <int TYPE, int TG, int NW>
 __global__ __launch_bounds__(NW * 64) void k_gemv_mt(WeightView wv, const float *__restrict__ x,
-                                                     float *__restrict__ y, uint32_t tokens, int S) {
+                                                     float *__restrict__ y, uint32_t tokens, uint32_t s_log2) {
   using W = MtW<TYPE>;
   using ST = MtStage<TYPE>;
   constexpr bool kTab = TYPE == IQ2_XXS;
@@ -822,9 +851,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(WeightView wv, const float 
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t rows = wv.rows, k = wv.k;
-  const uint32_t RT = (uint32_t)NW / (uint32_t)S, rt = wave / (uint32_t)S, sl = wave % (uint32_t)S;
+  // S = 2^s_log2 k slices (shifts: no divisions before the first loads)
+  const uint32_t S = 1u << s_log2, RT = (uint32_t)NW >> s_log2, rt = wave >> s_log2, sl = wave & (S - 1u);
   const uint32_t r0 = (blockIdx.x * RT + rt) * 16u;  // first row of the wave
-  const uint32_t ks = k / (uint32_t)S, k0 = sl * ks, passes = ks / 256u;
+  const uint32_t ks = k >> s_log2, k0 = sl * ks, passes = ks / 256u;
   // per token: digits 3 k bytes + 32, group data k / 8 floats + 4 (the
   // padding spreads the 4 tokens of an MFMA over different LDS banks)
   const uint32_t dstr = 3u * k + 32u, mstr = k / 8u + 4u;
@@ -869,7 +899,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(WeightView wv, const float 
   XOct xo[kXr];
 #pragma unroll
   for (uint32_t i = 0; i < kXr; ++i)
-    if (tid + NT * i < noct) x_load(x, k, tid + NT * i, xo[i]);
+    if (tid + NT * i < noct) x_load<(uint32_t)T>(x, k, tid + NT * i, xo[i]);
   uint64_t gent = 0;
   if constexpr (kTab) gent = c_grid_mx[tid & 255u];
   __asm__ volatile("" ::: "memory");
@@ -881,11 +911,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(WeightView wv, const float 
   }
 #pragma unroll
   for (uint32_t i = 0; i < kXr; ++i)
-    if (tid + NT * i < noct) x_store(xo[i], k, tid + NT * i, xl, dstr, metab, mstr);
+    if (tid + NT * i < noct) x_store<(uint32_t)T>(xo[i], k, tid + NT * i, xl, dstr, metab, mstr);
   for (uint32_t o = tid + NT * kXr; o < noct; o += NT) {
     XOct v;
-    x_load(x, k, o, v);
-    x_store(v, k, o, xl, dstr, metab, mstr);
+    x_load<(uint32_t)T>(x, k, o, v);
+    x_store<(uint32_t)T>(v, k, o, xl, dstr, metab, mstr);
   }
   if (tid < 4u) ((uint32_t *)(xl + xbytes))[tid] = 0u;  // the zero plane
   // tokens past `tokens`: zero digits and group data
@@ -1111,7 +1141,13 @@ static hipError_t mx_launch(const WeightView &wv, const float *x, float *y, cons
     if (e != hipSuccess) return e;
     grid = grid < res ? grid : res;
   }
-  hipLaunchKernelGGL((k_gemv_mx<TYPE, T, NW>), dim3(grid), dim3(NW * 64), p.lds_bytes, s, wv, x, y, p.ksplit);
+  MxGeo geo;
+  geo.s_log2 = (uint32_t)__builtin_ctz((unsigned)p.ksplit);
+  geo.ntask = wv.k / 64u / (uint32_t)p.ksplit;
+  geo.passes = (geo.ntask + 15u) / 16u;
+  geo.tq = p.tiles / grid;
+  geo.tr = p.tiles % grid;
+  hipLaunchKernelGGL((k_gemv_mx<TYPE, T, NW>), dim3(grid), dim3(NW * 64), p.lds_bytes, s, wv, x, y, geo);
   return hipGetLastError();
 }
 
@@ -1210,7 +1246,7 @@ static hipError_t mt_launch(const WeightView &wv, const float *x, float *y, uint
     attr = true;
   }
   hipLaunchKernelGGL((k_gemv_mt<TYPE, TG, NW>), dim3(p.grid), dim3(NW * 64), p.lds_bytes, s, wv, x, y, tokens,
-                     p.ksplit);
+                     (uint32_t)__builtin_ctz((unsigned)p.ksplit));
   return hipGetLastError();
 }
 
