@@ -205,7 +205,8 @@ def main():
             after = ctx.stats()
             groups = after["skinny"] - before["skinny"]
             path = "gemm" if after["gemm"] > before["gemm"] else (
-                f"gemv x {groups} token groups" if groups else "gemv")
+                "split-x" if after["split"] > before["split"] else (
+                    f"gemv x {groups} token groups" if groups else "gemv"))
             steps = 40 if cfg.gemm else 100
             t_ms = time_steps(torch, ctx, cfg, steps, 5)
             gb = cfg.bytes / (t_ms * 1e-3) / 1e9

@@ -31,6 +31,9 @@ struct eff_ctx {
   size_t topk_scratch_bytes = 0;
   void *xh_scratch = nullptr;       // fp16 copy of the GEMM activations
   size_t xh_scratch_bytes = 0;
+  void *sx_scratch = nullptr;       // x as fp16 hi/lo parts for the split-x product
+  size_t sx_scratch_bytes = 0;
+  int64_t sx_config = 0;
 };
 
 struct eff_buf {
@@ -115,7 +118,10 @@ int weight_view(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint
   return EFF_OK;
 }
 
+int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens);
+
 int run_gemv(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
+  if (ctx->gemv_kernel == 0 && sx_applies(wv, tokens)) return run_sx(ctx, wv, x, y, tokens);
   GemvPlan p;
   hipError_t e;
   if (ctx->gemv_kernel == 0 && gemv_mt_plan(wv, tokens, p)) {
@@ -142,6 +148,16 @@ int grow(eff_ctx *ctx, void **p, size_t *have, size_t need, const char *what) {
   }
   if (hipMalloc(p, need) != hipSuccess) return fail(ctx, EFF_E_NOMEM, "%s scratch of %zu bytes", what, need);
   *have = need;
+  return EFF_OK;
+}
+
+// Split-x matrix-core product (Q2_K, Q4_K, IQ2_XXS from 4 tokens, f32-accurate).
+int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
+  int rc = grow(ctx, &ctx->sx_scratch, &ctx->sx_scratch_bytes, sx_x_bytes(wv.type, tokens, wv.k), "split-x");
+  if (rc) return rc;
+  hipError_t e = launch_sx(wv, x, y, tokens, ctx->sx_scratch, (int)ctx->sx_config, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "split-x launch");
+  ++ctx->stats.split;
   return EFF_OK;
 }
 
@@ -179,6 +195,7 @@ int eff_shutdown(eff_ctx *ctx) {
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->topk_scratch) (void)hipFree(ctx->topk_scratch);
   if (ctx->xh_scratch) (void)hipFree(ctx->xh_scratch);
+  if (ctx->sx_scratch) (void)hipFree(ctx->sx_scratch);
   if (ctx->own) (void)hipStreamDestroy(ctx->own);
   delete ctx;
   return EFF_OK;
@@ -216,6 +233,10 @@ int eff_set_option(eff_ctx *ctx, int option, int64_t value) {
     case EFF_OPT_GEMV_KERNEL:
       if (value < 0 || value > 1) return fail(ctx, EFF_E_INVALID, "GEMV kernel must be 0 or 1, got %lld", (long long)value);
       ctx->gemv_kernel = value;
+      return EFF_OK;
+    case EFF_OPT_SPLIT_CONFIG:
+      if (value < 0 || value > 2) return fail(ctx, EFF_E_INVALID, "split-x configuration must be 0, 1 or 2, got %lld", (long long)value);
+      ctx->sx_config = value;
       return EFF_OK;
     default: return fail(ctx, EFF_E_INVALID, "unknown option %d", option);
   }
@@ -364,6 +385,10 @@ int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint
     if (!rc) ++ctx->stats.gemv;
     return rc;
   }
+  // Q2_K, Q4_K, IQ2_XXS: the reference has no f16 GEMM for these types (DRIFT
+  // and GEMM2 read Q8_0/Q4_0 only) and runs its f32 kernel at every token
+  // count; so does this router, on the split-x matrix cores.
+  if (ctx->gemv_kernel == 0 && sx_applies(wv, tokens)) return run_sx(ctx, wv, xp, yp, tokens);
   if ((int64_t)tokens >= ctx->gemm_min_tokens) {
     rc = run_gemm(ctx, wv, xp, yp, tokens);
     if (!rc) ++ctx->stats.gemm;

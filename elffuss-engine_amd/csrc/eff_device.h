@@ -72,6 +72,38 @@ __device__ __forceinline__ float h2f(uint32_t h) {
 }
 
 
+// ---------------------------------------------------------------------------
+// Direct-to-LDS loads: 4 or 16 bytes per lane from the buffer (voffset +
+// soffset) into LDS at lds + 4 * lane or lds + 16 * lane. Written as inline
+// assembly so that the compiler, which cannot tell a stage being filled from
+// one being read, adds no vmcnt(0) before LDS reads; callers wait explicitly
+// (wait_vm) before reading what they loaded.
+__device__ __forceinline__ void dma16(rsrc_t r, const uint8_t *lds, uint32_t voff, uint32_t soff) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(r), "s"(so)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ void dma4(rsrc_t r, const uint8_t *lds, uint32_t voff, uint32_t soff) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(r), "s"(so)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
+template <uint32_t N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((int)((N & 15u) | ((N >> 4) << 14) | 0x0F70u));
+}
+
+
 // Where the blocks of a weight tile live: `q` covers the GGUF blocks (or the
 // Q8_0R quants) from the tile's first block on, `s` the Q8_0R scales.
 struct BufSrc {

@@ -48,26 +48,6 @@ constexpr uint32_t kWM = 1, kWN = 4, kNW = kWM * kWN, kFN = kBN / 32 / kWN;
 constexpr uint32_t kWDma = (kWG + kNW - 1) / kNW;  // weight loads of a wave per step (at most)
 static_assert(kWS % 1024 == 0, "whole loads");
 
-// 16 bytes per lane from the buffer (voffset + soffset) into LDS at
-// lds + 16 * lane. Written as inline assembly so that the compiler, which
-// cannot tell the stages' loads and reads apart, adds no vmcnt(0) before the
-// reads of the other stages; the waits are explicit (wait_vm).
-__device__ __forceinline__ void dma16(rsrc_t r, const uint8_t *lds, uint32_t voff, uint32_t soff) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(m0), "v"(voff), "s"(r), "s"(so)
-               : "memory", "m0");
-}
-
-// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
-template <uint32_t N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N < 64, "vmcnt");
-  __builtin_amdgcn_s_waitcnt((int)((N & 15u) | ((N >> 4) << 14) | 0x0F70u));
-}
-
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const uint32_t *)p; }
 
 // BM tokens per tile; KS workgroups split k (KS = 2: the two halves are

@@ -1,0 +1,500 @@
+// Quantized matrix products from 4 tokens up for Q2_K, Q4_K and IQ2_XXS, to
+// f32 accuracy (the reference runs these types through its f32 generic
+// kernel at every token count, ops.js:1013-1099; its f16 GEMMs read Q8_0/Q4_0
+// only, kernels.drift.wgsl.js:33, kernels.gemm2.wgsl.js:51):
+//   Y[t][row] = sum_k W[row][k] X[t][k].
+//
+// Weights. Per 256-weight block the decoders of kernels.wgsl.js:194-250 and
+// 368-396 are an integer u times the block scale, minus a group minimum:
+//   Q2_K     w = d (sc & 15) q - dmin (sc >> 4)   u = (sc & 15) q <= 45     (16-weight groups)
+//   Q4_K     w = d sc q - dmin m                  u = sc q        <= 945    (32-weight groups)
+//   IQ2_XXS  w = (d / 8) (2 ls + 1) (+-g)         u = (2 ls + 1)(+-g) <= 1333
+// so  sum_k w x = d sum_k u x - dmin sum_g mn_g S_g,  S_g = sum of x over group g.
+// Every u is an integer below 2048, exact in fp16.
+//
+// x. Per token and block, x is scaled by 2^-e with max|x| < 2^(e) and split
+// into fp16 parts hi = fp16(x 2^(14-e)), lo = fp16(x 2^(14-e) - hi): 22
+// significant bits. k_sx_prep writes them (and hi/lo of the group sums) once
+// per launch, in the operand order of the matrix instruction.
+//
+// MFMA. v_mfma_f32_32x32x16_f16 multiplies A = 16 tokens x {hi, lo} (32 rows)
+// by B = u of 32 weight rows (16 k): products of fp16 values are exact in the
+// f32 accumulator. Lane l holds D for weight row l % 32 and x rows
+// 8 (v / 4) + 4 (l / 32) + v % 4: v < 8 the hi part of a token, v + 8 its lo
+// part. One more MFMA per block forms the minimum sums (A = group sums, B =
+// the group minima), and each block is folded once:
+//   acc += ((D_hi + D_lo) d - (Dm_hi + Dm_lo) dmin') 2^(e - 14).
+//
+// Workgroup: NW waves over the same 32 RF weight rows and TT tiles of 16
+// tokens, each wave on its own k blocks; the waves' sums are added in a fixed
+// order through LDS. Raw blocks are staged per wave by direct-to-LDS dword
+// loads into rows of an odd number of dwords (the 32 rows a matrix
+// instruction reads land in 32 different banks).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/elffuss_amd.h"
+#include "eff_device.h"
+#include "eff_formats.h"
+#include "eff_kernels.h"
+
+namespace eff {
+
+static __constant__ uint64_t c_grid_sx[256] = {
+#include "iq2xxs_grid.inc"
+};
+
+namespace {
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t kSxP = 4;  // steps of x fragments loaded ahead
+
+template <int TYPE>
+constexpr uint32_t sx_slots() {  // x slots of 1 KB per (token tile, block): 16 steps (+ group sums)
+  return TYPE == IQ2_XXS ? 16u : 17u;
+}
+
+// ---------------------------------------------------------------------------
+// x -> fp16 hi/lo parts. A wave per (token, block); lane l holds x values
+// 4l .. 4l+3 of the block, i.e. step l / 4, lane half (l / 2) % 2, halves
+// 4 (l % 2) .. of the 8 a lane feeds to one matrix instruction.
+// Layout per (token tile tt, block b): slot s (1 KB) at ((tt nb + b) NS + s) KB,
+// lane L's 16 bytes at 16 L, L = 32 half + 16 part + token % 16.
+// xp[(tt nb + b) 16 + token % 16] = 2^(e - 14) (NaN for a block holding a
+// non-finite x, which makes every output of that token non-finite).
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_sx_prep(const float *__restrict__ x, uint32_t tokens, uint32_t k,
+                                                 uint8_t *__restrict__ xa, float *__restrict__ xp) {
+  constexpr uint32_t NS = sx_slots<TYPE>();
+  const uint32_t lane = threadIdx.x & 63u, bi = blockIdx.x, nb = k / 256u;
+  const uint32_t t = blockIdx.y * 4u + (threadIdx.x >> 6);
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (t < tokens) v = *(const float4 *)(x + (uint64_t)t * k + 256u * bi + 4u * lane);
+  const bool fin = isfinite(v.x) && isfinite(v.y) && isfinite(v.z) && isfinite(v.w);
+  float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  m = fin ? m : INFINITY;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  const bool ok = m < INFINITY;
+  int e = 0;
+  if (ok && m > 0.f) (void)frexpf(m, &e);  // m < 2^e
+  const int sh = 14 - e;
+  float xs[4] = {ldexpf(v.x, sh), ldexpf(v.y, sh), ldexpf(v.z, sh), ldexpf(v.w, sh)};
+  if (!ok) xs[0] = xs[1] = xs[2] = xs[3] = 0.f;
+  half4 hi, lo;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hi[i] = (_Float16)xs[i];
+    lo[i] = (_Float16)(xs[i] - (float)hi[i]);
+  }
+  const uint32_t tt = t >> 4, tl = t & 15u;
+  uint8_t *blk = xa + ((uint64_t)tt * nb + bi) * NS * 1024u;
+  uint8_t *slot = blk + (lane >> 2) * 1024u;
+  const uint32_t hf = (lane >> 1) & 1u, q = lane & 1u;
+  *(half4 *)(slot + 16u * (32u * hf + tl) + 8u * q) = hi;
+  *(half4 *)(slot + 16u * (32u * hf + 16u + tl) + 8u * q) = lo;
+  if constexpr (TYPE != IQ2_XXS) {
+    // group sums (16 values for Q2_K, 32 for Q4_K), scaled to the range of x
+    constexpr uint32_t GL = TYPE == Q2_K ? 4u : 8u;  // lanes per group
+    float sum = (xs[0] + xs[1]) + (xs[2] + xs[3]);
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    if (GL == 8u) sum += __shfl_xor(sum, 4);
+    const float sp = sum * (TYPE == Q2_K ? 0.0625f : 0.03125f);
+    const _Float16 shi = (_Float16)sp, slo = (_Float16)(sp - (float)shi);
+    uint8_t *ms = blk + 16u * 1024u;
+    if (lane % GL == 0u) {
+      const uint32_t g = lane / GL, hm = g >> 3, jj = g & 7u;
+      *(_Float16 *)(ms + 16u * (32u * hm + tl) + 2u * jj) = shi;
+      *(_Float16 *)(ms + 16u * (32u * hm + 16u + tl) + 2u * jj) = slo;
+    }
+    if (TYPE == Q4_K && lane < 2u) *(u32x4 *)(ms + 16u * (32u + 16u * lane + tl)) = u32x4{0u, 0u, 0u, 0u};
+  }
+  if (lane == 0u) xp[((uint64_t)tt * nb + bi) * 16u + tl] = ok ? ldexpf(1.f, e - 14) : NAN;
+}
+
+// ---------------------------------------------------------------------------
+// Weight operands. `r` points to the staged dwords of the lane's row (the
+// block's first byte at byte offset `a` of r[0]); `step` returns the 8
+// weights u of step s (k 16 s + 8 h .. + 7 of the block) for lane half h.
+
+// 4 bytes b (each < 1024 after the caller's masking) -> 1024 + b as fp16 pairs
+__device__ __forceinline__ half2v h1024_lo(uint32_t v) {
+  return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u));
+}
+__device__ __forceinline__ half2v h1024_hi(uint32_t v) {
+  return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u));
+}
+
+// 8 unsigned bytes q (v0: q0..q3, v1: q4..q7) -> sc * q as fp16, exact
+// (sc * q < 2048; the fused multiply-add rounds once: (1024 + q) sc - 1024 sc)
+__device__ __forceinline__ half8 dec_scaled(uint32_t v0, uint32_t v1, uint32_t sc) {
+  const _Float16 s = (_Float16)(float)sc, o = (_Float16)(-1024.f * (float)sc);
+  const half2v s2 = {s, s}, o2 = {o, o};
+  const half2v a = __builtin_elementwise_fma(h1024_lo(v0), s2, o2);
+  const half2v b = __builtin_elementwise_fma(h1024_hi(v0), s2, o2);
+  const half2v c = __builtin_elementwise_fma(h1024_lo(v1), s2, o2);
+  const half2v d = __builtin_elementwise_fma(h1024_hi(v1), s2, o2);
+  return half8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+// 8 unsigned bytes -> fp16 (exact below 1024)
+__device__ __forceinline__ half8 dec_plain(uint32_t v0, uint32_t v1) {
+  const half2v o2 = {(_Float16)-1024.f, (_Float16)-1024.f};
+  const half2v a = h1024_lo(v0) + o2, b = h1024_hi(v0) + o2, c = h1024_lo(v1) + o2, d = h1024_hi(v1) + o2;
+  return half8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+__device__ __forceinline__ uint32_t byte_of(const uint32_t *w, uint32_t i) { return (w[i >> 2] >> (8u * (i & 3u))) & 0xFFu; }
+
+template <int TYPE> struct SxW;
+
+// Q2_K, 84 bytes: scales[16] | qs[64] | d | dmin (kernels.wgsl.js:194-222).
+// Step s = the 16-weight group s: qs bytes 32 n + 16 h' + i at bit shift 2 g
+// (s = 8 n + 2 g + h'), scale byte s.
+template <> struct SxW<Q2_K> {
+  static constexpr uint32_t BB = 84, DW = 21, ST = 21;
+  static constexpr bool MINS = true;
+  uint32_t sc[4];
+  float d, dm;
+  __device__ void block(const uint32_t *r, uint32_t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[i] = r[i];
+    const uint32_t w = r[20];
+    d = h2f(w & 0xFFFFu);
+    dm = 16.f * h2f(w >> 16);  // group sums are stored divided by 16
+  }
+  __device__ half8 step(const uint32_t *r, int s, uint32_t h, const uint32_t *) const {
+    const int n = s >> 3, hp = s & 1, g = (s >> 1) & 3;
+    const uint32_t *p = r + 4 + 8 * n + 4 * hp + 2u * h;
+    const uint32_t v0 = (p[0] >> (2 * g)) & 0x03030303u, v1 = (p[1] >> (2 * g)) & 0x03030303u;
+    return dec_scaled(v0, v1, byte_of(sc, (uint32_t)s) & 15u);
+  }
+  __device__ half8 mins(uint32_t h) const {
+    const uint32_t w0 = h ? sc[2] : sc[0], w1 = h ? sc[3] : sc[1];
+    return dec_plain((w0 >> 4) & 0x0F0F0F0Fu, (w1 >> 4) & 0x0F0F0F0Fu);
+  }
+};
+
+// Q4_K, 144 bytes: d | dmin | scales[12] | qs[128] (kernels.wgsl.js:94-104,
+// 227-250). Step s: sub-block pair j = s / 4, nibble (s / 2) % 2, qs bytes
+// 32 j + 16 (s % 2) + 8 h ..; 6-bit scale and minimum of sub-block s / 2.
+template <> struct SxW<Q4_K> {
+  static constexpr uint32_t BB = 144, DW = 36, ST = 37;
+  static constexpr bool MINS = true;
+  uint32_t q[3];
+  float d, dm;
+  __device__ void block(const uint32_t *r, uint32_t) {
+    const uint32_t w = r[0];
+    d = h2f(w & 0xFFFFu);
+    dm = 32.f * h2f(w >> 16);  // group sums are stored divided by 32
+    q[0] = r[1];
+    q[1] = r[2];
+    q[2] = r[3];
+  }
+  __device__ uint32_t scale(uint32_t i) const {
+    return i < 4u ? byte_of(q, i) & 63u : (byte_of(q, i + 4u) & 15u) | ((byte_of(q, i - 4u) >> 6) << 4);
+  }
+  __device__ uint32_t minv(uint32_t i) const {
+    return i < 4u ? byte_of(q, i + 4u) & 63u : (byte_of(q, i + 4u) >> 4) | ((byte_of(q, i) >> 6) << 4);
+  }
+  __device__ half8 step(const uint32_t *r, int s, uint32_t h, const uint32_t *) const {
+    const int j = s >> 2, nib = (s >> 1) & 1;
+    const uint32_t *p = r + 4 + 8 * j + 4 * (s & 1) + 2u * h;
+    const uint32_t v0 = (p[0] >> (4 * nib)) & 0x0F0F0F0Fu, v1 = (p[1] >> (4 * nib)) & 0x0F0F0F0Fu;
+    return dec_scaled(v0, v1, scale((uint32_t)s >> 1));
+  }
+  __device__ half8 mins(uint32_t h) const {
+    uint32_t v0 = 0, v1 = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      v0 |= minv(i) << (8u * i);
+      v1 |= minv(i + 4u) << (8u * i);
+    }
+    const half8 m = dec_plain(v0, v1);
+    const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+    return h ? z : m;
+  }
+};
+
+// IQ2_XXS, 66 bytes: d | 8 x (grid indices a0, signs + scale a1)
+// (kernels.wgsl.js:368-396). Step s: group s / 2, grid entry l = 2 (s % 2) + h.
+// LDS tables: the grid as fp16 (256 x 16 bytes) and the fp16 sign bits of
+// each 7-bit sign field with its parity bit (128 x 16 bytes).
+template <> struct SxW<IQ2_XXS> {
+  static constexpr uint32_t BB = 66, DW = 17, ST = 17;
+  static constexpr bool MINS = false;
+  uint32_t a;  // byte offset of the block in r[0] (0 or 2)
+  float d, dm;
+  __device__ void block(const uint32_t *r, uint32_t off) {
+    a = off;
+    d = 0.125f * h2f(off ? (r[0] >> 16) : (r[0] & 0xFFFFu));
+    dm = 0.f;
+  }
+  __device__ half8 step(const uint32_t *r, int s, uint32_t h, const uint32_t *tab) const {
+    const uint32_t ib = (uint32_t)s >> 1, o = a + 2u + 8u * ib, sh = o & 3u;
+    const uint32_t *p = r + (o >> 2);
+    const uint32_t w0 = p[0], w1 = p[1], w2 = p[2];
+    const uint32_t a0 = __builtin_amdgcn_alignbyte(w1, w0, sh), a1 = __builtin_amdgcn_alignbyte(w2, w1, sh);
+    const uint32_t l = 2u * ((uint32_t)s & 1u) + h;
+    const uint32_t gi = (a0 >> (8u * l)) & 0xFFu, sg = (a1 >> (7u * l)) & 127u;
+    const u32x4 g = *(const u32x4 *)(tab + 4u * gi), m = *(const u32x4 *)(tab + 1024u + 4u * sg);
+    const _Float16 c = (_Float16)(float)(2u * (a1 >> 28) + 1u);
+    const half2v c2 = {c, c};
+    const half2v v0 = __builtin_bit_cast(half2v, g.x ^ m.x) * c2, v1 = __builtin_bit_cast(half2v, g.y ^ m.y) * c2;
+    const half2v v2 = __builtin_bit_cast(half2v, g.z ^ m.z) * c2, v3 = __builtin_bit_cast(half2v, g.w ^ m.w) * c2;
+    return half8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
+  }
+  __device__ half8 mins(uint32_t) const { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
+};
+
+constexpr uint32_t kSxTab = 6144;  // IQ2_XXS tables in LDS
+
+template <int TYPE, int TT, int RF, int NW>
+struct SxLds {
+  using W = SxW<TYPE>;
+  static constexpr uint32_t ROWS = 32u * RF;
+  static constexpr uint32_t ND = (ROWS * W::ST + 63u) / 64u;  // staging loads per lane and block
+  // stage bytes per wave, with 16 bytes of slack: the IQ2_XXS reader takes
+  // one dword past a row (unused when the block is 4-byte aligned)
+  static constexpr uint32_t SB = ND * 256u + 16u;
+  static constexpr uint32_t NE = (uint32_t)TT * RF * 512u;     // sums per wave
+  static constexpr uint32_t WORK = NW * SB > NW * NE * 4u ? NW * SB : NW * NE * 4u;
+  static constexpr uint32_t TAB = TYPE == IQ2_XXS ? kSxTab : 0u;
+  static constexpr uint32_t BYTES = TAB + WORK;
+};
+
+template <int TYPE, int TT, int RF, int NW>
+__global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__restrict__ xa,
+                                                const float *__restrict__ xp, float *__restrict__ y,
+                                                uint32_t tokens, uint32_t nbw, uint32_t xa_bytes) {
+  using W = SxW<TYPE>;
+  using L = SxLds<TYPE, TT, RF, NW>;
+  constexpr uint32_t NS = sx_slots<TYPE>();
+  constexpr uint32_t ROWS = L::ROWS, ND = L::ND;
+  __shared__ __align__(16) uint8_t lds[L::BYTES];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, j = lane & 31u, h = lane >> 5;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t rows = wv.rows, nb = wv.bpr, r0 = blockIdx.x * ROWS, tg = blockIdx.y;
+  const uint32_t rb = (uint32_t)wv.row_bytes;
+  uint32_t *tab = (uint32_t *)lds;
+  uint8_t *stage = lds + L::TAB + wave * L::SB;
+
+  if constexpr (TYPE == IQ2_XXS) {
+    if (tid < 256u) {
+      const uint64_t g = c_grid_sx[tid];
+      const half8 v = dec_plain((uint32_t)g, (uint32_t)(g >> 32));
+      *(half8 *)(tab + 4u * tid) = v;
+    }
+    if (tid < 128u) {
+      const uint32_t s8 = tid | ((uint32_t)(__builtin_popcount(tid) & 1) << 7);
+      u32x4 m;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        m[i] = (((s8 >> (2 * i)) & 1u) ? 0x8000u : 0u) | (((s8 >> (2 * i + 1)) & 1u) ? 0x80000000u : 0u);
+      *(u32x4 *)(tab + 1024u + 4u * tid) = m;
+    }
+    __syncthreads();
+  }
+
+  // staging: dword q = 64 i + lane of the stage is dword q % ST of row q / ST
+  // of the tile (the last dwords of a row and of the stage repeat valid ones)
+  const rsrc_t wsrc = make_rsrc(wv.w, wv.w_bytes);
+  uint32_t soff[ND];
+#pragma unroll
+  for (uint32_t i = 0; i < ND; ++i) {
+    const uint32_t q = 64u * i + lane, rr = q / W::ST, dw = min(q - rr * W::ST, W::DW - 1u);
+    soff[i] = min(r0 + min(rr, ROWS - 1u), rows - 1u) * rb + 4u * dw;
+  }
+  const rsrc_t xsrc = make_rsrc(xa, xa_bytes);
+
+  float acc[TT][RF][8];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+    for (int f = 0; f < RF; ++f)
+#pragma unroll
+      for (int v = 0; v < 8; ++v) acc[tt][f][v] = 0.f;
+
+  const uint32_t b0 = wave * nbw, b1 = min(b0 + nbw, nb);
+  for (uint32_t bi = b0; bi < b1; ++bi) {
+    // this block of the tile's rows into the wave's stage
+    const uint32_t bo = bi * W::BB;
+#pragma unroll
+    for (uint32_t i = 0; i < ND; ++i) {
+      if constexpr ((W::BB & 3u) == 0u)
+        dma4(wsrc, stage + 256u * i, soff[i], bo);
+      else  // staged from the 4-byte aligned floor of the block's first byte
+        dma4(wsrc, stage + 256u * i, (soff[i] + bo) & ~3u, 0u);
+    }
+    // x fragments of the first steps
+    auto xoff = [&](uint32_t tt, uint32_t s) {
+      return (((tg * TT + tt) * nb + bi) * NS + s) * 1024u;
+    };
+    u32x4 A[kSxP][TT];
+#pragma unroll
+    for (uint32_t s = 0; s < kSxP; ++s)
+#pragma unroll
+      for (uint32_t tt = 0; tt < (uint32_t)TT; ++tt)
+        A[s][tt] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)(16u * lane), (int)xoff(tt, s), 0);
+    wait_vm<kSxP * TT>();
+
+    W w[RF];
+    const uint32_t *rp[RF];
+#pragma unroll
+    for (int f = 0; f < RF; ++f) {
+      const uint32_t row = min(r0 + 32u * f + j, rows - 1u);
+      const uint32_t a = (row * rb + bo) & 3u;
+      rp[f] = (const uint32_t *)(stage + 4u * W::ST * (32u * f + j));
+      w[f].block(rp[f], a);
+    }
+    float16v D[TT][RF];
+#pragma unroll
+    for (uint32_t s = 0; s < 16u; ++s) {
+      half8 B[RF];
+#pragma unroll
+      for (int f = 0; f < RF; ++f) B[f] = w[f].step(rp[f], (int)s, h, tab);
+      const u32x4 *As = A[s % kSxP];
+      half8 a8[TT];
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) a8[tt] = __builtin_bit_cast(half8, As[tt]);
+      if (s + kSxP < 16u) {
+#pragma unroll
+        for (uint32_t tt = 0; tt < (uint32_t)TT; ++tt)
+          A[s % kSxP][tt] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)(16u * lane), (int)xoff(tt, s + kSxP), 0);
+      }
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int f = 0; f < RF; ++f) {
+          const float16v c = s == 0u ? float16v{} : D[tt][f];
+          D[tt][f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8[tt], B[f], c, 0, 0, 0);
+        }
+    }
+    // minimum sums, scales of the tokens, and the fold of the block
+#pragma unroll
+    for (uint32_t tt = 0; tt < (uint32_t)TT; ++tt) {
+      half8 am = {0, 0, 0, 0, 0, 0, 0, 0};
+      if constexpr (W::MINS)
+        am = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)(16u * lane), (int)xoff(tt, 16u), 0));
+      // (plain loads: a 16-byte buffer load whose elements are taken one by one
+      // as floats is narrowed to one dword by this compiler, every element then
+      // reading the first)
+      const float *pp = xp + ((tg * TT + tt) * nb + bi) * 16u + 4u * h;
+      const float4 pa = *(const float4 *)pp, pb = *(const float4 *)(pp + 8);
+      const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+#pragma unroll
+      for (int f = 0; f < RF; ++f) {
+        float16v Dm{};
+        if constexpr (W::MINS) Dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, w[f].mins(h), float16v{}, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          float t = (D[tt][f][v] + D[tt][f][v + 8]) * w[f].d;
+          if constexpr (W::MINS) t = __builtin_fmaf(-(Dm[v] + Dm[v + 8]), w[f].dm, t);
+          acc[tt][f][v] = __builtin_fmaf(t, pv[v], acc[tt][f][v]);
+        }
+      }
+    }
+  }
+
+  // the waves' sums, added in wave order
+  __syncthreads();
+  float *red = (float *)(lds + L::TAB);
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+    for (int f = 0; f < RF; ++f)
+#pragma unroll
+      for (int v = 0; v < 8; ++v) red[wave * L::NE + ((tt * RF + f) * 8u + v) * 64u + lane] = acc[tt][f][v];
+  __syncthreads();
+  for (uint32_t e = tid; e < L::NE; e += NW * 64u) {
+    float sum = 0.f;
+#pragma unroll
+    for (uint32_t w = 0; w < (uint32_t)NW; ++w) sum += red[w * L::NE + e];
+    const uint32_t le = e & 63u, v = (e >> 6) & 7u, fr = e >> 9, f = fr % RF, tt = fr / RF;
+    const uint32_t row = r0 + 32u * f + (le & 31u);
+    const uint32_t tok = (tg * TT + tt) * 16u + 8u * (v >> 2) + 4u * (le >> 5) + (v & 3u);
+    if (row < rows && tok < tokens) y[(uint64_t)tok * rows + row] = sum;
+  }
+}
+
+// Token tiles of 16 per wave (tt) and token groups (grid y); the x scratch
+// covers groups * tt tiles (tokens past `tokens` are zero).
+struct SxPlan {
+  uint32_t tt, cfg, groups, row_tiles, nbw;  // cfg 0: RF 1 x 8 waves, 1: RF 2 x 4 waves
+};
+
+void sx_tiles(uint32_t tokens, uint32_t &tt, uint32_t &groups) {
+  const uint32_t ttn = (tokens + 15u) / 16u;
+  tt = ttn <= 1u ? 1u : ttn <= 2u ? 2u : 4u;
+  groups = (ttn + tt - 1u) / tt;
+}
+
+SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg) {
+  SxPlan p;
+  sx_tiles(tokens, p.tt, p.groups);
+  p.cfg = cfg ? (uint32_t)(cfg - 1) : (p.tt == 4u ? 1u : 0u);
+  const uint32_t rows_per = p.cfg ? 64u : 32u, nw = p.cfg ? 4u : 8u;
+  p.row_tiles = (wv.rows + rows_per - 1u) / rows_per;
+  p.nbw = (wv.bpr + nw - 1u) / nw;
+  return p;
+}
+
+template <int TYPE, int TT, int RF, int NW>
+hipError_t sx_go(const WeightView &wv, const uint8_t *xa, const float *xp, float *y, uint32_t tokens,
+                 const SxPlan &p, hipStream_t s) {
+  const uint64_t tiles = (uint64_t)p.groups * p.tt;
+  const uint32_t xa_bytes = (uint32_t)(tiles * wv.bpr * sx_slots<TYPE>() * 1024u);
+  hipLaunchKernelGGL((k_sx<TYPE, TT, RF, NW>), dim3(p.row_tiles, p.groups), dim3(NW * 64), 0, s, wv, xa, xp, y,
+                     tokens, p.nbw, xa_bytes);
+  return hipGetLastError();
+}
+
+template <int TYPE, int TT>
+hipError_t sx_cfg(const WeightView &wv, const uint8_t *xa, const float *xp, float *y, uint32_t tokens,
+                  const SxPlan &p, hipStream_t s) {
+  return p.cfg ? sx_go<TYPE, TT, 2, 4>(wv, xa, xp, y, tokens, p, s) : sx_go<TYPE, TT, 1, 8>(wv, xa, xp, y, tokens, p, s);
+}
+
+template <int TYPE>
+hipError_t sx_type(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint8_t *scratch, int cfg,
+                   hipStream_t s) {
+  const SxPlan p = sx_plan(wv, tokens, cfg);
+  const uint32_t tiles = p.groups * p.tt, nb = wv.bpr;
+  uint8_t *xa = scratch;
+  float *xp = (float *)(scratch + (uint64_t)tiles * nb * sx_slots<TYPE>() * 1024u);
+  hipLaunchKernelGGL((k_sx_prep<TYPE>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, wv.k, xa, xp);
+  switch (p.tt) {
+    case 1: return sx_cfg<TYPE, 1>(wv, xa, xp, y, tokens, p, s);
+    case 2: return sx_cfg<TYPE, 2>(wv, xa, xp, y, tokens, p, s);
+    default: return sx_cfg<TYPE, 4>(wv, xa, xp, y, tokens, p, s);
+  }
+}
+
+}  // namespace
+
+bool sx_applies(const WeightView &wv, uint32_t tokens) {
+  return (wv.type == Q2_K || wv.type == Q4_K || wv.type == IQ2_XXS) && tokens >= 4u && wv.k % 256u == 0u;
+}
+
+size_t sx_x_bytes(int type, uint32_t tokens, uint32_t k) {
+  uint32_t tt, groups;
+  sx_tiles(tokens, tt, groups);
+  const uint64_t tiles = (uint64_t)tt * groups, nb = k / 256u;
+  return (size_t)(tiles * nb * (type == IQ2_XXS ? 16u : 17u) * 1024u + tiles * nb * 64u);
+}
+
+hipError_t launch_sx(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *scratch, int cfg,
+                     hipStream_t s) {
+  uint8_t *sc = (uint8_t *)scratch;
+  switch (wv.type) {
+    case Q2_K: return sx_type<Q2_K>(wv, x, y, tokens, sc, cfg, s);
+    case Q4_K: return sx_type<Q4_K>(wv, x, y, tokens, sc, cfg, s);
+    case IQ2_XXS: return sx_type<IQ2_XXS>(wv, x, y, tokens, sc, cfg, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace eff

@@ -60,6 +60,15 @@ uint32_t gemm_big_tile_log2(uint32_t tokens);
 hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens,
                            hipStream_t stream);
 
+// Split-x matrix-core product (eff_gemm_sx.hip): Q2_K, Q4_K, IQ2_XXS from 4
+// tokens, k % 256 == 0, f32-accurate. `scratch` holds sx_x_bytes(...) bytes
+// (x as fp16 hi/lo parts and the block scales). cfg: 0 automatic, 1: 32 rows x
+// 8 waves per workgroup, 2: 64 rows x 4 waves.
+bool sx_applies(const WeightView &wv, uint32_t tokens);
+size_t sx_x_bytes(int type, uint32_t tokens, uint32_t k);
+hipError_t launch_sx(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *scratch, int cfg,
+                     hipStream_t stream);
+
 hipError_t launch_dequant(const WeightView &wv, uint32_t n_blocks, float *out, hipStream_t stream);
 
 // Top-k scratch: per chunk 2 u32 (count, flags) + 2 * kTopkChunkCap u32 (id, bits).

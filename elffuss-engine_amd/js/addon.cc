@@ -269,6 +269,7 @@ napi_value Stats(napi_env env, napi_callback_info info) {
   napi_set_named_property(env, o, "dequant", make_int(env, (int64_t)s.dequant));
   napi_set_named_property(env, o, "topk", make_int(env, (int64_t)s.topk));
   napi_set_named_property(env, o, "notApplicable", make_int(env, (int64_t)s.not_applicable));
+  napi_set_named_property(env, o, "split", make_int(env, (int64_t)s.split));
   return o;
 }
 

@@ -42,16 +42,19 @@ def test_js_shim_gpu(eff, orc, tmp_path):
     out = json.loads((tmp_path / "out.json").read_text())
     for name, (base, w, x, rows, k, tokens) in data.items():
         ot = orc.NAMES[base]
-        ref = (orc.gemm_f16 if tokens >= 64 else orc.gemv_f64)(ot, w, rows, k, x, tokens)
+        # matmul: f32-accurate for the split-x types at every M, fp16 GEMM from 64 tokens otherwise
+        f32 = tokens < 64 or base in ("Q2_K", "Q4_K", "IQ2_XXS")
+        ref = (orc.gemv_f64 if f32 else orc.gemm_f16)(ot, w, rows, k, x, tokens)
         check_close(np.array(out[name], np.float32), ref, f"js matmul {name}")
         if tokens <= 8:
             check_close(np.array(out[name + ":gemv"], np.float32), ref, f"js gemv {name}")
         if tokens >= 64:
-            check_close(np.array(out[name + ":gemm2"], np.float32), ref, f"js gemm2 {name}")
+            check_close(np.array(out[name + ":gemm2"], np.float32), orc.gemm_f16(ot, w, rows, k, x, tokens),
+                        f"js gemm2 {name}")
         e, _ = eff.geometry(base)
         assert np.array_equal(np.array(out[name + ":dequant"], np.uint32),
                               orc.dequant(ot, w, rows * k // e).view(np.uint32))
     ids, bits, _ = orc.topk(logits.view(np.uint32), 40)
     assert out["topk"]["ids"] == ids.tolist() and out["topk"]["bits"] == bits.tolist()
     assert out["topk"]["bitsS"] == logits.view(np.uint32)[[5, 69999]].tolist()
-    assert out["stats"]["topk"] == 1 and out["stats"]["gemm"] >= 2
+    assert out["stats"]["topk"] == 1 and out["stats"]["gemm"] >= 1 and out["stats"]["split"] >= 2

@@ -191,6 +191,81 @@ def test_gemm_q8_0_k_not_multiple_of_step(ctx, eff, orc):
     check_close(yb.read(np.float32), orc.gemm_f16(orc.Q8_0, gguf, rows, k, x, tokens), "gemm Q8_0 k=96")
 
 
+# ---- split-x product (Q2_K, Q4_K, IQ2_XXS from 4 tokens) -----------------------------
+
+SPLIT_TYPES = ["Q2_K", "Q4_K", "IQ2_XXS"]
+
+
+@pytest.mark.parametrize("tname", SPLIT_TYPES)
+@pytest.mark.parametrize("tokens", [4, 7, 16, 17, 33, 64, 100, 129])
+def test_split_x_vs_f64_oracle(ctx, eff, orc, tname, tokens):
+    """f32 accuracy at every token count: 1, 2 and 4 token tiles per wave and
+    several token groups; rows not a multiple of the 32/64-row tiles; k = 2304
+    (9 blocks: waves with one and with two blocks, odd IQ2_XXS block offsets)."""
+    rows, k = 77, 2304
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 300 + tokens)
+    x = eff.fill_normal(3000 + tokens, 1.0, tokens * k)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    before = ctx.stats()["split"]
+    ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+    assert ctx.stats()["split"] == before + 1
+    check_close(yb.read(np.float32), orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens),
+                f"split-x {tname} M={tokens}")
+    for b in (wb, xb, yb):
+        b.free()
+
+
+@pytest.mark.parametrize("tname", SPLIT_TYPES)
+@pytest.mark.parametrize("k", [256, 512, 8192])
+def test_split_x_k_and_configs(ctx, eff, orc, tname, k):
+    """One block per row, fewer blocks than waves, many blocks per wave; both
+    workgroup configurations (32 rows x 8 waves, 64 rows x 4 waves) meet the bar."""
+    rows, tokens = 100, 20
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 400 + k)
+    x = eff.fill_normal(4000 + k, 1.0, tokens * k)
+    wb, xb = ctx.upload(data), ctx.upload(x)
+    ref = orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens)
+    for cfg in (1, 2):
+        yb = ctx.alloc(tokens * rows * 4)
+        ctx.set_option(eff.OPT_SPLIT_CONFIG, cfg)
+        try:
+            ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+        finally:
+            ctx.set_option(eff.OPT_SPLIT_CONFIG, 0)
+        check_close(yb.read(np.float32), ref, f"split-x {tname} k={k} cfg={cfg}")
+        yb.free()
+
+
+@pytest.mark.parametrize("tname", SPLIT_TYPES)
+def test_split_x_dynamic_range_and_non_finite(ctx, eff, orc, tname):
+    """x scaled per (token, 256-block): zero, tiny, huge and subnormal values in
+    one block, outliers among ordinary values, a whole token at 1e-3; a NaN or an
+    infinity makes only its own token's outputs non-finite."""
+    rows, k, tokens = 40, 2048, 6
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 77)
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 1, (tokens, k)).astype(np.float32)
+    x[0, :32] = 0.0
+    x[0, 32:64] *= 1e-30
+    x[0, 64:96] *= 1e30
+    x[1, ::37] *= 1e4
+    x[1, 96:128] = np.float32(1e-40)
+    x[2, :] *= 1e-3
+    x[3, 256:512] = 0.0
+    wb, xb, yb = ctx.upload(data), ctx.upload(x.reshape(-1)), ctx.alloc(tokens * rows * 4)
+    ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+    check_close(yb.read(np.float32), orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x.reshape(-1), tokens),
+                f"split-x {tname} x range")
+    x[4, 700] = np.nan
+    x[5, 1500] = np.inf
+    xb2 = ctx.upload(x.reshape(-1))
+    ctx.qmatmul(t, wb, xb2, yb, rows, k, tokens)
+    y = yb.read(np.float32).reshape(tokens, rows)
+    assert np.all(~np.isfinite(y[4])) and np.all(~np.isfinite(y[5])) and np.all(np.isfinite(y[:4]))
+    for b in (wb, xb, xb2, yb):
+        b.free()
+
+
 # ---- router, NOT_APPLICABLE and errors -----------------------------------------------
 
 def test_router_paths_and_stats(ctx, eff, orc):
@@ -198,16 +273,28 @@ def test_router_paths_and_stats(ctx, eff, orc):
     t, data, gguf, n = make_weights(eff, "Q4_K", rows, k, 90)
     wb = ctx.upload(data)
     before = ctx.stats()
-    for tokens, oracle_fn in ((1, orc.gemv_f64), (9, orc.gemv_f64), (33, orc.gemv_f64), (64, orc.gemm_f16)):
+    for tokens in (1, 5, 9, 33, 64):
         x = eff.fill_normal(91 + tokens, 1.0, tokens * k)
         xb, yb = ctx.upload(x), ctx.alloc(tokens * rows * 4)
         ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
-        check_close(yb.read(np.float32), oracle_fn(orc.Q4_K, gguf, rows, k, x, tokens), f"matmul T={tokens}")
+        check_close(yb.read(np.float32), orc.gemv_f64(orc.Q4_K, gguf, rows, k, x, tokens), f"matmul T={tokens}")
     after = ctx.stats()
-    assert after["gemv"] - before["gemv"] == 1
-    # 9..63 tokens: groups of 16 on the multi-token matrix-core GEMV (Q4_K, k % 256 == 0)
-    assert after["skinny"] - before["skinny"] == 1 + 3
-    assert after["gemm"] - before["gemm"] == 1
+    # 1..8 tokens count as GEMV calls; Q4_K from 4 tokens runs the split-x
+    # product at every token count (f32 accuracy, as the reference's generic kernel)
+    assert after["gemv"] - before["gemv"] == 2
+    assert after["split"] - before["split"] == 4
+    assert after["skinny"] == before["skinny"] and after["gemm"] == before["gemm"]
+    # Q8_0 keeps the token-group GEMV below 64 tokens and the fp16 GEMM from 64
+    t8, data8, gguf8, _ = make_weights(eff, "Q8_0", rows, k, 92)
+    w8 = ctx.upload(data8)
+    before = ctx.stats()
+    for tokens, oracle_fn in ((33, orc.gemv_f64), (64, orc.gemm_f16)):
+        x = eff.fill_normal(93 + tokens, 1.0, tokens * k)
+        xb, yb = ctx.upload(x), ctx.alloc(tokens * rows * 4)
+        ctx.qmatmul(t8, w8, xb, yb, rows, k, tokens)
+        check_close(yb.read(np.float32), oracle_fn(orc.Q8_0, gguf8, rows, k, x, tokens), f"matmul Q8_0 T={tokens}")
+    after = ctx.stats()
+    assert after["skinny"] - before["skinny"] == 3 and after["gemm"] - before["gemm"] == 1
 
 
 def test_not_applicable_and_errors(ctx, eff):
