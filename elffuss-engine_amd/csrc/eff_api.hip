@@ -235,7 +235,7 @@ int eff_set_option(eff_ctx *ctx, int option, int64_t value) {
       ctx->gemv_kernel = value;
       return EFF_OK;
     case EFF_OPT_SPLIT_CONFIG:
-      if (value < 0 || value > 2) return fail(ctx, EFF_E_INVALID, "split-x configuration must be 0, 1 or 2, got %lld", (long long)value);
+      if (value < 0 || value > 3) return fail(ctx, EFF_E_INVALID, "split-x configuration must be 0..3, got %lld", (long long)value);
       ctx->sx_config = value;
       return EFF_OK;
     default: return fail(ctx, EFF_E_INVALID, "unknown option %d", option);

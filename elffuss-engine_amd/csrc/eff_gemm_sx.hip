@@ -49,7 +49,6 @@ namespace {
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
-constexpr uint32_t kSxP = 4;  // steps of x fragments loaded ahead
 
 template <int TYPE>
 constexpr uint32_t sx_slots() {  // x slots of 1 KB per (token tile, block): 16 steps (+ group sums)
@@ -64,11 +63,18 @@ constexpr uint32_t sx_slots() {  // x slots of 1 KB per (token tile, block): 16 
 // lane L's 16 bytes at 16 L, L = 32 half + 16 part + token % 16.
 // xp[(tt nb + b) 16 + token % 16] = 2^(e - 14) (NaN for a block holding a
 // non-finite x, which makes every output of that token non-finite).
+// With yz > 0 the kernel also zeroes y[0 .. yz) (the main kernel then adds
+// its two k halves into y).
 template <int TYPE>
 __global__ __launch_bounds__(256) void k_sx_prep(const float *__restrict__ x, uint32_t tokens, uint32_t k,
-                                                 uint8_t *__restrict__ xa, float *__restrict__ xp) {
+                                                 uint8_t *__restrict__ xa, float *__restrict__ xp,
+                                                 float *__restrict__ y, uint32_t yz) {
   constexpr uint32_t NS = sx_slots<TYPE>();
   const uint32_t lane = threadIdx.x & 63u, bi = blockIdx.x, nb = k / 256u;
+  {
+    const uint32_t n = gridDim.x * gridDim.y * 256u;
+    for (uint32_t i = (blockIdx.y * gridDim.x + blockIdx.x) * 256u + threadIdx.x; i < yz; i += n) y[i] = 0.f;
+  }
   const uint32_t t = blockIdx.y * 4u + (threadIdx.x >> 6);
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
   if (t < tokens) v = *(const float4 *)(x + (uint64_t)t * k + 256u * bi + 4u * lane);
@@ -266,18 +272,21 @@ struct SxLds {
   static constexpr uint32_t BYTES = TAB + WORK;
 };
 
-template <int TYPE, int TT, int RF, int NW>
+template <int TYPE, int TT, int RF, int NW, int KS>
 __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__restrict__ xa,
                                                 const float *__restrict__ xp, float *__restrict__ y,
                                                 uint32_t tokens, uint32_t nbw, uint32_t xa_bytes) {
   using W = SxW<TYPE>;
   using L = SxLds<TYPE, TT, RF, NW>;
   constexpr uint32_t NS = sx_slots<TYPE>();
+  constexpr uint32_t P = TT == 1 ? 16u : TT == 2 ? 8u : 4u;  // steps of x fragments loaded ahead
   constexpr uint32_t ROWS = L::ROWS, ND = L::ND;
   __shared__ __align__(16) uint8_t lds[L::BYTES];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, j = lane & 31u, h = lane >> 5;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t rows = wv.rows, nb = wv.bpr, r0 = blockIdx.x * ROWS, tg = blockIdx.y;
+  // KS = 2: workgroup pairs take the two halves of k and add into y
+  const uint32_t kh = blockIdx.x % (uint32_t)KS;
+  const uint32_t rows = wv.rows, nb = wv.bpr, r0 = blockIdx.x / (uint32_t)KS * ROWS, tg = blockIdx.y;
   const uint32_t rb = (uint32_t)wv.row_bytes;
   uint32_t *tab = (uint32_t *)lds;
   uint8_t *stage = lds + L::TAB + wave * L::SB;
@@ -318,7 +327,8 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
 #pragma unroll
       for (int v = 0; v < 8; ++v) acc[tt][f][v] = 0.f;
 
-  const uint32_t b0 = wave * nbw, b1 = min(b0 + nbw, nb);
+  const uint32_t bl = kh * nb / (uint32_t)KS, bh = (kh + 1u) * nb / (uint32_t)KS;
+  const uint32_t b0 = bl + wave * nbw, b1 = min(b0 + nbw, bh);
   for (uint32_t bi = b0; bi < b1; ++bi) {
     // this block of the tile's rows into the wave's stage
     const uint32_t bo = bi * W::BB;
@@ -333,13 +343,32 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
     auto xoff = [&](uint32_t tt, uint32_t s) {
       return (((tg * TT + tt) * nb + bi) * NS + s) * 1024u;
     };
-    u32x4 A[kSxP][TT];
+    // (each group of loads is followed by a compiler memory barrier, which
+    // keeps it where it is: the compiler otherwise moves loads down to their
+    // first use, and every step then waits a full round trip)
+    u32x4 A[P][TT];
 #pragma unroll
-    for (uint32_t s = 0; s < kSxP; ++s)
+    for (uint32_t s = 0; s < P; ++s)
 #pragma unroll
       for (uint32_t tt = 0; tt < (uint32_t)TT; ++tt)
         A[s][tt] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)(16u * lane), (int)xoff(tt, s), 0);
-    wait_vm<kSxP * TT>();
+    // the group sums and the tokens' block scales, for the fold (plain loads
+    // for the scales: a 16-byte buffer load whose elements are taken one by
+    // one as floats is narrowed to one dword by this compiler, every element
+    // then reading the first)
+    half8 am[TT];
+    float4 pa[TT], pb[TT];
+#pragma unroll
+    for (uint32_t tt = 0; tt < (uint32_t)TT; ++tt) {
+      am[tt] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+      if constexpr (W::MINS)
+        am[tt] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)(16u * lane), (int)xoff(tt, 16u), 0));
+      const float *pp = xp + ((tg * TT + tt) * nb + bi) * 16u + 4u * h;
+      pa[tt] = *(const float4 *)pp;
+      pb[tt] = *(const float4 *)(pp + 8);
+    }
+    __asm__ volatile("" ::: "memory");
+    wait_vm<P * TT + (W::MINS ? TT : 0) + 2 * TT>();
 
     W w[RF];
     const uint32_t *rp[RF];
@@ -356,14 +385,15 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
       half8 B[RF];
 #pragma unroll
       for (int f = 0; f < RF; ++f) B[f] = w[f].step(rp[f], (int)s, h, tab);
-      const u32x4 *As = A[s % kSxP];
+      const u32x4 *As = A[s % P];
       half8 a8[TT];
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) a8[tt] = __builtin_bit_cast(half8, As[tt]);
-      if (s + kSxP < 16u) {
+      if (s + P < 16u) {
 #pragma unroll
         for (uint32_t tt = 0; tt < (uint32_t)TT; ++tt)
-          A[s % kSxP][tt] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)(16u * lane), (int)xoff(tt, s + kSxP), 0);
+          A[s % P][tt] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)(16u * lane), (int)xoff(tt, s + P), 0);
+        __asm__ volatile("" ::: "memory");
       }
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt)
@@ -376,19 +406,11 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
     // minimum sums, scales of the tokens, and the fold of the block
 #pragma unroll
     for (uint32_t tt = 0; tt < (uint32_t)TT; ++tt) {
-      half8 am = {0, 0, 0, 0, 0, 0, 0, 0};
-      if constexpr (W::MINS)
-        am = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)(16u * lane), (int)xoff(tt, 16u), 0));
-      // (plain loads: a 16-byte buffer load whose elements are taken one by one
-      // as floats is narrowed to one dword by this compiler, every element then
-      // reading the first)
-      const float *pp = xp + ((tg * TT + tt) * nb + bi) * 16u + 4u * h;
-      const float4 pa = *(const float4 *)pp, pb = *(const float4 *)(pp + 8);
-      const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+      const float pv[8] = {pa[tt].x, pa[tt].y, pa[tt].z, pa[tt].w, pb[tt].x, pb[tt].y, pb[tt].z, pb[tt].w};
 #pragma unroll
       for (int f = 0; f < RF; ++f) {
         float16v Dm{};
-        if constexpr (W::MINS) Dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, w[f].mins(h), float16v{}, 0, 0, 0);
+        if constexpr (W::MINS) Dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[tt], w[f].mins(h), float16v{}, 0, 0, 0);
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
           float t = (D[tt][f][v] + D[tt][f][v + 8]) * w[f].d;
@@ -416,14 +438,20 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
     const uint32_t le = e & 63u, v = (e >> 6) & 7u, fr = e >> 9, f = fr % RF, tt = fr / RF;
     const uint32_t row = r0 + 32u * f + (le & 31u);
     const uint32_t tok = (tg * TT + tt) * 16u + 8u * (v >> 2) + 4u * (le >> 5) + (v & 3u);
-    if (row < rows && tok < tokens) y[(uint64_t)tok * rows + row] = sum;
+    if (row < rows && tok < tokens) {
+      if constexpr (KS == 1)
+        y[(uint64_t)tok * rows + row] = sum;
+      else  // 0 + a + b: the same bits in either order
+        unsafeAtomicAdd(y + (uint64_t)tok * rows + row, sum);
+    }
   }
 }
 
 // Token tiles of 16 per wave (tt) and token groups (grid y); the x scratch
 // covers groups * tt tiles (tokens past `tokens` are zero).
 struct SxPlan {
-  uint32_t tt, cfg, groups, row_tiles, nbw;  // cfg 0: RF 1 x 8 waves, 1: RF 2 x 4 waves
+  // cfg 0: 32 rows x 8 waves; 1: 64 rows x 4 waves; 2: 64 rows x 4 waves, k halves in two workgroups
+  uint32_t tt, cfg, groups, row_tiles, nbw;
 };
 
 void sx_tiles(uint32_t tokens, uint32_t &tt, uint32_t &groups) {
@@ -435,27 +463,33 @@ void sx_tiles(uint32_t tokens, uint32_t &tt, uint32_t &groups) {
 SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg) {
   SxPlan p;
   sx_tiles(tokens, p.tt, p.groups);
+  // measured: 32 rows x 8 waves up to 32 tokens per tile group, 64 rows x 4
+  // waves for 64 (the k halves in two workgroups were slower at every M)
   p.cfg = cfg ? (uint32_t)(cfg - 1) : (p.tt == 4u ? 1u : 0u);
-  const uint32_t rows_per = p.cfg ? 64u : 32u, nw = p.cfg ? 4u : 8u;
+  const uint32_t rows_per = p.cfg ? 64u : 32u, nw = p.cfg ? 4u : 8u, ks = p.cfg == 2u ? 2u : 1u;
   p.row_tiles = (wv.rows + rows_per - 1u) / rows_per;
-  p.nbw = (wv.bpr + nw - 1u) / nw;
+  p.nbw = ((wv.bpr + ks - 1u) / ks + nw - 1u) / nw;
   return p;
 }
 
-template <int TYPE, int TT, int RF, int NW>
+template <int TYPE, int TT, int RF, int NW, int KS>
 hipError_t sx_go(const WeightView &wv, const uint8_t *xa, const float *xp, float *y, uint32_t tokens,
                  const SxPlan &p, hipStream_t s) {
   const uint64_t tiles = (uint64_t)p.groups * p.tt;
   const uint32_t xa_bytes = (uint32_t)(tiles * wv.bpr * sx_slots<TYPE>() * 1024u);
-  hipLaunchKernelGGL((k_sx<TYPE, TT, RF, NW>), dim3(p.row_tiles, p.groups), dim3(NW * 64), 0, s, wv, xa, xp, y,
-                     tokens, p.nbw, xa_bytes);
+  hipLaunchKernelGGL((k_sx<TYPE, TT, RF, NW, KS>), dim3(p.row_tiles * KS, p.groups), dim3(NW * 64), 0, s, wv, xa,
+                     xp, y, tokens, p.nbw, xa_bytes);
   return hipGetLastError();
 }
 
 template <int TYPE, int TT>
 hipError_t sx_cfg(const WeightView &wv, const uint8_t *xa, const float *xp, float *y, uint32_t tokens,
                   const SxPlan &p, hipStream_t s) {
-  return p.cfg ? sx_go<TYPE, TT, 2, 4>(wv, xa, xp, y, tokens, p, s) : sx_go<TYPE, TT, 1, 8>(wv, xa, xp, y, tokens, p, s);
+  switch (p.cfg) {
+    case 0: return sx_go<TYPE, TT, 1, 8, 1>(wv, xa, xp, y, tokens, p, s);
+    case 1: return sx_go<TYPE, TT, 2, 4, 1>(wv, xa, xp, y, tokens, p, s);
+    default: return sx_go<TYPE, TT, 2, 4, 2>(wv, xa, xp, y, tokens, p, s);
+  }
 }
 
 template <int TYPE>
@@ -465,7 +499,8 @@ hipError_t sx_type(const WeightView &wv, const float *x, float *y, uint32_t toke
   const uint32_t tiles = p.groups * p.tt, nb = wv.bpr;
   uint8_t *xa = scratch;
   float *xp = (float *)(scratch + (uint64_t)tiles * nb * sx_slots<TYPE>() * 1024u);
-  hipLaunchKernelGGL((k_sx_prep<TYPE>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, wv.k, xa, xp);
+  const uint32_t yz = p.cfg == 2u ? tokens * wv.rows : 0u;
+  hipLaunchKernelGGL((k_sx_prep<TYPE>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, wv.k, xa, xp, y, yz);
   switch (p.tt) {
     case 1: return sx_cfg<TYPE, 1>(wv, xa, xp, y, tokens, p, s);
     case 2: return sx_cfg<TYPE, 2>(wv, xa, xp, y, tokens, p, s);

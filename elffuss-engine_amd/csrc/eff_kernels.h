@@ -63,7 +63,8 @@ hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, u
 // Split-x matrix-core product (eff_gemm_sx.hip): Q2_K, Q4_K, IQ2_XXS from 4
 // tokens, k % 256 == 0, f32-accurate. `scratch` holds sx_x_bytes(...) bytes
 // (x as fp16 hi/lo parts and the block scales). cfg: 0 automatic, 1: 32 rows x
-// 8 waves per workgroup, 2: 64 rows x 4 waves.
+// 8 waves per workgroup, 2: 64 rows x 4 waves, 3: as 2 with the two halves of k
+// in two workgroups.
 bool sx_applies(const WeightView &wv, uint32_t tokens);
 size_t sx_x_bytes(int type, uint32_t tokens, uint32_t k);
 hipError_t launch_sx(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *scratch, int cfg,

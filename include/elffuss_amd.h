@@ -52,8 +52,9 @@ extern "C" {
 #define EFF_OPT_GEMV_MAX_TOKENS  1  /* tokens <= this go to the GEMV kernels (default 8) */
 #define EFF_OPT_GEMM_MIN_TOKENS  2  /* tokens >= this go to the fp16 MFMA GEMM (default 64; __ELFFUSS_DRIFT_DESDE) */
 #define EFF_OPT_GEMV_KERNEL      3  /* 0: int8 matrix-core GEMV where it applies (default), 1: f32 vector GEMV */
-#define EFF_OPT_SPLIT_CONFIG     4  /* split-x product workgroups: 0 automatic (default), 1: 32 rows x 8 waves,
-                                       2: 64 rows x 4 waves (tuning; results are the same bits either way) */
+#define EFF_OPT_SPLIT_CONFIG     4  /* split-x product workgroups (tuning): 0 automatic (default), 1: 32 rows x
+                                       8 waves, 2: 64 rows x 4 waves, 3: 64 rows x 4 waves with k halves in two
+                                       workgroups added into y */
 
 /* ---- top-k output layout (kernels.topk.wgsl.js:40-60) ------------------- */
 #define EFF_TOPK_M_MAX     192   /* largest M = K' + |S| accepted (TOPK_M_MAX) */

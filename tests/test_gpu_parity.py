@@ -218,21 +218,30 @@ def test_split_x_vs_f64_oracle(ctx, eff, orc, tname, tokens):
 @pytest.mark.parametrize("tname", SPLIT_TYPES)
 @pytest.mark.parametrize("k", [256, 512, 8192])
 def test_split_x_k_and_configs(ctx, eff, orc, tname, k):
-    """One block per row, fewer blocks than waves, many blocks per wave; both
-    workgroup configurations (32 rows x 8 waves, 64 rows x 4 waves) meet the bar."""
+    """One block per row, fewer blocks than waves, many blocks per wave; every
+    workgroup configuration (32 rows x 8 waves, 64 rows x 4 waves, and the same
+    with the halves of k in two workgroups) meets the bar."""
     rows, tokens = 100, 20
     t, data, gguf, n = make_weights(eff, tname, rows, k, 400 + k)
     x = eff.fill_normal(4000 + k, 1.0, tokens * k)
     wb, xb = ctx.upload(data), ctx.upload(x)
     ref = orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens)
-    for cfg in (1, 2):
+    for cfg in (1, 2, 3):
         yb = ctx.alloc(tokens * rows * 4)
         ctx.set_option(eff.OPT_SPLIT_CONFIG, cfg)
         try:
             ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
         finally:
             ctx.set_option(eff.OPT_SPLIT_CONFIG, 0)
-        check_close(yb.read(np.float32), ref, f"split-x {tname} k={k} cfg={cfg}")
+        got = yb.read(np.uint32)
+        check_close(got.view(np.float32), ref, f"split-x {tname} k={k} cfg={cfg}")
+        if cfg == 3:    # two partial sums added into y: the same bits on every call
+            ctx.set_option(eff.OPT_SPLIT_CONFIG, cfg)
+            try:
+                ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+            finally:
+                ctx.set_option(eff.OPT_SPLIT_CONFIG, 0)
+            assert np.array_equal(yb.read(np.uint32), got)
         yb.free()
 
 
