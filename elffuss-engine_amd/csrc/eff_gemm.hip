@@ -13,8 +13,9 @@
 // direct-to-LDS loads (buffer_load ... lds), issued two steps ahead:
 //  * x: the fp16 x of the step (prepared by k_x_to_f16 as one contiguous run
 //    of 256 x 64 halves), 16-byte chunk c of token t stored at chunk
-//    c ^ (t & 7) of the token's 128-byte row, so that the 32 tokens of a
-//    fragment read one chunk column without bank conflicts;
+//    c ^ ((t >> 1) & 7) of the token's 128-byte row, so that the 16 lanes
+//    one LDS cycle serves (16 x 16 bytes over the 64 banks) read 16
+//    different bank quads when a fragment reads one chunk column;
 //  * W: the raw bytes of each row's two blocks (68 bytes, read as five
 //    16-byte chunks from the 4-byte aligned start), 80 bytes per row.
 // The MFMA waves decode their weight fragments from the raw bytes in
@@ -93,10 +94,13 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
   const uint32_t rb = (uint32_t)wv.row_bytes;
   const uint32_t rmax = rows - 1u - n0;  // last valid row of the tile (rows past it repeat it)
 
-  // Per-lane load offsets. x: load j of wave w fills chunk slots
-  // 64 (8 w + j) + lane = 8 t + p of the stage, token t, stored chunk p,
-  // holding x chunk c = p ^ (t & 7) (t & 7 = lane >> 3 here).
-  const uint32_t xl = (lane >> 3) * 128u + (((lane & 7u) ^ (lane >> 3)) << 4);
+  // Per-lane load offsets. x: load i of wave w fills the 1 KB slot
+  // kXDma w + i, i.e. tokens t = 8 slot + lane / 8, stored chunk p = lane % 8,
+  // holding x chunk c = p ^ ((t >> 1) & 7) = p ^ (4 (slot & 1) + lane / 16)
+  // (kXDma is even, so slot & 1 = i & 1).
+  static_assert(kXDma % 2 == 0, "x slot parity");
+  const uint32_t xl0 = (lane >> 3) * 128u + (((lane & 7u) ^ (lane >> 4)) << 4);
+  const uint32_t xl1 = (lane >> 3) * 128u + (((lane & 7u) ^ (4u + (lane >> 4))) << 4);
   // W: load j of wave w is load g = w + kNW j of the step (those with
   // g < kWG); its chunk q = 64 g + lane is chunk q % 5 of row q / 5.
   const uint32_t nwl = wave < kWG % kNW || kWG % kNW == 0 ? kWDma : kWDma - 1u;
@@ -114,7 +118,7 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
       if ((int)(i % 4u) != g) continue;
       if (i < kXDma) {
         const uint32_t slot = kXDma * wave + i;
-        dma16(xsrc, xs + 1024u * slot, xl + 1024u * slot, (s0 + s) * kXS);
+        dma16(xsrc, xs + 1024u * slot, ((i & 1u) ? xl1 : xl0) + 1024u * slot, (s0 + s) * kXS);
       } else {
         const uint32_t j = i - kXDma;
         if (j < nwl) dma16(src.q, ws + 1024u * (wave + kNW * j), wl[j], (s0 + s) * 68u);
@@ -135,12 +139,12 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
   };
 
   // Fragment geometry. A: token 128 wm + 32 fi + n, chunk (2 m + h) stored
-  // at ((2 m + h) ^ (n & 7)); B: row 128 wn + 32 fj + n.
+  // at ((2 m + h) ^ ((n >> 1) & 7)); B: row 128 wn + 32 fj + n.
   const uint32_t n = lane & 31u, h = lane >> 5;
   const uint32_t abase = (kFM * 32u * wm + n) * 128u;
   uint32_t acol[4];
 #pragma unroll
-  for (uint32_t m = 0; m < 4; ++m) acol[m] = ((4u * (m >> 1) + 2u * h + (m & 1u)) ^ (n & 7u)) << 4;
+  for (uint32_t m = 0; m < 4; ++m) acol[m] = ((4u * (m >> 1) + 2u * h + (m & 1u)) ^ ((n >> 1) & 7u)) << 4;
   const uint32_t brow = (kFN * 32u * wn + n) * kRB;
 
   float16v acc[kFM][kFN];
