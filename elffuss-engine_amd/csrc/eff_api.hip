@@ -357,6 +357,39 @@ int eff_qgemv(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32
   return rc;
 }
 
+int eff_qgemv_multi(eff_ctx *ctx, int type, int mode, uint32_t n, eff_buf *const *ws, eff_buf *x,
+                    eff_buf *const *ys, const uint32_t *rows, uint32_t k, uint32_t tokens) {
+  if (!ctx) return EFF_E_INVALID;
+  if (mode != EFF_GEMV_SECTIONS && mode != EFF_GEMV_SWIGLU)
+    return fail(ctx, EFF_E_INVALID, "gemv multi: unknown mode %d", mode);
+  if (!ws || !ys || !rows) return fail(ctx, EFF_E_INVALID, "gemv multi: null array");
+  // the reference's gateUp takes two matrices and secciones two to four; 1..3 tokens
+  if (n < 2 || n > 4 || (mode == EFF_GEMV_SWIGLU && n != 2) || tokens < 1 || tokens > 3 || ctx->gemv_kernel != 0) {
+    ++ctx->stats.not_applicable;
+    return EFF_NOT_APPLICABLE;
+  }
+  if (mode == EFF_GEMV_SWIGLU && rows[0] != rows[1])
+    return fail(ctx, EFF_E_SHAPE, "gemv gate+up: gate has %u rows and up %u", rows[0], rows[1]);
+  WeightView wvs[4];
+  float *yp[4] = {nullptr, nullptr, nullptr, nullptr};
+  for (uint32_t i = 0; i < n; ++i) {
+    eff_buf *yb = mode == EFF_GEMV_SWIGLU ? ys[0] : ys[i];
+    int rc = weight_view(ctx, type, ws[i], x, yb, rows[i], k, tokens, wvs[i], "gemv multi");
+    if (rc) return rc;
+    yp[i] = (float *)yb->ptr;
+  }
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  if (!gemv_mx_multi_applies(wvs[0], tokens, mode)) {
+    ++ctx->stats.not_applicable;
+    return EFF_NOT_APPLICABLE;
+  }
+  hipError_t e = launch_gemv_mx_multi(mode, n, wvs, (const float *)x->ptr, yp, tokens, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "gemv multi launch");
+  ++ctx->stats.fused;
+  return EFF_OK;
+}
+
 int eff_qgemm(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k, uint32_t tokens) {
   if (!ctx) return EFF_E_INVALID;
   if (tokens == 0 || (int64_t)tokens < ctx->gemm_min_tokens) {

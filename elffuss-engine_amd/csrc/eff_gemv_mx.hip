@@ -458,9 +458,27 @@ struct MxGeo {
   uint32_t tq, tr;  // row tiles = tq * grid + tr
 };
 
-template <int TYPE, int T, int NW>
+// Fused launches over up to 4 matrices of one type and k sharing x
+// (ops.gemv.js:166-215). F = 1, sections: the row tiles of matrix q are the
+// launch's tiles [tend[q-1], tend[q]), and each matrix writes its own y.
+// F = 2, gate + up: the S slices of a row quad are doubled, the waves of the
+// upper half reading matrix 1, and y[0] = silu(gate) * up
+// (kernels.gemv.wgsl.js:436, 517-518). A row's sums are formed exactly as in a
+// one-matrix launch with the same slices, so the outputs are the same bits.
+struct MxSec {
+  uint32_t n;        // matrices
+  uint32_t tend[4];  // sections: end tile of each matrix
+  uint32_t rows[4];
+  const uint8_t *w[4];
+  uint64_t w_bytes[4], scales_off[4];
+  float *y[4];
+};
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+template <int TYPE, int T, int NW, int F>
 __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float *__restrict__ x,
-                                                     float *__restrict__ y, MxGeo geo) {
+                                                     float *__restrict__ y, MxGeo geo, MxSec sec) {
   using TK = Task<TYPE>;
   using ST = Stage<TK::RB, TK::ALIGN>;
   using ST2 = Stage2<TYPE>;
@@ -481,16 +499,44 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
   const uint32_t rows = wv.rows, k = wv.k;
   const uint32_t S = 1u << geo.s_log2, G4 = (uint32_t)NW >> geo.s_log2;
   const uint32_t gq = wave >> geo.s_log2, sl = wave & (S - 1u), RPT = 4u * G4;
-  const BufSrc src = make_src(wv, 0);
+  // gate + up: SR slices per matrix, this wave's k slice and matrix
+  const uint32_t SR = F == 2 ? S >> 1 : S, ksl = sl & (SR - 1u), wmat = F == 2 ? sl / SR : 0u;
+  // the section of a tile (F = 1) and its first tile
+  auto sec_of = [&](uint32_t tile, uint32_t &first) {
+    uint32_t q = 0;
+    first = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 3u; ++i)
+      if (i + 1u < sec.n && tile >= sec.tend[i]) {
+        q = i + 1u;
+        first = sec.tend[i];
+      }
+    return q;
+  };
+  auto src_of = [&](uint32_t q) {
+    WeightView m = wv;
+    m.w = sec.w[q];
+    m.w_bytes = sec.w_bytes[q];
+    m.scales_off = sec.scales_off[q];
+    return make_src(m, 0);
+  };
+  BufSrc src = F == 2 ? src_of(wmat) : make_src(wv, 0);
   const uint32_t xbytes = (uint32_t)T * k * 3u + (uint32_t)T * (k / 8u) * 4u;
   uint8_t *const stg = xl + xbytes + wave * SBT;
   float *red = (float *)(xl + xbytes + (uint32_t)NW * SBT);
 
-  const uint32_t ntask = geo.ntask, t0 = sl * ntask, passes = geo.passes;
+  const uint32_t ntask = geo.ntask, t0 = ksl * ntask, passes = geo.passes;
   const uint32_t my_tiles = geo.tq + (blockIdx.x < geo.tr ? 1u : 0u), nitems = my_tiles * passes;
   // bytes of a row: GGUF blocks, or the quants of Q8_0R (its scales: 2 per block)
   const uint32_t rbytes = TYPE == Q8_0R ? 32u * wv.bpr : (uint32_t)wv.row_bytes, sbytes = 2u * wv.bpr;
-  auto row_of = [&](uint32_t tile, uint32_t r) { return min(tile * RPT + 4u * gq + r, rows - 1u); };
+  auto row_of = [&](uint32_t tile, uint32_t r) {
+    if constexpr (F == 1) {
+      uint32_t first;
+      const uint32_t q = sec_of(tile, first);
+      return min((tile - first) * RPT + 4u * gq + r, sec.rows[q] - 1u);
+    }
+    return min(tile * RPT + 4u * gq + r, rows - 1u);
+  };
 
   // This lane's chunks: chunk q = lane + 64j is chunk q % CPR of row q / CPR,
   // stored at byte 16q of the stage.
@@ -511,6 +557,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
   // the scalar offset of the load when the region start is 4-byte aligned).
   uint32_t vo[ST::LOADS], vo2 = 0;
   auto set_tile = [&](uint32_t tile) {
+    if constexpr (F == 1) {
+      uint32_t first;
+      src = src_of(sec_of(tile, first));
+    }
 #pragma unroll
     for (uint32_t j = 0; j < ST::LOADS; ++j) vo[j] = row_of(tile, s_r[j]) * rbytes + (TK::ALIGN >= 4u ? s_ch[j] : 0u);
     if constexpr (ST2::LOADS > 0) vo2 = row_of(tile, s2_r) * sbytes + s2_ch;
@@ -640,11 +690,21 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
   auto finish = [&](uint32_t tile) {
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = slot_sum(acc[t]);
+    // the tile's output: its matrix's y and rows, and the tile within the matrix
+    float *yo = y;
+    uint32_t ro = rows, lt = tile;
+    if constexpr (F == 1) {
+      uint32_t first;
+      const uint32_t q = sec_of(tile, first);
+      yo = sec.y[q];
+      ro = sec.rows[q];
+      lt = tile - first;
+    }
     if (S == 1) {
-      const uint32_t r = tile * RPT + 4u * gq + c;
-      if (b == 0u && r < rows) {
+      const uint32_t r = lt * RPT + 4u * gq + c;
+      if (b == 0u && r < ro) {
 #pragma unroll
-        for (int t = 0; t < T; ++t) y[(uint64_t)t * rows + r] = acc[t];
+        for (int t = 0; t < T; ++t) yo[(uint64_t)t * ro + r] = acc[t];
       }
     } else {
       if (b == 0u) {
@@ -654,10 +714,25 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mx(WeightView wv, const float 
       __syncthreads();
       if (tid < RPT * (uint32_t)T) {
         const uint32_t rq = tid / (4u * (uint32_t)T), rc = (tid / (uint32_t)T) % 4u, t = tid % (uint32_t)T;
-        float v = 0.f;
-        for (uint32_t q = 0; q < (uint32_t)S; ++q) v += red[((rq * (uint32_t)S + q) * 4u + rc) * (uint32_t)T + t];
-        const uint32_t r = tile * RPT + 4u * rq + rc;
-        if (r < rows) y[(uint64_t)t * rows + r] = v;
+        auto at = [&](uint32_t q) { return red[((rq * (uint32_t)S + q) * 4u + rc) * (uint32_t)T + t]; };
+        float v;
+        if constexpr (F == 2) {
+          // gate and up, each summed as a one-matrix launch of SR slices sums it
+          float g = 0.f, u = 0.f;
+          if (SR == 1u) {
+            g = at(0);
+            u = at(1);
+          } else {
+            for (uint32_t q = 0; q < SR; ++q) g += at(q);
+            for (uint32_t q = 0; q < SR; ++q) u += at(SR + q);
+          }
+          v = silu(g) * u;
+        } else {
+          v = 0.f;
+          for (uint32_t q = 0; q < (uint32_t)S; ++q) v += at(q);
+        }
+        const uint32_t r = lt * RPT + 4u * rq + rc;
+        if (r < ro) yo[(uint64_t)t * ro + r] = v;
       }
     }
 #pragma unroll
@@ -1113,11 +1188,11 @@ bool gemv_mx_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p) {
 
 // Workgroups resident at once on the current device for this kernel and LDS
 // size (persistent grids are sized to it).
-template <int TYPE, int T, int NW>
+template <int TYPE, int T, int NW, int F>
 static hipError_t mx_resident(size_t lds, uint32_t &out) {
   static bool attr = false;
   if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_mx<TYPE, T, NW>,
+    const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_mx<TYPE, T, NW, F>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMxMaxLds);
     if (e != hipSuccess) return e;
     attr = true;
@@ -1126,34 +1201,44 @@ static hipError_t mx_resident(size_t lds, uint32_t &out) {
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e == hipSuccess)
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_gemv_mx<TYPE, T, NW>, NW * 64, lds);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_gemv_mx<TYPE, T, NW, F>, NW * 64, lds);
   if (e != hipSuccess) return e;
   out = (uint32_t)(cus > 0 ? cus : 1) * (uint32_t)(per > 0 ? per : 1);
   return hipSuccess;
 }
 
-template <int TYPE, int T, int NW>
-static hipError_t mx_launch(const WeightView &wv, const float *x, float *y, const GemvPlan &p, hipStream_t s) {
+// p.ksplit slices per matrix; `sec` is unused for F = 0. Gate + up runs
+// 2 p.ksplit slices per row quad (one tile per workgroup).
+template <int TYPE, int T, int NW, int F>
+static hipError_t mx_launch(const WeightView &wv, const float *x, float *y, const GemvPlan &p, const MxSec &sec,
+                            hipStream_t s) {
+  const uint32_t slices = (uint32_t)p.ksplit * (F == 2 ? 2u : 1u);
   uint32_t grid = p.tiles;
-  if (p.ksplit == 1) {
+  if (slices == 1) {
     uint32_t res = 0;
-    const hipError_t e = mx_resident<TYPE, T, NW>(p.lds_bytes, res);
+    const hipError_t e = mx_resident<TYPE, T, NW, F>(p.lds_bytes, res);
     if (e != hipSuccess) return e;
     grid = grid < res ? grid : res;
+  } else if (F != 0) {
+    // (the attribute is set once per kernel, as the persistent launch does)
+    uint32_t res = 0;
+    const hipError_t e = mx_resident<TYPE, T, NW, F>(p.lds_bytes, res);
+    if (e != hipSuccess) return e;
   }
   MxGeo geo;
-  geo.s_log2 = (uint32_t)__builtin_ctz((unsigned)p.ksplit);
+  geo.s_log2 = (uint32_t)__builtin_ctz(slices);
   geo.ntask = wv.k / 64u / (uint32_t)p.ksplit;
   geo.passes = (geo.ntask + 15u) / 16u;
   geo.tq = p.tiles / grid;
   geo.tr = p.tiles % grid;
-  hipLaunchKernelGGL((k_gemv_mx<TYPE, T, NW>), dim3(grid), dim3(NW * 64), p.lds_bytes, s, wv, x, y, geo);
+  hipLaunchKernelGGL((k_gemv_mx<TYPE, T, NW, F>), dim3(grid), dim3(NW * 64), p.lds_bytes, s, wv, x, y, geo, sec);
   return hipGetLastError();
 }
 
 template <int TYPE, int T>
 static hipError_t mx_go(const WeightView &wv, const float *x, float *y, const GemvPlan &p, hipStream_t s) {
-  return p.waves == 8 ? mx_launch<TYPE, T, 8>(wv, x, y, p, s) : mx_launch<TYPE, T, 4>(wv, x, y, p, s);
+  const MxSec none{};
+  return p.waves == 8 ? mx_launch<TYPE, T, 8, 0>(wv, x, y, p, none, s) : mx_launch<TYPE, T, 4, 0>(wv, x, y, p, none, s);
 }
 
 template <int TYPE>
@@ -1276,6 +1361,80 @@ hipError_t launch_gemv_mt(const WeightView &wv, const float *x, float *y, uint32
     case Q6_K: return mt_t<Q6_K>(wv, x, y, tokens, p, s);
     case Q2_K: return mt_t<Q2_K>(wv, x, y, tokens, p, s);
     case IQ2_XXS: return mt_t<IQ2_XXS>(wv, x, y, tokens, p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Fused launches: the plan of matrix 0 (k slices and waves, so that every row
+// is summed as its one-matrix launch sums it); gate + up runs 8 waves.
+namespace {
+
+bool mx_multi_plan(const WeightView &wv0, uint32_t tokens, int mode, GemvPlan &p) {
+  if (tokens < 1 || tokens > 3 || !gemv_mx_plan(wv0, tokens, p)) return false;
+  if (mode == 2) {
+    p.waves = 8;
+    p.lds_bytes = mx_lds_bytes(wv0, tokens, 8);
+    if (p.lds_bytes > kMxMaxLds || 2 * p.ksplit > 8) return false;
+  }
+  return true;
+}
+
+template <int TYPE, int T, int F>
+hipError_t mx_multi_go(uint32_t n, const WeightView *wvs, const float *x, float *const *ys, const GemvPlan &p0,
+                       hipStream_t s) {
+  GemvPlan p = p0;
+  const uint32_t slices = (uint32_t)p.ksplit * (F == 2 ? 2u : 1u);
+  const uint32_t rpt = 4u * (uint32_t)p.waves / slices;
+  MxSec sec{};
+  sec.n = n;
+  uint32_t tiles = 0;
+  for (uint32_t q = 0; q < n; ++q) {
+    sec.rows[q] = wvs[q].rows;
+    sec.w[q] = wvs[q].w;
+    sec.w_bytes[q] = wvs[q].w_bytes;
+    sec.scales_off[q] = wvs[q].scales_off;
+    sec.y[q] = ys[q];
+    tiles += F == 1 || q == 0 ? (wvs[q].rows + rpt - 1u) / rpt : 0u;
+    sec.tend[q] = tiles;
+  }
+  p.tiles = tiles;
+  if (p.waves == 8) return mx_launch<TYPE, T, 8, F>(wvs[0], x, ys[0], p, sec, s);
+  if constexpr (F == 1) return mx_launch<TYPE, T, 4, F>(wvs[0], x, ys[0], p, sec, s);
+  return hipErrorInvalidValue;
+}
+
+template <int TYPE>
+hipError_t mx_multi_t(int mode, uint32_t n, const WeightView *wvs, const float *x, float *const *ys, uint32_t tokens,
+                      const GemvPlan &p, hipStream_t s) {
+  switch (tokens * 4u + (uint32_t)mode) {
+    case 1 * 4 + 1: return mx_multi_go<TYPE, 1, 1>(n, wvs, x, ys, p, s);
+    case 2 * 4 + 1: return mx_multi_go<TYPE, 2, 1>(n, wvs, x, ys, p, s);
+    case 3 * 4 + 1: return mx_multi_go<TYPE, 3, 1>(n, wvs, x, ys, p, s);
+    case 1 * 4 + 2: return mx_multi_go<TYPE, 1, 2>(n, wvs, x, ys, p, s);
+    case 2 * 4 + 2: return mx_multi_go<TYPE, 2, 2>(n, wvs, x, ys, p, s);
+    case 3 * 4 + 2: return mx_multi_go<TYPE, 3, 2>(n, wvs, x, ys, p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool gemv_mx_multi_applies(const WeightView &wv0, uint32_t tokens, int mode) {
+  GemvPlan p;
+  return mx_multi_plan(wv0, tokens, mode, p);
+}
+
+hipError_t launch_gemv_mx_multi(int mode, uint32_t n, const WeightView *wvs, const float *x, float *const *ys,
+                                uint32_t tokens, hipStream_t s) {
+  GemvPlan p;
+  if (n < 1 || n > 4 || !mx_multi_plan(wvs[0], tokens, mode, p)) return hipErrorInvalidValue;
+  switch (wvs[0].type) {
+    case Q8_0: return mx_multi_t<Q8_0>(mode, n, wvs, x, ys, tokens, p, s);
+    case Q8_0R: return mx_multi_t<Q8_0R>(mode, n, wvs, x, ys, tokens, p, s);
+    case Q4_K: return mx_multi_t<Q4_K>(mode, n, wvs, x, ys, tokens, p, s);
+    case Q6_K: return mx_multi_t<Q6_K>(mode, n, wvs, x, ys, tokens, p, s);
+    case Q2_K: return mx_multi_t<Q2_K>(mode, n, wvs, x, ys, tokens, p, s);
+    case IQ2_XXS: return mx_multi_t<IQ2_XXS>(mode, n, wvs, x, ys, tokens, p, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -42,6 +42,13 @@ bool gemv_mx_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p);
 void gemv_mx_override(int waves, int ksplit);
 hipError_t launch_gemv_mx(const WeightView &wv, const float *x, float *y, uint32_t tokens,
                           const GemvPlan &p, hipStream_t stream);
+// Fused matrix-core GEMV over n (1..4) matrices of one type and k that share
+// x, for 1..3 tokens: mode 1 sections (ys[i] = W_i x), mode 2 gate + up
+// (n = 2, equal rows, ys[0] = silu(W_0 x) * (W_1 x)). Each row is summed as
+// its one-matrix launch sums it when the plans agree (always for gate + up).
+bool gemv_mx_multi_applies(const WeightView &wv0, uint32_t tokens, int mode);
+hipError_t launch_gemv_mx_multi(int mode, uint32_t n, const WeightView *wvs, const float *x, float *const *ys,
+                                uint32_t tokens, hipStream_t stream);
 // Multi-token matrix-core GEMV (16 rows x 4 tokens per MFMA): 4..16 tokens
 // per launch, Q8_0/Q4_K/Q6_K/Q2_K/IQ2_XXS, k % 256 == 0.
 bool gemv_mt_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p);

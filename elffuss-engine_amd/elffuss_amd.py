@@ -21,6 +21,7 @@ E_INVALID, E_TYPE, E_SHAPE, E_MARK, E_BOUNDS, E_DEVICE, E_NOMEM = -1, -2, -3, -4
 Q8_0, Q2_K, Q4_K, Q6_K, IQ2_XXS, Q8_0R = 8, 10, 12, 14, 16, 264
 TYPES = {"Q8_0": Q8_0, "Q2_K": Q2_K, "Q4_K": Q4_K, "Q6_K": Q6_K, "IQ2_XXS": IQ2_XXS, "Q8_0R": Q8_0R}
 OPT_GEMV_MAX_TOKENS, OPT_GEMM_MIN_TOKENS, OPT_GEMV_KERNEL, OPT_SPLIT_CONFIG = 1, 2, 3, 4
+GEMV_SECTIONS, GEMV_SWIGLU = 1, 2
 TOPK_HEADER, TOPK_P_MAX, TOPK_CAP, TOPK_M_MAX = 8, 128, 256, 192
 
 ERRORS = {E_INVALID: "invalid argument", E_TYPE: "unsupported type", E_SHAPE: "shape",
@@ -40,7 +41,7 @@ class NotApplicable(Exception):
 class Stats(ctypes.Structure):
     _fields_ = [("gemv", ctypes.c_uint64), ("gemm", ctypes.c_uint64), ("skinny", ctypes.c_uint64),
                 ("dequant", ctypes.c_uint64), ("topk", ctypes.c_uint64), ("not_applicable", ctypes.c_uint64),
-                ("split", ctypes.c_uint64)]
+                ("split", ctypes.c_uint64), ("fused", ctypes.c_uint64)]
 
 
 _lib = None
@@ -89,6 +90,8 @@ def lib():
         "eff_qmatmul": ([p, i32, p, p, p, u32, u32, u32], i32),
         "eff_qgemv": ([p, i32, p, p, p, u32, u32, u32], i32),
         "eff_qgemm": ([p, i32, p, p, p, u32, u32, u32], i32),
+        "eff_qgemv_multi": ([p, i32, i32, u32, ctypes.POINTER(p), p, ctypes.POINTER(p), ctypes.POINTER(u32), u32, u32],
+                            i32),
         "eff_dequant": ([p, i32, p, p, u32], i32),
         "eff_topk": ([p, p, u32, u32, u32, p, u32, u32, p], i32),
         "eff_topk_out_bytes": ([], sz),
@@ -106,7 +109,7 @@ EXPORTED = ("eff_type_from_name eff_type_name eff_type_geometry eff_init eff_shu
             "eff_buf_free eff_buf_size eff_buf_device_ptr eff_buf_write eff_buf_read eff_buf_copy "
             "eff_bytes_reordered eff_bytes_buffer_r eff_blocks_from_buffer eff_scales_from eff_buf_mark_r "
             "eff_buf_blocks_r eff_repack eff_unrepack eff_quantize eff_fill_normal eff_qmatmul eff_qgemv "
-            "eff_qgemm eff_dequant eff_topk eff_topk_out_bytes").split()
+            "eff_qgemm eff_qgemv_multi eff_dequant eff_topk eff_topk_out_bytes").split()
 
 
 def type_code(t):
@@ -281,6 +284,14 @@ class Context:
 
     def qgemv(self, t, w, x, y, rows, k, tokens=1):
         self._check(lib().eff_qgemv(self.h, type_code(t), w.handle, x.handle, y.handle, rows, k, tokens))
+
+    def qgemv_multi(self, t, mode, ws, x, ys, rows, k, tokens=1):
+        """Fused GEMV (mode GEMV_SECTIONS or GEMV_SWIGLU) over the buffers ws, into ys."""
+        n = len(ws)
+        wa = (ctypes.c_void_p * n)(*[w.handle for w in ws])
+        ya = (ctypes.c_void_p * len(ys))(*[y.handle for y in ys])
+        ra = (ctypes.c_uint32 * n)(*rows)
+        self._check(lib().eff_qgemv_multi(self.h, type_code(t), mode, n, wa, x.handle, ya, ra, k, tokens))
 
     def qgemm(self, t, w, x, y, rows, k, tokens):
         self._check(lib().eff_qgemm(self.h, type_code(t), w.handle, x.handle, y.handle, rows, k, tokens))

@@ -270,6 +270,7 @@ napi_value Stats(napi_env env, napi_callback_info info) {
   napi_set_named_property(env, o, "topk", make_int(env, (int64_t)s.topk));
   napi_set_named_property(env, o, "notApplicable", make_int(env, (int64_t)s.not_applicable));
   napi_set_named_property(env, o, "split", make_int(env, (int64_t)s.split));
+  napi_set_named_property(env, o, "fused", make_int(env, (int64_t)s.fused));
   return o;
 }
 
@@ -407,6 +408,34 @@ napi_value QMatmul(napi_env env, napi_callback_info info) { return MatCall(env, 
 napi_value QGemv(napi_env env, napi_callback_info info) { return MatCall(env, info, eff_qgemv); }
 napi_value QGemm(napi_env env, napi_callback_info info) { return MatCall(env, info, eff_qgemm); }
 
+// qgemvMulti(ctx, type, mode, [w...], x, [y...], [rows...], k, tokens)
+napi_value QGemvMulti(napi_env env, napi_callback_info info) {
+  napi_value a[9];
+  get_args(env, info, 9, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  eff_buf *ws[4] = {nullptr, nullptr, nullptr, nullptr}, *ys[4] = {nullptr, nullptr, nullptr, nullptr};
+  uint32_t rows[4] = {0, 0, 0, 0}, nw = 0, ny = 0, nr = 0;
+  napi_get_array_length(env, a[3], &nw);
+  napi_get_array_length(env, a[5], &ny);
+  napi_get_array_length(env, a[6], &nr);
+  if (nw > 4 || ny > 4 || nr != nw) return throw_msg(env, "gemv multi: 1..4 weights, as many row counts, at most 4 outputs");
+  for (uint32_t i = 0; i < nw; ++i) {
+    napi_value v;
+    napi_get_element(env, a[3], i, &v);
+    ws[i] = external<eff_buf>(env, v);
+    napi_get_element(env, a[6], i, &v);
+    rows[i] = (uint32_t)i64(env, v);
+  }
+  for (uint32_t i = 0; i < ny; ++i) {
+    napi_value v;
+    napi_get_element(env, a[5], i, &v);
+    ys[i] = external<eff_buf>(env, v);
+  }
+  return status(env, ctx, eff_qgemv_multi(ctx, (int)i64(env, a[1]), (int)i64(env, a[2]), nw, ws,
+                                          external<eff_buf>(env, a[4]), ys, rows, (uint32_t)i64(env, a[7]),
+                                          (uint32_t)i64(env, a[8], 1)));
+}
+
 napi_value Dequant(napi_env env, napi_callback_info info) {
   napi_value a[5];
   get_args(env, info, 5, a);
@@ -440,7 +469,7 @@ napi_value Register(napi_env env, napi_value exports) {
       {"init", Init}, {"shutdown", Shutdown}, {"sync", Sync}, {"setOption", SetOption}, {"stats", Stats},
       {"bufAlloc", BufAlloc}, {"bufFree", BufFree}, {"bufWrite", BufWrite}, {"bufRead", BufRead},
       {"bufReadAsync", BufReadAsync}, {"bufSize", BufSize}, {"bufMarkR", BufMarkR}, {"bufBlocksR", BufBlocksR},
-      {"qmatmul", QMatmul}, {"qgemv", QGemv}, {"qgemm", QGemm}, {"dequant", Dequant}, {"topk", TopK},
+      {"qmatmul", QMatmul}, {"qgemv", QGemv}, {"qgemvMulti", QGemvMulti}, {"qgemm", QGemm}, {"dequant", Dequant}, {"topk", TopK},
       {"topkOutBytes", TopKOutBytes},
   };
   for (auto &f : fns) {

@@ -21,7 +21,8 @@ const path = require('path');
 const native = require(path.join(__dirname, 'elffuss_amd.node'));
 
 const STATUS = { NOT_APPLICABLE: 1, E_INVALID: -1, E_TYPE: -2, E_SHAPE: -3, E_MARK: -4, E_BOUNDS: -5, E_DEVICE: -6 };
-const OPT = { GEMV_MAX_TOKENS: 1, GEMM_MIN_TOKENS: 2, GEMV_KERNEL: 3 };
+const OPT = { GEMV_MAX_TOKENS: 1, GEMM_MIN_TOKENS: 2, GEMV_KERNEL: 3, SPLIT_CONFIG: 4 };
+const GEMV_MODE = { SECTIONS: 1, SWIGLU: 2 };
 const TOPK = { M_MAX: 192, P_MAX: 128, CAP: 256, CABECERA: 8, N_MAX: 1 << 24, POR_TROZO: 4096 };
 
 // ---- types (gguf.js:51-64, kernels.wgsl.js QUANT_TYPES) --------------------
@@ -204,7 +205,7 @@ function creaBufferR(device, t, tipoR) {
 // createGemvOps (ops.gemv.js:44-221): the decode GEMV, null when it does not apply.
 function createGemvOps(device, deps) {
   const ctx = deps.ctx;
-  const hechos = { matmul: 0 };
+  const hechos = { matmul: 0, gateUp: 0, secciones: 0 };
   return {
     matmul(tipo, wBuf, xBuf, rows, k, tokens) {
       const t = tokens === undefined ? 1 : tokens;
@@ -215,6 +216,32 @@ function createGemvOps(device, deps) {
       if (r === null) return Promise.resolve(null);
       hechos.matmul++;
       return Promise.resolve(y);
+    },
+    // silu(W_gate·x)·(W_up·x) in one launch (ops.gemv.js:166-190).
+    gateUp(tipo, wGate, wUp, xBuf, rows, k, tokens) {
+      const t = tokens === undefined ? 1 : tokens;
+      const i = QUANT_TYPES[tipo];
+      if (!i || !(t >= 1) || k % i.blockElems !== 0) return Promise.resolve(null);
+      const y = ctx.alloc(rows * t * 4, 'swiglu.out');
+      const r = native.qgemvMulti(device._ctx, i.code, GEMV_MODE.SWIGLU, [wGate._h, wUp._h], xBuf._h, [y._h],
+        [rows, rows], k, t);
+      if (r === null) return Promise.resolve(null);
+      hechos.gateUp++;
+      return Promise.resolve(y);
+    },
+    // 2 to 4 matrices sharing x, each with its rows and its output, in one
+    // launch; the outputs in the order of the weights (ops.gemv.js:192-215).
+    secciones(tipo, ws, xBuf, filas, k, tokens) {
+      const t = tokens === undefined ? 1 : tokens;
+      const i = QUANT_TYPES[tipo];
+      const n = ws.length;
+      if (!i || n < 2 || n > 4 || filas.length !== n || !(t >= 1) || k % i.blockElems !== 0) return Promise.resolve(null);
+      const ys = filas.map((f) => ctx.alloc(f * t * 4, 'matmul.y'));
+      const r = native.qgemvMulti(device._ctx, i.code, GEMV_MODE.SECTIONS, ws.map((w) => w._h), xBuf._h,
+        ys.map((y) => y._h), filas, k, t);
+      if (r === null) return Promise.resolve(null);
+      hechos.secciones++;
+      return Promise.resolve(ys);
     },
     despachados() { return Object.assign({}, hechos); },
     rechazados() { return []; },
@@ -339,7 +366,7 @@ function createTopKGPU(device, ctx) {
 }
 
 module.exports = {
-  native, STATUS, OPT, TOPK, QUANT_TYPES, quantInfo,
+  native, STATUS, OPT, GEMV_MODE, TOPK, QUANT_TYPES, quantInfo,
   requestDevice, readback, createContext,
   createQuantOps, createGemvOps, createGemm2Ops, createTopKGPU, estadisticasTopK,
   TIPOS_R, TIPO_R, TIPO_GGUF, bytesReordenado, bytesBufferR, bloquesDeBuffer, escalasDesde,

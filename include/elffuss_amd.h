@@ -56,6 +56,10 @@ extern "C" {
                                        8 waves, 2: 64 rows x 4 waves, 3: 64 rows x 4 waves with k halves in two
                                        workgroups added into y */
 
+/* ---- fused GEMV modes (gemv2Shader `modo`, kernels.gemv.wgsl.js:370-375) -- */
+#define EFF_GEMV_SECTIONS  1  /* 'secciones': ys[i] = W_i x for 2..4 matrices */
+#define EFF_GEMV_SWIGLU    2  /* 'swiglu': ys[0] = silu(W_gate x) * (W_up x) */
+
 /* ---- top-k output layout (kernels.topk.wgsl.js:40-60) ------------------- */
 #define EFF_TOPK_M_MAX     192   /* largest M = K' + |S| accepted (TOPK_M_MAX) */
 #define EFF_TOPK_P_MAX     128   /* penalised ids (TOPK_P_MAX) */
@@ -76,6 +80,7 @@ typedef struct eff_stats {
   uint64_t topk;        /* top-k launches (chunk + final pair) */
   uint64_t not_applicable;  /* calls answered EFF_NOT_APPLICABLE */
   uint64_t split;       /* split-x matrix-core launches (Q2_K, Q4_K, IQ2_XXS from 4 tokens) */
+  uint64_t fused;       /* fused GEMV launches (eff_qgemv_multi) */
 } eff_stats;
 
 /* ---- types and geometry -------------------------------------------------- */
@@ -205,6 +210,18 @@ int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
  * accumulation, 1..GEMV max tokens. EFF_NOT_APPLICABLE outside that range. */
 int eff_qgemv(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
               uint32_t rows, uint32_t k, uint32_t tokens);
+
+/* Fused decode GEMV over matrices of one type and k that share x, 1..3
+ * tokens, one launch with x prepared once. Replaces quant.gemv.secciones
+ * (ops.gemv.js:192-215; mode EFF_GEMV_SECTIONS, n = 2..4, ys[i] = W_i x with
+ * rows[i] rows) and quant.gemv.gateUp (ops.gemv.js:166-190; mode
+ * EFF_GEMV_SWIGLU, n = 2, rows[0] == rows[1], ys[0] = silu(W_0 x) * (W_1 x),
+ * silu(v) = v / (1 + exp(-v))). Every output equals the one-matrix GEMV's
+ * bits when the planner gives both the same k split (always for gate + up).
+ * EFF_NOT_APPLICABLE (the reference's null) for other n or tokens, or when the
+ * f32 vector GEMV is selected; EFF_E_SHAPE for gate and up of unequal rows. */
+int eff_qgemv_multi(eff_ctx *ctx, int type, int mode, uint32_t n, eff_buf *const *ws, eff_buf *x,
+                    eff_buf *const *ys, const uint32_t *rows, uint32_t k, uint32_t tokens);
 
 /* The prefill GEMM alone (quant.gemm2.matmul, ops.gemm2.js:266-280): x and
  * the dequantized weights rounded to fp16, MFMA with fp32 accumulation.

@@ -31,6 +31,15 @@ async function main() {
     const xBuf = ops.upload(x, 'x');
     const y = await ops.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens);
     out[c.name] = Array.from(await rd(y, c.rows * c.tokens));
+    if (c.tokens <= 3) {
+      // the fused forms over the same matrix twice: silu(y) * y, and [y, y]
+      const ysw = await ops.gemv.gateUp(c.type, wBuf, wBuf, xBuf, c.rows, c.k, c.tokens);
+      out[c.name + ':gateup'] = Array.from(await rd(ysw, c.rows * c.tokens));
+      const ys = await ops.gemv.secciones(c.type, [wBuf, wBuf], xBuf, [c.rows, c.rows], c.k, c.tokens);
+      out[c.name + ':sec0'] = Array.from(await rd(ys[0], c.rows * c.tokens));
+      out[c.name + ':sec1'] = Array.from(await rd(ys[1], c.rows * c.tokens));
+      assert.strictEqual(await ops.gemv.secciones(c.type, [wBuf], xBuf, [c.rows], c.k, c.tokens), null);
+    }
     if (c.tokens <= 8) {
       const yg = await ops.gemv.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens);
       out[c.name + ':gemv'] = Array.from(await rd(yg, c.rows * c.tokens));

@@ -48,6 +48,12 @@ def test_js_shim_gpu(eff, orc, tmp_path):
         check_close(np.array(out[name], np.float32), ref, f"js matmul {name}")
         if tokens <= 8:
             check_close(np.array(out[name + ":gemv"], np.float32), ref, f"js gemv {name}")
+        if tokens <= 3:
+            yg = np.array(out[name + ":gemv"], np.float32)
+            assert np.array_equal(np.array(out[name + ":sec0"], np.float32).view(np.uint32), yg.view(np.uint32))
+            assert np.array_equal(np.array(out[name + ":sec1"], np.float32).view(np.uint32), yg.view(np.uint32))
+            want = (yg / (np.float32(1) + np.exp(-yg))) * yg
+            assert np.allclose(np.array(out[name + ":gateup"], np.float32), want, rtol=4e-6, atol=0)
         if tokens >= 64:
             check_close(np.array(out[name + ":gemm2"], np.float32), orc.gemm_f16(ot, w, rows, k, x, tokens),
                         f"js gemm2 {name}")

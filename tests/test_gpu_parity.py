@@ -191,6 +191,112 @@ def test_gemm_q8_0_k_not_multiple_of_step(ctx, eff, orc):
     check_close(yb.read(np.float32), orc.gemm_f16(orc.Q8_0, gguf, rows, k, x, tokens), "gemm Q8_0 k=96")
 
 
+# ---- fused decode GEMV (gemv.gateUp, gemv.secciones) -----------------------------------
+
+def silu64(v):
+    v = np.asarray(v, np.float64)
+    return v / (1.0 + np.exp(-v))
+
+
+@pytest.mark.parametrize("tname", TYPES)
+@pytest.mark.parametrize("tokens", [1, 2, 3])
+def test_fused_gate_up(ctx, eff, orc, tname, tokens):
+    """silu(W_gate x) * (W_up x) in one launch: against the f64 oracle, and
+    against silu applied to the two one-matrix GEMVs' outputs (the same sums)."""
+    rows, k = 300, 2048
+    tg, dg, gg, n = make_weights(eff, tname, rows, k, 60 + tokens)
+    _, du, gu, _ = make_weights(eff, tname, rows, k, 61 + tokens)
+    x = eff.fill_normal(62 + tokens, 1.0, tokens * k)
+    wg, wu, xb = upload_w(ctx, eff, tname, dg, n), upload_w(ctx, eff, tname, du, n), ctx.upload(x)
+    y, yg, yu = (ctx.alloc(tokens * rows * 4) for _ in range(3))
+    before = ctx.stats()["fused"]
+    t = tg
+    ctx.qgemv_multi(t, eff.GEMV_SWIGLU, [wg, wu], xb, [y], [rows, rows], k, tokens)
+    assert ctx.stats()["fused"] == before + 1
+    ctx.qgemv(t, wg, xb, yg, rows, k, tokens)
+    ctx.qgemv(t, wu, xb, yu, rows, k, tokens)
+    got = y.read(np.float32)
+    g32, u32 = yg.read(np.float32), yu.read(np.float32)
+    want = (g32 / (np.float32(1) + np.exp(-g32))) * u32
+    assert np.allclose(got, want, rtol=4e-6, atol=0), f"max rel {np.max(np.abs(got - want) / np.abs(want)):.2e}"
+    ot = oracle_type(orc, tname)
+    ref = silu64(orc.gemv_f64(ot, gg, rows, k, x, tokens)) * orc.gemv_f64(ot, gu, rows, k, x, tokens)
+    check_close(got, ref, f"gate+up {tname} T={tokens}")
+    for b in (wg, wu, xb, y, yg, yu):
+        b.free()
+
+
+@pytest.mark.parametrize("tname", TYPES)
+@pytest.mark.parametrize("n", [2, 3, 4])
+def test_fused_sections_same_bits(ctx, eff, orc, tname, n):
+    """2-4 matrices of one shape sharing x: each output is bit-identical to the
+    one-matrix GEMV of that matrix."""
+    rows, k, tokens = 130, 1024, 2
+    ws, ggufs = [], []
+    for i in range(n):
+        t, d, g, nb = make_weights(eff, tname, rows, k, 70 + i)
+        ws.append(upload_w(ctx, eff, tname, d, nb))
+        ggufs.append(g)
+    x = eff.fill_normal(75, 1.0, tokens * k)
+    xb = ctx.upload(x)
+    ys = [ctx.alloc(tokens * rows * 4) for _ in range(n)]
+    ctx.qgemv_multi(t, eff.GEMV_SECTIONS, ws, xb, ys, [rows] * n, k, tokens)
+    for i in range(n):
+        y1 = ctx.alloc(tokens * rows * 4)
+        ctx.qgemv(t, ws[i], xb, y1, rows, k, tokens)
+        assert np.array_equal(ys[i].read(np.uint32), y1.read(np.uint32)), f"section {i}"
+        check_close(ys[i].read(np.float32), orc.gemv_f64(oracle_type(orc, tname), ggufs[i], rows, k, x, tokens),
+                    f"sections {tname} {i}/{n}")
+        y1.free()
+
+
+@pytest.mark.parametrize("tname", ["Q8_0", "Q4_K", "Q6_K", "IQ2_XXS"])
+def test_fused_sections_mixed_rows(ctx, eff, orc, tname):
+    """Q, K, V and gate-like sections of different rows (2048 + 512 + 512 + 77):
+    every output meets the f64 bar, and the launch count is one."""
+    k, tokens, rows = 2048, 1, [2048, 512, 512, 77]
+    ws, ggufs = [], []
+    for i, r in enumerate(rows):
+        t, d, g, nb = make_weights(eff, tname, r, k, 80 + i)
+        ws.append(upload_w(ctx, eff, tname, d, nb))
+        ggufs.append(g)
+    x = eff.fill_normal(85, 1.0, tokens * k)
+    xb = ctx.upload(x)
+    ys = [ctx.alloc(tokens * r * 4) for r in rows]
+    before = ctx.stats()
+    ctx.qgemv_multi(t, eff.GEMV_SECTIONS, ws, xb, ys, rows, k, tokens)
+    after = ctx.stats()
+    assert after["fused"] == before["fused"] + 1 and after["gemv"] == before["gemv"]
+    for i, r in enumerate(rows):
+        check_close(ys[i].read(np.float32), orc.gemv_f64(oracle_type(orc, tname), ggufs[i], r, k, x, tokens),
+                    f"sections {tname} rows={r}")
+
+
+def test_fused_not_applicable_and_errors(ctx, eff):
+    rows, k = 64, 512
+    t, d, g, nb = make_weights(eff, "Q4_K", rows, k, 90)
+    w, w2 = ctx.upload(d), ctx.upload(d)
+    xb, y = ctx.alloc(4 * k * 4), ctx.alloc(4 * rows * 4)
+    with pytest.raises(eff.NotApplicable):      # one matrix
+        ctx.qgemv_multi(t, eff.GEMV_SECTIONS, [w], xb, [y], [rows], k, 1)
+    with pytest.raises(eff.NotApplicable):      # four tokens
+        ctx.qgemv_multi(t, eff.GEMV_SECTIONS, [w, w2], xb, [y, y], [rows, rows], k, 4)
+    with pytest.raises(eff.NotApplicable):      # gate + up takes two matrices
+        ctx.qgemv_multi(t, eff.GEMV_SWIGLU, [w, w2, w], xb, [y], [rows, rows, rows], k, 1)
+    ctx.set_option(eff.OPT_GEMV_KERNEL, 1)
+    try:
+        with pytest.raises(eff.NotApplicable):  # the f32 vector GEMV has no fused form
+            ctx.qgemv_multi(t, eff.GEMV_SWIGLU, [w, w2], xb, [y], [rows, rows], k, 1)
+    finally:
+        ctx.set_option(eff.OPT_GEMV_KERNEL, 0)
+    with pytest.raises(eff.EffError) as e:
+        ctx.qgemv_multi(t, eff.GEMV_SWIGLU, [w, w2], xb, [y], [rows, rows // 2], k, 1)
+    assert e.value.code == eff.E_SHAPE
+    with pytest.raises(eff.EffError) as e:
+        ctx.qgemv_multi(t, eff.GEMV_SECTIONS, [w, w2], xb, [y, y], [rows, rows], 300, 1)
+    assert e.value.code == eff.E_SHAPE
+
+
 # ---- split-x product (Q2_K, Q4_K, IQ2_XXS from 4 tokens) -----------------------------
 
 SPLIT_TYPES = ["Q2_K", "Q4_K", "IQ2_XXS"]
