@@ -77,6 +77,41 @@ class Config:
             b.free()
 
 
+class FusedConfig:
+    """Several matrices of one type sharing x, 1 token: the fused GEMV
+    (gemv.gateUp / gemv.secciones) as one step, or the one-matrix GEMVs."""
+
+    def __init__(self, eff, ctx, tname, rows_list, k, mode, seed, fused=True):
+        self.eff, self.tname, self.rows, self.k, self.mode, self.fused = eff, tname, rows_list, k, mode, fused
+        self.t = eff.TYPES[tname]
+        self.sets = []
+        data = [eff.quantize(tname, eff.fill_normal(seed + i, 0.02, r * k)) for i, r in enumerate(rows_list)]
+        per = sum(d.nbytes for d in data)
+        self.copies = max(2, min(256, ROTATE_BYTES // per + 1))
+        for _ in range(self.copies):
+            self.sets.append([ctx.upload(d) for d in data])
+        self.x = ctx.upload(eff.fill_normal(seed + 9, 1.0, k))
+        nout = 1 if mode == eff.GEMV_SWIGLU else len(rows_list)
+        self.ys = [ctx.alloc(rows_list[i] * 4) for i in range(nout)]
+        self.yt = [ctx.alloc(r * 4) for r in rows_list]   # outputs of the one-matrix GEMVs
+        ctx.sync()
+        self.bytes = per + 4 * k + 4 * sum(rows_list[:nout])
+        self.flops = 2.0 * k * sum(rows_list)
+        self.gemm = False
+
+    def step(self, ctx, i):
+        ws = self.sets[i % self.copies]
+        if self.fused:
+            ctx.qgemv_multi(self.t, self.mode, ws, self.x, self.ys, self.rows, self.k, 1)
+        else:
+            for w, y, r in zip(ws, self.yt, self.rows):
+                ctx.qgemv(self.t, w, self.x, y, r, self.k, 1)
+
+    def free(self):
+        for b in [b for st in self.sets for b in st] + [self.x] + self.ys + self.yt:
+            b.free()
+
+
 def time_steps(torch, ctx, cfg, steps, warmup):
     """Average ms per step over `steps` graph-replayed steps (after `warmup`)."""
     stream = torch.cuda.current_stream()
@@ -219,6 +254,27 @@ def main():
                           "roofline_frac": round((mfma_t if bound == "mfma" else hbm_t) / (t_ms * 1e-3), 4),
                           "path": path}
             cfg.free()
+            print(f"# {key}: {sweep[key]}", file=sys.stderr, flush=True)
+
+    # F1: the fused decode GEMV against the one-matrix GEMVs it replaces
+    if not args.no_sweep:
+        fplan = [("F1 gate+up", "Q4_K", [8192, 8192], 2048, eff.GEMV_SWIGLU),
+                 ("F1 sections q+k+v", "Q4_K", [2048, 512, 512], 2048, eff.GEMV_SECTIONS)]
+        for tag, tn, rl, k, mode in fplan:
+            key = f"{tag} {tn} rows={'+'.join(map(str, rl))} K={k} M=1"
+            if args.only and args.only not in key:
+                continue
+            res = {}
+            for fused in (True, False):
+                cfg = FusedConfig(eff, ctx, tn, rl, k, mode, 900 + len(rl), fused)
+                t_ms = time_steps(torch, ctx, cfg, 100, 5)
+                res["fused" if fused else "separate"] = t_ms
+                nbytes = cfg.bytes
+                cfg.free()
+            sweep[key] = {"us": round(res["fused"] * 1e3, 2), "separate_us": round(res["separate"] * 1e3, 2),
+                          "GB/s": round(nbytes / (res["fused"] * 1e-3) / 1e9, 1), "bound": "hbm",
+                          "roofline_frac": round(nbytes / (HBM_PEAK_GBS * 1e9) / (res["fused"] * 1e-3), 4),
+                          "path": "fused gemv"}
             print(f"# {key}: {sweep[key]}", file=sys.stderr, flush=True)
 
     base = None
