@@ -470,6 +470,85 @@ int eff_dequant(eff_ctx *ctx, int type, eff_buf *w, eff_buf *out, uint32_t n_blo
   return EFF_OK;
 }
 
+namespace {
+
+// Shared checks of the gather entry points (quant.gather, ops.js:1104-1110).
+int gather_view(eff_ctx *ctx, int type, eff_buf *w, eff_buf *ids, uint32_t dim, uint32_t tokens, WeightView &wv,
+                const char *who) {
+  if (!w || !ids) return fail(ctx, EFF_E_INVALID, "%s: null buffer", who);
+  if (!type_known(type)) return fail(ctx, EFF_E_TYPE, "%s: unsupported quantization type %d", who, type);
+  const Geometry g = geometry(type);
+  if (dim == 0 || dim % g.elems)
+    return fail(ctx, EFF_E_SHAPE, "%s %s: dim=%u is not a multiple of %u", who, eff_type_name(type), dim, g.elems);
+  if ((uint64_t)tokens * 4 > ids->size)
+    return fail(ctx, EFF_E_BOUNDS, "%s: %u ids need %llu bytes and the buffer has %zu", who, tokens,
+                (unsigned long long)tokens * 4, ids->size);
+  wv = WeightView{};
+  wv.w = (const uint8_t *)w->ptr;
+  wv.type = type;
+  wv.k = dim;
+  wv.bpr = dim / g.elems;
+  wv.row_bytes = (uint64_t)wv.bpr * g.bytes;
+  wv.w_bytes = w->size + (w->owned ? kSlack : 16);
+  if (type == EFF_TYPE_Q8_0R) {
+    if (w->mark_type != EFF_TYPE_Q8_0R)
+      return fail(ctx, EFF_E_MARK, "%s Q8_0R: the buffer does not carry the mark of a repacked tensor", who);
+    if (w->mark_blocks < wv.bpr)
+      return fail(ctx, EFF_E_MARK, "%s Q8_0R: a row of %u blocks and a tensor of %u", who, wv.bpr, w->mark_blocks);
+    wv.scales_off = (uint64_t)32 * w->mark_blocks;
+  } else if (wv.row_bytes > w->size) {
+    return fail(ctx, EFF_E_BOUNDS, "%s %s: a row needs %llu bytes and the table has %zu", who, eff_type_name(type),
+                (unsigned long long)wv.row_bytes, w->size);
+  }
+  return EFF_OK;
+}
+
+int check_out(eff_ctx *ctx, eff_buf *b, uint64_t bytes, const char *who) {
+  if (!b) return fail(ctx, EFF_E_INVALID, "%s: null buffer", who);
+  if (bytes > b->size)
+    return fail(ctx, EFF_E_BOUNDS, "%s: needs %llu bytes and the buffer has %zu", who, (unsigned long long)bytes,
+                b->size);
+  if ((uintptr_t)b->ptr & 15) return fail(ctx, EFF_E_INVALID, "%s: device buffers must be 16-byte aligned", who);
+  return EFF_OK;
+}
+
+}  // namespace
+
+int eff_gather(eff_ctx *ctx, int type, eff_buf *w, eff_buf *ids, eff_buf *out, uint32_t dim, uint32_t tokens) {
+  if (!ctx) return EFF_E_INVALID;
+  WeightView wv;
+  int rc = gather_view(ctx, type, w, ids, dim, tokens, wv, "gather");
+  if (rc || (rc = check_out(ctx, out, (uint64_t)tokens * dim * 4, "gather"))) return rc;
+  if (tokens == 0) return EFF_OK;
+  if ((rc = use_device(ctx))) return rc;
+  hipError_t e = launch_gather(wv, (const uint32_t *)ids->ptr, tokens, (float *)out->ptr, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "gather launch");
+  ++ctx->stats.gather;
+  return EFF_OK;
+}
+
+int eff_gather_norm(eff_ctx *ctx, int type, eff_buf *w, eff_buf *ids, eff_buf *wn, float eps, eff_buf *x,
+                    eff_buf *nrm, uint32_t dim, uint32_t tokens) {
+  if (!ctx) return EFF_E_INVALID;
+  if (type == EFF_TYPE_IQ2_XXS)
+    return fail(ctx, EFF_E_TYPE, "gather+norm: IQ2_XXS has no block reader here (its grid is not bound)");
+  WeightView wv;
+  int rc = gather_view(ctx, type, w, ids, dim, tokens, wv, "gather+norm");
+  if (rc) return rc;
+  if (dim > kGatherNormMaxDim) return fail(ctx, EFF_E_SHAPE, "gather+norm: dim=%u above %u", dim, kGatherNormMaxDim);
+  if ((rc = check_out(ctx, x, (uint64_t)tokens * dim * 4, "gather+norm x")) ||
+      (rc = check_out(ctx, nrm, (uint64_t)tokens * dim * 4, "gather+norm nrm")) ||
+      (rc = check_out(ctx, wn, (uint64_t)dim * 4, "gather+norm weights")))
+    return rc;
+  if (tokens == 0) return EFF_OK;
+  if ((rc = use_device(ctx))) return rc;
+  hipError_t e = launch_gather_norm(wv, (const uint32_t *)ids->ptr, tokens, (const float *)wn->ptr, eps,
+                                    (float *)x->ptr, (float *)nrm->ptr, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "gather+norm launch");
+  ++ctx->stats.gather;
+  return EFF_OK;
+}
+
 size_t eff_topk_out_bytes(void) { return sizeof(uint32_t) * (EFF_TOPK_HEADER + EFF_TOPK_P_MAX + 2 * EFF_TOPK_CAP); }
 
 int eff_topk(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint32_t m, const uint32_t *penal_ids,

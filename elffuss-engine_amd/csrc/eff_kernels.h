@@ -77,6 +77,13 @@ size_t sx_x_bytes(int type, uint32_t tokens, uint32_t k);
 hipError_t launch_sx(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *scratch, int cfg,
                      hipStream_t stream);
 
+// Embedding gather: out[t] = dequantized row ids[t] (bit-identical to dequant);
+// with the norm, also nrm[t] = x[t] / sqrt(mean(x[t]^2) + eps) * wn, dim <= kGatherNormMaxDim.
+constexpr uint32_t kGatherNormMaxDim = 32768;
+hipError_t launch_gather(const WeightView &wv, const uint32_t *ids, uint32_t tokens, float *out, hipStream_t stream);
+hipError_t launch_gather_norm(const WeightView &wv, const uint32_t *ids, uint32_t tokens, const float *wn, float eps,
+                              float *x, float *nrm, hipStream_t stream);
+
 hipError_t launch_dequant(const WeightView &wv, uint32_t n_blocks, float *out, hipStream_t stream);
 
 // Top-k scratch: per chunk 2 u32 (count, flags) + 2 * kTopkChunkCap u32 (id, bits).

@@ -387,6 +387,90 @@ __global__ __launch_bounds__(256) void k_dequant(WeightView wv, uint32_t n_block
 }
 
 // ---------------------------------------------------------------------------
+// Embedding gather (quant.gather, ops.js:1104-1118; gatherShader,
+// kernels.wgsl.js:1188-1221): out[t][:] = the dequantized row ids[t] of W,
+// decoded a unit at a time by the same decoder as k_dequant (bit-identical to
+// it). Rows are read through the buffer descriptor, so an id past the table
+// reads zeros. One thread per (token, unit).
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_gather(WeightView wv, const uint32_t *__restrict__ ids, uint32_t tokens,
+                                                float *__restrict__ out) {
+  __shared__ uint32_t grid[TYPE == IQ2_XXS ? 512 : 1];
+  stage_grid<TYPE>(grid);
+  if constexpr (TYPE == IQ2_XXS) __syncthreads();
+  constexpr uint32_t upb = units_per_block<TYPE>();
+  const uint32_t upr = wv.bpr * upb;  // units per row
+  const uint64_t gu = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (gu >= (uint64_t)tokens * upr) return;
+  const uint32_t t = (uint32_t)(gu / upr), u = (uint32_t)(gu % upr), b = u / upb, sub = u % upb;
+  const BufSrc src = make_src(wv, 0);
+  Raw<TYPE> r;
+  load_raw<TYPE>(r, src, ids[t] * wv.bpr + b, sub);
+  float v[32];
+  dequant_unit<TYPE>(r, grid, v);
+  uint32_t o0, o1;
+  unit_runs<TYPE>(sub, o0, o1);
+  float *dst = out + (uint64_t)t * wv.k + (uint64_t)b * block_elems<TYPE>();
+#pragma unroll
+  for (int i = 0; i < 16; i += 4) {
+    *(float4 *)(dst + o0 + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+    *(float4 *)(dst + o1 + i) = make_float4(v[16 + i], v[17 + i], v[18 + i], v[19 + i]);
+  }
+}
+
+// Gather + the first layer's RMS norm (gatherNormaShader,
+// kernels.fusion.wgsl.js:164-206): one workgroup per token writes the row to
+// x and nrm = x * (1 / sqrt(sum(x^2) / dim + eps)) * wn. The row stays in LDS
+// between the two phases; the squares are summed per thread over the columns
+// c = tid + 256 j, then across the workgroup in a fixed order.
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_gather_norm(WeightView wv, const uint32_t *__restrict__ ids,
+                                                     const float *__restrict__ wn, float eps, float *__restrict__ x,
+                                                     float *__restrict__ nrm) {
+  extern __shared__ __align__(16) float row[];
+  __shared__ float part[256];
+  __shared__ uint32_t grid[TYPE == IQ2_XXS ? 512 : 1];
+  stage_grid<TYPE>(grid);
+  if constexpr (TYPE == IQ2_XXS) __syncthreads();
+  constexpr uint32_t upb = units_per_block<TYPE>();
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, dim = wv.k, upr = wv.bpr * upb;
+  const uint32_t id = ids[t];
+  const BufSrc src = make_src(wv, 0);
+  for (uint32_t u = tid; u < upr; u += 256u) {
+    const uint32_t b = u / upb, sub = u % upb;
+    Raw<TYPE> r;
+    load_raw<TYPE>(r, src, id * wv.bpr + b, sub);
+    float v[32];
+    dequant_unit<TYPE>(r, grid, v);
+    uint32_t o0, o1;
+    unit_runs<TYPE>(sub, o0, o1);
+    float *dl = row + b * block_elems<TYPE>();
+    float *dg = x + (uint64_t)t * dim + b * block_elems<TYPE>();
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const float4 a = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+      const float4 c = make_float4(v[16 + i], v[17 + i], v[18 + i], v[19 + i]);
+      *(float4 *)(dl + o0 + i) = a;
+      *(float4 *)(dl + o1 + i) = c;
+      *(float4 *)(dg + o0 + i) = a;
+      *(float4 *)(dg + o1 + i) = c;
+    }
+  }
+  __syncthreads();
+  float acc = 0.f;
+  for (uint32_t c = tid; c < dim; c += 256u) acc = __builtin_fmaf(row[c], row[c], acc);
+  part[tid] = acc;
+  __syncthreads();
+  for (uint32_t off = 128u; off > 0u; off >>= 1) {
+    if (tid < off) part[tid] += part[tid + off];
+    __syncthreads();
+  }
+  const float scale = 1.0f / sqrtf(part[0] / (float)dim + eps);
+  float *dn = nrm + (uint64_t)t * dim;
+  for (uint32_t c = tid; c < dim; c += 256u) dn[c] = row[c] * scale * wn[c];
+}
+
+// ---------------------------------------------------------------------------
 // GEMV: Y[t][row] = sum_k W[row][k] X[t][k], 1..8 tokens, f32 accumulation.
 //
 // A workgroup is 4 waves arranged as G = 4/S row groups x S slices of k. Each
@@ -1265,6 +1349,52 @@ hipError_t launch_dequant(const WeightView &wv, uint32_t n_blocks, float *out, h
     case Q6_K: return dequant_go<Q6_K>(wv, n_blocks, out, s);
     case Q2_K: return dequant_go<Q2_K>(wv, n_blocks, out, s);
     case IQ2_XXS: return dequant_go<IQ2_XXS>(wv, n_blocks, out, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int TYPE>
+static hipError_t gather_go(const WeightView &wv, const uint32_t *ids, uint32_t tokens, float *out, hipStream_t s) {
+  const uint64_t units = (uint64_t)tokens * wv.bpr * units_per_block<TYPE>();
+  hipLaunchKernelGGL((k_gather<TYPE>), dim3((uint32_t)((units + 255) / 256)), dim3(256), 0, s, wv, ids, tokens, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(const WeightView &wv, const uint32_t *ids, uint32_t tokens, float *out, hipStream_t s) {
+  switch (wv.type) {
+    case Q8_0: return gather_go<Q8_0>(wv, ids, tokens, out, s);
+    case Q8_0R: return gather_go<Q8_0R>(wv, ids, tokens, out, s);
+    case Q4_K: return gather_go<Q4_K>(wv, ids, tokens, out, s);
+    case Q6_K: return gather_go<Q6_K>(wv, ids, tokens, out, s);
+    case Q2_K: return gather_go<Q2_K>(wv, ids, tokens, out, s);
+    case IQ2_XXS: return gather_go<IQ2_XXS>(wv, ids, tokens, out, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int TYPE>
+static hipError_t gather_norm_go(const WeightView &wv, const uint32_t *ids, uint32_t tokens, const float *wn, float eps,
+                                 float *x, float *nrm, hipStream_t s) {
+  const size_t lds = (size_t)wv.k * 4u;
+  static bool attr = false;
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute((const void *)k_gather_norm<TYPE>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGatherNormMaxDim * 4);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  hipLaunchKernelGGL((k_gather_norm<TYPE>), dim3(tokens), dim3(256), lds, s, wv, ids, wn, eps, x, nrm);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_norm(const WeightView &wv, const uint32_t *ids, uint32_t tokens, const float *wn, float eps,
+                              float *x, float *nrm, hipStream_t s) {
+  switch (wv.type) {
+    case Q8_0: return gather_norm_go<Q8_0>(wv, ids, tokens, wn, eps, x, nrm, s);
+    case Q8_0R: return gather_norm_go<Q8_0R>(wv, ids, tokens, wn, eps, x, nrm, s);
+    case Q4_K: return gather_norm_go<Q4_K>(wv, ids, tokens, wn, eps, x, nrm, s);
+    case Q6_K: return gather_norm_go<Q6_K>(wv, ids, tokens, wn, eps, x, nrm, s);
+    case Q2_K: return gather_norm_go<Q2_K>(wv, ids, tokens, wn, eps, x, nrm, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -41,7 +41,7 @@ class NotApplicable(Exception):
 class Stats(ctypes.Structure):
     _fields_ = [("gemv", ctypes.c_uint64), ("gemm", ctypes.c_uint64), ("skinny", ctypes.c_uint64),
                 ("dequant", ctypes.c_uint64), ("topk", ctypes.c_uint64), ("not_applicable", ctypes.c_uint64),
-                ("split", ctypes.c_uint64), ("fused", ctypes.c_uint64)]
+                ("split", ctypes.c_uint64), ("fused", ctypes.c_uint64), ("gather", ctypes.c_uint64)]
 
 
 _lib = None
@@ -93,6 +93,8 @@ def lib():
         "eff_qgemv_multi": ([p, i32, i32, u32, ctypes.POINTER(p), p, ctypes.POINTER(p), ctypes.POINTER(u32), u32, u32],
                             i32),
         "eff_dequant": ([p, i32, p, p, u32], i32),
+        "eff_gather": ([p, i32, p, p, p, u32, u32], i32),
+        "eff_gather_norm": ([p, i32, p, p, p, ctypes.c_float, p, p, u32, u32], i32),
         "eff_topk": ([p, p, u32, u32, u32, p, u32, u32, p], i32),
         "eff_topk_out_bytes": ([], sz),
     }
@@ -109,7 +111,7 @@ EXPORTED = ("eff_type_from_name eff_type_name eff_type_geometry eff_init eff_shu
             "eff_buf_free eff_buf_size eff_buf_device_ptr eff_buf_write eff_buf_read eff_buf_copy "
             "eff_bytes_reordered eff_bytes_buffer_r eff_blocks_from_buffer eff_scales_from eff_buf_mark_r "
             "eff_buf_blocks_r eff_repack eff_unrepack eff_quantize eff_fill_normal eff_qmatmul eff_qgemv "
-            "eff_qgemm eff_qgemv_multi eff_dequant eff_topk eff_topk_out_bytes").split()
+            "eff_qgemm eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_out_bytes").split()
 
 
 def type_code(t):
@@ -298,6 +300,13 @@ class Context:
 
     def dequant(self, t, w, out, n_blocks):
         self._check(lib().eff_dequant(self.h, type_code(t), w.handle, out.handle, n_blocks))
+
+    def gather(self, t, w, ids, out, dim, tokens):
+        self._check(lib().eff_gather(self.h, type_code(t), w.handle, ids.handle, out.handle, dim, tokens))
+
+    def gather_norm(self, t, w, ids, wn, eps, x, nrm, dim, tokens):
+        self._check(lib().eff_gather_norm(self.h, type_code(t), w.handle, ids.handle, wn.handle, eps, x.handle,
+                                          nrm.handle, dim, tokens))
 
     def topk(self, logits, base, vocab, m, penal_ids=(), serial=1, out=None):
         ids = np.ascontiguousarray(np.asarray(penal_ids, dtype=np.uint32))

@@ -271,6 +271,7 @@ napi_value Stats(napi_env env, napi_callback_info info) {
   napi_set_named_property(env, o, "notApplicable", make_int(env, (int64_t)s.not_applicable));
   napi_set_named_property(env, o, "split", make_int(env, (int64_t)s.split));
   napi_set_named_property(env, o, "fused", make_int(env, (int64_t)s.fused));
+  napi_set_named_property(env, o, "gather", make_int(env, (int64_t)s.gather));
   return o;
 }
 
@@ -444,6 +445,28 @@ napi_value Dequant(napi_env env, napi_callback_info info) {
                                       external<eff_buf>(env, a[3]), (uint32_t)i64(env, a[4])));
 }
 
+// gather(ctx, type, w, ids, out, dim, tokens)
+napi_value Gather(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  get_args(env, info, 7, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  return status(env, ctx, eff_gather(ctx, (int)i64(env, a[1]), external<eff_buf>(env, a[2]), external<eff_buf>(env, a[3]),
+                                     external<eff_buf>(env, a[4]), (uint32_t)i64(env, a[5]), (uint32_t)i64(env, a[6])));
+}
+
+// gatherNorm(ctx, type, w, ids, wn, eps, x, nrm, dim, tokens)
+napi_value GatherNorm(napi_env env, napi_callback_info info) {
+  napi_value a[10];
+  get_args(env, info, 10, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  double eps = 0;
+  napi_get_value_double(env, a[5], &eps);
+  return status(env, ctx, eff_gather_norm(ctx, (int)i64(env, a[1]), external<eff_buf>(env, a[2]),
+                                          external<eff_buf>(env, a[3]), external<eff_buf>(env, a[4]), (float)eps,
+                                          external<eff_buf>(env, a[6]), external<eff_buf>(env, a[7]),
+                                          (uint32_t)i64(env, a[8]), (uint32_t)i64(env, a[9])));
+}
+
 // topk(ctx, logits, base, vocab, m, penalIds (Uint32Array|null), serial, out)
 napi_value TopK(napi_env env, napi_callback_info info) {
   napi_value a[8];
@@ -469,7 +492,7 @@ napi_value Register(napi_env env, napi_value exports) {
       {"init", Init}, {"shutdown", Shutdown}, {"sync", Sync}, {"setOption", SetOption}, {"stats", Stats},
       {"bufAlloc", BufAlloc}, {"bufFree", BufFree}, {"bufWrite", BufWrite}, {"bufRead", BufRead},
       {"bufReadAsync", BufReadAsync}, {"bufSize", BufSize}, {"bufMarkR", BufMarkR}, {"bufBlocksR", BufBlocksR},
-      {"qmatmul", QMatmul}, {"qgemv", QGemv}, {"qgemvMulti", QGemvMulti}, {"qgemm", QGemm}, {"dequant", Dequant}, {"topk", TopK},
+      {"qmatmul", QMatmul}, {"qgemv", QGemv}, {"qgemvMulti", QGemvMulti}, {"qgemm", QGemm}, {"dequant", Dequant}, {"gather", Gather}, {"gatherNorm", GatherNorm}, {"topk", TopK},
       {"topkOutBytes", TopKOutBytes},
   };
   for (auto &f : fns) {

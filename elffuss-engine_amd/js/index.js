@@ -248,6 +248,25 @@ function createGemvOps(device, deps) {
   };
 }
 
+// createFusionOps, the part on this path (ops.fusion.js:154-170): the
+// embedding gather fused with the first layer's RMS norm.
+const TIPOS_GATHER_NORMA = new Set(['Q8_0', 'Q2_K', 'Q4_K', 'Q6_K', 'Q8_0R']);
+function createFusionOps(device, deps) {
+  const ctx = deps.ctx;
+  return {
+    gatherNorma(type, wBuf, idsBuf, wNorm, dim, tokens, eps) {
+      const i = QUANT_TYPES[type];
+      if (!i || !TIPOS_GATHER_NORMA.has(type)) throw new Error(`gather+norma: tipo «${type}» sin lector de bloque`);
+      if (dim % i.blockElems !== 0) throw new Error(`gather+norma ${type}: dim=${dim} no es múltiplo de ${i.blockElems}`);
+      if (TIPOS_R.has(type)) compruebaBufferR(type, wBuf, { porFila: dim / i.blockElems }, 'gather+norma');
+      const x = ctx.alloc(tokens * dim * 4, 'embd');
+      const nrm = ctx.alloc(tokens * dim * 4, 'fusion.nrm');
+      native.gatherNorm(device._ctx, i.code, wBuf._h, idsBuf._h, wNorm._h, eps, x._h, nrm._h, dim, tokens);
+      return Promise.resolve({ x, nrm });
+    },
+  };
+}
+
 // createGemm2Ops (ops.gemm2.js:259-303): the prefill GEMM, null when it does not apply.
 function createGemm2Ops(ctx) {
   const device = ctx.device;
@@ -297,6 +316,16 @@ function createQuantOps(device, opts) {
       const out = ctx.alloc(nBlocks * i.blockElems * 4, 'dequant.out');
       native.dequant(device._ctx, i.code, wBuf._h, out._h, nBlocks);
       return Promise.resolve(out);
+    },
+    // Rows ids[t] of a quantized table (the embeddings) as f32 [tokens][dim]
+    // (ops.js:1104-1118); throws when dim is not a multiple of the block.
+    gather(type, wBuf, idsBuf, dim, tokens) {
+      const i = quantInfo(type);
+      if (dim % i.blockElems !== 0) throw new Error(`gather ${type}: dim=${dim} no es múltiplo de ${i.blockElems}`);
+      if (TIPOS_R.has(type)) compruebaBufferR(type, wBuf, { porFila: dim / i.blockElems }, 'gather');
+      const dst = ctx.alloc(tokens * dim * 4, 'embd');
+      native.gather(device._ctx, i.code, wBuf._h, idsBuf._h, dst._h, dim, tokens);
+      return Promise.resolve(dst);
     },
     // Y[tokens][rows] = W . X (ops.js:827-1101); throws when k is not a
     // multiple of the block, or for an unmarked repacked buffer.
@@ -368,7 +397,7 @@ function createTopKGPU(device, ctx) {
 module.exports = {
   native, STATUS, OPT, GEMV_MODE, TOPK, QUANT_TYPES, quantInfo,
   requestDevice, readback, createContext,
-  createQuantOps, createGemvOps, createGemm2Ops, createTopKGPU, estadisticasTopK,
+  createQuantOps, createGemvOps, createGemm2Ops, createFusionOps, createTopKGPU, estadisticasTopK, TIPOS_GATHER_NORMA,
   TIPOS_R, TIPO_R, TIPO_GGUF, bytesReordenado, bytesBufferR, bloquesDeBuffer, escalasDesde,
   reordena, vuelveAlGGUF, marcaBufferR, bloquesR, compruebaBufferR, creaBufferR,
   quantize: (type, f32) => native.quantize(quantInfo(type).code, f32),

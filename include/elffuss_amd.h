@@ -81,6 +81,7 @@ typedef struct eff_stats {
   uint64_t not_applicable;  /* calls answered EFF_NOT_APPLICABLE */
   uint64_t split;       /* split-x matrix-core launches (Q2_K, Q4_K, IQ2_XXS from 4 tokens) */
   uint64_t fused;       /* fused GEMV launches (eff_qgemv_multi) */
+  uint64_t gather;      /* gather launches (eff_gather, eff_gather_norm) */
 } eff_stats;
 
 /* ---- types and geometry -------------------------------------------------- */
@@ -232,6 +233,20 @@ int eff_qgemm(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
 /* Dequantize n_blocks blocks to f32, bit-exact with the reference decoders
  * (quant.dequant, ops.js:813-823; dequantShader, kernels.wgsl.js:903-922). */
 int eff_dequant(eff_ctx *ctx, int type, eff_buf *w, eff_buf *out, uint32_t n_blocks);
+
+/* Rows of a quantized table as f32, the embedding lookup: out[t][0..dim) is
+ * the dequantized row ids[t] of w for t < tokens (ids: u32 in a device buffer;
+ * an id past the table reads zeros). Bit-identical to eff_dequant of that row.
+ * Replaces quant.gather (ops.js:1104-1118). EFF_E_SHAPE if dim % block_elems. */
+int eff_gather(eff_ctx *ctx, int type, eff_buf *w, eff_buf *ids, eff_buf *out, uint32_t dim, uint32_t tokens);
+
+/* The gather fused with the first layer's RMS norm (fusion.gatherNorma,
+ * ops.fusion.js:154-170; kernels.fusion.wgsl.js:164-206): x as eff_gather, and
+ * nrm[t][c] = x[t][c] * (1 / sqrt(sum_c x[t][c]^2 / dim + eps)) * wn[c].
+ * dim <= 32768. EFF_E_TYPE for IQ2_XXS (the reference's closed list,
+ * kernels.fusion.wgsl.js:159-161). */
+int eff_gather_norm(eff_ctx *ctx, int type, eff_buf *w, eff_buf *ids, eff_buf *wn, float eps, eff_buf *x,
+                    eff_buf *nrm, uint32_t dim, uint32_t tokens);
 
 /* Exact top-m of logits[base .. base+vocab) ordered by (f32 value desc with
  * -0 == +0, index asc), plus the raw logits of the penalised ids. Writes the

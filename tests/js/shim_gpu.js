@@ -52,6 +52,20 @@ async function main() {
     } else {
       assert.strictEqual(await ops.gemm2.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens), null);
     }
+    // embedding rows 0, rows-1 and 1 of the same table, and the fused norm
+    const ids = ops.upload(Uint32Array.from([0, c.rows - 1, 1]), 'ids');
+    const ge = await ops.gather(c.type, wBuf, ids, c.k, 3);
+    out[c.name + ':gather'] = Array.from(new Uint32Array(await eff.readback(device, ge, 0, 3 * c.k * 4)));
+    if (eff.TIPOS_GATHER_NORMA.has(c.type)) {
+      const wn = ops.upload(new Float32Array(c.k).fill(1.5), 'wn');
+      const fus = eff.createFusionOps(device, { ctx: ops.ctx });
+      const r = await fus.gatherNorma(c.type, wBuf, ids, wn, c.k, 3, 1e-6);
+      out[c.name + ':gnx'] = Array.from(new Uint32Array(await eff.readback(device, r.x, 0, 3 * c.k * 4)));
+      out[c.name + ':gnn'] = Array.from(await rd(r.nrm, 3 * c.k));
+    } else {
+      const fus = eff.createFusionOps(device, { ctx: ops.ctx });
+      assert.throws(() => fus.gatherNorma(c.type, wBuf, ids, ids, c.k, 3, 1e-6), /lector/);
+    }
     const nb = c.rows * c.k / eff.QUANT_TYPES[c.type].blockElems;
     const dq = await ops.dequant(c.type, wBuf, nb);
     out[c.name + ':dequant'] = Array.from(new Uint32Array(await eff.readback(device, dq, 0, nb * eff.QUANT_TYPES[c.type].blockElems * 4)));

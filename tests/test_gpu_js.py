@@ -58,8 +58,16 @@ def test_js_shim_gpu(eff, orc, tmp_path):
             check_close(np.array(out[name + ":gemm2"], np.float32), orc.gemm_f16(ot, w, rows, k, x, tokens),
                         f"js gemm2 {name}")
         e, _ = eff.geometry(base)
-        assert np.array_equal(np.array(out[name + ":dequant"], np.uint32),
-                              orc.dequant(ot, w, rows * k // e).view(np.uint32))
+        table = orc.dequant(ot, w, rows * k // e)
+        assert np.array_equal(np.array(out[name + ":dequant"], np.uint32), table.view(np.uint32))
+        sel = table.reshape(rows, k)[[0, rows - 1, 1]]
+        assert np.array_equal(np.array(out[name + ":gather"], np.uint32).reshape(3, k), sel.view(np.uint32))
+        if name + ":gnx" in out:
+            assert np.array_equal(np.array(out[name + ":gnx"], np.uint32).reshape(3, k), sel.view(np.uint32))
+            s64 = sel.astype(np.float64)
+            want = s64 / np.sqrt((s64 * s64).sum(axis=1, keepdims=True) / k + 1e-6) * 1.5
+            got = np.array(out[name + ":gnn"], np.float64).reshape(3, k)
+            assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-30)) < 2e-6
     ids, bits, _ = orc.topk(logits.view(np.uint32), 40)
     assert out["topk"]["ids"] == ids.tolist() and out["topk"]["bits"] == bits.tolist()
     assert out["topk"]["bitsS"] == logits.view(np.uint32)[[5, 69999]].tolist()
