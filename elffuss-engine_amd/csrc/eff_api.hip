@@ -335,6 +335,30 @@ int eff_buf_mark_r(eff_buf *buf, int type_r, uint32_t n) {
   return EFF_OK;
 }
 
+int eff_buf_write_r(eff_ctx *ctx, eff_buf *buf, int type_r, uint32_t first_block, const void *src,
+                    uint32_t n_blocks) {
+  if (!ctx || !buf || (!src && n_blocks)) return EFF_E_INVALID;
+  if (type_r != EFF_TYPE_Q8_0R) return fail(ctx, EFF_E_TYPE, "write R: %d is not a repacked type", type_r);
+  if (buf->mark_type != EFF_TYPE_Q8_0R)
+    return fail(ctx, EFF_E_MARK, "write R: the buffer does not carry the mark of a repacked tensor");
+  const uint32_t N = buf->mark_blocks;
+  if (first_block > N || n_blocks > N - first_block)
+    return fail(ctx, EFF_E_BOUNDS, "write R: blocks %u..%u past a tensor of %u", first_block,
+                first_block + n_blocks, N);
+  if (!n_blocks) return EFF_OK;
+  std::string tmp(eff_bytes_reordered(type_r, n_blocks), '\0');  // 34 n rounded up to a word
+  int rc = eff_repack(type_r, src, n_blocks, &tmp[0], tmp.size());
+  if (rc) return fail(ctx, rc, "write R: repack failed");
+  if ((rc = use_device(ctx))) return rc;
+  char *base = (char *)buf->ptr;
+  EFF_HIP(ctx, hipMemcpyAsync(base + (size_t)32 * first_block, tmp.data(), (size_t)32 * n_blocks,
+                              hipMemcpyHostToDevice, ctx->stream));
+  EFF_HIP(ctx, hipMemcpyAsync(base + (size_t)32 * N + (size_t)2 * first_block, tmp.data() + (size_t)32 * n_blocks,
+                              (size_t)2 * n_blocks, hipMemcpyHostToDevice, ctx->stream));
+  EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return EFF_OK;
+}
+
 int eff_buf_blocks_r(const eff_buf *buf, uint32_t *n) {
   if (!buf || !n) return EFF_E_INVALID;
   if (buf->mark_type != EFF_TYPE_Q8_0R) return EFF_E_MARK;

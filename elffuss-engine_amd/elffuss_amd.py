@@ -83,6 +83,7 @@ def lib():
         "eff_scales_from": ([i32, u32], u32),
         "eff_buf_mark_r": ([p, i32, u32], i32),
         "eff_buf_blocks_r": ([p, ctypes.POINTER(u32)], i32),
+        "eff_buf_write_r": ([p, p, i32, u32, p, u32], i32),
         "eff_repack": ([i32, p, u32, p, sz], i32),
         "eff_unrepack": ([i32, p, sz, u32, p], i32),
         "eff_quantize": ([i32, p, sz, p, sz], i32),
@@ -110,7 +111,7 @@ EXPORTED = ("eff_type_from_name eff_type_name eff_type_geometry eff_init eff_shu
             "eff_stream eff_set_stream eff_sync eff_set_option eff_get_stats eff_buf_alloc eff_buf_wrap "
             "eff_buf_free eff_buf_size eff_buf_device_ptr eff_buf_write eff_buf_read eff_buf_copy "
             "eff_bytes_reordered eff_bytes_buffer_r eff_blocks_from_buffer eff_scales_from eff_buf_mark_r "
-            "eff_buf_blocks_r eff_repack eff_unrepack eff_quantize eff_fill_normal eff_qmatmul eff_qgemv "
+            "eff_buf_blocks_r eff_buf_write_r eff_repack eff_unrepack eff_quantize eff_fill_normal eff_qmatmul eff_qgemv "
             "eff_qgemm eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_out_bytes").split()
 
 
@@ -206,6 +207,14 @@ class Buffer:
         rc = lib().eff_buf_mark_r(self.handle, Q8_0R, n_blocks)
         if rc:
             raise EffError(rc, f"mark_r: buffer of {self.size} bytes for {n_blocks} blocks")
+
+    def write_r(self, first_block, gguf_bytes):
+        """Repack GGUF Q8_0 blocks (bytes) into this marked buffer from block first_block."""
+        a = np.ascontiguousarray(gguf_bytes, dtype=np.uint8)
+        if a.nbytes % 34:
+            raise ValueError(f"write_r: {a.nbytes} bytes are not whole 34-byte blocks")
+        self.ctx._check(lib().eff_buf_write_r(self.ctx.h, self.handle, Q8_0R, first_block, a.ctypes.data,
+                                              a.nbytes // 34))
 
     def blocks_r(self):
         n = ctypes.c_uint32()

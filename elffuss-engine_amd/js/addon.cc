@@ -383,6 +383,20 @@ napi_value BufMarkR(napi_env env, napi_callback_info info) {
   return make_int(env, eff_buf_mark_r(external<eff_buf>(env, a[0]), (int)i64(env, a[1]), (uint32_t)i64(env, a[2])));
 }
 
+// bufWriteR(ctx, buf, typeR, firstBlock, ggufBytes): one chunk of the
+// chunked Q8_0R upload (repack.js:318-345), repacked on the host.
+napi_value BufWriteR(napi_env env, napi_callback_info info) {
+  napi_value a[5];
+  get_args(env, info, 5, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  void *src;
+  size_t len;
+  if (!bytes_of(env, a[4], &src, &len)) return throw_msg(env, "bufWriteR: data must be an ArrayBuffer or view");
+  if (len % 34) return throw_msg(env, "bufWriteR: data is not whole 34-byte blocks", EFF_E_INVALID);
+  return status(env, ctx, eff_buf_write_r(ctx, external<eff_buf>(env, a[1]), (int)i64(env, a[2]),
+                                          (uint32_t)i64(env, a[3]), src, (uint32_t)(len / 34)));
+}
+
 napi_value BufBlocksR(napi_env env, napi_callback_info info) {
   napi_value a[1];
   get_args(env, info, 1, a);
@@ -491,7 +505,7 @@ napi_value Register(napi_env env, napi_value exports) {
       {"repack", Repack}, {"unrepack", Unrepack}, {"quantize", Quantize}, {"fillNormal", FillNormal},
       {"init", Init}, {"shutdown", Shutdown}, {"sync", Sync}, {"setOption", SetOption}, {"stats", Stats},
       {"bufAlloc", BufAlloc}, {"bufFree", BufFree}, {"bufWrite", BufWrite}, {"bufRead", BufRead},
-      {"bufReadAsync", BufReadAsync}, {"bufSize", BufSize}, {"bufMarkR", BufMarkR}, {"bufBlocksR", BufBlocksR},
+      {"bufReadAsync", BufReadAsync}, {"bufSize", BufSize}, {"bufMarkR", BufMarkR}, {"bufBlocksR", BufBlocksR}, {"bufWriteR", BufWriteR},
       {"qmatmul", QMatmul}, {"qgemv", QGemv}, {"qgemvMulti", QGemvMulti}, {"qgemm", QGemm}, {"dequant", Dequant}, {"gather", Gather}, {"gatherNorm", GatherNorm}, {"topk", TopK},
       {"topkOutBytes", TopKOutBytes},
   };

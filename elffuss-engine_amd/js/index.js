@@ -200,6 +200,172 @@ function creaBufferR(device, t, tipoR) {
   return marcaBufferR(buf, tipoR, nBloques);
 }
 
+// ---- load path (gguf.js:97-111, model.js:141-330, repack.js:69-84, 308-345) ---
+
+// [block elements, block bytes] of the tensor types a load accepts: the GGUF
+// types with a kernel here, and the float types a model carries beside them
+// (norm weights, biases), which go up as plain bytes (gguf.js:51-64).
+const GEOMETRIA_CARGA = { F32: [1, 4], F16: [1, 2] };
+for (const name of TYPE_NAMES) {
+  if (!TIPOS_R.has(name)) GEOMETRIA_CARGA[name] = [QUANT_TYPES[name].blockElems, QUANT_TYPES[name].blockBytes];
+}
+
+// Bytes of a tensor: whole blocks along dims[0] times the other dims
+// (tensorBytes, gguf.js:104-111); 0 for a type the load does not accept.
+function tensorBytes(dims, typeName) {
+  const g = GEOMETRIA_CARGA[typeName];
+  if (!g) return 0;
+  let n = (dims[0] / g[0]) * g[1];
+  for (let i = 1; i < dims.length; i++) n *= dims[i];
+  return n;
+}
+
+// The descriptor that travels with a repacked buffer: a copy with the internal
+// type, the file's type kept beside it (comoReordenado, repack.js:78-80).
+function comoReordenado(t, tipoR) {
+  return Object.assign({}, t, { typeName: tipoR, typeNameGGUF: t.typeName });
+}
+
+function incompleto(que, pedidos, llegaron) {
+  return new Error(`${que}: pedidos ${pedidos} bytes y llegaron ${llegaron}`);
+}
+
+// subeReordenadoPorTrozos (repack.js:318-345): a Q8_0 tensor too large for
+// one read goes up in chunks of whole blocks, an even number per chunk as the
+// reference cuts them, each repacked on the host and written to its quants and
+// scales regions of the marked buffer by the library (eff_buf_write_r).
+// `cuenta(msLeer, msSubir, bytes)` is called once per chunk.
+async function subeReordenadoPorTrozos(o) {
+  const { device, ranged, t, buf, tipoR } = o;
+  if (!TIPOS_R.has(tipoR)) throw new Error(`subeReordenadoPorTrozos: «${tipoR}» no es un tipo reordenado`);
+  const ahora = o.ahora || Date.now;
+  const cuenta = o.cuenta || (() => {});
+  const B = QUANT_TYPES.Q8_0.blockBytes;
+  const N = t.nElements / QUANT_TYPES.Q8_0.blockElems;
+  const porTrozo = Math.max(2, 2 * Math.floor(o.trozo / (2 * B)));
+  for (let b0 = 0; b0 < N; b0 += porTrozo) {
+    const nb = Math.min(porTrozo, N - b0);
+    const t0 = ahora();
+    const raw = await ranged.slice(t.start + b0 * B, nb * B);
+    const t1 = ahora();
+    // A short chunk would go up as weights without a single error.
+    if (raw.byteLength !== nb * B) throw incompleto(`trozo incompleto en «${t.name}»`, nb * B, raw.byteLength);
+    native.bufWriteR(device._ctx, buf._h, R_CODE, b0, raw);
+    cuenta(t1 - t0, ahora() - t1, nb * B);
+  }
+}
+
+// The weight upload of loadModel (model.js:141-330) over a tensor table
+// ({name, typeName, dims, nElements, nBytes, start} per tensor, as parseGGUF
+// gives it) and a ranged handle ({size, slice(offset, length) -> Promise of
+// an ArrayBuffer}):
+//   * every type must have a kernel (or be F32/F16) before a byte moves;
+//   * tensors that follow each other in the file are read together, in spans
+//     of up to `tramo` bytes (default 128 MiB); a larger tensor is read alone
+//     in chunks of `trozo` bytes (default 32 MiB);
+//   * each tensor gets its own buffer with 4 bytes of slack after the data,
+//     zero like the rest of a new buffer;
+//   * with `reorden` (the __ELFFUSS_REPACK switch, read once per load) Q8_0
+//     tensors go up repacked as Q8_0R into marked buffers, and their
+//     descriptor says Q8_0R.
+// Resolves to { pesos: Map name -> { buf, t }, stats }.
+async function cargaTensores(device, ranged, tensores, opciones) {
+  const o = opciones || {};
+  const onProgress = o.onProgress || (() => {});
+  const conReorden = o.reorden === true;
+  const TRAMO = Math.max(1, Math.floor(o.tramo || 128 * 1048576));
+  const TROZO = Math.max(1, Math.floor(o.trozo || 32 * 1048576));
+  const ahora = o.ahora || (() => (typeof performance !== 'undefined' ? performance.now() : Date.now()));
+  const limite = device.limits.maxStorageBufferBindingSize;
+
+  const sinKernel = new Map();
+  for (const t of tensores) {
+    if (!GEOMETRIA_CARGA[t.typeName] && !sinKernel.has(t.typeName)) sinKernel.set(t.typeName, t.name);
+  }
+  if (sinKernel.size) {
+    throw new Error('el fichero trae tipos sin kernel: ' +
+      Array.from(sinKernel, ([k, n]) => `${k} (p.ej. «${n}»)`).join(', '));
+  }
+
+  const tramos = [];
+  for (const t of tensores) {
+    if (t.nBytes > limite) throw new Error(`«${t.name}» son ${t.nBytes} bytes y el límite de binding es ${limite}`);
+    const ult = tramos[tramos.length - 1];
+    // Only a tensor that starts where the previous one ends joins its span:
+    // padding between them would otherwise become part of a weight.
+    if (ult && t.start === ult.fin && ult.fin - ult.ini + t.nBytes <= TRAMO) {
+      ult.fin += t.nBytes;
+      ult.ts.push(t);
+    } else {
+      tramos.push({ ini: t.start, fin: t.start + t.nBytes, ts: [t] });
+    }
+  }
+
+  const pesos = new Map();
+  const stats = { msLeer: 0, msSubir: 0, trozos: 0, tramos: tramos.length, reordenados: 0, bytes: 0 };
+  const total = tensores.reduce((n, t) => n + t.nBytes, 0);
+  const avanza = (n, nombre) => { stats.bytes += n; onProgress(stats.bytes, total, nombre); };
+  const conHolgura = (t) => device.createBuffer({ size: Math.ceil((t.nBytes + 4) / 4) * 4, label: t.name });
+  const tipoRDe = (t) => (conReorden && TIPO_R[t.typeName]) || null;
+
+  for (const tr of tramos) {
+    const largo = tr.fin - tr.ini;
+    if (largo > TRAMO) {
+      const t = tr.ts[0];
+      const tipoR = tipoRDe(t);
+      if (tipoR) {
+        const buf = creaBufferR(device, t, tipoR);
+        await subeReordenadoPorTrozos({
+          device, ranged, t, buf, tipoR, trozo: TROZO, ahora,
+          cuenta: (leer, subir, n) => {
+            stats.msLeer += leer; stats.msSubir += subir; stats.trozos++;
+            avanza(n, t.name);
+          },
+        });
+        pesos.set(t.name, { buf, t: comoReordenado(t, tipoR) });
+        stats.reordenados++;
+        continue;
+      }
+      const buf = conHolgura(t);
+      for (let off = 0; off < t.nBytes; off += TROZO) {
+        const len = Math.min(TROZO, t.nBytes - off);
+        const t0 = ahora();
+        const raw = await ranged.slice(t.start + off, len);
+        const t1 = ahora();
+        if (raw.byteLength !== len) throw incompleto(`trozo incompleto en «${t.name}»`, len, raw.byteLength);
+        device.queue.writeBuffer(buf, off, raw);
+        stats.msLeer += t1 - t0; stats.msSubir += ahora() - t1; stats.trozos++;
+        avanza(len, t.name);
+      }
+      pesos.set(t.name, { buf, t });
+      continue;
+    }
+
+    const t0 = ahora();
+    const span = new Uint8Array(await ranged.slice(tr.ini, largo));
+    stats.msLeer += ahora() - t0; stats.trozos++;
+    if (span.byteLength !== largo) throw incompleto(`tramo incompleto desde ${tr.ini}`, largo, span.byteLength);
+    for (const t of tr.ts) {
+      const tipoR = tipoRDe(t);
+      const t1 = ahora();
+      const bytes = span.subarray(t.start - tr.ini, t.start - tr.ini + t.nBytes);
+      let buf;
+      if (tipoR) {
+        buf = creaBufferR(device, t, tipoR);
+        native.bufWriteR(device._ctx, buf._h, R_CODE, 0, bytes);
+        stats.reordenados++;
+      } else {
+        buf = conHolgura(t);
+        device.queue.writeBuffer(buf, 0, bytes);
+      }
+      stats.msSubir += ahora() - t1;
+      avanza(t.nBytes, t.name);
+      pesos.set(t.name, { buf, t: tipoR ? comoReordenado(t, tipoR) : t });
+    }
+  }
+  return { pesos, stats };
+}
+
 // ---- operators ---------------------------------------------------------------
 
 // createGemvOps (ops.gemv.js:44-221): the decode GEMV, null when it does not apply.
@@ -400,6 +566,7 @@ module.exports = {
   createQuantOps, createGemvOps, createGemm2Ops, createFusionOps, createTopKGPU, estadisticasTopK, TIPOS_GATHER_NORMA,
   TIPOS_R, TIPO_R, TIPO_GGUF, bytesReordenado, bytesBufferR, bloquesDeBuffer, escalasDesde,
   reordena, vuelveAlGGUF, marcaBufferR, bloquesR, compruebaBufferR, creaBufferR,
+  tensorBytes, comoReordenado, subeReordenadoPorTrozos, cargaTensores,
   quantize: (type, f32) => native.quantize(quantInfo(type).code, f32),
   fillNormal: (seed, sigma, n) => native.fillNormal(seed, sigma, n),
 };

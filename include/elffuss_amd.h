@@ -184,6 +184,16 @@ int eff_repack(int type_r, const void *src, uint32_t n_blocks, void *dst, size_t
 /* Inverse: Q8_0R back to GGUF blocks, 34n bytes (vuelveAlGGUF, repack.js:204-219). */
 int eff_unrepack(int type_r, const void *src, size_t src_bytes, uint32_t n_blocks, void *dst);
 
+/* Upload a chunk of a tensor into its repacked buffer: n_blocks GGUF Q8_0
+ * blocks (34 bytes each, host memory) that are blocks first_block.. of the
+ * tensor, repacked and written to their two regions of `buf` (quants at
+ * 32 first_block, scales at 32 N + 2 first_block, N from the buffer's mark).
+ * Synchronous with respect to `src`. Replaces one chunk of
+ * subeReordenadoPorTrozos (repack.js:318-345). EFF_E_MARK for an unmarked
+ * buffer, EFF_E_BOUNDS for blocks past the tensor. */
+int eff_buf_write_r(eff_ctx *ctx, eff_buf *buf, int type_r, uint32_t first_block, const void *src,
+                    uint32_t n_blocks);
+
 /* ---- host data preparation ---------------------------------------------- */
 
 /* Quantize n floats (n a multiple of the block) into GGUF blocks. Q8_0 follows

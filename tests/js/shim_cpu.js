@@ -46,4 +46,49 @@ assert.deepStrictEqual(Array.from(new Int8Array(q.buffer, 2, 6)), [127, 3, -2, 1
 // deterministic generator
 const a = eff.fillNormal(5, 0.02, 1000), b = eff.fillNormal(5, 0.02, 10);
 for (let i = 0; i < 10; i++) assert.strictEqual(a[i], b[i]);
-console.log('shim_cpu ok');
+
+// The load path over a recording device (the repacked form needs the
+// library's device buffers and is checked on the GPU): spans, chunks, the
+// 4 bytes of slack, progress, and the errors raised before a byte moves.
+async function cargaCpu() {
+  const file = new Uint8Array(1200);
+  for (let i = 0; i < file.length; i++) file[i] = (i * 7 + 3) & 255;
+  const lecturas = [];
+  const ranged = {
+    size: file.length,
+    slice(off, len) { lecturas.push([off, len]); return Promise.resolve(file.slice(off, off + len).buffer); },
+  };
+  const dev = {
+    limits: { maxStorageBufferBindingSize: 4096 },
+    createBuffer(d) { return { size: d.size, label: d.label, datos: new Uint8Array(d.size) }; },
+    queue: { writeBuffer(b, off, data) { b.datos.set(new Uint8Array(data), off); } },
+  };
+  const t = (name, typeName, dims, start) => ({ name, typeName, dims, nElements: dims.reduce((p, q) => p * q, 1),
+    nBytes: eff.tensorBytes(dims, typeName), start });
+  const tabla = [t('a', 'Q8_0', [64, 2], 0), t('b', 'F32', [3], 136), t('c', 'Q4_K', [256], 160),
+    t('d', 'Q6_K', [256, 4], 304), t('e', 'F16', [5], 1144)];
+  assert.deepStrictEqual(tabla.map((u) => u.nBytes), [136, 12, 144, 840, 10]);
+  const prog = [];
+  const { pesos, stats } = await eff.cargaTensores(dev, ranged, tabla,
+    { tramo: 512, trozo: 300, onProgress: (u, tot, n) => prog.push([u, tot, n]) });
+  // [a b] one span; c after 12 bytes of padding; d larger than a span, in
+  // chunks of 300; e does not fit in d's span
+  assert.deepStrictEqual(lecturas, [[0, 148], [160, 144], [304, 300], [604, 300], [904, 240], [1144, 10]]);
+  assert.strictEqual(stats.tramos, 4);
+  assert.strictEqual(stats.trozos, 6);
+  assert.strictEqual(stats.reordenados, 0);
+  assert.deepStrictEqual(prog[prog.length - 1], [1142, 1142, 'e']);
+  for (const u of tabla) {
+    const { buf, t: d } = pesos.get(u.name);
+    assert.strictEqual(d, u);
+    assert.strictEqual(buf.size, Math.ceil((u.nBytes + 4) / 4) * 4);
+    assert.deepStrictEqual(Array.from(buf.datos.subarray(0, u.nBytes)), Array.from(file.subarray(u.start, u.start + u.nBytes)));
+    assert.ok(buf.datos.subarray(u.nBytes).every((v) => v === 0));
+  }
+  await assert.rejects(eff.cargaTensores(dev, ranged, [t('x', 'Q8_0', [32, 200], 0)], {}), /límite de binding/);
+  await assert.rejects(eff.cargaTensores(dev, ranged, [t('x', 'Q4_0', [32], 0), t('y', 'BF16', [2], 18)], {}),
+    /sin kernel: Q4_0 \(p\.ej\. «x»\), BF16 \(p\.ej\. «y»\)/);
+  assert.deepStrictEqual(eff.comoReordenado(tabla[0], 'Q8_0R'), Object.assign({}, tabla[0], { typeName: 'Q8_0R', typeNameGGUF: 'Q8_0' }));
+}
+
+cargaCpu().then(() => console.log('shim_cpu ok'), (e) => { console.error(e); process.exit(1); });

@@ -7,6 +7,13 @@ const fs = require('fs');
 const path = require('path');
 const eff = require(path.join(__dirname, '..', '..', 'elffuss-engine_amd', 'js', 'index.js'));
 
+// A file of float32 values. readFileSync may return a view into a shared
+// pool for small files, so the copy starts at the view's own offset.
+function leeF32(file) {
+  const b = fs.readFileSync(file);
+  return new Float32Array(b.buffer.slice(b.byteOffset, b.byteOffset + b.length));
+}
+
 async function main() {
   const dir = process.argv[2];
   const meta = JSON.parse(fs.readFileSync(path.join(dir, 'meta.json'), 'utf8'));
@@ -16,7 +23,7 @@ async function main() {
   const rd = async (buf, n) => new Float32Array(await eff.readback(device, buf, 0, n * 4));
   for (const c of meta.cases) {
     const w = fs.readFileSync(path.join(dir, c.w));
-    const x = new Float32Array(fs.readFileSync(path.join(dir, c.x)).buffer.slice(0));
+    const x = leeF32(path.join(dir, c.x));
     let wBuf;
     if (c.type === 'Q8_0R') {
       const n = c.rows * c.k / 32;
@@ -73,7 +80,7 @@ async function main() {
     ops.ctx.recycle();
   }
   // top-k over a logits vector, candidates through createTopKGPU
-  const logits = new Float32Array(fs.readFileSync(path.join(dir, meta.topk.logits)).buffer.slice(0));
+  const logits = leeF32(path.join(dir, meta.topk.logits));
   const lb = ops.upload(logits, 'logits');
   const tk = eff.createTopKGPU(device, ops.ctx);
   const c = await tk.candidatos(lb, 0, logits.length, { M: meta.topk.m, S: Uint32Array.from(meta.topk.S) });
