@@ -19,6 +19,7 @@
 const path = require('path');
 
 const native = require(path.join(__dirname, 'elffuss_amd.node'));
+const muestreo = require(path.join(__dirname, 'muestreo.js'));
 
 const STATUS = { NOT_APPLICABLE: 1, E_INVALID: -1, E_TYPE: -2, E_SHAPE: -3, E_MARK: -4, E_BOUNDS: -5, E_DEVICE: -6 };
 const OPT = { GEMV_MAX_TOKENS: 1, GEMM_MIN_TOKENS: 2, GEMV_KERNEL: 3, SPLIT_CONFIG: 4 };
@@ -522,8 +523,11 @@ function createQuantOps(device, opts) {
 
 // createTopKGPU (ops.topk.js:42-190): candidatos() returns the exact top-M by
 // (value desc, index asc) of one logits vector plus the raw logits of the
-// penalised ids, or null when the device result must not be used.
+// penalised ids, or null when the device result must not be used; muestrea()
+// is the whole step (plan, candidates, sample() on the handful) and returns
+// the token sample() would give over the whole vector, or null.
 const estadisticasTopK = { gpu: 0, respaldo: 0, motivos: {} };
+const ahoraMs = () => (typeof performance !== 'undefined' ? performance.now() : Date.now());
 
 function createTopKGPU(device, ctx) {
   const out = device.createBuffer({ size: native.topkOutBytes(), label: 'topk.out' });
@@ -544,18 +548,27 @@ function createTopKGPU(device, ctx) {
     const r = native.topk(device._ctx, logits._h, base, vocab, plan.M, S, esta, out._h);
     if (r === null) return respaldo('no aplica');
     const u = new Uint32Array(await readback(device, out, 0, out.size));
-    if (u[4] !== esta) return respaldo('serie');
-    if (u[1] !== 0) return respaldo(u[1] & 2 ? 'NaN' : 'no cupo');
-    const n = u[0];
-    const ini = TOPK.CABECERA + TOPK.P_MAX;
-    const ids = new Uint32Array(n), bits = new Uint32Array(n);
-    for (let q = 0; q < n; q++) { ids[q] = u[ini + 2 * q]; bits[q] = u[ini + 2 * q + 1]; }
-    stats.gpu++; estadisticasTopK.gpu++;
-    return { ids, bits, bitsS: u.slice(TOPK.CABECERA, TOPK.CABECERA + S.length) };
+    const c = muestreo.leeSalidaTopK(u, { S }, Math.ceil(vocab / TOPK.POR_TROZO), esta);
+    return c.motivo ? respaldo(c.motivo) : c;
   }
   return {
     stats,
     candidatos,
+    // `opts` as for sample() without `previos`, which comes in two halves
+    // (the prompt and the generated ids). Resolves to { id, msLectura,
+    // msMuestreo }, or null: then the caller reads the whole vector.
+    async muestrea(logits, base, vocab, opts, previosA, previosB) {
+      const t0 = ahoraMs();
+      const plan = muestreo.planTopK(vocab, opts, previosA, previosB);
+      if (!plan) return respaldo('muestreo sin tope');
+      const c = await candidatos(logits, base, vocab, plan);
+      if (!c) return null;
+      const t1 = ahoraMs();
+      const id = muestreo.muestraCandidatos(plan, c.ids, c.bits, c.bitsS, opts);
+      if (id === null) return respaldo('incoherente');
+      stats.gpu++; estadisticasTopK.gpu++;
+      return { id, msLectura: t1 - t0, msMuestreo: ahoraMs() - t1 };
+    },
     destroy() { out.destroy(); },
   };
 }
@@ -567,6 +580,8 @@ module.exports = {
   TIPOS_R, TIPO_R, TIPO_GGUF, bytesReordenado, bytesBufferR, bloquesDeBuffer, escalasDesde,
   reordena, vuelveAlGGUF, marcaBufferR, bloquesR, compruebaBufferR, creaBufferR,
   tensorBytes, comoReordenado, subeReordenadoPorTrozos, cargaTensores,
+  sample: muestreo.sample, topKIndices: muestreo.topKIndices, uniforme: muestreo.uniforme,
+  planTopK: muestreo.planTopK, leeSalidaTopK: muestreo.leeSalidaTopK, muestraCandidatos: muestreo.muestraCandidatos,
   quantize: (type, f32) => native.quantize(quantInfo(type).code, f32),
   fillNormal: (seed, sigma, n) => native.fillNormal(seed, sigma, n),
 };

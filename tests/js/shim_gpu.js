@@ -85,6 +85,28 @@ async function main() {
   const tk = eff.createTopKGPU(device, ops.ctx);
   const c = await tk.candidatos(lb, 0, logits.length, { M: meta.topk.m, S: Uint32Array.from(meta.topk.S) });
   out.topk = { ids: Array.from(c.ids), bits: Array.from(c.bits), bitsS: Array.from(c.bitsS) };
+  // the whole step: plan, device candidates, sample() on the handful, against
+  // sample() over the vector read back
+  const todo = new Float32Array(await eff.readback(device, lb, 0, logits.length * 4));
+  const ajustes = [
+    [{}, [5, 69999, 120], [101, 101]],
+    [{ repeatPenalty: 1 }, [], []],
+    [{ temperature: 0.8, topK: 40, topP: 0.9, minP: 0.05, seed: 7 }, [100, 101, 102], [139]],
+    [{ temperature: 1.3, topK: 150, seed: 12345, presence: 1.5, repeatLastN: 32 }, Array.from({ length: 40 }, (_, i) => 100 + i), [3]],
+    [{ temperature: 0.5, topK: 1, seed: 3, repeatPenalty: 0.7 }, [100, -1, 70000], []],
+  ];
+  out.muestrea = [];
+  for (const [opts, A, B] of ajustes) {
+    for (let paso = 0; paso < 4; paso++) {
+      const o = Object.assign({}, opts, { seed: (opts.seed || 1) + paso });
+      const r = await tk.muestrea(lb, 0, logits.length, o, A, B);
+      const want = eff.sample(Float32Array.from(todo), Object.assign({}, o, { previos: A.concat(B) }));
+      out.muestrea.push({ got: r === null ? null : r.id, want });
+    }
+  }
+  // a temperature without top-k cannot use the handful
+  assert.strictEqual(await tk.muestrea(lb, 0, logits.length, { temperature: 1 }, [], []), null);
+  out.topkStats = tk.stats;
   out.stats = device.stats();
   fs.writeFileSync(path.join(dir, 'out.json'), JSON.stringify(out));
   device.destroy();

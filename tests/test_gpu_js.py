@@ -71,4 +71,10 @@ def test_js_shim_gpu(eff, orc, tmp_path):
     ids, bits, _ = orc.topk(logits.view(np.uint32), 40)
     assert out["topk"]["ids"] == ids.tolist() and out["topk"]["bits"] == bits.tolist()
     assert out["topk"]["bitsS"] == logits.view(np.uint32)[[5, 69999]].tolist()
-    assert out["stats"]["topk"] == 1 and out["stats"]["gemm"] >= 1 and out["stats"]["split"] >= 2
+    # sample() over the device candidates gives the token of sample() over the whole vector
+    assert len(out["muestrea"]) == 20
+    for i, m in enumerate(out["muestrea"]):
+        assert m["got"] is not None and m["got"] == m["want"], (i, m)
+    assert out["topkStats"]["gpu"] == 20 and out["topkStats"]["respaldo"] == 1
+    assert out["topkStats"]["motivos"] == {"muestreo sin tope": 1}
+    assert out["stats"]["topk"] == 21 and out["stats"]["gemm"] >= 1 and out["stats"]["split"] >= 2
