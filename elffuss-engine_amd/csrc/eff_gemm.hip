@@ -1,13 +1,14 @@
-// Prefill GEMM for Q8_0 weights at >= 1024 tokens:
+// Prefill GEMM for Q8_0 weights from 256 tokens:
 //   Y[t][row] = sum_k fp16(W[row][k]) fp16(X[t][k]), fp32 accumulation
 // (the operand roundings of kernels.drift.wgsl.js:65-142 and the f16 tiles of
 // ops.gemm2.js).
 //
-// A workgroup of 4 waves computes a 256-token x 256-row tile; wave (wm, wn)
-// owns tokens 128 wm.. and rows 128 wn.., i.e. 4 x 4 fragments of
-// v_mfma_f32_32x32x16_f16 (256 accumulators). Each fragment operand is read
-// once per k slot and used by 4 MFMAs, which keeps the LDS traffic per MFMA
-// at a level the LDS can sustain (about 128 bytes per clock per CU).
+// A workgroup of 4 waves computes a BM-token x BN-row tile (256 x 256 from
+// 1024 tokens, 128 x 128 below, so that 512 tokens still give 256
+// workgroups); wave w owns every token of the tile and rows BN/4 w.., i.e.
+// BM/32 x BN/128 fragments of v_mfma_f32_32x32x16_f16 (256 accumulators for
+// the large tile). Each A fragment is read once per k slot and used by the
+// wave's BN/128 MFMAs of that slot, and each B fragment by its BM/32.
 //
 // k steps of 64 (two Q8_0 blocks) flow through three LDS stages filled by
 // direct-to-LDS loads (buffer_load ... lds), issued two steps ahead:
@@ -39,25 +40,25 @@ namespace eff {
 
 namespace {
 
-constexpr uint32_t kBN = 256, kBK = 64;   // tile rows, k per step
+constexpr uint32_t kBK = 64;              // k per step
 constexpr uint32_t kRB = 80;              // raw weight bytes per row and stage
-constexpr uint32_t kWS = kBN * kRB;       // weight stage bytes (20 KB)
-constexpr uint32_t kWG = kWS / 1024;      // weight loads per step (64 lanes x 16 bytes each)
-// waves along tokens x along rows (one wave per SIMD); 32 x 32 fragments
-// along rows per wave
-constexpr uint32_t kWM = 1, kWN = 4, kNW = kWM * kWN, kFN = kBN / 32 / kWN;
-constexpr uint32_t kWDma = (kWG + kNW - 1) / kNW;  // weight loads of a wave per step (at most)
-static_assert(kWS % 1024 == 0, "whole loads");
+// waves along tokens x along rows (one wave per SIMD)
+constexpr uint32_t kWM = 1, kWN = 4, kNW = kWM * kWN;
 
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const uint32_t *)p; }
 
-// BM tokens per tile; KS workgroups split k (KS = 2: the two halves are
-// added into y, zeroed beforehand, with atomic adds, which give the same
-// bits in either order: 0 + a + b = a + b).
-template <uint32_t BM, uint32_t KS>
+// BM tokens x BN rows per tile; KS workgroups split k (KS = 2: the two
+// halves are added into y, zeroed beforehand, with atomic adds, which give the
+// same bits in either order: 0 + a + b = a + b).
+template <uint32_t BM, uint32_t BN, uint32_t KS>
 __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Float16 *__restrict__ xh,
                                                  float *__restrict__ y, uint32_t tokens, uint32_t row_tiles,
                                                  uint32_t tok_tiles) {
+  constexpr uint32_t kWS = BN * kRB;                  // weight stage bytes
+  constexpr uint32_t kWG = kWS / 1024;                // weight loads per step (64 lanes x 16 bytes each)
+  constexpr uint32_t kFN = BN / 32 / kWN;             // 32 x 32 fragments along rows per wave
+  constexpr uint32_t kWDma = (kWG + kNW - 1) / kNW;   // weight loads of a wave per step (at most)
+  static_assert(kWS % 1024 == 0 && kFN >= 1, "whole loads");
   constexpr uint32_t kXS = BM * kBK * 2;   // x stage bytes
   constexpr uint32_t kXDma = kXS / 1024 / kNW;  // x loads per wave and step
   static_assert(kXS % (1024 * kNW) == 0, "x loads");
@@ -82,7 +83,7 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
   if (ntiles % 8u == 0u) lin = (blockIdx.x % 8u) * (ntiles / 8u) + blockIdx.x / 8u;
   const uint32_t kq = lin / (row_tiles * tok_tiles);
   lin %= row_tiles * tok_tiles;
-  const uint32_t n0 = (lin / tok_tiles) * kBN, tt = lin % tok_tiles, t0 = tt * BM;
+  const uint32_t n0 = (lin / tok_tiles) * BN, tt = lin % tok_tiles, t0 = tt * BM;
   const uint32_t rows = wv.rows, k = wv.k;
   const uint32_t steps_all = (k + kBK - 1u) / kBK;
   // this workgroup's steps: s0 .. s0 + steps - 1 (absolute step numbers)
@@ -323,15 +324,15 @@ __global__ __launch_bounds__(256) void k_zero(float4 *__restrict__ p, uint64_t n
   if (i < n4) p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
-template <uint32_t BM, uint32_t KS>
+template <uint32_t BM, uint32_t BN, uint32_t KS>
 hipError_t gemm_q8_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
-  const uint32_t tok_tiles = (tokens + BM - 1) / BM, row_tiles = (wv.rows + kBN - 1) / kBN;
+  const uint32_t tok_tiles = (tokens + BM - 1) / BM, row_tiles = (wv.rows + BN - 1) / BN;
   if (KS > 1) {
     // y is zeroed by a kernel (not a memset node) so that graph replays stay exact
     const uint64_t n4 = (uint64_t)tokens * wv.rows / 4u;
     hipLaunchKernelGGL(k_zero, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, s, (float4 *)y, n4);
   }
-  hipLaunchKernelGGL((k_gemm_q8<BM, KS>), dim3(row_tiles * tok_tiles * KS), dim3(kNW * 64), 0, s, wv, xh, y, tokens,
+  hipLaunchKernelGGL((k_gemm_q8<BM, BN, KS>), dim3(row_tiles * tok_tiles * KS), dim3(kNW * 64), 0, s, wv, xh, y, tokens,
                      row_tiles, tok_tiles);
   return hipGetLastError();
 }
@@ -345,10 +346,10 @@ bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows) {
 uint32_t gemm_big_tile_log2(uint32_t tokens) { return tokens >= 1024 ? 8u : 7u; }
 
 hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
-  // >= 1024 tokens: 256-token tiles fill the GPU; below, 128-token tiles
-  // with k split in two
-  if (tokens >= 1024) return gemm_q8_go<256, 1>(wv, xh, y, tokens, s);
-  return gemm_q8_go<128, 1>(wv, xh, y, tokens, s);
+  // >= 1024 tokens: 256 x 256 tiles fill the GPU; below, 128 x 128 tiles
+  // (at 512 tokens: 256 workgroups, where 128 x 256 tiles left half the CUs idle)
+  if (tokens >= 1024) return gemm_q8_go<256, 256, 1>(wv, xh, y, tokens, s);
+  return gemm_q8_go<128, 128, 1>(wv, xh, y, tokens, s);
 }
 
 }  // namespace eff

@@ -169,8 +169,9 @@ def test_q8_0r_gemv_bit_identical_to_q8_0(ctx, eff):
 @pytest.mark.parametrize("tokens", [64, 100, 200, 300, 1100])
 def test_gemm_vs_fp16_oracle(ctx, eff, orc, tname, tokens):
     """Every tile configuration: 128 x 32 (< 256 tokens), 128 x 128 with a
-    k split (>= 256), 256 x 128 (>= 1024; Q6_K stays on 128 x 128); rows and
-    tokens not multiples of the tiles."""
+    k split (>= 256), 256 x 128 (>= 1024; Q6_K stays on 128 x 128); Q8_0 from
+    256 tokens on 128 x 128 tiles (300) and 256 x 256 (1100); rows and tokens
+    not multiples of the tiles."""
     rows, k = 130, 512
     t, data, gguf, n = make_weights(eff, tname, rows, k, 40 + tokens)
     x = eff.fill_normal(2000 + tokens, 1.0, tokens * k)
