@@ -112,8 +112,10 @@ class FusedConfig:
             b.free()
 
 
-def time_steps(torch, ctx, cfg, steps, warmup):
-    """Average ms per step over `steps` graph-replayed steps (after `warmup`)."""
+def time_steps(torch, ctx, cfg, steps, warmup, warm_replays=1, timed=1):
+    """Average ms per step over `steps` graph-replayed steps (after `warmup`
+    eager steps and `warm_replays` untimed replays); with `timed` > 1 the
+    median of that many timed replays."""
     stream = torch.cuda.current_stream()
     ctx.set_stream(stream.cuda_stream)
     for i in range(warmup):
@@ -125,14 +127,18 @@ def time_steps(torch, ctx, cfg, steps, warmup):
         for i in range(steps):
             cfg.step(ctx, i)
     ctx.set_stream(stream.cuda_stream)
-    g.replay()                       # one untimed replay: first-touch of the graph
+    for _ in range(warm_replays):    # untimed replays: first touch of the graph, and warm-up
+        g.replay()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    g.replay()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    times = []
+    for _ in range(timed):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        g.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) / steps)
+    ms = sorted(times)[len(times) // 2]
     del g
     ctx.set_stream(None)
     return ms
@@ -243,7 +249,8 @@ def main():
                 "split-x" if after["split"] > before["split"] else (
                     f"gemv x {groups} token groups" if groups else "gemv"))
             steps = 40 if cfg.gemm else 100
-            t_ms = time_steps(torch, ctx, cfg, steps, 5)
+            # steady state: the first replays over the >= 1 GiB weight rotation run slower
+            t_ms = time_steps(torch, ctx, cfg, steps, 5, warm_replays=3, timed=3)
             gb = cfg.bytes / (t_ms * 1e-3) / 1e9
             tf = cfg.flops / (t_ms * 1e-3) / 1e12
             hbm_t = cfg.bytes / (HBM_PEAK_GBS * 1e9)
@@ -267,7 +274,7 @@ def main():
             res = {}
             for fused in (True, False):
                 cfg = FusedConfig(eff, ctx, tn, rl, k, mode, 900 + len(rl), fused)
-                t_ms = time_steps(torch, ctx, cfg, 100, 5)
+                t_ms = time_steps(torch, ctx, cfg, 100, 5, warm_replays=3, timed=3)
                 res["fused" if fused else "separate"] = t_ms
                 nbytes = cfg.bytes
                 cfg.free()
