@@ -207,7 +207,8 @@ def main():
     ms, gbs = float("nan"), float("nan")
     if not args.no_head:
         head = Config(eff, ctx, "Q4_K", 2048, 8192, 1, 202)
-        ms = time_steps(torch, ctx, head, args.steps, args.warmup)
+        # W eager warm-up steps and three untimed replays of the K captured steps, then one timed replay
+        ms = time_steps(torch, ctx, head, args.steps, args.warmup, warm_replays=3)
         gbs = head.bytes / (ms * 1e-3) / 1e9
         head.free()
 
