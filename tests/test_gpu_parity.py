@@ -464,8 +464,8 @@ def run_topk(ctx, eff, vals, m, base=0, penal=(), serial=7):
     return eff.parse_topk(out.read(np.uint32))
 
 
-@pytest.mark.parametrize("vocab,m", [(1, 1), (100, 40), (4096, 40), (4097, 40), (65536, 40),
-                                     (70000, 192), (10, 40), (200000, 7)])
+@pytest.mark.parametrize("vocab,m", [(1, 1), (100, 40), (4096, 40), (4097, 40), (65536, 40), (65536, 100),
+                                     (65536, 192), (70000, 192), (10, 40), (200000, 7)])
 def test_topk_bit_exact(ctx, eff, orc, vocab, m):
     rng = np.random.default_rng(vocab + m)
     vals = rng.normal(0, 3, vocab).astype(np.float32)
@@ -490,6 +490,30 @@ def test_topk_flags_nan_and_limits(ctx, eff):
         ctx.topk(lb, 0, vals.size, 193)
     with pytest.raises(eff.NotApplicable):
         ctx.topk(lb, 0, vals.size, 40, penal_ids=list(range(129)))
+
+
+@pytest.mark.parametrize("layout", ["periodic", "ascending", "descending", "two_levels"])
+def test_topk_layouts(ctx, eff, orc, layout):
+    """Layouts against the per-thread-maximum threshold of the select: "periodic"
+    puts the large logits on 48 of every 256 positions, so each chunk keeps 768
+    composites above its threshold and takes the radix fallback; sorted inputs
+    put a chunk's largest logits on one stride."""
+    rng = np.random.default_rng(5)
+    vocab, m = 65536, 48
+    j = np.arange(vocab)
+    if layout == "periodic":
+        vals = np.where(j % 256 < 48, 10.0, 0.0) + rng.normal(0, 1, vocab)
+    elif layout == "ascending":
+        vals = j * 1e-3
+    elif layout == "descending":
+        vals = -j * 1e-3
+    else:
+        vals = np.where(rng.random(vocab) < 0.01, 5.0, -5.0)
+    vals = vals.astype(np.float32)
+    r = run_topk(ctx, eff, vals, m)
+    ids, bits, nan = orc.topk(vals.view(np.uint32), m)
+    assert r["n"] == len(ids) and r["flags"] == 0
+    assert np.array_equal(r["ids"], ids) and np.array_equal(r["bits"], bits)
 
 
 def test_topk_all_equal(ctx, eff):
