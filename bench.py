@@ -1,17 +1,25 @@
 """Benchmark of the quantized matrix-product path on one MI355X.
 
-Headline (`value`): BASELINE.json configs[1], Q4_K GEMV N=2048 x K=8192, M=1,
-as algorithmic HBM GB/s = (weight block bytes + x bytes + y bytes) / time per
-step. A step is one GEMV over one batch. Inputs are resident in HBM before the
-timed region; each step reads a different copy of W (copies rotate over more
-than 1 GiB, four times the 256 MB MALL), so no step is served by cache. The
-timed steps are replayed from a HIP graph (torch.cuda.CUDAGraph over the
-library's launches on torch's stream) and bracketed with HIP events on that
-stream.
+Headline (`value`): BASELINE.json configs[3], the largest single-GPU
+configuration: the Q6_K output-projection GEMV N=65536 x K=2048 (M=1) followed
+by the exact top-40 over its logits, as algorithmic HBM GB/s = (weight block
+bytes + x bytes + logits bytes) / time per step. A step is one head GEMV plus
+one top-k over one batch. Inputs are resident in HBM before the timed region.
 
-Also reported: the roofline fraction of the GEMV kernel, the reference CPU
-path timed on this host (oracle restatement, cpu_baseline), and a sweep of
-every BASELINE.json configuration (GB/s or TFLOP/s and roofline fraction).
+Weight rotation: every configuration keeps C distinct copies of W totalling
+>= 1 GiB (four times the 256 MB MALL), step i reads copy i % C, and every
+timed replay of the K captured steps is preceded by an untimed replay of the
+steps that complete the cycle, so every copy is read again only after all C
+copies (>= 1 GiB) have been streamed: no step is served by the MALL, whatever
+K is. The timed steps are replayed from a HIP graph (torch.cuda.CUDAGraph over
+the library's launches on torch's stream) and bracketed with HIP events on
+that stream.
+
+Also reported: the roofline fraction of the dominant kernel (the GEMV, timed
+alone the same way), the reference CPU path timed on this host
+(cpu_baseline: the oracle's restatement of cpu-kernels.js's Q8_0 integer path,
+which runs the Q6_K head requantized to Q8_0), and a sweep of every
+BASELINE.json configuration.
 """
 import argparse
 import json
@@ -28,6 +36,7 @@ import __graft_entry__ as ge  # noqa: E402
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 FP16_PEAK_TFLOPS = 2516.6      # MI355X dense fp16 MFMA (256 CU x 2.4 GHz x 4096 flop/clk)
 ROTATE_BYTES = 1 << 30         # distinct weight bytes cycled through per config
+MALL_BYTES = 256 << 20         # MI355X Infinity Cache
 METRIC = "Q-GEMV HBM GB/s and Q-GEMM TFLOPS, % of MI355X roofline, per quant type"
 
 
@@ -47,6 +56,7 @@ class Config:
         e, _ = eff.geometry(base)
         n = rows * k // e
         data = eff.repack(w, n) if tname == "Q8_0R" else w
+        self.w_bytes = data.nbytes
         self.copies = max(2, min(256, ROTATE_BYTES // data.nbytes + 1))
         self.w = []
         first = ctx.upload(data)
@@ -87,6 +97,7 @@ class FusedConfig:
         self.sets = []
         data = [eff.quantize(tname, eff.fill_normal(seed + i, 0.02, r * k)) for i, r in enumerate(rows_list)]
         per = sum(d.nbytes for d in data)
+        self.w_bytes = per
         self.copies = max(2, min(256, ROTATE_BYTES // per + 1))
         for _ in range(self.copies):
             self.sets.append([ctx.upload(d) for d in data])
@@ -112,26 +123,48 @@ class FusedConfig:
             b.free()
 
 
+def rotation(cfg, steps):
+    """What the timed steps of `cfg` read: copies, bytes, reuse distance."""
+    per = cfg.w_bytes
+    return {"copies": cfg.copies, "bytes_per_copy": per, "reuse_distance_bytes": cfg.copies * per,
+            "distinct_bytes_in_timed_steps": min(steps, cfg.copies) * per}
+
+
 def time_steps(torch, ctx, cfg, steps, warmup, warm_replays=1, timed=1):
     """Average ms per step over `steps` graph-replayed steps (after `warmup`
     eager steps and `warm_replays` untimed replays); with `timed` > 1 the
-    median of that many timed replays."""
+    median of that many timed replays. Each replay of the timed graph is
+    preceded by an untimed graph of the steps that complete the rotation
+    cycle, so that every weight copy is reused only after all of them."""
+    rot = rotation(cfg, steps)
+    assert rot["reuse_distance_bytes"] >= 2 * MALL_BYTES, rot
     stream = torch.cuda.current_stream()
     ctx.set_stream(stream.cuda_stream)
     for i in range(warmup):
         cfg.step(ctx, i)
     torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
+    pad = (-steps) % cfg.copies
+    g, gpad = torch.cuda.CUDAGraph(), None
     with torch.cuda.graph(g):
         ctx.set_stream(torch.cuda.current_stream().cuda_stream)
         for i in range(steps):
             cfg.step(ctx, i)
+    if pad:
+        gpad = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gpad):
+            ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+            for i in range(steps, steps + pad):
+                cfg.step(ctx, i)
     ctx.set_stream(stream.cuda_stream)
     for _ in range(warm_replays):    # untimed replays: first touch of the graph, and warm-up
+        if gpad is not None:
+            gpad.replay()
         g.replay()
     torch.cuda.synchronize()
     times = []
     for _ in range(timed):
+        if gpad is not None:
+            gpad.replay()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
         g.replay()
@@ -139,44 +172,111 @@ def time_steps(torch, ctx, cfg, steps, warmup, warm_replays=1, timed=1):
         torch.cuda.synchronize()
         times.append(start.elapsed_time(end) / steps)
     ms = sorted(times)[len(times) // 2]
-    del g
+    del g, gpad
     ctx.set_stream(None)
     return ms
 
 
-def cpu_baseline(eff, orc, tname, rows, k, seconds):
-    """The reference CPU path restated (oracle): Q8_0 via quantized activations
-    and integer dots, other types via f32 dequantize-and-dot, pool of threads
-    claiming row chunks. Threads: the reference policy min(8, cores/2)
-    (cpu.js:107-113) and all cores."""
-    base = "Q8_0" if tname == "Q8_0R" else tname
-    w = eff.quantize(base, eff.fill_normal(7, 0.02, rows * k))
-    x = eff.fill_normal(8, 1.0, k)
-    cores = os.cpu_count() or 1
+def cpu_model():
     try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
         pass
-    res = {}
-    for label, threads in (("reference_policy", max(1, min(8, cores // 2))), ("all_cores", cores)):
-        orc.cpu_matmul(orc.NAMES[base], w, rows, k, x, 1, threads)   # warm-up
-        n, t0 = 0, time.perf_counter()
-        while True:
-            orc.cpu_matmul(orc.NAMES[base], w, rows, k, x, 1, threads)
-            n += 1
-            dt = time.perf_counter() - t0
-            if dt >= seconds / 2:
-                break
-        res[label] = (threads, n, dt)
-    bytes_ = alg_bytes(eff, tname, rows, k, 1)
-    th, n, dt = res["reference_policy"]
-    th2, n2, dt2 = res["all_cores"]
-    kind_note = ("integer-dot path of cpu-kernels.js (Q8 activations), restated"
-                 if base == "Q8_0" else
-                 "f32 dequantize-and-dot restatement (the reference CPU path has no kernel for this type)")
-    return {"value": round(bytes_ * n / dt / 1e9, 3), "unit": "GB/s", "cores": th, "kind": "port",
-            "sample": f"{n} full {tname} GEMVs N={rows} K={k} M=1 in {dt:.1f} s with {th} threads; {kind_note}",
-            "all_cores": {"value": round(bytes_ * n2 / dt2 / 1e9, 3), "cores": th2}}
+    return "unknown"
+
+
+def host_cores():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def time_cpu(fn, seconds):
+    """(runs, seconds) of fn() repeated for about `seconds` after one warm-up."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            return n, dt
+
+
+def cpu_baseline(eff, orc, seconds):
+    """The reference CPU path (cpu-kernels.js driven by cpu-trabajo.js) as the
+    oracle restates it: x quantized to 8-bit blocks, integer dots against Q8_0
+    blocks, a pool of threads claiming row chunks (cpu.js:140-216, 350-381).
+    Threads: the reference policy min(8, cores/2) (cpu.js:107-113), and all
+    cores of this process (at most 16, the box's share of one GPU).
+
+    Headline leg (C4): the reference's CPU path has no Q6_K kernel and runs a
+    tied Q6_K head requantized to Q8_0 at load (cpu.js:268-287), so one step is
+    the 65536 x 2048 Q8_0 matvec over the requantized head plus the exact
+    top-40 of its logits; `value` is the headline's algorithmic bytes per
+    second of that step, so that it reads beside the GPU's `value`.
+    Sweep legs: C1 (Q8_0 GEMV 8192 x 2048) and C3 M=512 (Q8_0 8192 x 2048 x 512)."""
+    cores = host_cores()
+    pol = max(1, min(8, cores // 2))
+    allc = max(1, min(16, cores))
+    rows, k = 65536, 2048
+    q6 = eff.quantize("Q6_K", eff.fill_normal(404, 0.02, rows * k))
+    head = orc.quantize_q8_0(orc.dequant(orc.Q6_K, q6, rows * k // 256))   # load-time requantization
+    x = eff.fill_normal(405, 1.0, k)
+
+    def head_step(threads):
+        def f():
+            y = orc.cpu_matmul(orc.Q8_0, head, rows, k, x, 1, threads)
+            orc.topk(y.view(np.uint32).ravel(), 40)
+        return f
+
+    head_bytes = alg_bytes(eff, "Q6_K", rows, k, 1)
+    n, dt = time_cpu(head_step(pol), seconds * 0.4)
+    n2, dt2 = time_cpu(head_step(allc), seconds * 0.15)
+    out = {"value": round(head_bytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": pol, "kind": "port",
+           "sample": (f"{n} steps of the C4 head on the reference CPU path in {dt:.1f} s with {pol} threads: "
+                      f"65536x2048 Q8_0 matvec over the head requantized from Q6_K (cpu.js:268-287) with "
+                      f"8-bit x blocks and integer dots (cpu.js:350-381), plus the exact top-40; value = the "
+                      f"headline's {head_bytes} algorithmic bytes per step / step time; "
+                      f"{1e3 * dt / n:.2f} ms per step"),
+           "ms_per_step": round(1e3 * dt / n, 3),
+           "all_cores": {"value": round(head_bytes * n2 / dt2 / 1e9, 3), "cores": allc,
+                         "ms_per_step": round(1e3 * dt2 / n2, 3)},
+           "cpu_model": cpu_model(), "host_cores": cores}
+    sweep = {}
+    for tag, r, kk, m, sec in (("C1 Q8_0 N=8192 K=2048 M=1", 8192, 2048, 1, seconds * 0.15),
+                               ("C3 Q8_0 N=8192 K=2048 M=512", 8192, 2048, 512, seconds * 0.3)):
+        w = eff.quantize("Q8_0", eff.fill_normal(7, 0.02, r * kk))
+        xs = eff.fill_normal(8, 1.0, m * kk)
+        n, dt = time_cpu(lambda: orc.cpu_matmul(orc.Q8_0, w, r, kk, xs, m, pol), sec)
+        ms = 1e3 * dt / n
+        e = {"ms": round(ms, 3), "threads": pol}
+        if m == 1:
+            e["GB/s"] = round(alg_bytes(eff, "Q8_0", r, kk, 1) / (ms * 1e-3) / 1e9, 3)
+        else:
+            e["TFLOP/s"] = round(2.0 * r * kk * m / (ms * 1e-3) / 1e12, 4)
+        sweep[tag] = e
+    out["sweep"] = sweep
+    return out
+
+
+def js_chain():
+    """Wall time per operation of a Node-driven decode chain through the N-API
+    addon (elffuss-engine_amd/js/bench_cadena.js), or None without node."""
+    import shutil
+    import subprocess
+    node = shutil.which("node")
+    if not node:
+        return None
+    r = subprocess.run([node, os.path.join(ROOT, "elffuss-engine_amd", "js", "bench_cadena.js"), "200", "30"],
+                       capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        return {"error": (r.stderr or r.stdout)[-300:]}
+    return json.loads(r.stdout.strip().splitlines()[-1])
 
 
 def main():
@@ -186,7 +286,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-js", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--only", default="", help="run only sweep entries whose name contains this text")
     ap.add_argument("--no-head", action="store_true", help="skip the headline measurement")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -194,7 +295,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path is single-GPU by design (got --gpus {args.gpus}); "
-              "the sharding design is described in DESIGN.md", file=sys.stderr)
+              "how it would shard over several GPUs is described in DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -203,14 +304,23 @@ def main():
     ctx = eff.Context(0)
     torch.cuda.init()
 
-    # Headline: configs[1]
-    ms, gbs = float("nan"), float("nan")
+    # Headline: configs[3], the Q6_K head GEMV + top-40 (the largest single-GPU configuration)
+    rows, k = 65536, 2048
+    ms = ms_gemv = gbs = gemv_gbs = float("nan")
+    rot = None
     if not args.no_head:
-        head = Config(eff, ctx, "Q4_K", 2048, 8192, 1, 202)
+        head = Config(eff, ctx, "Q6_K", rows, k, 1, 404, topk=40)
         # W eager warm-up steps and three untimed replays of the K captured steps, then one timed replay
         ms = time_steps(torch, ctx, head, args.steps, args.warmup, warm_replays=3)
+        rot = rotation(head, args.steps)
         gbs = head.bytes / (ms * 1e-3) / 1e9
+        # the dominant kernel alone (same weights and rotation): the GEMV's time per launch
+        head.topk = 0
+        ms_gemv = time_steps(torch, ctx, head, args.steps, args.warmup, warm_replays=3)
+        gemv_gbs = head.bytes / (ms_gemv * 1e-3) / 1e9
         head.free()
+        print(f"# headline: {ms * 1e3:.2f} us per step ({gbs:.1f} GB/s), GEMV alone {ms_gemv * 1e3:.2f} us",
+              file=sys.stderr, flush=True)
 
     if args.copy_probe:
         nbytes = args.copy_probe << 20
@@ -225,7 +335,7 @@ def main():
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("q4_k_gemv_2048x8192", {}).get("hbm_bytes_per_dispatch")
+            traffic = json.load(f).get("q6_k_gemv_65536x2048", {}).get("hbm_bytes_per_dispatch")
 
     sweep = {}
     if not args.no_sweep:
@@ -236,11 +346,11 @@ def main():
         for tn in ("Q2_K", "IQ2_XXS"):
             for m in (1, 8, 32, 128):
                 plan.append(("C5", tn, 8192, 2048, m, 0))
-        for tag, tn, rows, k, m, tk in plan:
-            key = f"{tag} {tn} N={rows} K={k} M={m}" + (" +top40" if tk else "")
+        for tag, tn, r, kk, m, tk in plan:
+            key = f"{tag} {tn} N={r} K={kk} M={m}" + (" +top40" if tk else "")
             if args.only and args.only not in key:
                 continue
-            cfg = Config(eff, ctx, tn, rows, k, m, 300 + rows + m, topk=tk)
+            cfg = Config(eff, ctx, tn, r, kk, m, 300 + r + m, topk=tk)
             # the router's choice for this shape, from its launch counters
             before = ctx.stats()
             cfg.step(ctx, 0)
@@ -250,7 +360,7 @@ def main():
                 "split-x" if after["split"] > before["split"] else (
                     f"gemv x {groups} token groups" if groups else "gemv"))
             steps = 40 if cfg.gemm else 100
-            # steady state: the first replays over the >= 1 GiB weight rotation run slower
+            # steady state: the median of three timed replays after three untimed ones
             t_ms = time_steps(torch, ctx, cfg, steps, 5, warm_replays=3, timed=3)
             gb = cfg.bytes / (t_ms * 1e-3) / 1e9
             tf = cfg.flops / (t_ms * 1e-3) / 1e12
@@ -260,7 +370,7 @@ def main():
             sweep[key] = {"us": round(t_ms * 1e3, 2), "GB/s": round(gb, 1), "TFLOP/s": round(tf, 2),
                           "bound": bound,
                           "roofline_frac": round((mfma_t if bound == "mfma" else hbm_t) / (t_ms * 1e-3), 4),
-                          "path": path}
+                          "path": path, "reuse_distance_MB": round(rotation(cfg, steps)["reuse_distance_bytes"] / 1e6)}
             cfg.free()
             print(f"# {key}: {sweep[key]}", file=sys.stderr, flush=True)
 
@@ -268,13 +378,13 @@ def main():
     if not args.no_sweep:
         fplan = [("F1 gate+up", "Q4_K", [8192, 8192], 2048, eff.GEMV_SWIGLU),
                  ("F1 sections q+k+v", "Q4_K", [2048, 512, 512], 2048, eff.GEMV_SECTIONS)]
-        for tag, tn, rl, k, mode in fplan:
-            key = f"{tag} {tn} rows={'+'.join(map(str, rl))} K={k} M=1"
+        for tag, tn, rl, kk, mode in fplan:
+            key = f"{tag} {tn} rows={'+'.join(map(str, rl))} K={kk} M=1"
             if args.only and args.only not in key:
                 continue
             res = {}
             for fused in (True, False):
-                cfg = FusedConfig(eff, ctx, tn, rl, k, mode, 900 + len(rl), fused)
+                cfg = FusedConfig(eff, ctx, tn, rl, kk, mode, 900 + len(rl), fused)
                 t_ms = time_steps(torch, ctx, cfg, 100, 5, warm_replays=3, timed=3)
                 res["fused" if fused else "separate"] = t_ms
                 nbytes = cfg.bytes
@@ -285,21 +395,31 @@ def main():
                           "path": "fused gemv"}
             print(f"# {key}: {sweep[key]}", file=sys.stderr, flush=True)
 
+    chain = None
+    if not args.no_js and not args.only:
+        chain = js_chain()
+        print(f"# js chain: {chain}", file=sys.stderr, flush=True)
+
     base = None
     if not args.no_cpu:
-        orc = ge.oracle()
-        base = cpu_baseline(eff, orc, "Q4_K", 2048, 8192, args.cpu_seconds)
+        base = cpu_baseline(eff, ge.oracle(), args.cpu_seconds)
 
     line = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic (weights N(0,0.02) quantized to Q4_K, x N(0,1), fixed seeds)",
-        "config": {"workload": "configs[1]: Q4_K GEMV N=2048 x K=8192, M=1 (decode)", "rows": 2048, "k": 8192,
-                   "tokens": 1, "weight_copies_rotated": ">= 1 GiB"},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "dtype": "int8 MFMA (Q6_K weights as int8; x as 3 int8 digit planes = 22 bits per 32-value group; "
+                 "int32 sums, f32 scales); top-k on u32 keys",
+        "data": "synthetic (weights N(0,0.02) quantized to Q6_K, x N(0,1), fixed seeds)",
+        "config": {"workload": "configs[3]: Q6_K output-projection GEMV N=65536 x K=2048, M=1, + exact top-40 "
+                               "of the logits (decode head)",
+                   "rows": rows, "k": k, "tokens": 1, "top_k": 40, "weight_rotation": rot,
+                   "gemv_alone_ms_per_step": round(ms_gemv, 5)},
+        "roofline": {"bound": "hbm", "kernel": "k_gemv_mx (Q6_K, 1 token)", "achieved": round(gemv_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic},
         "cpu_baseline": base,
+        "js_chain": chain,
         "sweep": sweep,
     }
     ctx.close()

@@ -6,7 +6,10 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <deque>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/elffuss_amd.h"
 #include "eff_formats.h"
@@ -34,6 +37,31 @@ struct eff_ctx {
   void *sx_scratch = nullptr;       // x as fp16 hi/lo parts for the split-x product
   size_t sx_scratch_bytes = 0;
   int64_t sx_config = 0;
+  // Pinned staging ring of eff_buf_write: the source bytes are copied here on
+  // the calling thread and the device copy is enqueued from here, so a write
+  // returns without waiting for the device. `pend` holds the ring ranges whose
+  // copies may still be in flight, oldest first, with the event after each.
+  struct Pend {
+    size_t a, b;
+    hipEvent_t ev;
+  };
+  uint8_t *stage = nullptr;
+  size_t stage_head = 0;
+  std::deque<Pend> stage_pend;
+  std::vector<hipEvent_t> events;   // recorded and completed, ready for reuse
+  // Pinned blocks of finished reads (eff_read_begin / eff_read_end), reused.
+  std::mutex read_mu;
+  std::vector<std::pair<void *, size_t>> read_blocks;
+};
+
+// An enqueued device -> host read (eff_read_begin).
+struct eff_read {
+  eff_ctx *ctx = nullptr;
+  void *host = nullptr;   // pinned block of `cap` bytes
+  size_t cap = 0, n = 0;
+  hipEvent_t ev = nullptr;
+  int rc = EFF_OK;
+  std::string error;
 };
 
 struct eff_buf {
@@ -120,6 +148,10 @@ int weight_view(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint
 
 int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens);
 
+// Types whose prefill the router sends to the fp16 GEMM: those the
+// reference's fp16 GEMMs accept (GEMM2_TIPOS, kernels.gemm2.wgsl.js:51).
+bool router_gemm_type(int type) { return type == EFF_TYPE_Q8_0 || type == EFF_TYPE_Q8_0R; }
+
 int run_gemv(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
   if (ctx->gemv_kernel == 0 && sx_applies(wv, tokens)) return run_sx(ctx, wv, x, y, tokens);
   GemvPlan p;
@@ -161,11 +193,68 @@ int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_
   return EFF_OK;
 }
 
-int run_gemm(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
-  int rc = grow(ctx, &ctx->xh_scratch, &ctx->xh_scratch_bytes, gemm_x_bytes(wv.type, tokens, wv.k, wv.rows), "gemm x");
+int run_gemm(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens, uint32_t plan) {
+  int rc = grow(ctx, &ctx->xh_scratch, &ctx->xh_scratch_bytes, gemm_x_bytes(wv.type, tokens, plan, wv.k, wv.rows),
+                "gemm x");
   if (rc) return rc;
-  hipError_t e = launch_gemm(wv, x, y, tokens, ctx->xh_scratch, ctx->stream);
+  hipError_t e = launch_gemm(wv, x, y, tokens, plan, ctx->xh_scratch, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
+  return EFF_OK;
+}
+
+// Writes of at most this many bytes go through the staging ring and return
+// without waiting; the ring holds twice as much.
+constexpr size_t kStageMaxWrite = (size_t)4 << 20;
+constexpr size_t kStageBytes = 2 * kStageMaxWrite;
+
+int take_event(eff_ctx *ctx, hipEvent_t *ev) {
+  if (!ctx->events.empty()) {
+    *ev = ctx->events.back();
+    ctx->events.pop_back();
+    return EFF_OK;
+  }
+  EFF_HIP(ctx, hipEventCreateWithFlags(ev, hipEventDisableTiming));
+  return EFF_OK;
+}
+
+// A range of `n` bytes of the staging ring whose earlier copies have ended.
+int stage_reserve(eff_ctx *ctx, size_t n, uint8_t **out) {
+  if (!ctx->stage) {
+    void *p = nullptr;
+    if (hipHostMalloc(&p, kStageBytes, hipHostMallocDefault) != hipSuccess)
+      return fail(ctx, EFF_E_NOMEM, "pinned staging of %zu bytes", kStageBytes);
+    ctx->stage = (uint8_t *)p;
+    ctx->stage_head = 0;
+  }
+  // retire the copies that have ended (oldest first)
+  while (!ctx->stage_pend.empty() && hipEventQuery(ctx->stage_pend.front().ev) == hipSuccess) {
+    ctx->events.push_back(ctx->stage_pend.front().ev);
+    ctx->stage_pend.pop_front();
+  }
+  size_t a = ctx->stage_head;
+  if (a + n > kStageBytes) a = 0;
+  const size_t b = a + n;
+  for (auto it = ctx->stage_pend.begin(); it != ctx->stage_pend.end();) {
+    if (it->a < b && a < it->b) {
+      EFF_HIP(ctx, hipEventSynchronize(it->ev));
+      ctx->events.push_back(it->ev);
+      it = ctx->stage_pend.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  ctx->stage_head = b;
+  *out = ctx->stage + a;
+  return EFF_OK;
+}
+
+// Record the end of the copy just enqueued from stage[a, a + n).
+int stage_commit(eff_ctx *ctx, size_t a, size_t n) {
+  hipEvent_t ev;
+  int rc = take_event(ctx, &ev);
+  if (rc) return rc;
+  EFF_HIP(ctx, hipEventRecord(ev, ctx->stream));
+  ctx->stage_pend.push_back({a, a + n, ev});
   return EFF_OK;
 }
 
@@ -196,6 +285,10 @@ int eff_shutdown(eff_ctx *ctx) {
   if (ctx->topk_scratch) (void)hipFree(ctx->topk_scratch);
   if (ctx->xh_scratch) (void)hipFree(ctx->xh_scratch);
   if (ctx->sx_scratch) (void)hipFree(ctx->sx_scratch);
+  for (auto &p : ctx->stage_pend) (void)hipEventDestroy(p.ev);
+  for (hipEvent_t ev : ctx->events) (void)hipEventDestroy(ev);
+  if (ctx->stage) (void)hipHostFree(ctx->stage);
+  for (auto &b : ctx->read_blocks) (void)hipHostFree(b.first);
   if (ctx->own) (void)hipStreamDestroy(ctx->own);
   delete ctx;
   return EFF_OK;
@@ -256,7 +349,9 @@ int eff_buf_alloc(eff_ctx *ctx, size_t bytes, eff_buf **out) {
   if (rc) return rc;
   void *p = nullptr;
   if (hipMalloc(&p, bytes + kSlack) != hipSuccess) return fail(ctx, EFF_E_NOMEM, "hipMalloc of %zu bytes failed", bytes + kSlack);
-  if (hipMemsetAsync(p, 0, bytes + kSlack, ctx->stream) != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess) {
+  // The clear is ordered on the context's stream: every later operation on
+  // that stream sees zeros, and the host does not wait.
+  if (hipMemsetAsync(p, 0, bytes + kSlack, ctx->stream) != hipSuccess) {
     (void)hipFree(p);
     return fail(ctx, EFF_E_DEVICE, "clearing a new buffer failed");
   }
@@ -298,10 +393,23 @@ int eff_buf_write(eff_ctx *ctx, eff_buf *buf, size_t off, const void *src, size_
   if (!n) return EFF_OK;
   int rc = use_device(ctx);
   if (rc) return rc;
-  // Synchronous with respect to `src`: the host memory may be reused on return.
-  EFF_HIP(ctx, hipMemcpyAsync((char *)buf->ptr + off, src, n, hipMemcpyHostToDevice, ctx->stream));
-  EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  return EFF_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  EFF_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(ctx, EFF_E_INVALID, "write: host data cannot be written into a stream under graph capture");
+  char *dst = (char *)buf->ptr + off;
+  if (n > kStageMaxWrite) {
+    // Large uploads (weights at load time): the copy is waited for, so `src`
+    // may be reused on return.
+    EFF_HIP(ctx, hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, ctx->stream));
+    EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return EFF_OK;
+  }
+  uint8_t *st = nullptr;
+  if ((rc = stage_reserve(ctx, n, &st))) return rc;
+  memcpy(st, src, n);
+  EFF_HIP(ctx, hipMemcpyAsync(dst, st, n, hipMemcpyHostToDevice, ctx->stream));
+  return stage_commit(ctx, (size_t)(st - ctx->stage), n);
 }
 
 int eff_buf_read(eff_ctx *ctx, eff_buf *buf, size_t off, void *dst, size_t n) {
@@ -311,6 +419,74 @@ int eff_buf_read(eff_ctx *ctx, eff_buf *buf, size_t off, void *dst, size_t n) {
   if (rc) return rc;
   if (n) EFF_HIP(ctx, hipMemcpyAsync(dst, (const char *)buf->ptr + off, n, hipMemcpyDeviceToHost, ctx->stream));
   EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return EFF_OK;
+}
+
+int eff_read_begin(eff_ctx *ctx, eff_buf *buf, size_t off, size_t n, eff_read **out) {
+  if (!ctx || !buf || !out) return EFF_E_INVALID;
+  *out = nullptr;
+  if (off > buf->size || n > buf->size - off) return fail(ctx, EFF_E_BOUNDS, "read of %zu bytes at %zu past a %zu-byte buffer", n, off, buf->size);
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  eff_read *r = new eff_read();
+  r->ctx = ctx;
+  r->n = n;
+  {
+    std::lock_guard<std::mutex> lk(ctx->read_mu);
+    for (size_t i = 0; i < ctx->read_blocks.size(); ++i) {
+      if (ctx->read_blocks[i].second >= n) {
+        r->host = ctx->read_blocks[i].first;
+        r->cap = ctx->read_blocks[i].second;
+        ctx->read_blocks.erase(ctx->read_blocks.begin() + i);
+        break;
+      }
+    }
+  }
+  if (!r->host) {
+    r->cap = n < 65536 ? 65536 : n;
+    if (hipHostMalloc(&r->host, r->cap, hipHostMallocDefault) != hipSuccess) {
+      delete r;
+      return fail(ctx, EFF_E_NOMEM, "pinned read block of %zu bytes", n);
+    }
+  }
+  hipError_t e = hipEventCreateWithFlags(&r->ev, hipEventDisableTiming);
+  if (e == hipSuccess && n) e = hipMemcpyAsync(r->host, (const char *)buf->ptr + off, n, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipEventRecord(r->ev, ctx->stream);
+  if (e != hipSuccess) {
+    eff_read_release(r);
+    return hip_fail(ctx, e, "read begin");
+  }
+  *out = r;
+  return EFF_OK;
+}
+
+int eff_read_end(eff_read *r, void *dst) {
+  if (!r || (!dst && r->n)) return EFF_E_INVALID;
+  hipError_t e = hipSetDevice(r->ctx->device);
+  if (e == hipSuccess) e = hipEventSynchronize(r->ev);
+  if (e != hipSuccess) {
+    r->rc = EFF_E_DEVICE;
+    r->error = std::string("read: ") + hipGetErrorString(e);
+    return r->rc;
+  }
+  if (r->n) memcpy(dst, r->host, r->n);
+  return EFF_OK;
+}
+
+const char *eff_read_error(const eff_read *r) { return r ? r->error.c_str() : "no read"; }
+
+int eff_read_release(eff_read *r) {
+  if (!r) return EFF_E_INVALID;
+  (void)hipSetDevice(r->ctx->device);
+  if (r->ev) {
+    (void)hipEventSynchronize(r->ev);
+    (void)hipEventDestroy(r->ev);
+  }
+  if (r->host) {
+    std::lock_guard<std::mutex> lk(r->ctx->read_mu);
+    r->ctx->read_blocks.push_back({r->host, r->cap});
+  }
+  delete r;
   return EFF_OK;
 }
 
@@ -424,7 +600,25 @@ int eff_qgemm(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32
   int rc = weight_view(ctx, type, w, x, y, rows, k, tokens, wv, "gemm");
   if (rc) return rc;
   if ((rc = use_device(ctx))) return rc;
-  rc = run_gemm(ctx, wv, (const float *)x->ptr, (float *)y->ptr, tokens);
+  rc = run_gemm(ctx, wv, (const float *)x->ptr, (float *)y->ptr, tokens, tokens);
+  if (!rc) ++ctx->stats.gemm;
+  return rc;
+}
+
+int eff_qgemm_planned(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k,
+                      uint32_t tokens, uint32_t plan_tokens) {
+  if (!ctx) return EFF_E_INVALID;
+  if (plan_tokens == 0 || (int64_t)plan_tokens < ctx->gemm_min_tokens) {
+    ++ctx->stats.not_applicable;
+    return EFF_NOT_APPLICABLE;
+  }
+  if (tokens > plan_tokens)
+    return fail(ctx, EFF_E_INVALID, "gemm planned: %u tokens under the plan of %u", tokens, plan_tokens);
+  WeightView wv;
+  int rc = weight_view(ctx, type, w, x, y, rows, k, tokens, wv, "gemm planned");
+  if (rc) return rc;
+  if ((rc = use_device(ctx))) return rc;
+  rc = run_gemm(ctx, wv, (const float *)x->ptr, (float *)y->ptr, tokens, plan_tokens);
   if (!rc) ++ctx->stats.gemm;
   return rc;
 }
@@ -446,8 +640,12 @@ int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint
   // and GEMM2 read Q8_0/Q4_0 only) and runs its f32 kernel at every token
   // count; so does this router, on the split-x matrix cores.
   if (ctx->gemv_kernel == 0 && sx_applies(wv, tokens)) return run_sx(ctx, wv, xp, yp, tokens);
-  if ((int64_t)tokens >= ctx->gemm_min_tokens) {
-    rc = run_gemm(ctx, wv, xp, yp, tokens);
+  // The fp16 GEMM is the reference's DRIFT/GEMM2 semantics, which exist for
+  // Q8_0 (and Q4_0) only (kernels.drift.wgsl.js:33, kernels.gemm2.wgsl.js:51);
+  // Q6_K prefill stays on its f32 path there (ops.js:117-128), and here on the
+  // token-group GEMV below at every token count.
+  if ((int64_t)tokens >= ctx->gemm_min_tokens && router_gemm_type(type)) {
+    rc = run_gemm(ctx, wv, xp, yp, tokens, tokens);
     if (!rc) ++ctx->stats.gemm;
     return rc;
   }

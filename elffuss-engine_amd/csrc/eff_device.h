@@ -77,23 +77,24 @@ __device__ __forceinline__ float h2f(uint32_t h) {
 // soffset) into LDS at lds + 4 * lane or lds + 16 * lane. Written as inline
 // assembly so that the compiler, which cannot tell a stage being filled from
 // one being read, adds no vmcnt(0) before LDS reads; callers wait explicitly
-// (wait_vm) before reading what they loaded.
+// (wait_vm) before reading what they loaded. The LDS address goes in through
+// an m0 operand constraint, so the compiler itself sets m0 for the load.
 __device__ __forceinline__ void dma16(rsrc_t r, const uint8_t *lds, uint32_t voff, uint32_t soff) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
   const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
                :
-               : "s"(m0), "v"(voff), "s"(r), "s"(so)
-               : "memory", "m0");
+               : "v"(voff), "s"(r), "s"(so), "{m0}"(m0)
+               : "memory");
 }
 
 __device__ __forceinline__ void dma4(rsrc_t r, const uint8_t *lds, uint32_t voff, uint32_t soff) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
   const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+  asm volatile("buffer_load_dword %0, %1, %2 offen lds"
                :
-               : "s"(m0), "v"(voff), "s"(r), "s"(so)
-               : "memory", "m0");
+               : "v"(voff), "s"(r), "s"(so), "{m0}"(m0)
+               : "memory");
 }
 
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).

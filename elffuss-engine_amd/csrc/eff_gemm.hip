@@ -345,10 +345,11 @@ bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows) {
 
 uint32_t gemm_big_tile_log2(uint32_t tokens) { return tokens >= 1024 ? 8u : 7u; }
 
-hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
+hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
+                           hipStream_t s) {
   // >= 1024 tokens: 256 x 256 tiles fill the GPU; below, 128 x 128 tiles
   // (at 512 tokens: 256 workgroups, where 128 x 256 tiles left half the CUs idle)
-  if (tokens >= 1024) return gemm_q8_go<256, 256, 1>(wv, xh, y, tokens, s);
+  if (plan >= 1024) return gemm_q8_go<256, 256, 1>(wv, xh, y, tokens, s);
   return gemm_q8_go<128, 128, 1>(wv, xh, y, tokens, s);
 }
 

@@ -1281,54 +1281,60 @@ static hipError_t gemm_cfg(const WeightView &wv, const _Float16 *xh, float *y, u
 // spread them over the CUs).
 static bool gemm_wide(int type, uint32_t tokens) { return type != Q6_K && tokens >= 1024; }
 
+// The configuration is chosen by `plan` (the token count of the batch the
+// plan is made for) and run over `tokens` <= plan tokens: each output row
+// depends only on its x row and W, summed in the configuration's order, so a
+// run over fewer tokens gives the bits the same rows get in the whole batch.
 template <int TYPE>
-static hipError_t gemm_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
+static hipError_t gemm_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
+                          hipStream_t s) {
   if constexpr (TYPE != Q6_K) {
-    if (gemm_wide(TYPE, tokens)) return gemm_cfg<TYPE, 256, 128, 64, 2, 2, 1>(wv, xh, y, tokens, s);
+    if (gemm_wide(TYPE, plan)) return gemm_cfg<TYPE, 256, 128, 64, 2, 2, 1>(wv, xh, y, tokens, s);
   }
-  if (tokens >= 256) return gemm_cfg<TYPE, 128, 128, 128, 2, 1, 2>(wv, xh, y, tokens, s);
+  if (plan >= 256) return gemm_cfg<TYPE, 128, 128, 128, 2, 1, 2>(wv, xh, y, tokens, s);
   return gemm_cfg<TYPE, 128, 32, 128, 1, 1, 4>(wv, xh, y, tokens, s);
 }
 
 // Token tile and k step of the chosen configuration (log2), as the x layout needs them.
-static void gemm_x_tile(int type, uint32_t tokens, uint32_t k, uint32_t rows, uint32_t &bm_log2,
+static void gemm_x_tile(int type, uint32_t plan, uint32_t k, uint32_t rows, uint32_t &bm_log2,
                         uint32_t &bk_log2) {
-  if (gemm_big_applies(type, tokens, k, rows)) {
-    bm_log2 = gemm_big_tile_log2(tokens);
+  if (gemm_big_applies(type, plan, k, rows)) {
+    bm_log2 = gemm_big_tile_log2(plan);
     bk_log2 = 6;
-  } else if (gemm_wide(type, tokens)) {
+  } else if (gemm_wide(type, plan)) {
     bm_log2 = 8; bk_log2 = 6;
   } else {
     bm_log2 = 7; bk_log2 = 7;
   }
 }
 
-size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t k, uint32_t rows) {
+size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows) {
   uint32_t bm, bk;
-  gemm_x_tile(type, tokens, k, rows, bm, bk);
+  gemm_x_tile(type, plan, k, rows, bm, bk);
   const uint64_t tiles = (tokens + (1u << bm) - 1) >> bm, steps = (k + (1u << bk) - 1) >> bk;
   return (size_t)(tiles * steps) << (bm + bk + 1);
 }
 
-hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *xh_scratch,
-                       hipStream_t s) {
+hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint32_t plan,
+                       void *xh_scratch, hipStream_t s) {
+  if (plan < tokens) return hipErrorInvalidValue;
   uint32_t bm, bk;
-  gemm_x_tile(wv.type, tokens, wv.k, wv.rows, bm, bk);
+  gemm_x_tile(wv.type, plan, wv.k, wv.rows, bm, bk);
   const uint32_t steps = (wv.k + (1u << bk) - 1) >> bk;
-  const uint64_t n8 = (uint64_t)gemm_x_bytes(wv.type, tokens, wv.k, wv.rows) / 16u;
+  const uint64_t n8 = (uint64_t)gemm_x_bytes(wv.type, tokens, plan, wv.k, wv.rows) / 16u;
   _Float16 *xh = (_Float16 *)xh_scratch;
   hipLaunchKernelGGL(k_x_to_f16, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, s, x, xh, tokens, wv.k, bm, bk,
                      steps, n8);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (gemm_big_applies(wv.type, tokens, wv.k, wv.rows)) return launch_gemm_big(wv, xh, y, tokens, s);
+  if (gemm_big_applies(wv.type, plan, wv.k, wv.rows)) return launch_gemm_big(wv, xh, y, tokens, plan, s);
   switch (wv.type) {
-    case Q8_0: return gemm_go<Q8_0>(wv, xh, y, tokens, s);
-    case Q8_0R: return gemm_go<Q8_0R>(wv, xh, y, tokens, s);
-    case Q4_K: return gemm_go<Q4_K>(wv, xh, y, tokens, s);
-    case Q6_K: return gemm_go<Q6_K>(wv, xh, y, tokens, s);
-    case Q2_K: return gemm_go<Q2_K>(wv, xh, y, tokens, s);
-    case IQ2_XXS: return gemm_go<IQ2_XXS>(wv, xh, y, tokens, s);
+    case Q8_0: return gemm_go<Q8_0>(wv, xh, y, tokens, plan, s);
+    case Q8_0R: return gemm_go<Q8_0R>(wv, xh, y, tokens, plan, s);
+    case Q4_K: return gemm_go<Q4_K>(wv, xh, y, tokens, plan, s);
+    case Q6_K: return gemm_go<Q6_K>(wv, xh, y, tokens, plan, s);
+    case Q2_K: return gemm_go<Q2_K>(wv, xh, y, tokens, plan, s);
+    case IQ2_XXS: return gemm_go<IQ2_XXS>(wv, xh, y, tokens, plan, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -77,6 +77,10 @@ def lib():
         "eff_buf_write": ([p, p, sz, p, sz], i32),
         "eff_buf_read": ([p, p, sz, p, sz], i32),
         "eff_buf_copy": ([p, p, sz, p, sz, sz], i32),
+        "eff_read_begin": ([p, p, sz, sz, ctypes.POINTER(p)], i32),
+        "eff_read_end": ([p, p], i32),
+        "eff_read_error": ([p], ctypes.c_char_p),
+        "eff_read_release": ([p], i32),
         "eff_bytes_reordered": ([i32, u32], sz),
         "eff_bytes_buffer_r": ([i32, u32], sz),
         "eff_blocks_from_buffer": ([i32, sz], u32),
@@ -91,6 +95,7 @@ def lib():
         "eff_qmatmul": ([p, i32, p, p, p, u32, u32, u32], i32),
         "eff_qgemv": ([p, i32, p, p, p, u32, u32, u32], i32),
         "eff_qgemm": ([p, i32, p, p, p, u32, u32, u32], i32),
+        "eff_qgemm_planned": ([p, i32, p, p, p, u32, u32, u32, u32], i32),
         "eff_qgemv_multi": ([p, i32, i32, u32, ctypes.POINTER(p), p, ctypes.POINTER(p), ctypes.POINTER(u32), u32, u32],
                             i32),
         "eff_dequant": ([p, i32, p, p, u32], i32),
@@ -110,9 +115,10 @@ def lib():
 EXPORTED = ("eff_type_from_name eff_type_name eff_type_geometry eff_init eff_shutdown eff_last_error "
             "eff_stream eff_set_stream eff_sync eff_set_option eff_get_stats eff_buf_alloc eff_buf_wrap "
             "eff_buf_free eff_buf_size eff_buf_device_ptr eff_buf_write eff_buf_read eff_buf_copy "
+            "eff_read_begin eff_read_end eff_read_error eff_read_release "
             "eff_bytes_reordered eff_bytes_buffer_r eff_blocks_from_buffer eff_scales_from eff_buf_mark_r "
             "eff_buf_blocks_r eff_buf_write_r eff_repack eff_unrepack eff_quantize eff_fill_normal eff_qmatmul eff_qgemv "
-            "eff_qgemm eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_out_bytes").split()
+            "eff_qgemm eff_qgemm_planned eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_out_bytes").split()
 
 
 def type_code(t):
@@ -306,6 +312,29 @@ class Context:
 
     def qgemm(self, t, w, x, y, rows, k, tokens):
         self._check(lib().eff_qgemm(self.h, type_code(t), w.handle, x.handle, y.handle, rows, k, tokens))
+
+    def qgemm_planned(self, t, w, x, y, rows, k, tokens, plan_tokens):
+        """The GEMM over `tokens` rows of x with the configuration of a `plan_tokens` batch."""
+        self._check(lib().eff_qgemm_planned(self.h, type_code(t), w.handle, x.handle, y.handle, rows, k, tokens,
+                                            plan_tokens))
+
+    def read_async(self, buf, dtype=np.uint8, count=None, offset=0):
+        """Enqueue a readback now; returns a callable that waits and gives the array."""
+        dt = np.dtype(dtype)
+        n = (buf.size - offset) // dt.itemsize if count is None else count
+        r = ctypes.c_void_p()
+        self._check(lib().eff_read_begin(self.h, buf.handle, offset, n * dt.itemsize, ctypes.byref(r)))
+
+        def finish():
+            out = np.empty(n, dtype=dt)
+            try:
+                rc = lib().eff_read_end(r, out.ctypes.data)
+                if rc:
+                    raise EffError(rc, lib().eff_read_error(r).decode())
+            finally:
+                lib().eff_read_release(r)
+            return out
+        return finish
 
     def dequant(self, t, w, out, n_blocks):
         self._check(lib().eff_dequant(self.h, type_code(t), w.handle, out.handle, n_blocks))

@@ -317,14 +317,17 @@ napi_value BufRead(napi_env env, napi_callback_info info) {
   return ab;
 }
 
-// Asynchronous read: the blocking copy runs on the libuv pool, the Promise
-// resolves with an ArrayBuffer (the readback of device.js:165-200).
+// Asynchronous read (the readback of device.js:165-200): the device -> host
+// copy is enqueued on the calling thread, so the snapshot holds exactly the
+// work recorded before readback(); a libuv worker only waits for that copy;
+// the Promise resolves with an ArrayBuffer. The ticket owns its pinned
+// memory, and its error message is its own (the context's is not touched
+// from the worker).
 struct ReadWork {
   napi_async_work work;
   napi_deferred deferred;
-  eff_ctx *ctx;
-  eff_buf *buf;
-  size_t off, n;
+  eff_read *ticket;
+  size_t n;
   std::vector<uint8_t> data;
   int rc;
   std::string err;
@@ -333,16 +336,19 @@ struct ReadWork {
 void read_execute(napi_env, void *p) {
   ReadWork *w = (ReadWork *)p;
   w->data.resize(w->n);
-  w->rc = eff_buf_read(w->ctx, w->buf, w->off, w->data.data(), w->n);
-  if (w->rc) w->err = eff_last_error(w->ctx);
+  w->rc = eff_read_end(w->ticket, w->data.data());
+  if (w->rc) w->err = eff_read_error(w->ticket);
 }
 
 void read_complete(napi_env env, napi_status, void *p) {
   ReadWork *w = (ReadWork *)p;
+  eff_read_release(w->ticket);
   if (w->rc) {
-    napi_value m, e;
+    napi_value m, e, c;
     napi_create_string_utf8(env, w->err.c_str(), w->err.size(), &m);
     napi_create_error(env, nullptr, m, &e);
+    napi_create_int32(env, w->rc, &c);
+    napi_set_named_property(env, e, "code", c);
     napi_reject_deferred(env, w->deferred, e);
   } else {
     void *dst;
@@ -358,14 +364,18 @@ void read_complete(napi_env env, napi_status, void *p) {
 napi_value BufReadAsync(napi_env env, napi_callback_info info) {
   napi_value a[4];
   get_args(env, info, 4, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  const size_t n = (size_t)i64(env, a[3]);
+  eff_read *ticket = nullptr;
+  int rc = eff_read_begin(ctx, external<eff_buf>(env, a[1]), (size_t)i64(env, a[2]), n, &ticket);
+  if (rc) return throw_msg(env, ctx ? eff_last_error(ctx) : "readback", rc);
   ReadWork *w = new ReadWork();
-  w->ctx = external<eff_ctx>(env, a[0]);
-  w->buf = external<eff_buf>(env, a[1]);
-  w->off = (size_t)i64(env, a[2]);
-  w->n = (size_t)i64(env, a[3]);
+  w->ticket = ticket;
+  w->n = n;
+  w->rc = 0;
   napi_value promise, name;
   napi_create_promise(env, &w->deferred, &promise);
-  napi_create_string_utf8(env, "eff_buf_read", NAPI_AUTO_LENGTH, &name);
+  napi_create_string_utf8(env, "eff_read_end", NAPI_AUTO_LENGTH, &name);
   napi_create_async_work(env, nullptr, name, read_execute, read_complete, w, &w->work);
   napi_queue_async_work(env, w->work);
   return promise;
@@ -422,6 +432,17 @@ napi_value MatCall(napi_env env, napi_callback_info info, MatFn fn) {
 napi_value QMatmul(napi_env env, napi_callback_info info) { return MatCall(env, info, eff_qmatmul); }
 napi_value QGemv(napi_env env, napi_callback_info info) { return MatCall(env, info, eff_qgemv); }
 napi_value QGemm(napi_env env, napi_callback_info info) { return MatCall(env, info, eff_qgemm); }
+
+// qgemmPlanned(ctx, type, w, x, y, rows, k, tokens, planTokens)
+napi_value QGemmPlanned(napi_env env, napi_callback_info info) {
+  napi_value a[9];
+  get_args(env, info, 9, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  int rc = eff_qgemm_planned(ctx, (int)i64(env, a[1]), external<eff_buf>(env, a[2]), external<eff_buf>(env, a[3]),
+                             external<eff_buf>(env, a[4]), (uint32_t)i64(env, a[5]), (uint32_t)i64(env, a[6]),
+                             (uint32_t)i64(env, a[7], 1), (uint32_t)i64(env, a[8], 1));
+  return status(env, ctx, rc);
+}
 
 // qgemvMulti(ctx, type, mode, [w...], x, [y...], [rows...], k, tokens)
 napi_value QGemvMulti(napi_env env, napi_callback_info info) {
@@ -506,7 +527,7 @@ napi_value Register(napi_env env, napi_value exports) {
       {"init", Init}, {"shutdown", Shutdown}, {"sync", Sync}, {"setOption", SetOption}, {"stats", Stats},
       {"bufAlloc", BufAlloc}, {"bufFree", BufFree}, {"bufWrite", BufWrite}, {"bufRead", BufRead},
       {"bufReadAsync", BufReadAsync}, {"bufSize", BufSize}, {"bufMarkR", BufMarkR}, {"bufBlocksR", BufBlocksR}, {"bufWriteR", BufWriteR},
-      {"qmatmul", QMatmul}, {"qgemv", QGemv}, {"qgemvMulti", QGemvMulti}, {"qgemm", QGemm}, {"dequant", Dequant}, {"gather", Gather}, {"gatherNorm", GatherNorm}, {"topk", TopK},
+      {"qmatmul", QMatmul}, {"qgemv", QGemv}, {"qgemvMulti", QGemvMulti}, {"qgemm", QGemm}, {"qgemmPlanned", QGemmPlanned}, {"dequant", Dequant}, {"gather", Gather}, {"gatherNorm", GatherNorm}, {"topk", TopK},
       {"topkOutBytes", TopKOutBytes},
   };
   for (auto &f : fns) {

@@ -70,6 +70,8 @@ function requestDevice(opts) {
   const ctx = native.init(o.device || 0);
   const device = {
     _ctx: ctx,
+    // the library's defaults (include/elffuss_amd.h); setOption keeps this in step
+    _opts: { 1: 8, 2: 64, 3: 0, 4: 0 },
     features: new Set(['shader-f16']),
     limits: { maxStorageBufferBindingSize: 2 ** 32, maxComputeWorkgroupStorageSize: 163840 },
     createBuffer(desc) {
@@ -96,6 +98,10 @@ function requestDevice(opts) {
     },
     setOption(option, value) {
       native.setOption(ctx, option, value);
+      device._opts[option] = value;
+    },
+    option(option) {
+      return device._opts[option];
     },
     stats() {
       return native.stats(ctx);
@@ -114,21 +120,84 @@ function readback(device, buf, offset, size) {
   return native.bufReadAsync(device._ctx, buf._h, off, n);
 }
 
-// The ops context: allocations live until recycle() (ops.js:233-307).
+// The ops context and its buffer pool (ops.js:233-307). Buffers are lent by
+// size class (bytes rounded up to 256) and live until recycle() (the end of a
+// token) or recycleDesde(marca, ...vivos) (between layers); returned buffers
+// go back to their class and are lent again without touching the device.
+// Reuse is safe without waiting because every operation is enqueued on the
+// one stream, in order: a buffer lent again is written after the operations
+// that read it in its previous life. A class that nobody asked for during more
+// than POZO_RESPIRO tokens is destroyed (ops.js:264-279). Each handout gets a
+// fresh number in `marcaDe` (the reference's marca de reparto): a key for
+// anything derived from a buffer that must not survive its reuse.
+const POZO_RESPIRO = 2;
+
 function createContext(device) {
-  const scratch = [];
-  return {
+  const ctx = {
     device,
-    scratch,
-    alloc(bytes, label) {
-      const b = device.createBuffer({ size: Math.max(4, Math.ceil(bytes / 256) * 256), label });
-      scratch.push(b);
-      return b;
-    },
-    recycle() {
-      for (const b of scratch.splice(0)) b.destroy();
-    },
+    scratch: [],              // { buf, size } lent since the last recycle, in order
+    scratchFree: new Map(),   // size -> [buf]
+    marcaDe: new WeakMap(),
+    picoBytes: 0,
+    vivosBytes: 0,
+    _usoTalla: new Map(),     // size -> last token it was lent in
+    _tokenPozo: 0,
   };
+  let reparto = 0;
+  ctx.alloc = function (bytes, label) {
+    const size = Math.max(4, Math.ceil(bytes / 256) * 256);
+    const free = ctx.scratchFree.get(size);
+    let buf = free && free.pop();
+    if (!buf) buf = device.createBuffer({ size, label });
+    ctx._usoTalla.set(size, ctx._tokenPozo);
+    ctx.marcaDe.set(buf, ++reparto);
+    ctx.scratch.push({ buf, size });
+    ctx.vivosBytes += size;
+    if (ctx.vivosBytes > ctx.picoBytes) ctx.picoBytes = ctx.vivosBytes;
+    return buf;
+  };
+  const devuelve = (e) => {
+    if (!ctx.scratchFree.has(e.size)) ctx.scratchFree.set(e.size, []);
+    ctx.scratchFree.get(e.size).push(e.buf);
+  };
+  // Everything lent goes back to the pool; the model calls it after a token.
+  ctx.recycle = function () {
+    for (const e of ctx.scratch) devuelve(e);
+    ctx.scratch = [];
+    ctx.vivosBytes = 0;
+    ctx._tokenPozo++;
+    for (const [size, lista] of ctx.scratchFree) {
+      const uso = ctx._usoTalla.has(size) ? ctx._usoTalla.get(size) : 0;
+      if (ctx._tokenPozo - uso <= POZO_RESPIRO) continue;
+      for (const b of lista) b.destroy();
+      ctx.scratchFree.delete(size);
+      ctx._usoTalla.delete(size);
+    }
+  };
+  // What was lent from position `marca` of ctx.scratch on goes back, except
+  // the buffers in `vivos` (recycling between layers, ops.js:283-307).
+  ctx.recycleDesde = function (marca, ...vivos) {
+    const guardar = new Set(vivos);
+    const quedan = [];
+    for (let i = marca; i < ctx.scratch.length; i++) {
+      const e = ctx.scratch[i];
+      if (guardar.has(e.buf)) { quedan.push(e); continue; }
+      devuelve(e);
+      ctx.vivosBytes -= e.size;
+    }
+    ctx.scratch.length = marca;
+    for (const e of quedan) ctx.scratch.push(e);
+  };
+  // Destroys every pooled and lent buffer (end of the session).
+  ctx.destroy = function () {
+    for (const e of ctx.scratch) e.buf.destroy();
+    for (const lista of ctx.scratchFree.values()) for (const b of lista) b.destroy();
+    ctx.scratch = [];
+    ctx.scratchFree.clear();
+    ctx._usoTalla.clear();
+    ctx.vivosBytes = 0;
+  };
+  return ctx;
 }
 
 // ---- repacked layout (repack.js, kernels.bloques.wgsl.js) ---------------------
@@ -434,39 +503,53 @@ function createFusionOps(device, deps) {
   };
 }
 
-// createGemm2Ops (ops.gemm2.js:259-303): the prefill GEMM, null when it does not apply.
+// createGemm2Ops (ops.gemm2.js:259-303): the prefill GEMM, null when it does
+// not apply. The plan follows planGemm2 (ops.gemm2.js:82-126): the fp16 GEMM
+// takes Q8_0 and Q8_0R (GEMM2_TIPOS, kernels.gemm2.wgsl.js:51; Q4_0 has no
+// kernel here), k a multiple of 32, tokens >= the DRIFT threshold (the GEMM
+// min option, __ELFFUSS_DRIFT_DESDE, default 64) and rows a multiple of 16.
+const GEMM2_TIPOS = new Set(['Q8_0', 'Q8_0R']);
+
 function createGemm2Ops(ctx) {
   const device = ctx.device;
-  return {
+  const desde = () => device.option(OPT.GEMM_MIN_TOKENS);
+  const ops = {
+    // What this shape would run (null: the caller's usual path).
     plan(type, rows, k, tokens) {
       const i = QUANT_TYPES[type];
-      const min = 64;
-      if (!i || k % 32 !== 0 || !(tokens >= min)) return null;
-      return { via: 'mfma-f16', type, bpr: k / i.blockElems };
+      if (!i || !GEMM2_TIPOS.has(type) || k % 32 !== 0 || !(tokens >= 1)) return null;
+      if (!(tokens >= desde()) || rows % 16 !== 0) return null;
+      return { via: 'mfma-f16', type, bpr: k / i.blockElems, lote: tokens };
     },
     olvida() {},
     matmul(type, wBuf, xBuf, rows, k, tokens) {
+      if (tokens < 4 && tokens < desde()) return Promise.resolve(null);
+      const pl = ops.plan(type, rows, k, tokens);
+      if (!pl) return Promise.resolve(null);
       const i = QUANT_TYPES[type];
-      if (!i) return Promise.resolve(null);
+      if (TIPOS_R.has(type)) compruebaBufferR(type, wBuf, { bloques: rows * pl.bpr }, 'gemm2');
       const y = ctx.alloc(rows * tokens * 4, 'matmul.y');
       const r = native.qgemm(device._ctx, i.code, wBuf._h, xBuf._h, y._h, rows, k, tokens);
       return Promise.resolve(r === null ? null : y);
     },
-    reproducible(type, rows, k, lote) { return this.plan(type, rows, k, lote) !== null; },
-    // The last-layer tail: one token computed with the plan of the whole batch.
+    // The kernel's output for one token depends only on its x row and W,
+    // summed in the order of the batch's configuration, so the tail is
+    // reproducible whenever the batch has a plan.
+    reproducible(type, rows, k, lote) { return ops.plan(type, rows, k, lote) !== null; },
+    // The last-layer tail (ops.gemm2.js:282-303): `x1` is one row, the last
+    // token of a batch of `lote`; computed with the batch's plan (same kernel,
+    // tile and k order), it gives the bits of that token's row in the batch.
     cola(type, wBuf, x1, rows, k, lote) {
-      if (!this.reproducible(type, rows, k, lote)) return Promise.resolve(null);
+      const pl = ops.plan(type, rows, k, lote);
+      if (!pl) return Promise.resolve(null);
       const i = QUANT_TYPES[type];
-      device.setOption(OPT.GEMM_MIN_TOKENS, 1);
-      try {
-        const y = ctx.alloc(rows * 4, 'matmul.y');
-        native.qgemm(device._ctx, i.code, wBuf._h, x1._h, y._h, rows, k, 1);
-        return Promise.resolve(y);
-      } finally {
-        device.setOption(OPT.GEMM_MIN_TOKENS, 64);
-      }
+      if (TIPOS_R.has(type)) compruebaBufferR(type, wBuf, { bloques: rows * pl.bpr }, 'gemm2');
+      const y = ctx.alloc(rows * 4, 'matmul.y');
+      const r = native.qgemmPlanned(device._ctx, i.code, wBuf._h, x1._h, y._h, rows, k, 1, lote);
+      return Promise.resolve(r === null ? null : y);
     },
   };
+  return ops;
 }
 
 // createQuantOps (ops.js:748-1142).
@@ -576,7 +659,7 @@ function createTopKGPU(device, ctx) {
 module.exports = {
   native, STATUS, OPT, GEMV_MODE, TOPK, QUANT_TYPES, quantInfo,
   requestDevice, readback, createContext,
-  createQuantOps, createGemvOps, createGemm2Ops, createFusionOps, createTopKGPU, estadisticasTopK, TIPOS_GATHER_NORMA,
+  createQuantOps, createGemvOps, createGemm2Ops, GEMM2_TIPOS, createFusionOps, createTopKGPU, estadisticasTopK, TIPOS_GATHER_NORMA,
   TIPOS_R, TIPO_R, TIPO_GGUF, bytesReordenado, bytesBufferR, bloquesDeBuffer, escalasDesde,
   reordena, vuelveAlGGUF, marcaBufferR, bloquesR, compruebaBufferR, creaBufferR,
   tensorBytes, comoReordenado, subeReordenadoPorTrozos, cargaTensores,

@@ -69,6 +69,7 @@ extern "C" {
 
 typedef struct eff_ctx eff_ctx;
 typedef struct eff_buf eff_buf;
+typedef struct eff_read eff_read;
 
 /* Dispatch counters: lets a caller assert that a fast path really ran
  * (ops.gemv.js:92-95 `hechos`, ops.topk.js:36-40 `estadisticasTopK`). */
@@ -130,7 +131,9 @@ int eff_get_stats(const eff_ctx *ctx, eff_stats *out);
 
 /* Allocate `bytes` of device memory (plus hidden read slack; the reference's
  * loader leaves 4 bytes after every tensor, model.js:248-254). Contents are
- * zero. Replaces ctx.alloc/createBuffer (ops.js:233-281). */
+ * zero for every later operation on the context's stream: the clear is
+ * enqueued there and the host does not wait. Replaces device.createBuffer
+ * behind the ctx.alloc pool (ops.js:233-281), which the JS host keeps. */
 int eff_buf_alloc(eff_ctx *ctx, size_t bytes, eff_buf **out);
 
 /* Wrap caller-owned device memory of `bytes` bytes (not freed by
@@ -141,12 +144,27 @@ int eff_buf_free(eff_ctx *ctx, eff_buf *buf);
 size_t eff_buf_size(const eff_buf *buf);
 void *eff_buf_device_ptr(const eff_buf *buf);
 
-/* Host -> device, enqueued on the stream (queue.writeBuffer). `src` is copied
- * before return. */
+/* Host -> device, enqueued on the stream (queue.writeBuffer). `src` may be
+ * reused on return: up to 4 MiB it is copied into a pinned staging ring and
+ * the call does not wait for the device (it waits only when the ring range it
+ * needs is still being copied); larger writes wait for their copy. Refused
+ * (EFF_E_INVALID) on a stream under graph capture. */
 int eff_buf_write(eff_ctx *ctx, eff_buf *buf, size_t offset, const void *src, size_t n);
 
 /* Device -> host; waits for prior work (readback, device.js:165-200). */
 int eff_buf_read(eff_ctx *ctx, eff_buf *buf, size_t offset, void *dst, size_t n);
+
+/* The readback split in two (device.js:165-200, mapAsync): eff_read_begin
+ * enqueues the copy of n bytes into pinned host memory on the context's
+ * stream, now, so the snapshot holds exactly the work enqueued before it;
+ * eff_read_end (any thread) waits for that copy and copies the bytes to dst;
+ * eff_read_release frees the ticket. The buffer may be reused by later
+ * operations on the stream right after eff_read_begin. eff_read_end's errors
+ * are described by eff_read_error (the context's message is not touched). */
+int eff_read_begin(eff_ctx *ctx, eff_buf *buf, size_t offset, size_t n, eff_read **out);
+int eff_read_end(eff_read *r, void *dst);
+const char *eff_read_error(const eff_read *r);
+int eff_read_release(eff_read *r);
 
 /* Device -> device copy, enqueued. */
 int eff_buf_copy(eff_ctx *ctx, eff_buf *dst, size_t dst_offset, eff_buf *src,
@@ -212,7 +230,10 @@ int eff_fill_normal(uint32_t seed, float sigma, float *dst, size_t n);
 
 /* Y[tokens][rows] = W (rows x k, quantized) . X[tokens][k]; X and Y are f32.
  * Router of quant.matmul (ops.js:827-1101): tokens <= GEMV max -> GEMV;
- * tokens >= GEMM min -> fp16 MFMA GEMM; in between -> GEMV over token groups.
+ * Q2_K, Q4_K, IQ2_XXS from 4 tokens -> split-x product (f32-accurate);
+ * Q8_0/Q8_0R at tokens >= GEMM min -> fp16 MFMA GEMM (the reference's
+ * DRIFT/GEMM2 types, kernels.drift.wgsl.js:33); otherwise (Q6_K at every
+ * token count, Q8_0 below GEMM min) -> GEMV over token groups, f32-accurate.
  * EFF_E_SHAPE if k % block_elems != 0. */
 int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
                 uint32_t rows, uint32_t k, uint32_t tokens);
@@ -239,6 +260,15 @@ int eff_qgemv_multi(eff_ctx *ctx, int type, int mode, uint32_t n, eff_buf *const
  * EFF_NOT_APPLICABLE when tokens < GEMM min (planGemm2 returning null). */
 int eff_qgemm(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
               uint32_t rows, uint32_t k, uint32_t tokens);
+
+/* The prefill GEMM over `tokens` rows of x with the kernel configuration
+ * eff_qgemm chooses for `plan_tokens` tokens (tokens <= plan_tokens). A row's
+ * output depends only on its x row and W, summed in that configuration's
+ * order, so tokens = 1 with the last x row of a batch gives the bits of the
+ * batch's last output row: gemm2.cola (ops.gemm2.js:282-303).
+ * EFF_NOT_APPLICABLE when plan_tokens < GEMM min. */
+int eff_qgemm_planned(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
+                      uint32_t rows, uint32_t k, uint32_t tokens, uint32_t plan_tokens);
 
 /* Dequantize n_blocks blocks to f32, bit-exact with the reference decoders
  * (quant.dequant, ops.js:813-823; dequantShader, kernels.wgsl.js:903-922). */

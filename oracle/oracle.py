@@ -5,14 +5,17 @@ cpu_baseline leg of bench.py, as the checker. The product never imports it.
 Each function names the reference code it restates in oracle.c.
 """
 import ctypes
+import json
 import os
-import re
 
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
-GRID_INC = os.path.join(os.path.dirname(HERE), "elffuss-engine_amd", "csrc", "iq2xxs_grid.inc")
+# The IQ2_XXS grid as the reference holds it (quant-tables.js:40-105), read
+# from the committed fixture that tests/golden/gen_iq2xxs_grid.py extracts from
+# the reference's text; independent of the product's own table.
+GRID_FIXTURE = os.path.join(os.path.dirname(HERE), "tests", "golden", "iq2xxs_grid.json")
 
 Q8_0, Q2_K, Q4_K, Q6_K, IQ2_XXS, Q8_0R = 8, 10, 12, 14, 16, 264
 GEOMETRY = {Q8_0: (32, 34), Q8_0R: (32, 34), Q2_K: (256, 84), Q4_K: (256, 144),
@@ -24,14 +27,10 @@ _lib = None
 
 def grid_words():
     """The IQ2_XXS grid as 512 u32 words (word 2e = bytes 0..3 of entry e)."""
-    text = open(GRID_INC).read()
-    vals = [int(v, 16) for v in re.findall(r"0x([0-9a-fA-F]{16})ull", text)]
-    assert len(vals) == 256, len(vals)
-    out = np.zeros(512, dtype=np.uint32)
-    for e, v in enumerate(vals):
-        out[2 * e] = v & 0xFFFFFFFF
-        out[2 * e + 1] = v >> 32
-    return out
+    with open(GRID_FIXTURE) as f:
+        words = json.load(f)["words"]
+    assert len(words) == 512, len(words)
+    return np.asarray(words, dtype=np.uint32)
 
 
 def lib():

@@ -91,4 +91,66 @@ async function cargaCpu() {
   assert.deepStrictEqual(eff.comoReordenado(tabla[0], 'Q8_0R'), Object.assign({}, tabla[0], { typeName: 'Q8_0R', typeNameGGUF: 'Q8_0' }));
 }
 
+// The ops-context pool (ops.js:233-307) over a recording device: size classes
+// of 256 bytes, buffers lent again after recycle() without creating or
+// destroying anything, a fresh handout mark each time, recycleDesde keeping
+// the live buffers, and classes idle for more than two tokens destroyed.
+function poolCpu() {
+  const creados = [], destruidos = [];
+  const dev = {
+    createBuffer(d) {
+      const b = { size: d.size, label: d.label, destroy() { destruidos.push(b); } };
+      creados.push(b);
+      return b;
+    },
+  };
+  const ctx = eff.createContext(dev);
+  const a = ctx.alloc(10, 'a'), b = ctx.alloc(256, 'b'), c = ctx.alloc(257, 'c');
+  assert.deepStrictEqual([a.size, b.size, c.size], [256, 256, 512]);
+  assert.notStrictEqual(a, b);
+  assert.strictEqual(ctx.vivosBytes, 1024);
+  const marcaA = ctx.marcaDe.get(a);
+  ctx.recycle();
+  assert.strictEqual(ctx.vivosBytes, 0);
+  assert.strictEqual(ctx.picoBytes, 1024);
+  const a2 = ctx.alloc(200), c2 = ctx.alloc(400);
+  assert.ok(a2 === a || a2 === b);
+  assert.strictEqual(c2, c);
+  assert.notStrictEqual(ctx.marcaDe.get(a2), marcaA);
+  assert.strictEqual(creados.length, 3);
+  // between layers: everything after the mark goes back except the survivors
+  const marca = ctx.scratch.length;
+  const d = ctx.alloc(256), e = ctx.alloc(1000), f = ctx.alloc(256);
+  ctx.recycleDesde(marca, e);
+  assert.deepStrictEqual(ctx.scratch.map((x) => x.buf), [a2, c2, e]);
+  assert.strictEqual(ctx.alloc(256), f);
+  assert.strictEqual(ctx.alloc(256), d);
+  assert.strictEqual(destruidos.length, 0);
+  // a class nobody asks for during more than POZO_RESPIRO tokens is destroyed
+  ctx.recycle();
+  for (let i = 0; i < 3; i++) { ctx.alloc(256); ctx.recycle(); }
+  assert.ok(destruidos.includes(c) && destruidos.includes(e));
+  assert.ok(!destruidos.includes(a) && !destruidos.includes(b));
+  ctx.destroy();
+  assert.strictEqual(new Set(destruidos).size, creados.length);
+}
+
+// gemm2.plan / reproducible (ops.gemm2.js:82-126, 282-303): the fp16 GEMM
+// only for Q8_0 and Q8_0R, k a multiple of 32, tokens from the DRIFT
+// threshold and rows a multiple of 16; null otherwise.
+function gemm2Cpu() {
+  const device = { option: (o) => (o === eff.OPT.GEMM_MIN_TOKENS ? 64 : 8) };
+  const g = eff.createGemm2Ops({ device });
+  assert.ok(g.plan('Q8_0', 4096, 2048, 64));
+  assert.ok(g.plan('Q8_0R', 4096, 2048, 512));
+  for (const [t, rows, k, n] of [['Q8_0', 4096, 2048, 63], ['Q8_0', 4100, 2048, 512], ['Q4_K', 4096, 2048, 512],
+    ['Q6_K', 4096, 2048, 512], ['Q2_K', 4096, 2048, 512], ['IQ2_XXS', 4096, 2048, 512], ['Q4_0', 4096, 2048, 512]]) {
+    assert.strictEqual(g.plan(t, rows, k, n), null, `${t} ${rows} ${k} ${n}`);
+    assert.strictEqual(g.reproducible(t, rows, k, n), false);
+  }
+  assert.strictEqual(g.reproducible('Q8_0', 4096, 2048, 300), true);
+}
+
+poolCpu();
+gemm2Cpu();
 cargaCpu().then(() => console.log('shim_cpu ok'), (e) => { console.error(e); process.exit(1); });

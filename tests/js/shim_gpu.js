@@ -55,7 +55,22 @@ async function main() {
     }
     if (c.tokens >= 64) {
       const ym = await ops.gemm2.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens);
-      out[c.name + ':gemm2'] = Array.from(await rd(ym, c.rows * c.tokens));
+      if (eff.GEMM2_TIPOS.has(c.type)) {
+        out[c.name + ':gemm2'] = Array.from(await rd(ym, c.rows * c.tokens));
+        // the tail: the last token alone with the batch's plan gives its row's bits
+        assert.ok(ops.gemm2.reproducible(c.type, c.rows, c.k, c.tokens));
+        const x1 = ops.upload(x.subarray((c.tokens - 1) * c.k), 'x1');
+        const yc = await ops.gemm2.cola(c.type, wBuf, x1, c.rows, c.k, c.tokens);
+        const cola = new Uint32Array(await eff.readback(device, yc, 0, c.rows * 4));
+        const ult = new Uint32Array(await eff.readback(device, ym, (c.tokens - 1) * c.rows * 4, c.rows * 4));
+        assert.deepStrictEqual(Array.from(cola), Array.from(ult));
+        out[c.name + ':cola'] = true;
+      } else {
+        assert.strictEqual(ym, null);
+        assert.strictEqual(ops.gemm2.plan(c.type, c.rows, c.k, c.tokens), null);
+        assert.strictEqual(ops.gemm2.reproducible(c.type, c.rows, c.k, c.tokens), false);
+        assert.strictEqual(await ops.gemm2.cola(c.type, wBuf, xBuf, c.rows, c.k, c.tokens), null);
+      }
     } else {
       assert.strictEqual(await ops.gemm2.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens), null);
     }
@@ -77,6 +92,11 @@ async function main() {
     const dq = await ops.dequant(c.type, wBuf, nb);
     out[c.name + ':dequant'] = Array.from(new Uint32Array(await eff.readback(device, dq, 0, nb * eff.QUANT_TYPES[c.type].blockElems * 4)));
     assert.throws(() => ops.matmul(c.type, wBuf, xBuf, c.rows, c.k + 1, 1), /múltiplo/);
+    // the pool lends the same buffers again after the token, without new allocations
+    const clases = ops.ctx.scratch.map((e) => e.size);
+    const antes = new Set(ops.ctx.scratch.map((e) => e.buf));
+    ops.ctx.recycle();
+    for (const sz of clases) assert.ok(antes.has(ops.ctx.alloc(sz)));
     ops.ctx.recycle();
   }
   // top-k over a logits vector, candidates through createTopKGPU

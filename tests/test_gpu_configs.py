@@ -1,6 +1,7 @@
 """The BASELINE.json configurations at their full sizes, through the C ABI,
-against the oracle (whole outputs for GEMV, contiguous row slices for the
-large GEMMs) and, for C4, the top-40 of the GPU's own logits bit-exact."""
+against the oracle (whole outputs everywhere; the large products also against
+the oracle's own routines on row slices) and, for C4, the top-40 of the GPU's
+own logits bit-exact."""
 import numpy as np
 import pytest
 
@@ -41,10 +42,29 @@ def test_c2_q4_k_gemv_2048x8192(ctx, eff, orc):
     check_close(y, orc.gemv_f64(orc.Q4_K, gguf, 2048, 8192, x, 1), "C2 Q4_K")
 
 
+def full_f16_ref(orc, ot, gguf, rows, k, x, tokens):
+    """The fp16-rounded oracle over every row: the exact f32 dequantization
+    rounded to fp16 (fp16(d q), the reference's f16 weight tile) times x
+    rounded to fp16, accumulated in f64 (equal to orc.gemm_f16, which
+    tests/test_oracle.py checks)."""
+    w16 = orc.dequant(ot, gguf, rows * k // orc.GEOMETRY[ot][0]).astype(np.float16).astype(np.float64)
+    x16 = np.asarray(x, np.float32).astype(np.float16).astype(np.float64)
+    return x16.reshape(tokens, k) @ w16.reshape(rows, k).T
+
+
+def full_f64_ref(orc, ot, gguf, rows, k, x, tokens):
+    """The f64 oracle over every row: the exact dequantization times f32 x."""
+    w = orc.dequant(ot, gguf, rows * k // orc.GEOMETRY[ot][0]).astype(np.float64)
+    return np.asarray(x, np.float64).reshape(tokens, k) @ w.reshape(rows, k).T
+
+
 @pytest.mark.parametrize("tokens", [512, 2048])
 def test_c3_q8_0_gemm(ctx, eff, orc, tokens):
+    """The whole output (all 8192 rows), against the fp16-rounded oracle; the
+    oracle's own gemm_f16 on two row slices as a cross-check."""
     rows, k = 8192, 2048
     gguf, x, y = run(ctx, eff, "Q8_0", rows, k, tokens, 303)
+    check_close(y, full_f16_ref(orc, orc.Q8_0, gguf, rows, k, x, tokens), f"C3 M={tokens} all rows")
     for r0, r1 in ((0, 96), (rows - 160, rows)):
         ref = orc.gemm_f16(orc.Q8_0, row_slice(eff, "Q8_0", gguf, k, r0, r1), r1 - r0, k, x, tokens)
         check_close(y[:, r0:r1], ref, f"C3 M={tokens} rows {r0}:{r1}")
@@ -76,6 +96,7 @@ def test_c5_low_bit_sweep(ctx, eff, orc, tname, tokens):
     if tokens < 64:
         check_close(y, orc.gemv_f64(ot, gguf, rows, k, x, tokens), f"C5 {tname} M={tokens}")
     else:
+        check_close(y, full_f64_ref(orc, ot, gguf, rows, k, x, tokens), f"C5 {tname} M={tokens} all rows")
         for r0, r1 in ((0, 512), (rows - 512, rows)):
             ref = orc.gemv_f64(ot, row_slice(eff, tname, gguf, k, r0, r1), r1 - r0, k, x, tokens)
             check_close(y[:, r0:r1], ref, f"C5 {tname} M={tokens} rows {r0}:{r1}")

@@ -19,7 +19,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 def test_js_shim_gpu(eff, orc, tmp_path):
     cases = []
     spec = [("q4k_t1", "Q4_K", 96, 2048, 1), ("q8r_t3", "Q8_0R", 64, 1024, 3), ("q6k_t2", "Q6_K", 40, 512, 2),
-            ("iq2_t9", "IQ2_XXS", 48, 512, 9), ("q2k_t64", "Q2_K", 64, 512, 64)]
+            ("iq2_t9", "IQ2_XXS", 48, 512, 9), ("q2k_t64", "Q2_K", 64, 512, 64), ("q6k_t64", "Q6_K", 48, 512, 64),
+            ("q8_t100", "Q8_0", 64, 512, 100), ("q8_t300", "Q8_0", 80, 512, 300), ("q8r_t70", "Q8_0R", 32, 256, 70)]
     data = {}
     for i, (name, t, rows, k, tokens) in enumerate(spec):
         base = "Q8_0" if t == "Q8_0R" else t
@@ -42,8 +43,9 @@ def test_js_shim_gpu(eff, orc, tmp_path):
     out = json.loads((tmp_path / "out.json").read_text())
     for name, (base, w, x, rows, k, tokens) in data.items():
         ot = orc.NAMES[base]
-        # matmul: f32-accurate for the split-x types at every M, fp16 GEMM from 64 tokens otherwise
-        f32 = tokens < 64 or base in ("Q2_K", "Q4_K", "IQ2_XXS")
+        # matmul: f32-accurate below 64 tokens and for every type but Q8_0 at any M; the fp16 GEMM
+        # (the reference's DRIFT/GEMM2 rounding) for Q8_0 and Q8_0R from 64 tokens
+        f32 = tokens < 64 or base != "Q8_0"
         ref = (orc.gemv_f64 if f32 else orc.gemm_f16)(ot, w, rows, k, x, tokens)
         check_close(np.array(out[name], np.float32), ref, f"js matmul {name}")
         if tokens <= 8:
@@ -54,9 +56,10 @@ def test_js_shim_gpu(eff, orc, tmp_path):
             assert np.array_equal(np.array(out[name + ":sec1"], np.float32).view(np.uint32), yg.view(np.uint32))
             want = (yg / (np.float32(1) + np.exp(-yg))) * yg
             assert np.allclose(np.array(out[name + ":gateup"], np.float32), want, rtol=4e-6, atol=0)
-        if tokens >= 64:
+        if tokens >= 64 and base == "Q8_0":
             check_close(np.array(out[name + ":gemm2"], np.float32), orc.gemm_f16(ot, w, rows, k, x, tokens),
                         f"js gemm2 {name}")
+            assert out[name + ":cola"] is True
         e, _ = eff.geometry(base)
         table = orc.dequant(ot, w, rows * k // e)
         assert np.array_equal(np.array(out[name + ":dequant"], np.uint32), table.view(np.uint32))

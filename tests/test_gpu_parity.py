@@ -413,6 +413,72 @@ def test_router_paths_and_stats(ctx, eff, orc):
     assert after["skinny"] - before["skinny"] == 3 and after["gemm"] - before["gemm"] == 1
 
 
+@pytest.mark.parametrize("tokens", [64, 100, 512])
+def test_router_q6_k_prefill_is_f32_accurate(ctx, eff, orc, tokens):
+    """Q6_K prefill through quant.matmul stays f32-accurate (the reference's
+    fp16 GEMMs read Q8_0/Q4_0 only and its Q6_K prefill runs the f32 generic
+    kernel, ops.js:117-128): against the f64 oracle, no fp16 GEMM launched."""
+    rows, k = 1000, 2048
+    t, data, gguf, n = make_weights(eff, "Q6_K", rows, k, 600 + tokens)
+    x = eff.fill_normal(601 + tokens, 1.0, tokens * k)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    before = ctx.stats()
+    ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+    after = ctx.stats()
+    check_close(yb.read(np.float32), orc.gemv_f64(orc.Q6_K, gguf, rows, k, x, tokens), f"matmul Q6_K T={tokens}")
+    assert after["gemm"] == before["gemm"]
+    assert after["skinny"] - before["skinny"] == (tokens + 15) // 16
+    for b in (wb, xb, yb):
+        b.free()
+
+
+@pytest.mark.parametrize("tname,lote", [("Q8_0", 100), ("Q8_0", 300), ("Q8_0", 1100), ("Q8_0R", 300),
+                                        ("Q8_0R", 1100)])
+def test_gemm_planned_tail_gives_the_batch_row_bits(ctx, eff, tname, lote):
+    """gemm2.cola (ops.gemm2.js:282-303): the last token run alone with the
+    batch's plan gives the bits of the batch's last row (128 x 32 tiles at
+    100 tokens, 128 x 128 at 300, 256 x 256 / 256 x 128 at 1100); the first
+    token too, and a run over the first 3 tokens."""
+    rows, k = 272, 1024
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 700 + lote)
+    x = eff.fill_normal(701 + lote, 1.0, lote * k)
+    wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x), ctx.alloc(lote * rows * 4)
+    ctx.qgemm(t, wb, xb, yb, rows, k, lote)
+    y = yb.read(np.uint32).reshape(lote, rows)
+    x1, y1, y3 = ctx.upload(x[(lote - 1) * k:]), ctx.alloc(rows * 4), ctx.alloc(3 * rows * 4)
+    ctx.qgemm_planned(t, wb, x1, y1, rows, k, 1, lote)
+    assert np.array_equal(y1.read(np.uint32), y[lote - 1])
+    ctx.qgemm_planned(t, wb, xb, y3, rows, k, 3, lote)
+    assert np.array_equal(y3.read(np.uint32).reshape(3, rows), y[:3])
+    with pytest.raises(eff.NotApplicable):
+        ctx.qgemm_planned(t, wb, x1, y1, rows, k, 1, 63)
+    with pytest.raises(eff.EffError):
+        ctx.qgemm_planned(t, wb, xb, yb, rows, k, lote + 1, lote)
+    for b in (wb, xb, yb, x1, y1, y3):
+        b.free()
+
+
+def test_read_ticket_snapshots_at_begin(ctx, eff):
+    """eff_read_begin enqueues the copy at once: a write enqueued after it is
+    not in the snapshot; the buffer can be reused right away."""
+    a = np.arange(4096, dtype=np.uint32)
+    b = ctx.upload(a)
+    fin = ctx.read_async(b, np.uint32)
+    b.write(a[::-1].copy())
+    assert np.array_equal(fin(), a)
+    assert np.array_equal(b.read(np.uint32), a[::-1])
+    # 600 writes of 16 KiB go through the 8 MiB staging ring (wrapping once);
+    # each lands in order
+    c = ctx.alloc(4 * 16384)
+    for i in range(600):
+        c.write(np.full(4096, i, np.uint32), offset=16384 * (i % 4))
+    got = c.read(np.uint32).reshape(4, 4096)
+    for j in range(4):
+        assert np.all(got[j] == 596 + j)
+    b.free()
+    c.free()
+
+
 def test_not_applicable_and_errors(ctx, eff):
     rows, k = 8, 256
     t, data, gguf, n = make_weights(eff, "Q4_K", rows, k, 1)

@@ -8,10 +8,17 @@ oracle function is pinned here by something independent of its own formula:
   * closed-form special blocks (unit scales, zero mins) with known answers;
   * the reference's second statement of the Q8_0/Q6_K decoders (cpu.js:45-80);
   * known answers stated in the reference's comments (repack.js:225-229,
-    kernels.bloques.wgsl.js:128-135, kernels.wgsl.js:381-384).
+    kernels.bloques.wgsl.js:128-135, kernels.wgsl.js:381-384);
+  * the IQ2_XXS grid fixture extracted from the reference's text
+    (tests/golden/iq2xxs_grid.json, quant-tables.js:40-105), which the oracle
+    loads and the product's own table is compared with.
 """
+import os
+
 import numpy as np
 import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 RNG = np.random.default_rng(1234)
 
@@ -58,6 +65,18 @@ def test_grid_invariants(orc):
     assert counts == {8: 1127, 25: 556, 43: 365}
     # first entries of ggml's iq2xxs_grid
     assert entries[0] == 0x0808080808080808 and entries[1] == 0x080808080808082B
+
+
+def test_product_grid_equals_the_reference_fixture(orc):
+    """The product's table (csrc/iq2xxs_grid.inc, 256 u64) holds exactly the
+    words of the reference's IQ2XXS_GRID (the fixture extracted from
+    quant-tables.js:40-105), entry by entry and in order."""
+    import re
+    inc = os.path.join(ROOT, "elffuss-engine_amd", "csrc", "iq2xxs_grid.inc")
+    vals = [int(v, 16) for v in re.findall(r"0x([0-9a-fA-F]{16})ull", open(inc).read())]
+    g = orc.grid_words()
+    assert len(vals) == 256
+    assert vals == [int(g[2 * e]) | (int(g[2 * e + 1]) << 32) for e in range(256)]
 
 
 # ---- block encoders (encode side of the GGUF layouts) ------------------------
