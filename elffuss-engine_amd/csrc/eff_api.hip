@@ -17,6 +17,25 @@
 
 using namespace eff;
 
+// Scratch of eff_topk_noalloc: the top-k chunk candidates of one call of at
+// most kNoAllocMaxVocab logits, in a fixed device array. Every GPU the library
+// runs on holds its own copy until the process ends. Host code never uses the
+// array's name as an address: eff_init looks up each device's copy once, with
+// that device current (hipGetSymbolAddress), and the entry point passes that
+// pointer. The kernels write every scratch word before they read it, so no
+// call needs it cleared; calls that overlap on one GPU share it and race.
+static constexpr uint32_t kNoAllocMaxVocab = 262144;
+static constexpr size_t kNoAllocBytes = eff::topk_scratch_bytes_for(kNoAllocMaxVocab);
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];        // per device: the address of its `scratch`
+hipError_t g_scratch_err[kMaxDevices];   // per device: the lookup's result, once done
+bool g_scratch_done[kMaxDevices];
+}  // namespace
+
 // Bytes allocated past every eff_buf_alloc request. Kernels read at most 4
 // bytes past a block (the reference's loader slack, model.js:248-254).
 static constexpr size_t kSlack = 256;
@@ -274,6 +293,17 @@ int eff_init(int device, eff_ctx **out) {
     return EFF_E_DEVICE;
   }
   ctx->stream = ctx->own;
+  if (device < kMaxDevices) {
+    // once per device, with the device current: the address of its copy of
+    // the no-alloc scratch (a lookup, not an allocation)
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_done[device]) {
+      void *p = nullptr;
+      g_scratch_err[device] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      g_scratch_ptr[device] = g_scratch_err[device] == hipSuccess ? p : nullptr;
+      g_scratch_done[device] = true;
+    }
+  }
   *out = ctx;
   return EFF_OK;
 }
@@ -692,6 +722,8 @@ int eff_dequant(eff_ctx *ctx, int type, eff_buf *w, eff_buf *out, uint32_t n_blo
   return EFF_OK;
 }
 
+}  // extern "C"
+
 namespace {
 
 // Shared checks of the gather entry points (quant.gather, ops.js:1104-1110).
@@ -725,6 +757,23 @@ int gather_view(eff_ctx *ctx, int type, eff_buf *w, eff_buf *ids, uint32_t dim, 
   return EFF_OK;
 }
 
+// The checks of the top-k entry points (createTopKGPU().candidatos,
+// ops.topk.js:99-165): outside the limits the reference falls back to a full
+// readback (ops.topk.js:104-105, topk.js:114-117), i.e. NOT_APPLICABLE here.
+int topk_check(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint32_t m, const uint32_t *penal_ids,
+               uint32_t n_penal, eff_buf *out, const char *who) {
+  if (!logits || !out) return fail(ctx, EFF_E_INVALID, "%s: null buffer", who);
+  if (n_penal && !penal_ids) return fail(ctx, EFF_E_INVALID, "%s: null penalised ids", who);
+  if (vocab == 0 || vocab >= EFF_TOPK_N_MAX || m == 0 || m > EFF_TOPK_M_MAX || n_penal > EFF_TOPK_P_MAX) {
+    ++ctx->stats.not_applicable;
+    return EFF_NOT_APPLICABLE;
+  }
+  if (((uint64_t)base + vocab) * 4 > logits->size) return fail(ctx, EFF_E_BOUNDS, "%s: logits buffer too small", who);
+  if (out->size < eff_topk_out_bytes())
+    return fail(ctx, EFF_E_BOUNDS, "%s: output buffer needs %zu bytes", who, eff_topk_out_bytes());
+  return EFF_OK;
+}
+
 int check_out(eff_ctx *ctx, eff_buf *b, uint64_t bytes, const char *who) {
   if (!b) return fail(ctx, EFF_E_INVALID, "%s: null buffer", who);
   if (bytes > b->size)
@@ -735,6 +784,8 @@ int check_out(eff_ctx *ctx, eff_buf *b, uint64_t bytes, const char *who) {
 }
 
 }  // namespace
+
+extern "C" {
 
 int eff_gather(eff_ctx *ctx, int type, eff_buf *w, eff_buf *ids, eff_buf *out, uint32_t dim, uint32_t tokens) {
   if (!ctx) return EFF_E_INVALID;
@@ -776,17 +827,9 @@ size_t eff_topk_out_bytes(void) { return sizeof(uint32_t) * (EFF_TOPK_HEADER + E
 int eff_topk(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint32_t m, const uint32_t *penal_ids,
              uint32_t n_penal, uint32_t serial, eff_buf *out) {
   if (!ctx) return EFF_E_INVALID;
-  if (!logits || !out) return fail(ctx, EFF_E_INVALID, "topk: null buffer");
-  if (n_penal && !penal_ids) return fail(ctx, EFF_E_INVALID, "topk: null penalised ids");
-  // Outside these limits the reference falls back to a full readback (ops.topk.js:104-105, topk.js:114-117).
-  if (vocab == 0 || vocab >= EFF_TOPK_N_MAX || m == 0 || m > EFF_TOPK_M_MAX || n_penal > EFF_TOPK_P_MAX) {
-    ++ctx->stats.not_applicable;
-    return EFF_NOT_APPLICABLE;
-  }
-  if (((uint64_t)base + vocab) * 4 > logits->size) return fail(ctx, EFF_E_BOUNDS, "topk: logits buffer too small");
-  if (out->size < eff_topk_out_bytes()) return fail(ctx, EFF_E_BOUNDS, "topk: output buffer needs %zu bytes", eff_topk_out_bytes());
-  int rc = use_device(ctx);
+  int rc = topk_check(ctx, logits, base, vocab, m, penal_ids, n_penal, out, "topk");
   if (rc) return rc;
+  if ((rc = use_device(ctx))) return rc;
   size_t need = topk_scratch_bytes(vocab);
   if (need > ctx->topk_scratch_bytes) {
     if (ctx->topk_scratch) {
@@ -801,6 +844,26 @@ int eff_topk(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint3
   hipError_t e = launch_topk((const uint32_t *)logits->ptr, base, vocab, m, penal_ids, n_penal, serial,
                              (uint32_t *)ctx->topk_scratch, (uint32_t *)out->ptr, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "topk launch");
+  ++ctx->stats.topk;
+  return EFF_OK;
+}
+
+int eff_topk_noalloc(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint32_t m,
+                     const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, eff_buf *out) {
+  if (!ctx) return EFF_E_INVALID;
+  int rc = topk_check(ctx, logits, base, vocab, m, penal_ids, n_penal, out, "topk noalloc");
+  if (rc) return rc;
+  if (vocab > kNoAllocMaxVocab)
+    return fail(ctx, EFF_E_BOUNDS, "topk noalloc: a vocabulary of %u logits is above the %u its fixed scratch holds "
+                "(eff_topk has no such limit)", vocab, kNoAllocMaxVocab);
+  if (ctx->device >= kMaxDevices || !g_scratch_done[ctx->device])
+    return fail(ctx, EFF_E_DEVICE, "topk noalloc: the fixed scratch of device %d was not looked up", ctx->device);
+  if (!g_scratch_ptr[ctx->device])
+    return hip_fail(ctx, g_scratch_err[ctx->device], "topk noalloc: hipGetSymbolAddress of the fixed scratch");
+  if ((rc = use_device(ctx))) return rc;
+  hipError_t e = launch_topk((const uint32_t *)logits->ptr, base, vocab, m, penal_ids, n_penal, serial,
+                             (uint32_t *)g_scratch_ptr[ctx->device], (uint32_t *)out->ptr, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "topk noalloc launch");
   ++ctx->stats.topk;
   return EFF_OK;
 }

@@ -92,6 +92,10 @@ hipError_t launch_dequant(const WeightView &wv, uint32_t n_blocks, float *out, h
 // Top-k scratch: per chunk 2 u32 (count, flags) + 2 * kTopkChunkCap u32 (id, bits).
 constexpr uint32_t kTopkChunk = 4096;     // logits per chunk workgroup
 constexpr uint32_t kTopkChunkCap = 256;   // candidates kept per chunk (>= M max)
+constexpr size_t topk_scratch_bytes_for(uint32_t vocab) {
+  return sizeof(uint32_t) * ((size_t)2 * ((vocab + kTopkChunk - 1) / kTopkChunk) +
+                             (size_t)2 * ((vocab + kTopkChunk - 1) / kTopkChunk) * kTopkChunkCap);
+}
 size_t topk_scratch_bytes(uint32_t vocab);
 
 hipError_t launch_topk(const uint32_t *logits, uint32_t base, uint32_t vocab, uint32_t m,

@@ -1405,10 +1405,7 @@ hipError_t launch_gather_norm(const WeightView &wv, const uint32_t *ids, uint32_
   }
 }
 
-size_t topk_scratch_bytes(uint32_t vocab) {
-  uint32_t chunks = (vocab + kTopkChunk - 1) / kTopkChunk;
-  return sizeof(uint32_t) * ((size_t)2 * chunks + (size_t)2 * chunks * kTopkChunkCap);
-}
+size_t topk_scratch_bytes(uint32_t vocab) { return topk_scratch_bytes_for(vocab); }
 
 hipError_t launch_topk(const uint32_t *logits, uint32_t base, uint32_t vocab, uint32_t m,
                        const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, uint32_t *scratch,

@@ -23,6 +23,7 @@ TYPES = {"Q8_0": Q8_0, "Q2_K": Q2_K, "Q4_K": Q4_K, "Q6_K": Q6_K, "IQ2_XXS": IQ2_
 OPT_GEMV_MAX_TOKENS, OPT_GEMM_MIN_TOKENS, OPT_GEMV_KERNEL, OPT_SPLIT_CONFIG = 1, 2, 3, 4
 GEMV_SECTIONS, GEMV_SWIGLU = 1, 2
 TOPK_HEADER, TOPK_P_MAX, TOPK_CAP, TOPK_M_MAX = 8, 128, 256, 192
+TOPK_NOALLOC_MAX_VOCAB = 262144
 
 ERRORS = {E_INVALID: "invalid argument", E_TYPE: "unsupported type", E_SHAPE: "shape",
           E_MARK: "repack mark", E_BOUNDS: "bounds", E_DEVICE: "device", E_NOMEM: "out of memory"}
@@ -102,6 +103,7 @@ def lib():
         "eff_gather": ([p, i32, p, p, p, u32, u32], i32),
         "eff_gather_norm": ([p, i32, p, p, p, ctypes.c_float, p, p, u32, u32], i32),
         "eff_topk": ([p, p, u32, u32, u32, p, u32, u32, p], i32),
+        "eff_topk_noalloc": ([p, p, u32, u32, u32, p, u32, u32, p], i32),
         "eff_topk_out_bytes": ([], sz),
     }
     for name, (args, res) in sig.items():
@@ -118,7 +120,7 @@ EXPORTED = ("eff_type_from_name eff_type_name eff_type_geometry eff_init eff_shu
             "eff_read_begin eff_read_end eff_read_error eff_read_release "
             "eff_bytes_reordered eff_bytes_buffer_r eff_blocks_from_buffer eff_scales_from eff_buf_mark_r "
             "eff_buf_blocks_r eff_buf_write_r eff_repack eff_unrepack eff_quantize eff_fill_normal eff_qmatmul eff_qgemv "
-            "eff_qgemm eff_qgemm_planned eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_out_bytes").split()
+            "eff_qgemm eff_qgemm_planned eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_noalloc eff_topk_out_bytes").split()
 
 
 def type_code(t):
@@ -352,6 +354,16 @@ class Context:
             out = self.alloc(lib().eff_topk_out_bytes())
         self._check(lib().eff_topk(self.h, logits.handle, base, vocab, m,
                                    ids.ctypes.data if ids.size else None, ids.size, serial, out.handle))
+        return out
+
+
+    def topk_noalloc(self, logits, base, vocab, m, penal_ids=(), serial=1, out=None):
+        """eff_topk_noalloc: the top-k with the library's fixed scratch (no allocation)."""
+        ids = np.ascontiguousarray(np.asarray(penal_ids, dtype=np.uint32))
+        if out is None:
+            out = self.alloc(lib().eff_topk_out_bytes())
+        self._check(lib().eff_topk_noalloc(self.h, logits.handle, base, vocab, m,
+                                           ids.ctypes.data if ids.size else None, ids.size, serial, out.handle))
         return out
 
 
