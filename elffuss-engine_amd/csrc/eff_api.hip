@@ -17,15 +17,16 @@
 
 using namespace eff;
 
-// Scratch of eff_topk_noalloc: the top-k chunk candidates of one call of at
-// most kNoAllocMaxVocab logits, in a fixed device array. Every GPU the library
-// runs on holds its own copy until the process ends. Host code never uses the
-// array's name as an address: eff_init looks up each device's copy once, with
-// that device current (hipGetSymbolAddress), and the entry point passes that
-// pointer. The kernels write every scratch word before they read it, so no
-// call needs it cleared; calls that overlap on one GPU share it and race.
-static constexpr uint32_t kNoAllocMaxVocab = 262144;
-static constexpr size_t kNoAllocBytes = eff::topk_scratch_bytes_for(kNoAllocMaxVocab);
+// Scratch of eff_topk_noalloc: the top-k group records of one call, in a
+// fixed device array of 64 KiB (the records of the largest vocabulary the
+// top-k accepts). Every GPU the library runs on holds its own copy until the
+// process ends. Host code never uses the array's name as an address: eff_init
+// looks up each device's copy once, with that device current
+// (hipGetSymbolAddress), and the entry point passes that pointer. The first
+// kernel writes every record the second reads, so no call needs the array
+// cleared; calls that overlap on one GPU share it and race.
+static constexpr size_t kNoAllocBytes = eff::kTopkScratchMax;
+static_assert(eff::topk_scratch_bytes_for(EFF_TOPK_N_MAX - 1u) <= kNoAllocBytes, "no-alloc scratch too small");
 static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
 
 namespace {
@@ -853,9 +854,9 @@ int eff_topk_noalloc(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t voca
   if (!ctx) return EFF_E_INVALID;
   int rc = topk_check(ctx, logits, base, vocab, m, penal_ids, n_penal, out, "topk noalloc");
   if (rc) return rc;
-  if (vocab > kNoAllocMaxVocab)
-    return fail(ctx, EFF_E_BOUNDS, "topk noalloc: a vocabulary of %u logits is above the %u its fixed scratch holds "
-                "(eff_topk has no such limit)", vocab, kNoAllocMaxVocab);
+  if (topk_scratch_bytes(vocab) > kNoAllocBytes)
+    return fail(ctx, EFF_E_BOUNDS, "topk noalloc: a vocabulary of %u logits needs %zu scratch bytes and the fixed "
+                "scratch holds %zu", vocab, topk_scratch_bytes(vocab), kNoAllocBytes);
   if (ctx->device >= kMaxDevices || !g_scratch_done[ctx->device])
     return fail(ctx, EFF_E_DEVICE, "topk noalloc: the fixed scratch of device %d was not looked up", ctx->device);
   if (!g_scratch_ptr[ctx->device])

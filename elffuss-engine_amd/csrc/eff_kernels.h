@@ -89,13 +89,20 @@ hipError_t launch_gather_norm(const WeightView &wv, const uint32_t *ids, uint32_
 
 hipError_t launch_dequant(const WeightView &wv, uint32_t n_blocks, float *out, hipStream_t stream);
 
-// Top-k scratch: per chunk 2 u32 (count, flags) + 2 * kTopkChunkCap u32 (id, bits).
-constexpr uint32_t kTopkChunk = 4096;     // logits per chunk workgroup
-constexpr uint32_t kTopkChunkCap = 256;   // candidates kept per chunk (>= M max)
-constexpr size_t topk_scratch_bytes_for(uint32_t vocab) {
-  return sizeof(uint32_t) * ((size_t)2 * ((vocab + kTopkChunk - 1) / kTopkChunk) +
-                             (size_t)2 * ((vocab + kTopkChunk - 1) / kTopkChunk) * kTopkChunkCap);
+// Top-k (eff_topk.hip). The logits are cut into G <= kTopkGroupsMax groups
+// of 256 * ceil(vocab / 65536) consecutive logits; the first kernel writes
+// one kTopkRecordBytes record per group (its 4 largest elements), the second
+// selects from the records. The scratch is G records, at most 16 KiB for
+// any vocabulary.
+constexpr uint32_t kTopkGroupsMax = 256;
+constexpr uint32_t kTopkRecordBytes = 64;
+constexpr uint32_t kTopkRecordChunk = 4096;   // the reference's logits per chunk (header field `chunks`)
+constexpr uint32_t topk_group_size(uint32_t vocab) { return 256u * ((vocab + 65535u) / 65536u); }
+constexpr uint32_t topk_groups(uint32_t vocab) {
+  return (vocab + topk_group_size(vocab) - 1u) / topk_group_size(vocab);
 }
+constexpr size_t topk_scratch_bytes_for(uint32_t vocab) { return (size_t)topk_groups(vocab) * kTopkRecordBytes; }
+constexpr size_t kTopkScratchMax = (size_t)kTopkGroupsMax * kTopkRecordBytes;
 size_t topk_scratch_bytes(uint32_t vocab);
 
 hipError_t launch_topk(const uint32_t *logits, uint32_t base, uint32_t vocab, uint32_t m,

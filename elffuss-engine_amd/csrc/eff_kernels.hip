@@ -920,273 +920,6 @@ __global__ __launch_bounds__(512) void k_gemm(WeightView wv, const _Float16 *__r
 }
 
 // ---------------------------------------------------------------------------
-// Top-k. Order key of an f32 bit pattern: -0 counts as +0, positives get the
-// sign bit set, negatives are inverted, so u32 order = f32 order
-// (kernels.topk.wgsl.js:75-82). Elements are compared by the 64-bit composite
-// (key << 32 | ~index): larger composite = larger value, ties to lower index.
-__device__ __forceinline__ uint32_t order_key(uint32_t bits) {
-  uint32_t b = bits == 0x80000000u ? 0u : bits;
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-__device__ __forceinline__ bool is_nan_bits(uint32_t bits) { return (bits & 0x7FFFFFFFu) > 0x7F800000u; }
-
-struct TopkPenal {
-  uint32_t ids[128];
-};
-
-// Radix select over 64-bit composites with 11-bit digits from the top (six
-// rounds: 11 x 5 + 9 bits). The first digit is the sign, exponent and two
-// mantissa bits of the value, which spreads typical logit distributions over
-// enough bins that the histogram's atomic updates rarely collide. After it,
-// the `need` largest composites among the candidates are exactly those with
-// (c & mask) >= prefix. Every thread of the 256 calls it with its own
-// candidates (vals[0..N), valid flags); hist holds 2048 bins, scan 4 words,
-// st 4 words.
-constexpr int RS_BINS = 2048;
-template <int N>
-__device__ void radix_select(const uint64_t *vals, const bool *valid, uint32_t need, uint32_t *hist,
-                             uint32_t *scan, uint64_t &prefix_out, uint64_t &mask_out, uint32_t *st) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint64_t prefix = 0, mask = 0;
-  // st: [0] still needed, [1] digit, [2] done
-  if (tid == 0) { st[0] = need; st[2] = need == 0u; }
-  __syncthreads();
-  for (int round = 0; round < 6; ++round) {
-    if (st[2]) break;
-    const int width = round < 5 ? 11 : 9, shift = 64 - 11 * round - width;
-    const uint64_t dmask = ((uint64_t)1 << width) - 1u;
-    {
-      const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-      *(uint4 *)(hist + 8 * tid) = z;
-      *(uint4 *)(hist + 8 * tid + 4) = z;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < N; ++e)
-      if (valid[e] && (vals[e] & mask) == prefix) atomicAdd(&hist[(uint32_t)((vals[e] >> shift) & dmask)], 1u);
-    __syncthreads();
-    // thread t owns bins 8t..8t+7; suffix sums of the thread totals
-    const uint4 h0 = *(const uint4 *)(hist + 8 * tid), h1 = *(const uint4 *)(hist + 8 * tid + 4);
-    const uint32_t h[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-    uint32_t tot = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) tot += h[j];
-    uint32_t v = tot;  // inclusive suffix sum within the wave (higher lanes hold higher bins)
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t o = __shfl_down(v, off, 64);
-      if (lane + off < 64) v += o;
-    }
-    if (lane == 0) scan[wave] = v;  // wave total
-    __syncthreads();
-    uint32_t above = v - tot;       // bins above 8t+7 within the wave
-    for (int w = wave + 1; w < 4; ++w) above += scan[w];
-    const uint32_t nd = st[0];
-    __syncthreads();
-#pragma unroll
-    for (int j = 7; j >= 0; --j) {
-      if (above < nd && above + h[j] >= nd) {
-        st[1] = (uint32_t)(8 * tid + j);
-        st[0] = nd - above;
-        st[2] = (h[j] == nd - above) ? 1u : 0u;
-      }
-      above += h[j];
-    }
-    __syncthreads();
-    prefix |= (uint64_t)st[1] << shift;
-    mask |= dmask << shift;
-  }
-  prefix_out = prefix;
-  mask_out = mask;
-}
-
-constexpr int TK_E = kTopkChunk / 256;  // logits per thread
-
-__global__ __launch_bounds__(256) void k_topk_chunks(const uint32_t *__restrict__ logits, uint32_t base,
-                                                     uint32_t vocab, uint32_t m, uint32_t *__restrict__ scratch) {
-  __shared__ uint32_t hist[RS_BINS], scan[4], st[4], flag, nout;
-  const int tid = threadIdx.x;
-  const uint32_t g = blockIdx.x, ini = g * kTopkChunk;
-  if (tid == 0) { flag = 0; nout = 0; }
-  uint64_t c[TK_E];
-  bool valid[TK_E];
-  uint32_t bits[TK_E];
-  bool nan = false;
-  uint32_t nvalid = 0;
-  // all loads first (clamped into the vocabulary), then the keys
-#pragma unroll
-  for (int e = 0; e < TK_E; ++e) {
-    const uint32_t j = ini + (uint32_t)e * 256u + (uint32_t)tid;
-    bits[e] = logits[base + min(j, vocab - 1u)];
-  }
-#pragma unroll
-  for (int e = 0; e < TK_E; ++e) {
-    const uint32_t j = ini + (uint32_t)e * 256u + (uint32_t)tid;
-    valid[e] = j < vocab;
-    if (!valid[e]) bits[e] = 0u;
-    c[e] = ((uint64_t)order_key(bits[e]) << 32) | (uint64_t)(~j);
-    if (valid[e] && is_nan_bits(bits[e])) nan = true;
-  }
-  nvalid = vocab > ini ? min(kTopkChunk, vocab - ini) : 0u;
-  __syncthreads();
-  if (nan) atomicOr(&flag, 2u);
-  uint64_t prefix, mask;
-  radix_select<TK_E>(c, valid, min(m, nvalid), hist, scan, prefix, mask, st);
-  uint32_t *hdr = scratch + 2u * g;
-  uint32_t *pairs = scratch + 2u * gridDim.x + (uint64_t)g * 2u * kTopkChunkCap;
-  const uint32_t need = min(m, nvalid);
-#pragma unroll
-  for (int e = 0; e < TK_E; ++e) {
-    if (need && valid[e] && (c[e] & mask) >= prefix) {
-      const uint32_t s = atomicAdd(&nout, 1u);
-      if (s < kTopkChunkCap) {
-        pairs[2 * s] = ini + (uint32_t)e * 256u + (uint32_t)tid;
-        pairs[2 * s + 1] = bits[e];
-      }
-    }
-  }
-  __syncthreads();
-  if (tid == 0) {
-    hdr[0] = min(nout, kTopkChunkCap);
-    hdr[1] = flag | (nout > kTopkChunkCap ? 1u : 0u);
-  }
-}
-
-__global__ __launch_bounds__(256) void k_topk_final(const uint32_t *__restrict__ logits, uint32_t base,
-                                                    uint32_t vocab, uint32_t m, TopkPenal penal, uint32_t n_penal,
-                                                    uint32_t serial, uint32_t chunks,
-                                                    const uint32_t *__restrict__ scratch, uint32_t *__restrict__ out) {
-  __shared__ uint32_t hist[RS_BINS], scan[4], st[4], flags, nsel, total_s;
-  __shared__ uint64_t sel_c[EFF_TOPK_CAP];
-  __shared__ uint32_t sel_b[EFF_TOPK_CAP];
-  __shared__ uint32_t cnt[EFF_TOPK_N_MAX / kTopkChunk];   // candidates per chunk
-  const int tid = threadIdx.x;
-  if (tid == 0) { flags = 0; nsel = 0; total_s = 0; }
-  __syncthreads();
-  // chunk headers, read once (in parallel) into LDS
-  for (uint32_t g = tid; g < chunks; g += 256) {
-    const uint2 hg = *(const uint2 *)(scratch + 2 * g);
-    cnt[g] = hg.x;
-    atomicAdd(&total_s, hg.x);
-    if (hg.y) atomicOr(&flags, hg.y);
-  }
-  // penalised ids: their raw logits (the penalty itself is applied by the sampler)
-  if ((uint32_t)tid < n_penal && tid < EFF_TOPK_P_MAX) {
-    const uint32_t id = penal.ids[tid];
-    out[EFF_TOPK_HEADER + tid] = id < vocab ? logits[base + id] : 0u;
-  } else if (tid < EFF_TOPK_P_MAX) {
-    out[EFF_TOPK_HEADER + tid] = 0u;
-  }
-  const uint32_t *pairs = scratch + 2u * chunks;
-  uint64_t prefix = 0, mask = 0;
-  __syncthreads();
-  const uint32_t need = min(m, total_s);
-  // Candidates are visited in passes of 256 x 4 slots; the select needs them
-  // all at once, so they are gathered per pass into registers when they fit
-  // (chunks * cap <= 4096 slots), else streamed over several selects.
-  const uint32_t slots = chunks * kTopkChunkCap;
-  if (slots <= 4096u) {
-    uint64_t c[16];
-    uint32_t bits[16];
-    bool valid[16];
-    // all loads first (every slot of the scratch exists; unused slots hold
-    // stale values and are masked by `valid`)
-    uint2 pr[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const uint32_t sidx = min((uint32_t)e * 256u + (uint32_t)tid, slots - 1u);
-      pr[e] = *(const uint2 *)(pairs + 2 * (uint64_t)sidx);
-    }
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const uint32_t sidx = (uint32_t)e * 256u + (uint32_t)tid;
-      const uint32_t g = sidx / kTopkChunkCap, s = sidx % kTopkChunkCap;
-      valid[e] = sidx < slots && s < cnt[min(g, chunks - 1u)];
-      bits[e] = pr[e].y;
-      c[e] = ((uint64_t)order_key(pr[e].y) << 32) | (uint64_t)(~pr[e].x);
-    }
-    radix_select<16>(c, valid, need, hist, scan, prefix, mask, st);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      if (need && valid[e] && (c[e] & mask) >= prefix) {
-        const uint32_t q = atomicAdd(&nsel, 1u);
-        if (q < EFF_TOPK_CAP) {
-          sel_c[q] = c[e];
-          sel_b[q] = bits[e];
-        }
-      }
-    }
-  } else {
-    // Large vocabularies: stream the candidate slots; each round re-reads them.
-    uint64_t pre = 0, msk = 0;
-    if (tid == 0) { st[0] = need; st[2] = need == 0u; }
-    __syncthreads();
-    for (int round = 0; round < 8; ++round) {
-      if (st[2]) break;
-      const int shift = 56 - 8 * round;
-      hist[tid] = 0;
-      __syncthreads();
-      for (uint32_t sidx = tid; sidx < slots; sidx += 256) {
-        const uint32_t g = sidx / kTopkChunkCap, s = sidx % kTopkChunkCap;
-        if (s >= cnt[g]) continue;
-        const uint64_t cc = ((uint64_t)order_key(pairs[2 * (uint64_t)sidx + 1]) << 32) | (uint64_t)(~pairs[2 * (uint64_t)sidx]);
-        if ((cc & msk) == pre) atomicAdd(&hist[(uint32_t)(cc >> shift) & 255u], 1u);
-      }
-      __syncthreads();
-      if (tid == 0) {
-        uint32_t nd = st[0], acc = 0;
-        for (int d = 255; d >= 0; --d) {
-          if (acc + hist[d] >= nd) {
-            st[1] = (uint32_t)d;
-            st[0] = nd - acc;
-            st[2] = hist[d] == nd - acc;
-            break;
-          }
-          acc += hist[d];
-        }
-      }
-      __syncthreads();
-      pre |= (uint64_t)st[1] << shift;
-      msk |= (uint64_t)255u << shift;
-    }
-    for (uint32_t sidx = tid; sidx < slots; sidx += 256) {
-      const uint32_t g = sidx / kTopkChunkCap, s = sidx % kTopkChunkCap;
-      if (!need || s >= cnt[g]) continue;
-      const uint32_t b = pairs[2 * (uint64_t)sidx + 1];
-      const uint64_t cc = ((uint64_t)order_key(b) << 32) | (uint64_t)(~pairs[2 * (uint64_t)sidx]);
-      if ((cc & msk) >= pre) {
-        const uint32_t q = atomicAdd(&nsel, 1u);
-        if (q < EFF_TOPK_CAP) { sel_c[q] = cc; sel_b[q] = b; }
-      }
-    }
-  }
-  __syncthreads();
-  const uint32_t n = min(nsel, (uint32_t)EFF_TOPK_CAP);
-  uint32_t *outp = out + EFF_TOPK_HEADER + EFF_TOPK_P_MAX;
-  // rank = number of selected composites larger than this one (all distinct)
-  for (uint32_t i = tid; i < EFF_TOPK_CAP; i += 256) {
-    if (i < n) {
-      const uint64_t ci = sel_c[i];
-      uint32_t rank = 0;
-      for (uint32_t j = 0; j < n; ++j) rank += sel_c[j] > ci ? 1u : 0u;
-      outp[2 * rank] = ~(uint32_t)ci;
-      outp[2 * rank + 1] = sel_b[i];
-    } else {
-      outp[2 * i] = 0u;
-      outp[2 * i + 1] = 0u;
-    }
-  }
-  if (tid == 0) {
-    out[0] = n;
-    out[1] = flags | (nsel > EFF_TOPK_CAP ? 4u : 0u);
-    out[2] = n_penal;
-    out[3] = chunks;
-    out[4] = serial;
-    out[5] = out[6] = out[7] = 0u;
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Host-side launchers.
 
 GemvPlan plan_gemv(const WeightView &wv, uint32_t tokens) {
@@ -1403,22 +1136,6 @@ hipError_t launch_gather_norm(const WeightView &wv, const uint32_t *ids, uint32_
     case Q2_K: return gather_norm_go<Q2_K>(wv, ids, tokens, wn, eps, x, nrm, s);
     default: return hipErrorInvalidValue;
   }
-}
-
-size_t topk_scratch_bytes(uint32_t vocab) { return topk_scratch_bytes_for(vocab); }
-
-hipError_t launch_topk(const uint32_t *logits, uint32_t base, uint32_t vocab, uint32_t m,
-                       const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, uint32_t *scratch,
-                       uint32_t *out, hipStream_t s) {
-  const uint32_t chunks = (vocab + kTopkChunk - 1) / kTopkChunk;
-  TopkPenal pen{};
-  for (uint32_t i = 0; i < n_penal && i < 128; ++i) pen.ids[i] = penal_ids[i];
-  hipLaunchKernelGGL(k_topk_chunks, dim3(chunks), dim3(256), 0, s, logits, base, vocab, m, scratch);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_topk_final, dim3(1), dim3(256), 0, s, logits, base, vocab, m, pen, n_penal, serial,
-                     chunks, (const uint32_t *)scratch, out);
-  return hipGetLastError();
 }
 
 }  // namespace eff

@@ -531,7 +531,8 @@ def run_topk(ctx, eff, vals, m, base=0, penal=(), serial=7):
 
 
 @pytest.mark.parametrize("vocab,m", [(1, 1), (100, 40), (4096, 40), (4097, 40), (65536, 40), (65536, 100),
-                                     (65536, 192), (70000, 192), (10, 40), (200000, 7)])
+                                     (65536, 192), (70000, 192), (10, 40), (200000, 7), (63, 40), (65, 40),
+                                     (257, 192), (1 << 20, 100), (65537, 40)])
 def test_topk_bit_exact(ctx, eff, orc, vocab, m):
     rng = np.random.default_rng(vocab + m)
     vals = rng.normal(0, 3, vocab).astype(np.float32)
@@ -576,6 +577,23 @@ def test_topk_layouts(ctx, eff, orc, layout):
     else:
         vals = np.where(rng.random(vocab) < 0.01, 5.0, -5.0)
     vals = vals.astype(np.float32)
+    r = run_topk(ctx, eff, vals, m)
+    ids, bits, nan = orc.topk(vals.view(np.uint32), m)
+    assert r["n"] == len(ids) and r["flags"] == 0
+    assert np.array_equal(r["ids"], ids) and np.array_equal(r["bits"], bits)
+
+
+@pytest.mark.parametrize("vocab,m", [(65536, 192), (3000001, 150)])
+def test_topk_clustered_in_one_group(ctx, eff, orc, vocab, m):
+    """All the largest logits inside one group of consecutive logits (64 at
+    vocab 65536, 64 * 46 at 3,000,001): the group's 4-element list is
+    saturated and the select reads the group whole."""
+    rng = np.random.default_rng(vocab)
+    vals = rng.normal(0, 1, vocab).astype(np.float32)
+    gs = 64 * ((vocab + 65535) // 65536)
+    g0 = (vocab // gs // 2) * gs
+    vals[g0:g0 + gs] = 50.0 + rng.normal(0, 1, gs).astype(np.float32)
+    vals[g0 + 7] = vals[g0 + 9]                                 # a tie inside the group
     r = run_topk(ctx, eff, vals, m)
     ids, bits, nan = orc.topk(vals.view(np.uint32), m)
     assert r["n"] == len(ids) and r["flags"] == 0

@@ -1,7 +1,7 @@
 """eff_topk_noalloc through the C ABI against eff_topk: the same record on two
 calls in a row, the second over a smaller vocabulary (the fixed scratch still
 holds the first call's candidates when it starts), with ties, a penalty list
-and a base offset; and the vocabulary limit of the fixed scratch."""
+and a base offset; a large vocabulary; and the calls it does not apply to."""
 import numpy as np
 import pytest
 
@@ -31,14 +31,18 @@ def test_topk_noalloc_matches_topk_on_two_calls(ctx, eff):
         b.free()
 
 
-def test_topk_noalloc_limit_and_not_applicable(ctx, eff):
-    big = ctx.alloc(4 * (eff.TOPK_NOALLOC_MAX_VOCAB + 1))
-    with pytest.raises(eff.EffError) as e:
-        ctx.topk_noalloc(big, 0, eff.TOPK_NOALLOC_MAX_VOCAB + 1, 40)
-    assert e.value.code == eff.E_BOUNDS and "262144" in str(e.value)
+def test_topk_noalloc_large_vocab_and_not_applicable(ctx, eff):
+    """The fixed scratch holds the records of every vocabulary the top-k
+    accepts (below 2^24): 2^20 logits give eff_topk's record; past the
+    limits it answers NOT_APPLICABLE as eff_topk does."""
+    vocab = 1 << 20
+    vals = np.random.default_rng(9).normal(0, 2, vocab).astype(np.float32)
+    lb = ctx.upload(vals)
+    want = ctx.topk(lb, 0, vocab, 100, [1, 2], serial=3).read(np.uint32)
+    got = ctx.topk_noalloc(lb, 0, vocab, 100, [1, 2], serial=3).read(np.uint32)
+    assert np.array_equal(got, want)
     with pytest.raises(eff.NotApplicable):
-        ctx.topk_noalloc(big, 0, 1000, eff.TOPK_M_MAX + 1)
-    out = ctx.topk_noalloc(big, 0, eff.TOPK_NOALLOC_MAX_VOCAB, 5)    # exactly at the limit
-    assert eff.parse_topk(out.read(np.uint32))["n"] == 5
-    big.free()
-    out.free()
+        ctx.topk_noalloc(lb, 0, 1000, eff.TOPK_M_MAX + 1)
+    with pytest.raises(eff.NotApplicable):
+        ctx.topk_noalloc(lb, 0, 1000, 40, penal_ids=list(range(eff.TOPK_P_MAX + 1)))
+    lb.free()
