@@ -18,7 +18,7 @@
 using namespace eff;
 
 // Scratch of eff_topk_noalloc: the top-k group records of one call, in a
-// fixed device array of 64 KiB (the records of the largest vocabulary the
+// fixed device array of 16 KiB (the records of the largest vocabulary the
 // top-k accepts). Every GPU the library runs on holds its own copy until the
 // process ends. Host code never uses the array's name as an address: eff_init
 // looks up each device's copy once, with that device current
