@@ -48,8 +48,9 @@ def alg_bytes(eff, tname, rows, k, tokens):
 
 
 class Config:
-    def __init__(self, eff, ctx, tname, rows, k, tokens, seed, topk=0):
+    def __init__(self, eff, ctx, tname, rows, k, tokens, seed, topk=0, fused_head=True):
         self.tname, self.rows, self.k, self.tokens, self.topk = tname, rows, k, tokens, topk
+        self.fused_head = fused_head and tokens == 1
         base = "Q8_0" if tname == "Q8_0R" else tname
         self.t = eff.TYPES[tname]
         w = eff.quantize(base, eff.fill_normal(seed, 0.02, rows * k))
@@ -78,7 +79,12 @@ class Config:
         self.gemm = tokens >= 64
 
     def step(self, ctx, i):
-        ctx.qmatmul(self.t, self.w[i % self.copies], self.x, self.y, self.rows, self.k, self.tokens)
+        w = self.w[i % self.copies]
+        if self.topk and self.fused_head:
+            # the decode head: the GEMV and the top-k of its logits as one call
+            ctx.qgemv_topk(self.t, w, self.x, self.y, self.rows, self.k, self.topk, (), i + 1, self.out)
+            return
+        ctx.qmatmul(self.t, w, self.x, self.y, self.rows, self.k, self.tokens)
         if self.topk:
             ctx.topk(self.y, 0, self.rows, self.topk, (), i + 1, self.out)
 
@@ -342,7 +348,8 @@ def main():
         plan = [("C1", "Q8_0", 8192, 2048, 1, 0), ("C1", "Q8_0R", 8192, 2048, 1, 0),
                 ("C2", "Q4_K", 2048, 8192, 1, 0),
                 ("C3", "Q8_0", 8192, 2048, 512, 0), ("C3", "Q8_0", 8192, 2048, 2048, 0),
-                ("C4", "Q6_K", 65536, 2048, 1, 0), ("C4+top40", "Q6_K", 65536, 2048, 1, 40)]
+                ("C4", "Q6_K", 65536, 2048, 1, 0), ("C4+top40", "Q6_K", 65536, 2048, 1, 40),
+                ("C4+top40 separate", "Q6_K", 65536, 2048, 1, -40)]
         for tn in ("Q2_K", "IQ2_XXS"):
             for m in (1, 8, 32, 128):
                 plan.append(("C5", tn, 8192, 2048, m, 0))
@@ -350,7 +357,8 @@ def main():
             key = f"{tag} {tn} N={r} K={kk} M={m}" + (" +top40" if tk else "")
             if args.only and args.only not in key:
                 continue
-            cfg = Config(eff, ctx, tn, r, kk, m, 300 + r + m, topk=tk)
+            # tk < 0: the GEMV and the top-k as two calls (eff_qmatmul, eff_topk)
+            cfg = Config(eff, ctx, tn, r, kk, m, 300 + r + m, topk=abs(tk), fused_head=tk > 0)
             # the router's choice for this shape, from its launch counters
             before = ctx.stats()
             cfg.step(ctx, 0)
@@ -370,7 +378,8 @@ def main():
             sweep[key] = {"us": round(t_ms * 1e3, 2), "GB/s": round(gb, 1), "TFLOP/s": round(tf, 2),
                           "bound": bound,
                           "roofline_frac": round((mfma_t if bound == "mfma" else hbm_t) / (t_ms * 1e-3), 4),
-                          "path": path, "reuse_distance_MB": round(rotation(cfg, steps)["reuse_distance_bytes"] / 1e6)}
+                          "path": path + (" + top-k" if tk < 0 else " + fused top-k records" if tk else ""),
+                          "reuse_distance_MB": round(rotation(cfg, steps)["reuse_distance_bytes"] / 1e6)}
             cfg.free()
             print(f"# {key}: {sweep[key]}", file=sys.stderr, flush=True)
 

@@ -176,7 +176,9 @@ int run_gemv(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint3
   if (ctx->gemv_kernel == 0 && sx_applies(wv, tokens)) return run_sx(ctx, wv, x, y, tokens);
   GemvPlan p;
   hipError_t e;
-  if (ctx->gemv_kernel == 0 && gemv_mt_plan(wv, tokens, p)) {
+  if (ctx->gemv_kernel == 0 && gemv_rows_applies(wv, tokens)) {
+    e = launch_gemv_rows(wv, x, y, nullptr, ctx->stream);
+  } else if (ctx->gemv_kernel == 0 && gemv_mt_plan(wv, tokens, p)) {
     e = launch_gemv_mt(wv, x, y, tokens, p, ctx->stream);
   } else if (ctx->gemv_kernel == 0 && gemv_mx_plan(wv, tokens, p)) {
     e = launch_gemv_mx(wv, x, y, tokens, p, ctx->stream);
@@ -611,7 +613,11 @@ int eff_qgemv_multi(eff_ctx *ctx, int type, int mode, uint32_t n, eff_buf *const
   }
   int rc = use_device(ctx);
   if (rc) return rc;
-  if (!gemv_mx_multi_applies(wvs[0], tokens, mode)) {
+  // a matrix whose one-matrix GEMV runs the row kernel would not get that
+  // GEMV's bits from a fused launch: not applicable, the caller runs them apart
+  bool rows_kernel = false;
+  for (uint32_t i = 0; i < n; ++i) rows_kernel = rows_kernel || gemv_rows_applies(wvs[i], tokens);
+  if (rows_kernel || !gemv_mx_multi_applies(wvs[0], tokens, mode)) {
     ++ctx->stats.not_applicable;
     return EFF_NOT_APPLICABLE;
   }
@@ -845,6 +851,39 @@ int eff_topk(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint3
   hipError_t e = launch_topk((const uint32_t *)logits->ptr, base, vocab, m, penal_ids, n_penal, serial,
                              (uint32_t *)ctx->topk_scratch, (uint32_t *)out->ptr, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "topk launch");
+  ++ctx->stats.topk;
+  return EFF_OK;
+}
+
+int eff_qgemv_topk(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k, uint32_t m,
+                   const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, eff_buf *out) {
+  if (!ctx) return EFF_E_INVALID;
+  // the top-k's limits first, so that a NOT_APPLICABLE call enqueues nothing
+  int rc = topk_check(ctx, y, 0, rows, m, penal_ids, n_penal, out, "gemv+topk");
+  if (rc) return rc;
+  WeightView wv;
+  if ((rc = weight_view(ctx, type, w, x, y, rows, k, 1, wv, "gemv+topk"))) return rc;
+  if ((rc = use_device(ctx))) return rc;
+  const float *xp = (const float *)x->ptr;
+  float *yp = (float *)y->ptr;
+  if (ctx->gemv_kernel == 0 && gemv_rows_applies(wv, 1) && gemv_rows_groups(wv) <= kTopkPickGroupsMax) {
+    // the GEMV writes the top-k's group records; one launch selects from them
+    const uint32_t groups = gemv_rows_groups(wv);
+    if ((rc = grow(ctx, &ctx->topk_scratch, &ctx->topk_scratch_bytes, (size_t)groups * kTopkRecordBytes, "topk")))
+      return rc;
+    hipError_t e = launch_gemv_rows(wv, xp, yp, (uint8_t *)ctx->topk_scratch, ctx->stream);
+    if (e == hipSuccess)
+      e = launch_topk_pick((const uint32_t *)yp, rows, m, penal_ids, n_penal, serial, gemv_rows_group_size(), groups,
+                           (const uint8_t *)ctx->topk_scratch, (uint32_t *)out->ptr, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "gemv+topk launch");
+  } else {
+    if ((rc = run_gemv(ctx, wv, xp, yp, 1))) return rc;
+    if ((rc = grow(ctx, &ctx->topk_scratch, &ctx->topk_scratch_bytes, topk_scratch_bytes(rows), "topk"))) return rc;
+    hipError_t e = launch_topk((const uint32_t *)yp, 0, rows, m, penal_ids, n_penal, serial,
+                               (uint32_t *)ctx->topk_scratch, (uint32_t *)out->ptr, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "topk launch");
+  }
+  ++ctx->stats.gemv;
   ++ctx->stats.topk;
   return EFF_OK;
 }

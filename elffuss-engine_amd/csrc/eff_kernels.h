@@ -49,6 +49,14 @@ hipError_t launch_gemv_mx(const WeightView &wv, const float *x, float *y, uint32
 bool gemv_mx_multi_applies(const WeightView &wv0, uint32_t tokens, int mode);
 hipError_t launch_gemv_mx_multi(int mode, uint32_t n, const WeightView *wvs, const float *x, float *const *ys,
                                 uint32_t tokens, hipStream_t stream);
+// One-token GEMV for Q6_K matrices of >= 32768 rows (the output projection):
+// a lane per half row-block, x digits as LDS broadcasts (eff_gemv_rows.hip).
+// With `rec` non-null the kernel also writes the top-k records of its groups
+// of gemv_rows_group_size() consecutive rows (gemv_rows_groups(wv) of them).
+bool gemv_rows_applies(const WeightView &wv, uint32_t tokens);
+uint32_t gemv_rows_groups(const WeightView &wv);
+uint32_t gemv_rows_group_size();
+hipError_t launch_gemv_rows(const WeightView &wv, const float *x, float *y, uint8_t *rec, hipStream_t stream);
 // Multi-token matrix-core GEMV (16 rows x 4 tokens per MFMA): 4..16 tokens
 // per launch, Q8_0/Q4_K/Q6_K/Q2_K/IQ2_XXS, k % 256 == 0.
 bool gemv_mt_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p);
@@ -105,6 +113,12 @@ constexpr size_t topk_scratch_bytes_for(uint32_t vocab) { return (size_t)topk_gr
 constexpr size_t kTopkScratchMax = (size_t)kTopkGroupsMax * kTopkRecordBytes;
 size_t topk_scratch_bytes(uint32_t vocab);
 
+// The selecting half alone, over `groups` records (<= kTopkPickGroupsMax) of
+// groups of `gs` consecutive logits written by another kernel.
+constexpr uint32_t kTopkPickGroupsMax = 1024;
+hipError_t launch_topk_pick(const uint32_t *logits, uint32_t vocab, uint32_t m, const uint32_t *penal_ids,
+                            uint32_t n_penal, uint32_t serial, uint32_t gs, uint32_t groups, const uint8_t *rec,
+                            uint32_t *out, hipStream_t stream);
 hipError_t launch_topk(const uint32_t *logits, uint32_t base, uint32_t vocab, uint32_t m,
                        const uint32_t *penal_ids_dev, uint32_t n_penal, uint32_t serial,
                        uint32_t *scratch, uint32_t *out, hipStream_t stream);

@@ -3,11 +3,7 @@
 // as the reference's output record (kernels.topk.wgsl.js:40-60,
 // ops.topk.js:99-165; the order of sample.js:44-67).
 //
-// Elements are compared by the 64-bit composite (order_key(bits) << 32 |
-// ~index): unique per element, larger composite = larger value, ties to the
-// lower index. order_key maps f32 order to u32 order with -0 = +0
-// (kernels.topk.wgsl.js:75-82). A valid element's composite is never 0
-// (~index has its top 8 bits set for index < 2^24), so 0 marks "none".
+// Composites, records and the wave helpers are in eff_topk.h.
 //
 // Two launches:
 //  * k_topk_groups: the vector is cut into G <= 256 groups of
@@ -32,71 +28,15 @@
 
 #include "../../include/elffuss_amd.h"
 #include "eff_kernels.h"
+#include "eff_topk.h"
 
 namespace eff {
 
 namespace {
 
-__device__ __forceinline__ uint32_t order_key(uint32_t bits) {
-  const uint32_t b = bits == 0x80000000u ? 0u : bits;
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-__device__ __forceinline__ bool is_nan_bits(uint32_t bits) { return (bits & 0x7FFFFFFFu) > 0x7F800000u; }
-
-__device__ __forceinline__ uint64_t composite(uint32_t bits, uint32_t idx) {
-  return ((uint64_t)order_key(bits) << 32) | (uint64_t)(~idx);
-}
-
 struct TopkPenal {
   uint32_t ids[EFF_TOPK_P_MAX];
 };
-
-// Sorted insertion into a lane's 4 largest (c0 > c1 > c2 > c3).
-struct Top4 {
-  uint64_t c[4] = {0, 0, 0, 0};
-  uint32_t b[4] = {0, 0, 0, 0};
-  __device__ __forceinline__ void add(uint64_t v, uint32_t bits) {
-    if (v <= c[3]) return;
-    c[3] = v;
-    b[3] = bits;
-#pragma unroll
-    for (int i = 3; i > 0; --i) {
-      if (c[i] > c[i - 1]) {
-        const uint64_t t = c[i];
-        c[i] = c[i - 1];
-        c[i - 1] = t;
-        const uint32_t u = b[i];
-        b[i] = b[i - 1];
-        b[i - 1] = u;
-      }
-    }
-  }
-};
-
-// Wave-wide maximum / minimum of a u32 (every lane active): DPP within rows
-// of 16 (quad xor 1, quad xor 2, half-row mirror, row mirror), then the four
-// rows through scalar reads. The result is wave-uniform.
-template <bool MAX>
-__device__ __forceinline__ uint32_t wave_ext(uint32_t v) {
-  auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
-  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));
-  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));
-  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false));
-  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xF, 0xF, false));
-  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-  return op(op(r0, r1), op(r2, r3));
-}
-
-// Wave-wide maximum / minimum of a u64, as its high word then the low word
-// among the lanes holding that high word.
-template <bool MAX>
-__device__ __forceinline__ uint64_t wave_ext64(uint64_t v) {
-  const uint32_t h = wave_ext<MAX>((uint32_t)(v >> 32));
-  const uint32_t l = wave_ext<MAX>((uint32_t)(v >> 32) == h ? (uint32_t)v : (MAX ? 0u : 0xFFFFFFFFu));
-  return ((uint64_t)h << 32) | l;
-}
 
 // Record of a group (kTopkRecordBytes = 64): u64 c[4] (0 past the group's
 // elements), u32 bits[4], u32 nan flag, 12 bytes unused.
@@ -124,38 +64,7 @@ __global__ __launch_bounds__(64) void k_topk_groups(const uint32_t *__restrict__
       }
     }
   }
-  // the group's 4 largest: 4 rounds of a wave maximum over the lanes' heads
-  uint64_t out_c[4];
-  uint32_t out_b[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const uint64_t mx = wave_ext64<true>(t.c[0]);
-    const bool mine = mx != 0u && t.c[0] == mx;
-    const uint64_t win = __ballot(mine);
-    const int src = win ? (int)__builtin_ctzll(win) : 0;
-    out_c[r] = mx;
-    out_b[r] = mx ? (uint32_t)__builtin_amdgcn_readlane((int)t.b[0], src) : 0u;
-    if (mine) {  // the winning lane pops its head
-      t.c[0] = t.c[1]; t.b[0] = t.b[1];
-      t.c[1] = t.c[2]; t.b[1] = t.b[2];
-      t.c[2] = t.c[3]; t.b[2] = t.b[3];
-      t.c[3] = 0u; t.b[3] = 0u;
-    }
-  }
-  const bool any_nan = __ballot(nan) != 0u;
-  if (lane < 4u) {
-    uint4 *dst = (uint4 *)(rec + (uint64_t)g * kTopkRecordBytes);
-    uint4 v;
-    if (lane < 2u) {
-      const uint64_t a = out_c[2 * lane], b = out_c[2 * lane + 1];
-      v = make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
-    } else if (lane == 2u) {
-      v = make_uint4(out_b[0], out_b[1], out_b[2], out_b[3]);
-    } else {
-      v = make_uint4(any_nan ? 1u : 0u, 0u, 0u, 0u);
-    }
-    dst[lane] = v;
-  }
+  topk_record_wave(t, nan, rec + (uint64_t)g * kTopkRecordBytes);
 }
 
 constexpr int kPickThreads = 256;
@@ -247,31 +156,38 @@ __device__ uint64_t select_top(uint32_t need, Visit visit, PickShared &sh) {
   return lo;  // not reached: each round narrows the candidates in play
 }
 
+// R records per thread: thread t holds the records of groups t + 256 r.
+template <int R>
 __global__ __launch_bounds__(kPickThreads) void k_topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab,
                                                             uint32_t m, TopkPenal penal, uint32_t n_penal,
-                                                            uint32_t serial, uint32_t per, uint32_t groups,
+                                                            uint32_t serial, uint32_t gs, uint32_t groups,
                                                             const uint8_t *__restrict__ rec,
                                                             uint32_t *__restrict__ out) {
   __shared__ PickShared sh;
   __shared__ uint32_t flags, nsat, ncand, nsel;
-  __shared__ uint32_t satg[kTopkGroupsMax];
+  __shared__ uint32_t satg[kPickThreads * R];
   __shared__ uint64_t cand_c[kCandMax];
   __shared__ uint32_t cand_b[kCandMax];
   __shared__ uint32_t cand_r[kCandMax];
   const int tid = threadIdx.x, lane = tid & 63;
-  const uint32_t gs = 64u * per;
-  uint64_t c[4] = {0, 0, 0, 0};
-  uint32_t b[4] = {0, 0, 0, 0};
+  uint64_t c[R][4];
+  uint32_t b[R][4];
   uint32_t nan = 0;
-  if ((uint32_t)tid < groups) {
-    const uint4 *r = (const uint4 *)(rec + (uint64_t)tid * kTopkRecordBytes);
-    const uint4 q0 = r[0], q1 = r[1], q2 = r[2], q3 = r[3];
-    c[0] = ((uint64_t)q0.y << 32) | q0.x;
-    c[1] = ((uint64_t)q0.w << 32) | q0.z;
-    c[2] = ((uint64_t)q1.y << 32) | q1.x;
-    c[3] = ((uint64_t)q1.w << 32) | q1.z;
-    b[0] = q2.x; b[1] = q2.y; b[2] = q2.z; b[3] = q2.w;
-    nan = q3.x;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t g = (uint32_t)tid + kPickThreads * r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { c[r][i] = 0u; b[r][i] = 0u; }
+    if (g < groups) {
+      const uint4 *rp = (const uint4 *)(rec + (uint64_t)g * kTopkRecordBytes);
+      const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2], q3 = rp[3];
+      c[r][0] = ((uint64_t)q0.y << 32) | q0.x;
+      c[r][1] = ((uint64_t)q0.w << 32) | q0.z;
+      c[r][2] = ((uint64_t)q1.y << 32) | q1.x;
+      c[r][3] = ((uint64_t)q1.w << 32) | q1.z;
+      b[r][0] = q2.x; b[r][1] = q2.y; b[r][2] = q2.z; b[r][3] = q2.w;
+      nan |= q3.x;
+    }
   }
   // penalised ids: their raw logits (the penalty itself is applied by the sampler)
   uint32_t pv = 0u;
@@ -286,19 +202,30 @@ __global__ __launch_bounds__(kPickThreads) void k_topk_pick(const uint32_t *__re
   __syncthreads();
   if (lane == 0 && wnan) atomicOr(&flags, 2u);
   const uint32_t need = min(m, vocab);
+  // tau: the need-th largest group maximum (0 when there are no more groups).
+  // Every one of the overall need largest is >= tau, and only the `need`
+  // groups whose maximum is >= tau list composites >= tau.
   uint64_t tau = 0;
-  if (groups > need) tau = select_top(need, [&](auto f) { if (c[0]) f(c[0]); }, sh);
+  if (groups > need) {
+    tau = select_top(need, [&](auto f) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (c[r][0]) f(c[r][0]);
+    }, sh);
+  }
   // the listed composites >= tau: at most 4 need of them
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (c[i] && c[i] >= tau) {
-      const uint32_t q = atomicAdd(&ncand, 1u);
-      if (q < kCandMax) {
-        cand_c[q] = c[i];
-        cand_b[q] = b[i];
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (c[r][i] && c[r][i] >= tau) {
+        const uint32_t q = atomicAdd(&ncand, 1u);
+        if (q < kCandMax) {
+          cand_c[q] = c[r][i];
+          cand_b[q] = b[r][i];
+        }
       }
     }
-  }
   __syncthreads();
   const uint32_t nc = min(ncand, kCandMax);
   uint64_t T = 0;        // exactly `need` candidates (of the final set) are >= T
@@ -331,9 +258,14 @@ __global__ __launch_bounds__(kPickThreads) void k_topk_pick(const uint32_t *__re
     ranked = true;
   }
   // saturated groups: more than 4 elements and the 4th listed one selected
-  const uint32_t gcount = (uint32_t)tid < groups ? min(gs, vocab - (uint32_t)tid * gs) : 0u;
-  const bool sat = gcount > 4u && c[3] >= T;
-  if (sat) satg[atomicAdd(&nsat, 1u)] = (uint32_t)tid;
+  bool sat[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t g = (uint32_t)tid + kPickThreads * r;
+    const uint32_t gcount = g < groups ? min(gs, vocab - g * gs) : 0u;
+    sat[r] = gcount > 4u && c[r][3] >= T;
+    if (sat[r]) satg[atomicAdd(&nsat, 1u)] = g;
+  }
   __syncthreads();
   const uint32_t ns = nsat;
   uint32_t *pairs = out + EFF_TOPK_HEADER + EFF_TOPK_P_MAX;
@@ -358,20 +290,26 @@ __global__ __launch_bounds__(kPickThreads) void k_topk_pick(const uint32_t *__re
     };
     if (ns) {
       // the unsaturated groups' lists plus every element of the saturated groups
-      if (sat) c[0] = c[1] = c[2] = c[3] = 0u;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (sat[r]) c[r][0] = c[r][1] = c[r][2] = c[r][3] = 0u;
       T = select_top(need, [&](auto f) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (c[i]) f(c[i]);
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (c[r][i]) f(c[r][i]);
         stream([&](uint64_t v, uint32_t) { f(v); });
       }, sh);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (c[i] && c[i] >= T) {
-          const uint32_t q = atomicAdd(&nsel, 1u);
-          if (q < EFF_TOPK_M_MAX) { cand_c[q] = c[i]; cand_b[q] = b[i]; }
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (c[r][i] && c[r][i] >= T) {
+            const uint32_t q = atomicAdd(&nsel, 1u);
+            if (q < EFF_TOPK_M_MAX) { cand_c[q] = c[r][i]; cand_b[q] = b[r][i]; }
+          }
         }
-      }
       stream([&](uint64_t v, uint32_t bits) {
         if (v >= T) {
           const uint32_t q = atomicAdd(&nsel, 1u);
@@ -413,6 +351,26 @@ __global__ __launch_bounds__(kPickThreads) void k_topk_pick(const uint32_t *__re
 
 size_t topk_scratch_bytes(uint32_t vocab) { return topk_scratch_bytes_for(vocab); }
 
+hipError_t launch_topk_pick(const uint32_t *logits, uint32_t vocab, uint32_t m, const uint32_t *penal_ids,
+                            uint32_t n_penal, uint32_t serial, uint32_t gs, uint32_t groups, const uint8_t *rec,
+                            uint32_t *out, hipStream_t s) {
+  if (vocab == 0 || vocab >= EFF_TOPK_N_MAX || m == 0 || m > EFF_TOPK_M_MAX || n_penal > EFF_TOPK_P_MAX ||
+      groups == 0 || groups > kTopkPickGroupsMax || (uint64_t)groups * gs < vocab)
+    return hipErrorInvalidValue;
+  TopkPenal pen{};
+  for (uint32_t i = 0; i < n_penal; ++i) pen.ids[i] = penal_ids[i];
+  if (groups <= (uint32_t)kPickThreads)
+    hipLaunchKernelGGL((k_topk_pick<1>), dim3(1), dim3(kPickThreads), 0, s, logits, vocab, m, pen, n_penal, serial, gs,
+                       groups, rec, out);
+  else if (groups <= 2u * kPickThreads)
+    hipLaunchKernelGGL((k_topk_pick<2>), dim3(1), dim3(kPickThreads), 0, s, logits, vocab, m, pen, n_penal, serial, gs,
+                       groups, rec, out);
+  else
+    hipLaunchKernelGGL((k_topk_pick<4>), dim3(1), dim3(kPickThreads), 0, s, logits, vocab, m, pen, n_penal, serial, gs,
+                       groups, rec, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_topk(const uint32_t *logits, uint32_t base, uint32_t vocab, uint32_t m,
                        const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, uint32_t *scratch,
                        uint32_t *out, hipStream_t s) {
@@ -420,15 +378,11 @@ hipError_t launch_topk(const uint32_t *logits, uint32_t base, uint32_t vocab, ui
     return hipErrorInvalidValue;
   const uint32_t gs = topk_group_size(vocab), groups = topk_groups(vocab);
   if (groups > kTopkGroupsMax) return hipErrorInvalidValue;
-  TopkPenal pen{};
-  for (uint32_t i = 0; i < n_penal; ++i) pen.ids[i] = penal_ids[i];
   const uint32_t *lg = logits + base;
   hipLaunchKernelGGL(k_topk_groups, dim3(groups), dim3(64), 0, s, lg, vocab, gs / 64u, (uint8_t *)scratch);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_topk_pick, dim3(1), dim3(kPickThreads), 0, s, lg, vocab, m, pen, n_penal, serial, gs / 64u,
-                     groups, (const uint8_t *)scratch, out);
-  return hipGetLastError();
+  return launch_topk_pick(lg, vocab, m, penal_ids, n_penal, serial, gs, groups, (const uint8_t *)scratch, out, s);
 }
 
 }  // namespace eff

@@ -104,6 +104,7 @@ def lib():
         "eff_gather_norm": ([p, i32, p, p, p, ctypes.c_float, p, p, u32, u32], i32),
         "eff_topk": ([p, p, u32, u32, u32, p, u32, u32, p], i32),
         "eff_topk_noalloc": ([p, p, u32, u32, u32, p, u32, u32, p], i32),
+        "eff_qgemv_topk": ([p, i32, p, p, p, u32, u32, u32, p, u32, u32, p], i32),
         "eff_topk_out_bytes": ([], sz),
     }
     for name, (args, res) in sig.items():
@@ -120,7 +121,7 @@ EXPORTED = ("eff_type_from_name eff_type_name eff_type_geometry eff_init eff_shu
             "eff_read_begin eff_read_end eff_read_error eff_read_release "
             "eff_bytes_reordered eff_bytes_buffer_r eff_blocks_from_buffer eff_scales_from eff_buf_mark_r "
             "eff_buf_blocks_r eff_buf_write_r eff_repack eff_unrepack eff_quantize eff_fill_normal eff_qmatmul eff_qgemv "
-            "eff_qgemm eff_qgemm_planned eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_noalloc eff_topk_out_bytes").split()
+            "eff_qgemm eff_qgemm_planned eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_noalloc eff_qgemv_topk eff_topk_out_bytes").split()
 
 
 def type_code(t):
@@ -356,6 +357,15 @@ class Context:
                                    ids.ctypes.data if ids.size else None, ids.size, serial, out.handle))
         return out
 
+
+    def qgemv_topk(self, t, w, x, y, rows, k, m, penal_ids=(), serial=1, out=None):
+        """eff_qgemv_topk: y = W x (one token), then the top-m record of y into `out`."""
+        ids = np.ascontiguousarray(np.asarray(penal_ids, dtype=np.uint32))
+        if out is None:
+            out = self.alloc(lib().eff_topk_out_bytes())
+        self._check(lib().eff_qgemv_topk(self.h, type_code(t), w.handle, x.handle, y.handle, rows, k, m,
+                                         ids.ctypes.data if ids.size else None, ids.size, serial, out.handle))
+        return out
 
     def topk_noalloc(self, logits, base, vocab, m, penal_ids=(), serial=1, out=None):
         """eff_topk_noalloc: the top-k with the library's fixed scratch (no allocation)."""

@@ -299,6 +299,19 @@ int eff_gather_norm(eff_ctx *ctx, int type, eff_buf *w, eff_buf *ids, eff_buf *w
 int eff_topk(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint32_t m,
              const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, eff_buf *out);
 
+/* The decode head: y[0 .. rows) = W x for one token (as eff_qmatmul with
+ * tokens = 1), then the exact top-m of y written to `out` exactly as
+ * eff_topk(y, 0, rows, m, penal_ids, n_penal, serial, out) writes it. This is
+ * the output projection fused with top-k = 40 of north_star's configuration
+ * 4; the reference runs the two as separate passes (model.js:1145-1177, then
+ * createTopKGPU().candidatos, ops.topk.js:99-165). For Q6_K matrices of
+ * 32768 .. 131072 rows the GEMV kernel also writes the top-k's per-group
+ * records and one more launch selects from them; other shapes run the GEMV
+ * and eff_topk. The same NOT_APPLICABLE cases as eff_topk, checked before
+ * anything is enqueued. */
+int eff_qgemv_topk(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k,
+                   uint32_t m, const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, eff_buf *out);
+
 /* eff_topk without any device allocation. No counterpart in the reference:
  * it is for callers that cannot allocate (code under HIP graph capture,
  * serving loops that forbid hipMalloc). The top-k's group records go to a

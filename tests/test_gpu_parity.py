@@ -151,6 +151,56 @@ def test_gemv_non_finite_x(ctx, eff, gemv_kernel, tname):
     assert np.all(~np.isfinite(y[0])) and np.all(~np.isfinite(y[1])) and np.all(np.isfinite(y[2]))
 
 
+# ---- the row GEMV for Q6_K matrices with many rows (the output projection) -------------
+
+@pytest.mark.parametrize("rows,k", [(32768, 512), (32805, 4608), (40001, 2048), (32769, 8192)])
+def test_gemv_rows_q6_k_vs_f64_oracle(ctx, eff, orc, rows, k):
+    """One token of a Q6_K matrix of >= 32768 rows runs the row kernel (a lane
+    per half row-block): row counts that are not a multiple of the 128-row
+    workgroup, an odd number of blocks per row (block starts at both 2-byte
+    alignments in every column), and k up to 32 blocks."""
+    t, data, gguf, n = make_weights(eff, "Q6_K", rows, k, rows + k)
+    x = eff.fill_normal(rows + 1, 1.0, k)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(rows * 4)
+    ctx.qmatmul(t, wb, xb, yb, rows, k, 1)
+    check_close(yb.read(np.float32)[None, :], orc.gemv_f64(orc.Q6_K, gguf, rows, k, x, 1), f"rows Q6_K {rows}x{k}")
+    for b in (wb, xb, yb):
+        b.free()
+
+
+def test_gemv_rows_q6_k_x_range_non_finite_and_fused(ctx, eff, orc):
+    """The row kernel on x of mixed magnitudes (zeros, 1e-30, 1e30, outliers,
+    subnormals) keeps the f64 bounds; a NaN or an infinity in x makes every
+    output non-finite; fused launches over such a matrix are not applicable
+    (their one-matrix GEMV is the row kernel)."""
+    rows, k = 32800, 2048
+    t, data, gguf, n = make_weights(eff, "Q6_K", rows, k, 91)
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 1, k).astype(np.float32)
+    x[:32] = 0.0
+    x[32:64] *= 1e-30
+    x[64:96] *= 1e30
+    x[200::37] *= 1e4
+    x[96:128] = np.float32(1e-40)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(rows * 4)
+    ctx.qgemv(t, wb, xb, yb, rows, k, 1)
+    check_close(yb.read(np.float32)[None, :], orc.gemv_f64(orc.Q6_K, gguf, rows, k, x, 1), "rows Q6_K x range")
+    for v in (np.nan, np.inf):
+        x2 = eff.fill_normal(92, 1.0, k)
+        x2[777] = v
+        xb2 = ctx.upload(x2)
+        ctx.qgemv(t, wb, xb2, yb, rows, k, 1)
+        assert np.all(~np.isfinite(yb.read(np.float32)))
+        xb2.free()
+    y2 = ctx.alloc(rows * 4)
+    with pytest.raises(eff.NotApplicable):
+        ctx.qgemv_multi(t, eff.GEMV_SWIGLU, [wb, wb], xb, [yb], [rows, rows], k, 1)
+    with pytest.raises(eff.NotApplicable):
+        ctx.qgemv_multi(t, eff.GEMV_SECTIONS, [wb, wb], xb, [yb, y2], [rows, rows], k, 1)
+    for b in (wb, xb, yb, y2):
+        b.free()
+
+
 def test_q8_0r_gemv_bit_identical_to_q8_0(ctx, eff):
     """Repacked and GGUF layouts give the same bits (kernels.wgsl.js:831-839)."""
     rows, k = 300, 2048
@@ -598,6 +648,48 @@ def test_topk_clustered_in_one_group(ctx, eff, orc, vocab, m):
     ids, bits, nan = orc.topk(vals.view(np.uint32), m)
     assert r["n"] == len(ids) and r["flags"] == 0
     assert np.array_equal(r["ids"], ids) and np.array_equal(r["bits"], bits)
+
+
+@pytest.mark.parametrize("tname,rows,k,m,cluster", [
+    ("Q6_K", 65536, 2048, 40, False),      # the C4 head: records from the GEMV, 512 groups
+    ("Q6_K", 40001, 2048, 192, True),      # ragged rows; the largest logits in one 128-row group
+    ("Q6_K", 65664, 512, 100, True),       # 513 groups
+    ("Q6_K", 131073, 512, 40, False),      # more groups than one selection holds: GEMV, then eff_topk
+    ("Q8_0", 50000, 512, 40, False),       # no row kernel: GEMV, then eff_topk
+])
+def test_qgemv_topk_equals_gemv_then_topk(ctx, eff, orc, tname, rows, k, m, cluster):
+    """eff_qgemv_topk gives the logits and the top-k record of eff_qmatmul
+    followed by eff_topk, bit for bit, and the record is the oracle's top-m of
+    those logits."""
+    base = "Q8_0" if tname == "Q8_0R" else tname
+    wf = eff.fill_normal(rows % 1000 + 1011, 0.02, rows * k).reshape(rows, k)
+    if cluster:
+        wf[5000:5128] *= 40.0                              # one group's rows dominate
+    w = eff.quantize(base, wf)
+    x = eff.fill_normal(12, 1.0, k)
+    t = eff.TYPES[tname]
+    wb, xb, y1, y2 = ctx.upload(w), ctx.upload(x), ctx.alloc(rows * 4), ctx.alloc(rows * 4)
+    pen = [3, rows - 1]
+    o1 = ctx.qgemv_topk(t, wb, xb, y1, rows, k, m, pen, serial=5)
+    ctx.qmatmul(t, wb, xb, y2, rows, k, 1)
+    o2 = ctx.topk(y2, 0, rows, m, pen, serial=5)
+    ya, yb_ = y1.read(np.uint32), y2.read(np.uint32)
+    assert np.array_equal(ya, yb_)
+    ra, rb = o1.read(np.uint32), o2.read(np.uint32)
+    assert np.array_equal(ra, rb)
+    r = eff.parse_topk(ra)
+    ids, bits, nan = orc.topk(ya, m)
+    assert r["n"] == m and r["flags"] == 0 and r["serial"] == 5
+    assert np.array_equal(r["ids"], ids) and np.array_equal(r["bits"], bits)
+    if cluster:   # the boosted rows hold the largest logits
+        assert np.all((r["ids"][:32] >= 5000) & (r["ids"][:32] < 5128))
+    # a call the top-k does not apply to enqueues nothing
+    y1.write(np.zeros(rows, np.uint32))
+    with pytest.raises(eff.NotApplicable):
+        ctx.qgemv_topk(t, wb, xb, y1, rows, k, eff.TOPK_M_MAX + 1)
+    assert not np.any(y1.read(np.uint32))
+    for b in (wb, xb, y1, y2, o1, o2):
+        b.free()
 
 
 def test_topk_all_equal(ctx, eff):
