@@ -424,7 +424,7 @@ def main():
                                "of the logits (decode head)",
                    "rows": rows, "k": k, "tokens": 1, "top_k": 40, "weight_rotation": rot,
                    "gemv_alone_ms_per_step": round(ms_gemv, 5)},
-        "roofline": {"bound": "hbm", "kernel": "k_gemv_mx (Q6_K, 1 token)", "achieved": round(gemv_gbs, 1),
+        "roofline": {"bound": "hbm", "kernel": "k_gemv_rows_q6k (Q6_K, 1 token)", "achieved": round(gemv_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic},
         "cpu_baseline": base,

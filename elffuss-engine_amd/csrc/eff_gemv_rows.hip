@@ -3,11 +3,11 @@
 // half of a row's 256-weight block, so the rows' sums need no cross-lane
 // reduction and x is read as a broadcast.
 //
-// Weights. A wave owns a tile of 32 rows x one block column. The tile's bytes
-// (32 x 210, each row from its 4-byte aligned start, 240-byte LDS rows) come
-// in by direct-to-LDS loads (coalesced 16-byte chunks), into one 8 KB buffer
-// per wave; the load of the next block column goes out as soon as the
-// current tile is in registers. Lane l < 32 takes weights 0..127 of row l,
+// Weights. A wave owns a tile of 32 rows x one block column at a time. The
+// tile's bytes (32 x 210, each row from its 4-byte aligned start, 240-byte LDS
+// rows) come in by direct-to-LDS loads (coalesced 16-byte chunks), into one
+// 8 KB buffer per wave; the load of the next tile goes out as soon as the
+// current one is in registers. Lane l < 32 takes weights 0..127 of row l,
 // lane l + 32 weights 128..255 (the halves n = 0, 1 of kernels.wgsl.js:
 // 269-330): ql bytes 64n.., qh bytes 32n.., scales 8n..8n+7 and d. With the
 // 240-byte row pitch the 16-byte reads of 16 lanes fall in 16 different bank
@@ -22,11 +22,17 @@
 // against digits read as LDS broadcasts (all lanes of a half read the same
 // address).
 //
-// Workgroup: 8 waves = 4 row groups x 2 k slices (each wave walks half of the
-// block columns); the two slices of a row are added in a fixed order. With
-// REC the workgroup also writes the top-k record of its 128 rows (their 4
-// largest logits, eff_topk.h), so that the top-k over the logits only has to
-// select from the records.
+// Workgroup: 128 rows, 8 waves = RG row groups x KS k slices (KS = 8 when the
+// matrix has at least 8 block columns). Slice s takes the block columns
+// s, s + KS, s + 2 KS, ... of each of its tiles, so the KS waves of a row group
+// load neighbouring blocks of the same 32 rows at about the same time: the
+// 128-byte lines two neighbouring blocks share are fetched from memory once
+// and found in L2 by the second wave. (When one wave walks consecutive block
+// columns of its rows, the shared lines have left L2 before its next load and
+// the kernel reads 1.3 x the matrix.) A row's KS slice sums are added in a
+// fixed order. With REC the workgroup also writes the top-k record of its 128
+// rows (their 4 largest logits, eff_topk.h), so that the top-k over the logits
+// only has to select from the records.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -41,139 +47,186 @@ namespace eff {
 
 namespace {
 
-constexpr uint32_t kRowsWaves = 8, kRowsKS = 2, kRowsGroups = kRowsWaves / kRowsKS;
+constexpr uint32_t kRowsWaves = 8;
 constexpr uint32_t kRowsTile = 32;                    // rows per wave tile
-constexpr uint32_t kRowsPerWG = kRowsGroups * kRowsTile;
+constexpr uint32_t kRowsPerWG = 128;
 constexpr uint32_t kRowsPitch = 240;                  // LDS bytes per tile row (15 chunks)
 constexpr uint32_t kRowsBuf = 8192;                   // LDS bytes per wave (8 loads of 1 KB)
+constexpr uint32_t kRowsRed = 4096;                   // LDS bytes of the slice sums (128 rows x up to 8 slices)
 constexpr uint32_t kRowsMin = 32768;
 constexpr uint32_t kRowsMaxK = 16384;
 
-template <bool REC>
-__global__ __launch_bounds__(kRowsWaves * 64) void k_gemv_rows_q6k(WeightView wv, const float *__restrict__ x,
-                                                                    float *__restrict__ y, uint8_t *__restrict__ rec) {
+// LDS: the x region first (digits, 3 k bytes, then the group data, k bytes),
+// so that its reads' offsets fit the 16-bit offset field of the LDS
+// instructions; then the slice sums (kRowsRed) and the workgroup's outputs
+// (512 B); then the 8 wave buffers.
+__host__ __device__ constexpr uint32_t rows_tiles_at(uint32_t k) { return 4u * k + kRowsRed + 512u; }
+
+template <bool REC, uint32_t KS>
+// amdgpu_waves_per_eu(4): at most 128 VGPRs, so that two workgroups share a CU.
+__global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gemv_rows_q6k(
+    WeightView wv, const float *__restrict__ x, float *__restrict__ y, uint8_t *__restrict__ rec) {
+  constexpr uint32_t RG = kRowsWaves / KS;                 // row groups
+  constexpr uint32_t T = kRowsPerWG / (RG * kRowsTile);    // tiles per wave
   extern __shared__ __align__(16) uint8_t lds[];
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t k = wv.k, bpr = wv.bpr, rows = wv.rows;
-  uint8_t *const tile = lds + wave * kRowsBuf;
-  uint8_t *const xl = lds + kRowsWaves * kRowsBuf;
-  const uint32_t rg = wave / kRowsKS, ks = wave % kRowsKS;
-  const uint32_t r0 = (blockIdx.x * kRowsGroups + rg) * kRowsTile;
-  const uint32_t j0 = ks * bpr / kRowsKS, j1 = (ks + 1u) * bpr / kRowsKS;
+  uint8_t *const xl = lds;
+  uint8_t *const tile = lds + rows_tiles_at(k) + wave * kRowsBuf;
+  float *const red = (float *)(lds + 4u * k);                   // slice sums
+  uint32_t *const fin = (uint32_t *)(lds + 4u * k + kRowsRed);   // the workgroup's outputs, for the record
+  const uint32_t rg = wave / KS, ks = wave % KS;
+  const uint32_t ncol = bpr > ks ? (bpr - ks + KS - 1u) / KS : 0u;   // block columns of this slice
   const rsrc_t src = make_rsrc(wv.w, wv.w_bytes);
+  // first row of tile t of this wave
+  auto tile_row = [&](uint32_t t) { return blockIdx.x * kRowsPerWG + (t * RG + rg) * kRowsTile; };
 
   // Load i of the lane fills LDS chunk s = 64 i + lane = row s / 15, chunk
   // s % 15 of that row; chunk 14 repeats 13 (a cache hit) so that rows are
-  // 240 bytes apart; slots past the 32 rows repeat row 31.
-  uint32_t srow[8], sch[8];
+  // 240 bytes apart; slots past the 32 rows repeat row 31. A tile row starts
+  // at its block's 4-byte aligned byte. Block (r, j) starts at
+  // B = (r bpr + j) 210, B mod 4 = 2 ((r bpr + j) mod 2); with tile rows
+  // r = r0 + rsub (r0 even) and bpr even, B - B mod 4 = S + rsub bpr 210 for
+  // S = (r0 bpr + j) 210 - 2 (j mod 2): a per-lane constant plus S.
+  auto slot = [&](uint32_t i, uint32_t &rs, uint32_t &ch) {
+    const uint32_t sl = 64u * i + lane, r = sl / 15u, c = sl - 15u * r;
+    rs = min(r, kRowsTile - 1u);
+    ch = r >= kRowsTile ? 0u : 16u * min(c, 13u);
+  };
+  uint32_t voff[8];
 #pragma unroll
   for (uint32_t i = 0; i < 8; ++i) {
-    const uint32_t sl = 64u * i + lane, r = sl / 15u, c = sl - 15u * r;
-    srow[i] = min(r0 + min(r, kRowsTile - 1u), rows - 1u);
-    sch[i] = r >= kRowsTile ? 0u : 16u * min(c, 13u);
+    uint32_t rs, ch;
+    slot(i, rs, ch);
+    voff[i] = rs * bpr * 210u + ch;
   }
-  auto issue = [&](uint32_t j) {
+  const bool even = (bpr & 1u) == 0u;
+  auto issue = [&](uint32_t t, uint32_t j) {
+    const uint32_t r0 = tile_row(t);
+    if (even && r0 + kRowsTile <= rows) {
+      const uint32_t S = (r0 * bpr + j) * 210u - 2u * (j & 1u);
 #pragma unroll
-    for (uint32_t i = 0; i < 8; ++i) dma16(src, tile + 1024u * i, (((srow[i] * bpr + j) * 210u) & ~3u) + sch[i], 0);
+      for (uint32_t i = 0; i < 8; ++i) dma16(src, tile + 1024u * i, S + voff[i], 0);
+    } else {
+      // odd block count or the matrix's last rows: each row's own start, rows clamped
+#pragma unroll
+      for (uint32_t i = 0; i < 8; ++i) {
+        uint32_t rs, ch;
+        slot(i, rs, ch);
+        const uint32_t r = min(r0 + rs, rows - 1u);
+        dma16(src, tile + 1024u * i, (((r * bpr + j) * 210u) & ~3u) + ch, 0);
+      }
+    }
   };
-  if (j0 < j1) issue(j0);
+  if (ncol) issue(0u, ks);
 
-  // x digits of the whole k, once per workgroup
+  // x digits and group data of the whole k, once per workgroup
+  int32_t *const meta = (int32_t *)(xl + 3u * k);
   for (uint32_t o = tid; o < k / 8u; o += kRowsWaves * 64u) {
     XOct v;
     x_load<1>(x, k, o, v);
-    x_store<1>(v, k, o, xl, k * 3u, (float *)(xl + k * 3u), k / 8u);
+    x_store_tsum(v, o, xl, meta);
   }
   __syncthreads();
-  const uint8_t *dig = xl;
-  const float *meta = (const float *)(xl + k * 3u);
 
   const uint32_t rr = lane & 31u, n = lane >> 5;
-  const uint32_t row = r0 + rr, rowc = min(row, rows - 1u);
-  float acc = 0.f;
-  for (uint32_t j = j0; j < j1; ++j) {
-    wait_vm<0>();   // this tile's loads (the only ones in flight)
-    const uint8_t *t = tile + kRowsPitch * rr;
-    uint32_t a[20], q[12], sv[8];
+  const uint8_t *tp = tile + kRowsPitch * rr;         // this lane's tile row
+#pragma unroll 1
+  for (uint32_t t = 0; t < T; ++t) {
+    float acc = 0.f;
+    const uint32_t rowc = min(tile_row(t) + rr, rows - 1u);
+    // block (rowc, j) starts sh = B mod 4 bytes past its row's copy in LDS
+    const uint32_t par = even ? 0u : ((rowc * bpr) & 1u);
+    for (uint32_t c = 0; c < ncol; ++c) {
+      const uint32_t j = ks + KS * c;
+      wait_vm<0>();   // this tile's loads (the only ones in flight)
+      uint32_t a[20], q[12];
 #pragma unroll
-    for (uint32_t i = 0; i < 5; ++i) {
-      const u32x4 v = *(const u32x4 *)(t + 64u * n + 16u * i);
-      a[4 * i] = v.x; a[4 * i + 1] = v.y; a[4 * i + 2] = v.z; a[4 * i + 3] = v.w;
-    }
-#pragma unroll
-    for (uint32_t i = 0; i < 3; ++i) {
-      const u32x4 v = *(const u32x4 *)(t + 128u + 32u * n + 16u * i);
-      q[4 * i] = v.x; q[4 * i + 1] = v.y; q[4 * i + 2] = v.z; q[4 * i + 3] = v.w;
-    }
-#pragma unroll
-    for (uint32_t i = 0; i < 2; ++i) {
-      const u32x4 v = *(const u32x4 *)(t + 192u + 16u * i);
-      sv[4 * i] = v.x; sv[4 * i + 1] = v.y; sv[4 * i + 2] = v.z; sv[4 * i + 3] = v.w;
-    }
-    // the tile is in registers: the buffer takes the next block column
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-    if (j + 1u < j1) issue(j + 1u);
-    // the block starts sh = 0 or 2 bytes past the aligned start of its row's copy
-    const uint32_t sh = ((rowc * bpr + j) * 210u) & 3u;
-    uint32_t QL[16], QH[8];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) QL[i] = __builtin_amdgcn_alignbyte(a[i + 1], a[i], sh);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) QH[i] = __builtin_amdgcn_alignbyte(q[i + 1], q[i], sh);
-    const uint32_t s0 = __builtin_amdgcn_alignbyte(sv[2 * n + 1], sv[2 * n], sh);
-    const uint32_t s1 = __builtin_amdgcn_alignbyte(sv[2 * n + 2], sv[2 * n + 1], sh);
-    const uint32_t dw = __builtin_amdgcn_alignbyte(sv[5], sv[4], sh);
-    // this half's x: 8 runs of 16 from k = 256 j + 128 n
-    const uint8_t *dj = dig + (16u * j + 8u * n) * 48u;
-    const float *mj = meta + 4u * (8u * j + 4u * n);
-    float accb = 0.f;
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        // weights 32 g + 16 hh + 4 i .. + 3 of the half (ql nibble, 2 bits of qh)
-        uint32_t u[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int lc = 4 * hh + i;
-          const uint32_t ql = QL[8 * (g & 1) + lc], qh = QH[lc];
-          const uint32_t lo = (g & 2) ? (ql >> 4) : ql;
-          const uint32_t hi = g == 0 ? (qh << 4) : g == 1 ? (qh << 2) : g == 2 ? qh : (qh >> 2);
-          u[i] = (lo & 0x0F0F0F0Fu) | (hi & 0x30303030u);
-        }
-        const uint32_t run = 2u * g + hh;   // 16-weight run of the half
-        const uint8_t *dA = dj + run * 48u;
-        int D[3];
-#pragma unroll
-        for (int p = 0; p < 3; ++p) {
-          const u32x4 X = *(const u32x4 *)(dA + 16 * p);
-          int d = __builtin_amdgcn_sdot4((int)u[0], (int)X.x, 0, false);
-          d = __builtin_amdgcn_sdot4((int)u[1], (int)X.y, d, false);
-          d = __builtin_amdgcn_sdot4((int)u[2], (int)X.z, d, false);
-          D[p] = __builtin_amdgcn_sdot4((int)u[3], (int)X.w, d, false);
-        }
-        const float4 M = *(const float4 *)(mj + 4u * (run / 2u));   // {p, sum x[0..15], sum x[16..31]}
-        const float s16 = hh ? M.z : M.y;
-        const float sc = (float)(int)__builtin_amdgcn_sbfe((int)(run < 4u ? s0 : s1), 8u * (run & 3u), 8);
-        const float f = __builtin_fmaf((float)(D[2] * 256 + D[1]), 256.f, (float)D[0]);
-        accb = __builtin_fmaf(sc, __builtin_fmaf(M.x, f, -32.f * s16), accb);
+      for (uint32_t i = 0; i < 5; ++i) {
+        const u32x4 v = *(const u32x4 *)(tp + 64u * n + 16u * i);
+        a[4 * i] = v.x; a[4 * i + 1] = v.y; a[4 * i + 2] = v.z; a[4 * i + 3] = v.w;
       }
-    acc = __builtin_fmaf(h2f(dw & 0xFFFFu), accb, acc);
-  }
-  // the two halves of a row, then its two k slices in order
-  acc += __shfl_xor(acc, 32);
-  float *red = (float *)xl;   // the x digits are no longer read
-  __syncthreads();
-  if (n == 0u) red[wave * kRowsTile + rr] = acc;
-  __syncthreads();
-  uint32_t *fin = (uint32_t *)(xl + 1024u);   // the workgroup's outputs, for the record
-  if (ks == 0u && n == 0u) {
-    float v = red[wave * kRowsTile + rr];
 #pragma unroll
-    for (uint32_t q2 = 1; q2 < kRowsKS; ++q2) v += red[(wave + q2) * kRowsTile + rr];
+      for (uint32_t i = 0; i < 3; ++i) {
+        const u32x4 v = *(const u32x4 *)(tp + 128u + 32u * n + 16u * i);
+        q[4 * i] = v.x; q[4 * i + 1] = v.y; q[4 * i + 2] = v.z; q[4 * i + 3] = v.w;
+      }
+      // this half's 8 scales (bytes 192 + 8n ..) and d (bytes 208, 209)
+      const uint2 sw = *(const uint2 *)(tp + 192u + 8u * n);
+      const uint32_t sw2 = *(const uint32_t *)(tp + 200u + 8u * n);
+      const uint2 dd = *(const uint2 *)(tp + 208u);
+      // the tile is in registers: the buffer takes the next one
+      __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+      {
+        const bool last = c + 1u >= ncol;
+        const uint32_t tn = last ? t + 1u : t;
+        if (tn < T) issue(tn, last ? ks : j + KS);
+      }
+      const uint32_t sh = 2u * ((par + j) & 1u);
+      uint32_t QL[16], QH[8];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) QL[i] = __builtin_amdgcn_alignbyte(a[i + 1], a[i], sh);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) QH[i] = __builtin_amdgcn_alignbyte(q[i + 1], q[i], sh);
+      const uint32_t s0 = __builtin_amdgcn_alignbyte(sw.y, sw.x, sh);
+      const uint32_t s1 = __builtin_amdgcn_alignbyte(sw2, sw.y, sh);
+      const uint32_t dw = __builtin_amdgcn_alignbyte(dd.y, dd.x, sh);
+      // this half's x: 8 runs of 16 from k = 256 j + 128 n; its 4 groups' data
+      const uint8_t *dj = xl + (16u * j + 8u * n) * 48u;
+      const int32_t *mj = meta + 8u * (8u * j + 4u * n);
+      float accb = 0.f;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int4 Ma = *(const int4 *)(mj + 8 * g);       // -32 T of values 0..15, p
+        const int4 Mb = *(const int4 *)(mj + 8 * g + 4);   // -32 T of values 16..31
+        float accg = 0.f;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          // weights 32 g + 16 hh + 4 i .. + 3 of the half (ql nibble, 2 bits of qh)
+          uint32_t u[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int lc = 4 * hh + i;
+            const uint32_t ql = QL[8 * (g & 1) + lc], qh = QH[lc];
+            const uint32_t lo = (g & 2) ? (ql >> 4) : ql;
+            const uint32_t hi = g == 0 ? (qh << 4) : g == 1 ? (qh << 2) : g == 2 ? qh : (qh >> 2);
+            u[i] = (lo & 0x0F0F0F0Fu) | (hi & 0x30303030u);
+          }
+          const uint32_t run = 2u * g + hh;   // 16-weight run of the half
+          const uint8_t *dA = dj + run * 48u;
+          const int init[3] = {hh ? Mb.x : Ma.x, hh ? Mb.y : Ma.y, hh ? Mb.z : Ma.z};
+          int D[3];
+#pragma unroll
+          for (int pp = 0; pp < 3; ++pp) {
+            const u32x4 X = *(const u32x4 *)(dA + 16 * pp);
+            int d = __builtin_amdgcn_sdot4((int)u[0], (int)X.x, init[pp], false);
+            d = __builtin_amdgcn_sdot4((int)u[1], (int)X.y, d, false);
+            d = __builtin_amdgcn_sdot4((int)u[2], (int)X.z, d, false);
+            D[pp] = __builtin_amdgcn_sdot4((int)u[3], (int)X.w, d, false);
+          }
+          // sum (u - 32) digits, as sum over planes of 256^d D_d (|D_d| < 2^17)
+          const float f = __builtin_fmaf((float)(D[2] * 256 + D[1]), 256.f, (float)D[0]);
+          const float sc = (float)(int)__builtin_amdgcn_sbfe((int)(run < 4u ? s0 : s1), 8u * (run & 3u), 8);
+          accg = __builtin_fmaf(sc, f, accg);
+        }
+        accb = __builtin_fmaf(__builtin_bit_cast(float, Ma.w), accg, accb);
+      }
+      acc = __builtin_fmaf(h2f(dw & 0xFFFFu), accb, acc);
+    }
+    // the two halves of a row; the slice sum of the row
+    acc += __shfl_xor(acc, 32);
+    if (n == 0u) red[((t * RG + rg) * KS + ks) * kRowsTile + rr] = acc;
+  }
+  // a row's KS slice sums in order
+  __syncthreads();
+  if (tid < kRowsPerWG) {
+    const uint32_t qt = tid / kRowsTile, r = tid % kRowsTile, row = blockIdx.x * kRowsPerWG + tid;
+    float v = red[qt * KS * kRowsTile + r];
+#pragma unroll
+    for (uint32_t s2 = 1; s2 < KS; ++s2) v += red[(qt * KS + s2) * kRowsTile + r];
     if (row < rows) y[row] = v;
-    if constexpr (REC) fin[rg * kRowsTile + rr] = __builtin_bit_cast(uint32_t, v);
+    if constexpr (REC) fin[tid] = __builtin_bit_cast(uint32_t, v);
   }
   if constexpr (REC) {
     __syncthreads();
@@ -199,31 +252,39 @@ __global__ __launch_bounds__(kRowsWaves * 64) void k_gemv_rows_q6k(WeightView wv
 }  // namespace
 
 bool gemv_rows_applies(const WeightView &wv, uint32_t tokens) {
-  return wv.type == Q6_K && tokens == 1u && wv.rows >= kRowsMin && wv.k <= kRowsMaxK && wv.bpr >= kRowsKS &&
+  return wv.type == Q6_K && tokens == 1u && wv.rows >= kRowsMin && wv.k <= kRowsMaxK && wv.bpr >= 2u &&
          (uint64_t)wv.rows * wv.row_bytes + 16u < (1ull << 32);   // 32-bit byte offsets
 }
 
 uint32_t gemv_rows_groups(const WeightView &wv) { return (wv.rows + kRowsPerWG - 1u) / kRowsPerWG; }
 uint32_t gemv_rows_group_size() { return kRowsPerWG; }
 
-hipError_t launch_gemv_rows(const WeightView &wv, const float *x, float *y, uint8_t *rec, hipStream_t s) {
-  if (!gemv_rows_applies(wv, 1u)) return hipErrorInvalidValue;
-  static bool attr[2] = {false, false};
-  const void *fn = rec ? (const void *)k_gemv_rows_q6k<true> : (const void *)k_gemv_rows_q6k<false>;
-  if (!attr[rec ? 1 : 0]) {
+template <bool REC, uint32_t KS>
+hipError_t launch_rows_ks(const WeightView &wv, const float *x, float *y, uint8_t *rec, uint32_t lds, hipStream_t s) {
+  static bool attr = false;
+  const void *fn = (const void *)k_gemv_rows_q6k<REC, KS>;
+  if (!attr) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMxMaxLds);
     if (e != hipSuccess) return e;
-    attr[rec ? 1 : 0] = true;
+    attr = true;
   }
-  // the x digits region also holds the slice sums (1 KB) and the outputs (512 B) at the end
-  const uint32_t xbytes = wv.k * 3u + (wv.k / 8u) * 4u;
-  const uint32_t lds = kRowsWaves * kRowsBuf + (xbytes > 1536u ? xbytes : 1536u);
-  const uint32_t grid = gemv_rows_groups(wv);
-  if (rec)
-    hipLaunchKernelGGL((k_gemv_rows_q6k<true>), dim3(grid), dim3(kRowsWaves * 64), lds, s, wv, x, y, rec);
-  else
-    hipLaunchKernelGGL((k_gemv_rows_q6k<false>), dim3(grid), dim3(kRowsWaves * 64), lds, s, wv, x, y, rec);
+  hipLaunchKernelGGL((k_gemv_rows_q6k<REC, KS>), dim3(gemv_rows_groups(wv)), dim3(kRowsWaves * 64), lds, s, wv, x, y,
+                     rec);
   return hipGetLastError();
+}
+
+template <bool REC>
+hipError_t launch_rows(const WeightView &wv, const float *x, float *y, uint8_t *rec, uint32_t lds, hipStream_t s) {
+  // as many k slices as block columns, up to the 8 waves
+  if (wv.bpr >= 8u) return launch_rows_ks<REC, 8>(wv, x, y, rec, lds, s);
+  if (wv.bpr >= 4u) return launch_rows_ks<REC, 4>(wv, x, y, rec, lds, s);
+  return launch_rows_ks<REC, 2>(wv, x, y, rec, lds, s);
+}
+
+hipError_t launch_gemv_rows(const WeightView &wv, const float *x, float *y, uint8_t *rec, hipStream_t s) {
+  if (!gemv_rows_applies(wv, 1u)) return hipErrorInvalidValue;
+  const uint32_t lds = rows_tiles_at(wv.k) + kRowsWaves * kRowsBuf;
+  return rec ? launch_rows<true>(wv, x, y, rec, lds, s) : launch_rows<false>(wv, x, y, rec, lds, s);
 }
 
 }  // namespace eff
