@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/elffuss_amd.h"
 #include "eff_kernels.h"
 
 namespace eff {
@@ -80,7 +81,10 @@ __device__ __forceinline__ uint64_t wave_ext64(uint64_t v) {
 
 // The group's record from the lanes' own 4 largest (every lane of the wave
 // active): 4 rounds of a wave maximum over the lanes' heads; lanes 0..3 write
-// the 64 bytes at `rec`.
+// the 64 bytes at `rec`. WT: as device-scope atomic stores, which write
+// through to memory, so that a workgroup on another XCD can read the record
+// once the writer's stores have completed.
+template <bool WT = false>
 __device__ __forceinline__ void topk_record_wave(Top4 t, bool nan, uint8_t *rec) {
   const uint32_t lane = threadIdx.x & 63u;
   uint64_t out_c[4];
@@ -111,7 +115,387 @@ __device__ __forceinline__ void topk_record_wave(Top4 t, bool nan, uint8_t *rec)
     } else {
       v = make_uint4(any_nan ? 1u : 0u, 0u, 0u, 0u);
     }
-    ((uint4 *)rec)[lane] = v;
+    if constexpr (WT) {
+      uint32_t *w = (uint32_t *)rec + 4u * lane;
+      __hip_atomic_store(w, v.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(w + 1, v.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(w + 2, v.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(w + 3, v.w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      ((uint4 *)rec)[lane] = v;
+    }
+  }
+}
+
+// ---- the selection over the records (k_topk_pick and the row GEMV's last
+// workgroup) ----------------------------------------------------------------
+
+struct TopkPenal {
+  uint32_t ids[EFF_TOPK_P_MAX];
+};
+
+constexpr uint32_t kCandMax = 4u * EFF_TOPK_M_MAX;   // listed composites >= tau at most
+
+// Inclusive prefix sum over the 64 lanes of a wave (every lane active): DPP
+// shifts within rows of 16, then the row totals broadcast to the rows above.
+__device__ __forceinline__ uint32_t wave_scan(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);   // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true);   // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true);   // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true);   // row_shr:8
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return v;
+}
+
+// LDS of a selection by NT threads holding R records each.
+template <int NT, int R>
+struct PickLds {
+  uint32_t hist[256];   // bin 255 - d counts digit d (descending digits in ascending bins)
+  uint32_t st[4];
+  uint32_t flags, nsat, ncand, nsel;
+  uint64_t wmin[NT / 64], wmax[NT / 64], wkth[NT / 64];
+  uint32_t satg[NT * R];
+  alignas(16) uint64_t cand_c[kCandMax + 4];   // 4 zero entries past the candidates (rank reads in pairs)
+  uint32_t cand_b[kCandMax];
+  uint32_t cand_r[kCandMax];
+};
+
+// Radix select over distinct 64-bit candidates: returns T such that exactly
+// `need` candidates are >= T (1 <= need <= number of candidates). Each round
+// finds the smallest and largest candidate still in play, places an 8-bit
+// digit window at their highest differing bit, and keeps the bin that holds
+// the need-th largest. `visit(f)` calls f(c) for each candidate the calling
+// thread holds. Every thread of the workgroup calls it.
+template <int NT, class Visit, class L>
+__device__ uint64_t select_top(uint32_t need, Visit visit, L &sh) {
+  constexpr int NW = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint64_t lo = 0, hi = ~(uint64_t)0;
+  uint32_t rem = need;
+  for (int round = 0; round < 16; ++round) {
+    uint64_t mn = ~(uint64_t)0, mx = 0;
+    visit([&](uint64_t c) {
+      if (c >= lo && c <= hi) {
+        mn = c < mn ? c : mn;
+        mx = c > mx ? c : mx;
+      }
+    });
+    mn = wave_ext64<false>(mn);
+    mx = wave_ext64<true>(mx);
+    if (lane == 0) {
+      sh.wmin[wave] = mn;
+      sh.wmax[wave] = mx;
+    }
+    if (tid < 256) sh.hist[tid] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      mn = sh.wmin[w] < mn ? sh.wmin[w] : mn;
+      mx = sh.wmax[w] > mx ? sh.wmax[w] : mx;
+    }
+    if (mn == mx) return mn;  // one candidate left in play: the need-th
+    const int hb = 63 - __builtin_clzll(mn ^ mx);
+    const int shift = hb >= 7 ? hb - 7 : 0;
+    const uint64_t top = shift + 8 >= 64 ? 0 : (mx >> (shift + 8)) << (shift + 8);  // bits above the window
+    visit([&](uint64_t c) {
+      if (c >= lo && c <= hi) atomicAdd(&sh.hist[255u - ((uint32_t)(c >> shift) & 255u)], 1u);
+    });
+    __syncthreads();
+    if (wave == 0) {
+      // lane l holds bins 4l .. 4l+3, i.e. digits 255 - 4l down to 252 - 4l
+      const uint4 h = *(const uint4 *)(sh.hist + 4 * lane);
+      const uint32_t hh[4] = {h.x, h.y, h.z, h.w};
+      const uint32_t tot = h.x + h.y + h.z + h.w;
+      uint32_t above = wave_scan(tot) - tot;  // candidates in play with larger digits
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (above < rem && above + hh[q] >= rem) {
+          sh.st[0] = 255u - (uint32_t)(4 * lane + q);
+          sh.st[1] = rem - above;
+          sh.st[2] = hh[q] == rem - above ? 1u : 0u;
+        }
+        above += hh[q];
+      }
+    }
+    __syncthreads();
+    const uint32_t digit = sh.st[0];
+    const uint64_t blo = top | ((uint64_t)digit << shift);
+    if (sh.st[2]) return blo;   // the bin and everything above it: exactly need
+    rem = sh.st[1];
+    lo = blo;
+    hi = blo + (((uint64_t)1 << shift) - 1u);
+  }
+  return lo;  // not reached: each round narrows the candidates in play
+}
+
+// The top-m selection over `groups` records of groups of gs consecutive
+// logits (record g at rec + 64 g), by the NT threads of one workgroup, thread
+// t holding the records of groups t + NT r (r < R); writes the output record
+// of kernels.topk.wgsl.js:40-60.
+//
+// tau: a lower bound of the need-th largest group maximum. Every one of the
+// overall need largest elements is >= the need-th largest maximum, so the
+// need largest of the listed composites >= tau (ranked by counting) are the
+// answer, unless some group has more than 4 elements and its 4th listed
+// composite is among them ("saturated"): an element a group does not list is
+// below its 4th, and if that 4th is not selected, need listed composites beat
+// it. Otherwise the select runs again over the unsaturated groups' lists plus
+// every element of the saturated groups, read from memory. The winners are
+// written sorted by (value desc, index asc).
+//
+// tau is first the smallest of the waves' kw-th largest maxima, kw =
+// ceil(need / NW) (NW kw >= need of the maxima are >= it, so it is a lower
+// bound; need <= 64 here): kw rounds of a wave maximum, no selection. When that leaves more listed composites
+// than the candidate space, or need > 64, tau is the need-th largest maximum
+// exactly, by select_top (then at most 4 need composites are listed >= it).
+template <int NT, int R>
+__device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, uint32_t m, const TopkPenal &penal,
+                          uint32_t n_penal, uint32_t serial, uint32_t gs, uint32_t groups,
+                          const uint8_t *__restrict__ rec, uint32_t *__restrict__ out, PickLds<NT, R> &sh) {
+  constexpr int NW = NT / 64, KW = 64 / NW;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint64_t c[R][4];
+  uint32_t b[R][4];
+  uint32_t nan = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t g = (uint32_t)tid + NT * r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { c[r][i] = 0u; b[r][i] = 0u; }
+    if (g < groups) {
+      const uint4 *rp = (const uint4 *)(rec + (uint64_t)g * kTopkRecordBytes);
+      const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2], q3 = rp[3];
+      c[r][0] = ((uint64_t)q0.y << 32) | q0.x;
+      c[r][1] = ((uint64_t)q0.w << 32) | q0.z;
+      c[r][2] = ((uint64_t)q1.y << 32) | q1.x;
+      c[r][3] = ((uint64_t)q1.w << 32) | q1.z;
+      b[r][0] = q2.x; b[r][1] = q2.y; b[r][2] = q2.z; b[r][3] = q2.w;
+      nan |= q3.x;
+    }
+  }
+  // penalised ids: their raw logits (the penalty itself is applied by the sampler)
+  uint32_t pv = 0u;
+  if ((uint32_t)tid < n_penal && penal.ids[tid] < vocab) pv = logits[penal.ids[tid]];
+  const bool wnan = __ballot(nan != 0u) != 0u;
+  if (tid == 0) {
+    sh.flags = 0u;
+    sh.nsat = 0u;
+    sh.ncand = 0u;
+    sh.nsel = 0u;
+  }
+  __syncthreads();
+  if (lane == 0 && wnan) atomicOr(&sh.flags, 2u);
+  const uint32_t need = min(m, vocab);
+  // the listed composites >= th into the candidate space (counted past it):
+  // a wave prefix sum of the lanes' counts and one LDS atomic per wave
+  auto compact = [&](uint64_t th) {
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cnt += (c[r][i] && c[r][i] >= th) ? 1u : 0u;
+    const uint32_t incl = wave_scan(cnt);
+    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    uint32_t base = 0;
+    if (total) {
+      if (lane == 0) base = atomicAdd(&sh.ncand, total);
+      base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+    }
+    uint32_t q = base + incl - cnt;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (c[r][i] && c[r][i] >= th) {
+          if (q < kCandMax) {
+            sh.cand_c[q] = c[r][i];
+            sh.cand_b[q] = b[r][i];
+          }
+          ++q;
+        }
+      }
+  };
+  uint64_t tau = 0;
+  uint32_t nc = 0;
+  bool done = false;
+  if (groups > need && need <= (uint32_t)(NW * KW)) {
+    // on the maxima's high words (order keys): kth = the wave's kw-th largest
+    // distinct key, tq = the smallest composite with the waves' smallest such
+    // key (0, and the exact tau below, when a wave runs out of keys). Equal
+    // keys leave at most fewer distinct values, so tq stays a lower bound.
+    uint32_t v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = (uint32_t)(c[r][0] >> 32);
+    uint32_t kth = 0;
+    const int kw = (int)((need + NW - 1u) / NW);   // NW kw >= need of the maxima are >= tq
+    for (int q = 0; q < kw; ++q) {
+      uint32_t lb = 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) lb = v[r] > lb ? v[r] : lb;
+      kth = wave_ext<true>(lb);   // 0 once the wave's maxima run out
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[r] = v[r] == kth ? 0u : v[r];
+    }
+    if (lane == 0) sh.wkth[wave] = (uint64_t)kth << 32;
+    __syncthreads();
+    uint64_t tq = ~(uint64_t)0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) tq = sh.wkth[w] < tq ? sh.wkth[w] : tq;
+    if (tq != 0u) {
+      compact(tq);
+      __syncthreads();
+      nc = sh.ncand;
+      __syncthreads();
+      if (nc <= kCandMax) {
+        tau = tq;
+        done = true;
+      } else if (tid == 0) {
+        sh.ncand = 0u;   // too many: the exact tau below
+      }
+    }
+  }
+  if (!done) {
+    if (groups > need) {
+      // the need-th largest group maximum
+      tau = select_top<NT>(need, [&](auto f) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (c[r][0]) f(c[r][0]);
+      }, sh);
+    }
+    compact(tau);
+    __syncthreads();
+    nc = min(sh.ncand, kCandMax);
+  }
+  if (tid < 4) sh.cand_c[nc + tid] = 0u;   // the zero entries past the candidates
+  __syncthreads();
+  uint64_t T = 0;        // exactly `need` candidates (of the final set) are >= T
+  bool ranked = false;   // cand_r holds every candidate's rank
+  if (nc <= need) {
+    // exactly the need candidates >= tau (tau is then one of them, a group
+    // maximum); or, with no more groups than need, every listed composite
+    // (groups with more than 4 elements then count as saturated below and are
+    // read whole)
+    T = groups > need ? tau : 0;
+  } else {
+    // rank = candidates above, counted by P threads of one wave per candidate,
+    // each over a contiguous quarter-aligned range read in pairs (the zero
+    // entries past the candidates count for nothing: every composite is > 0)
+    uint32_t P = 64;
+    while (P > 1 && nc * P > (uint32_t)NT) P >>= 1;
+    const uint32_t span = ((nc + P - 1u) / P + 3u) & ~3u;
+    for (uint32_t i0 = 0; i0 < nc; i0 += NT / P) {
+      const uint32_t i = i0 + (uint32_t)tid / P, part = (uint32_t)tid % P;
+      uint32_t rank = 0;
+      uint64_t ci = 0;
+      if (i < nc) {
+        ci = sh.cand_c[i];
+        const uint32_t j0 = part * span, j1 = min(j0 + span, (nc + 3u) & ~3u);
+#pragma unroll 4
+        for (uint32_t j = j0; j < j1; j += 4u) {
+          const ulonglong2 p0 = *(const ulonglong2 *)(sh.cand_c + j);
+          const ulonglong2 p1 = *(const ulonglong2 *)(sh.cand_c + j + 2);
+          rank += (p0.x > ci ? 1u : 0u) + (p0.y > ci ? 1u : 0u) + (p1.x > ci ? 1u : 0u) + (p1.y > ci ? 1u : 0u);
+        }
+      }
+      for (uint32_t o = 1; o < P; o <<= 1) rank += (uint32_t)__shfl_xor((int)rank, (int)o, 64);
+      if (i < nc && part == 0u) {
+        sh.cand_r[i] = rank;
+        if (rank == need - 1u) sh.wmin[0] = ci;   // the need-th largest candidate
+      }
+    }
+    __syncthreads();
+    T = sh.wmin[0];
+    ranked = true;
+  }
+  // saturated groups: more than 4 elements and the 4th listed one selected
+  bool sat[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t g = (uint32_t)tid + NT * r;
+    const uint32_t gcount = g < groups ? min(gs, vocab - g * gs) : 0u;
+    sat[r] = gcount > 4u && c[r][3] >= T;
+    if (sat[r]) sh.satg[atomicAdd(&sh.nsat, 1u)] = g;
+  }
+  __syncthreads();
+  const uint32_t ns = sh.nsat;
+  uint32_t *pairs = out + EFF_TOPK_HEADER + EFF_TOPK_P_MAX;
+  uint32_t n = need;
+  if (ns == 0u && ranked) {
+    // the candidates' ranks are final: the winners go straight to their slots
+    for (uint32_t i = (uint32_t)tid; i < nc; i += NT) {
+      if (sh.cand_r[i] < need) {
+        pairs[2 * sh.cand_r[i]] = ~(uint32_t)sh.cand_c[i];
+        pairs[2 * sh.cand_r[i] + 1] = sh.cand_b[i];
+      }
+    }
+  } else {
+    auto stream = [&](auto f) {
+      for (uint32_t i = (uint32_t)tid; i < ns * gs; i += NT) {
+        const uint32_t e = sh.satg[i / gs] * gs + i % gs;
+        if (e < vocab) {
+          const uint32_t bits = logits[e];
+          f(composite(bits, e), bits);
+        }
+      }
+    };
+    if (ns) {
+      // the unsaturated groups' lists plus every element of the saturated groups
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (sat[r]) c[r][0] = c[r][1] = c[r][2] = c[r][3] = 0u;
+      T = select_top<NT>(need, [&](auto f) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (c[r][i]) f(c[r][i]);
+        stream([&](uint64_t v, uint32_t) { f(v); });
+      }, sh);
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (c[r][i] && c[r][i] >= T) {
+            const uint32_t q = atomicAdd(&sh.nsel, 1u);
+            if (q < EFF_TOPK_M_MAX) { sh.cand_c[q] = c[r][i]; sh.cand_b[q] = b[r][i]; }
+          }
+        }
+      stream([&](uint64_t v, uint32_t bits) {
+        if (v >= T) {
+          const uint32_t q = atomicAdd(&sh.nsel, 1u);
+          if (q < EFF_TOPK_M_MAX) { sh.cand_c[q] = v; sh.cand_b[q] = bits; }
+        }
+      });
+    } else {
+      // winners among the candidates in LDS (all of them: nc <= need), in place
+      if (tid == 0) sh.nsel = nc;
+    }
+    __syncthreads();
+    n = min(sh.nsel, (uint32_t)EFF_TOPK_M_MAX);
+    // rank = winners above, counted by one thread per winner
+    for (uint32_t i = (uint32_t)tid; i < n; i += NT) {
+      const uint64_t ci = sh.cand_c[i];
+      uint32_t rank = 0;
+      for (uint32_t j = 0; j < n; ++j) rank += sh.cand_c[j] > ci ? 1u : 0u;
+      pairs[2 * rank] = ~(uint32_t)ci;
+      pairs[2 * rank + 1] = sh.cand_b[i];
+    }
+  }
+  // unused pair slots, the penalised logits and the header
+  for (uint32_t slot = n + (uint32_t)tid; slot < EFF_TOPK_CAP; slot += NT) {
+    pairs[2 * slot] = 0u;
+    pairs[2 * slot + 1] = 0u;
+  }
+  if (tid < (int)EFF_TOPK_P_MAX) out[EFF_TOPK_HEADER + tid] = pv;
+  if (tid == 0) {
+    out[0] = n;
+    out[1] = sh.flags | (n != need ? 4u : 0u);
+    out[2] = n_penal;
+    out[3] = (vocab + kTopkRecordChunk - 1u) / kTopkRecordChunk;
+    out[4] = serial;
+    out[5] = out[6] = out[7] = 0u;
   }
 }
 
