@@ -305,10 +305,12 @@ int eff_topk(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint3
  * the output projection fused with top-k = 40 of north_star's configuration
  * 4; the reference runs the two as separate passes (model.js:1145-1177, then
  * createTopKGPU().candidatos, ops.topk.js:99-165). For Q6_K matrices of
- * 32768 .. 131072 rows the GEMV kernel also writes the top-k's per-group
- * records and one more launch selects from them; other shapes run the GEMV
- * and eff_topk. The same NOT_APPLICABLE cases as eff_topk, checked before
- * anything is enqueued. */
+ * 32768 .. 131072 rows this is one launch: every workgroup of the GEMV also
+ * writes the top-k record of its 128 rows, and the last one to finish selects
+ * from all records. Other shapes run the GEMV and eff_topk. Calls on one
+ * context are stream-ordered; the context's arrival counter is not shared
+ * with other contexts. The same NOT_APPLICABLE cases as eff_topk, checked
+ * before anything is enqueued. */
 int eff_qgemv_topk(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k,
                    uint32_t m, const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, eff_buf *out);
 

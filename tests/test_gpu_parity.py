@@ -153,7 +153,8 @@ def test_gemv_non_finite_x(ctx, eff, gemv_kernel, tname):
 
 # ---- the row GEMV for Q6_K matrices with many rows (the output projection) -------------
 
-@pytest.mark.parametrize("rows,k", [(32768, 512), (32805, 4608), (40001, 2048), (32769, 8192)])
+@pytest.mark.parametrize("rows,k", [(32768, 512), (32805, 4608), (40001, 2048), (32769, 8192), (32800, 2304),
+                                      (33000, 768)])
 def test_gemv_rows_q6_k_vs_f64_oracle(ctx, eff, orc, rows, k):
     """One token of a Q6_K matrix of >= 32768 rows runs the row kernel (a lane
     per half row-block): row counts that are not a multiple of the 128-row
@@ -654,6 +655,8 @@ def test_topk_clustered_in_one_group(ctx, eff, orc, vocab, m):
     ("Q6_K", 65536, 2048, 40, False),      # the C4 head: records from the GEMV, 512 groups
     ("Q6_K", 40001, 2048, 192, True),      # ragged rows; the largest logits in one 128-row group
     ("Q6_K", 65664, 512, 100, True),       # 513 groups
+    ("Q6_K", 65536, 512, 40, True),        # the wave-maximum threshold, then a saturated group read whole
+    ("Q6_K", 40000, 2304, 40, False),      # an odd block count per row (per-row load offsets)
     ("Q6_K", 131073, 512, 40, False),      # more groups than one selection holds: GEMV, then eff_topk
     ("Q8_0", 50000, 512, 40, False),       # no row kernel: GEMV, then eff_topk
 ])
