@@ -868,7 +868,7 @@ int eff_qgemv_topk(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, u
   if ((rc = use_device(ctx))) return rc;
   const float *xp = (const float *)x->ptr;
   float *yp = (float *)y->ptr;
-  if (ctx->gemv_kernel == 0 && gemv_rows_applies(wv, 1) && gemv_rows_groups(wv) <= kTopkPickGroupsMax) {
+  if (ctx->gemv_kernel == 0 && gemv_rows_applies(wv, 1) && gemv_rows_groups(wv) <= kRowsTopkGroupsMax) {
     // one launch: the GEMV writes the top-k's group records and its last
     // workgroup selects from them
     const uint32_t groups = gemv_rows_groups(wv);

@@ -323,7 +323,7 @@ hipError_t launch_gemv_rows_topk(const WeightView &wv, const float *x, float *y,
                                  uint32_t m, const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial,
                                  uint32_t *out, hipStream_t s) {
   const uint32_t groups = gemv_rows_groups(wv);
-  if (!gemv_rows_applies(wv, 1u) || groups > 2u * kRowsWaves * 64u || m == 0 || m > EFF_TOPK_M_MAX ||
+  if (!gemv_rows_applies(wv, 1u) || groups > kRowsTopkGroupsMax || m == 0 || m > EFF_TOPK_M_MAX ||
       n_penal > EFF_TOPK_P_MAX || wv.rows >= EFF_TOPK_N_MAX)
     return hipErrorInvalidValue;
   RowsPick pk{};

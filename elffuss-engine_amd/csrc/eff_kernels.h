@@ -57,9 +57,10 @@ uint32_t gemv_rows_group_size();
 hipError_t launch_gemv_rows(const WeightView &wv, const float *x, float *y, hipStream_t stream);
 // The same GEMV fused with the top-m of its logits (the decode head): every
 // workgroup writes the top-k record of its gemv_rows_group_size() rows to rec
-// (gemv_rows_groups(wv) <= 1024 records); the last one to finish selects from
-// them into out. `arrivals` is a device word that is zero before the launch
+// (gemv_rows_groups(wv) <= kRowsTopkGroupsMax records); the last one to
+// finish selects from them into out. `arrivals` is a device word that is zero before the launch
 // and zero again after it; launches sharing it must not overlap.
+constexpr uint32_t kRowsTopkGroupsMax = 1024;
 hipError_t launch_gemv_rows_topk(const WeightView &wv, const float *x, float *y, uint8_t *rec, uint32_t *arrivals,
                                  uint32_t m, const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial,
                                  uint32_t *out, hipStream_t stream);
@@ -119,12 +120,6 @@ constexpr size_t topk_scratch_bytes_for(uint32_t vocab) { return (size_t)topk_gr
 constexpr size_t kTopkScratchMax = (size_t)kTopkGroupsMax * kTopkRecordBytes;
 size_t topk_scratch_bytes(uint32_t vocab);
 
-// The selecting half alone, over `groups` records (<= kTopkPickGroupsMax) of
-// groups of `gs` consecutive logits written by another kernel.
-constexpr uint32_t kTopkPickGroupsMax = 1024;
-hipError_t launch_topk_pick(const uint32_t *logits, uint32_t vocab, uint32_t m, const uint32_t *penal_ids,
-                            uint32_t n_penal, uint32_t serial, uint32_t gs, uint32_t groups, const uint8_t *rec,
-                            uint32_t *out, hipStream_t stream);
 hipError_t launch_topk(const uint32_t *logits, uint32_t base, uint32_t vocab, uint32_t m,
                        const uint32_t *penal_ids_dev, uint32_t n_penal, uint32_t serial,
                        uint32_t *scratch, uint32_t *out, hipStream_t stream);

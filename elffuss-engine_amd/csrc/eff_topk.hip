@@ -55,40 +55,32 @@ __global__ __launch_bounds__(64) void k_topk_groups(const uint32_t *__restrict__
 
 constexpr int kPickThreads = 256;
 
-// R records per thread: thread t holds the records of groups t + 256 r.
-template <int R>
+// One record per thread (groups <= 256).
 __global__ __launch_bounds__(kPickThreads) void k_topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab,
                                                             uint32_t m, TopkPenal penal, uint32_t n_penal,
                                                             uint32_t serial, uint32_t gs, uint32_t groups,
                                                             const uint8_t *__restrict__ rec,
                                                             uint32_t *__restrict__ out) {
-  __shared__ PickLds<kPickThreads, R> sh;
-  topk_pick<kPickThreads, R>(logits, vocab, m, penal, n_penal, serial, gs, groups, rec, out, sh);
+  __shared__ PickLds<kPickThreads, 1> sh;
+  topk_pick<kPickThreads, 1>(logits, vocab, m, penal, n_penal, serial, gs, groups, rec, out, sh);
+}
+
+// The selecting half alone, over `groups` (<= 256) records of groups of `gs`
+// consecutive logits.
+hipError_t launch_topk_pick(const uint32_t *logits, uint32_t vocab, uint32_t m, const uint32_t *penal_ids,
+                            uint32_t n_penal, uint32_t serial, uint32_t gs, uint32_t groups, const uint8_t *rec,
+                            uint32_t *out, hipStream_t s) {
+  if (groups == 0 || groups > (uint32_t)kPickThreads || (uint64_t)groups * gs < vocab) return hipErrorInvalidValue;
+  TopkPenal pen{};
+  for (uint32_t i = 0; i < n_penal; ++i) pen.ids[i] = penal_ids[i];
+  hipLaunchKernelGGL(k_topk_pick, dim3(1), dim3(kPickThreads), 0, s, logits, vocab, m, pen, n_penal, serial, gs,
+                     groups, rec, out);
+  return hipGetLastError();
 }
 
 }  // namespace
 
 size_t topk_scratch_bytes(uint32_t vocab) { return topk_scratch_bytes_for(vocab); }
-
-hipError_t launch_topk_pick(const uint32_t *logits, uint32_t vocab, uint32_t m, const uint32_t *penal_ids,
-                            uint32_t n_penal, uint32_t serial, uint32_t gs, uint32_t groups, const uint8_t *rec,
-                            uint32_t *out, hipStream_t s) {
-  if (vocab == 0 || vocab >= EFF_TOPK_N_MAX || m == 0 || m > EFF_TOPK_M_MAX || n_penal > EFF_TOPK_P_MAX ||
-      groups == 0 || groups > kTopkPickGroupsMax || (uint64_t)groups * gs < vocab)
-    return hipErrorInvalidValue;
-  TopkPenal pen{};
-  for (uint32_t i = 0; i < n_penal; ++i) pen.ids[i] = penal_ids[i];
-  if (groups <= (uint32_t)kPickThreads)
-    hipLaunchKernelGGL((k_topk_pick<1>), dim3(1), dim3(kPickThreads), 0, s, logits, vocab, m, pen, n_penal, serial, gs,
-                       groups, rec, out);
-  else if (groups <= 2u * kPickThreads)
-    hipLaunchKernelGGL((k_topk_pick<2>), dim3(1), dim3(kPickThreads), 0, s, logits, vocab, m, pen, n_penal, serial, gs,
-                       groups, rec, out);
-  else
-    hipLaunchKernelGGL((k_topk_pick<4>), dim3(1), dim3(kPickThreads), 0, s, logits, vocab, m, pen, n_penal, serial, gs,
-                       groups, rec, out);
-  return hipGetLastError();
-}
 
 hipError_t launch_topk(const uint32_t *logits, uint32_t base, uint32_t vocab, uint32_t m,
                        const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, uint32_t *scratch,
