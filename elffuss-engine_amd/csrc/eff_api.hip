@@ -52,7 +52,6 @@ struct eff_ctx {
   eff_stats stats{};
   void *topk_scratch = nullptr;
   size_t topk_scratch_bytes = 0;
-  uint32_t *arrivals = nullptr;     // the fused head's arrival counter (zero between launches)
   void *xh_scratch = nullptr;       // fp16 copy of the GEMM activations
   size_t xh_scratch_bytes = 0;
   void *sx_scratch = nullptr;       // x as fp16 hi/lo parts for the split-x product
@@ -317,7 +316,6 @@ int eff_shutdown(eff_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->topk_scratch) (void)hipFree(ctx->topk_scratch);
-  if (ctx->arrivals) (void)hipFree(ctx->arrivals);
   if (ctx->xh_scratch) (void)hipFree(ctx->xh_scratch);
   if (ctx->sx_scratch) (void)hipFree(ctx->sx_scratch);
   for (auto &p : ctx->stage_pend) (void)hipEventDestroy(p.ev);
@@ -869,17 +867,12 @@ int eff_qgemv_topk(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, u
   const float *xp = (const float *)x->ptr;
   float *yp = (float *)y->ptr;
   if (ctx->gemv_kernel == 0 && gemv_rows_applies(wv, 1) && gemv_rows_groups(wv) <= kRowsTopkGroupsMax) {
-    // one launch: the GEMV writes the top-k's group records and its last
-    // workgroup selects from them
+    // the GEMV writes the top-k's group records; one launch selects from them
     const uint32_t groups = gemv_rows_groups(wv);
     if ((rc = grow(ctx, &ctx->topk_scratch, &ctx->topk_scratch_bytes, (size_t)groups * kTopkRecordBytes, "topk")))
       return rc;
-    if (!ctx->arrivals) {
-      if (hipMalloc(&ctx->arrivals, 256) != hipSuccess) return fail(ctx, EFF_E_NOMEM, "topk arrival counter");
-      EFF_HIP(ctx, hipMemset(ctx->arrivals, 0, 256));
-    }
-    hipError_t e = launch_gemv_rows_topk(wv, xp, yp, (uint8_t *)ctx->topk_scratch, ctx->arrivals, m, penal_ids,
-                                         n_penal, serial, (uint32_t *)out->ptr, ctx->stream);
+    hipError_t e = launch_gemv_rows_topk(wv, xp, yp, (uint8_t *)ctx->topk_scratch, m, penal_ids, n_penal, serial,
+                                         (uint32_t *)out->ptr, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "gemv+topk launch");
   } else {
     if ((rc = run_gemv(ctx, wv, xp, yp, 1))) return rc;

@@ -56,11 +56,9 @@ constexpr uint32_t kRowsRed = 4096;                   // LDS bytes of the slice 
 constexpr uint32_t kRowsMin = 32768;
 constexpr uint32_t kRowsMaxK = 16384;
 
-// The selection's arguments for the fused head, and the arrival counter
-// (zero before the launch; the last workgroup to arrive resets it).
+// The selection's arguments for the head's top-k.
 struct RowsPick {
   uint32_t *out;
-  uint32_t *arrivals;
   uint32_t m, n_penal, serial;
   TopkPenal penal;
 };
@@ -71,13 +69,12 @@ struct RowsPick {
 // (512 B); then the 8 wave buffers.
 __host__ __device__ constexpr uint32_t rows_tiles_at(uint32_t k) { return 4u * k + kRowsRed + 512u; }
 
-// PR > 0: the fused head. Each workgroup also writes the top-k record of its
-// 128 rows; the last workgroup to finish selects the top-m from all records
-// (topk_pick with PR records per thread) and resets the arrival counter.
-template <int PR, uint32_t KS>
+// REC: the decode head. Each workgroup also writes the top-k record of its
+// 128 rows (their 4 largest logits, eff_topk.h) for k_rows_pick.
+template <bool REC, uint32_t KS>
 // amdgpu_waves_per_eu(4): at most 128 VGPRs, so that two workgroups share a CU.
 __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gemv_rows_q6k(
-    WeightView wv, const float *__restrict__ x, float *__restrict__ y, uint8_t *__restrict__ rec, RowsPick pk) {
+    WeightView wv, const float *__restrict__ x, float *__restrict__ y, uint8_t *__restrict__ rec) {
   constexpr uint32_t RG = kRowsWaves / KS;                 // row groups
   constexpr uint32_t T = kRowsPerWG / (RG * kRowsTile);    // tiles per wave
   extern __shared__ __align__(16) uint8_t lds[];
@@ -237,15 +234,10 @@ __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu
     float v = red[qt * KS * kRowsTile + r];
 #pragma unroll
     for (uint32_t s2 = 1; s2 < KS; ++s2) v += red[(qt * KS + s2) * kRowsTile + r];
-    if constexpr (PR > 0) {
-      // written through to memory, for the selecting workgroup
-      if (row < rows) __hip_atomic_store(y + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      fin[tid] = __builtin_bit_cast(uint32_t, v);
-    } else {
-      if (row < rows) y[row] = v;
-    }
+    if (row < rows) y[row] = v;
+    if constexpr (REC) fin[tid] = __builtin_bit_cast(uint32_t, v);
   }
-  if constexpr (PR > 0) {
+  if constexpr (REC) {
     __syncthreads();
     if (wave == 0u) {
       // rows l and l + 64 of the workgroup's 128
@@ -261,46 +253,42 @@ __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu
           t.add(composite(bits, e), bits);
         }
       }
-      topk_record_wave<true>(t, nan, rec + (uint64_t)blockIdx.x * kTopkRecordBytes);
+      topk_record_wave(t, nan, rec + (uint64_t)blockIdx.x * kTopkRecordBytes);
     }
-    // this workgroup's logits (waves 0, 1) and record (wave 0), written
-    // through, have completed before it counts itself (an agent-scope release
-    // fence would also write back each XCD's whole L2, once per workgroup)
-    if (wave < 2u) __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-    __syncthreads();
-    if (tid == 0) fin[0] = atomicAdd(pk.arrivals, 1u) == gridDim.x - 1u ? 1u : 0u;
-    __syncthreads();
-    // (fin lies past the selection's first LDS writes, made after this read)
-    if (fin[0] == 0u) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // every other workgroup's logits and record
-    topk_pick<kRowsWaves * 64, PR>((const uint32_t *)y, rows, pk.m, pk.penal, pk.n_penal, pk.serial, kRowsPerWG,
-                                   gridDim.x, rec, pk.out, *(PickLds<kRowsWaves * 64, PR> *)lds);
-    if (tid == 0) *pk.arrivals = 0u;
   }
 }
 
-template <int PR, uint32_t KS>
-hipError_t launch_rows_ks(const WeightView &wv, const float *x, float *y, uint8_t *rec, const RowsPick &pk,
-                          uint32_t lds, hipStream_t s) {
+// The selection over the records a k_gemv_rows_q6k<true, KS> launch wrote,
+// by 512 threads with R records each (topk_pick, eff_topk.h).
+template <int R>
+__global__ __launch_bounds__(kRowsWaves * 64) void k_rows_pick(const uint32_t *__restrict__ logits, uint32_t vocab,
+                                                               RowsPick pk, uint32_t groups,
+                                                               const uint8_t *__restrict__ rec) {
+  __shared__ PickLds<kRowsWaves * 64, R> sh;
+  topk_pick<kRowsWaves * 64, R>(logits, vocab, pk.m, pk.penal, pk.n_penal, pk.serial, kRowsPerWG, groups, rec, pk.out,
+                                sh);
+}
+
+template <bool REC, uint32_t KS>
+hipError_t launch_rows_ks(const WeightView &wv, const float *x, float *y, uint8_t *rec, uint32_t lds, hipStream_t s) {
   static bool attr = false;
-  const void *fn = (const void *)k_gemv_rows_q6k<PR, KS>;
+  const void *fn = (const void *)k_gemv_rows_q6k<REC, KS>;
   if (!attr) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMxMaxLds);
     if (e != hipSuccess) return e;
     attr = true;
   }
-  hipLaunchKernelGGL((k_gemv_rows_q6k<PR, KS>), dim3(gemv_rows_groups(wv)), dim3(kRowsWaves * 64), lds, s, wv, x, y,
-                     rec, pk);
+  hipLaunchKernelGGL((k_gemv_rows_q6k<REC, KS>), dim3(gemv_rows_groups(wv)), dim3(kRowsWaves * 64), lds, s, wv, x, y,
+                     rec);
   return hipGetLastError();
 }
 
-template <int PR>
-hipError_t launch_rows(const WeightView &wv, const float *x, float *y, uint8_t *rec, const RowsPick &pk,
-                       uint32_t lds, hipStream_t s) {
+template <bool REC>
+hipError_t launch_rows(const WeightView &wv, const float *x, float *y, uint8_t *rec, uint32_t lds, hipStream_t s) {
   // as many k slices as block columns, up to the 8 waves
-  if (wv.bpr >= 8u) return launch_rows_ks<PR, 8>(wv, x, y, rec, pk, lds, s);
-  if (wv.bpr >= 4u) return launch_rows_ks<PR, 4>(wv, x, y, rec, pk, lds, s);
-  return launch_rows_ks<PR, 2>(wv, x, y, rec, pk, lds, s);
+  if (wv.bpr >= 8u) return launch_rows_ks<REC, 8>(wv, x, y, rec, lds, s);
+  if (wv.bpr >= 4u) return launch_rows_ks<REC, 4>(wv, x, y, rec, lds, s);
+  return launch_rows_ks<REC, 2>(wv, x, y, rec, lds, s);
 }
 
 }  // namespace
@@ -316,31 +304,31 @@ uint32_t gemv_rows_group_size() { return kRowsPerWG; }
 hipError_t launch_gemv_rows(const WeightView &wv, const float *x, float *y, hipStream_t s) {
   if (!gemv_rows_applies(wv, 1u)) return hipErrorInvalidValue;
   const uint32_t lds = rows_tiles_at(wv.k) + kRowsWaves * kRowsBuf;
-  return launch_rows<0>(wv, x, y, nullptr, RowsPick{}, lds, s);
+  return launch_rows<false>(wv, x, y, nullptr, lds, s);
 }
 
-hipError_t launch_gemv_rows_topk(const WeightView &wv, const float *x, float *y, uint8_t *rec, uint32_t *arrivals,
-                                 uint32_t m, const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial,
-                                 uint32_t *out, hipStream_t s) {
+hipError_t launch_gemv_rows_topk(const WeightView &wv, const float *x, float *y, uint8_t *rec, uint32_t m,
+                                 const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, uint32_t *out,
+                                 hipStream_t s) {
   const uint32_t groups = gemv_rows_groups(wv);
   if (!gemv_rows_applies(wv, 1u) || groups > kRowsTopkGroupsMax || m == 0 || m > EFF_TOPK_M_MAX ||
       n_penal > EFF_TOPK_P_MAX || wv.rows >= EFF_TOPK_N_MAX)
     return hipErrorInvalidValue;
   RowsPick pk{};
   pk.out = out;
-  pk.arrivals = arrivals;
   pk.m = m;
   pk.n_penal = n_penal;
   pk.serial = serial;
   for (uint32_t i = 0; i < n_penal; ++i) pk.penal.ids[i] = penal_ids[i];
-  // the x region and tiles, and at least the selection's LDS
-  uint32_t lds = rows_tiles_at(wv.k) + kRowsWaves * kRowsBuf;
-  if (groups <= kRowsWaves * 64u) {
-    lds = max(lds, (uint32_t)sizeof(PickLds<kRowsWaves * 64, 1>));
-    return launch_rows<1>(wv, x, y, rec, pk, lds, s);
-  }
-  lds = max(lds, (uint32_t)sizeof(PickLds<kRowsWaves * 64, 2>));
-  return launch_rows<2>(wv, x, y, rec, pk, lds, s);
+  hipError_t e = launch_rows<true>(wv, x, y, rec, rows_tiles_at(wv.k) + kRowsWaves * kRowsBuf, s);
+  if (e != hipSuccess) return e;
+  if (groups <= kRowsWaves * 64u)
+    hipLaunchKernelGGL((k_rows_pick<1>), dim3(1), dim3(kRowsWaves * 64), 0, s, (const uint32_t *)y, wv.rows, pk,
+                       groups, rec);
+  else
+    hipLaunchKernelGGL((k_rows_pick<2>), dim3(1), dim3(kRowsWaves * 64), 0, s, (const uint32_t *)y, wv.rows, pk,
+                       groups, rec);
+  return hipGetLastError();
 }
 
 }  // namespace eff

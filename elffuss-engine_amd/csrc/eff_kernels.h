@@ -55,15 +55,14 @@ bool gemv_rows_applies(const WeightView &wv, uint32_t tokens);
 uint32_t gemv_rows_groups(const WeightView &wv);
 uint32_t gemv_rows_group_size();
 hipError_t launch_gemv_rows(const WeightView &wv, const float *x, float *y, hipStream_t stream);
-// The same GEMV fused with the top-m of its logits (the decode head): every
-// workgroup writes the top-k record of its gemv_rows_group_size() rows to rec
-// (gemv_rows_groups(wv) <= kRowsTopkGroupsMax records); the last one to
-// finish selects from them into out. `arrivals` is a device word that is zero before the launch
-// and zero again after it; launches sharing it must not overlap.
+// The same GEMV with the top-m of its logits (the decode head): every
+// workgroup of the GEMV also writes the top-k record of its
+// gemv_rows_group_size() rows to rec (gemv_rows_groups(wv) <=
+// kRowsTopkGroupsMax records), and one more launch selects from them into out.
 constexpr uint32_t kRowsTopkGroupsMax = 1024;
-hipError_t launch_gemv_rows_topk(const WeightView &wv, const float *x, float *y, uint8_t *rec, uint32_t *arrivals,
-                                 uint32_t m, const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial,
-                                 uint32_t *out, hipStream_t stream);
+hipError_t launch_gemv_rows_topk(const WeightView &wv, const float *x, float *y, uint8_t *rec, uint32_t m,
+                                 const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, uint32_t *out,
+                                 hipStream_t stream);
 // Multi-token matrix-core GEMV (16 rows x 4 tokens per MFMA): 4..16 tokens
 // per launch, Q8_0/Q4_K/Q6_K/Q2_K/IQ2_XXS, k % 256 == 0.
 bool gemv_mt_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p);

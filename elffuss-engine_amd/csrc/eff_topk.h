@@ -81,10 +81,7 @@ __device__ __forceinline__ uint64_t wave_ext64(uint64_t v) {
 
 // The group's record from the lanes' own 4 largest (every lane of the wave
 // active): 4 rounds of a wave maximum over the lanes' heads; lanes 0..3 write
-// the 64 bytes at `rec`. WT: as device-scope atomic stores, which write
-// through to memory, so that a workgroup on another XCD can read the record
-// once the writer's stores have completed.
-template <bool WT = false>
+// the 64 bytes at `rec`.
 __device__ __forceinline__ void topk_record_wave(Top4 t, bool nan, uint8_t *rec) {
   const uint32_t lane = threadIdx.x & 63u;
   uint64_t out_c[4];
@@ -115,20 +112,11 @@ __device__ __forceinline__ void topk_record_wave(Top4 t, bool nan, uint8_t *rec)
     } else {
       v = make_uint4(any_nan ? 1u : 0u, 0u, 0u, 0u);
     }
-    if constexpr (WT) {
-      uint32_t *w = (uint32_t *)rec + 4u * lane;
-      __hip_atomic_store(w, v.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(w + 1, v.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(w + 2, v.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(w + 3, v.w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      ((uint4 *)rec)[lane] = v;
-    }
+    ((uint4 *)rec)[lane] = v;
   }
 }
 
-// ---- the selection over the records (k_topk_pick and the row GEMV's last
-// workgroup) ----------------------------------------------------------------
+// ---- the selection over the records (k_topk_pick, k_rows_pick) -------------
 
 struct TopkPenal {
   uint32_t ids[EFF_TOPK_P_MAX];

@@ -6,8 +6,8 @@
  * Python) calls these functions with plain pointers and sizes. Device memory
  * is held in opaque buffers; every launch is enqueued on the context's HIP
  * stream and returns without waiting, as the reference records dispatches into
- * an open compute pass and returns (ops.js:667-710). Only eff_buf_read and
- * eff_sync wait for the device (device.js:165-200, readback).
+ * an open compute pass and returns (ops.js:667-710). Only eff_buf_read,
+ * eff_read_end and eff_sync wait for the device (device.js:165-200, readback).
  *
  * Return codes follow the reference's error conventions:
  *   EFF_OK              success;
@@ -78,7 +78,7 @@ typedef struct eff_stats {
   uint64_t gemm;        /* fp16 MFMA GEMM launches */
   uint64_t skinny;      /* GEMV launches over token groups (GEMV max < tokens < GEMM min) */
   uint64_t dequant;     /* dequant launches */
-  uint64_t topk;        /* top-k launches (chunk + final pair) */
+  uint64_t topk;        /* top-k calls (records + selection; eff_topk, eff_topk_noalloc, eff_qgemv_topk) */
   uint64_t not_applicable;  /* calls answered EFF_NOT_APPLICABLE */
   uint64_t split;       /* split-x matrix-core launches (Q2_K, Q4_K, IQ2_XXS from 4 tokens) */
   uint64_t fused;       /* fused GEMV launches (eff_qgemv_multi) */
@@ -305,12 +305,10 @@ int eff_topk(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint3
  * the output projection fused with top-k = 40 of north_star's configuration
  * 4; the reference runs the two as separate passes (model.js:1145-1177, then
  * createTopKGPU().candidatos, ops.topk.js:99-165). For Q6_K matrices of
- * 32768 .. 131072 rows this is one launch: every workgroup of the GEMV also
- * writes the top-k record of its 128 rows, and the last one to finish selects
- * from all records. Other shapes run the GEMV and eff_topk. Calls on one
- * context are stream-ordered; the context's arrival counter is not shared
- * with other contexts. The same NOT_APPLICABLE cases as eff_topk, checked
- * before anything is enqueued. */
+ * 32768 .. 131072 rows every workgroup of the GEMV also writes the top-k
+ * record of its 128 rows, and one more launch selects from the records; other
+ * shapes run the GEMV and eff_topk. The same NOT_APPLICABLE cases as
+ * eff_topk, checked before anything is enqueued. */
 int eff_qgemv_topk(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k,
                    uint32_t m, const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, eff_buf *out);
 
