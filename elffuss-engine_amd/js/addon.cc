@@ -518,6 +518,24 @@ napi_value TopK(napi_env env, napi_callback_info info) {
                                    (uint32_t)(len / 4), (uint32_t)i64(env, a[6]), external<eff_buf>(env, a[7])));
 }
 
+// qgemvTopk(ctx, type, w, x, y, rows, k, m, penalIds (Uint32Array|null), serial, out)
+napi_value QGemvTopK(napi_env env, napi_callback_info info) {
+  napi_value a[11];
+  get_args(env, info, 11, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  void *ids = nullptr;
+  size_t len = 0;
+  napi_valuetype t;
+  napi_typeof(env, a[8], &t);
+  if (t != napi_null && t != napi_undefined && !bytes_of(env, a[8], &ids, &len))
+    return throw_msg(env, "qgemvTopk: penalised ids must be a Uint32Array");
+  return status(env, ctx, eff_qgemv_topk(ctx, (int)i64(env, a[1]), external<eff_buf>(env, a[2]),
+                                         external<eff_buf>(env, a[3]), external<eff_buf>(env, a[4]),
+                                         (uint32_t)i64(env, a[5]), (uint32_t)i64(env, a[6]), (uint32_t)i64(env, a[7]),
+                                         (const uint32_t *)ids, (uint32_t)(len / 4), (uint32_t)i64(env, a[9]),
+                                         external<eff_buf>(env, a[10])));
+}
+
 napi_value TopKOutBytes(napi_env env, napi_callback_info) { return make_int(env, (int64_t)eff_topk_out_bytes()); }
 
 napi_value Register(napi_env env, napi_value exports) {
@@ -527,7 +545,7 @@ napi_value Register(napi_env env, napi_value exports) {
       {"init", Init}, {"shutdown", Shutdown}, {"sync", Sync}, {"setOption", SetOption}, {"stats", Stats},
       {"bufAlloc", BufAlloc}, {"bufFree", BufFree}, {"bufWrite", BufWrite}, {"bufRead", BufRead},
       {"bufReadAsync", BufReadAsync}, {"bufSize", BufSize}, {"bufMarkR", BufMarkR}, {"bufBlocksR", BufBlocksR}, {"bufWriteR", BufWriteR},
-      {"qmatmul", QMatmul}, {"qgemv", QGemv}, {"qgemvMulti", QGemvMulti}, {"qgemm", QGemm}, {"qgemmPlanned", QGemmPlanned}, {"dequant", Dequant}, {"gather", Gather}, {"gatherNorm", GatherNorm}, {"topk", TopK},
+      {"qmatmul", QMatmul}, {"qgemv", QGemv}, {"qgemvMulti", QGemvMulti}, {"qgemm", QGemm}, {"qgemmPlanned", QGemmPlanned}, {"dequant", Dequant}, {"gather", Gather}, {"gatherNorm", GatherNorm}, {"topk", TopK}, {"qgemvTopk", QGemvTopK},
       {"topkOutBytes", TopKOutBytes},
   };
   for (auto &f : fns) {

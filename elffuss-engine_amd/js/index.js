@@ -608,7 +608,9 @@ function createQuantOps(device, opts) {
 // (value desc, index asc) of one logits vector plus the raw logits of the
 // penalised ids, or null when the device result must not be used; muestrea()
 // is the whole step (plan, candidates, sample() on the handful) and returns
-// the token sample() would give over the whole vector, or null.
+// the token sample() would give over the whole vector, or null. cabeza() and
+// muestreaCabeza() do the same from the head's weights and x, computing the
+// logits on the way (one call for the GEMV and the top-k).
 const estadisticasTopK = { gpu: 0, respaldo: 0, motivos: {} };
 const ahoraMs = () => (typeof performance !== 'undefined' ? performance.now() : Date.now());
 
@@ -634,9 +636,34 @@ function createTopKGPU(device, ctx) {
     const c = muestreo.leeSalidaTopK(u, { S }, Math.ceil(vocab / TOPK.POR_TROZO), esta);
     return c.motivo ? respaldo(c.motivo) : c;
   }
+  // The head (model.js:1145-1177: the output projection of one token, then
+  // candidatos() over its logits) as one call, eff_qgemv_topk. Resolves to
+  // { logits, candidatos }: the logits always (a pooled buffer), the
+  // candidates as candidatos() gives them, or null (then the caller reads the
+  // logits as before).
+  async function cabeza(type, wBuf, xBuf, vocab, k, plan) {
+    const i = quantInfo(type);
+    if (k % i.blockElems !== 0) throw new Error(`matmul ${type}: k=${k} no es múltiplo de ${i.blockElems}`);
+    if (TIPOS_R.has(type)) compruebaBufferR(type, wBuf, { bloques: vocab * (k / i.blockElems) }, 'matmul');
+    const logits = ctx.alloc(vocab * 4, 'matmul.y');
+    const soloLogits = (motivo) => {
+      native.qmatmul(device._ctx, i.code, wBuf._h, xBuf._h, logits._h, vocab, k, 1);
+      return { logits, candidatos: respaldo(motivo) };
+    };
+    if (vocab >= TOPK.N_MAX) return soloLogits('vocabulario');
+    serie = ((serie + 1) >>> 0) || 1;
+    const esta = serie;
+    const S = plan.S || new Uint32Array(0);
+    const r = native.qgemvTopk(device._ctx, i.code, wBuf._h, xBuf._h, logits._h, vocab, k, plan.M, S, esta, out._h);
+    if (r === null) return soloLogits('no aplica');   // nothing was enqueued
+    const u = new Uint32Array(await readback(device, out, 0, out.size));
+    const c = muestreo.leeSalidaTopK(u, { S }, Math.ceil(vocab / TOPK.POR_TROZO), esta);
+    return { logits, candidatos: c.motivo ? respaldo(c.motivo) : c };
+  }
   return {
     stats,
     candidatos,
+    cabeza,
     // `opts` as for sample() without `previos`, which comes in two halves
     // (the prompt and the generated ids). Resolves to { id, msLectura,
     // msMuestreo }, or null: then the caller reads the whole vector.
@@ -651,6 +678,31 @@ function createTopKGPU(device, ctx) {
       if (id === null) return respaldo('incoherente');
       stats.gpu++; estadisticasTopK.gpu++;
       return { id, msLectura: t1 - t0, msMuestreo: ahoraMs() - t1 };
+    },
+    // muestrea() over the head: resolves to { logits, id, msLectura,
+    // msMuestreo }, id null when the caller has to sample the logits itself.
+    async muestreaCabeza(type, wBuf, xBuf, vocab, k, opts, previosA, previosB) {
+      const t0 = ahoraMs();
+      const plan = muestreo.planTopK(vocab, opts, previosA, previosB);
+      if (!plan) {
+        const i = quantInfo(type);
+        if (k % i.blockElems !== 0) throw new Error(`matmul ${type}: k=${k} no es múltiplo de ${i.blockElems}`);
+        if (TIPOS_R.has(type)) compruebaBufferR(type, wBuf, { bloques: vocab * (k / i.blockElems) }, 'matmul');
+        const logits = ctx.alloc(vocab * 4, 'matmul.y');
+        native.qmatmul(device._ctx, i.code, wBuf._h, xBuf._h, logits._h, vocab, k, 1);
+        respaldo('muestreo sin tope');
+        return { logits, id: null };
+      }
+      const { logits, candidatos: c } = await cabeza(type, wBuf, xBuf, vocab, k, plan);
+      if (!c) return { logits, id: null };
+      const t1 = ahoraMs();
+      const id = muestreo.muestraCandidatos(plan, c.ids, c.bits, c.bitsS, opts);
+      if (id === null) {
+        respaldo('incoherente');
+        return { logits, id: null };
+      }
+      stats.gpu++; estadisticasTopK.gpu++;
+      return { logits, id, msLectura: t1 - t0, msMuestreo: ahoraMs() - t1 };
     },
     destroy() { out.destroy(); },
   };

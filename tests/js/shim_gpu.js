@@ -126,8 +126,41 @@ async function main() {
   }
   // a temperature without top-k cannot use the handful
   assert.strictEqual(await tk.muestrea(lb, 0, logits.length, { temperature: 1 }, [], []), null);
-  out.topkStats = tk.stats;
+  out.topkStats = JSON.parse(JSON.stringify(tk.stats));
   out.stats = device.stats();
+  // the head in one call (cabeza): the logits of quant.matmul and the
+  // candidates candidatos() finds in them, bit for bit; muestreaCabeza picks
+  // the token muestrea picks from those logits (a second top-k object, so the
+  // counts above stay the first one's)
+  {
+    const tk2 = eff.createTopKGPU(device, ops.ctx);
+    const rows = 40000, k = 512;
+    const wB = ops.upload(eff.quantize('Q6_K', eff.fillNormal(77, 0.02, rows * k)), 'head');
+    const xh = ops.upload(eff.fillNormal(78, 1.0, k), 'xh');
+    const plan = { M: 40, S: Uint32Array.from([3, rows - 1]) };
+    const r = await tk2.cabeza('Q6_K', wB, xh, rows, k, plan);
+    const y = await ops.matmul('Q6_K', wB, xh, rows, k, 1);
+    const a = new Uint32Array(await eff.readback(device, r.logits, 0, rows * 4));
+    const b = new Uint32Array(await eff.readback(device, y, 0, rows * 4));
+    assert.deepStrictEqual(Array.from(a), Array.from(b));
+    const c2 = await tk2.candidatos(y, 0, rows, plan);
+    assert.ok(r.candidatos !== null && c2 !== null);
+    assert.deepStrictEqual(Array.from(r.candidatos.ids), Array.from(c2.ids));
+    assert.deepStrictEqual(Array.from(r.candidatos.bits), Array.from(c2.bits));
+    assert.deepStrictEqual(Array.from(r.candidatos.bitsS), Array.from(c2.bitsS));
+    const o = { temperature: 0.8, topK: 40, topP: 0.9, seed: 5 };
+    const m1 = await tk2.muestreaCabeza('Q6_K', wB, xh, rows, k, o, [3], [rows - 1]);
+    const m2 = await tk2.muestrea(y, 0, rows, o, [3], [rows - 1]);
+    assert.ok(m1.id !== null && m1.id === m2.id);
+    // no top-k in the settings: no plan, the logits alone
+    const m3 = await tk2.muestreaCabeza('Q6_K', wB, xh, rows, k, { temperature: 1 }, [], []);
+    assert.strictEqual(m3.id, null);
+    const c3 = new Uint32Array(await eff.readback(device, m3.logits, 0, rows * 4));
+    assert.deepStrictEqual(Array.from(c3), Array.from(b));
+    await assert.rejects(tk2.cabeza('Q6_K', wB, xh, rows, k + 1, plan), /múltiplo/);
+    out.cabeza = true;
+    tk2.destroy();
+  }
   fs.writeFileSync(path.join(dir, 'out.json'), JSON.stringify(out));
   device.destroy();
   console.log('shim_gpu ok');

@@ -81,3 +81,4 @@ def test_js_shim_gpu(eff, orc, tmp_path):
     assert out["topkStats"]["gpu"] == 20 and out["topkStats"]["respaldo"] == 1
     assert out["topkStats"]["motivos"] == {"muestreo sin tope": 1}
     assert out["stats"]["topk"] == 21 and out["stats"]["gemm"] >= 1 and out["stats"]["split"] >= 2
+    assert out["cabeza"] is True   # the head GEMV + top-k in one call, checked inside the shim
