@@ -52,7 +52,7 @@ constexpr uint32_t kRowsTile = 32;                    // rows per wave tile
 constexpr uint32_t kRowsPerWG = 128;
 constexpr uint32_t kRowsPitch = 240;                  // LDS bytes per tile row (15 chunks)
 constexpr uint32_t kRowsBuf = 8192;                   // LDS bytes per wave (8 loads of 1 KB)
-constexpr uint32_t kRowsRed = 4096;                   // LDS bytes of the slice sums (128 rows x up to 8 slices)
+constexpr uint32_t kRowsRed = kRowsPerWG * 8u * 4u;   // LDS bytes of the slice sums (the rows x up to 8 slices)
 constexpr uint32_t kRowsMin = 32768;
 constexpr uint32_t kRowsMaxK = 16384;
 
@@ -67,7 +67,84 @@ struct RowsPick {
 // so that its reads' offsets fit the 16-bit offset field of the LDS
 // instructions; then the slice sums (kRowsRed) and the workgroup's outputs
 // (512 B); then the 8 wave buffers.
-__host__ __device__ constexpr uint32_t rows_tiles_at(uint32_t k) { return 4u * k + kRowsRed + 512u; }
+__host__ __device__ constexpr uint32_t rows_tiles_at(uint32_t k) { return 4u * k + kRowsRed + 4u * kRowsPerWG; }
+
+// One lane's half row-block (128 weights): the tile row's ql/qh words `a`, `q`
+// (aligned copies of LDS), its scale words and d, the block's byte shift, and
+// the x digits and group data of block column j; acc += d * sum (w x).
+__device__ __forceinline__ void rows_half_block(float &acc, const uint32_t (&a)[20], const uint32_t (&q)[12], uint2 sw,
+                                                uint32_t sw2, uint2 dd, uint32_t sh, const uint8_t *xl,
+                                                const int32_t *meta, uint32_t j, uint32_t n) {
+  uint32_t QL[16], QH[8];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) QL[i] = __builtin_amdgcn_alignbyte(a[i + 1], a[i], sh);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) QH[i] = __builtin_amdgcn_alignbyte(q[i + 1], q[i], sh);
+  const uint32_t s0 = __builtin_amdgcn_alignbyte(sw.y, sw.x, sh);
+  const uint32_t s1 = __builtin_amdgcn_alignbyte(sw2, sw.y, sh);
+  const uint32_t dw = __builtin_amdgcn_alignbyte(dd.y, dd.x, sh);
+  // this half's x: 8 runs of 16 from k = 256 j + 128 n; its 4 groups' data
+  const uint8_t *dj = xl + (16u * j + 8u * n) * 48u;
+  const int32_t *mj = meta + 8u * (8u * j + 4u * n);
+  float accb = 0.f;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int4 Ma = *(const int4 *)(mj + 8 * g);       // -32 T of values 0..15, p
+    const int4 Mb = *(const int4 *)(mj + 8 * g + 4);   // -32 T of values 16..31
+    float accg = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      // weights 32 g + 16 hh + 4 i .. + 3 of the half (ql nibble, 2 bits of qh)
+      uint32_t u[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int lc = 4 * hh + i;
+        const uint32_t ql = QL[8 * (g & 1) + lc], qh = QH[lc];
+        const uint32_t lo = (g & 2) ? (ql >> 4) : ql;
+        const uint32_t hi = g == 0 ? (qh << 4) : g == 1 ? (qh << 2) : g == 2 ? qh : (qh >> 2);
+        u[i] = (lo & 0x0F0F0F0Fu) | (hi & 0x30303030u);
+      }
+      const uint32_t run = 2u * g + hh;   // 16-weight run of the half
+      const uint8_t *dA = dj + run * 48u;
+      const int init[3] = {hh ? Mb.x : Ma.x, hh ? Mb.y : Ma.y, hh ? Mb.z : Ma.z};
+      int D[3];
+#pragma unroll
+      for (int pp = 0; pp < 3; ++pp) {
+        const u32x4 X = *(const u32x4 *)(dA + 16 * pp);
+        int d = __builtin_amdgcn_sdot4((int)u[0], (int)X.x, init[pp], false);
+        d = __builtin_amdgcn_sdot4((int)u[1], (int)X.y, d, false);
+        d = __builtin_amdgcn_sdot4((int)u[2], (int)X.z, d, false);
+        D[pp] = __builtin_amdgcn_sdot4((int)u[3], (int)X.w, d, false);
+      }
+      // sum (u - 32) digits, as sum over planes of 256^d D_d (|D_d| < 2^17)
+      const float f = __builtin_fmaf((float)(D[2] * 256 + D[1]), 256.f, (float)D[0]);
+      const float sc = (float)(int)__builtin_amdgcn_sbfe((int)(run < 4u ? s0 : s1), 8u * (run & 3u), 8);
+      accg = __builtin_fmaf(sc, f, accg);
+    }
+    accb = __builtin_fmaf(__builtin_bit_cast(float, Ma.w), accg, accb);
+  }
+  acc = __builtin_fmaf(h2f(dw & 0xFFFFu), accb, acc);
+}
+
+// A lane's tile row into registers: ql/qh words of its half, its scale
+// words and d (the tile row starts 16-byte aligned).
+__device__ __forceinline__ void rows_read(const uint8_t *tp, uint32_t n, uint32_t (&a)[20], uint32_t (&q)[12],
+                                          uint2 &sw, uint32_t &sw2, uint2 &dd) {
+#pragma unroll
+  for (uint32_t i = 0; i < 5; ++i) {
+    const u32x4 v = *(const u32x4 *)(tp + 64u * n + 16u * i);
+    a[4 * i] = v.x; a[4 * i + 1] = v.y; a[4 * i + 2] = v.z; a[4 * i + 3] = v.w;
+  }
+#pragma unroll
+  for (uint32_t i = 0; i < 3; ++i) {
+    const u32x4 v = *(const u32x4 *)(tp + 128u + 32u * n + 16u * i);
+    q[4 * i] = v.x; q[4 * i + 1] = v.y; q[4 * i + 2] = v.z; q[4 * i + 3] = v.w;
+  }
+  // this half's 8 scales (bytes 192 + 8n ..) and d (bytes 208, 209)
+  sw = *(const uint2 *)(tp + 192u + 8u * n);
+  sw2 = *(const uint32_t *)(tp + 200u + 8u * n);
+  dd = *(const uint2 *)(tp + 208u);
+}
 
 // REC: the decode head. Each workgroup also writes the top-k record of its
 // 128 rows (their 4 largest logits, eff_topk.h) for k_rows_pick.
@@ -150,21 +227,9 @@ __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu
     for (uint32_t c = 0; c < ncol; ++c) {
       const uint32_t j = ks + KS * c;
       wait_vm<0>();   // this tile's loads (the only ones in flight)
-      uint32_t a[20], q[12];
-#pragma unroll
-      for (uint32_t i = 0; i < 5; ++i) {
-        const u32x4 v = *(const u32x4 *)(tp + 64u * n + 16u * i);
-        a[4 * i] = v.x; a[4 * i + 1] = v.y; a[4 * i + 2] = v.z; a[4 * i + 3] = v.w;
-      }
-#pragma unroll
-      for (uint32_t i = 0; i < 3; ++i) {
-        const u32x4 v = *(const u32x4 *)(tp + 128u + 32u * n + 16u * i);
-        q[4 * i] = v.x; q[4 * i + 1] = v.y; q[4 * i + 2] = v.z; q[4 * i + 3] = v.w;
-      }
-      // this half's 8 scales (bytes 192 + 8n ..) and d (bytes 208, 209)
-      const uint2 sw = *(const uint2 *)(tp + 192u + 8u * n);
-      const uint32_t sw2 = *(const uint32_t *)(tp + 200u + 8u * n);
-      const uint2 dd = *(const uint2 *)(tp + 208u);
+      uint32_t a[20], q[12], sw2;
+      uint2 sw, dd;
+      rows_read(tp, n, a, q, sw, sw2, dd);
       // the tile is in registers: the buffer takes the next one
       __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
       {
@@ -172,56 +237,7 @@ __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu
         const uint32_t tn = last ? t + 1u : t;
         if (tn < T) issue(tn, last ? ks : j + KS);
       }
-      const uint32_t sh = 2u * ((par + j) & 1u);
-      uint32_t QL[16], QH[8];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) QL[i] = __builtin_amdgcn_alignbyte(a[i + 1], a[i], sh);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) QH[i] = __builtin_amdgcn_alignbyte(q[i + 1], q[i], sh);
-      const uint32_t s0 = __builtin_amdgcn_alignbyte(sw.y, sw.x, sh);
-      const uint32_t s1 = __builtin_amdgcn_alignbyte(sw2, sw.y, sh);
-      const uint32_t dw = __builtin_amdgcn_alignbyte(dd.y, dd.x, sh);
-      // this half's x: 8 runs of 16 from k = 256 j + 128 n; its 4 groups' data
-      const uint8_t *dj = xl + (16u * j + 8u * n) * 48u;
-      const int32_t *mj = meta + 8u * (8u * j + 4u * n);
-      float accb = 0.f;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int4 Ma = *(const int4 *)(mj + 8 * g);       // -32 T of values 0..15, p
-        const int4 Mb = *(const int4 *)(mj + 8 * g + 4);   // -32 T of values 16..31
-        float accg = 0.f;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          // weights 32 g + 16 hh + 4 i .. + 3 of the half (ql nibble, 2 bits of qh)
-          uint32_t u[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int lc = 4 * hh + i;
-            const uint32_t ql = QL[8 * (g & 1) + lc], qh = QH[lc];
-            const uint32_t lo = (g & 2) ? (ql >> 4) : ql;
-            const uint32_t hi = g == 0 ? (qh << 4) : g == 1 ? (qh << 2) : g == 2 ? qh : (qh >> 2);
-            u[i] = (lo & 0x0F0F0F0Fu) | (hi & 0x30303030u);
-          }
-          const uint32_t run = 2u * g + hh;   // 16-weight run of the half
-          const uint8_t *dA = dj + run * 48u;
-          const int init[3] = {hh ? Mb.x : Ma.x, hh ? Mb.y : Ma.y, hh ? Mb.z : Ma.z};
-          int D[3];
-#pragma unroll
-          for (int pp = 0; pp < 3; ++pp) {
-            const u32x4 X = *(const u32x4 *)(dA + 16 * pp);
-            int d = __builtin_amdgcn_sdot4((int)u[0], (int)X.x, init[pp], false);
-            d = __builtin_amdgcn_sdot4((int)u[1], (int)X.y, d, false);
-            d = __builtin_amdgcn_sdot4((int)u[2], (int)X.z, d, false);
-            D[pp] = __builtin_amdgcn_sdot4((int)u[3], (int)X.w, d, false);
-          }
-          // sum (u - 32) digits, as sum over planes of 256^d D_d (|D_d| < 2^17)
-          const float f = __builtin_fmaf((float)(D[2] * 256 + D[1]), 256.f, (float)D[0]);
-          const float sc = (float)(int)__builtin_amdgcn_sbfe((int)(run < 4u ? s0 : s1), 8u * (run & 3u), 8);
-          accg = __builtin_fmaf(sc, f, accg);
-        }
-        accb = __builtin_fmaf(__builtin_bit_cast(float, Ma.w), accg, accb);
-      }
-      acc = __builtin_fmaf(h2f(dw & 0xFFFFu), accb, acc);
+      rows_half_block(acc, a, q, sw, sw2, dd, 2u * ((par + j) & 1u), xl, meta, j, n);
     }
     // the two halves of a row; the slice sum of the row
     acc += __shfl_xor(acc, 32);
@@ -245,7 +261,7 @@ __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu
       Top4 t;
       bool nan = false;
 #pragma unroll
-      for (uint32_t h = 0; h < 2u; ++h) {
+      for (uint32_t h = 0; h < kRowsPerWG / 64u; ++h) {
         const uint32_t i = lane + 64u * h, e = base + i;
         if (e < rows) {
           const uint32_t bits = fin[i];
