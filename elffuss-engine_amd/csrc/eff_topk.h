@@ -17,6 +17,7 @@
 #include <stdint.h>
 
 #include "../../include/elffuss_amd.h"
+#include "eff_device.h"
 #include "eff_kernels.h"
 
 namespace eff {
@@ -61,10 +62,11 @@ struct Top4 {
 template <bool MAX>
 __device__ __forceinline__ uint32_t wave_ext(uint32_t v) {
   auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
-  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));
-  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));
-  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false));
-  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xF, 0xF, false));
+  constexpr int id = MAX ? 0 : -1;   // the operation's identity (the patterns permute whole rows)
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0xB1, 0xF, 0xF, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x4E, 0xF, 0xF, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x141, 0xF, 0xF, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x140, 0xF, 0xF, false));
   const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
   const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
   return op(op(r0, r1), op(r2, r3));
@@ -141,13 +143,28 @@ template <int NT, int R>
 struct PickLds {
   uint32_t hist[256];   // bin 255 - d counts digit d (descending digits in ascending bins)
   uint32_t st[4];
-  uint32_t flags, nsat, ncand, nsel;
+  uint32_t flags, nsat, nsel;
   uint64_t wmin[NT / 64], wmax[NT / 64], wkth[NT / 64];
+  uint32_t wtot[NT / 64];   // the waves' candidate counts
+  uint32_t fsat;            // a saturated group's 4th listed composite was selected
   uint32_t satg[NT * R];
   alignas(16) uint64_t cand_c[kCandMax + 4];   // 4 zero entries past the candidates (rank reads in pairs)
   uint32_t cand_b[kCandMax];
-  uint32_t cand_r[kCandMax];
+  uint32_t cand_f[kCandMax];   // 1: the 4th listed composite of a group of more than 4 elements
 };
+
+// Sum of v over aligned groups of P consecutive lanes (P a power of two <= 64,
+// wave-uniform; every lane active), each lane getting its group's sum: DPP
+// within rows (quad swaps, half-row and row mirrors), then lane shuffles.
+__device__ __forceinline__ uint32_t group_sum(uint32_t v, uint32_t P) {
+  if (P >= 2u) v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+  if (P >= 4u) v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+  if (P >= 8u) v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false);
+  if (P >= 16u) v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false);
+  if (P >= 32u) v += (uint32_t)__shfl_xor((int)v, 16, 64);
+  if (P >= 64u) v += (uint32_t)__shfl_xor((int)v, 32, 64);
+  return v;
+}
 
 // Radix select over distinct 64-bit candidates: returns T such that exactly
 // `need` candidates are >= T (1 <= need <= number of candidates). Each round
@@ -246,37 +263,47 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
   uint64_t c[R][4];
   uint32_t b[R][4];
   uint32_t nan = 0;
+  // penalised ids: their raw logits (the penalty itself is applied by the
+  // sampler). Every thread loads, from clamped places, so that the loads are
+  // issued in a fixed order and each wait covers only what it needs.
+  const uint32_t pid = penal.ids[min((uint32_t)tid, (uint32_t)EFF_TOPK_P_MAX - 1u)];
+  // records through a buffer descriptor of the groups' bytes: a group past
+  // the last reads as zeros (no composites, no NaN)
+  const rsrc_t rs = make_rsrc(rec, (uint64_t)groups * kTopkRecordBytes);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const uint32_t g = (uint32_t)tid + NT * r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { c[r][i] = 0u; b[r][i] = 0u; }
-    if (g < groups) {
-      const uint4 *rp = (const uint4 *)(rec + (uint64_t)g * kTopkRecordBytes);
-      const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2], q3 = rp[3];
-      c[r][0] = ((uint64_t)q0.y << 32) | q0.x;
-      c[r][1] = ((uint64_t)q0.w << 32) | q0.z;
-      c[r][2] = ((uint64_t)q1.y << 32) | q1.x;
-      c[r][3] = ((uint64_t)q1.w << 32) | q1.z;
-      b[r][0] = q2.x; b[r][1] = q2.y; b[r][2] = q2.z; b[r][3] = q2.w;
-      nan |= q3.x;
-    }
+    const int off = (tid + NT * r) * (int)kTopkRecordBytes;
+    const u32x4 q0 = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+    const u32x4 q1 = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, 0, 0);
+    const u32x4 q2 = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 32, 0, 0);
+    const uint32_t q3 = __builtin_amdgcn_raw_buffer_load_b32(rs, off + 48, 0, 0);
+    c[r][0] = ((uint64_t)q0.y << 32) | q0.x;
+    c[r][1] = ((uint64_t)q0.w << 32) | q0.z;
+    c[r][2] = ((uint64_t)q1.y << 32) | q1.x;
+    c[r][3] = ((uint64_t)q1.w << 32) | q1.z;
+    b[r][0] = q2.x; b[r][1] = q2.y; b[r][2] = q2.z; b[r][3] = q2.w;
+    nan |= q3;
   }
-  // penalised ids: their raw logits (the penalty itself is applied by the sampler)
-  uint32_t pv = 0u;
-  if ((uint32_t)tid < n_penal && penal.ids[tid] < vocab) pv = logits[penal.ids[tid]];
+  const bool pok = (uint32_t)tid < n_penal && pid < vocab;
+  const uint32_t pl = logits[pok ? pid : 0u];
+  const uint32_t pv = pok ? pl : 0u;
   const bool wnan = __ballot(nan != 0u) != 0u;
   if (tid == 0) {
     sh.flags = 0u;
     sh.nsat = 0u;
-    sh.ncand = 0u;
     sh.nsel = 0u;
+    sh.fsat = 0u;
   }
-  __syncthreads();
-  if (lane == 0 && wnan) atomicOr(&sh.flags, 2u);
   const uint32_t need = min(m, vocab);
-  // the listed composites >= th into the candidate space (counted past it):
-  // a wave prefix sum of the lanes' counts and one LDS atomic per wave
+  uint32_t *const pairs = out + EFF_TOPK_HEADER + EFF_TOPK_P_MAX;
+  // group g of the thread's record r holds more than 4 elements
+  auto over4 = [&](int r) {
+    const uint32_t g = (uint32_t)tid + NT * r;
+    return g < groups && min(gs, vocab - g * gs) > 4u;
+  };
+  // the listed composites >= th into the candidate space in thread order (a
+  // wave prefix sum of the lanes' counts, the waves' totals through LDS);
+  // returns their number (only the first kCandMax are stored)
   auto compact = [&](uint64_t th) {
     uint32_t cnt = 0;
 #pragma unroll
@@ -284,13 +311,15 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
 #pragma unroll
       for (int i = 0; i < 4; ++i) cnt += (c[r][i] && c[r][i] >= th) ? 1u : 0u;
     const uint32_t incl = wave_scan(cnt);
-    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-    uint32_t base = 0;
-    if (total) {
-      if (lane == 0) base = atomicAdd(&sh.ncand, total);
-      base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+    if (lane == 63) sh.wtot[wave] = incl;
+    __syncthreads();
+    uint32_t q = incl - cnt, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t t = sh.wtot[w];
+      q += w < wave ? t : 0u;
+      tot += t;
     }
-    uint32_t q = base + incl - cnt;
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -299,19 +328,19 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
           if (q < kCandMax) {
             sh.cand_c[q] = c[r][i];
             sh.cand_b[q] = b[r][i];
+            sh.cand_f[q] = i == 3 && over4(r) ? 1u : 0u;
           }
           ++q;
         }
       }
+    return tot;
   };
-  uint64_t tau = 0;
-  uint32_t nc = 0;
-  bool done = false;
-  if (groups > need && need <= (uint32_t)(NW * KW)) {
+  const bool fast = groups > need && need <= (uint32_t)(NW * KW);
+  if (fast) {
     // on the maxima's high words (order keys): kth = the wave's kw-th largest
-    // distinct key, tq = the smallest composite with the waves' smallest such
-    // key (0, and the exact tau below, when a wave runs out of keys). Equal
-    // keys leave at most fewer distinct values, so tq stays a lower bound.
+    // distinct key (0 once the wave's maxima run out). Equal keys leave at
+    // most fewer distinct values, so the smallest of the waves' kth stays a
+    // lower bound.
     uint32_t v[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) v[r] = (uint32_t)(c[r][0] >> 32);
@@ -321,60 +350,60 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
       uint32_t lb = 0;
 #pragma unroll
       for (int r = 0; r < R; ++r) lb = v[r] > lb ? v[r] : lb;
-      kth = wave_ext<true>(lb);   // 0 once the wave's maxima run out
+      kth = wave_ext<true>(lb);
 #pragma unroll
       for (int r = 0; r < R; ++r) v[r] = v[r] == kth ? 0u : v[r];
     }
     if (lane == 0) sh.wkth[wave] = (uint64_t)kth << 32;
-    __syncthreads();
+  }
+  __syncthreads();
+  if (lane == 0 && wnan) atomicOr(&sh.flags, 2u);
+  uint64_t tau = 0;
+  uint32_t nc = ~0u;
+  if (fast) {
     uint64_t tq = ~(uint64_t)0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) tq = sh.wkth[w] < tq ? sh.wkth[w] : tq;
     if (tq != 0u) {
-      compact(tq);
-      __syncthreads();
-      nc = sh.ncand;
-      __syncthreads();
-      if (nc <= kCandMax) {
-        tau = tq;
-        done = true;
-      } else if (tid == 0) {
-        sh.ncand = 0u;   // too many: the exact tau below
-      }
+      nc = compact(tq);
+      tau = tq;
     }
   }
-  if (!done) {
+  if (nc > kCandMax) {
+    // no bound, or too many candidates: tau = the need-th largest group
+    // maximum exactly (at most 4 need composites are listed >= it), or 0 with
+    // no more groups than need (at most 4 need listed composites in all)
+    tau = 0;
     if (groups > need) {
-      // the need-th largest group maximum
       tau = select_top<NT>(need, [&](auto f) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
           if (c[r][0]) f(c[r][0]);
       }, sh);
     }
-    compact(tau);
-    __syncthreads();
-    nc = min(sh.ncand, kCandMax);
+    nc = min(compact(tau), kCandMax);
   }
   if (tid < 4) sh.cand_c[nc + tid] = 0u;   // the zero entries past the candidates
   __syncthreads();
-  uint64_t T = 0;        // exactly `need` candidates (of the final set) are >= T
-  bool ranked = false;   // cand_r holds every candidate's rank
-  if (nc <= need) {
-    // exactly the need candidates >= tau (tau is then one of them, a group
-    // maximum); or, with no more groups than need, every listed composite
-    // (groups with more than 4 elements then count as saturated below and are
-    // read whole)
-    T = groups > need ? tau : 0;
-  } else {
-    // rank = candidates above, counted by P threads of one wave per candidate,
-    // each over a contiguous quarter-aligned range read in pairs (the zero
-    // entries past the candidates count for nothing: every composite is > 0)
-    uint32_t P = 64;
-    while (P > 1 && nc * P > (uint32_t)NT) P >>= 1;
-    const uint32_t span = ((nc + P - 1u) / P + 3u) & ~3u;
-    for (uint32_t i0 = 0; i0 < nc; i0 += NT / P) {
-      const uint32_t i = i0 + (uint32_t)tid / P, part = (uint32_t)tid % P;
+  // the slots past need stay empty: stores issued once the records are used
+  // (the count of memory operations in flight is in order, so a wait for a
+  // load issued earlier would also wait for these)
+  for (uint32_t slot = need + (uint32_t)tid; slot < EFF_TOPK_CAP; slot += NT) {
+    pairs[2 * slot] = 0u;
+    pairs[2 * slot + 1] = 0u;
+  }
+  // rank = candidates above, counted by P threads of one wave per candidate,
+  // each over a contiguous quarter-aligned range read in pairs (the zero
+  // entries past the candidates count for nothing: every composite is > 0).
+  // The need largest go straight to their slots; a group's 4th listed
+  // composite among them means the group may hold more of the answer.
+  {
+    uint32_t lp = 6;   // P = 2^lp threads per candidate
+    while (lp > 0 && (nc << lp) > (uint32_t)NT) --lp;
+    const uint32_t P = 1u << lp;
+    const uint32_t span = (((nc + P - 1u) >> lp) + 3u) & ~3u;
+    for (uint32_t i0 = 0; i0 < nc; i0 += (uint32_t)NT >> lp) {
+      const uint32_t i = i0 + ((uint32_t)tid >> lp), part = (uint32_t)tid & (P - 1u);
       uint32_t rank = 0;
       uint64_t ci = 0;
       if (i < nc) {
@@ -387,38 +416,30 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
           rank += (p0.x > ci ? 1u : 0u) + (p0.y > ci ? 1u : 0u) + (p1.x > ci ? 1u : 0u) + (p1.y > ci ? 1u : 0u);
         }
       }
-      for (uint32_t o = 1; o < P; o <<= 1) rank += (uint32_t)__shfl_xor((int)rank, (int)o, 64);
-      if (i < nc && part == 0u) {
-        sh.cand_r[i] = rank;
+      rank = group_sum(rank, P);
+      if (i < nc && part == 0u && rank < need) {
+        pairs[2 * rank] = ~(uint32_t)ci;
+        pairs[2 * rank + 1] = sh.cand_b[i];
         if (rank == need - 1u) sh.wmin[0] = ci;   // the need-th largest candidate
+        if (sh.cand_f[i]) sh.fsat = 1u;
       }
     }
-    __syncthreads();
-    T = sh.wmin[0];
-    ranked = true;
-  }
-  // saturated groups: more than 4 elements and the 4th listed one selected
-  bool sat[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const uint32_t g = (uint32_t)tid + NT * r;
-    const uint32_t gcount = g < groups ? min(gs, vocab - g * gs) : 0u;
-    sat[r] = gcount > 4u && c[r][3] >= T;
-    if (sat[r]) sh.satg[atomicAdd(&sh.nsat, 1u)] = g;
   }
   __syncthreads();
-  const uint32_t ns = sh.nsat;
-  uint32_t *pairs = out + EFF_TOPK_HEADER + EFF_TOPK_P_MAX;
-  uint32_t n = need;
-  if (ns == 0u && ranked) {
-    // the candidates' ranks are final: the winners go straight to their slots
-    for (uint32_t i = (uint32_t)tid; i < nc; i += NT) {
-      if (sh.cand_r[i] < need) {
-        pairs[2 * sh.cand_r[i]] = ~(uint32_t)sh.cand_c[i];
-        pairs[2 * sh.cand_r[i] + 1] = sh.cand_b[i];
-      }
+  uint32_t n = min(nc, need);
+  if (sh.fsat) {
+    // saturated groups: more than 4 elements and the 4th listed one selected.
+    // T: exactly `need` candidates are >= T (every candidate when they are
+    // at most need).
+    const uint64_t T = nc > need ? sh.wmin[0] : (groups > need ? tau : 0u);
+    bool sat[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      sat[r] = over4(r) && c[r][3] >= T;
+      if (sat[r]) sh.satg[atomicAdd(&sh.nsat, 1u)] = (uint32_t)tid + NT * r;
     }
-  } else {
+    __syncthreads();
+    const uint32_t ns = sh.nsat;
     auto stream = [&](auto f) {
       for (uint32_t i = (uint32_t)tid; i < ns * gs; i += NT) {
         const uint32_t e = sh.satg[i / gs] * gs + i % gs;
@@ -433,7 +454,7 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
 #pragma unroll
       for (int r = 0; r < R; ++r)
         if (sat[r]) c[r][0] = c[r][1] = c[r][2] = c[r][3] = 0u;
-      T = select_top<NT>(need, [&](auto f) {
+      const uint64_t T2 = select_top<NT>(need, [&](auto f) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -445,20 +466,19 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
       for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          if (c[r][i] && c[r][i] >= T) {
+          if (c[r][i] && c[r][i] >= T2) {
             const uint32_t q = atomicAdd(&sh.nsel, 1u);
             if (q < EFF_TOPK_M_MAX) { sh.cand_c[q] = c[r][i]; sh.cand_b[q] = b[r][i]; }
           }
         }
       stream([&](uint64_t v, uint32_t bits) {
-        if (v >= T) {
+        if (v >= T2) {
           const uint32_t q = atomicAdd(&sh.nsel, 1u);
           if (q < EFF_TOPK_M_MAX) { sh.cand_c[q] = v; sh.cand_b[q] = bits; }
         }
       });
-    } else {
-      // winners among the candidates in LDS (all of them: nc <= need), in place
-      if (tid == 0) sh.nsel = nc;
+    } else if (tid == 0) {
+      sh.nsel = n;   // not reached (a selected 4th listed composite is >= T): the candidates as ranked
     }
     __syncthreads();
     n = min(sh.nsel, (uint32_t)EFF_TOPK_M_MAX);
@@ -471,8 +491,8 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
       pairs[2 * rank + 1] = sh.cand_b[i];
     }
   }
-  // unused pair slots, the penalised logits and the header
-  for (uint32_t slot = n + (uint32_t)tid; slot < EFF_TOPK_CAP; slot += NT) {
+  // slots below need left empty, the penalised logits and the header
+  for (uint32_t slot = n + (uint32_t)tid; slot < need; slot += NT) {
     pairs[2 * slot] = 0u;
     pairs[2 * slot + 1] = 0u;
   }
