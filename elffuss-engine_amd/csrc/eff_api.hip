@@ -18,7 +18,7 @@
 using namespace eff;
 
 // Scratch of eff_topk_noalloc: the top-k group records of one call, in a
-// fixed device array of 16 KiB (the records of the largest vocabulary the
+// fixed device array of 18 KiB (the records of the largest vocabulary the
 // top-k accepts). Every GPU the library runs on holds its own copy until the
 // process ends. Host code never uses the array's name as an address: eff_init
 // looks up each device's copy once, with that device current
@@ -27,6 +27,7 @@ using namespace eff;
 // cleared; calls that overlap on one GPU share it and race.
 static constexpr size_t kNoAllocBytes = eff::kTopkScratchMax;
 static_assert(eff::topk_scratch_bytes_for(EFF_TOPK_N_MAX - 1u) <= kNoAllocBytes, "no-alloc scratch too small");
+static_assert(kNoAllocBytes == EFF_TOPK_NOALLOC_SCRATCH_BYTES, "no-alloc scratch size differs from the header's");
 static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
 
 namespace {
@@ -869,7 +870,7 @@ int eff_qgemv_topk(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, u
   if (ctx->gemv_kernel == 0 && gemv_rows_applies(wv, 1) && gemv_rows_groups(wv) <= kRowsTopkGroupsMax) {
     // the GEMV writes the top-k's group records; one launch selects from them
     const uint32_t groups = gemv_rows_groups(wv);
-    if ((rc = grow(ctx, &ctx->topk_scratch, &ctx->topk_scratch_bytes, (size_t)groups * kTopkRecordBytes, "topk")))
+    if ((rc = grow(ctx, &ctx->topk_scratch, &ctx->topk_scratch_bytes, (size_t)groups * kTopkGroupBytes, "topk")))
       return rc;
     hipError_t e = launch_gemv_rows_topk(wv, xp, yp, (uint8_t *)ctx->topk_scratch, m, penal_ids, n_penal, serial,
                                          (uint32_t *)out->ptr, ctx->stream);

@@ -269,7 +269,7 @@ __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu
           t.add(composite(bits, e), bits);
         }
       }
-      topk_record_wave(t, nan, rec + (uint64_t)blockIdx.x * kTopkRecordBytes);
+      topk_record_wave(t, nan, rec, blockIdx.x, gridDim.x);
     }
   }
 }

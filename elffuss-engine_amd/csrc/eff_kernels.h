@@ -105,18 +105,20 @@ hipError_t launch_dequant(const WeightView &wv, uint32_t n_blocks, float *out, h
 
 // Top-k (eff_topk.hip). The logits are cut into G <= kTopkGroupsMax groups
 // of 256 * ceil(vocab / 65536) consecutive logits; the first kernel writes
-// one kTopkRecordBytes record per group (its 4 largest elements), the second
-// selects from the records. The scratch is G records, at most 16 KiB for
-// any vocabulary.
+// one kTopkRecordBytes record per group (its 4 largest elements) and, in an
+// array after the G records, each group's largest composite (8 bytes); the
+// second selects from them. The scratch is G x kTopkGroupBytes, at most
+// 18 KiB for any vocabulary.
 constexpr uint32_t kTopkGroupsMax = 256;
 constexpr uint32_t kTopkRecordBytes = 64;
+constexpr uint32_t kTopkGroupBytes = kTopkRecordBytes + 8u;
 constexpr uint32_t kTopkRecordChunk = 4096;   // the reference's logits per chunk (header field `chunks`)
 constexpr uint32_t topk_group_size(uint32_t vocab) { return 256u * ((vocab + 65535u) / 65536u); }
 constexpr uint32_t topk_groups(uint32_t vocab) {
   return (vocab + topk_group_size(vocab) - 1u) / topk_group_size(vocab);
 }
-constexpr size_t topk_scratch_bytes_for(uint32_t vocab) { return (size_t)topk_groups(vocab) * kTopkRecordBytes; }
-constexpr size_t kTopkScratchMax = (size_t)kTopkGroupsMax * kTopkRecordBytes;
+constexpr size_t topk_scratch_bytes_for(uint32_t vocab) { return (size_t)topk_groups(vocab) * kTopkGroupBytes; }
+constexpr size_t kTopkScratchMax = (size_t)kTopkGroupsMax * kTopkGroupBytes;
 size_t topk_scratch_bytes(uint32_t vocab);
 
 hipError_t launch_topk(const uint32_t *logits, uint32_t base, uint32_t vocab, uint32_t m,

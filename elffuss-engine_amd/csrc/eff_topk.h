@@ -10,7 +10,9 @@
 // Record of a group of consecutive logits (kTopkRecordBytes = 64): u64 c[4]
 // (its 4 largest composites, descending, 0 past the group's elements), u32
 // bits[4] (their raw logits), u32 nan flag (1 when the group holds a NaN),
-// 12 bytes unused.
+// 12 bytes unused. The G records of a selection are followed by an array of
+// the G groups' largest composites (c[0] again, 8 bytes each), so that the
+// selection's first step reads 8 contiguous bytes per group.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -57,19 +59,22 @@ struct Top4 {
 };
 
 // Wave-wide maximum / minimum of a u32 (every lane active): DPP within rows
-// of 16 (quad xor 1, quad xor 2, half-row mirror, row mirror), then the four
-// rows through scalar reads. The result is wave-uniform.
+// of 16 (quad xor 1, quad xor 2, half-row mirror, row mirror), then rows 0 + 1
+// into row 1 and 2 + 3 into row 3 (row_bcast:15), rows 1 into 3
+// (row_bcast:31), and lane 63 read out. The result is wave-uniform. The DPP
+// moves read the operation's identity where a row takes no source, so each
+// fuses into the operation.
 template <bool MAX>
 __device__ __forceinline__ uint32_t wave_ext(uint32_t v) {
   auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
-  constexpr int id = MAX ? 0 : -1;   // the operation's identity (the patterns permute whole rows)
+  constexpr int id = MAX ? 0 : -1;
   v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0xB1, 0xF, 0xF, false));
   v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x4E, 0xF, 0xF, false));
   v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x141, 0xF, 0xF, false));
   v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x140, 0xF, 0xF, false));
-  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-  return op(op(r0, r1), op(r2, r3));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x142, 0xA, 0xF, false));   // row_bcast:15
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x143, 0xC, 0xF, false));   // row_bcast:31
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // Wave-wide maximum / minimum of a u64, as its high word then the low word
@@ -81,10 +86,11 @@ __device__ __forceinline__ uint64_t wave_ext64(uint64_t v) {
   return ((uint64_t)h << 32) | l;
 }
 
-// The group's record from the lanes' own 4 largest (every lane of the wave
+// Group g's record from the lanes' own 4 largest (every lane of the wave
 // active): 4 rounds of a wave maximum over the lanes' heads; lanes 0..3 write
-// the 64 bytes at `rec`.
-__device__ __forceinline__ void topk_record_wave(Top4 t, bool nan, uint8_t *rec) {
+// the 64 bytes of record g of `recs`, lane 4 the group's largest composite
+// into the array after the `groups` records.
+__device__ __forceinline__ void topk_record_wave(Top4 t, bool nan, uint8_t *recs, uint32_t g, uint32_t groups) {
   const uint32_t lane = threadIdx.x & 63u;
   uint64_t out_c[4];
   uint32_t out_b[4];
@@ -104,6 +110,8 @@ __device__ __forceinline__ void topk_record_wave(Top4 t, bool nan, uint8_t *rec)
     }
   }
   const bool any_nan = __ballot(nan) != 0u;
+  uint8_t *const rec = recs + (uint64_t)g * kTopkRecordBytes;
+  if (lane == 4u) *(uint64_t *)(recs + (uint64_t)groups * kTopkRecordBytes + 8u * g) = out_c[0];
   if (lane < 4u) {
     uint4 v;
     if (lane < 2u) {
@@ -263,13 +271,13 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
   uint64_t c[R][4];
   uint32_t b[R][4];
   uint32_t nan = 0;
-  // penalised ids: their raw logits (the penalty itself is applied by the
-  // sampler). Every thread loads, from clamped places, so that the loads are
-  // issued in a fixed order and each wait covers only what it needs.
-  const uint32_t pid = penal.ids[min((uint32_t)tid, (uint32_t)EFF_TOPK_P_MAX - 1u)];
-  // records through a buffer descriptor of the groups' bytes: a group past
-  // the last reads as zeros (no composites, no NaN)
+  // the groups' maxima, then their records, through buffer descriptors of
+  // their bytes: a group past the last reads as zeros (no composites, no NaN)
+  const rsrc_t ms = make_rsrc(rec + (uint64_t)groups * kTopkRecordBytes, (uint64_t)groups * 8u);
   const rsrc_t rs = make_rsrc(rec, (uint64_t)groups * kTopkRecordBytes);
+  uint32_t mk[R];   // the maxima's high words (order keys)
+#pragma unroll
+  for (int r = 0; r < R; ++r) mk[r] = __builtin_amdgcn_raw_buffer_load_b32(ms, (tid + NT * r) * 8 + 4, 0, 0);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int off = (tid + NT * r) * (int)kTopkRecordBytes;
@@ -284,10 +292,11 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
     b[r][0] = q2.x; b[r][1] = q2.y; b[r][2] = q2.z; b[r][3] = q2.w;
     nan |= q3;
   }
-  const bool pok = (uint32_t)tid < n_penal && pid < vocab;
-  const uint32_t pl = logits[pok ? pid : 0u];
-  const uint32_t pv = pok ? pl : 0u;
-  const bool wnan = __ballot(nan != 0u) != 0u;
+  // penalised ids: their raw logits (the penalty itself is applied by the
+  // sampler). Every thread loads, from clamped places, after the maxima and
+  // the records: the loads complete in order, and the first step waits only
+  // for the maxima.
+  const uint32_t pid = penal.ids[min((uint32_t)tid, (uint32_t)EFF_TOPK_P_MAX - 1u)];
   if (tid == 0) {
     sh.flags = 0u;
     sh.nsat = 0u;
@@ -343,7 +352,7 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
     // lower bound.
     uint32_t v[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) v[r] = (uint32_t)(c[r][0] >> 32);
+    for (int r = 0; r < R; ++r) v[r] = mk[r];
     uint32_t kth = 0;
     const int kw = (int)((need + NW - 1u) / NW);   // NW kw >= need of the maxima are >= tq
     for (int q = 0; q < kw; ++q) {
@@ -356,7 +365,11 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
     }
     if (lane == 0) sh.wkth[wave] = (uint64_t)kth << 32;
   }
+  const bool pok = (uint32_t)tid < n_penal && pid < vocab;
+  const uint32_t pl = logits[pok ? pid : 0u];
+  const uint32_t pv = pok ? pl : 0u;
   __syncthreads();
+  const bool wnan = __ballot(nan != 0u) != 0u;   // every lane active
   if (lane == 0 && wnan) atomicOr(&sh.flags, 2u);
   uint64_t tau = 0;
   uint32_t nc = ~0u;

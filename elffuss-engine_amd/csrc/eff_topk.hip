@@ -24,8 +24,9 @@ namespace eff {
 
 namespace {
 
-// Record of a group (kTopkRecordBytes = 64): u64 c[4] (0 past the group's
-// elements), u32 bits[4], u32 nan flag, 12 bytes unused.
+// Record of group g (kTopkRecordBytes = 64; eff_topk.h): u64 c[4] (0 past the
+// group's elements), u32 bits[4], u32 nan flag, 12 bytes unused; c[0] also in
+// the maxima array after the gridDim.x records.
 __global__ __launch_bounds__(64) void k_topk_groups(const uint32_t *__restrict__ logits, uint32_t vocab,
                                                     uint32_t per, uint8_t *__restrict__ rec) {
   const uint32_t lane = threadIdx.x;
@@ -50,7 +51,7 @@ __global__ __launch_bounds__(64) void k_topk_groups(const uint32_t *__restrict__
       }
     }
   }
-  topk_record_wave(t, nan, rec + (uint64_t)g * kTopkRecordBytes);
+  topk_record_wave(t, nan, rec, g, gridDim.x);
 }
 
 constexpr int kPickThreads = 256;

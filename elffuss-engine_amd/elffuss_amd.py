@@ -23,7 +23,7 @@ TYPES = {"Q8_0": Q8_0, "Q2_K": Q2_K, "Q4_K": Q4_K, "Q6_K": Q6_K, "IQ2_XXS": IQ2_
 OPT_GEMV_MAX_TOKENS, OPT_GEMM_MIN_TOKENS, OPT_GEMV_KERNEL, OPT_SPLIT_CONFIG = 1, 2, 3, 4
 GEMV_SECTIONS, GEMV_SWIGLU = 1, 2
 TOPK_HEADER, TOPK_P_MAX, TOPK_CAP, TOPK_M_MAX = 8, 128, 256, 192
-TOPK_NOALLOC_SCRATCH_BYTES = 16384
+TOPK_NOALLOC_SCRATCH_BYTES = 18432
 
 ERRORS = {E_INVALID: "invalid argument", E_TYPE: "unsupported type", E_SHAPE: "shape",
           E_MARK: "repack mark", E_BOUNDS: "bounds", E_DEVICE: "device", E_NOMEM: "out of memory"}

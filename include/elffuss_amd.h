@@ -315,13 +315,13 @@ int eff_qgemv_topk(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, u
 /* eff_topk without any device allocation. No counterpart in the reference:
  * it is for callers that cannot allocate (code under HIP graph capture,
  * serving loops that forbid hipMalloc). The top-k's group records go to a
- * fixed device array of the library (16 KiB, one per GPU, held until the
+ * fixed device array of the library (18 KiB, one per GPU, held until the
  * process ends) instead of the context's scratch; it holds the records of
  * every vocabulary eff_topk accepts (vocab < EFF_TOPK_N_MAX), and a call that
  * would need more is refused with EFF_E_BOUNDS. Same output and
  * NOT_APPLICABLE cases as eff_topk. Calls that overlap on one GPU (several
  * streams or contexts at once) share the array and race. */
-#define EFF_TOPK_NOALLOC_SCRATCH_BYTES 16384u
+#define EFF_TOPK_NOALLOC_SCRATCH_BYTES 18432u
 int eff_topk_noalloc(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint32_t m,
                      const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, eff_buf *out);
 
