@@ -58,6 +58,7 @@ struct eff_ctx {
   void *sx_scratch = nullptr;       // x as fp16 hi/lo parts for the split-x product
   size_t sx_scratch_bytes = 0;
   int64_t sx_config = 0;
+  int64_t sx_min_tokens = 0;        // 0: the measured default (sx_routes)
   // Pinned staging ring of eff_buf_write: the source bytes are copied here on
   // the calling thread and the device copy is enqueued from here, so a write
   // returns without waiting for the device. `pend` holds the ring ranges whose
@@ -173,8 +174,17 @@ int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_
 // reference's fp16 GEMMs accept (GEMM2_TIPOS, kernels.gemm2.wgsl.js:51).
 bool router_gemm_type(int type) { return type == EFF_TYPE_Q8_0 || type == EFF_TYPE_Q8_0R; }
 
+// The split-x product from 8 tokens (Q4_K: 9); below, the int8 matrix-core
+// GEMVs, which are as accurate and were faster at 4 tokens (C5 shapes: 6.0 /
+// 6.9 / 6.2 us against 8.3 / 8.3 / 8.9 for Q2_K / IQ2_XXS / Q4_K) and about
+// even at 8 (Q4_K: 8.2 against 8.9).
+bool sx_routes(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens) {
+  const int64_t lo = ctx->sx_min_tokens ? ctx->sx_min_tokens : (wv.type == Q4_K ? 9 : 8);
+  return ctx->gemv_kernel == 0 && sx_applies(wv, tokens) && (int64_t)tokens >= lo;
+}
+
 int run_gemv(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
-  if (ctx->gemv_kernel == 0 && sx_applies(wv, tokens)) return run_sx(ctx, wv, x, y, tokens);
+  if (sx_routes(ctx, wv, tokens)) return run_sx(ctx, wv, x, y, tokens);
   GemvPlan p;
   hipError_t e;
   if (ctx->gemv_kernel == 0 && gemv_rows_applies(wv, tokens)) {
@@ -364,6 +374,11 @@ int eff_set_option(eff_ctx *ctx, int option, int64_t value) {
     case EFF_OPT_SPLIT_CONFIG:
       if (value < 0 || value > 3) return fail(ctx, EFF_E_INVALID, "split-x configuration must be 0..3, got %lld", (long long)value);
       ctx->sx_config = value;
+      return EFF_OK;
+    case EFF_OPT_SPLIT_MIN_TOKENS:
+      if (value != 0 && value < 4)
+        return fail(ctx, EFF_E_INVALID, "split-x min tokens must be 0 or >= 4, got %lld", (long long)value);
+      ctx->sx_min_tokens = value;
       return EFF_OK;
     default: return fail(ctx, EFF_E_INVALID, "unknown option %d", option);
   }
@@ -677,7 +692,7 @@ int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint
   // Q2_K, Q4_K, IQ2_XXS: the reference has no f16 GEMM for these types (DRIFT
   // and GEMM2 read Q8_0/Q4_0 only) and runs its f32 kernel at every token
   // count; so does this router, on the split-x matrix cores.
-  if (ctx->gemv_kernel == 0 && sx_applies(wv, tokens)) return run_sx(ctx, wv, xp, yp, tokens);
+  if (sx_routes(ctx, wv, tokens)) return run_sx(ctx, wv, xp, yp, tokens);
   // The fp16 GEMM is the reference's DRIFT/GEMM2 semantics, which exist for
   // Q8_0 (and Q4_0) only (kernels.drift.wgsl.js:33, kernels.gemm2.wgsl.js:51);
   // Q6_K prefill stays on its f32 path there (ops.js:117-128), and here on the

@@ -55,6 +55,8 @@ extern "C" {
 #define EFF_OPT_SPLIT_CONFIG     4  /* split-x product workgroups (tuning): 0 automatic (default), 1: 32 rows x
                                        8 waves, 2: 64 rows x 4 waves, 3: 64 rows x 4 waves with k halves in two
                                        workgroups added into y */
+#define EFF_OPT_SPLIT_MIN_TOKENS 5  /* Q2_K, Q4_K, IQ2_XXS: tokens >= this run the split-x product, fewer the int8
+                                       matrix-core GEMVs (0: automatic, 8 and 9 for Q4_K (default); else >= 4) */
 
 /* ---- fused GEMV modes (gemv2Shader `modo`, kernels.gemv.wgsl.js:370-375) -- */
 #define EFF_GEMV_SECTIONS  1  /* 'secciones': ys[i] = W_i x for 2..4 matrices */
@@ -80,7 +82,7 @@ typedef struct eff_stats {
   uint64_t dequant;     /* dequant launches */
   uint64_t topk;        /* top-k calls (records + selection; eff_topk, eff_topk_noalloc, eff_qgemv_topk) */
   uint64_t not_applicable;  /* calls answered EFF_NOT_APPLICABLE */
-  uint64_t split;       /* split-x matrix-core launches (Q2_K, Q4_K, IQ2_XXS from 4 tokens) */
+  uint64_t split;       /* split-x matrix-core launches (Q2_K, Q4_K, IQ2_XXS from EFF_OPT_SPLIT_MIN_TOKENS) */
   uint64_t fused;       /* fused GEMV launches (eff_qgemv_multi) */
   uint64_t gather;      /* gather launches (eff_gather, eff_gather_norm) */
 } eff_stats;
@@ -230,7 +232,8 @@ int eff_fill_normal(uint32_t seed, float sigma, float *dst, size_t n);
 
 /* Y[tokens][rows] = W (rows x k, quantized) . X[tokens][k]; X and Y are f32.
  * Router of quant.matmul (ops.js:827-1101): tokens <= GEMV max -> GEMV;
- * Q2_K, Q4_K, IQ2_XXS from 4 tokens -> split-x product (f32-accurate);
+ * Q2_K, Q4_K, IQ2_XXS from EFF_OPT_SPLIT_MIN_TOKENS (8; 9 for Q4_K) -> split-x
+ * product (f32-accurate; fewer tokens run the int8 matrix-core GEMVs, as accurate);
  * Q8_0/Q8_0R at tokens >= GEMM min -> fp16 MFMA GEMM (the reference's
  * DRIFT/GEMM2 types, kernels.drift.wgsl.js:33); otherwise (Q6_K at every
  * token count, Q8_0 below GEMM min) -> GEMV over token groups, f32-accurate.

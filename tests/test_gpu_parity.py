@@ -349,14 +349,22 @@ def test_fused_not_applicable_and_errors(ctx, eff):
     assert e.value.code == eff.E_SHAPE
 
 
-# ---- split-x product (Q2_K, Q4_K, IQ2_XXS from 4 tokens) -----------------------------
+# ---- split-x product (Q2_K, Q4_K, IQ2_XXS; from 8 tokens by default, from 4 here) ----
+
+@pytest.fixture
+def split_from_4(ctx, eff):
+    """The split-x product at every token count it accepts (4 and up)."""
+    ctx.set_option(eff.OPT_SPLIT_MIN_TOKENS, 4)
+    yield
+    ctx.set_option(eff.OPT_SPLIT_MIN_TOKENS, 0)
+
 
 SPLIT_TYPES = ["Q2_K", "Q4_K", "IQ2_XXS"]
 
 
 @pytest.mark.parametrize("tname", SPLIT_TYPES)
 @pytest.mark.parametrize("tokens", [4, 7, 16, 17, 33, 64, 100, 129])
-def test_split_x_vs_f64_oracle(ctx, eff, orc, tname, tokens):
+def test_split_x_vs_f64_oracle(ctx, eff, orc, tname, tokens, split_from_4):
     """f32 accuracy at every token count: 1, 2 and 4 token tiles per wave and
     several token groups; rows not a multiple of the 32/64-row tiles; k = 2304
     (9 blocks: waves with one and with two blocks, odd IQ2_XXS block offsets)."""
@@ -404,7 +412,7 @@ def test_split_x_k_and_configs(ctx, eff, orc, tname, k):
 
 
 @pytest.mark.parametrize("tname", SPLIT_TYPES)
-def test_split_x_dynamic_range_and_non_finite(ctx, eff, orc, tname):
+def test_split_x_dynamic_range_and_non_finite(ctx, eff, orc, tname, split_from_4):
     """x scaled per (token, 256-block): zero, tiny, huge and subnormal values in
     one block, outliers among ordinary values, a whole token at 1e-3; a NaN or an
     infinity makes only its own token's outputs non-finite."""
@@ -446,10 +454,11 @@ def test_router_paths_and_stats(ctx, eff, orc):
         ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
         check_close(yb.read(np.float32), orc.gemv_f64(orc.Q4_K, gguf, rows, k, x, tokens), f"matmul T={tokens}")
     after = ctx.stats()
-    # 1..8 tokens count as GEMV calls; Q4_K from 4 tokens runs the split-x
-    # product at every token count (f32 accuracy, as the reference's generic kernel)
+    # 1..8 tokens count as GEMV calls (the int8 matrix-core GEMVs); Q4_K from 9
+    # tokens runs the split-x product at every token count (f32 accuracy, as
+    # the reference's generic kernel)
     assert after["gemv"] - before["gemv"] == 2
-    assert after["split"] - before["split"] == 4
+    assert after["split"] - before["split"] == 3
     assert after["skinny"] == before["skinny"] and after["gemm"] == before["gemm"]
     # Q8_0 keeps the token-group GEMV below 64 tokens and the fp16 GEMM from 64
     t8, data8, gguf8, _ = make_weights(eff, "Q8_0", rows, k, 92)
@@ -462,6 +471,31 @@ def test_router_paths_and_stats(ctx, eff, orc):
         check_close(yb.read(np.float32), oracle_fn(orc.Q8_0, gguf8, rows, k, x, tokens), f"matmul Q8_0 T={tokens}")
     after = ctx.stats()
     assert after["skinny"] - before["skinny"] == 3 and after["gemm"] - before["gemm"] == 1
+
+
+def test_router_split_x_threshold(ctx, eff, orc):
+    """Q2_K: 7 tokens run the int8 matrix-core GEMV, 8 the split-x product, both
+    against the f64 oracle; the option moves the threshold and refuses 1..3."""
+    rows, k = 96, 512
+    t, data, gguf, n = make_weights(eff, "Q2_K", rows, k, 95)
+    wb = ctx.upload(data)
+    for tokens, low, split in ((7, 0, 0), (8, 0, 1), (7, 4, 1)):
+        x = eff.fill_normal(96 + tokens, 1.0, tokens * k)
+        xb, yb = ctx.upload(x), ctx.alloc(tokens * rows * 4)
+        ctx.set_option(eff.OPT_SPLIT_MIN_TOKENS, low)
+        try:
+            before = ctx.stats()["split"]
+            ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+            assert ctx.stats()["split"] - before == split, (tokens, low)
+        finally:
+            ctx.set_option(eff.OPT_SPLIT_MIN_TOKENS, 0)
+        check_close(yb.read(np.float32), orc.gemv_f64(orc.Q2_K, gguf, rows, k, x, tokens),
+                    f"matmul Q2_K T={tokens} split-x from {low or 'default'}")
+        xb.free()
+        yb.free()
+    with pytest.raises(eff.EffError):
+        ctx.set_option(eff.OPT_SPLIT_MIN_TOKENS, 3)
+    wb.free()
 
 
 @pytest.mark.parametrize("tokens", [64, 100, 512])
