@@ -122,6 +122,99 @@ __global__ __launch_bounds__(256) void k_sx_prep(const float *__restrict__ x, ui
 }
 
 // ---------------------------------------------------------------------------
+// The same preparation inside the product for up to 8 tokens (one block of
+// 8 tokens per call, the wave's lanes holding 4 values of each as in
+// k_sx_prep, the same arithmetic): into the wave's LDS, whose fragment slots
+// hold only the rows of tokens 0..7 (kSxFxSlot bytes: row
+// 16 hf + 8 part + token, the MFMA lanes of tokens 8..15 reading zeros), and
+// the token's scale into xps[token]. Row r of slot s sits at r ^ (s % 16):
+// the 16 slots a store spans are 512 bytes apart, and without the swizzle
+// its lanes would fall into the same banks.
+constexpr uint32_t kSxFxSlot = 512;
+
+__device__ __forceinline__ uint32_t sx_fx_at(uint32_t s, uint32_t row) { return s * kSxFxSlot + 16u * (row ^ (s & 15u)); }
+
+// All 8 token rows of one block (v[t]: token t's 4 values of the lane; rows
+// of absent tokens read zeros), phase by phase across the tokens so that
+// their 8 dependent chains interleave.
+template <int TYPE>
+__device__ __forceinline__ void sx_fill8(const float4 (&v)[8], uint32_t lane, uint8_t *fr, float *xps) {
+  // max |x| of each token's block as u32 bit patterns (non-negative floats
+  // order as their bits; a non-finite value counts as infinity): DPP within
+  // rows, then rows 1 and 3 (row_bcast:15), row 3 (row_bcast:31), lane 63
+  uint32_t m[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const bool fin = isfinite(v[t].x) && isfinite(v[t].y) && isfinite(v[t].z) && isfinite(v[t].w);
+    const uint32_t a = max(max(__float_as_uint(fabsf(v[t].x)), __float_as_uint(fabsf(v[t].y))),
+                           max(__float_as_uint(fabsf(v[t].z)), __float_as_uint(fabsf(v[t].w))));
+    m[t] = fin ? a : 0x7F800000u;
+  }
+#define SX_DPP_MAX(ctrl, rmask)                                                                 \
+  _Pragma("unroll") for (int t = 0; t < 8; ++t)                                                 \
+    m[t] = max(m[t], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m[t], ctrl, rmask, 0xF, false));
+  SX_DPP_MAX(0xB1, 0xF)
+  SX_DPP_MAX(0x4E, 0xF)
+  SX_DPP_MAX(0x141, 0xF)
+  SX_DPP_MAX(0x140, 0xF)
+  SX_DPP_MAX(0x142, 0xA)
+  SX_DPP_MAX(0x143, 0xC)
+#undef SX_DPP_MAX
+  float xs[8][4];
+  float sc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const float mf = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)m[t], 63));
+    const bool ok = mf < INFINITY;
+    int e = 0;
+    if (ok && mf > 0.f) (void)frexpf(mf, &e);  // mf < 2^e
+    const int sh = 14 - e;
+    xs[t][0] = ok ? ldexpf(v[t].x, sh) : 0.f;
+    xs[t][1] = ok ? ldexpf(v[t].y, sh) : 0.f;
+    xs[t][2] = ok ? ldexpf(v[t].z, sh) : 0.f;
+    xs[t][3] = ok ? ldexpf(v[t].w, sh) : 0.f;
+    sc[t] = ok ? ldexpf(1.f, e - 14) : NAN;
+  }
+  const uint32_t st = lane >> 2, hf = (lane >> 1) & 1u, q = lane & 1u;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    half4 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      hi[i] = (_Float16)xs[t][i];
+      lo[i] = (_Float16)(xs[t][i] - (float)hi[i]);
+    }
+    *(half4 *)(fr + sx_fx_at(st, 16u * hf + t) + 8u * q) = hi;
+    *(half4 *)(fr + sx_fx_at(st, 16u * hf + 8u + t) + 8u * q) = lo;
+  }
+  if constexpr (TYPE != IQ2_XXS) {
+    static_assert(TYPE == Q2_K, "16-value group sums");
+    // group sums: the 4 lanes of a group, (own + lane ^ 1) + (lane ^ 2)'s pair
+    float sum[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) sum[t] = (xs[t][0] + xs[t][1]) + (xs[t][2] + xs[t][3]);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      sum[t] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum[t]), 0xB1, 0xF, 0xF, false));
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      sum[t] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum[t]), 0x4E, 0xF, 0xF, false));
+    if (lane % 4u == 0u) {
+      const uint32_t g = lane / 4u, hm = g >> 3, jj = g & 7u;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const float sp = sum[t] * 0.0625f;
+        const _Float16 shi = (_Float16)sp, slo = (_Float16)(sp - (float)shi);
+        *(_Float16 *)(fr + sx_fx_at(16u, 16u * hm + t) + 2u * jj) = shi;
+        *(_Float16 *)(fr + sx_fx_at(16u, 16u * hm + 8u + t) + 2u * jj) = slo;
+      }
+    }
+  }
+  if (lane < 8u) xps[lane] = lane == 0u ? sc[0] : lane == 1u ? sc[1] : lane == 2u ? sc[2] : lane == 3u ? sc[3]
+                            : lane == 4u ? sc[4] : lane == 5u ? sc[5] : lane == 6u ? sc[6] : sc[7];
+}
+
+// ---------------------------------------------------------------------------
 // Weight operands. `r` points to the staged dwords of the lane's row (the
 // block's first byte at byte offset `a` of r[0]); `step` returns the 8
 // weights u of step s (k 16 s + 8 h .. + 7 of the block) for lane half h.
@@ -272,16 +365,31 @@ struct SxLds {
   static constexpr uint32_t BYTES = TAB + WORK;
 };
 
-template <int TYPE, int TT, int RF, int NW, int KS>
+// FX: up to 8 tokens, x prepared by the product itself (sx_fill) from the
+// f32 xf: per wave, block by block, x's rows go to LDS by direct-to-LDS loads
+// issued before the block's weights, so that the preparation runs while the
+// weights are in flight. LDS (dynamic): the tables and stages as without FX,
+// then per wave sx_fx_bytes<TYPE>(): 8 x 1 KB of raw x, NS fragment slots of
+// kSxFxSlot bytes, 16 scales.
+template <int TYPE>
+constexpr uint32_t sx_fx_bytes() {
+  return 8u * 1024u + sx_slots<TYPE>() * kSxFxSlot + 64u;
+}
+
+template <int TYPE, int TT, int RF, int NW, int KS, bool FX>
 __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__restrict__ xa,
                                                 const float *__restrict__ xp, float *__restrict__ y,
-                                                uint32_t tokens, uint32_t nbw, uint32_t xa_bytes) {
+                                                uint32_t tokens, uint32_t nbw, uint32_t xa_bytes,
+                                                const float *__restrict__ xf) {
   using W = SxW<TYPE>;
   using L = SxLds<TYPE, TT, RF, NW>;
+  static_assert(!FX || (TT == 1 && KS == 1), "the fused preparation covers one token tile");
   constexpr uint32_t NS = sx_slots<TYPE>();
   constexpr uint32_t P = TT == 1 ? 16u : TT == 2 ? 8u : 4u;  // steps of x fragments loaded ahead
   constexpr uint32_t ROWS = L::ROWS, ND = L::ND;
-  __shared__ __align__(16) uint8_t lds[L::BYTES];
+  __shared__ __align__(16) uint8_t lds_s[FX ? 16u : L::BYTES];
+  extern __shared__ __align__(16) uint8_t lds_d[];
+  uint8_t *const lds = FX ? lds_d : lds_s;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, j = lane & 31u, h = lane >> 5;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // KS = 2: workgroup pairs take the two halves of k and add into y
@@ -318,6 +426,18 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
     soff[i] = min(r0 + min(rr, ROWS - 1u), rows - 1u) * rb + 4u * dw;
   }
   const rsrc_t xsrc = make_rsrc(xa, xa_bytes);
+  // FX: this wave's raw x, fragments and scales
+  uint8_t *const xw = lds + L::TAB + L::WORK + wave * sx_fx_bytes<TYPE>();
+  uint8_t *const xfr = xw + 8u * 1024u;
+  float *const xps = (float *)(xfr + NS * kSxFxSlot);
+  const rsrc_t fsrc = make_rsrc(xf, (uint64_t)tokens * wv.k * 4u);
+  // the lane's fragment row, and whether it is a row of tokens 0..7
+  const uint32_t frow = 16u * (lane >> 5) + 8u * ((lane >> 4) & 1u) + (lane & 7u);
+  const bool fval = (lane & 15u) < 8u;
+  if constexpr (FX) {
+    // the rows of tokens past `tokens` and their scales stay zero
+    for (uint32_t o = 16u * lane; o < NS * kSxFxSlot + 64u; o += 1024u) *(u32x4 *)(xfr + o) = u32x4{0u, 0u, 0u, 0u};
+  }
 
   float acc[TT][RF][8];
 #pragma unroll
@@ -330,6 +450,9 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
   const uint32_t bl = kh * nb / (uint32_t)KS, bh = (kh + 1u) * nb / (uint32_t)KS;
   const uint32_t b0 = bl + wave * nbw, b1 = min(b0 + nbw, bh);
   for (uint32_t bi = b0; bi < b1; ++bi) {
+    // FX: the block's x, token by token, ahead of its weights
+    if constexpr (FX)
+      for (uint32_t t = 0; t < tokens; ++t) dma16(fsrc, xw + 1024u * t, 16u * lane, (t * wv.k + 256u * bi) * 4u);
     // this block of the tile's rows into the wave's stage
     const uint32_t bo = bi * W::BB;
 #pragma unroll
@@ -343,10 +466,28 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
     auto xoff = [&](uint32_t tt, uint32_t s) {
       return (((tg * TT + tt) * nb + bi) * NS + s) * 1024u;
     };
+    u32x4 A[FX ? 1 : P][TT];
+    half8 am[TT];
+    float4 pa[TT], pb[TT];
+    if constexpr (FX) {
+      // the raw x is in (its loads went out before the weights'); prepare it
+      wait_vm<ND>();
+      float4 v[8];
+#pragma unroll
+      for (uint32_t t = 0; t < 8u; ++t)
+        v[t] = t < tokens ? *(const float4 *)(xw + 1024u * t + 16u * lane) : make_float4(0.f, 0.f, 0.f, 0.f);
+      // all 8 rows every block (tokens past `tokens` read zeros and give zero rows)
+      sx_fill8<TYPE>(v, lane, xfr, xps);
+      am[0] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+      if constexpr (W::MINS)
+        am[0] = fval ? *(const half8 *)(xfr + sx_fx_at(16u, frow)) : am[0];
+      pa[0] = *(const float4 *)(xps + 4u * h);
+      pb[0] = *(const float4 *)(xps + 8u + 4u * h);
+      wait_vm<0>();
+    } else {
     // (each group of loads is followed by a compiler memory barrier, which
     // keeps it where it is: the compiler otherwise moves loads down to their
     // first use, and every step then waits a full round trip)
-    u32x4 A[P][TT];
 #pragma unroll
     for (uint32_t s = 0; s < P; ++s)
 #pragma unroll
@@ -356,8 +497,6 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
     // for the scales: a 16-byte buffer load whose elements are taken one by
     // one as floats is narrowed to one dword by this compiler, every element
     // then reading the first)
-    half8 am[TT];
-    float4 pa[TT], pb[TT];
 #pragma unroll
     for (uint32_t tt = 0; tt < (uint32_t)TT; ++tt) {
       am[tt] = half8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -369,6 +508,7 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
     }
     __asm__ volatile("" ::: "memory");
     wait_vm<P * TT + (W::MINS ? TT : 0) + 2 * TT>();
+    }
 
     W w[RF];
     const uint32_t *rp[RF];
@@ -385,15 +525,19 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
       half8 B[RF];
 #pragma unroll
       for (int f = 0; f < RF; ++f) B[f] = w[f].step(rp[f], (int)s, h, tab);
-      const u32x4 *As = A[s % P];
       half8 a8[TT];
+      if constexpr (FX) {
+        const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+        a8[0] = fval ? *(const half8 *)(xfr + sx_fx_at(s, frow)) : z;
+      } else {
 #pragma unroll
-      for (int tt = 0; tt < TT; ++tt) a8[tt] = __builtin_bit_cast(half8, As[tt]);
-      if (s + P < 16u) {
+        for (int tt = 0; tt < TT; ++tt) a8[tt] = __builtin_bit_cast(half8, A[s % P][tt]);
+        if (s + P < 16u) {
 #pragma unroll
-        for (uint32_t tt = 0; tt < (uint32_t)TT; ++tt)
-          A[s % P][tt] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)(16u * lane), (int)xoff(tt, s + P), 0);
-        __asm__ volatile("" ::: "memory");
+          for (uint32_t tt = 0; tt < (uint32_t)TT; ++tt)
+            A[s % P][tt] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)(16u * lane), (int)xoff(tt, s + P), 0);
+          __asm__ volatile("" ::: "memory");
+        }
       }
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt)
@@ -477,8 +621,26 @@ hipError_t sx_go(const WeightView &wv, const uint8_t *xa, const float *xp, float
                  const SxPlan &p, hipStream_t s) {
   const uint64_t tiles = (uint64_t)p.groups * p.tt;
   const uint32_t xa_bytes = (uint32_t)(tiles * wv.bpr * sx_slots<TYPE>() * 1024u);
-  hipLaunchKernelGGL((k_sx<TYPE, TT, RF, NW, KS>), dim3(p.row_tiles * KS, p.groups), dim3(NW * 64), 0, s, wv, xa,
-                     xp, y, tokens, p.nbw, xa_bytes);
+  hipLaunchKernelGGL((k_sx<TYPE, TT, RF, NW, KS, false>), dim3(p.row_tiles * KS, p.groups), dim3(NW * 64), 0, s, wv,
+                     xa, xp, y, tokens, p.nbw, xa_bytes, nullptr);
+  return hipGetLastError();
+}
+
+// The product with its own preparation (up to 8 tokens, 32 rows x 8 waves).
+template <int TYPE>
+hipError_t sx_go_fx(const WeightView &wv, const float *x, float *y, uint32_t tokens, const SxPlan &p, hipStream_t s) {
+  using L = SxLds<TYPE, 1, 1, 8>;
+  constexpr uint32_t lds = L::TAB + L::WORK + 8u * sx_fx_bytes<TYPE>();
+  static_assert(lds + 16u <= kMxMaxLds, "fused split-x LDS");
+  static bool attr = false;
+  const void *fn = (const void *)k_sx<TYPE, 1, 1, 8, 1, true>;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  hipLaunchKernelGGL((k_sx<TYPE, 1, 1, 8, 1, true>), dim3(p.row_tiles, 1), dim3(8 * 64), lds, s, wv, nullptr, nullptr,
+                     y, tokens, p.nbw, 0u, x);
   return hipGetLastError();
 }
 
@@ -496,6 +658,9 @@ template <int TYPE>
 hipError_t sx_type(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint8_t *scratch, int cfg,
                    hipStream_t s) {
   const SxPlan p = sx_plan(wv, tokens, cfg);
+  // up to 8 tokens of Q2_K / IQ2_XXS with the automatic plan: one launch
+  if constexpr (TYPE == Q2_K || TYPE == IQ2_XXS)
+    if (cfg == 0 && tokens <= 8u && p.cfg == 0u) return sx_go_fx<TYPE>(wv, x, y, tokens, p, s);
   const uint32_t tiles = p.groups * p.tt, nb = wv.bpr;
   uint8_t *xa = scratch;
   float *xp = (float *)(scratch + (uint64_t)tiles * nb * sx_slots<TYPE>() * 1024u);

@@ -411,6 +411,34 @@ def test_split_x_k_and_configs(ctx, eff, orc, tname, k):
         yb.free()
 
 
+@pytest.mark.parametrize("tname", ["Q2_K", "IQ2_XXS"])
+@pytest.mark.parametrize("tokens,k", [(4, 2304), (8, 2048), (8, 4096), (5, 256)])
+def test_split_x_one_launch_bit_identical(ctx, eff, orc, tname, tokens, k, split_from_4):
+    """Up to 8 tokens of Q2_K / IQ2_XXS the product prepares x itself (one
+    launch); the same 32 x 8 plan with the preparation launch
+    (EFF_OPT_SPLIT_CONFIG = 1) gives the same bits, and both meet the f64 bar
+    (one and two blocks per wave, a single block per row)."""
+    rows = 300
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 500 + tokens + k)
+    x = eff.fill_normal(5000 + tokens + k, 1.0, tokens * k)
+    wb, xb = ctx.upload(data), ctx.upload(x)
+    got = []
+    for cfg in (0, 1):
+        yb = ctx.alloc(tokens * rows * 4)
+        ctx.set_option(eff.OPT_SPLIT_CONFIG, cfg)
+        try:
+            ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+        finally:
+            ctx.set_option(eff.OPT_SPLIT_CONFIG, 0)
+        got.append(yb.read(np.uint32))
+        yb.free()
+    assert np.array_equal(got[0], got[1])
+    check_close(got[0].view(np.float32), orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens),
+                f"split-x one launch {tname} M={tokens} k={k}")
+    wb.free()
+    xb.free()
+
+
 @pytest.mark.parametrize("tname", SPLIT_TYPES)
 def test_split_x_dynamic_range_and_non_finite(ctx, eff, orc, tname, split_from_4):
     """x scaled per (token, 256-block): zero, tiny, huge and subnormal values in
