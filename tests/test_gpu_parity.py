@@ -719,6 +719,7 @@ def test_topk_clustered_in_one_group(ctx, eff, orc, vocab, m):
     ("Q6_K", 65664, 512, 100, True),       # 513 groups
     ("Q6_K", 65536, 512, 40, True),        # the wave-maximum threshold, then a saturated group read whole
     ("Q6_K", 40000, 2304, 40, False),      # an odd block count per row (per-row load offsets)
+    ("Q6_K", 131072, 512, 64, False),      # 1024 groups, the most one selection holds (two per thread)
     ("Q6_K", 131073, 512, 40, False),      # more groups than one selection holds: GEMV, then eff_topk
     ("Q8_0", 50000, 512, 40, False),       # no row kernel: GEMV, then eff_topk
 ])
@@ -754,6 +755,25 @@ def test_qgemv_topk_equals_gemv_then_topk(ctx, eff, orc, tname, rows, k, m, clus
         ctx.qgemv_topk(t, wb, xb, y1, rows, k, eff.TOPK_M_MAX + 1)
     assert not np.any(y1.read(np.uint32))
     for b in (wb, xb, y1, y2, o1, o2):
+        b.free()
+
+
+def test_qgemv_topk_nan_in_x(ctx, eff, orc):
+    """A NaN in x makes every logit of the head NaN: the record from the GEMV's
+    group records equals eff_topk over the same logits bit for bit, NaN flag set."""
+    rows, k, m = 65536, 512, 40
+    w = eff.quantize("Q6_K", eff.fill_normal(21, 0.02, rows * k))
+    x = eff.fill_normal(22, 1.0, k)
+    x[100] = np.nan
+    t = eff.TYPES["Q6_K"]
+    wb, xb, y1 = ctx.upload(w), ctx.upload(x), ctx.alloc(rows * 4)
+    o1 = ctx.qgemv_topk(t, wb, xb, y1, rows, k, m, [], serial=9)
+    o2 = ctx.topk(y1, 0, rows, m, [], serial=9)
+    assert np.all(np.isnan(y1.read(np.float32)))
+    ra, rb = o1.read(np.uint32), o2.read(np.uint32)
+    assert np.array_equal(ra, rb)
+    assert eff.parse_topk(ra)["flags"] & 2
+    for b in (wb, xb, y1, o1, o2):
         b.free()
 
 
