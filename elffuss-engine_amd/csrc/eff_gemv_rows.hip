@@ -147,7 +147,8 @@ __device__ __forceinline__ void rows_read(const uint8_t *tp, uint32_t n, uint32_
 }
 
 // REC: the decode head. Each workgroup also writes the top-k record of its
-// 128 rows (their 4 largest logits, eff_topk.h) for k_rows_pick.
+// 128 rows, its 4 interleaved tiles of 32 (their 4 largest logits,
+// eff_topk.h), for k_rows_pick.
 template <bool REC, uint32_t KS>
 // amdgpu_waves_per_eu(4): at most 128 VGPRs, so that two workgroups share a CU.
 __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gemv_rows_q6k(
@@ -166,7 +167,10 @@ __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu
   const uint32_t ncol = bpr > ks ? (bpr - ks + KS - 1u) / KS : 0u;   // block columns of this slice
   const rsrc_t src = make_rsrc(wv.w, wv.w_bytes);
   // first row of tile t of this wave
-  auto tile_row = [&](uint32_t t) { return blockIdx.x * kRowsPerWG + (t * RG + rg) * kRowsTile; };
+  // first row of tile t of this wave: the workgroups' tiles interleave (tile
+  // q of workgroup b is the matrix's tile q G + b), so that the workgroups
+  // running at once read one region of the matrix rather than G far apart
+  auto tile_row = [&](uint32_t t) { return ((t * RG + rg) * gridDim.x + blockIdx.x) * kRowsTile; };
 
   // Load i of the lane fills LDS chunk s = 64 i + lane = row s / 15, chunk
   // s % 15 of that row; chunk 14 repeats 13 (a cache hit) so that rows are
@@ -246,7 +250,7 @@ __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu
   // a row's KS slice sums in order
   __syncthreads();
   if (tid < kRowsPerWG) {
-    const uint32_t qt = tid / kRowsTile, r = tid % kRowsTile, row = blockIdx.x * kRowsPerWG + tid;
+    const uint32_t qt = tid / kRowsTile, r = tid % kRowsTile, row = (qt * gridDim.x + blockIdx.x) * kRowsTile + r;
     float v = red[qt * KS * kRowsTile + r];
 #pragma unroll
     for (uint32_t s2 = 1; s2 < KS; ++s2) v += red[(qt * KS + s2) * kRowsTile + r];
@@ -256,13 +260,12 @@ __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu
   if constexpr (REC) {
     __syncthreads();
     if (wave == 0u) {
-      // rows l and l + 64 of the workgroup's 128
-      const uint32_t base = blockIdx.x * kRowsPerWG;
+      // outputs l and l + 64 of the workgroup's 128 (tile i / 32, row i % 32)
       Top4 t;
       bool nan = false;
 #pragma unroll
       for (uint32_t h = 0; h < kRowsPerWG / 64u; ++h) {
-        const uint32_t i = lane + 64u * h, e = base + i;
+        const uint32_t i = lane + 64u * h, e = ((i / kRowsTile) * gridDim.x + blockIdx.x) * kRowsTile + i % kRowsTile;
         if (e < rows) {
           const uint32_t bits = fin[i];
           nan |= is_nan_bits(bits);
@@ -281,7 +284,8 @@ __global__ __launch_bounds__(kRowsWaves * 64) void k_rows_pick(const uint32_t *_
                                                                RowsPick pk, uint32_t groups,
                                                                const uint8_t *__restrict__ rec) {
   __shared__ PickLds<kRowsWaves * 64, R> sh;
-  topk_pick<kRowsWaves * 64, R>(logits, vocab, pk.m, pk.penal, pk.n_penal, pk.serial, kRowsPerWG, groups, rec, pk.out,
+  topk_pick<kRowsWaves * 64, R, kRowsTile>(logits, vocab, pk.m, pk.penal, pk.n_penal, pk.serial, kRowsPerWG, groups,
+                                           rec, pk.out,
                                 sh);
 }
 

@@ -57,7 +57,8 @@ uint32_t gemv_rows_group_size();
 hipError_t launch_gemv_rows(const WeightView &wv, const float *x, float *y, hipStream_t stream);
 // The same GEMV with the top-m of its logits (the decode head): every
 // workgroup of the GEMV also writes the top-k record of its
-// gemv_rows_group_size() rows to rec (gemv_rows_groups(wv) <=
+// gemv_rows_group_size() rows (G = gemv_rows_groups(wv) workgroups; group g is
+// the tiles of 32 rows starting at rows (q G + g) 32, q < 4) to rec (G <=
 // kRowsTopkGroupsMax records), and one more launch selects from them into out.
 constexpr uint32_t kRowsTopkGroupsMax = 1024;
 hipError_t launch_gemv_rows_topk(const WeightView &wv, const float *x, float *y, uint8_t *rec, uint32_t m,
