@@ -607,9 +607,12 @@ void sx_tiles(uint32_t tokens, uint32_t &tt, uint32_t &groups) {
 SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg) {
   SxPlan p;
   sx_tiles(tokens, p.tt, p.groups);
-  // measured: 32 rows x 8 waves up to 32 tokens per tile group, 64 rows x 4
-  // waves for 64 (the k halves in two workgroups were slower at every M)
-  p.cfg = cfg ? (uint32_t)(cfg - 1) : (p.tt == 4u ? 1u : 0u);
+  // measured (C5 shapes): 32 rows x 8 waves up to 32 tokens per tile group;
+  // 64 rows x 4 waves for 64 once the token groups give it 256 workgroups
+  // (M = 96, 128), else 32 x 8 again (M = 48, 64: 13.9 / 14.1 us against
+  // 19.2 / 19.4 for Q2_K); the k halves in two workgroups were slower at every M
+  const uint32_t rt64 = (wv.rows + 63u) / 64u;
+  p.cfg = cfg ? (uint32_t)(cfg - 1) : (p.tt == 4u && p.groups * rt64 >= 256u ? 1u : 0u);
   const uint32_t rows_per = p.cfg ? 64u : 32u, nw = p.cfg ? 4u : 8u, ks = p.cfg == 2u ? 2u : 1u;
   p.row_tiles = (wv.rows + rows_per - 1u) / rows_per;
   p.nbw = ((wv.bpr + ks - 1u) / ks + nw - 1u) / nw;
