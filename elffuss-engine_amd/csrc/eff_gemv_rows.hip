@@ -49,25 +49,86 @@ namespace {
 
 constexpr uint32_t kRowsWaves = 8;
 constexpr uint32_t kRowsTile = 32;                    // rows per wave tile
-constexpr uint32_t kRowsPerWG = 128;
+constexpr uint32_t kRowsPerWG = 128;                  // rows per workgroup on average (4 tiles)
+constexpr uint32_t kRowsTilesLong = 7;                // tiles of the grid's first half (KS = 8)
+constexpr uint32_t kRowsTilesShort = 2u * (kRowsPerWG / kRowsTile) - kRowsTilesLong;   // and of its second half
+constexpr uint32_t kRowsTilesMax = kRowsTilesLong > kRowsTilesShort ? kRowsTilesLong : kRowsTilesShort;
 constexpr uint32_t kRowsPitch = 240;                  // LDS bytes per tile row (15 chunks)
 constexpr uint32_t kRowsBuf = 8192;                   // LDS bytes per wave (8 loads of 1 KB)
-constexpr uint32_t kRowsRed = kRowsPerWG * 8u * 4u;   // LDS bytes of the slice sums (the rows x up to 8 slices)
+constexpr uint32_t kRowsRed = kRowsTilesMax * kRowsTile * 8u * 4u;   // LDS bytes of the slice sums (rows x up to 8 slices)
 constexpr uint32_t kRowsMin = 32768;
 constexpr uint32_t kRowsMaxK = 16384;
+static_assert(kRowsTilesLong + kRowsTilesShort == 2u * (kRowsPerWG / kRowsTile) && kRowsTilesShort >= 1u,
+              "every workgroup has tiles (and writes its record)");
+
+// The tiles of 32 rows of the G workgroups (G even, H = G / 2; A tiles for
+// workgroup b < H, B for the others, A + B = 8: 128 rows per workgroup on
+// average). In round q < m = min(A, B) every workgroup b takes tile q G + b,
+// so that the workgroups running at once read one region of the matrix
+// rather than G far apart; then the half with more tiles takes tile
+// m G + (q - m) H + b mod H in round q >= m. The dispatcher places the
+// workgroups in index order, so every CU holds one workgroup of each half,
+// and the first half's loads are served ahead: with 4 tiles each, its
+// workgroups ended after 13.4 us, the second half's after 19.1 (C4). A = 7, B = 1 measured fastest
+// (C4: 21.0 us against 21.5-21.7 for 4 + 4; 3 + 5 21.0-21.5, 5 + 3 21.4,
+// 6 + 2 22.0-22.5, 8 tiles on one workgroup per CU 21.9). It also maps the
+// head's top-k groups for topk_pick.
+struct RowsSched {
+  uint32_t G, H, A, B;   // A tiles for b < H, B for the others
+  __host__ __device__ uint32_t ntiles(uint32_t b) const { return b < H ? A : B; }
+  __host__ __device__ uint32_t tile(uint32_t b, uint32_t q) const {
+    const uint32_t m = A < B ? A : B;
+    return q < m ? q * G + b : m * G + (q - m) * H + (b < H ? b : b - H);
+  }
+  // The record of workgroup b is group rec_group(b) of the top-k: the two
+  // halves alternate, so that every wave of the selection holds as many
+  // groups of each size (its threshold is a bound over each wave's largest
+  // group maxima: with the short groups in waves of their own it falls to
+  // their maxima, and 3 to 4 times as many listed logits pass it).
+  __device__ uint32_t rec_group(uint32_t b) const { return b < H ? 2u * b : 2u * (b - H) + 1u; }
+  __device__ uint32_t wg_of(uint32_t g) const { return (g & 1u) ? H + (g >> 1) : g >> 1; }
+  // topk_pick's group map: element j of group g is row j % 32 of the tile
+  // j / 32 of workgroup wg_of(g)
+  __device__ uint32_t size() const { return (A > B ? A : B) * kRowsTile; }
+  __device__ uint32_t elem(uint32_t g, uint32_t j) const {
+    const uint32_t b = wg_of(g);
+    return j < ntiles(b) * kRowsTile ? tile(b, j / kRowsTile) * kRowsTile + j % kRowsTile : ~0u;
+  }
+  __device__ uint32_t count(uint32_t g, uint32_t vocab) const {
+    const uint32_t b = wg_of(g);
+    uint32_t n = 0;
+    for (uint32_t q = 0; q < ntiles(b); ++q) {
+      const uint32_t e0 = tile(b, q) * kRowsTile;
+      n += e0 < vocab ? min(kRowsTile, vocab - e0) : 0u;
+    }
+    return n;
+  }
+};
+
+// KS = 8 (one row group) splits the tiles unevenly (a wave takes all of its
+// workgroup's tiles); fewer k slices give every workgroup 4 tiles.
+template <uint32_t KS>
+__host__ __device__ RowsSched rows_sched(uint32_t G) {
+  const bool split = KS == 8u;
+  return RowsSched{G, G / 2u, split ? kRowsTilesLong : kRowsPerWG / kRowsTile,
+                   split ? kRowsTilesShort : kRowsPerWG / kRowsTile};
+}
 
 // The selection's arguments for the head's top-k.
 struct RowsPick {
   uint32_t *out;
   uint32_t m, n_penal, serial;
+  RowsSched sched;   // the GEMV's tiles
   TopkPenal penal;
 };
 
 // LDS: the x region first (digits, 3 k bytes, then the group data, k bytes),
 // so that its reads' offsets fit the 16-bit offset field of the LDS
 // instructions; then the slice sums (kRowsRed) and the workgroup's outputs
-// (512 B); then the 8 wave buffers.
-__host__ __device__ constexpr uint32_t rows_tiles_at(uint32_t k) { return 4u * k + kRowsRed + 4u * kRowsPerWG; }
+// (4 bytes per row); then the 8 wave buffers.
+__host__ __device__ constexpr uint32_t rows_tiles_at(uint32_t k) {
+  return 4u * k + kRowsRed + 4u * kRowsTilesMax * kRowsTile;
+}
 
 // One lane's half row-block (128 weights): the tile row's ql/qh words `a`, `q`
 // (aligned copies of LDS), its scale words and d, the block's byte shift, and
@@ -154,7 +215,9 @@ template <bool REC, uint32_t KS>
 __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gemv_rows_q6k(
     WeightView wv, const float *__restrict__ x, float *__restrict__ y, uint8_t *__restrict__ rec) {
   constexpr uint32_t RG = kRowsWaves / KS;                 // row groups
-  constexpr uint32_t T = kRowsPerWG / (RG * kRowsTile);    // tiles per wave
+  const RowsSched sc = rows_sched<KS>(gridDim.x);
+  const uint32_t nt = sc.ntiles(blockIdx.x);               // the workgroup's tiles
+  const uint32_t T = nt / RG;                              // tiles per wave
   extern __shared__ __align__(16) uint8_t lds[];
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -166,11 +229,8 @@ __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu
   const uint32_t rg = wave / KS, ks = wave % KS;
   const uint32_t ncol = bpr > ks ? (bpr - ks + KS - 1u) / KS : 0u;   // block columns of this slice
   const rsrc_t src = make_rsrc(wv.w, wv.w_bytes);
-  // first row of tile t of this wave
-  // first row of tile t of this wave: the workgroups' tiles interleave (tile
-  // q of workgroup b is the matrix's tile q G + b), so that the workgroups
-  // running at once read one region of the matrix rather than G far apart
-  auto tile_row = [&](uint32_t t) { return ((t * RG + rg) * gridDim.x + blockIdx.x) * kRowsTile; };
+  // first row of tile t of this wave (the workgroup's tile t RG + rg)
+  auto tile_row = [&](uint32_t t) { return sc.tile(blockIdx.x, t * RG + rg) * kRowsTile; };
 
   // Load i of the lane fills LDS chunk s = 64 i + lane = row s / 15, chunk
   // s % 15 of that row; chunk 14 repeats 13 (a cache hit) so that rows are
@@ -249,8 +309,8 @@ __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu
   }
   // a row's KS slice sums in order
   __syncthreads();
-  if (tid < kRowsPerWG) {
-    const uint32_t qt = tid / kRowsTile, r = tid % kRowsTile, row = (qt * gridDim.x + blockIdx.x) * kRowsTile + r;
+  if (tid < nt * kRowsTile) {
+    const uint32_t qt = tid / kRowsTile, r = tid % kRowsTile, row = sc.tile(blockIdx.x, qt) * kRowsTile + r;
     float v = red[qt * KS * kRowsTile + r];
 #pragma unroll
     for (uint32_t s2 = 1; s2 < KS; ++s2) v += red[(qt * KS + s2) * kRowsTile + r];
@@ -260,19 +320,20 @@ __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu
   if constexpr (REC) {
     __syncthreads();
     if (wave == 0u) {
-      // outputs l and l + 64 of the workgroup's 128 (tile i / 32, row i % 32)
+      // outputs l, l + 64, .. of the workgroup's 32 nt (tile i / 32, row i % 32)
       Top4 t;
       bool nan = false;
 #pragma unroll
-      for (uint32_t h = 0; h < kRowsPerWG / 64u; ++h) {
-        const uint32_t i = lane + 64u * h, e = ((i / kRowsTile) * gridDim.x + blockIdx.x) * kRowsTile + i % kRowsTile;
+      for (uint32_t h = 0; h < (kRowsTilesMax * kRowsTile + 63u) / 64u; ++h) {
+        const uint32_t i = lane + 64u * h;
+        const uint32_t e = i < nt * kRowsTile ? sc.tile(blockIdx.x, i / kRowsTile) * kRowsTile + i % kRowsTile : ~0u;
         if (e < rows) {
           const uint32_t bits = fin[i];
           nan |= is_nan_bits(bits);
           t.add(composite(bits, e), bits);
         }
       }
-      topk_record_wave(t, nan, rec, blockIdx.x, gridDim.x);
+      topk_record_wave(t, nan, rec, sc.rec_group(blockIdx.x), gridDim.x);
     }
   }
 }
@@ -284,8 +345,7 @@ __global__ __launch_bounds__(kRowsWaves * 64) void k_rows_pick(const uint32_t *_
                                                                RowsPick pk, uint32_t groups,
                                                                const uint8_t *__restrict__ rec) {
   __shared__ PickLds<kRowsWaves * 64, R> sh;
-  topk_pick<kRowsWaves * 64, R, kRowsTile>(logits, vocab, pk.m, pk.penal, pk.n_penal, pk.serial, kRowsPerWG, groups,
-                                           rec, pk.out,
+  topk_pick<kRowsWaves * 64, R>(logits, vocab, pk.m, pk.penal, pk.n_penal, pk.serial, pk.sched, groups, rec, pk.out,
                                 sh);
 }
 
@@ -318,8 +378,8 @@ bool gemv_rows_applies(const WeightView &wv, uint32_t tokens) {
          (uint64_t)wv.rows * wv.row_bytes + 16u < (1ull << 32);   // 32-bit byte offsets
 }
 
-uint32_t gemv_rows_groups(const WeightView &wv) { return (wv.rows + kRowsPerWG - 1u) / kRowsPerWG; }
-uint32_t gemv_rows_group_size() { return kRowsPerWG; }
+// an even count, for the two halves of the grid
+uint32_t gemv_rows_groups(const WeightView &wv) { return ((wv.rows + 2u * kRowsPerWG - 1u) / (2u * kRowsPerWG)) * 2u; }
 
 hipError_t launch_gemv_rows(const WeightView &wv, const float *x, float *y, hipStream_t s) {
   if (!gemv_rows_applies(wv, 1u)) return hipErrorInvalidValue;
@@ -339,6 +399,8 @@ hipError_t launch_gemv_rows_topk(const WeightView &wv, const float *x, float *y,
   pk.m = m;
   pk.n_penal = n_penal;
   pk.serial = serial;
+  const uint32_t G = gemv_rows_groups(wv);
+  pk.sched = wv.bpr >= 8u ? rows_sched<8>(G) : wv.bpr >= 4u ? rows_sched<4>(G) : rows_sched<2>(G);
   for (uint32_t i = 0; i < n_penal; ++i) pk.penal.ids[i] = penal_ids[i];
   hipError_t e = launch_rows<true>(wv, x, y, rec, rows_tiles_at(wv.k) + kRowsWaves * kRowsBuf, s);
   if (e != hipSuccess) return e;

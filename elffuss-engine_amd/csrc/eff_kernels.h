@@ -53,13 +53,12 @@ hipError_t launch_gemv_mx_multi(int mode, uint32_t n, const WeightView *wvs, con
 // a lane per half row-block, x digits as LDS broadcasts (eff_gemv_rows.hip).
 bool gemv_rows_applies(const WeightView &wv, uint32_t tokens);
 uint32_t gemv_rows_groups(const WeightView &wv);
-uint32_t gemv_rows_group_size();
 hipError_t launch_gemv_rows(const WeightView &wv, const float *x, float *y, hipStream_t stream);
 // The same GEMV with the top-m of its logits (the decode head): every
-// workgroup of the GEMV also writes the top-k record of its
-// gemv_rows_group_size() rows (G = gemv_rows_groups(wv) workgroups; group g is
-// the tiles of 32 rows starting at rows (q G + g) 32, q < 4) to rec (G <=
-// kRowsTopkGroupsMax records), and one more launch selects from them into out.
+// workgroup of the GEMV also writes the top-k record of its rows (G =
+// gemv_rows_groups(wv) workgroups, each over 2 to 5 tiles of 32 rows spread
+// over the matrix) to rec (G <= kRowsTopkGroupsMax records), and one more
+// launch selects from them into out.
 constexpr uint32_t kRowsTopkGroupsMax = 1024;
 hipError_t launch_gemv_rows_topk(const WeightView &wv, const float *x, float *y, uint8_t *rec, uint32_t m,
                                  const uint32_t *penal_ids, uint32_t n_penal, uint32_t serial, uint32_t *out,

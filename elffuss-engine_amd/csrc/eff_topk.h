@@ -242,12 +242,22 @@ __device__ uint64_t select_top(uint32_t need, Visit visit, L &sh) {
   return lo;  // not reached: each round narrows the candidates in play
 }
 
-// The top-m selection over `groups` records of groups of gs logits (record g
-// at rec + 64 g), by the NT threads of one workgroup, thread t holding the
-// records of groups t + NT r (r < R); writes the output record of
-// kernels.topk.wgsl.js:40-60. TILE = 0: group g is logits g gs .. g gs + gs - 1;
-// TILE > 0: it is gs / TILE tiles of TILE logits, tile t starting at
-// (t groups + g) TILE (the head GEMV's interleaved tiles).
+// Groups of gs consecutive logits: group g is logits g gs .. g gs + gs - 1.
+struct FlatGroups {
+  uint32_t gs;
+  __device__ uint32_t size() const { return gs; }   // elements of the largest group
+  __device__ uint32_t elem(uint32_t g, uint32_t j) const { return g * gs + j; }
+  __device__ uint32_t count(uint32_t g, uint32_t vocab) const {   // its elements below vocab
+    return g * gs < vocab ? min(gs, vocab - g * gs) : 0u;
+  }
+};
+
+// The top-m selection over `groups` records (record g at rec + 64 g), by the
+// NT threads of one workgroup, thread t holding the records of groups
+// t + NT r (r < R); writes the output record of kernels.topk.wgsl.js:40-60.
+// `map` gives the logits of group g: map.elem(g, j) for j < map.size(), those
+// below vocab counted by map.count(g, vocab) (FlatGroups, or the head GEMV's
+// tiles).
 //
 // tau: a lower bound of the need-th largest group maximum. Every one of the
 // overall need largest elements is >= the need-th largest maximum, so the
@@ -264,9 +274,9 @@ __device__ uint64_t select_top(uint32_t need, Visit visit, L &sh) {
 // bound; need <= 64 here): kw rounds of a wave maximum, no selection. When that leaves more listed composites
 // than the candidate space, or need > 64, tau is the need-th largest maximum
 // exactly, by select_top (then at most 4 need composites are listed >= it).
-template <int NT, int R, uint32_t TILE = 0>
+template <int NT, int R, class Map>
 __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, uint32_t m, const TopkPenal &penal,
-                          uint32_t n_penal, uint32_t serial, uint32_t gs, uint32_t groups,
+                          uint32_t n_penal, uint32_t serial, const Map &map, uint32_t groups,
                           const uint8_t *__restrict__ rec, uint32_t *__restrict__ out, PickLds<NT, R> &sh) {
   constexpr int NW = NT / 64, KW = 64 / NW;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -310,17 +320,7 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
   // group g of the thread's record r holds more than 4 elements
   auto over4 = [&](int r) {
     const uint32_t g = (uint32_t)tid + NT * r;
-    if (g >= groups) return false;
-    if constexpr (TILE == 0) {
-      return min(gs, vocab - g * gs) > 4u;
-    } else {
-      uint32_t n = 0;
-      for (uint32_t t = 0; t < gs / TILE; ++t) {
-        const uint32_t e0 = (t * groups + g) * TILE;
-        n += e0 < vocab ? min(TILE, vocab - e0) : 0u;
-      }
-      return n > 4u;
-    }
+    return g < groups && map.count(g, vocab) > 4u;
   };
   // the listed composites >= th into the candidate space in thread order (a
   // wave prefix sum of the lanes' counts, the waves' totals through LDS);
@@ -465,10 +465,11 @@ __device__ void topk_pick(const uint32_t *__restrict__ logits, uint32_t vocab, u
     }
     __syncthreads();
     const uint32_t ns = sh.nsat;
+    const uint32_t gs = map.size();
     auto stream = [&](auto f) {
       for (uint32_t i = (uint32_t)tid; i < ns * gs; i += NT) {
         const uint32_t g = sh.satg[i / gs], j = i % gs;
-        const uint32_t e = TILE ? ((j / (TILE ? TILE : 1u)) * groups + g) * TILE + j % (TILE ? TILE : 1u) : g * gs + j;
+        const uint32_t e = map.elem(g, j);   // past vocab for j past the group's elements
         if (e < vocab) {
           const uint32_t bits = logits[e];
           f(composite(bits, e), bits);

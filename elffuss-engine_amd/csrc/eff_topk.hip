@@ -63,7 +63,7 @@ __global__ __launch_bounds__(kPickThreads) void k_topk_pick(const uint32_t *__re
                                                             const uint8_t *__restrict__ rec,
                                                             uint32_t *__restrict__ out) {
   __shared__ PickLds<kPickThreads, 1> sh;
-  topk_pick<kPickThreads, 1>(logits, vocab, m, penal, n_penal, serial, gs, groups, rec, out, sh);
+  topk_pick<kPickThreads, 1>(logits, vocab, m, penal, n_penal, serial, FlatGroups{gs}, groups, rec, out, sh);
 }
 
 // The selecting half alone, over `groups` (<= 256) records of groups of `gs`

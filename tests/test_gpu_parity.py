@@ -714,14 +714,15 @@ def test_topk_clustered_in_one_group(ctx, eff, orc, vocab, m):
 
 
 @pytest.mark.parametrize("tname,rows,k,m,cluster", [
-    ("Q6_K", 65536, 2048, 40, False),      # the C4 head: records from the GEMV, 512 groups
-    ("Q6_K", 40001, 2048, 192, True),      # ragged rows; the largest logits in one 128-row group
-    ("Q6_K", 65664, 512, 100, True),       # 513 groups
-    ("Q6_K", 65536, 512, 40, True),        # the wave-maximum threshold, then a saturated group read whole
-    ("Q6_K", 40000, 2304, 40, False),      # an odd block count per row (per-row load offsets)
-    ("Q6_K", 131072, 512, 64, False),      # 1024 groups, the most one selection holds (two per thread)
-    ("Q6_K", 131073, 512, 40, False),      # more groups than one selection holds: GEMV, then eff_topk
-    ("Q8_0", 50000, 512, 40, False),       # no row kernel: GEMV, then eff_topk
+    ("Q6_K", 65536, 2048, 40, 0),          # the C4 head: records from the GEMV, 512 groups of 7 or 1 tiles
+    ("Q6_K", 40001, 2048, 192, 5000),      # ragged rows; the largest logits in 5 tiles of 32 rows
+    ("Q6_K", 65536, 2048, 40, 60000),      # ... in tiles the first half of the grid takes last (its 7th)
+    ("Q6_K", 65664, 512, 100, 5000),       # 513 groups of 4 tiles (an even grid: 514)
+    ("Q6_K", 65536, 512, 40, 5000),        # the wave-maximum threshold, then saturated groups read whole
+    ("Q6_K", 40000, 2304, 40, 0),          # an odd block count per row (per-row load offsets)
+    ("Q6_K", 131072, 512, 64, 0),          # 1024 groups, the most one selection holds (two per thread)
+    ("Q6_K", 131073, 512, 40, 0),          # more groups than one selection holds: GEMV, then eff_topk
+    ("Q8_0", 50000, 512, 40, 0),           # no row kernel: GEMV, then eff_topk
 ])
 def test_qgemv_topk_equals_gemv_then_topk(ctx, eff, orc, tname, rows, k, m, cluster):
     """eff_qgemv_topk gives the logits and the top-k record of eff_qmatmul
@@ -730,7 +731,7 @@ def test_qgemv_topk_equals_gemv_then_topk(ctx, eff, orc, tname, rows, k, m, clus
     base = "Q8_0" if tname == "Q8_0R" else tname
     wf = eff.fill_normal(rows % 1000 + 1011, 0.02, rows * k).reshape(rows, k)
     if cluster:
-        wf[5000:5128] *= 40.0                              # one group's rows dominate
+        wf[cluster:cluster + 128] *= 40.0                  # these rows dominate
     w = eff.quantize(base, wf)
     x = eff.fill_normal(12, 1.0, k)
     t = eff.TYPES[tname]
@@ -748,7 +749,7 @@ def test_qgemv_topk_equals_gemv_then_topk(ctx, eff, orc, tname, rows, k, m, clus
     assert r["n"] == m and r["flags"] == 0 and r["serial"] == 5
     assert np.array_equal(r["ids"], ids) and np.array_equal(r["bits"], bits)
     if cluster:   # the boosted rows hold the largest logits
-        assert np.all((r["ids"][:32] >= 5000) & (r["ids"][:32] < 5128))
+        assert np.all((r["ids"][:32] >= cluster) & (r["ids"][:32] < cluster + 128))
     # a call the top-k does not apply to enqueues nothing
     y1.write(np.zeros(rows, np.uint32))
     with pytest.raises(eff.NotApplicable):
