@@ -50,16 +50,19 @@ namespace {
 constexpr uint32_t kRowsWaves = 8;
 constexpr uint32_t kRowsTile = 32;                    // rows per wave tile
 constexpr uint32_t kRowsPerWG = 128;                  // rows per workgroup on average (4 tiles)
-constexpr uint32_t kRowsTilesLong = 7;                // tiles of the grid's first half (KS = 8)
-constexpr uint32_t kRowsTilesShort = 2u * (kRowsPerWG / kRowsTile) - kRowsTilesLong;   // and of its second half
-constexpr uint32_t kRowsTilesMax = kRowsTilesLong > kRowsTilesShort ? kRowsTilesLong : kRowsTilesShort;
+constexpr uint32_t kRowsTilesPair = 2u * (kRowsPerWG / kRowsTile);   // tiles of a CU's two workgroups
+constexpr uint32_t kRowsTilesFirst[2] = {7, 3};       // tiles of the grid's first half (KS = 8), without / with REC
+constexpr uint32_t kRowsTilesMax = 7;                 // of any workgroup
 constexpr uint32_t kRowsPitch = 240;                  // LDS bytes per tile row (15 chunks)
 constexpr uint32_t kRowsBuf = 8192;                   // LDS bytes per wave (8 loads of 1 KB)
 constexpr uint32_t kRowsRed = kRowsTilesMax * kRowsTile * 8u * 4u;   // LDS bytes of the slice sums (rows x up to 8 slices)
 constexpr uint32_t kRowsMin = 32768;
 constexpr uint32_t kRowsMaxK = 16384;
-static_assert(kRowsTilesLong + kRowsTilesShort == 2u * (kRowsPerWG / kRowsTile) && kRowsTilesShort >= 1u,
-              "every workgroup has tiles (and writes its record)");
+static_assert(kRowsTilesFirst[0] < kRowsTilesPair && kRowsTilesFirst[1] < kRowsTilesPair &&
+                  kRowsTilesFirst[0] <= kRowsTilesMax && kRowsTilesFirst[1] <= kRowsTilesMax &&
+                  kRowsTilesPair - kRowsTilesFirst[0] <= kRowsTilesMax &&
+                  kRowsTilesPair - kRowsTilesFirst[1] <= kRowsTilesMax,
+              "every workgroup has tiles (and writes its record), at most kRowsTilesMax");
 
 // The tiles of 32 rows of the G workgroups (G even, H = G / 2; A tiles for
 // workgroup b < H, B for the others, A + B = 8: 128 rows per workgroup on
@@ -69,10 +72,10 @@ static_assert(kRowsTilesLong + kRowsTilesShort == 2u * (kRowsPerWG / kRowsTile) 
 // m G + (q - m) H + b mod H in round q >= m. The dispatcher places the
 // workgroups in index order, so every CU holds one workgroup of each half,
 // and the first half's loads are served ahead: with 4 tiles each, its
-// workgroups ended after 13.4 us, the second half's after 19.1 (C4). A = 7, B = 1 measured fastest
-// (C4: 21.0 us against 21.5-21.7 for 4 + 4; 3 + 5 21.0-21.5, 5 + 3 21.4,
-// 6 + 2 22.0-22.5, 8 tiles on one workgroup per CU 21.9). It also maps the
-// head's top-k groups for topk_pick.
+// workgroups ended after 13.4 us, the second half's after 19.1 (C4). For the
+// GEMV A = 7, B = 1 measured fastest (C4: 20.9-21.0 us against 21.5-21.7 for
+// 4 + 4; 3 + 5 21.0-21.5, 5 + 3 21.4-21.9, 6 + 2 22.0-22.5, 8 tiles on one
+// workgroup per CU 21.9). It also maps the head's top-k groups for topk_pick.
 struct RowsSched {
   uint32_t G, H, A, B;   // A tiles for b < H, B for the others
   __host__ __device__ uint32_t ntiles(uint32_t b) const { return b < H ? A : B; }
@@ -106,12 +109,14 @@ struct RowsSched {
 };
 
 // KS = 8 (one row group) splits the tiles unevenly (a wave takes all of its
-// workgroup's tiles); fewer k slices give every workgroup 4 tiles.
-template <uint32_t KS>
+// workgroup's tiles), 7 + 1 for the GEMV and 3 + 5 with the records (C4 with
+// the selection: 26.68 us per step against 26.83 for 7 + 1 and 27.15 for
+// 4 + 4); fewer k slices give every workgroup 4 tiles.
+template <uint32_t KS, bool REC>
 __host__ __device__ RowsSched rows_sched(uint32_t G) {
   const bool split = KS == 8u;
-  return RowsSched{G, G / 2u, split ? kRowsTilesLong : kRowsPerWG / kRowsTile,
-                   split ? kRowsTilesShort : kRowsPerWG / kRowsTile};
+  const uint32_t a = kRowsTilesFirst[REC ? 1 : 0];
+  return RowsSched{G, G / 2u, split ? a : kRowsTilesPair / 2u, split ? kRowsTilesPair - a : kRowsTilesPair / 2u};
 }
 
 // The selection's arguments for the head's top-k.
@@ -215,7 +220,7 @@ template <bool REC, uint32_t KS>
 __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gemv_rows_q6k(
     WeightView wv, const float *__restrict__ x, float *__restrict__ y, uint8_t *__restrict__ rec) {
   constexpr uint32_t RG = kRowsWaves / KS;                 // row groups
-  const RowsSched sc = rows_sched<KS>(gridDim.x);
+  const RowsSched sc = rows_sched<KS, REC>(gridDim.x);
   const uint32_t nt = sc.ntiles(blockIdx.x);               // the workgroup's tiles
   const uint32_t T = nt / RG;                              // tiles per wave
   extern __shared__ __align__(16) uint8_t lds[];
@@ -400,7 +405,7 @@ hipError_t launch_gemv_rows_topk(const WeightView &wv, const float *x, float *y,
   pk.n_penal = n_penal;
   pk.serial = serial;
   const uint32_t G = gemv_rows_groups(wv);
-  pk.sched = wv.bpr >= 8u ? rows_sched<8>(G) : wv.bpr >= 4u ? rows_sched<4>(G) : rows_sched<2>(G);
+  pk.sched = wv.bpr >= 8u ? rows_sched<8, true>(G) : wv.bpr >= 4u ? rows_sched<4, true>(G) : rows_sched<2, true>(G);
   for (uint32_t i = 0; i < n_penal; ++i) pk.penal.ids[i] = penal_ids[i];
   hipError_t e = launch_rows<true>(wv, x, y, rec, rows_tiles_at(wv.k) + kRowsWaves * kRowsBuf, s);
   if (e != hipSuccess) return e;

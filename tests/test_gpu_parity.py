@@ -714,9 +714,9 @@ def test_topk_clustered_in_one_group(ctx, eff, orc, vocab, m):
 
 
 @pytest.mark.parametrize("tname,rows,k,m,cluster", [
-    ("Q6_K", 65536, 2048, 40, 0),          # the C4 head: records from the GEMV, 512 groups of 7 or 1 tiles
+    ("Q6_K", 65536, 2048, 40, 0),          # the C4 head: records from the GEMV, 512 groups of 3 or 5 tiles
     ("Q6_K", 40001, 2048, 192, 5000),      # ragged rows; the largest logits in 5 tiles of 32 rows
-    ("Q6_K", 65536, 2048, 40, 60000),      # ... in tiles the first half of the grid takes last (its 7th)
+    ("Q6_K", 65536, 2048, 40, 60000),      # ... in tiles the second half of the grid takes last (its 5th)
     ("Q6_K", 65664, 512, 100, 5000),       # 513 groups of 4 tiles (an even grid: 514)
     ("Q6_K", 65536, 512, 40, 5000),        # the wave-maximum threshold, then saturated groups read whole
     ("Q6_K", 40000, 2304, 40, 0),          # an odd block count per row (per-row load offsets)
