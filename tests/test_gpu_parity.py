@@ -154,12 +154,14 @@ def test_gemv_non_finite_x(ctx, eff, gemv_kernel, tname):
 # ---- the row GEMV for Q6_K matrices with many rows (the output projection) -------------
 
 @pytest.mark.parametrize("rows,k", [(32768, 512), (32805, 4608), (40001, 2048), (32769, 8192), (32800, 2304),
-                                      (33000, 768)])
+                                      (33000, 768), (140001, 2048)])
 def test_gemv_rows_q6_k_vs_f64_oracle(ctx, eff, orc, rows, k):
     """One token of a Q6_K matrix of >= 32768 rows runs the row kernel (a lane
-    per half row-block): row counts that are not a multiple of the 128-row
-    workgroup, an odd number of blocks per row (block starts at both 2-byte
-    alignments in every column), and k up to 32 blocks."""
+    per half row-block): row counts that are not a multiple of the workgroups'
+    rows (128 on average, 224 and 32 in the two halves of the grid from 8
+    blocks per row), an odd number of blocks per row (block starts at both
+    2-byte alignments in every column), k up to 32 blocks, and more workgroups
+    (1096) than the GPU holds at once."""
     t, data, gguf, n = make_weights(eff, "Q6_K", rows, k, rows + k)
     x = eff.fill_normal(rows + 1, 1.0, k)
     wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(rows * 4)
