@@ -22,16 +22,17 @@
 // against digits read as LDS broadcasts (all lanes of a half read the same
 // address).
 //
-// Workgroup: 128 rows, 8 waves = RG row groups x KS k slices (KS = 8 when the
-// matrix has at least 8 block columns). Slice s takes the block columns
+// Workgroup: 128 rows on average (tiles of 32 rows, RowsSched below), 8 waves
+// = RG row groups x KS k slices (KS = 8 when the matrix has at least 8 block
+// columns). Slice s takes the block columns
 // s, s + KS, s + 2 KS, ... of each of its tiles, so the KS waves of a row group
 // load neighbouring blocks of the same 32 rows at about the same time: the
 // 128-byte lines two neighbouring blocks share are fetched from memory once
 // and found in L2 by the second wave. (When one wave walks consecutive block
 // columns of its rows, the shared lines have left L2 before its next load and
 // the kernel reads 1.3 x the matrix.) A row's KS slice sums are added in a
-// fixed order. With REC the workgroup also writes the top-k record of its 128
-// rows (their 4 largest logits, eff_topk.h), so that the top-k over the logits
+// fixed order. With REC the workgroup also writes the top-k record of its rows
+// (their 4 largest logits, eff_topk.h), so that the top-k over the logits
 // only has to select from the records.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -213,8 +214,7 @@ __device__ __forceinline__ void rows_read(const uint8_t *tp, uint32_t n, uint32_
 }
 
 // REC: the decode head. Each workgroup also writes the top-k record of its
-// 128 rows, its 4 interleaved tiles of 32 (their 4 largest logits,
-// eff_topk.h), for k_rows_pick.
+// tiles (their 4 largest logits, eff_topk.h), for k_rows_pick.
 template <bool REC, uint32_t KS>
 // amdgpu_waves_per_eu(4): at most 128 VGPRs, so that two workgroups share a CU.
 __global__ __launch_bounds__(kRowsWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gemv_rows_q6k(

@@ -309,7 +309,8 @@ int eff_topk(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint3
  * 4; the reference runs the two as separate passes (model.js:1145-1177, then
  * createTopKGPU().candidatos, ops.topk.js:99-165). For Q6_K matrices of
  * 32768 .. 131072 rows every workgroup of the GEMV also writes the top-k
- * record of its 128 rows, and one more launch selects from the records; other
+ * record of its rows (128 on average), and one more launch selects from the
+ * records; other
  * shapes run the GEMV and eff_topk. The same NOT_APPLICABLE cases as
  * eff_topk, checked before anything is enqueued. */
 int eff_qgemv_topk(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k,
