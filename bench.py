@@ -140,8 +140,10 @@ def time_steps(torch, ctx, cfg, steps, warmup, warm_replays=1, timed=1):
     """Average ms per step over `steps` graph-replayed steps (after `warmup`
     eager steps and `warm_replays` untimed replays); with `timed` > 1 the
     median of that many timed replays. Each replay of the timed graph is
-    preceded by an untimed graph of the steps that complete the rotation
-    cycle, so that every weight copy is reused only after all of them."""
+    preceded, without a wait, by an untimed graph of the steps that complete
+    the rotation cycle (or by the graph itself when its steps are a whole
+    number of cycles), so that every weight copy is reused only after all of
+    them."""
     rot = rotation(cfg, steps)
     assert rot["reuse_distance_bytes"] >= 2 * MALL_BYTES, rot
     stream = torch.cuda.current_stream()
@@ -169,8 +171,14 @@ def time_steps(torch, ctx, cfg, steps, warmup, warm_replays=1, timed=1):
     torch.cuda.synchronize()
     times = []
     for _ in range(timed):
+        # an untimed replay ahead of the timed one (the rest of the rotation
+        # cycle, else the whole graph) keeps the GPU busy while the host
+        # submits the timed replay, so that the timed region holds the steps
+        # back to back and no wait for the submission
         if gpad is not None:
             gpad.replay()
+        else:
+            g.replay()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
         g.replay()
