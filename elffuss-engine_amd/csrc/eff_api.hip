@@ -58,6 +58,7 @@ struct eff_ctx {
   void *sx_scratch = nullptr;       // x as fp16 hi/lo parts for the split-x product
   size_t sx_scratch_bytes = 0;
   int64_t sx_config = 0;
+  int64_t gemm_config = 0;
   int64_t sx_min_tokens = 0;        // 0: the measured default (sx_routes)
   // Pinned staging ring of eff_buf_write: the source bytes are copied here on
   // the calling thread and the device copy is enqueued from here, so a write
@@ -227,10 +228,11 @@ int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_
 }
 
 int run_gemm(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens, uint32_t plan) {
-  int rc = grow(ctx, &ctx->xh_scratch, &ctx->xh_scratch_bytes, gemm_x_bytes(wv.type, tokens, plan, wv.k, wv.rows),
-                "gemm x");
+  const uint32_t cfg = (uint32_t)ctx->gemm_config;
+  int rc = grow(ctx, &ctx->xh_scratch, &ctx->xh_scratch_bytes,
+                gemm_x_bytes(wv.type, tokens, plan, wv.k, wv.rows, cfg), "gemm x");
   if (rc) return rc;
-  hipError_t e = launch_gemm(wv, x, y, tokens, plan, ctx->xh_scratch, ctx->stream);
+  hipError_t e = launch_gemm(wv, x, y, tokens, plan, cfg, ctx->xh_scratch, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
   return EFF_OK;
 }
@@ -379,6 +381,10 @@ int eff_set_option(eff_ctx *ctx, int option, int64_t value) {
       if (value != 0 && value < 4)
         return fail(ctx, EFF_E_INVALID, "split-x min tokens must be 0 or >= 4, got %lld", (long long)value);
       ctx->sx_min_tokens = value;
+      return EFF_OK;
+    case EFF_OPT_GEMM_CONFIG:
+      if (value < 0 || value > 6) return fail(ctx, EFF_E_INVALID, "GEMM configuration must be 0..6, got %lld", (long long)value);
+      ctx->gemm_config = value;
       return EFF_OK;
     default: return fail(ctx, EFF_E_INVALID, "unknown option %d", option);
   }

@@ -3,17 +3,19 @@
 // (the operand roundings of kernels.drift.wgsl.js:65-142 and the f16 tiles of
 // ops.gemm2.js).
 //
-// A workgroup of 4 waves computes a BM-token x BN-row tile (256 x 256 from
-// 1024 tokens, 128 x 128 below, so that 512 tokens still give 256
-// workgroups); wave w owns every token of the tile and rows BN/4 w.., i.e.
-// BM/32 x BN/128 fragments of v_mfma_f32_32x32x16_f16 (256 accumulators for
-// the large tile). Each A fragment is read once per k slot and used by the
-// wave's BN/128 MFMAs of that slot, and each B fragment by its BM/32.
+// A workgroup of 4 waves (one per SIMD) computes a BM-token x BN-row tile
+// (64 x 128 to 256 x 256, chosen by the token count: gemm_q8_choice); the
+// waves are WM along tokens x 4 / WM along rows, each over (BM / WM / 32) x
+// (BN / (4 / WM) / 32) fragments of v_mfma_f32_32x32x16_f16 (256
+// accumulators for 256 x 256). Each A fragment is read once per k slot and
+// used by the wave's row fragments of that slot, each B fragment by its
+// token fragments.
 //
-// k steps of 64 (two Q8_0 blocks) flow through three LDS stages filled by
-// direct-to-LDS loads (buffer_load ... lds), issued two steps ahead:
+// k steps of 64 (two Q8_0 blocks) flow through NS LDS stages (3 to 6)
+// filled by direct-to-LDS loads (buffer_load ... lds), issued NS - 1 steps
+// ahead:
 //  * x: the fp16 x of the step (prepared by k_x_to_f16 as one contiguous run
-//    of 256 x 64 halves), 16-byte chunk c of token t stored at chunk
+//    of BM x 64 halves), 16-byte chunk c of token t stored at chunk
 //    c ^ ((t >> 1) & 7) of the token's 128-byte row, so that the 16 lanes
 //    one LDS cycle serves (16 x 16 bytes over the 64 banks) read 16
 //    different bank quads when a fragment reads one chunk column;
@@ -42,18 +44,18 @@ namespace {
 
 constexpr uint32_t kBK = 64;              // k per step
 constexpr uint32_t kRB = 80;              // raw weight bytes per row and stage
-// waves along tokens x along rows (one wave per SIMD)
-constexpr uint32_t kWM = 1, kWN = 4, kNW = kWM * kWN;
+constexpr uint32_t kNW = 4;               // waves per workgroup (one per SIMD)
 
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const uint32_t *)p; }
 
-// BM tokens x BN rows per tile; KS workgroups split k (KS = 2: the two
-// halves are added into y, zeroed beforehand, with atomic adds, which give the
-// same bits in either order: 0 + a + b = a + b).
-template <uint32_t BM, uint32_t BN, uint32_t KS>
+// BM tokens x BN rows per tile. The 4 waves are WM along tokens x 4 / WM
+// along rows; NS stages (3..6), loads issued NS - 1 steps ahead.
+template <uint32_t BM, uint32_t BN, uint32_t WM, uint32_t NS>
 __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Float16 *__restrict__ xh,
                                                  float *__restrict__ y, uint32_t tokens, uint32_t row_tiles,
                                                  uint32_t tok_tiles) {
+  constexpr uint32_t kWM = WM, kWN = kNW / WM;
+  static_assert(kNW % WM == 0 && NS >= 3 && NS <= 6, "layout");
   constexpr uint32_t kWS = BN * kRB;                  // weight stage bytes
   constexpr uint32_t kWG = kWS / 1024;                // weight loads per step (64 lanes x 16 bytes each)
   constexpr uint32_t kFN = BN / 32 / kWN;             // 32 x 32 fragments along rows per wave
@@ -63,12 +65,26 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
   constexpr uint32_t kXDma = kXS / 1024 / kNW;  // x loads per wave and step
   static_assert(kXS % (1024 * kNW) == 0, "x loads");
   constexpr uint32_t kFM = BM / 32 / kWM;
-  static_assert(KS >= 1 && KS <= 2, "tile");
-  // three stages, each x (kXS bytes) then W (kWS bytes); separate objects,
+  // NS stages, each x (kXS bytes) then W (kWS bytes); separate objects,
   // so that the compiler can tell loads into one stage from reads of another
-  __shared__ __align__(16) uint8_t st0[kXS + kWS];
-  __shared__ __align__(16) uint8_t st1[kXS + kWS];
-  __shared__ __align__(16) uint8_t st2[kXS + kWS];
+  // (every stage index below is a compile-time constant)
+  constexpr uint32_t kSt = kXS + kWS;
+  __shared__ __align__(16) uint8_t st0[kSt];
+  __shared__ __align__(16) uint8_t st1[kSt];
+  __shared__ __align__(16) uint8_t st2[kSt];
+  __shared__ __align__(16) uint8_t st3[NS > 3 ? kSt : 16];
+  __shared__ __align__(16) uint8_t st4[NS > 4 ? kSt : 16];
+  __shared__ __align__(16) uint8_t st5[NS > 5 ? kSt : 16];
+  auto stage = [&](uint32_t i) -> const uint8_t * {
+    switch (i) {
+      case 0: return st0;
+      case 1: return st1;
+      case 2: return st2;
+      case 3: return st3;
+      case 4: return st4;
+      default: return st5;
+    }
+  };
 
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -77,17 +93,13 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
   // Tiles are dealt so that the workgroups of one XCD (blockIdx % 8) take a
   // contiguous run of tiles, token tiles fastest: they share x and W slices
   // through that XCD's L2.
-  // (k halves slowest: the XCDs of one half share its x and W slices)
-  const uint32_t ntiles = row_tiles * tok_tiles * KS;
+  const uint32_t ntiles = row_tiles * tok_tiles;
   uint32_t lin = blockIdx.x;
   if (ntiles % 8u == 0u) lin = (blockIdx.x % 8u) * (ntiles / 8u) + blockIdx.x / 8u;
-  const uint32_t kq = lin / (row_tiles * tok_tiles);
-  lin %= row_tiles * tok_tiles;
   const uint32_t n0 = (lin / tok_tiles) * BN, tt = lin % tok_tiles, t0 = tt * BM;
   const uint32_t rows = wv.rows, k = wv.k;
   const uint32_t steps_all = (k + kBK - 1u) / kBK;
-  // this workgroup's steps: s0 .. s0 + steps - 1 (absolute step numbers)
-  const uint32_t s0 = kq * steps_all / KS, steps = (kq + 1u) * steps_all / KS - s0, last = steps - 1u;
+  const uint32_t steps = steps_all, last = steps - 1u;
 
   // Sources: x run of this token tile, weight rows from the tile's first row.
   const rsrc_t xsrc = make_rsrc(xh + (uint64_t)tt * steps_all * (BM * kBK), (uint64_t)steps_all * kXS);
@@ -119,20 +131,20 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
       if ((int)(i % 4u) != g) continue;
       if (i < kXDma) {
         const uint32_t slot = kXDma * wave + i;
-        dma16(xsrc, xs + 1024u * slot, ((i & 1u) ? xl1 : xl0) + 1024u * slot, (s0 + s) * kXS);
+        dma16(xsrc, xs + 1024u * slot, ((i & 1u) ? xl1 : xl0) + 1024u * slot, s * kXS);
       } else {
         const uint32_t j = i - kXDma;
-        if (j < nwl) dma16(src.q, ws + 1024u * (wave + kNW * j), wl[j], (s0 + s) * 68u);
+        if (j < nwl) dma16(src.q, ws + 1024u * (wave + kNW * j), wl[j], s * 68u);
       }
     }
   };
-  // wait until this wave's loads of the previous step are complete (the
-  // next step's may be outstanding)
+  // wait until this wave's loads of the oldest step in flight are complete
+  // (those of the NS - 2 later steps may be outstanding)
   auto wait_prev = [&]() {
     if (kWG % kNW == 0 || nwl == kWDma)
-      wait_vm<kXDma + kWDma>();
+      wait_vm<(NS - 2u) * (kXDma + kWDma)>();
     else
-      wait_vm<kXDma + kWDma - 1>();
+      wait_vm<(NS - 2u) * (kXDma + kWDma - 1u)>();
   };
   auto issue = [&](uint32_t s, const uint8_t *xs, const uint8_t *ws) {
 #pragma unroll
@@ -230,17 +242,19 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
   };
 
   // the last step of k holds one block
-  const bool tail_half = (k % kBK) != 0u && s0 + steps == steps_all;
-  // Step s computes from stage cur; the operands of slot m + 1 are read and
-  // decoded while the 16 MFMAs of slot m run, and the loads of step s + 2
-  // go to stage tgt in four groups. Before the last slot's MFMAs, the wave
-  // waits for its loads of step s + 1 (at most the kDma loads of step s + 2
-  // may still be outstanding) and meets the others at a barrier: stage nxt
-  // is then complete, and every wave is done reading stage cur, which the
-  // loads of step s + 3 (issued during step s + 1) overwrite. Slot 0 of
-  // step s + 1 is then prepared during the last MFMAs of step s.
+  const bool tail_half = (k % kBK) != 0u;
+  // Step s computes from stage s % NS; the operands of slot m + 1 are read
+  // and decoded while the MFMAs of slot m run, and the loads of step
+  // s + NS - 1 go to stage tgt (the one step s - 1 read) in four groups.
+  // Before the last slot's MFMAs, the wave waits for its loads of step s + 1
+  // (those of steps s + 2 .. s + NS - 1 may still be outstanding) and meets
+  // the others at a barrier: stage nxt is then complete, and every wave is
+  // done reading stage cur, which the loads issued during step s + 1
+  // overwrite. Slot 0 of step s + 1 is then prepared during the last MFMAs
+  // of step s. Past the last step the loads repeat it into stages no step
+  // reads any more, so every step issues the same number of loads.
   auto step = [&](uint32_t s, const uint8_t *cur, const uint8_t *nxt, const uint8_t *tgt) {
-    const uint32_t sn = min(s + 2u, last);
+    const uint32_t sn = min(s + NS - 1u, last);
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       issue_group(m, sn, tgt, tgt + kXS);
@@ -277,24 +291,24 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
     }
   };
 
-  issue(0, st0, st0 + kXS);
-  issue(min(1u, last), st1, st1 + kXS);
+#pragma unroll
+  for (uint32_t j = 0; j + 1u < NS; ++j) issue(min(j, last), stage(j), stage(j) + kXS);
   wait_prev();
   __builtin_amdgcn_s_barrier();
   scales(st0 + kXS, !(tail_half && last == 0u));
   operands(st0, 0);
-  // three steps per iteration, so that the stages are fixed objects; the
-  // last one or two steps after the loop (no branch inside the loop: the
-  // accumulators stay in place). After the last step, the reads of a
-  // following step see stale stage contents and are not used.
+  // NS steps per iteration, so that the stages are fixed objects; the last
+  // steps after the loop (no branch inside the loop: the accumulators stay
+  // in place). After the last step, the reads of a following step see stale
+  // stage contents and are not used.
   uint32_t s = 0;
-  for (; s + 3u <= steps; s += 3u) {
-    step(s, st0, st1, st2);
-    step(s + 1u, st1, st2, st0);
-    step(s + 2u, st2, st0, st1);
+  for (; s + NS <= steps; s += NS) {
+#pragma unroll
+    for (uint32_t j = 0; j < NS; ++j) step(s + j, stage(j), stage((j + 1u) % NS), stage((j + NS - 1u) % NS));
   }
-  if (s < steps) step(s, st0, st1, st2);
-  if (s + 1u < steps) step(s + 1u, st1, st2, st0);
+#pragma unroll
+  for (uint32_t j = 0; j + 1u < NS; ++j)
+    if (s + j < steps) step(s + j, stage(j), stage((j + 1u) % NS), stage((j + NS - 1u) % NS));
   wait_vm<0>();
 
   // D[tok][row]: lane holds row (column) n of each fragment and tokens
@@ -308,49 +322,61 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const uint32_t tok = t0 + kFM * 32u * wm + 32u * fi + 8u * (v >> 2) + 4u * h + (v & 3);
-        if (tok < tokens) {
-          if constexpr (KS == 1)
-            y[(uint64_t)tok * rows + row] = acc[fi][fj][v];
-          else
-            unsafeAtomicAdd(y + (uint64_t)tok * rows + row, acc[fi][fj][v]);
-        }
+        if (tok < tokens) y[(uint64_t)tok * rows + row] = acc[fi][fj][v];
       }
   }
 }
 
 
-__global__ __launch_bounds__(256) void k_zero(float4 *__restrict__ p, uint64_t n4) {
-  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-  if (i < n4) p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-}
-
-template <uint32_t BM, uint32_t BN, uint32_t KS>
+template <uint32_t BM, uint32_t BN, uint32_t WM, uint32_t NS>
 hipError_t gemm_q8_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
   const uint32_t tok_tiles = (tokens + BM - 1) / BM, row_tiles = (wv.rows + BN - 1) / BN;
-  if (KS > 1) {
-    // y is zeroed by a kernel (not a memset node) so that graph replays stay exact
-    const uint64_t n4 = (uint64_t)tokens * wv.rows / 4u;
-    hipLaunchKernelGGL(k_zero, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, s, (float4 *)y, n4);
-  }
-  hipLaunchKernelGGL((k_gemm_q8<BM, BN, KS>), dim3(row_tiles * tok_tiles * KS), dim3(kNW * 64), 0, s, wv, xh, y, tokens,
+  hipLaunchKernelGGL((k_gemm_q8<BM, BN, WM, NS>), dim3(row_tiles * tok_tiles), dim3(kNW * 64), 0, s, wv, xh, y, tokens,
                      row_tiles, tok_tiles);
   return hipGetLastError();
+}
+
+// Tile configurations: tokens x rows per workgroup, waves along tokens, LDS
+// stages. cfg 0 chooses by the plan's token count (C3 shape, 8192 x 2048,
+// us per launch with the x conversion): 64 x 128 with 4 stages below 384
+// tokens (two workgroups per CU; M = 256: 23.8 against 30.5 for 128 x 128);
+// 128 x 128 with 6 stages below 768 (M = 512: 34.5 against 35.3 with 3
+// stages); 128 x 128 with 3 stages (two workgroups per CU) below 1536
+// (M = 1024: 55.2 against 66.5 for 256 x 256); 256 x 256 from 1536 (M = 2048:
+// 83.9 against 98.9 for 256 x 128 and 106 for 128 x 128).
+uint32_t gemm_q8_choice(uint32_t plan, uint32_t cfg) {
+  if (cfg >= 1 && cfg <= 6) return cfg;
+  if (plan < 384) return 4u;
+  if (plan < 768) return 3u;
+  if (plan < 1536) return 2u;
+  return 1u;
 }
 
 }  // namespace
 
 bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows) {
-  return type == Q8_0 && tokens >= 256 && k % 32u == 0 && (tokens >= 1024 || ((uint64_t)tokens * rows) % 4u == 0);
+  return type == Q8_0 && tokens >= 256 && k % 32u == 0;
 }
 
-uint32_t gemm_big_tile_log2(uint32_t tokens) { return tokens >= 1024 ? 8u : 7u; }
+uint32_t gemm_big_tile_log2(uint32_t tokens, uint32_t cfg) {
+  switch (gemm_q8_choice(tokens, cfg)) {
+    case 1: case 6: return 8u;
+    case 4: return 6u;
+    default: return 7u;
+  }
+}
 
 hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
-                           hipStream_t s) {
-  // >= 1024 tokens: 256 x 256 tiles fill the GPU; below, 128 x 128 tiles
-  // (at 512 tokens: 256 workgroups, where 128 x 256 tiles left half the CUs idle)
-  if (plan >= 1024) return gemm_q8_go<256, 256, 1>(wv, xh, y, tokens, s);
-  return gemm_q8_go<128, 128, 1>(wv, xh, y, tokens, s);
+                           uint32_t cfg, hipStream_t s) {
+  switch (gemm_q8_choice(plan, cfg)) {
+    case 1: return gemm_q8_go<256, 256, 1, 3>(wv, xh, y, tokens, s);
+    case 2: return gemm_q8_go<128, 128, 1, 3>(wv, xh, y, tokens, s);
+    case 3: return gemm_q8_go<128, 128, 1, 6>(wv, xh, y, tokens, s);
+    case 4: return gemm_q8_go<64, 128, 1, 4>(wv, xh, y, tokens, s);
+    case 5: return gemm_q8_go<128, 256, 1, 4>(wv, xh, y, tokens, s);
+    case 6: return gemm_q8_go<256, 128, 2, 3>(wv, xh, y, tokens, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace eff

@@ -74,15 +74,16 @@ hipError_t launch_gemv_mt(const WeightView &wv, const float *x, float *y, uint32
 // The kernel configuration is the one chosen for `plan` tokens (plan >=
 // tokens); a run over fewer tokens gives those rows the bits they get in a
 // run over `plan` tokens.
-size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows);
+// cfg: the Q8_0 tile configuration (EFF_OPT_GEMM_CONFIG; 0 automatic).
+size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg);
 hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint32_t plan,
-                       void *xh_scratch, hipStream_t stream);
+                       uint32_t cfg, void *xh_scratch, hipStream_t stream);
 // Q8_0 GEMM with direct-to-LDS staging (>= 256 tokens); x in the
 // [token tile][k step][2^gemm_big_tile_log2 tokens][64] layout.
 bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows);
-uint32_t gemm_big_tile_log2(uint32_t tokens);
+uint32_t gemm_big_tile_log2(uint32_t tokens, uint32_t cfg);
 hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
-                           hipStream_t stream);
+                           uint32_t cfg, hipStream_t stream);
 
 // Split-x matrix-core product (eff_gemm_sx.hip): Q2_K, Q4_K, IQ2_XXS from 4
 // tokens, k % 256 == 0, f32-accurate. `scratch` holds sx_x_bytes(...) bytes

@@ -1029,10 +1029,10 @@ static hipError_t gemm_go(const WeightView &wv, const _Float16 *xh, float *y, ui
 }
 
 // Token tile and k step of the chosen configuration (log2), as the x layout needs them.
-static void gemm_x_tile(int type, uint32_t plan, uint32_t k, uint32_t rows, uint32_t &bm_log2,
+static void gemm_x_tile(int type, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg, uint32_t &bm_log2,
                         uint32_t &bk_log2) {
   if (gemm_big_applies(type, plan, k, rows)) {
-    bm_log2 = gemm_big_tile_log2(plan);
+    bm_log2 = gemm_big_tile_log2(plan, cfg);
     bk_log2 = 6;
   } else if (gemm_wide(type, plan)) {
     bm_log2 = 8; bk_log2 = 6;
@@ -1041,26 +1041,26 @@ static void gemm_x_tile(int type, uint32_t plan, uint32_t k, uint32_t rows, uint
   }
 }
 
-size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows) {
+size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg) {
   uint32_t bm, bk;
-  gemm_x_tile(type, plan, k, rows, bm, bk);
+  gemm_x_tile(type, plan, k, rows, cfg, bm, bk);
   const uint64_t tiles = (tokens + (1u << bm) - 1) >> bm, steps = (k + (1u << bk) - 1) >> bk;
   return (size_t)(tiles * steps) << (bm + bk + 1);
 }
 
 hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint32_t plan,
-                       void *xh_scratch, hipStream_t s) {
+                       uint32_t cfg, void *xh_scratch, hipStream_t s) {
   if (plan < tokens) return hipErrorInvalidValue;
   uint32_t bm, bk;
-  gemm_x_tile(wv.type, plan, wv.k, wv.rows, bm, bk);
+  gemm_x_tile(wv.type, plan, wv.k, wv.rows, cfg, bm, bk);
   const uint32_t steps = (wv.k + (1u << bk) - 1) >> bk;
-  const uint64_t n8 = (uint64_t)gemm_x_bytes(wv.type, tokens, plan, wv.k, wv.rows) / 16u;
+  const uint64_t n8 = (uint64_t)gemm_x_bytes(wv.type, tokens, plan, wv.k, wv.rows, cfg) / 16u;
   _Float16 *xh = (_Float16 *)xh_scratch;
   hipLaunchKernelGGL(k_x_to_f16, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, s, x, xh, tokens, wv.k, bm, bk,
                      steps, n8);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (gemm_big_applies(wv.type, plan, wv.k, wv.rows)) return launch_gemm_big(wv, xh, y, tokens, plan, s);
+  if (gemm_big_applies(wv.type, plan, wv.k, wv.rows)) return launch_gemm_big(wv, xh, y, tokens, plan, cfg, s);
   switch (wv.type) {
     case Q8_0: return gemm_go<Q8_0>(wv, xh, y, tokens, plan, s);
     case Q8_0R: return gemm_go<Q8_0R>(wv, xh, y, tokens, plan, s);

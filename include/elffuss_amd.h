@@ -57,6 +57,10 @@ extern "C" {
                                        workgroups added into y */
 #define EFF_OPT_SPLIT_MIN_TOKENS 5  /* Q2_K, Q4_K, IQ2_XXS: tokens >= this run the split-x product, fewer the int8
                                        matrix-core GEMVs (0: automatic, 8 and 9 for Q4_K (default); else >= 4) */
+#define EFF_OPT_GEMM_CONFIG      6  /* Q8_0 GEMM from 256 tokens, tiles (tuning; tokens x rows, waves along tokens x
+                                       rows, LDS stages): 0 automatic (default), 1: 256x256 1x4 3, 2: 128x128 1x4 3,
+                                       3: 128x128 1x4 6, 4: 64x128 1x4 4, 5: 128x256 1x4 4, 6: 256x128 2x2 3; every
+                                       configuration sums each output in the same order (the same bits) */
 
 /* ---- fused GEMV modes (gemv2Shader `modo`, kernels.gemv.wgsl.js:370-375) -- */
 #define EFF_GEMV_SECTIONS  1  /* 'secciones': ys[i] = W_i x for 2..4 matrices */

@@ -245,6 +245,35 @@ def test_gemm_q8_0_k_not_multiple_of_step(ctx, eff, orc):
     check_close(yb.read(np.float32), orc.gemm_f16(orc.Q8_0, gguf, rows, k, x, tokens), "gemm Q8_0 k=96")
 
 
+@pytest.mark.parametrize("tokens", [300, 777])
+def test_gemm_q8_0_tile_configs_same_bits(ctx, eff, orc, tokens):
+    """Every Q8_0 tile configuration (EFF_OPT_GEMM_CONFIG 1..6: 256 x 256,
+    128 x 128 with 3 and 6 stages, 64 x 128, 128 x 256, 256 x 128 on 2 x 2
+    waves) sums each output in the same k order: the same bits as the
+    automatic choice, and the fp16-rounded oracle's values. Rows and tokens
+    are not multiples of any tile, and k ends in half a step (k % 64 = 32)."""
+    rows, k = 600, 544
+    t, data, gguf, n = make_weights(eff, "Q8_0", rows, k, 810 + tokens)
+    x = eff.fill_normal(811 + tokens, 1.0, tokens * k)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+    y0 = yb.read(np.uint32)
+    check_close(y0.view(np.float32), orc.gemm_f16(orc.Q8_0, gguf, rows, k, x, tokens), f"gemm Q8_0 M={tokens}")
+    try:
+        for cfg in range(1, 7):
+            ctx.set_option(eff.OPT_GEMM_CONFIG, cfg)
+            yb.write(np.full(tokens * rows, 0x7FC00000, np.uint32))
+            ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+            y = yb.read(np.uint32)
+            assert np.array_equal(y, y0), f"config {cfg}: {np.count_nonzero(y != y0)} outputs differ"
+        with pytest.raises(eff.EffError):
+            ctx.set_option(eff.OPT_GEMM_CONFIG, 7)
+    finally:
+        ctx.set_option(eff.OPT_GEMM_CONFIG, 0)
+    for b in (wb, xb, yb):
+        b.free()
+
+
 # ---- fused decode GEMV (gemv.gateUp, gemv.secciones) -----------------------------------
 
 def silu64(v):
