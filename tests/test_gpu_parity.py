@@ -245,14 +245,15 @@ def test_gemm_q8_0_k_not_multiple_of_step(ctx, eff, orc):
     check_close(yb.read(np.float32), orc.gemm_f16(orc.Q8_0, gguf, rows, k, x, tokens), "gemm Q8_0 k=96")
 
 
-@pytest.mark.parametrize("tokens", [300, 777])
-def test_gemm_q8_0_tile_configs_same_bits(ctx, eff, orc, tokens):
+@pytest.mark.parametrize("tokens,k", [(300, 544), (777, 544), (300, 96)])
+def test_gemm_q8_0_tile_configs_same_bits(ctx, eff, orc, tokens, k):
     """Every Q8_0 tile configuration (EFF_OPT_GEMM_CONFIG 1..6: 256 x 256,
     128 x 128 with 3 and 6 stages, 64 x 128, 128 x 256, 256 x 128 on 2 x 2
     waves) sums each output in the same k order: the same bits as the
     automatic choice, and the fp16-rounded oracle's values. Rows and tokens
-    are not multiples of any tile, and k ends in half a step (k % 64 = 32)."""
-    rows, k = 600, 544
+    are not multiples of any tile, k ends in half a step (k % 64 = 32), and
+    k = 96 has fewer steps than the deepest pipeline has stages."""
+    rows = 600
     t, data, gguf, n = make_weights(eff, "Q8_0", rows, k, 810 + tokens)
     x = eff.fill_normal(811 + tokens, 1.0, tokens * k)
     wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4)
