@@ -635,13 +635,9 @@ hipError_t sx_go_fx(const WeightView &wv, const float *x, float *y, uint32_t tok
   using L = SxLds<TYPE, 1, 1, 8>;
   constexpr uint32_t lds = L::TAB + L::WORK + 8u * sx_fx_bytes<TYPE>();
   static_assert(lds + 16u <= kMxMaxLds, "fused split-x LDS");
-  static bool attr = false;
-  const void *fn = (const void *)k_sx<TYPE, 1, 1, 8, 1, true>;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  const hipError_t e = lds_limit_once((const void *)k_sx<TYPE, 1, 1, 8, 1, true>, (int)lds, attr);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((k_sx<TYPE, 1, 1, 8, 1, true>), dim3(p.row_tiles, 1), dim3(8 * 64), lds, s, wv, nullptr, nullptr,
                      y, tokens, p.nbw, 0u, x);
   return hipGetLastError();

@@ -1109,15 +1109,11 @@ bool gemv_mx_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p) {
 // size (persistent grids are sized to it).
 template <int TYPE, int T, int NW, int F>
 static hipError_t mx_resident(size_t lds, uint32_t &out) {
-  static bool attr = false;
-  if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_mx<TYPE, T, NW, F>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMxMaxLds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  hipError_t e = lds_limit_once((const void *)k_gemv_mx<TYPE, T, NW, F>, (int)kMxMaxLds, attr);
+  if (e != hipSuccess) return e;
   int dev = 0, cus = 0, per = 0;
-  hipError_t e = hipGetDevice(&dev);
+  e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e == hipSuccess)
     e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_gemv_mx<TYPE, T, NW, F>, NW * 64, lds);
@@ -1242,13 +1238,9 @@ bool gemv_mt_plan(const WeightView &wv, uint32_t tokens, GemvPlan &p) {
 template <int TYPE, int TG, int NW>
 static hipError_t mt_launch(const WeightView &wv, const float *x, float *y, uint32_t tokens, const GemvPlan &p,
                             hipStream_t s) {
-  static bool attr = false;
-  if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void *)k_gemv_mt<TYPE, TG, NW>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMxMaxLds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  const hipError_t e = lds_limit_once((const void *)k_gemv_mt<TYPE, TG, NW>, (int)kMxMaxLds, attr);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((k_gemv_mt<TYPE, TG, NW>), dim3(p.grid), dim3(NW * 64), p.lds_bytes, s, wv, x, y, tokens,
                      (uint32_t)__builtin_ctz((unsigned)p.ksplit));
   return hipGetLastError();

@@ -356,13 +356,9 @@ __global__ __launch_bounds__(kRowsWaves * 64) void k_rows_pick(const uint32_t *_
 
 template <bool REC, uint32_t KS>
 hipError_t launch_rows_ks(const WeightView &wv, const float *x, float *y, uint8_t *rec, uint32_t lds, hipStream_t s) {
-  static bool attr = false;
-  const void *fn = (const void *)k_gemv_rows_q6k<REC, KS>;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMxMaxLds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  const hipError_t e = lds_limit_once((const void *)k_gemv_rows_q6k<REC, KS>, (int)kMxMaxLds, attr);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((k_gemv_rows_q6k<REC, KS>), dim3(gemv_rows_groups(wv)), dim3(kRowsWaves * 64), lds, s, wv, x, y,
                      rec);
   return hipGetLastError();

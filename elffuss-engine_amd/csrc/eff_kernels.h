@@ -5,7 +5,23 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace eff {
+
+// Raises the dynamic-LDS limit of kernel `fn` to `bytes` once per device: `done`
+// (one per kernel) holds a bit per device whose limit is set. Safe to call
+// from several threads (a second setter repeats the same idempotent call).
+inline hipError_t lds_limit_once(const void *fn, int bytes, std::atomic<uint64_t> &done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? 1ull << dev : 0ull;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+  return e;
+}
 
 // One quantized matrix W (rows x k) and its addressing.
 struct WeightView {

@@ -995,13 +995,9 @@ static hipError_t gemm_cfg(const WeightView &wv, const _Float16 *xh, float *y, u
   constexpr size_t lds = (stages > red ? stages : red) + (TYPE == IQ2_XXS ? 2048 : 0);
   constexpr int NS = gemm_sets<TYPE, BM, BN, BK>();
   static_assert(lds <= 160 * 1024, "LDS");
-  static bool attr = false;
-  if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void *)k_gemm<TYPE, BM, BN, BK, CM, CN, CK, NS>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  const hipError_t e = lds_limit_once((const void *)k_gemm<TYPE, BM, BN, BK, CM, CN, CK, NS>, (int)lds, attr);
+  if (e != hipSuccess) return e;
   const uint32_t tok_tiles = (tokens + BM - 1) / BM, row_tiles = (wv.rows + BN - 1) / BN;
   hipLaunchKernelGGL((k_gemm<TYPE, BM, BN, BK, CM, CN, CK, NS>), dim3(row_tiles * tok_tiles), dim3(512), lds, s, wv, xh,
                      y, tokens, row_tiles, tok_tiles);
@@ -1115,13 +1111,9 @@ template <int TYPE>
 static hipError_t gather_norm_go(const WeightView &wv, const uint32_t *ids, uint32_t tokens, const float *wn, float eps,
                                  float *x, float *nrm, hipStream_t s) {
   const size_t lds = (size_t)wv.k * 4u;
-  static bool attr = false;
-  if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void *)k_gather_norm<TYPE>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGatherNormMaxDim * 4);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  const hipError_t e = lds_limit_once((const void *)k_gather_norm<TYPE>, (int)kGatherNormMaxDim * 4, attr);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((k_gather_norm<TYPE>), dim3(tokens), dim3(256), lds, s, wv, ids, wn, eps, x, nrm);
   return hipGetLastError();
 }
