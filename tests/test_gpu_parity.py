@@ -638,6 +638,10 @@ def test_not_applicable_and_errors(ctx, eff):
     with pytest.raises(eff.EffError) as e:
         ctx.qmatmul(99, wb, xb, yb, rows, k, 1)
     assert e.value.code == eff.E_TYPE
+    for shape in ((0, k, 1), (rows, 0, 1), (rows, k, 0)):   # empty shapes are refused, nothing launched
+        with pytest.raises(eff.EffError) as e:
+            ctx.qmatmul(t, wb, xb, yb, *shape)
+        assert e.value.code == eff.E_INVALID and "empty" in str(e.value)
     with pytest.raises(eff.EffError) as e:
         ctx.qmatmul(t, wb, xb, yb, rows * 4, k, 1)      # W too small for the call
     assert e.value.code == eff.E_BOUNDS
