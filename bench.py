@@ -129,6 +129,30 @@ class FusedConfig:
             b.free()
 
 
+class ReadConfig:
+    """A plain streaming read of a configuration's weight copies
+    (eff_read_floor), rotated like its steps: the floor a GEMV's time is
+    compared with, beside the HBM roofline."""
+
+    def __init__(self, cfg, workgroups, unroll, sink):
+        self.w, self.copies, self.w_bytes = cfg.w, cfg.copies, cfg.w_bytes
+        self.workgroups, self.unroll, self.sink = workgroups, unroll, sink
+
+    def step(self, ctx, i):
+        ctx.read_floor(self.w[i % self.copies], self.w_bytes, self.workgroups, self.unroll, self.sink)
+
+
+# grid shapes of the read (workgroups of 256 threads, 16-byte loads in flight per lane): the fastest of them per
+# size in a sweep of 256-2048 workgroups x 1, 2, 4 loads
+READ_SHAPES = ((2048, 1), (1024, 2), (1024, 4))
+
+
+def read_floor_ms(torch, ctx, cfg, sink, steps):
+    """The fastest read of cfg's weight bytes over READ_SHAPES, ms per step."""
+    return min(time_steps(torch, ctx, ReadConfig(cfg, wg, un, sink), steps, 5, warm_replays=3, timed=3)
+               for wg, un in READ_SHAPES)
+
+
 def rotation(cfg, steps):
     """What the timed steps of `cfg` read: copies, bytes, reuse distance."""
     per = cfg.w_bytes
@@ -321,7 +345,8 @@ def main():
     # Headline: configs[3], the Q6_K head GEMV + top-40 (the largest single-GPU configuration)
     rows, k = 65536, 2048
     ms = ms_gemv = gbs = gemv_gbs = float("nan")
-    rot = None
+    rot = floor = None
+    sink = ctx.alloc(4 * 65536)
     if not args.no_head:
         head = Config(eff, ctx, "Q6_K", rows, k, 1, 404, topk=40)
         # W eager warm-up steps and three untimed replays of the K captured steps, then one timed replay
@@ -332,6 +357,12 @@ def main():
         head.topk = 0
         ms_gemv = time_steps(torch, ctx, head, args.steps, args.warmup, warm_replays=3)
         gemv_gbs = head.bytes / (ms_gemv * 1e-3) / 1e9
+        # the same weight bytes read plainly, rotated the same way
+        f_ms = read_floor_ms(torch, ctx, head, sink, args.steps)
+        floor = {"us": round(f_ms * 1e3, 2), "GB/s": round(head.w_bytes / (f_ms * 1e-3) / 1e9, 1),
+                 "gemv_frac_of_read": round(f_ms / ms_gemv, 4),
+                 "what": "eff_read_floor: the weight bytes read with 16-byte loads, no compute, the fastest of "
+                         + ", ".join(f"{w} x {u}" for w, u in READ_SHAPES) + " (workgroups x loads in flight)"}
         head.free()
         print(f"# headline: {ms * 1e3:.2f} us per step ({gbs:.1f} GB/s), GEMV alone {ms_gemv * 1e3:.2f} us",
               file=sys.stderr, flush=True)
@@ -388,6 +419,11 @@ def main():
                           "roofline_frac": round((mfma_t if bound == "mfma" else hbm_t) / (t_ms * 1e-3), 4),
                           "path": path + (" + top-k" if tk < 0 else " + fused top-k records" if tk else ""),
                           "reuse_distance_MB": round(rotation(cfg, steps)["reuse_distance_bytes"] / 1e6)}
+            if bound == "hbm" and not tk:
+                # a plain read of the same weight bytes (x and y not included), as a floor beside the roofline
+                f_ms = read_floor_ms(torch, ctx, cfg, sink, steps)
+                sweep[key]["read_floor_us"] = round(f_ms * 1e3, 2)
+                sweep[key]["frac_of_read_floor"] = round(f_ms / t_ms, 4)
             cfg.free()
             print(f"# {key}: {sweep[key]}", file=sys.stderr, flush=True)
 
@@ -435,10 +471,12 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "k_gemv_rows_q6k (Q6_K, 1 token)", "achieved": round(gemv_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic},
+        "read_floor": floor,
         "cpu_baseline": base,
         "js_chain": chain,
         "sweep": sweep,
     }
+    sink.free()
     ctx.close()
     print(json.dumps(line), flush=True)
 

@@ -722,6 +722,24 @@ int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint
   return EFF_OK;
 }
 
+int eff_read_floor(eff_ctx *ctx, eff_buf *src, size_t bytes, uint32_t workgroups, uint32_t unroll, eff_buf *sink) {
+  if (!ctx) return EFF_E_INVALID;
+  if (!src || !sink) return fail(ctx, EFF_E_INVALID, "read floor: null buffer");
+  if (bytes == 0 || workgroups == 0 || workgroups > 65535u || (unroll != 1u && unroll != 2u && unroll != 4u))
+    return fail(ctx, EFF_E_INVALID, "read floor: %zu bytes, %u workgroups, unroll %u (bytes > 0, 1..65535 workgroups, "
+                "unroll 1, 2 or 4)", bytes, workgroups, unroll);
+  if (bytes > src->size) return fail(ctx, EFF_E_BOUNDS, "read floor: %zu bytes from a buffer of %zu", bytes, src->size);
+  if ((uint64_t)workgroups * 4u > sink->size)
+    return fail(ctx, EFF_E_BOUNDS, "read floor: the sink needs %llu bytes and has %zu",
+                (unsigned long long)workgroups * 4u, sink->size);
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  const hipError_t e = launch_read_floor((const uint8_t *)src->ptr, bytes, workgroups, unroll, (uint32_t *)sink->ptr,
+                                         ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "read floor launch");
+  return EFF_OK;
+}
+
 int eff_dequant(eff_ctx *ctx, int type, eff_buf *w, eff_buf *out, uint32_t n_blocks) {
   if (!ctx) return EFF_E_INVALID;
   if (!w || !out) return fail(ctx, EFF_E_INVALID, "dequant: null buffer");

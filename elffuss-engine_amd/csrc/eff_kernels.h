@@ -120,6 +120,13 @@ hipError_t launch_gather_norm(const WeightView &wv, const uint32_t *ids, uint32_
 
 hipError_t launch_dequant(const WeightView &wv, uint32_t n_blocks, float *out, hipStream_t stream);
 
+// Streaming read of `bytes` bytes of src by `workgroups` workgroups of 256
+// threads, `unroll` (1, 2, 4) 16-byte loads in flight per lane; sink holds one
+// word per workgroup (written only in the unlikely event that a workgroup's XOR
+// of its bytes equals a fixed constant).
+hipError_t launch_read_floor(const uint8_t *src, uint64_t bytes, uint32_t workgroups, uint32_t unroll, uint32_t *sink,
+                             hipStream_t stream);
+
 // Top-k (eff_topk.hip). The logits are cut into G <= kTopkGroupsMax groups
 // of 256 * ceil(vocab / 65536) consecutive logits; the first kernel writes
 // one kTopkRecordBytes record per group (its 4 largest elements) and, in an

@@ -1076,6 +1076,45 @@ static hipError_t dequant_go(const WeightView &wv, uint32_t n_blocks, float *out
   return hipGetLastError();
 }
 
+// Streaming read of `bytes` bytes (the floor the GEMVs are measured against):
+// workgroup b reads the contiguous chunk [b chunk, (b + 1) chunk) with 16-byte
+// loads, U in flight per lane, and folds them with XOR. sink[b] is written only
+// when the fold equals `magic`, so the loads stay and nothing is written in
+// practice.
+template <int U>
+__global__ __launch_bounds__(256) void k_read_floor(const uint8_t *__restrict__ src, uint64_t bytes, uint32_t chunk,
+                                                    uint32_t *__restrict__ sink, uint32_t magic) {
+  const uint64_t base = (uint64_t)blockIdx.x * chunk;
+  if (base >= bytes) return;
+  const uint32_t n = (uint32_t)min<uint64_t>(bytes - base, chunk);
+  const rsrc_t r = make_rsrc(src + base, n);
+  uint32_t acc = 0;
+  for (uint32_t o = threadIdx.x * 16u; o < n; o += 256u * 16u * U) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(o + 4096u * u), 0, 0));
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  if (acc == magic) sink[blockIdx.x] = acc;
+}
+
+hipError_t launch_read_floor(const uint8_t *src, uint64_t bytes, uint32_t workgroups, uint32_t unroll, uint32_t *sink,
+                             hipStream_t s) {
+  const uint64_t per = (bytes + workgroups - 1u) / workgroups;
+  const uint64_t chunk = (per + 4095u) / 4096u * 4096u;
+  if (chunk > 0x7FFFF000u) return hipErrorInvalidValue;
+  const uint32_t magic = 0x9E3779B9u;
+  switch (unroll) {
+    case 1: hipLaunchKernelGGL(k_read_floor<1>, dim3(workgroups), dim3(256), 0, s, src, bytes, (uint32_t)chunk, sink, magic); break;
+    case 2: hipLaunchKernelGGL(k_read_floor<2>, dim3(workgroups), dim3(256), 0, s, src, bytes, (uint32_t)chunk, sink, magic); break;
+    case 4: hipLaunchKernelGGL(k_read_floor<4>, dim3(workgroups), dim3(256), 0, s, src, bytes, (uint32_t)chunk, sink, magic); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_dequant(const WeightView &wv, uint32_t n_blocks, float *out, hipStream_t s) {
   switch (wv.type) {
     case Q8_0: return dequant_go<Q8_0>(wv, n_blocks, out, s);

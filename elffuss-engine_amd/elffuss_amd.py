@@ -105,6 +105,7 @@ def lib():
         "eff_gather_norm": ([p, i32, p, p, p, ctypes.c_float, p, p, u32, u32], i32),
         "eff_topk": ([p, p, u32, u32, u32, p, u32, u32, p], i32),
         "eff_topk_noalloc": ([p, p, u32, u32, u32, p, u32, u32, p], i32),
+        "eff_read_floor": ([p, p, ctypes.c_size_t, u32, u32, p], i32),
         "eff_qgemv_topk": ([p, i32, p, p, p, u32, u32, u32, p, u32, u32, p], i32),
         "eff_topk_out_bytes": ([], sz),
     }
@@ -122,7 +123,7 @@ EXPORTED = ("eff_type_from_name eff_type_name eff_type_geometry eff_init eff_shu
             "eff_read_begin eff_read_end eff_read_error eff_read_release "
             "eff_bytes_reordered eff_bytes_buffer_r eff_blocks_from_buffer eff_scales_from eff_buf_mark_r "
             "eff_buf_blocks_r eff_buf_write_r eff_repack eff_unrepack eff_quantize eff_fill_normal eff_qmatmul eff_qgemv "
-            "eff_qgemm eff_qgemm_planned eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_noalloc eff_qgemv_topk eff_topk_out_bytes").split()
+            "eff_qgemm eff_qgemm_planned eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_noalloc eff_qgemv_topk eff_topk_out_bytes eff_read_floor").split()
 
 
 def type_code(t):
@@ -376,6 +377,10 @@ class Context:
         self._check(lib().eff_topk_noalloc(self.h, logits.handle, base, vocab, m,
                                            ids.ctypes.data if ids.size else None, ids.size, serial, out.handle))
         return out
+
+    def read_floor(self, src, nbytes, workgroups, unroll, sink):
+        """eff_read_floor: a streaming read of nbytes of src (measurement only)."""
+        self._check(lib().eff_read_floor(self.h, src.handle, nbytes, workgroups, unroll, sink.handle))
 
 
 def parse_topk(u):

@@ -336,6 +336,17 @@ int eff_topk_noalloc(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t voca
 /* Size in bytes of the top-k output record (topkBytesSalida). */
 size_t eff_topk_out_bytes(void);
 
+/* ---- measurement --------------------------------------------------------- */
+
+/* No counterpart in the reference: a streaming read of the first `bytes` bytes
+ * of `src`, on the context's stream, by `workgroups` (1..65535) workgroups of
+ * 256 threads, each reading one contiguous chunk with 16-byte loads, `unroll`
+ * (1, 2 or 4) in flight per lane. It computes nothing visible (`sink`, at least
+ * 4 * workgroups bytes, is written only if a workgroup's XOR of its bytes equals
+ * a fixed constant). The time of the same bytes read this way is the floor the
+ * benchmark holds each GEMV against, beside the HBM roofline. */
+int eff_read_floor(eff_ctx *ctx, eff_buf *src, size_t bytes, uint32_t workgroups, uint32_t unroll, eff_buf *sink);
+
 #ifdef __cplusplus
 }
 #endif

@@ -818,3 +818,22 @@ def test_topk_all_equal(ctx, eff):
     vals = np.full(9000, 1.5, np.float32)
     r = run_topk(ctx, eff, vals, 40)
     assert list(r["ids"]) == list(range(40))
+
+
+def test_read_floor_reads_and_checks_its_arguments(ctx, eff):
+    """eff_read_floor (the bench's streaming-read floor): every grid shape runs
+    over a buffer whose size is not a multiple of any chunk and leaves the sink
+    untouched (the XOR of the bytes is not its constant); bad shapes are refused."""
+    src = ctx.upload(np.arange(3 * 1024 * 1024 + 48, dtype=np.uint8))
+    sink = ctx.upload(np.zeros(4096, np.uint32))
+    for wg, un in ((2048, 1), (1024, 2), (1024, 4), (1, 4), (3, 1)):
+        ctx.read_floor(src, src.size - 16, wg, un, sink)
+    ctx.sync()
+    assert not sink.read(np.uint32).any()
+    for args, code in (((src.size + 1, 16, 1), eff.E_BOUNDS), ((1024, 16, 3), eff.E_INVALID),
+                       ((1024, 0, 1), eff.E_INVALID), ((1024, 8192, 1), eff.E_BOUNDS), ((0, 16, 1), eff.E_INVALID)):
+        with pytest.raises(eff.EffError) as e:
+            ctx.read_floor(src, args[0], args[1], args[2], sink)
+        assert e.value.code == code, args
+    src.free()
+    sink.free()
