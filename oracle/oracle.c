@@ -18,9 +18,16 @@
  *   repack / buffer math   pinned (known answers of repack.js:225-229, round trip)
  *   f64 GEMV, fp16 GEMM    pinned (numpy matmul of the dequantized matrix)
  *   top-k                  pinned (numpy lexsort, hand-made ties, -0 == +0)
- *   CPU path (Q8 activations + integer dot)  parity unpinned: its C source is
- *                          not shipped and its WASM cannot run here; restated
- *                          from the JS-visible contract only (cpu.js:24-27,350-381).
+ *   CPU path (Q8 activations + integer dot)  pinned to its stated model:
+ *                          block fields (|q| <= 127, a +-127 per nonzero block,
+ *                          half-step error, s = d * sum q, zero blocks), ties
+ *                          away from zero, lossless blocks = f64 within the f32
+ *                          combine bound, bits independent of threads and
+ *                          chunks. The model itself (the 40-byte block as f32
+ *                          d, f32 s, 32 int8; roundf) is the reference's
+ *                          compiled WASM, whose C source is not shipped and
+ *                          which cannot run here: that literal code stays
+ *                          parity unpinned (cpu.js:24-27,350-381).
  */
 #include <math.h>
 #include <pthread.h>

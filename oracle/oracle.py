@@ -57,6 +57,7 @@ def lib():
         L.or_repack.argtypes = [p, u32, p, u64]; L.or_repack.restype = i32
         L.or_unrepack.argtypes = [p, u32, p]; L.or_unrepack.restype = i32
         L.or_cpu_matmul.argtypes = [i32, p, u32, u32, p, u32, i32, p]; L.or_cpu_matmul.restype = i32
+        L.or_cpu_quantize_acts.argtypes = [p, u32, u32, p]; L.or_cpu_quantize_acts.restype = i32
         g = grid_words()
         L.or_set_grid(g.ctypes.data)
         _lib = L
@@ -161,6 +162,21 @@ def unrepack(src, n):
     s = np.ascontiguousarray(src, dtype=np.uint8)
     out = np.zeros(34 * n, dtype=np.uint8)
     lib().or_unrepack(_ptr(s), n, _ptr(out))
+    return out
+
+
+# One 40-byte activation block of the CPU path as the restatement models it
+# (cpu.js:25 BACT = 40): f32 d, f32 sum, 32 int8.
+ACT_BLOCK = np.dtype([("d", "<f4"), ("s", "<f4"), ("q", "i1", (32,))])
+
+
+def cpu_quantize_acts(x, k, tokens):
+    """The CPU path's activation blocks (or_cpu_quantize_acts): per 32 values
+    d = amax / 127, q = round(v / d) with ties away from zero, s = d * sum(q)."""
+    xs = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(tokens * (k // 32), dtype=ACT_BLOCK)
+    rc = lib().or_cpu_quantize_acts(_ptr(xs), k, tokens, _ptr(out))
+    assert rc == 0, rc
     return out
 
 

@@ -373,7 +373,109 @@ def test_topk_signed_zero_and_nan(orc):
     assert orc.topk_key(0x80000000) == orc.topk_key(0)
 
 
-# ---- CPU path (parity unpinned: see oracle.c) ----------------------------------
+# ---- CPU path: the restatement pinned to its stated model ---------------------------
+# The reference's CPU kernels ship only as compiled WebAssembly (not decoded, not runnable
+# here). The restatement models them from the JS-visible contract: 40-byte activation blocks
+# (cpu.js:25) as f32 d = amax/127, f32 s = d * sum(q), 32 int8 q = round(v/d) (C roundf, ties
+# away from zero, as ggml's Q8_1 quantizer), an int32 dot per block and an f32 combine
+# (cpu.js:350-381), over row chunks claimed by a pool (cpu.js:140-206, cpu-trabajo.js:27-72).
+# What pins each part of that model is below; the literal WASM stays unpinned.
+
+def _gamma(n):
+    u = 2.0 ** -24
+    return n * u / (1 - n * u)
+
+
+def test_cpu_acts_fields(orc):
+    """Every block: |q| <= 127, a +-127 in every nonzero block, x within half a
+    step of q*d, the sum field equal to d times the integer sum, and a zero
+    block all zero."""
+    k, tokens = 2048, 3
+    x = RNG.normal(0, 1, tokens * k).astype(np.float32)
+    x[64:96] = 0.0                                   # one zero block
+    x[300] = 1e30                                     # a block with one outlier
+    a = orc.cpu_quantize_acts(x, k, tokens)
+    q = a["q"].astype(np.int64)
+    d = a["d"].astype(np.float64)
+    xb = x.reshape(-1, 32).astype(np.float64)
+    assert np.all(np.abs(q) <= 127)
+    nz = np.any(xb != 0, axis=1)
+    assert np.all(np.max(np.abs(q[nz]), axis=1) == 127)
+    assert np.all(np.abs(xb - q * d[:, None]) <= d[:, None] * (0.5 + 2.0 ** -20))
+    amax = np.max(np.abs(xb), axis=1)
+    assert np.all(np.abs(d - amax / 127) <= amax / 127 * 2.0 ** -23)   # d = amax / 127 in f32
+    assert np.array_equal(a["s"], (a["d"] * q.sum(axis=1).astype(np.float32)).astype(np.float32))
+    z = 2                                             # x[64:96] is block 2
+    assert a["d"][z] == 0 and a["s"][z] == 0 and not np.any(a["q"][z])
+
+
+def test_cpu_acts_half_steps_round_away_from_zero(orc):
+    """With amax = 127 the step d is 1 and q = round(v) exactly: ties go away
+    from zero (C roundf, the modelled choice; JS Math.round would send -2.5 to
+    -2 and -0.5 to -0)."""
+    v = np.zeros(32, np.float32)
+    v[:9] = [127, 2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 126.5, -3.4999998]
+    a = orc.cpu_quantize_acts(v, 32, 1)
+    assert a["d"][0] == 1.0
+    assert a["q"][0][:9].tolist() == [127, 3, -3, 1, -1, 2, -2, 127, -3]
+
+
+@pytest.mark.parametrize("e", [-10, 0, 7])
+def test_cpu_path_lossless_blocks_match_f64(orc, eff, e):
+    """x of integers in [-127, 127] times 2^e with a +-127 in every block: the
+    quantization is lossless (d = 2^e) and the integer dots exact, so the
+    output differs from the f64 product only by the f32 combine, within
+    gamma_(nb+1) * sum of |block terms| (recursive summation)."""
+    rows, k, tokens = 96, 2048, 3
+    xi = RNG.integers(-127, 128, tokens * k).astype(np.float64)
+    xi[::32] = np.where(RNG.random(tokens * k // 32) < 0.5, -127.0, 127.0)
+    x = (xi * 2.0 ** e).astype(np.float32)
+    a = orc.cpu_quantize_acts(x, k, tokens)
+    assert np.all(a["d"] == np.float32(2.0 ** e))
+    w = eff.quantize(orc.Q8_0, RNG.normal(0, 0.02, rows * k).astype(np.float32))
+    got = orc.cpu_matmul(orc.Q8_0, w, rows, k, x, tokens, 3).astype(np.float64)
+    ref = orc.gemv_f64(orc.Q8_0, w, rows, k, x, tokens)
+    wd = orc.dequant(orc.Q8_0, w, rows * k // 32).astype(np.float64).reshape(rows, k // 32, 32)
+    terms = np.abs(np.einsum("rbi,tbi->trb", wd, x.astype(np.float64).reshape(tokens, k // 32, 32))).sum(axis=2)
+    bound = _gamma(k // 32 + 1) * terms * 1.0001
+    assert np.all(np.abs(got - ref) <= bound + 1e-300)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-6
+
+
+def test_cpu_path_zero_block_and_one_element(orc, eff):
+    """A zero x block contributes nothing (the output keeps its bits whatever
+    the weights of that block); a block holding one nonzero value v gives
+    w * v within the rounding of d and of the combine."""
+    rows, k = 64, 1024
+    w = eff.quantize(orc.Q8_0, RNG.normal(0, 0.02, rows * k).astype(np.float32))
+    x = RNG.normal(0, 1, k).astype(np.float32)
+    x[256:288] = 0.0                                  # block 8
+    y1 = orc.cpu_matmul(orc.Q8_0, w, rows, k, x, 1, 1)
+    w2 = w.copy().reshape(rows, k // 32, 34)
+    w2[:, 8, 2:] = RNG.integers(0, 256, (rows, 32), dtype=np.uint8)
+    y2 = orc.cpu_matmul(orc.Q8_0, w2.reshape(-1), rows, k, x, 1, 1)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    x1 = np.zeros(k, np.float32)
+    x1[300] = np.float32(-0.7318)
+    y = orc.cpu_matmul(orc.Q8_0, w, rows, k, x1, 1, 2)[0].astype(np.float64)
+    wd = orc.dequant(orc.Q8_0, w, rows * k // 32).astype(np.float64).reshape(rows, k)
+    want = wd[:, 300] * np.float64(x1[300])
+    assert np.all(np.abs(y - want) <= np.abs(want) * 4 * 2.0 ** -24)
+
+
+def test_cpu_path_same_bits_for_any_threads_and_chunks(orc, eff):
+    """The rows a thread takes are summed alone, so the output has the same
+    bits for 1 to 16 threads and for row counts that are no multiple of the
+    chunk (cpu.js:140,173: chunks of max(4, ceil(rows / 4n / 4) * 4) rows)."""
+    k = 512
+    for rows in (1, 5, 67, 1000, 4097):
+        w = eff.quantize(orc.Q8_0, RNG.normal(0, 0.02, rows * k).astype(np.float32))
+        x = RNG.normal(0, 1, 2 * k).astype(np.float32)
+        base = orc.cpu_matmul(orc.Q8_0, w, rows, k, x, 2, 1).view(np.uint32)
+        for threads in (2, 3, 4, 7, 8, 16):
+            got = orc.cpu_matmul(orc.Q8_0, w, rows, k, x, 2, threads).view(np.uint32)
+            assert np.array_equal(got, base), (rows, threads)
+
 
 def test_cpu_path_close_to_f64(orc, eff):
     rows, k = 64, 2048
