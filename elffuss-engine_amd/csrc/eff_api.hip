@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include <deque>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -42,6 +43,16 @@ bool g_scratch_done[kMaxDevices];
 // bytes past a block (the reference's loader slack, model.js:248-254).
 static constexpr size_t kSlack = 256;
 
+// Pinned blocks of finished reads (eff_read_begin / eff_read_end), reused.
+// Shared by a context and its live read tickets; the last owner frees them.
+struct ReadPool {
+  std::mutex mu;
+  std::vector<std::pair<void *, size_t>> blocks;
+  ~ReadPool() {
+    for (auto &b : blocks) (void)hipHostFree(b.first);
+  }
+};
+
 struct eff_ctx {
   int device = 0;
   hipStream_t own = nullptr;
@@ -72,14 +83,15 @@ struct eff_ctx {
   size_t stage_head = 0;
   std::deque<Pend> stage_pend;
   std::vector<hipEvent_t> events;   // recorded and completed, ready for reuse
-  // Pinned blocks of finished reads (eff_read_begin / eff_read_end), reused.
-  std::mutex read_mu;
-  std::vector<std::pair<void *, size_t>> read_blocks;
+  std::shared_ptr<ReadPool> reads = std::make_shared<ReadPool>();
 };
 
-// An enqueued device -> host read (eff_read_begin).
+// An enqueued device -> host read (eff_read_begin). The ticket keeps the
+// device number and a reference to its context's pool of pinned blocks, never
+// the context itself: it may be waited for and released after eff_shutdown.
 struct eff_read {
-  eff_ctx *ctx = nullptr;
+  int device = 0;
+  std::shared_ptr<ReadPool> pool;
   void *host = nullptr;   // pinned block of `cap` bytes
   size_t cap = 0, n = 0;
   hipEvent_t ev = nullptr;
@@ -93,6 +105,15 @@ struct eff_buf {
   bool owned = false;
   int mark_type = 0;        // EFF_TYPE_Q8_0R when marked
   uint32_t mark_blocks = 0; // N of the tensor
+};
+
+// The launches of one recording (eff_graph_begin .. eff_graph_end), ready to
+// be replayed on a context's stream.
+struct eff_graph {
+  int device = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  size_t nodes = 0;
 };
 
 namespace {
@@ -122,6 +143,17 @@ int hip_fail(eff_ctx *ctx, hipError_t e, const char *what) {
 // Select the context's device for the calling thread.
 int use_device(eff_ctx *ctx) {
   EFF_HIP(ctx, hipSetDevice(ctx->device));
+  return EFF_OK;
+}
+
+// EFF_E_INVALID when the context's stream is being recorded into a graph:
+// for the calls that wait for the device, allocate or move host data, none
+// of which a replay could repeat.
+int refuse_capture(eff_ctx *ctx, const char *who) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  EFF_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(ctx, EFF_E_INVALID, "%s: not allowed while the stream is recorded into a graph", who);
   return EFF_OK;
 }
 
@@ -206,6 +238,11 @@ int run_gemv(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint3
 // first call of a shape must be eager).
 int grow(eff_ctx *ctx, void **p, size_t *have, size_t need, const char *what) {
   if (need <= *have) return EFF_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  EFF_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(ctx, EFF_E_INVALID, "%s scratch of %zu bytes: it cannot grow while the stream is recorded into a "
+                "graph; run the largest call of this shape once before the recording", what, need);
   if (*p) {
     EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
     (void)hipFree(*p);
@@ -334,7 +371,7 @@ int eff_shutdown(eff_ctx *ctx) {
   for (auto &p : ctx->stage_pend) (void)hipEventDestroy(p.ev);
   for (hipEvent_t ev : ctx->events) (void)hipEventDestroy(ev);
   if (ctx->stage) (void)hipHostFree(ctx->stage);
-  for (auto &b : ctx->read_blocks) (void)hipHostFree(b.first);
+  ctx->reads.reset();   // the pinned blocks go with the last live read ticket
   if (ctx->own) (void)hipStreamDestroy(ctx->own);
   delete ctx;
   return EFF_OK;
@@ -353,7 +390,7 @@ int eff_set_stream(eff_ctx *ctx, void *hip_stream) {
 int eff_sync(eff_ctx *ctx) {
   if (!ctx) return EFF_E_INVALID;
   int rc = use_device(ctx);
-  if (rc) return rc;
+  if (rc || (rc = refuse_capture(ctx, "sync"))) return rc;
   EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return EFF_OK;
 }
@@ -402,12 +439,18 @@ int eff_buf_alloc(eff_ctx *ctx, size_t bytes, eff_buf **out) {
   if (bytes == 0) return fail(ctx, EFF_E_INVALID, "buffer of 0 bytes");
   int rc = use_device(ctx);
   if (rc) return rc;
+  // A clear recorded into a graph would be replayed with it (and memset nodes
+  // are avoided in captured graphs): buffers are made outside a recording.
+  if ((rc = refuse_capture(ctx, "alloc"))) return rc;
+  // Stream-ordered allocation from the device's memory pool, so that a
+  // buffer can also be given back in stream order (eff_buf_retire).
   void *p = nullptr;
-  if (hipMalloc(&p, bytes + kSlack) != hipSuccess) return fail(ctx, EFF_E_NOMEM, "hipMalloc of %zu bytes failed", bytes + kSlack);
+  if (hipMallocAsync(&p, bytes + kSlack, ctx->stream) != hipSuccess)
+    return fail(ctx, EFF_E_NOMEM, "allocation of %zu bytes failed", bytes + kSlack);
   // The clear is ordered on the context's stream: every later operation on
   // that stream sees zeros, and the host does not wait.
   if (hipMemsetAsync(p, 0, bytes + kSlack, ctx->stream) != hipSuccess) {
-    (void)hipFree(p);
+    (void)hipFreeAsync(p, ctx->stream);
     return fail(ctx, EFF_E_DEVICE, "clearing a new buffer failed");
   }
   eff_buf *b = new eff_buf();
@@ -431,9 +474,25 @@ int eff_buf_wrap(eff_ctx *ctx, void *device_ptr, size_t bytes, eff_buf **out) {
 int eff_buf_free(eff_ctx *ctx, eff_buf *buf) {
   if (!ctx || !buf) return EFF_E_INVALID;
   if (buf->owned) {
-    use_device(ctx);
-    (void)hipStreamSynchronize(ctx->stream);
-    (void)hipFree(buf->ptr);
+    // the work of every stream of the device ends first, so nothing still
+    // reads the memory when the pool may hand it out again
+    int rc = use_device(ctx);
+    if (rc || (rc = refuse_capture(ctx, "free"))) return rc;
+    (void)hipDeviceSynchronize();
+    (void)hipFreeAsync(buf->ptr, ctx->stream);
+  }
+  delete buf;
+  return EFF_OK;
+}
+
+int eff_buf_retire(eff_ctx *ctx, eff_buf *buf) {
+  if (!ctx || !buf) return EFF_E_INVALID;
+  if (buf->owned) {
+    int rc = use_device(ctx);
+    if (rc || (rc = refuse_capture(ctx, "retire"))) return rc;
+    // given back in stream order: the pool reuses the memory only after the
+    // work enqueued before this call on the context's stream has run
+    EFF_HIP(ctx, hipFreeAsync(buf->ptr, ctx->stream));
   }
   delete buf;
   return EFF_OK;
@@ -448,10 +507,7 @@ int eff_buf_write(eff_ctx *ctx, eff_buf *buf, size_t off, const void *src, size_
   if (!n) return EFF_OK;
   int rc = use_device(ctx);
   if (rc) return rc;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  EFF_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cs));
-  if (cs != hipStreamCaptureStatusNone)
-    return fail(ctx, EFF_E_INVALID, "write: host data cannot be written into a stream under graph capture");
+  if ((rc = refuse_capture(ctx, "write"))) return rc;
   char *dst = (char *)buf->ptr + off;
   if (n > kStageMaxWrite) {
     // Large uploads (weights at load time): the copy is waited for, so `src`
@@ -471,7 +527,7 @@ int eff_buf_read(eff_ctx *ctx, eff_buf *buf, size_t off, void *dst, size_t n) {
   if (!ctx || !buf || (!dst && n)) return EFF_E_INVALID;
   if (off > buf->size || n > buf->size - off) return fail(ctx, EFF_E_BOUNDS, "read of %zu bytes at %zu past a %zu-byte buffer", n, off, buf->size);
   int rc = use_device(ctx);
-  if (rc) return rc;
+  if (rc || (rc = refuse_capture(ctx, "read"))) return rc;
   if (n) EFF_HIP(ctx, hipMemcpyAsync(dst, (const char *)buf->ptr + off, n, hipMemcpyDeviceToHost, ctx->stream));
   EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return EFF_OK;
@@ -482,17 +538,19 @@ int eff_read_begin(eff_ctx *ctx, eff_buf *buf, size_t off, size_t n, eff_read **
   *out = nullptr;
   if (off > buf->size || n > buf->size - off) return fail(ctx, EFF_E_BOUNDS, "read of %zu bytes at %zu past a %zu-byte buffer", n, off, buf->size);
   int rc = use_device(ctx);
-  if (rc) return rc;
+  if (rc || (rc = refuse_capture(ctx, "readback"))) return rc;
   eff_read *r = new eff_read();
-  r->ctx = ctx;
+  r->device = ctx->device;
+  r->pool = ctx->reads;
   r->n = n;
   {
-    std::lock_guard<std::mutex> lk(ctx->read_mu);
-    for (size_t i = 0; i < ctx->read_blocks.size(); ++i) {
-      if (ctx->read_blocks[i].second >= n) {
-        r->host = ctx->read_blocks[i].first;
-        r->cap = ctx->read_blocks[i].second;
-        ctx->read_blocks.erase(ctx->read_blocks.begin() + i);
+    std::lock_guard<std::mutex> lk(r->pool->mu);
+    auto &blocks = r->pool->blocks;
+    for (size_t i = 0; i < blocks.size(); ++i) {
+      if (blocks[i].second >= n) {
+        r->host = blocks[i].first;
+        r->cap = blocks[i].second;
+        blocks.erase(blocks.begin() + i);
         break;
       }
     }
@@ -517,7 +575,7 @@ int eff_read_begin(eff_ctx *ctx, eff_buf *buf, size_t off, size_t n, eff_read **
 
 int eff_read_end(eff_read *r, void *dst) {
   if (!r || (!dst && r->n)) return EFF_E_INVALID;
-  hipError_t e = hipSetDevice(r->ctx->device);
+  hipError_t e = hipSetDevice(r->device);
   if (e == hipSuccess) e = hipEventSynchronize(r->ev);
   if (e != hipSuccess) {
     r->rc = EFF_E_DEVICE;
@@ -532,16 +590,16 @@ const char *eff_read_error(const eff_read *r) { return r ? r->error.c_str() : "n
 
 int eff_read_release(eff_read *r) {
   if (!r) return EFF_E_INVALID;
-  (void)hipSetDevice(r->ctx->device);
+  (void)hipSetDevice(r->device);
   if (r->ev) {
     (void)hipEventSynchronize(r->ev);
     (void)hipEventDestroy(r->ev);
   }
   if (r->host) {
-    std::lock_guard<std::mutex> lk(r->ctx->read_mu);
-    r->ctx->read_blocks.push_back({r->host, r->cap});
+    std::lock_guard<std::mutex> lk(r->pool->mu);
+    r->pool->blocks.push_back({r->host, r->cap});
   }
-  delete r;
+  delete r;   // the pool goes with its last owner (context or ticket)
   return EFF_OK;
 }
 
@@ -580,7 +638,7 @@ int eff_buf_write_r(eff_ctx *ctx, eff_buf *buf, int type_r, uint32_t first_block
   std::string tmp(eff_bytes_reordered(type_r, n_blocks), '\0');  // 34 n rounded up to a word
   int rc = eff_repack(type_r, src, n_blocks, &tmp[0], tmp.size());
   if (rc) return fail(ctx, rc, "write R: repack failed");
-  if ((rc = use_device(ctx))) return rc;
+  if ((rc = use_device(ctx)) || (rc = refuse_capture(ctx, "write R"))) return rc;
   char *base = (char *)buf->ptr;
   EFF_HIP(ctx, hipMemcpyAsync(base + (size_t)32 * first_block, tmp.data(), (size_t)32 * n_blocks,
                               hipMemcpyHostToDevice, ctx->stream));
@@ -877,17 +935,7 @@ int eff_topk(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uint3
   int rc = topk_check(ctx, logits, base, vocab, m, penal_ids, n_penal, out, "topk");
   if (rc) return rc;
   if ((rc = use_device(ctx))) return rc;
-  size_t need = topk_scratch_bytes(vocab);
-  if (need > ctx->topk_scratch_bytes) {
-    if (ctx->topk_scratch) {
-      EFF_HIP(ctx, hipStreamSynchronize(ctx->stream));
-      (void)hipFree(ctx->topk_scratch);
-      ctx->topk_scratch = nullptr;
-      ctx->topk_scratch_bytes = 0;
-    }
-    if (hipMalloc(&ctx->topk_scratch, need) != hipSuccess) return fail(ctx, EFF_E_NOMEM, "topk scratch of %zu bytes", need);
-    ctx->topk_scratch_bytes = need;
-  }
+  if ((rc = grow(ctx, &ctx->topk_scratch, &ctx->topk_scratch_bytes, topk_scratch_bytes(vocab), "topk"))) return rc;
   hipError_t e = launch_topk((const uint32_t *)logits->ptr, base, vocab, m, penal_ids, n_penal, serial,
                              (uint32_t *)ctx->topk_scratch, (uint32_t *)out->ptr, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "topk launch");
@@ -923,6 +971,64 @@ int eff_qgemv_topk(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, u
   }
   ++ctx->stats.gemv;
   ++ctx->stats.topk;
+  return EFF_OK;
+}
+
+int eff_graph_begin(eff_ctx *ctx) {
+  if (!ctx) return EFF_E_INVALID;
+  int rc = use_device(ctx);
+  if (rc || (rc = refuse_capture(ctx, "graph begin"))) return rc;
+  // thread-local: only calls from this thread that could not be recorded
+  // (waits, allocations) are refused while recording
+  EFF_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+  return EFF_OK;
+}
+
+int eff_graph_end(eff_ctx *ctx, eff_graph **out) {
+  if (!ctx || !out) return EFF_E_INVALID;
+  *out = nullptr;
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  EFF_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+  if (cs == hipStreamCaptureStatusNone) return fail(ctx, EFF_E_INVALID, "graph end: no recording is open");
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+  if (e != hipSuccess) {
+    if (g) (void)hipGraphDestroy(g);
+    return hip_fail(ctx, e, "graph end (a call made during the recording invalidated it)");
+  }
+  eff_graph *gr = new eff_graph();
+  gr->device = ctx->device;
+  gr->graph = g;
+  e = hipGraphGetNodes(g, nullptr, &gr->nodes);
+  if (e == hipSuccess) e = hipGraphInstantiate(&gr->exec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    eff_graph_destroy(gr);
+    return hip_fail(ctx, e, "graph instantiate");
+  }
+  *out = gr;
+  return EFF_OK;
+}
+
+int eff_graph_launch(eff_ctx *ctx, eff_graph *g) {
+  if (!ctx || !g) return EFF_E_INVALID;
+  if (g->device != ctx->device)
+    return fail(ctx, EFF_E_INVALID, "graph launch: recorded on device %d, the context is on %d", g->device, ctx->device);
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  EFF_HIP(ctx, hipGraphLaunch(g->exec, ctx->stream));
+  return EFF_OK;
+}
+
+size_t eff_graph_nodes(const eff_graph *g) { return g ? g->nodes : 0; }
+
+int eff_graph_destroy(eff_graph *g) {
+  if (!g) return EFF_E_INVALID;
+  (void)hipSetDevice(g->device);
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  delete g;
   return EFF_OK;
 }
 

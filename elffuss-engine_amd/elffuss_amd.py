@@ -74,6 +74,12 @@ def lib():
         "eff_buf_alloc": ([p, sz, ctypes.POINTER(p)], i32),
         "eff_buf_wrap": ([p, p, sz, ctypes.POINTER(p)], i32),
         "eff_buf_free": ([p, p], i32),
+        "eff_buf_retire": ([p, p], i32),
+        "eff_graph_begin": ([p], i32),
+        "eff_graph_end": ([p, ctypes.POINTER(p)], i32),
+        "eff_graph_launch": ([p, p], i32),
+        "eff_graph_nodes": ([p], sz),
+        "eff_graph_destroy": ([p], i32),
         "eff_buf_size": ([p], sz),
         "eff_buf_device_ptr": ([p], p),
         "eff_buf_write": ([p, p, sz, p, sz], i32),
@@ -119,7 +125,8 @@ def lib():
 
 EXPORTED = ("eff_type_from_name eff_type_name eff_type_geometry eff_init eff_shutdown eff_last_error "
             "eff_stream eff_set_stream eff_sync eff_set_option eff_get_stats eff_buf_alloc eff_buf_wrap "
-            "eff_buf_free eff_buf_size eff_buf_device_ptr eff_buf_write eff_buf_read eff_buf_copy "
+            "eff_buf_free eff_buf_retire eff_graph_begin eff_graph_end eff_graph_launch eff_graph_nodes "
+            "eff_graph_destroy eff_buf_size eff_buf_device_ptr eff_buf_write eff_buf_read eff_buf_copy "
             "eff_read_begin eff_read_end eff_read_error eff_read_release "
             "eff_bytes_reordered eff_bytes_buffer_r eff_blocks_from_buffer eff_scales_from eff_buf_mark_r "
             "eff_buf_blocks_r eff_buf_write_r eff_repack eff_unrepack eff_quantize eff_fill_normal eff_qmatmul eff_qgemv "
@@ -239,6 +246,31 @@ class Buffer:
             lib().eff_buf_free(self.ctx.h, self.handle)
             self.handle = None
 
+    def retire(self):
+        """Give the buffer back in stream order, without waiting (eff_buf_retire)."""
+        if self.handle:
+            self.ctx._check(lib().eff_buf_retire(self.ctx.h, self.handle))
+            self.handle = None
+
+
+class Graph:
+    """Launches recorded between Context.graph_begin() and graph_end()."""
+
+    def __init__(self, ctx, handle):
+        self.ctx, self.handle = ctx, handle
+
+    @property
+    def nodes(self):
+        return lib().eff_graph_nodes(self.handle)
+
+    def launch(self):
+        self.ctx._check(lib().eff_graph_launch(self.ctx.h, self.handle))
+
+    def destroy(self):
+        if self.handle:
+            lib().eff_graph_destroy(self.handle)
+            self.handle = None
+
 
 class Context:
     """One HIP device context and its stream (eff_init)."""
@@ -277,6 +309,15 @@ class Context:
 
     def sync(self):
         self._check(lib().eff_sync(self.h))
+
+    def graph_begin(self):
+        """Record (not run) the launches enqueued from now on (eff_graph_begin)."""
+        self._check(lib().eff_graph_begin(self.h))
+
+    def graph_end(self):
+        g = ctypes.c_void_p()
+        self._check(lib().eff_graph_end(self.h, ctypes.byref(g)))
+        return Graph(self, g)
 
     def set_option(self, opt, value):
         self._check(lib().eff_set_option(self.h, opt, value))

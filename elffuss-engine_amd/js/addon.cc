@@ -294,6 +294,57 @@ napi_value BufFree(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// GPUBuffer.destroy(): given back in stream order, no wait (eff_buf_retire).
+napi_value BufRetire(napi_env env, napi_callback_info info) {
+  napi_value a[2];
+  get_args(env, info, 2, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  int rc = eff_buf_retire(ctx, external<eff_buf>(env, a[1]));
+  if (rc) return throw_msg(env, ctx ? eff_last_error(ctx) : "retire", rc);
+  return undefined(env);
+}
+
+// Recorded launches (eff_graph_*): graphBegin(ctx); graphEnd(ctx) -> external;
+// graphLaunch(ctx, g); graphNodes(g) -> number; graphDestroy(g).
+napi_value GraphBegin(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  get_args(env, info, 1, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  return status(env, ctx, eff_graph_begin(ctx));
+}
+
+napi_value GraphEnd(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  get_args(env, info, 1, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  eff_graph *g = nullptr;
+  int rc = eff_graph_end(ctx, &g);
+  if (rc) return throw_msg(env, ctx ? eff_last_error(ctx) : "graph end", rc);
+  napi_value ext;
+  napi_create_external(env, g, nullptr, nullptr, &ext);
+  return ext;
+}
+
+napi_value GraphLaunch(napi_env env, napi_callback_info info) {
+  napi_value a[2];
+  get_args(env, info, 2, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  return status(env, ctx, eff_graph_launch(ctx, external<eff_graph>(env, a[1])));
+}
+
+napi_value GraphNodes(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  get_args(env, info, 1, a);
+  return make_int(env, (int64_t)eff_graph_nodes(external<eff_graph>(env, a[0])));
+}
+
+napi_value GraphDestroy(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  get_args(env, info, 1, a);
+  eff_graph_destroy(external<eff_graph>(env, a[0]));
+  return undefined(env);
+}
+
 napi_value BufWrite(napi_env env, napi_callback_info info) {
   napi_value a[4];
   get_args(env, info, 4, a);
@@ -546,7 +597,9 @@ napi_value Register(napi_env env, napi_value exports) {
       {"bufAlloc", BufAlloc}, {"bufFree", BufFree}, {"bufWrite", BufWrite}, {"bufRead", BufRead},
       {"bufReadAsync", BufReadAsync}, {"bufSize", BufSize}, {"bufMarkR", BufMarkR}, {"bufBlocksR", BufBlocksR}, {"bufWriteR", BufWriteR},
       {"qmatmul", QMatmul}, {"qgemv", QGemv}, {"qgemvMulti", QGemvMulti}, {"qgemm", QGemm}, {"qgemmPlanned", QGemmPlanned}, {"dequant", Dequant}, {"gather", Gather}, {"gatherNorm", GatherNorm}, {"topk", TopK}, {"qgemvTopk", QGemvTopK},
-      {"topkOutBytes", TopKOutBytes},
+      {"topkOutBytes", TopKOutBytes}, {"bufRetire", BufRetire}, {"graphBegin", GraphBegin},
+      {"graphEnd", GraphEnd}, {"graphLaunch", GraphLaunch}, {"graphNodes", GraphNodes},
+      {"graphDestroy", GraphDestroy},
   };
   for (auto &f : fns) {
     napi_value v;

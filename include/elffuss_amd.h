@@ -76,6 +76,7 @@ extern "C" {
 typedef struct eff_ctx eff_ctx;
 typedef struct eff_buf eff_buf;
 typedef struct eff_read eff_read;
+typedef struct eff_graph eff_graph;
 
 /* Dispatch counters: lets a caller assert that a fast path really ran
  * (ops.gemv.js:92-95 `hechos`, ops.topk.js:36-40 `estadisticasTopK`). */
@@ -111,7 +112,9 @@ int eff_type_geometry(int type, uint32_t *block_elems, uint32_t *block_bytes);
  * Replaces requestDevice + createOps (device.js:66-139, ops.js:1604-1633). */
 int eff_init(int device, eff_ctx **out);
 
-/* Release the context, its stream (if owned) and its scratch memory. */
+/* Release the context, its stream (if owned) and its scratch memory, after
+ * the work on its stream has ended. Read tickets still open (eff_read_begin)
+ * stay valid: they may be ended and released afterwards. */
 int eff_shutdown(eff_ctx *ctx);
 
 /* Message of the last error on this context ("" if none). */
@@ -133,20 +136,54 @@ int eff_set_option(eff_ctx *ctx, int option, int64_t value);
 /* Dispatch counters since eff_init. */
 int eff_get_stats(const eff_ctx *ctx, eff_stats *out);
 
+/* ---- recorded launches (the MI355X form of ctx.batch / ctx.corta) -------- */
+
+/* The reference records a layer's (or a token's) dispatches into one compute
+ * pass and submits them together (ctx.batch, ops.js:311-332; ctx.corta,
+ * ops.js:342-348). Here the launches enqueued on the context's stream between
+ * eff_graph_begin and eff_graph_end are recorded, not run, into a HIP graph;
+ * eff_graph_launch replays them, in order, on the context's stream without
+ * waiting, any number of times, with the same buffers and shapes (new inputs
+ * are written into the same buffers between replays). While recording, the
+ * calls that wait, allocate or move host data (eff_sync, eff_buf_alloc,
+ * eff_buf_free, eff_buf_retire, eff_buf_write, eff_buf_write_r, eff_buf_read,
+ * eff_read_begin, and an op whose scratch would have to grow) return
+ * EFF_E_INVALID and leave the recording open. An op's scratch is grown by
+ * its first call of a shape outside a recording. */
+int eff_graph_begin(eff_ctx *ctx);
+int eff_graph_end(eff_ctx *ctx, eff_graph **out);
+int eff_graph_launch(eff_ctx *ctx, eff_graph *g);
+/* Launches (graph nodes) a recording holds. */
+size_t eff_graph_nodes(const eff_graph *g);
+int eff_graph_destroy(eff_graph *g);
+
 /* ---- device buffers ------------------------------------------------------ */
 
 /* Allocate `bytes` of device memory (plus hidden read slack; the reference's
- * loader leaves 4 bytes after every tensor, model.js:248-254). Contents are
- * zero for every later operation on the context's stream: the clear is
- * enqueued there and the host does not wait. Replaces device.createBuffer
- * behind the ctx.alloc pool (ops.js:233-281), which the JS host keeps. */
+ * loader leaves 4 bytes after every tensor, model.js:248-254) from the
+ * device's stream-ordered memory pool. Contents are zero for every later
+ * operation on the context's stream: the clear is enqueued there and the host
+ * does not wait. Refused (EFF_E_INVALID) while the stream is under graph
+ * capture. Replaces device.createBuffer behind the ctx.alloc pool
+ * (ops.js:233-281), which the JS host keeps. */
 int eff_buf_alloc(eff_ctx *ctx, size_t bytes, eff_buf **out);
 
 /* Wrap caller-owned device memory of `bytes` bytes (not freed by
  * eff_buf_free). The caller must leave at least 16 readable bytes after it. */
 int eff_buf_wrap(eff_ctx *ctx, void *device_ptr, size_t bytes, eff_buf **out);
 
+/* Free a buffer after the work of every stream of the device has ended
+ * (a device wait). */
 int eff_buf_free(eff_ctx *ctx, eff_buf *buf);
+
+/* Free a buffer in stream order, without waiting: the memory goes back to
+ * the pool once the work enqueued before this call on the context's stream
+ * has run, and the handle is invalid on return. The caller guarantees that
+ * no work on another stream still reads the buffer. Replaces
+ * GPUBuffer.destroy(), which is safe with work already submitted (the pool's
+ * destruction of unused size classes, ops.js:264-279). Refused
+ * (EFF_E_INVALID) while the stream is under graph capture. */
+int eff_buf_retire(eff_ctx *ctx, eff_buf *buf);
 size_t eff_buf_size(const eff_buf *buf);
 void *eff_buf_device_ptr(const eff_buf *buf);
 

@@ -154,14 +154,15 @@ def test_gemv_non_finite_x(ctx, eff, gemv_kernel, tname):
 # ---- the row GEMV for Q6_K matrices with many rows (the output projection) -------------
 
 @pytest.mark.parametrize("rows,k", [(32768, 512), (32805, 4608), (40001, 2048), (32769, 8192), (32800, 2304),
-                                      (33000, 768), (140001, 2048)])
+                                      (33000, 768), (140001, 2048), (32800, 1024), (40001, 1536)])
 def test_gemv_rows_q6_k_vs_f64_oracle(ctx, eff, orc, rows, k):
     """One token of a Q6_K matrix of >= 32768 rows runs the row kernel (a lane
     per half row-block): row counts that are not a multiple of the workgroups'
     rows (128 on average, 224 and 32 in the two halves of the grid from 8
     blocks per row), an odd number of blocks per row (block starts at both
-    2-byte alignments in every column), k up to 32 blocks, and more workgroups
-    (1096) than the GPU holds at once."""
+    2-byte alignments in every column), k up to 32 blocks, more workgroups
+    (1096) than the GPU holds at once, and the 4-slice form (k of 4 to 7
+    blocks: 1024 and 1536)."""
     t, data, gguf, n = make_weights(eff, "Q6_K", rows, k, rows + k)
     x = eff.fill_normal(rows + 1, 1.0, k)
     wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(rows * 4)
@@ -758,6 +759,8 @@ def test_topk_clustered_in_one_group(ctx, eff, orc, vocab, m):
     ("Q6_K", 40000, 2304, 40, 0),          # an odd block count per row (per-row load offsets)
     ("Q6_K", 131072, 512, 64, 0),          # 1024 groups, the most one selection holds (two per thread)
     ("Q6_K", 131073, 512, 40, 0),          # more groups than one selection holds: GEMV, then eff_topk
+    ("Q6_K", 65536, 1024, 40, 0),          # 4 k slices per row group (k of 4 to 7 blocks)
+    ("Q6_K", 65536, 1280, 100, 30000),     # ... with an odd block count
     ("Q8_0", 50000, 512, 40, 0),           # no row kernel: GEMV, then eff_topk
 ])
 def test_qgemv_topk_equals_gemv_then_topk(ctx, eff, orc, tname, rows, k, m, cluster):

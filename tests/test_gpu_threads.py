@@ -2,7 +2,11 @@
 buffers), running products and top-ks at the same time: every output has the
 bits of the same call made alone. The calls go through ctypes, which releases
 the interpreter lock, so the library's shared state (the per-device kernel
-attributes, the no-alloc scratch lookup) is reached from both threads at once."""
+attributes) is reached from both threads at once, and each context's own
+scratch (the split-x x parts, the GEMM's fp16 x, the top-k records, and the
+head's records written by the row GEMV) is used concurrently with the other
+context's. The no-alloc top-k is left out: its fixed scratch is shared by every
+context of a GPU, and calls that overlap race by design."""
 import threading
 
 import numpy as np
@@ -28,6 +32,14 @@ def run_cases(eff, ctx, inputs, rounds):
         outs.append([yb.read(np.uint32) for _, _, yb in bufs])
         lb = bufs[-1][2]
         outs[-1].append(ctx.topk(lb, 0, CASES[-1][1], 40, [5], serial=3).read(np.uint32))
+        # the decode head: the row GEMV writing its records into this context's scratch, then the selection
+        wb, xb, _ = bufs[-1]
+        yh = ctx.alloc(CASES[-1][1] * 4)
+        rec = ctx.qgemv_topk(eff.TYPES["Q6_K"], wb, xb, yh, CASES[-1][1], CASES[-1][2], 40, [5], serial=3)
+        outs[-1].append(rec.read(np.uint32))
+        outs[-1].append(yh.read(np.uint32))
+        rec.free()
+        yh.free()
     for b in bufs:
         for x in b:
             x.free()
