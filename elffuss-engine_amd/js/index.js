@@ -56,9 +56,12 @@ class DeviceBuffer {
     this._h = native.bufAlloc(device._ctx, size);
     this._alive = true;
   }
+  // Like GPUBuffer.destroy(), safe with work already submitted and without a
+  // wait: the memory goes back in stream order (eff_buf_retire), after the
+  // work enqueued before on the context's stream.
   destroy() {
     if (this._alive) {
-      native.bufFree(this.device._ctx, this._h);
+      native.bufRetire(this.device._ctx, this._h);
       this._alive = false;
     }
   }
@@ -187,6 +190,64 @@ function createContext(device) {
     }
     ctx.scratch.length = marca;
     for (const e of quedan) ctx.scratch.push(e);
+  };
+  // A buffer lent by the last alloc() of this size goes back at once (an
+  // operation that found it does not apply after lending its output).
+  ctx.suelta = function (buf) {
+    for (let i = ctx.scratch.length - 1; i >= 0; i--) {
+      if (ctx.scratch[i].buf !== buf) continue;
+      const e = ctx.scratch.splice(i, 1)[0];
+      ctx.vivosBytes -= e.size;
+      devuelve(e);
+      return;
+    }
+  };
+  // Records what `fn` enqueues into a HIP graph, to replay it per token: the
+  // MI355X form of ctx.batch (ops.js:311-332), whose one submit per batch is
+  // here one graph launch per replay, with the host's per-launch cost paid
+  // once at recording. `fn` (async, device work only: no readback, no upload)
+  // runs first eagerly once, a rehearsal that creates the pool's buffers and
+  // the library's scratch for these shapes and whose outputs the first replay
+  // overwrites, and is then recorded. The buffers it takes from the pool
+  // belong to the recording until destroy(); its inputs stay where they
+  // were, so new values are written into the same buffers before each
+  // lanza(). Resolves to { salida (what the recorded run of fn returned),
+  // nodos, lanza(), destroy() }.
+  ctx.grabaGrafo = async function (fn) {
+    if (ctx._grabando) throw new Error('grabaGrafo: ya hay una grabación abierta');
+    const marca = ctx.scratch.length;
+    await fn();
+    ctx.recycleDesde(marca);
+    native.graphBegin(device._ctx);
+    ctx._grabando = true;
+    let salida;
+    try {
+      salida = await fn();
+    } catch (e) {
+      try { native.graphDestroy(native.graphEnd(device._ctx)); } catch (_) { /* the recording is gone */ }
+      ctx._grabando = false;
+      ctx.recycleDesde(marca);
+      throw e;
+    }
+    ctx._grabando = false;
+    const g = native.graphEnd(device._ctx);
+    const propios = ctx.scratch.splice(marca);
+    for (const e of propios) ctx.vivosBytes -= e.size;
+    let vivo = true;
+    return {
+      salida,
+      nodos: native.graphNodes(g),
+      lanza() {
+        if (!vivo) throw new Error('grabaGrafo: el grafo ya se destruyó');
+        native.graphLaunch(device._ctx, g);
+      },
+      destroy() {
+        if (!vivo) return;
+        vivo = false;
+        native.graphDestroy(g);
+        for (const e of propios) devuelve(e);
+      },
+    };
   };
   // Destroys every pooled and lent buffer (end of the session).
   ctx.destroy = function () {
@@ -438,30 +499,60 @@ async function cargaTensores(device, ranged, tensores, opciones) {
 
 // ---- operators ---------------------------------------------------------------
 
-// createGemvOps (ops.gemv.js:44-221): the decode GEMV, null when it does not apply.
+// createGemvOps (ops.gemv.js:44-221): the decode GEMV, null when it does not
+// apply. It applies where the reference's GEMV2 does (`prepara`,
+// ops.gemv.js:111-135): the types of GEMV2_TIPOS that exist here (Q8_0,
+// Q8_0R, Q6_K; kernels.gemv.wgsl.js:83-91), 1 to GEMV2_MAX_TOKENS = 3 tokens
+// (kernels.gemv.wgsl.js:79), k a whole number of blocks and, for Q8_0R, a
+// buffer whose mark passes compruebaBufferR (else null, and quant.matmul
+// throws with its reason). `deps.ampliado` widens it to every type of this
+// library and, for matmul, to 8 tokens. Applicability is decided before
+// anything is lent from the pool.
+const GEMV2_TIPOS = new Set(['Q8_0', 'Q8_0R', 'Q6_K']);
+const GEMV2_MAX_TOKENS = 3;
+
 function createGemvOps(device, deps) {
   const ctx = deps.ctx;
+  const ampliado = deps.ampliado === true;
   const hechos = { matmul: 0, gateUp: 0, secciones: 0 };
+  // The type's entry when the call applies, else null (ops.gemv.js:111-135).
+  const prepara = (tipo, k, t, maxT, bufs, filas) => {
+    const i = QUANT_TYPES[tipo];
+    if (!i || !(ampliado || GEMV2_TIPOS.has(tipo))) return null;
+    if (!Number.isInteger(t) || t < 1 || t > maxT) return null;
+    if (!(k > 0) || k % i.blockElems !== 0) return null;
+    for (let j = 0; j < bufs.length; j++) {
+      if (!(filas[j] >= 1) || !bufs[j] || !(bufs[j].size > 0)) return null;
+      if (TIPOS_R.has(tipo)) {
+        try {
+          compruebaBufferR(tipo, bufs[j], { bloques: filas[j] * (k / i.blockElems) }, 'gemv2');
+        } catch (_) {
+          return null;
+        }
+      }
+    }
+    return i;
+  };
   return {
     matmul(tipo, wBuf, xBuf, rows, k, tokens) {
       const t = tokens === undefined ? 1 : tokens;
-      const i = QUANT_TYPES[tipo];
-      if (!i || !(t >= 1) || k % i.blockElems !== 0) return Promise.resolve(null);
+      const i = prepara(tipo, k, t, ampliado ? 8 : GEMV2_MAX_TOKENS, [wBuf], [rows]);
+      if (!i) return Promise.resolve(null);
       const y = ctx.alloc(rows * t * 4, 'matmul.y');
       const r = native.qgemv(device._ctx, i.code, wBuf._h, xBuf._h, y._h, rows, k, t);
-      if (r === null) return Promise.resolve(null);
+      if (r === null) { ctx.suelta(y); return Promise.resolve(null); }
       hechos.matmul++;
       return Promise.resolve(y);
     },
     // silu(W_gate·x)·(W_up·x) in one launch (ops.gemv.js:166-190).
     gateUp(tipo, wGate, wUp, xBuf, rows, k, tokens) {
       const t = tokens === undefined ? 1 : tokens;
-      const i = QUANT_TYPES[tipo];
-      if (!i || !(t >= 1) || k % i.blockElems !== 0) return Promise.resolve(null);
+      const i = prepara(tipo, k, t, GEMV2_MAX_TOKENS, [wGate, wUp], [rows, rows]);
+      if (!i) return Promise.resolve(null);
       const y = ctx.alloc(rows * t * 4, 'swiglu.out');
       const r = native.qgemvMulti(device._ctx, i.code, GEMV_MODE.SWIGLU, [wGate._h, wUp._h], xBuf._h, [y._h],
         [rows, rows], k, t);
-      if (r === null) return Promise.resolve(null);
+      if (r === null) { ctx.suelta(y); return Promise.resolve(null); }
       hechos.gateUp++;
       return Promise.resolve(y);
     },
@@ -469,13 +560,14 @@ function createGemvOps(device, deps) {
     // launch; the outputs in the order of the weights (ops.gemv.js:192-215).
     secciones(tipo, ws, xBuf, filas, k, tokens) {
       const t = tokens === undefined ? 1 : tokens;
-      const i = QUANT_TYPES[tipo];
       const n = ws.length;
-      if (!i || n < 2 || n > 4 || filas.length !== n || !(t >= 1) || k % i.blockElems !== 0) return Promise.resolve(null);
+      if (n < 2 || n > 4 || filas.length !== n) return Promise.resolve(null);
+      const i = prepara(tipo, k, t, GEMV2_MAX_TOKENS, ws, filas);
+      if (!i) return Promise.resolve(null);
       const ys = filas.map((f) => ctx.alloc(f * t * 4, 'matmul.y'));
       const r = native.qgemvMulti(device._ctx, i.code, GEMV_MODE.SECTIONS, ws.map((w) => w._h), xBuf._h,
         ys.map((y) => y._h), filas, k, t);
-      if (r === null) return Promise.resolve(null);
+      if (r === null) { for (let j = ys.length - 1; j >= 0; j--) ctx.suelta(ys[j]); return Promise.resolve(null); }
       hechos.secciones++;
       return Promise.resolve(ys);
     },
@@ -552,11 +644,12 @@ function createGemm2Ops(ctx) {
   return ops;
 }
 
-// createQuantOps (ops.js:748-1142).
+// createQuantOps (ops.js:748-1142). opts: { ctx, gemvAmpliado } (the
+// latter widens quant.gemv, see createGemvOps).
 function createQuantOps(device, opts) {
   const o = opts || {};
   const ctx = o.ctx || createContext(device);
-  const gemv = createGemvOps(device, { ctx });
+  const gemv = createGemvOps(device, { ctx, ampliado: o.gemvAmpliado === true });
   const gemm2 = createGemm2Ops(ctx);
   return {
     // Whole tensor -> f32, bit-exact with the reference decoders (ops.js:813-823).
@@ -711,7 +804,7 @@ function createTopKGPU(device, ctx) {
 module.exports = {
   native, STATUS, OPT, GEMV_MODE, TOPK, QUANT_TYPES, quantInfo,
   requestDevice, readback, createContext,
-  createQuantOps, createGemvOps, createGemm2Ops, GEMM2_TIPOS, createFusionOps, createTopKGPU, estadisticasTopK, TIPOS_GATHER_NORMA,
+  createQuantOps, createGemvOps, GEMV2_TIPOS, GEMV2_MAX_TOKENS, createGemm2Ops, GEMM2_TIPOS, createFusionOps, createTopKGPU, estadisticasTopK, TIPOS_GATHER_NORMA,
   TIPOS_R, TIPO_R, TIPO_GGUF, bytesReordenado, bytesBufferR, bloquesDeBuffer, escalasDesde,
   reordena, vuelveAlGGUF, marcaBufferR, bloquesR, compruebaBufferR, creaBufferR,
   tensorBytes, comoReordenado, subeReordenadoPorTrozos, cargaTensores,

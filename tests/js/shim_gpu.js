@@ -19,6 +19,8 @@ async function main() {
   const meta = JSON.parse(fs.readFileSync(path.join(dir, 'meta.json'), 'utf8'));
   const device = await eff.requestDevice();
   const ops = eff.createQuantOps(device);
+  // the same context with quant.gemv widened to every type (and matmul to 8 tokens)
+  const amp = eff.createQuantOps(device, { ctx: ops.ctx, gemvAmpliado: true });
   const out = {};
   const rd = async (buf, n) => new Float32Array(await eff.readback(device, buf, 0, n * 4));
   for (const c of meta.cases) {
@@ -38,20 +40,27 @@ async function main() {
     const xBuf = ops.upload(x, 'x');
     const y = await ops.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens);
     out[c.name] = Array.from(await rd(y, c.rows * c.tokens));
+    // quant.gemv applies where the reference's GEMV2 does (Q8_0, Q8_0R, Q6_K; 1-3 tokens)
+    const gemv2 = eff.GEMV2_TIPOS.has(c.type) && c.tokens <= eff.GEMV2_MAX_TOKENS;
     if (c.tokens <= 3) {
       // the fused forms over the same matrix twice: silu(y) * y, and [y, y]
-      const ysw = await ops.gemv.gateUp(c.type, wBuf, wBuf, xBuf, c.rows, c.k, c.tokens);
+      const g = gemv2 ? ops.gemv : amp.gemv;
+      const ysw = await g.gateUp(c.type, wBuf, wBuf, xBuf, c.rows, c.k, c.tokens);
       out[c.name + ':gateup'] = Array.from(await rd(ysw, c.rows * c.tokens));
-      const ys = await ops.gemv.secciones(c.type, [wBuf, wBuf], xBuf, [c.rows, c.rows], c.k, c.tokens);
+      const ys = await g.secciones(c.type, [wBuf, wBuf], xBuf, [c.rows, c.rows], c.k, c.tokens);
       out[c.name + ':sec0'] = Array.from(await rd(ys[0], c.rows * c.tokens));
       out[c.name + ':sec1'] = Array.from(await rd(ys[1], c.rows * c.tokens));
-      assert.strictEqual(await ops.gemv.secciones(c.type, [wBuf], xBuf, [c.rows], c.k, c.tokens), null);
+      assert.strictEqual(await g.secciones(c.type, [wBuf], xBuf, [c.rows], c.k, c.tokens), null);
+    }
+    if (!gemv2) {
+      assert.strictEqual(await ops.gemv.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens), null);
+      assert.strictEqual(await ops.gemv.gateUp(c.type, wBuf, wBuf, xBuf, c.rows, c.k, c.tokens), null);
     }
     if (c.tokens <= 8) {
-      const yg = await ops.gemv.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens);
+      const yg = await (gemv2 ? ops.gemv : amp.gemv).matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens);
       out[c.name + ':gemv'] = Array.from(await rd(yg, c.rows * c.tokens));
     } else {
-      assert.strictEqual(await ops.gemv.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens), null);
+      assert.strictEqual(await amp.gemv.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens), null);
     }
     if (c.tokens >= 64) {
       const ym = await ops.gemm2.matmul(c.type, wBuf, xBuf, c.rows, c.k, c.tokens);

@@ -1,0 +1,146 @@
+'use strict';
+// GPU run of the JavaScript host's recorded launches and pool behaviour:
+//   * gemv ops answer null where the reference's GEMV2 does (types outside
+//     GEMV2_TIPOS, more than 3 tokens, an unmarked Q8_0R buffer), lending
+//     nothing from the pool; `gemvAmpliado` widens them;
+//   * ctx.recycle() destroys an expired size class without waiting for the
+//     device (the work enqueued before it still runs, and gives its result);
+//   * ctx.grabaGrafo records a chain of quant.matmul calls, and each replay,
+//     after new x is written, gives the bits of the same chain run eagerly.
+// Prints one JSON line with the figures the Python side checks.
+const assert = require('assert');
+const path = require('path');
+const eff = require(path.join(__dirname, '..', '..', 'elffuss-engine_amd', 'js', 'index.js'));
+
+const ahora = () => Number(process.hrtime.bigint()) / 1e3;   // microseconds
+
+async function main() {
+  const device = await eff.requestDevice();
+  const ops = eff.createQuantOps(device);
+  const ctx = ops.ctx;
+  const out = {};
+  const rd = async (buf, n) => new Uint32Array(await eff.readback(device, buf, 0, n * 4));
+
+  // ---- GEMV2 applicability ---------------------------------------------------
+  {
+    const rows = 64, k = 512;
+    const x = ops.upload(eff.fillNormal(5, 1.0, 4 * k), 'x');
+    const w4 = ops.upload(eff.quantize('Q4_K', eff.fillNormal(6, 0.02, rows * k)), 'w4');
+    const w8 = ops.upload(eff.quantize('Q8_0', eff.fillNormal(7, 0.02, rows * k)), 'w8');
+    const n = rows * k / 32;
+    const wr = device.createBuffer({ size: eff.bytesBufferR('Q8_0R', n), label: 'wr' });
+    device.queue.writeBuffer(wr, 0, eff.reordena('Q8_0', eff.quantize('Q8_0', eff.fillNormal(7, 0.02, rows * k)), n));
+    const prestados = ctx.scratch.length;
+    const nulos = [
+      await ops.gemv.matmul('Q4_K', w4, x, rows, k, 1),
+      await ops.gemv.matmul('Q8_0', w8, x, rows, k, 4),
+      await ops.gemv.matmul('Q8_0R', wr, x, rows, k, 1),          // unmarked
+      await ops.gemv.gateUp('Q4_K', w4, w4, x, rows, k, 1),
+      await ops.gemv.secciones('Q2_K', [w4, w4], x, [rows, rows], k, 1),
+      await ops.gemv.gateUp('Q8_0', w8, w8, x, rows, k, 4),
+    ];
+    assert.ok(nulos.every((v) => v === null));
+    assert.strictEqual(ctx.scratch.length, prestados);   // nothing was lent
+    assert.throws(() => ops.matmul('Q8_0R', wr, x, rows, k, 1), /marca/);
+    eff.marcaBufferR(wr, 'Q8_0R', n);
+    const a = await ops.gemv.matmul('Q8_0R', wr, x, rows, k, 3);
+    const b = await ops.gemv.matmul('Q8_0', w8, x, rows, k, 3);
+    assert.deepStrictEqual(Array.from(await rd(a, 3 * rows)), Array.from(await rd(b, 3 * rows)));
+    const amp = eff.createQuantOps(device, { ctx, gemvAmpliado: true });
+    const c = await amp.gemv.matmul('Q4_K', w4, x, rows, k, 4);
+    const d = await ops.matmul('Q4_K', w4, x, rows, k, 4);
+    assert.deepStrictEqual(Array.from(await rd(c, 4 * rows)), Array.from(await rd(d, 4 * rows)));
+    assert.strictEqual(await amp.gemv.matmul('Q4_K', w4, x, rows, k, 9), null);
+    out.gemv2 = true;
+    ctx.recycle();
+  }
+
+  // ---- recycle() without a device wait ----------------------------------------
+  {
+    const rows = 8192, k = 2048, m = 2048, reps = 60;
+    const w = device.createBuffer({ size: rows * k / 32 * 34 + 4, label: 'w' });
+    device.queue.writeBuffer(w, 0, eff.quantize('Q8_0', eff.fillNormal(8, 0.02, rows * k)));
+    const x = ctx.alloc(m * k * 4, 'x');
+    for (let i = 0; i < m; i += 64) device.queue.writeBuffer(x, i * k * 4, eff.fillNormal(9 + i, 1.0, 64 * k));
+    const y0 = await ops.matmul('Q8_0', w, x, rows, k, m);
+    const ref = await rd(y0, 4096);
+    ctx.alloc(12345, 'caduca');                       // a size class lent once
+    ctx.recycle(); ctx.recycle();
+    const talla = Math.ceil(12345 / 256) * 256;
+    assert.ok(ctx.scratchFree.has(talla));
+    const ys = ctx.alloc(m * rows * 4, 'y');            // the next token's output
+    await eff.readback(device, ys, 0, 4);              // the device is idle here
+    const t0 = ahora();
+    for (let i = 0; i < reps; i++) native(ops, w, x, ys, rows, k, m);
+    const t1 = ahora();
+    ctx.recycle();                                     // destroys the expired class
+    const t2 = ahora();
+    assert.ok(!ctx.scratchFree.has(talla));
+    const last = await rd(ys, 4096);
+    const t3 = ahora();
+    assert.deepStrictEqual(Array.from(last), Array.from(ref));
+    out.recycle = { enqueue_us: t1 - t0, recycle_us: t2 - t1, drain_us: t3 - t2 };
+  }
+
+  // ---- recorded chain -----------------------------------------------------------
+  {
+    const rows = 2048, k = 2048, porToken = 30;
+    const w = device.createBuffer({ size: Math.ceil((rows * k / 256 * 144 + 4) / 4) * 4, label: 'w' });
+    device.queue.writeBuffer(w, 0, eff.quantize('Q4_K', eff.fillNormal(1, 0.02, rows * k)));
+    const xIn = device.createBuffer({ size: k * 4, label: 'xin' });
+    const cadena = async () => {
+      let x = xIn;
+      for (let i = 0; i < porToken; i++) x = await ops.matmul('Q4_K', w, x, rows, k, 1);
+      return x;
+    };
+    const xs = [eff.fillNormal(2, 1.0, k), eff.fillNormal(3, 1.0, k), eff.fillNormal(4, 1.0, k)];
+    const eager = [];
+    for (const xv of xs) {
+      device.queue.writeBuffer(xIn, 0, xv);
+      eager.push(Array.from(await rd(await cadena(), 64)));
+      ctx.recycle();
+    }
+    // while recording, a readback or an upload is refused and the recording is dropped
+    await assert.rejects(ctx.grabaGrafo(async () => {
+      const y = await cadena();
+      await eff.readback(device, y, 0, 16);
+      return y;
+    }), /graph|grafo/);
+    const g = await ctx.grabaGrafo(cadena);
+    assert.ok(g.nodos >= porToken, `nodos ${g.nodos}`);
+    const replays = [];
+    for (let r = 0; r < 2; r++) {
+      for (const xv of xs) {
+        device.queue.writeBuffer(xIn, 0, xv);
+        g.lanza();
+        replays.push(Array.from(await rd(g.salida, 64)));
+        ctx.recycle();                                 // the recording keeps its buffers
+      }
+    }
+    for (let i = 0; i < replays.length; i++) assert.deepStrictEqual(replays[i], eager[i % 3]);
+    // host cost per operation: eager chain against replays
+    const tokens = 200;
+    let t0 = ahora();
+    for (let i = 0; i < tokens; i++) { device.queue.writeBuffer(xIn, 0, xs[0]); await cadena(); ctx.recycle(); }
+    await eff.readback(device, xIn, 0, 4);
+    const eagerUs = (ahora() - t0) / (tokens * porToken);
+    t0 = ahora();
+    for (let i = 0; i < tokens; i++) { device.queue.writeBuffer(xIn, 0, xs[0]); g.lanza(); }
+    await eff.readback(device, g.salida, 0, 4);
+    const grafoUs = (ahora() - t0) / (tokens * porToken);
+    g.destroy();
+    g.destroy();
+    assert.throws(() => g.lanza(), /destruy/);
+    out.grafo = { nodos: g.nodos, us_per_op_eager: eagerUs, us_per_op_graph: grafoUs };
+  }
+  ctx.destroy();
+  device.destroy();
+  console.log(JSON.stringify(out));
+}
+
+// quant.matmul without the pool (the GEMM into a fixed y), for the enqueue loop
+function native(ops, w, x, y, rows, k, m) {
+  eff.native.qmatmul(ops.ctx.device._ctx, eff.QUANT_TYPES.Q8_0.code, w._h, x._h, y._h, rows, k, m);
+}
+
+main().catch((e) => { console.error(e); process.exit(1); });

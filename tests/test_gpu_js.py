@@ -82,3 +82,23 @@ def test_js_shim_gpu(eff, orc, tmp_path):
     assert out["topkStats"]["motivos"] == {"muestreo sin tope": 1}
     assert out["stats"]["topk"] == 21 and out["stats"]["gemm"] >= 1 and out["stats"]["split"] >= 2
     assert out["cabeza"] is True   # the head GEMV + top-k in one call, checked inside the shim
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
+def test_js_graph_pool_and_gemv2_applicability():
+    """tests/js/shim_grafo.js: gemv ops are null where GEMV2 is (and lend
+    nothing), recycle() destroys an expired size class without waiting for the
+    device, and a recorded chain of 30 quant.matmul calls replays bit-equal to
+    the eager chain for each new x (the checks of bits are inside the shim)."""
+    r = subprocess.run(["node", os.path.join(HERE, "js", "shim_grafo.js")], capture_output=True, text=True,
+                       timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["gemv2"] is True
+    rc = out["recycle"]
+    # 60 GEMMs of 2048 x 8192 x 2048 were still running when recycle() returned
+    assert rc["drain_us"] > 2000, rc
+    assert rc["recycle_us"] < 0.1 * rc["drain_us"], rc
+    g = out["grafo"]
+    assert g["us_per_op_graph"] < g["us_per_op_eager"], g
