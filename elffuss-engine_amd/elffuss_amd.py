@@ -243,7 +243,7 @@ class Buffer:
 
     def free(self):
         if self.handle:
-            lib().eff_buf_free(self.ctx.h, self.handle)
+            self.ctx._check(lib().eff_buf_free(self.ctx.h, self.handle))
             self.handle = None
 
     def retire(self):

@@ -44,21 +44,30 @@ def test_graph_replays_give_the_eager_bits(ctx, eff):
         b.free()
 
 
-def test_calls_refused_while_recording(ctx, eff):
+def test_calls_refused_while_recording(eff):
     """Waits, allocations, host copies and scratch growth are refused while
-    recording (EFF_E_INVALID) and leave the recording usable."""
+    recording (EFF_E_INVALID) and leave the recording usable. A context of
+    its own, so that its split-x scratch holds exactly 16 tokens."""
+    with eff.Context(0) as ctx:
+        _refused_while_recording(ctx, eff)
+
+
+def _refused_while_recording(ctx, eff):
     rows, k = 256, 1024
     w = ctx.upload(eff.quantize("Q2_K", eff.fill_normal(51, 0.02, rows * k)))
     x = ctx.upload(eff.fill_normal(52, 1.0, 64 * k))
     y, y_ref = ctx.alloc(64 * rows * 4), ctx.alloc(64 * rows * 4)
     ctx.qmatmul(eff.Q2_K, w, x, y_ref, rows, k, 16)    # grows the split-x scratch for 16 tokens
     ctx.graph_begin()
-    for call in (lambda: ctx.alloc(64), lambda: y.write(np.zeros(4, np.float32)), lambda: y.read(np.uint32, 4),
-                 lambda: ctx.sync(), lambda: ctx.read_async(y, np.uint32, 4), lambda: w.retire(),
-                 lambda: ctx.qmatmul(eff.Q2_K, w, x, y, rows, k, 64)):   # 64 tokens: the scratch would grow
+    calls = {"alloc": lambda: ctx.alloc(64), "write": lambda: y.write(np.zeros(4, np.float32)),
+             "read": lambda: y.read(np.uint32, 4), "sync": lambda: ctx.sync(),
+             "readback": lambda: ctx.read_async(y, np.uint32, 4), "retire": lambda: w.retire(),
+             "free": lambda: y_ref.free(),
+             "grow": lambda: ctx.qmatmul(eff.Q2_K, w, x, y, rows, k, 64)}   # 64 tokens: the scratch would grow
+    for name, call in calls.items():
         with pytest.raises(eff.EffError) as e:
             call()
-        assert e.value.code == eff.E_INVALID
+        assert e.value.code == eff.E_INVALID, name
     ctx.qmatmul(eff.Q2_K, w, x, y, rows, k, 16)
     g = ctx.graph_end()
     g.launch()
