@@ -312,16 +312,22 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
   wait_vm<0>();
 
   // D[tok][row]: lane holds row (column) n of each fragment and tokens
-  // 8 (v / 4) + 4 h + v % 4.
+  // 8 (v / 4) + 4 h + v % 4. The lane number is read again here (an asm
+  // statement the compiler cannot merge with the first read), so that n and
+  // h are not held across the main loop: at 256 x 256 every register is in
+  // use there, and they would be spilled to scratch.
+  uint32_t lane_e;
+  __asm__ volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
+  const uint32_t ne = lane_e & 31u, he = lane_e >> 5;
 #pragma unroll
   for (int fj = 0; fj < (int)kFN; ++fj) {
-    const uint32_t row = n0 + kFN * 32u * wn + 32u * fj + n;
+    const uint32_t row = n0 + kFN * 32u * wn + 32u * fj + ne;
     if (row >= rows) continue;
 #pragma unroll
     for (int fi = 0; fi < (int)kFM; ++fi)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const uint32_t tok = t0 + kFM * 32u * wm + 32u * fi + 8u * (v >> 2) + 4u * h + (v & 3);
+        const uint32_t tok = t0 + kFM * 32u * wm + 32u * fi + 8u * (v >> 2) + 4u * he + (v & 3);
         if (tok < tokens) y[(uint64_t)tok * rows + row] = acc[fi][fj][v];
       }
   }

@@ -385,7 +385,9 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
   using L = SxLds<TYPE, TT, RF, NW>;
   static_assert(!FX || (TT == 1 && KS == 1), "the fused preparation covers one token tile");
   constexpr uint32_t NS = sx_slots<TYPE>();
-  constexpr uint32_t P = TT == 1 ? 16u : TT == 2 ? 8u : 4u;  // steps of x fragments loaded ahead
+  // steps of x fragments loaded ahead (Q4_K's 37-dword rows take 19 staging
+  // offsets per lane: 3 steps ahead at 4 token tiles keep it within the VGPRs)
+  constexpr uint32_t P = TT == 1 ? 16u : TT == 2 ? 8u : TYPE == Q4_K ? 3u : 4u;
   constexpr uint32_t ROWS = L::ROWS, ND = L::ND;
   __shared__ __align__(16) uint8_t lds_s[FX ? 16u : L::BYTES];
   extern __shared__ __align__(16) uint8_t lds_d[];
