@@ -146,6 +146,16 @@ int use_device(eff_ctx *ctx) {
   return EFF_OK;
 }
 
+// An output buffer of at least `bytes` bytes, 16-byte aligned.
+int check_out(eff_ctx *ctx, eff_buf *b, uint64_t bytes, const char *who) {
+  if (!b) return fail(ctx, EFF_E_INVALID, "%s: null buffer", who);
+  if (bytes > b->size)
+    return fail(ctx, EFF_E_BOUNDS, "%s: needs %llu bytes and the buffer has %zu", who, (unsigned long long)bytes,
+                b->size);
+  if ((uintptr_t)b->ptr & 15) return fail(ctx, EFF_E_INVALID, "%s: device buffers must be 16-byte aligned", who);
+  return EFF_OK;
+}
+
 // EFF_E_INVALID when the context's stream is being recorded into a graph:
 // for the calls that wait for the device, allocate or move host data, none
 // of which a replay could repeat.
@@ -271,6 +281,24 @@ int run_gemm(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint3
   if (rc) return rc;
   hipError_t e = launch_gemm(wv, x, y, tokens, plan, cfg, ctx->xh_scratch, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
+  ++ctx->stats.gemm_x;
+  return EFF_OK;
+}
+
+// The checks shared by the prepared-x GEMM entry points: the GEMM applies
+// (NOT_APPLICABLE otherwise, as eff_qgemm_planned), tokens under the plan.
+int gemm_prepared_check(eff_ctx *ctx, int type, uint32_t rows, uint32_t k, uint32_t tokens, uint32_t plan,
+                        const char *who) {
+  if (!type_known(type)) return fail(ctx, EFF_E_TYPE, "%s: unsupported quantization type %d", who, type);
+  if (rows == 0 || k == 0 || tokens == 0)
+    return fail(ctx, EFF_E_INVALID, "%s: empty shape rows=%u k=%u tokens=%u", who, rows, k, tokens);
+  const Geometry g = geometry(type);
+  if (k % g.elems) return fail(ctx, EFF_E_SHAPE, "%s %s: k=%u is not a multiple of %u", who, eff_type_name(type), k, g.elems);
+  if (plan == 0 || (int64_t)plan < ctx->gemm_min_tokens) {
+    ++ctx->stats.not_applicable;
+    return EFF_NOT_APPLICABLE;
+  }
+  if (tokens > plan) return fail(ctx, EFF_E_INVALID, "%s: %u tokens under the plan of %u", who, tokens, plan);
   return EFF_OK;
 }
 
@@ -740,6 +768,62 @@ int eff_qgemm_planned(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y
   return rc;
 }
 
+int eff_gemm_x_layout(eff_ctx *ctx, int type, uint32_t rows, uint32_t k, uint32_t tokens, uint32_t plan_tokens,
+                      size_t *bytes, uint32_t *layout) {
+  if (!ctx || !bytes || !layout) return EFF_E_INVALID;
+  const int rc = gemm_prepared_check(ctx, type, rows, k, tokens, plan_tokens, "gemm x layout");
+  if (rc) return rc;
+  const uint32_t cfg = (uint32_t)ctx->gemm_config;
+  *bytes = gemm_x_bytes(type, tokens, plan_tokens, k, rows, cfg);
+  *layout = gemm_x_layout(type, plan_tokens, k, rows, cfg);
+  return EFF_OK;
+}
+
+int eff_gemm_prepare_x(eff_ctx *ctx, int type, eff_buf *x, eff_buf *xh, uint32_t rows, uint32_t k, uint32_t tokens,
+                       uint32_t plan_tokens) {
+  if (!ctx) return EFF_E_INVALID;
+  if (!x || !xh) return fail(ctx, EFF_E_INVALID, "gemm prepare x: null buffer");
+  int rc = gemm_prepared_check(ctx, type, rows, k, tokens, plan_tokens, "gemm prepare x");
+  if (rc) return rc;
+  const uint32_t cfg = (uint32_t)ctx->gemm_config;
+  if ((uint64_t)tokens * k * 4 > x->size)
+    return fail(ctx, EFF_E_BOUNDS, "gemm prepare x: x needs %llu bytes and the buffer has %zu",
+                (unsigned long long)tokens * k * 4, x->size);
+  if ((rc = check_out(ctx, xh, gemm_x_bytes(type, tokens, plan_tokens, k, rows, cfg), "gemm prepare x")) ||
+      (rc = use_device(ctx)))
+    return rc;
+  if ((uintptr_t)x->ptr & 15) return fail(ctx, EFF_E_INVALID, "gemm prepare x: device buffers must be 16-byte aligned");
+  const hipError_t e = launch_gemm_x(type, (const float *)x->ptr, tokens, plan_tokens, k, rows, cfg, xh->ptr,
+                                     ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "gemm prepare x launch");
+  ++ctx->stats.gemm_x;
+  return EFF_OK;
+}
+
+int eff_qgemm_prepared(eff_ctx *ctx, int type, eff_buf *w, eff_buf *xh, eff_buf *y, uint32_t rows, uint32_t k,
+                       uint32_t tokens, uint32_t plan_tokens) {
+  if (!ctx) return EFF_E_INVALID;
+  if (!w || !xh || !y) return fail(ctx, EFF_E_INVALID, "gemm prepared: null buffer");
+  int rc = gemm_prepared_check(ctx, type, rows, k, tokens, plan_tokens, "gemm prepared");
+  if (rc) return rc;
+  const uint32_t cfg = (uint32_t)ctx->gemm_config;
+  // the weight view checks against a stand-in x of the call's size (the
+  // product reads xh, checked below)
+  eff_buf xs{};
+  xs.ptr = xh->ptr;
+  xs.size = (size_t)tokens * k * 4;
+  WeightView wv;
+  if ((rc = weight_view(ctx, type, w, &xs, y, rows, k, tokens, wv, "gemm prepared")) ||
+      (rc = check_out(ctx, xh, gemm_x_bytes(type, tokens, plan_tokens, k, rows, cfg), "gemm prepared x")) ||
+      (rc = use_device(ctx)))
+    return rc;
+  const hipError_t e = launch_gemm_prepared(wv, (const _Float16 *)xh->ptr, (float *)y->ptr, tokens, plan_tokens, cfg,
+                                            ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "gemm prepared launch");
+  ++ctx->stats.gemm;
+  return EFF_OK;
+}
+
 int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k, uint32_t tokens) {
   if (!ctx) return EFF_E_INVALID;
   WeightView wv;
@@ -879,14 +963,6 @@ int topk_check(eff_ctx *ctx, eff_buf *logits, uint32_t base, uint32_t vocab, uin
   return EFF_OK;
 }
 
-int check_out(eff_ctx *ctx, eff_buf *b, uint64_t bytes, const char *who) {
-  if (!b) return fail(ctx, EFF_E_INVALID, "%s: null buffer", who);
-  if (bytes > b->size)
-    return fail(ctx, EFF_E_BOUNDS, "%s: needs %llu bytes and the buffer has %zu", who, (unsigned long long)bytes,
-                b->size);
-  if ((uintptr_t)b->ptr & 15) return fail(ctx, EFF_E_INVALID, "%s: device buffers must be 16-byte aligned", who);
-  return EFF_OK;
-}
 
 }  // namespace
 

@@ -92,8 +92,15 @@ hipError_t launch_gemv_mt(const WeightView &wv, const float *x, float *y, uint32
 // run over `plan` tokens.
 // cfg: the Q8_0 tile configuration (EFF_OPT_GEMM_CONFIG; 0 automatic).
 size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg);
+// An id of that layout: equal ids, one prepared x serves both products.
+uint32_t gemm_x_layout(int type, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg);
 hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint32_t plan,
                        uint32_t cfg, void *xh_scratch, hipStream_t stream);
+// The two halves of launch_gemm: x into its fp16 layout, and the product from it.
+hipError_t launch_gemm_x(int type, const float *x, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows,
+                         uint32_t cfg, void *xh, hipStream_t stream);
+hipError_t launch_gemm_prepared(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
+                                uint32_t cfg, hipStream_t stream);
 // Q8_0 GEMM with direct-to-LDS staging (>= 256 tokens); x in the
 // [token tile][k step][2^gemm_big_tile_log2 tokens][64] layout.
 bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows);

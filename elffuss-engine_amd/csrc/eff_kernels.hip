@@ -1044,18 +1044,34 @@ size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t plan, uint32_t k, uint32
   return (size_t)(tiles * steps) << (bm + bk + 1);
 }
 
-hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint32_t plan,
-                       uint32_t cfg, void *xh_scratch, hipStream_t s) {
+uint32_t gemm_x_layout(int type, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg) {
+  uint32_t bm, bk;
+  gemm_x_tile(type, plan, k, rows, cfg, bm, bk);
+  return (bm << 4) | bk;
+}
+
+hipError_t launch_gemm_x(int type, const float *x, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows,
+                         uint32_t cfg, void *xh, hipStream_t s) {
   if (plan < tokens) return hipErrorInvalidValue;
   uint32_t bm, bk;
-  gemm_x_tile(wv.type, plan, wv.k, wv.rows, cfg, bm, bk);
-  const uint32_t steps = (wv.k + (1u << bk) - 1) >> bk;
-  const uint64_t n8 = (uint64_t)gemm_x_bytes(wv.type, tokens, plan, wv.k, wv.rows, cfg) / 16u;
-  _Float16 *xh = (_Float16 *)xh_scratch;
-  hipLaunchKernelGGL(k_x_to_f16, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, s, x, xh, tokens, wv.k, bm, bk,
-                     steps, n8);
-  hipError_t e = hipGetLastError();
+  gemm_x_tile(type, plan, k, rows, cfg, bm, bk);
+  const uint32_t steps = (k + (1u << bk) - 1) >> bk;
+  const uint64_t n8 = (uint64_t)gemm_x_bytes(type, tokens, plan, k, rows, cfg) / 16u;
+  hipLaunchKernelGGL(k_x_to_f16, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, s, x, (_Float16 *)xh, tokens, k,
+                     bm, bk, steps, n8);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint32_t plan,
+                       uint32_t cfg, void *xh_scratch, hipStream_t s) {
+  const hipError_t e = launch_gemm_x(wv.type, x, tokens, plan, wv.k, wv.rows, cfg, xh_scratch, s);
   if (e != hipSuccess) return e;
+  return launch_gemm_prepared(wv, (const _Float16 *)xh_scratch, y, tokens, plan, cfg, s);
+}
+
+hipError_t launch_gemm_prepared(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
+                                uint32_t cfg, hipStream_t s) {
+  if (plan < tokens) return hipErrorInvalidValue;
   if (gemm_big_applies(wv.type, plan, wv.k, wv.rows)) return launch_gemm_big(wv, xh, y, tokens, plan, cfg, s);
   switch (wv.type) {
     case Q8_0: return gemm_go<Q8_0>(wv, xh, y, tokens, plan, s);

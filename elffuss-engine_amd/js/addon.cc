@@ -272,6 +272,7 @@ napi_value Stats(napi_env env, napi_callback_info info) {
   napi_set_named_property(env, o, "split", make_int(env, (int64_t)s.split));
   napi_set_named_property(env, o, "fused", make_int(env, (int64_t)s.fused));
   napi_set_named_property(env, o, "gather", make_int(env, (int64_t)s.gather));
+  napi_set_named_property(env, o, "gemmX", make_int(env, (int64_t)s.gemm_x));
   return o;
 }
 
@@ -495,6 +496,45 @@ napi_value QGemmPlanned(napi_env env, napi_callback_info info) {
   return status(env, ctx, rc);
 }
 
+// gemmXLayout(ctx, type, rows, k, tokens, plan) -> {bytes, layout} | null
+napi_value GemmXLayout(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  get_args(env, info, 6, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  size_t bytes = 0;
+  uint32_t layout = 0;
+  int rc = eff_gemm_x_layout(ctx, (int)i64(env, a[1]), (uint32_t)i64(env, a[2]), (uint32_t)i64(env, a[3]),
+                             (uint32_t)i64(env, a[4], 1), (uint32_t)i64(env, a[5], 1), &bytes, &layout);
+  if (rc) return status(env, ctx, rc);
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "bytes", make_int(env, (int64_t)bytes));
+  napi_set_named_property(env, o, "layout", make_int(env, (int64_t)layout));
+  return o;
+}
+
+// gemmPrepareX(ctx, type, x, xh, rows, k, tokens, plan)
+napi_value GemmPrepareX(napi_env env, napi_callback_info info) {
+  napi_value a[8];
+  get_args(env, info, 8, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  int rc = eff_gemm_prepare_x(ctx, (int)i64(env, a[1]), external<eff_buf>(env, a[2]), external<eff_buf>(env, a[3]),
+                              (uint32_t)i64(env, a[4]), (uint32_t)i64(env, a[5]), (uint32_t)i64(env, a[6], 1),
+                              (uint32_t)i64(env, a[7], 1));
+  return status(env, ctx, rc);
+}
+
+// qgemmPrepared(ctx, type, w, xh, y, rows, k, tokens, plan)
+napi_value QGemmPrepared(napi_env env, napi_callback_info info) {
+  napi_value a[9];
+  get_args(env, info, 9, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  int rc = eff_qgemm_prepared(ctx, (int)i64(env, a[1]), external<eff_buf>(env, a[2]), external<eff_buf>(env, a[3]),
+                              external<eff_buf>(env, a[4]), (uint32_t)i64(env, a[5]), (uint32_t)i64(env, a[6]),
+                              (uint32_t)i64(env, a[7], 1), (uint32_t)i64(env, a[8], 1));
+  return status(env, ctx, rc);
+}
+
 // qgemvMulti(ctx, type, mode, [w...], x, [y...], [rows...], k, tokens)
 napi_value QGemvMulti(napi_env env, napi_callback_info info) {
   napi_value a[9];
@@ -599,7 +639,8 @@ napi_value Register(napi_env env, napi_value exports) {
       {"qmatmul", QMatmul}, {"qgemv", QGemv}, {"qgemvMulti", QGemvMulti}, {"qgemm", QGemm}, {"qgemmPlanned", QGemmPlanned}, {"dequant", Dequant}, {"gather", Gather}, {"gatherNorm", GatherNorm}, {"topk", TopK}, {"qgemvTopk", QGemvTopK},
       {"topkOutBytes", TopKOutBytes}, {"bufRetire", BufRetire}, {"graphBegin", GraphBegin},
       {"graphEnd", GraphEnd}, {"graphLaunch", GraphLaunch}, {"graphNodes", GraphNodes},
-      {"graphDestroy", GraphDestroy},
+      {"graphDestroy", GraphDestroy}, {"gemmXLayout", GemmXLayout}, {"gemmPrepareX", GemmPrepareX},
+      {"qgemmPrepared", QGemmPrepared},
   };
   for (auto &f : fns) {
     napi_value v;

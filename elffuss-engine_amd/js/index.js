@@ -605,6 +605,37 @@ const GEMM2_TIPOS = new Set(['Q8_0', 'Q8_0R']);
 function createGemm2Ops(ctx) {
   const device = ctx.device;
   const desde = () => device.option(OPT.GEMM_MIN_TOKENS);
+  // x -> fp16 with a memo (aF16, ops.gemm2.js:151-196): the same activation
+  // feeds several GEMMs in a row (the norm's output q, k, v; the FFN's gate
+  // and up), and the conversion is the same operation on the same bytes, so
+  // reusing it changes no bit. The key is the pool's allocation mark of x
+  // (ctx.marcaDe), not the buffer: a buffer lent again gets a new mark. A
+  // conversion is reused only while its own buffer is still lent under the
+  // mark it was made with (a returned one could be lent to the same call as
+  // its output). Here the library gives the bytes and an id of the layout the
+  // GEMM reads (eff_gemm_x_layout): a conversion serves every product whose
+  // layout id, tokens and k match. Four entries, oldest dropped first.
+  const prestado = (buf) => ctx.scratch.some((e) => e.buf === buf);
+  const memo = [];
+  function aF16(code, xBuf, rows, k, tokens, lote) {
+    const lay = native.gemmXLayout(device._ctx, code, rows, k, tokens, lote);
+    if (lay === null) return null;
+    const marca = ctx.marcaDe.get(xBuf);
+    if (marca !== undefined) {
+      for (let i = memo.length - 1; i >= 0; i--) {
+        const m = memo[i];
+        if (m.marca === marca && m.layout === lay.layout && m.tokens === tokens && m.k === k &&
+            ctx.marcaDe.get(m.xh) === m.marcaXh && prestado(m.xh)) return m.xh;
+      }
+    }
+    const xh = ctx.alloc(lay.bytes, 'gemm2.x');
+    native.gemmPrepareX(device._ctx, code, xBuf._h, xh._h, rows, k, tokens, lote);
+    if (marca !== undefined) {
+      memo.push({ marca, layout: lay.layout, tokens, k, xh, marcaXh: ctx.marcaDe.get(xh) });
+      if (memo.length > 4) memo.shift();
+    }
+    return xh;
+  }
   const ops = {
     // What this shape would run (null: the caller's usual path).
     plan(type, rows, k, tokens) {
@@ -613,15 +644,19 @@ function createGemm2Ops(ctx) {
       if (!(tokens >= desde()) || rows % 16 !== 0) return null;
       return { via: 'mfma-f16', type, bpr: k / i.blockElems, lote: tokens };
     },
-    olvida() {},
+    // Empties the x -> fp16 memo (for benches: so that one measurement does
+    // not save conversions another one pays, ops.gemm2.js:265-266).
+    olvida() { memo.length = 0; },
     matmul(type, wBuf, xBuf, rows, k, tokens) {
       if (tokens < 4 && tokens < desde()) return Promise.resolve(null);
       const pl = ops.plan(type, rows, k, tokens);
       if (!pl) return Promise.resolve(null);
       const i = QUANT_TYPES[type];
       if (TIPOS_R.has(type)) compruebaBufferR(type, wBuf, { bloques: rows * pl.bpr }, 'gemm2');
+      const xh = aF16(i.code, xBuf, rows, k, tokens, tokens);
+      if (!xh) return Promise.resolve(null);
       const y = ctx.alloc(rows * tokens * 4, 'matmul.y');
-      const r = native.qgemm(device._ctx, i.code, wBuf._h, xBuf._h, y._h, rows, k, tokens);
+      const r = native.qgemmPrepared(device._ctx, i.code, wBuf._h, xh._h, y._h, rows, k, tokens, tokens);
       return Promise.resolve(r === null ? null : y);
     },
     // The kernel's output for one token depends only on its x row and W,
@@ -636,8 +671,10 @@ function createGemm2Ops(ctx) {
       if (!pl) return Promise.resolve(null);
       const i = QUANT_TYPES[type];
       if (TIPOS_R.has(type)) compruebaBufferR(type, wBuf, { bloques: rows * pl.bpr }, 'gemm2');
+      const xh = aF16(i.code, x1, rows, k, 1, lote);
+      if (!xh) return Promise.resolve(null);
       const y = ctx.alloc(rows * 4, 'matmul.y');
-      const r = native.qgemmPlanned(device._ctx, i.code, wBuf._h, x1._h, y._h, rows, k, 1, lote);
+      const r = native.qgemmPrepared(device._ctx, i.code, wBuf._h, xh._h, y._h, rows, k, 1, lote);
       return Promise.resolve(r === null ? null : y);
     },
   };

@@ -90,6 +90,8 @@ typedef struct eff_stats {
   uint64_t split;       /* split-x matrix-core launches (Q2_K, Q4_K, IQ2_XXS from EFF_OPT_SPLIT_MIN_TOKENS) */
   uint64_t fused;       /* fused GEMV launches (eff_qgemv_multi) */
   uint64_t gather;      /* gather launches (eff_gather, eff_gather_norm) */
+  uint64_t gemm_x;      /* conversions of x to fp16 for the GEMM (one per eff_qgemm / eff_qgemm_planned /
+                           router GEMM call, one per eff_gemm_prepare_x) */
 } eff_stats;
 
 /* ---- types and geometry -------------------------------------------------- */
@@ -313,6 +315,26 @@ int eff_qgemm(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
  * EFF_NOT_APPLICABLE when plan_tokens < GEMM min. */
 int eff_qgemm_planned(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
                       uint32_t rows, uint32_t k, uint32_t tokens, uint32_t plan_tokens);
+
+/* x prepared once for several GEMMs: the reference converts x to fp16 once
+ * per activation and reuses it across the matmuls that read it (aF16, a memo
+ * keyed on the pool's allocation mark, ops.gemm2.js:151-196; cleared by
+ * olvida(), ops.gemm2.js:266). The JS host keeps that memo; the library
+ * provides the three steps:
+ *  - eff_gemm_x_layout: the bytes of x prepared for a GEMM of `tokens` rows
+ *    under the plan of `plan_tokens` (the configuration eff_qgemm_planned
+ *    would run), and an id of the layout: products whose ids, tokens and k
+ *    agree can share one prepared x. NOT_APPLICABLE where the GEMM is not.
+ *  - eff_gemm_prepare_x: x rounded to fp16 (RNE; f32AF16Shader,
+ *    kernels.drift.wgsl.js:34-63) into xh, in that layout.
+ *  - eff_qgemm_prepared: the GEMM from the prepared x: the same bits as
+ *    eff_qgemm_planned over x. */
+int eff_gemm_x_layout(eff_ctx *ctx, int type, uint32_t rows, uint32_t k, uint32_t tokens, uint32_t plan_tokens,
+                      size_t *bytes, uint32_t *layout);
+int eff_gemm_prepare_x(eff_ctx *ctx, int type, eff_buf *x, eff_buf *xh, uint32_t rows, uint32_t k, uint32_t tokens,
+                       uint32_t plan_tokens);
+int eff_qgemm_prepared(eff_ctx *ctx, int type, eff_buf *w, eff_buf *xh, eff_buf *y, uint32_t rows, uint32_t k,
+                       uint32_t tokens, uint32_t plan_tokens);
 
 /* Dequantize n_blocks blocks to f32, bit-exact with the reference decoders
  * (quant.dequant, ops.js:813-823; dequantShader, kernels.wgsl.js:903-922). */

@@ -55,6 +55,44 @@ async function main() {
     ctx.recycle();
   }
 
+  // ---- gemm2's x -> fp16 memo (aF16, keyed on the allocation mark) ------------
+  {
+    const k = 1024, m = 300;
+    const wq = device.createBuffer({ size: 272 * k / 32 * 34 + 4, label: 'wq' });
+    const wk = device.createBuffer({ size: 160 * k / 32 * 34 + 4, label: 'wk' });
+    device.queue.writeBuffer(wq, 0, eff.quantize('Q8_0', eff.fillNormal(21, 0.02, 272 * k)));
+    device.queue.writeBuffer(wk, 0, eff.quantize('Q8_0', eff.fillNormal(22, 0.02, 160 * k)));
+    const xv = eff.fillNormal(23, 1.0, m * k);
+    const x = ops.upload(xv, 'x');                       // a pool buffer: it has a mark
+    const conv = () => device.stats().gemmX;
+    const c0 = conv();
+    const yq = await ops.gemm2.matmul('Q8_0', wq, x, 272, k, m);
+    const yk = await ops.gemm2.matmul('Q8_0', wk, x, 160, k, m);
+    const c1 = conv();
+    // the same products without the memo: after olvida() the conversion is paid again
+    ops.gemm2.olvida();
+    const yk2 = await ops.gemm2.matmul('Q8_0', wk, x, 160, k, m);
+    const c2 = conv();
+    // x lent again (a new mark) is converted again
+    ctx.recycle();
+    const x2 = ops.upload(xv, 'x');
+    const yq2 = await ops.gemm2.matmul('Q8_0', wq, x2, 272, k, m);
+    const c3 = conv();
+    // a buffer from outside the pool has no mark: converted on every call
+    const xo = device.createBuffer({ size: m * k * 4, label: 'xo' });
+    device.queue.writeBuffer(xo, 0, xv);
+    const yq3 = await ops.gemm2.matmul('Q8_0', wq, xo, 272, k, m);
+    await ops.gemm2.matmul('Q8_0', wq, xo, 272, k, m);
+    const c4 = conv();
+    const ref = new Uint32Array(await eff.readback(device, yq, 0, 272 * m * 4));
+    assert.deepStrictEqual(Array.from(await rd(yq2, 272 * m)), Array.from(ref));
+    assert.deepStrictEqual(Array.from(await rd(yq3, 272 * m)), Array.from(ref));
+    assert.deepStrictEqual(Array.from(await rd(yk, 160 * m)), Array.from(await rd(yk2, 160 * m)));
+    out.memo = { q_k_shared: c1 - c0, after_olvida: c2 - c1, new_mark: c3 - c2, no_mark: c4 - c3 };
+    ctx.recycle();
+    xo.destroy(); wq.destroy(); wk.destroy();
+  }
+
   // ---- recycle() without a device wait ----------------------------------------
   {
     const rows = 8192, k = 2048, m = 2048, reps = 60;

@@ -604,6 +604,42 @@ def test_gemm_planned_tail_gives_the_batch_row_bits(ctx, eff, tname, lote):
         b.free()
 
 
+@pytest.mark.parametrize("tname,tokens,lote", [("Q8_0", 300, 300), ("Q8_0", 1100, 1100), ("Q8_0R", 100, 100),
+                                               ("Q8_0", 1, 300), ("Q8_0R", 3, 1100)])
+def test_gemm_prepared_x_serves_several_products(ctx, eff, tname, tokens, lote):
+    """x prepared once (eff_gemm_prepare_x) serves two products over other
+    weights (the q / k / v of one activation), each with the bits of
+    eff_qgemm_planned over x; one conversion in all; the layout id follows the
+    plan, and a call the GEMM does not apply to is NOT_APPLICABLE."""
+    k = 1024
+    rows = (272, 160)
+    ws = [make_weights(eff, tname, r, k, 750 + r + lote) for r in rows]
+    x = eff.fill_normal(751 + lote, 1.0, tokens * k)
+    xb = ctx.upload(x)
+    nbytes, lay = ctx.gemm_x_layout(ws[0][0], rows[0], k, tokens, lote)
+    assert (nbytes, lay) == ctx.gemm_x_layout(ws[1][0], rows[1], k, tokens, lote)
+    xh = ctx.alloc(nbytes)
+    wbs = [upload_w(ctx, eff, tname, data, n) for (t, data, gguf, n) in ws]
+    y1s = [ctx.alloc(tokens * r * 4) for r in rows]
+    before = ctx.stats()["gemm_x"]
+    ctx.gemm_prepare_x(ws[0][0], xb, xh, rows[0], k, tokens, lote)
+    for (t, _, _, _), r, wb, y1 in zip(ws, rows, wbs, y1s):
+        ctx.qgemm_prepared(t, wb, xh, y1, r, k, tokens, lote)
+    assert ctx.stats()["gemm_x"] == before + 1
+    for (t, _, _, _), r, wb, y1 in zip(ws, rows, wbs, y1s):
+        y2 = ctx.alloc(tokens * r * 4)
+        ctx.qgemm_planned(t, wb, xb, y2, r, k, tokens, lote)
+        assert np.array_equal(y1.read(np.uint32), y2.read(np.uint32)), (tname, r)
+        for b in (wb, y1, y2):
+            b.free()
+    with pytest.raises(eff.NotApplicable):
+        ctx.gemm_x_layout(ws[0][0], rows[0], k, 1, 63)
+    with pytest.raises(eff.EffError):
+        ctx.gemm_prepare_x(ws[0][0], xb, ctx.alloc(16), rows[0], k, tokens, lote)    # xh too small
+    xb.free()
+    xh.free()
+
+
 def test_read_ticket_snapshots_at_begin(ctx, eff):
     """eff_read_begin enqueues the copy at once: a write enqueued after it is
     not in the snapshot; the buffer can be reused right away."""
