@@ -6,6 +6,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <chrono>
 #include <deque>
 #include <memory>
 #include <mutex>
@@ -43,13 +44,18 @@ bool g_scratch_done[kMaxDevices];
 // bytes past a block (the reference's loader slack, model.js:248-254).
 static constexpr size_t kSlack = 256;
 
+// How long eff_read_end polls a read's completion before a blocking wait.
+static constexpr int64_t kReadSpinNs = 2000000;
+
 // Pinned blocks of finished reads (eff_read_begin / eff_read_end), reused.
 // Shared by a context and its live read tickets; the last owner frees them.
 struct ReadPool {
   std::mutex mu;
   std::vector<std::pair<void *, size_t>> blocks;
+  std::vector<hipEvent_t> events;   // completed tickets' events, for reuse
   ~ReadPool() {
     for (auto &b : blocks) (void)hipHostFree(b.first);
+    for (hipEvent_t ev : events) (void)hipEventDestroy(ev);
   }
 };
 
@@ -582,6 +588,10 @@ int eff_read_begin(eff_ctx *ctx, eff_buf *buf, size_t off, size_t n, eff_read **
         break;
       }
     }
+    if (!r->pool->events.empty()) {
+      r->ev = r->pool->events.back();
+      r->pool->events.pop_back();
+    }
   }
   if (!r->host) {
     r->cap = n < 65536 ? 65536 : n;
@@ -590,7 +600,7 @@ int eff_read_begin(eff_ctx *ctx, eff_buf *buf, size_t off, size_t n, eff_read **
       return fail(ctx, EFF_E_NOMEM, "pinned read block of %zu bytes", n);
     }
   }
-  hipError_t e = hipEventCreateWithFlags(&r->ev, hipEventDisableTiming);
+  hipError_t e = r->ev ? hipSuccess : hipEventCreateWithFlags(&r->ev, hipEventDisableTiming);
   if (e == hipSuccess && n) e = hipMemcpyAsync(r->host, (const char *)buf->ptr + off, n, hipMemcpyDeviceToHost, ctx->stream);
   if (e == hipSuccess) e = hipEventRecord(r->ev, ctx->stream);
   if (e != hipSuccess) {
@@ -604,7 +614,20 @@ int eff_read_begin(eff_ctx *ctx, eff_buf *buf, size_t off, size_t n, eff_read **
 int eff_read_end(eff_read *r, void *dst) {
   if (!r || (!dst && r->n)) return EFF_E_INVALID;
   hipError_t e = hipSetDevice(r->device);
-  if (e == hipSuccess) e = hipEventSynchronize(r->ev);
+  // A readback in a decode loop usually ends within microseconds of the call:
+  // the copy is polled for up to kReadSpinNs before the blocking wait, whose
+  // wake-up would otherwise add to every token.
+  if (e == hipSuccess) {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (;;) {
+      e = hipEventQuery(r->ev);
+      if (e != hipErrorNotReady) break;
+      if (std::chrono::steady_clock::now() - t0 > std::chrono::nanoseconds(kReadSpinNs)) {
+        e = hipEventSynchronize(r->ev);
+        break;
+      }
+    }
+  }
   if (e != hipSuccess) {
     r->rc = EFF_E_DEVICE;
     r->error = std::string("read: ") + hipGetErrorString(e);
@@ -614,19 +637,29 @@ int eff_read_end(eff_read *r, void *dst) {
   return EFF_OK;
 }
 
+int eff_read_poll(eff_read *r) {
+  if (!r) return EFF_E_INVALID;
+  hipError_t e = hipSetDevice(r->device);
+  if (e == hipSuccess) e = hipEventQuery(r->ev);
+  if (e == hipSuccess) return 1;
+  if (e == hipErrorNotReady) return 0;
+  r->rc = EFF_E_DEVICE;
+  r->error = std::string("read: ") + hipGetErrorString(e);
+  return r->rc;
+}
+
 const char *eff_read_error(const eff_read *r) { return r ? r->error.c_str() : "no read"; }
 
 int eff_read_release(eff_read *r) {
   if (!r) return EFF_E_INVALID;
   (void)hipSetDevice(r->device);
-  if (r->ev) {
-    (void)hipEventSynchronize(r->ev);
-    (void)hipEventDestroy(r->ev);
-  }
-  if (r->host) {
+  const bool done = !r->ev || hipEventSynchronize(r->ev) == hipSuccess;
+  {
     std::lock_guard<std::mutex> lk(r->pool->mu);
-    r->pool->blocks.push_back({r->host, r->cap});
+    if (r->host) r->pool->blocks.push_back({r->host, r->cap});
+    if (r->ev && done) r->pool->events.push_back(r->ev);   // completed: recorded again by a later read
   }
+  if (r->ev && !done) (void)hipEventDestroy(r->ev);
   delete r;   // the pool goes with its last owner (context or ticket)
   return EFF_OK;
 }

@@ -88,6 +88,7 @@ def lib():
         "eff_buf_copy": ([p, p, sz, p, sz, sz], i32),
         "eff_read_begin": ([p, p, sz, sz, ctypes.POINTER(p)], i32),
         "eff_read_end": ([p, p], i32),
+        "eff_read_poll": ([p], i32),
         "eff_read_error": ([p], ctypes.c_char_p),
         "eff_read_release": ([p], i32),
         "eff_bytes_reordered": ([i32, u32], sz),
@@ -131,7 +132,7 @@ EXPORTED = ("eff_type_from_name eff_type_name eff_type_geometry eff_init eff_shu
             "eff_stream eff_set_stream eff_sync eff_set_option eff_get_stats eff_buf_alloc eff_buf_wrap "
             "eff_buf_free eff_buf_retire eff_graph_begin eff_graph_end eff_graph_launch eff_graph_nodes "
             "eff_graph_destroy eff_buf_size eff_buf_device_ptr eff_buf_write eff_buf_read eff_buf_copy "
-            "eff_read_begin eff_read_end eff_read_error eff_read_release "
+            "eff_read_begin eff_read_end eff_read_poll eff_read_error eff_read_release "
             "eff_bytes_reordered eff_bytes_buffer_r eff_blocks_from_buffer eff_scales_from eff_buf_mark_r "
             "eff_buf_blocks_r eff_buf_write_r eff_repack eff_unrepack eff_quantize eff_fill_normal eff_qmatmul eff_qgemv "
             "eff_qgemm eff_qgemm_planned eff_gemm_x_layout eff_gemm_prepare_x eff_qgemm_prepared eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_noalloc eff_qgemv_topk eff_topk_out_bytes eff_read_floor").split()

@@ -208,6 +208,11 @@ int eff_buf_read(eff_ctx *ctx, eff_buf *buf, size_t offset, void *dst, size_t n)
  * are described by eff_read_error (the context's message is not touched). */
 int eff_read_begin(eff_ctx *ctx, eff_buf *buf, size_t offset, size_t n, eff_read **out);
 int eff_read_end(eff_read *r, void *dst);
+/* Without waiting: 1 once the ticket's copy has completed (eff_read_end
+ * then returns at once), 0 while it is in flight, negative on a device error
+ * (described by eff_read_error). Lets a host poll from its own loop instead
+ * of blocking a thread. */
+int eff_read_poll(eff_read *r);
 const char *eff_read_error(const eff_read *r);
 int eff_read_release(eff_read *r);
 

@@ -113,3 +113,26 @@ def test_read_ticket_outlives_its_context(eff):
     c.close()
     assert np.array_equal(finish(), data)
     assert np.array_equal(finish2(), data[16:32])
+
+
+def test_read_poll_then_end(ctx, eff):
+    """eff_read_poll answers without waiting (0 while the copy is in flight,
+    1 once it has completed) and eff_read_end then gives the bytes."""
+    import ctypes
+    data = np.arange(1 << 20, dtype=np.uint32)
+    b = ctx.upload(data)
+    r = ctypes.c_void_p()
+    ctx._check(eff.lib().eff_read_begin(ctx.h, b.handle, 0, data.nbytes, ctypes.byref(r)))
+    seen = set()
+    while True:
+        rc = eff.lib().eff_read_poll(r)
+        assert rc in (0, 1), rc
+        seen.add(rc)
+        if rc == 1:
+            break
+    assert 1 in seen
+    out = np.empty_like(data)
+    assert eff.lib().eff_read_end(r, out.ctypes.data) == 0
+    assert eff.lib().eff_read_release(r) == 0
+    assert np.array_equal(out, data)
+    b.free()
