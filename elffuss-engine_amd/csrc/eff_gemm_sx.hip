@@ -433,9 +433,10 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
   uint8_t *const xfr = xw + 8u * 1024u;
   float *const xps = (float *)(xfr + NS * kSxFxSlot);
   const rsrc_t fsrc = make_rsrc(xf, (uint64_t)tokens * wv.k * 4u);
-  // the lane's fragment row, and whether it is a row of tokens 0..7
+  // the lane's fragment row: lanes of tokens 8..15 read the row of token
+  // t - 8 (a D row depends only on its own A row, and those tokens' sums are
+  // never written), so that every read is unmasked and can be issued early
   const uint32_t frow = 16u * (lane >> 5) + 8u * ((lane >> 4) & 1u) + (lane & 7u);
-  const bool fval = (lane & 15u) < 8u;
   if constexpr (FX) {
     // the rows of tokens past `tokens` and their scales stay zero
     for (uint32_t o = 16u * lane; o < NS * kSxFxSlot + 64u; o += 1024u) *(u32x4 *)(xfr + o) = u32x4{0u, 0u, 0u, 0u};
@@ -469,6 +470,7 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
       return (((tg * TT + tt) * nb + bi) * NS + s) * 1024u;
     };
     u32x4 A[FX ? 1 : P][TT];
+    half8 xfa[FX ? 16 : 1];   // FX: the block's 16 x fragments, read from LDS at once
     half8 am[TT];
     float4 pa[TT], pb[TT];
     if constexpr (FX) {
@@ -481,10 +483,11 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
       // all 8 rows every block (tokens past `tokens` read zeros and give zero rows)
       sx_fill8<TYPE>(v, lane, xfr, xps);
       am[0] = half8{0, 0, 0, 0, 0, 0, 0, 0};
-      if constexpr (W::MINS)
-        am[0] = fval ? *(const half8 *)(xfr + sx_fx_at(16u, frow)) : am[0];
+      if constexpr (W::MINS) am[0] = *(const half8 *)(xfr + sx_fx_at(16u, frow));
       pa[0] = *(const float4 *)(xps + 4u * h);
       pb[0] = *(const float4 *)(xps + 8u + 4u * h);
+#pragma unroll
+      for (uint32_t st = 0; st < 16u; ++st) xfa[st] = *(const half8 *)(xfr + sx_fx_at(st, frow));
       wait_vm<0>();
     } else {
     // (each group of loads is followed by a compiler memory barrier, which
@@ -529,8 +532,7 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
       for (int f = 0; f < RF; ++f) B[f] = w[f].step(rp[f], (int)s, h, tab);
       half8 a8[TT];
       if constexpr (FX) {
-        const half8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-        a8[0] = fval ? *(const half8 *)(xfr + sx_fx_at(s, frow)) : z;
+        a8[0] = xfa[s];
       } else {
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt) a8[tt] = __builtin_bit_cast(half8, A[s % P][tt]);
