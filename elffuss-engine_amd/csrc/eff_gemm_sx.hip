@@ -271,6 +271,18 @@ template <> struct SxW<Q2_K> {
     const uint32_t v0 = (p[0] >> (2 * g)) & 0x03030303u, v1 = (p[1] >> (2 * g)) & 0x03030303u;
     return dec_scaled(v0, v1, byte_of(sc, (uint32_t)s) & 15u);
   }
+  // the qs dwords every step of lane half h reads: pr[4 n + 2 h' + i]
+  static constexpr int NP = 8;
+  __device__ void preload(const uint32_t *r, uint32_t h, uint32_t (&pr)[NP]) const {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) pr[i] = r[4 + 8 * (i >> 2) + 4 * ((i >> 1) & 1) + 2u * h + (i & 1)];
+  }
+  __device__ half8 step_pre(const uint32_t (&pr)[NP], int s, uint32_t, const uint32_t *) const {
+    const int n = s >> 3, hp = s & 1, g = (s >> 1) & 3;
+    const uint32_t v0 = (pr[4 * n + 2 * hp] >> (2 * g)) & 0x03030303u;
+    const uint32_t v1 = (pr[4 * n + 2 * hp + 1] >> (2 * g)) & 0x03030303u;
+    return dec_scaled(v0, v1, byte_of(sc, (uint32_t)s) & 15u);
+  }
   __device__ half8 mins(uint32_t h) const {
     const uint32_t w0 = h ? sc[2] : sc[0], w1 = h ? sc[3] : sc[1];
     return dec_plain((w0 >> 4) & 0x0F0F0F0Fu, (w1 >> 4) & 0x0F0F0F0Fu);
@@ -303,6 +315,18 @@ template <> struct SxW<Q4_K> {
     const int j = s >> 2, nib = (s >> 1) & 1;
     const uint32_t *p = r + 4 + 8 * j + 4 * (s & 1) + 2u * h;
     const uint32_t v0 = (p[0] >> (4 * nib)) & 0x0F0F0F0Fu, v1 = (p[1] >> (4 * nib)) & 0x0F0F0F0Fu;
+    return dec_scaled(v0, v1, scale((uint32_t)s >> 1));
+  }
+  // the qs dwords every step of lane half h reads: pr[4 j + 2 (s % 2) + i]
+  static constexpr int NP = 16;
+  __device__ void preload(const uint32_t *r, uint32_t h, uint32_t (&pr)[NP]) const {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) pr[i] = r[4 + 8 * (i >> 2) + 4 * ((i >> 1) & 1) + 2u * h + (i & 1)];
+  }
+  __device__ half8 step_pre(const uint32_t (&pr)[NP], int s, uint32_t, const uint32_t *) const {
+    const int j = s >> 2, nib = (s >> 1) & 1;
+    const uint32_t v0 = (pr[4 * j + 2 * (s & 1)] >> (4 * nib)) & 0x0F0F0F0Fu;
+    const uint32_t v1 = (pr[4 * j + 2 * (s & 1) + 1] >> (4 * nib)) & 0x0F0F0F0Fu;
     return dec_scaled(v0, v1, scale((uint32_t)s >> 1));
   }
   __device__ half8 mins(uint32_t h) const {
@@ -347,6 +371,27 @@ template <> struct SxW<IQ2_XXS> {
     return half8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
   }
   __device__ half8 mins(uint32_t) const { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
+  // the block's 17 dwords from the one holding its first group (dword
+  // (a + 2) / 4 of the row; the stage's slack covers the last)
+  static constexpr int NP = 17;
+  __device__ void preload(const uint32_t *r, uint32_t, uint32_t (&pr)[NP]) const {
+    const uint32_t *p = r + ((a + 2u) >> 2);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) pr[i] = p[i];
+  }
+  __device__ half8 step_pre(const uint32_t (&pr)[NP], int s, uint32_t h, const uint32_t *tab) const {
+    const uint32_t ib = (uint32_t)s >> 1, sh = (a + 2u) & 3u;
+    const uint32_t w0 = pr[2 * ib], w1 = pr[2 * ib + 1], w2 = pr[2 * ib + 2];
+    const uint32_t a0 = __builtin_amdgcn_alignbyte(w1, w0, sh), a1 = __builtin_amdgcn_alignbyte(w2, w1, sh);
+    const uint32_t l = 2u * ((uint32_t)s & 1u) + h;
+    const uint32_t gi = (a0 >> (8u * l)) & 0xFFu, sg = (a1 >> (7u * l)) & 127u;
+    const u32x4 g = *(const u32x4 *)(tab + 4u * gi), m = *(const u32x4 *)(tab + 1024u + 4u * sg);
+    const _Float16 c = (_Float16)(float)(2u * (a1 >> 28) + 1u);
+    const half2v c2 = {c, c};
+    const half2v v0 = __builtin_bit_cast(half2v, g.x ^ m.x) * c2, v1 = __builtin_bit_cast(half2v, g.y ^ m.y) * c2;
+    const half2v v2 = __builtin_bit_cast(half2v, g.z ^ m.z) * c2, v3 = __builtin_bit_cast(half2v, g.w ^ m.w) * c2;
+    return half8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
+  }
 };
 
 constexpr uint32_t kSxTab = 6144;  // IQ2_XXS tables in LDS
@@ -517,19 +562,28 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
 
     W w[RF];
     const uint32_t *rp[RF];
+    // PRE: the weight dwords of all 16 steps in registers before the steps
+    // (whose prefetch of x fragments keeps the compiler from hoisting LDS
+    // reads); the 4-tile kernels have no registers to spare
+    constexpr bool PRE = !FX && TT <= 2;
+    uint32_t pr[RF][PRE ? W::NP : 1];
 #pragma unroll
     for (int f = 0; f < RF; ++f) {
       const uint32_t row = min(r0 + 32u * f + j, rows - 1u);
       const uint32_t a = (row * rb + bo) & 3u;
       rp[f] = (const uint32_t *)(stage + 4u * W::ST * (32u * f + j));
       w[f].block(rp[f], a);
+      if constexpr (PRE) w[f].preload(rp[f], h, pr[f]);
     }
     float16v D[TT][RF];
 #pragma unroll
     for (uint32_t s = 0; s < 16u; ++s) {
       half8 B[RF];
 #pragma unroll
-      for (int f = 0; f < RF; ++f) B[f] = w[f].step(rp[f], (int)s, h, tab);
+      for (int f = 0; f < RF; ++f) {
+        if constexpr (PRE) B[f] = w[f].step_pre(pr[f], (int)s, h, tab);
+        else B[f] = w[f].step(rp[f], (int)s, h, tab);
+      }
       half8 a8[TT];
       if constexpr (FX) {
         a8[0] = xfa[s];
