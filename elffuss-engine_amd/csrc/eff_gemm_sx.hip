@@ -79,10 +79,19 @@ __global__ __launch_bounds__(256) void k_sx_prep(const float *__restrict__ x, ui
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
   if (t < tokens) v = *(const float4 *)(x + (uint64_t)t * k + 256u * bi + 4u * lane);
   const bool fin = isfinite(v.x) && isfinite(v.y) && isfinite(v.z) && isfinite(v.w);
-  float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  m = fin ? m : INFINITY;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  // the block's max |x| as u32 bit patterns (non-negative floats order as
+  // their bits; a non-finite value counts as infinity): DPP within rows,
+  // then rows 1 and 3 (row_bcast:15), row 3 (row_bcast:31), lane 63
+  uint32_t mb = max(max(__float_as_uint(fabsf(v.x)), __float_as_uint(fabsf(v.y))),
+                    max(__float_as_uint(fabsf(v.z)), __float_as_uint(fabsf(v.w))));
+  mb = fin ? mb : 0x7F800000u;
+  mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0xB1, 0xF, 0xF, false));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x4E, 0xF, 0xF, false));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x141, 0xF, 0xF, false));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x140, 0xF, 0xF, false));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x142, 0xA, 0xF, false));
+  mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x143, 0xC, 0xF, false));
+  const float m = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)mb, 63));
   const bool ok = m < INFINITY;
   int e = 0;
   if (ok && m > 0.f) (void)frexpf(m, &e);  // m < 2^e
@@ -104,10 +113,13 @@ __global__ __launch_bounds__(256) void k_sx_prep(const float *__restrict__ x, ui
   if constexpr (TYPE != IQ2_XXS) {
     // group sums (16 values for Q2_K, 32 for Q4_K), scaled to the range of x
     constexpr uint32_t GL = TYPE == Q2_K ? 4u : 8u;  // lanes per group
+    // the group's lanes: own + lane ^ 1, + lane ^ 2 (quad permutes), and
+    // for 8 lanes + the other quad's sum (row_half_mirror: lane 7 - i)
     float sum = (xs[0] + xs[1]) + (xs[2] + xs[3]);
-    sum += __shfl_xor(sum, 1);
-    sum += __shfl_xor(sum, 2);
-    if (GL == 8u) sum += __shfl_xor(sum, 4);
+    sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0xB1, 0xF, 0xF, false));
+    sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0x4E, 0xF, 0xF, false));
+    if (GL == 8u)
+      sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0x141, 0xF, 0xF, false));
     const float sp = sum * (TYPE == Q2_K ? 0.0625f : 0.03125f);
     const _Float16 shi = (_Float16)sp, slo = (_Float16)(sp - (float)shi);
     uint8_t *ms = blk + 16u * 1024u;
