@@ -153,6 +153,33 @@ def read_floor_ms(torch, ctx, cfg, sink, steps):
                for wg, un in READ_SHAPES)
 
 
+def vendor_gemm_ms(torch, m, k, n, reps=50):
+    """ms of torch.matmul on fp16 operands [m, k] x [k, n] (hipBLASLt on ROCm), replayed `reps` times in a
+    graph, median of 5: the library's own speed on this box for a shape the quantized GEMM runs, measured
+    only as a calibration (nothing of the quantized path uses it)."""
+    a = torch.randn(m, k, device="cuda", dtype=torch.float16)
+    b = torch.randn(k, n, device="cuda", dtype=torch.float16)
+    for _ in range(5):
+        c = a @ b
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            c = a @ b
+    g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(5):
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        g.replay()
+        s1.record()
+        torch.cuda.synchronize()
+        ts.append(s0.elapsed_time(s1) / reps)
+    del g, a, b, c
+    return sorted(ts)[2]
+
+
 def rotation(cfg, steps):
     """What the timed steps of `cfg` read: copies, bytes, reuse distance."""
     per = cfg.w_bytes
@@ -481,6 +508,12 @@ def main():
                 f_ms = read_floor_ms(torch, ctx, cfg, sink, steps)
                 sweep[key]["read_floor_us"] = round(f_ms * 1e3, 2)
                 sweep[key]["frac_of_read_floor"] = round(f_ms / t_ms, 4)
+            if bound == "mfma":
+                # the vendor's fp16 GEMM of the same shape (no dequantization, no x conversion), as a
+                # calibration beside the roofline
+                v_ms = vendor_gemm_ms(torch, m, kk, r)
+                sweep[key]["vendor_fp16_gemm_us"] = round(v_ms * 1e3, 2)
+                sweep[key]["frac_of_vendor"] = round(v_ms / t_ms, 4)
             cfg.free()
             print(f"# {key}: {sweep[key]}", file=sys.stderr, flush=True)
 
