@@ -223,12 +223,13 @@ int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_
 // reference's fp16 GEMMs accept (GEMM2_TIPOS, kernels.gemm2.wgsl.js:51).
 bool router_gemm_type(int type) { return type == EFF_TYPE_Q8_0 || type == EFF_TYPE_Q8_0R; }
 
-// The split-x product from 8 tokens (Q4_K: 9); below, the int8 matrix-core
-// GEMVs, which are as accurate and were faster at 4 tokens (C5 shapes: 6.0 /
-// 6.9 / 6.2 us against 8.3 / 8.3 / 8.9 for Q2_K / IQ2_XXS / Q4_K) and about
-// even at 8 (Q4_K: 8.2 against 8.9).
+// The split-x product from 5 tokens (Q4_K: 9); below, the int8 matrix-core
+// GEMVs, which are as accurate and faster at 4 tokens (C5 shapes: 5.75 / 6.72
+// us against 7.32 / 7.33 for Q2_K / IQ2_XXS); from 5 tokens split-x is as fast
+// or faster for those two types (5: 7.42 / 7.42 against 7.49 / 8.62; 7: 7.52 /
+// 7.56 against 7.75 / 8.90), for Q4_K from 9 (8: 8.66 against 7.90).
 bool sx_routes(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens) {
-  const int64_t lo = ctx->sx_min_tokens ? ctx->sx_min_tokens : (wv.type == Q4_K ? 9 : 8);
+  const int64_t lo = ctx->sx_min_tokens ? ctx->sx_min_tokens : (wv.type == Q4_K ? 9 : 5);
   return ctx->gemv_kernel == 0 && sx_applies(wv, tokens) && (int64_t)tokens >= lo;
 }
 

@@ -56,7 +56,7 @@ extern "C" {
                                        8 waves, 2: 64 rows x 4 waves, 3: 64 rows x 4 waves with k halves in two
                                        workgroups added into y */
 #define EFF_OPT_SPLIT_MIN_TOKENS 5  /* Q2_K, Q4_K, IQ2_XXS: tokens >= this run the split-x product, fewer the int8
-                                       matrix-core GEMVs (0: automatic, 8 and 9 for Q4_K (default); else >= 4) */
+                                       matrix-core GEMVs (0: automatic, 5 and 9 for Q4_K (default); else >= 4) */
 #define EFF_OPT_GEMM_CONFIG      6  /* Q8_0 GEMM from 256 tokens, tiles (tuning; tokens x rows, waves along tokens x
                                        rows, LDS stages): 0 automatic (default), 1: 256x256 1x4 3, 2: 128x128 1x4 3,
                                        3: 128x128 1x4 6, 4: 64x128 1x4 4, 5: 128x256 1x4 4, 6: 256x128 2x2 3; every
@@ -280,7 +280,7 @@ int eff_fill_normal(uint32_t seed, float sigma, float *dst, size_t n);
 
 /* Y[tokens][rows] = W (rows x k, quantized) . X[tokens][k]; X and Y are f32.
  * Router of quant.matmul (ops.js:827-1101): tokens <= GEMV max -> GEMV;
- * Q2_K, Q4_K, IQ2_XXS from EFF_OPT_SPLIT_MIN_TOKENS (8; 9 for Q4_K) -> split-x
+ * Q2_K, Q4_K, IQ2_XXS from EFF_OPT_SPLIT_MIN_TOKENS (5; 9 for Q4_K) -> split-x
  * product (f32-accurate; fewer tokens run the int8 matrix-core GEMVs, as accurate);
  * Q8_0/Q8_0R at tokens >= GEMM min -> fp16 MFMA GEMM (the reference's
  * DRIFT/GEMM2 types, kernels.drift.wgsl.js:33); otherwise (Q6_K at every

@@ -535,12 +535,12 @@ def test_router_paths_and_stats(ctx, eff, orc):
 
 
 def test_router_split_x_threshold(ctx, eff, orc):
-    """Q2_K: 7 tokens run the int8 matrix-core GEMV, 8 the split-x product, both
+    """Q2_K: 4 tokens run the int8 matrix-core GEMV, 5 the split-x product, both
     against the f64 oracle; the option moves the threshold and refuses 1..3."""
     rows, k = 96, 512
     t, data, gguf, n = make_weights(eff, "Q2_K", rows, k, 95)
     wb = ctx.upload(data)
-    for tokens, low, split in ((7, 0, 0), (8, 0, 1), (7, 4, 1)):
+    for tokens, low, split in ((4, 0, 0), (5, 0, 1), (7, 8, 0), (4, 4, 1)):
         x = eff.fill_normal(96 + tokens, 1.0, tokens * k)
         xb, yb = ctx.upload(x), ctx.alloc(tokens * rows * 4)
         ctx.set_option(eff.OPT_SPLIT_MIN_TOKENS, low)
