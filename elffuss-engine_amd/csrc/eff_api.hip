@@ -233,13 +233,22 @@ bool sx_routes(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens) {
   return ctx->gemv_kernel == 0 && sx_applies(wv, tokens) && (int64_t)tokens >= lo;
 }
 
+// The 16-row GEMV computes tokens in groups of 4: at 5 and 6 tokens it pays
+// for 8, and the 4-row GEMV (which scales with the token count) is faster
+// (µs, 5 / 6 tokens, 16-row against 4-row: Q8_0 8192 x 2048 9.00 / 9.24
+// against 8.21 / 8.70, 4096 x 4096 10.63 / 10.98 against 9.59 / 10.63; Q4_K
+// 8192 x 2048 7.46 / 7.73 against 6.69 / 7.18; Q6_K 4096 x 4096 11.80 /
+// 12.17 against 11.10 / 12.07); at 4, 7 and 8 tokens the 16-row GEMV is as
+// fast or faster.
+bool mt_routes(uint32_t tokens) { return tokens != 5u && tokens != 6u; }
+
 int run_gemv(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
   if (sx_routes(ctx, wv, tokens)) return run_sx(ctx, wv, x, y, tokens);
   GemvPlan p;
   hipError_t e;
   if (ctx->gemv_kernel == 0 && gemv_rows_applies(wv, tokens)) {
     e = launch_gemv_rows(wv, x, y, ctx->stream);
-  } else if (ctx->gemv_kernel == 0 && gemv_mt_plan(wv, tokens, p)) {
+  } else if (ctx->gemv_kernel == 0 && mt_routes(tokens) && gemv_mt_plan(wv, tokens, p)) {
     e = launch_gemv_mt(wv, x, y, tokens, p, ctx->stream);
   } else if (ctx->gemv_kernel == 0 && gemv_mx_plan(wv, tokens, p)) {
     e = launch_gemv_mx(wv, x, y, tokens, p, ctx->stream);
