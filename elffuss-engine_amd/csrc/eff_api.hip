@@ -228,8 +228,13 @@ bool router_gemm_type(int type) { return type == EFF_TYPE_Q8_0 || type == EFF_TY
 // us against 7.32 / 7.33 for Q2_K / IQ2_XXS); from 5 tokens split-x is as fast
 // or faster for those two types (5: 7.42 / 7.42 against 7.49 / 8.62; 7: 7.52 /
 // 7.56 against 7.75 / 8.90), for Q4_K from 9 (8: 8.66 against 7.90).
+// Q8_0 and Q6_K take it from 9 tokens, where the GEMV would run over token
+// groups; Q8_0 only below the fp16 GEMM's threshold (from there the
+// reference's DRIFT path, whose fp16 roundings the GEMM keeps).
 bool sx_routes(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens) {
-  const int64_t lo = ctx->sx_min_tokens ? ctx->sx_min_tokens : (wv.type == Q4_K ? 9 : 5);
+  const int64_t lo = ctx->sx_min_tokens ? ctx->sx_min_tokens
+                                        : (wv.type == Q2_K || wv.type == IQ2_XXS ? 5 : 9);
+  if (router_gemm_type(wv.type) && (int64_t)tokens >= ctx->gemm_min_tokens) return false;
   return ctx->gemv_kernel == 0 && sx_applies(wv, tokens) && (int64_t)tokens >= lo;
 }
 

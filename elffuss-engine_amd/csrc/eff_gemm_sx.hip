@@ -1,16 +1,21 @@
-// Quantized matrix products from 4 tokens up for Q2_K, Q4_K and IQ2_XXS, to
-// f32 accuracy (the reference runs these types through its f32 generic
-// kernel at every token count, ops.js:1013-1099; its f16 GEMMs read Q8_0/Q4_0
+// Quantized matrix products from 4 tokens up for Q2_K, Q4_K, IQ2_XXS, Q8_0
+// and Q6_K, to f32 accuracy (the reference runs the K/IQ types through its f32
+// generic kernel at every token count, ops.js:1013-1099, and Q8_0 below its
+// DRIFT threshold through its f32 tiled GEMM; its f16 GEMMs read Q8_0/Q4_0
 // only, kernels.drift.wgsl.js:33, kernels.gemm2.wgsl.js:51):
 //   Y[t][row] = sum_k W[row][k] X[t][k].
 //
-// Weights. Per 256-weight block the decoders of kernels.wgsl.js:194-250 and
-// 368-396 are an integer u times the block scale, minus a group minimum:
+// Weights. Per 256-weight block the decoders of kernels.wgsl.js:154-396 are
+// an integer u times a scale, minus a group minimum:
 //   Q2_K     w = d (sc & 15) q - dmin (sc >> 4)   u = (sc & 15) q <= 45     (16-weight groups)
 //   Q4_K     w = d sc q - dmin m                  u = sc q        <= 945    (32-weight groups)
 //   IQ2_XXS  w = (d / 8) (2 ls + 1) (+-g)         u = (2 ls + 1)(+-g) <= 1333
-// so  sum_k w x = d sum_k u x - dmin sum_g mn_g S_g,  S_g = sum of x over group g.
-// Every u is an integer below 2048, exact in fp16.
+//   Q8_0     w = d_j q                            u = q, |q| <= 127         (scale d_j per 32)
+//   Q6_K     w = d sc_j (q - 32)                  u = q - 32, |u| <= 32     (scale d sc_j per 16)
+// so for the first three  sum_k w x = d sum_k u x - dmin sum_g mn_g S_g,
+// S_g = sum of x over group g, with one scale per block; Q8_0 and Q6_K keep a
+// scale per 32 or 16 weights (sc_j u can pass 2048 for Q6_K). Every u is an
+// integer below 2048, exact in fp16.
 //
 // x. Per token and block, x is scaled by 2^-e with max|x| < 2^(e) and split
 // into fp16 parts hi = fp16(x 2^(14-e)), lo = fp16(x 2^(14-e) - hi): 22
@@ -24,6 +29,9 @@
 // part. One more MFMA per block forms the minimum sums (A = group sums, B =
 // the group minima), and each block is folded once:
 //   acc += ((D_hi + D_lo) d - (Dm_hi + Dm_lo) dmin') 2^(e - 14).
+// Q8_0 and Q6_K fold each group of FG steps (2: a 32-weight block, 1: 16
+// weights) with its own scale, starting the accumulation over after each:
+//   acc += (D_hi + D_lo) s_j 2^(e - 14).
 //
 // Workgroup: NW waves over the same 32 RF weight rows and TT tiles of 16
 // tokens, each wave on its own k blocks; the waves' sums are added in a fixed
@@ -50,9 +58,15 @@ namespace {
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 
+// Types with group minima (their group sums of x form a 17th slot)
+template <int TYPE>
+constexpr bool sx_mins() {
+  return TYPE == Q2_K || TYPE == Q4_K;
+}
+
 template <int TYPE>
 constexpr uint32_t sx_slots() {  // x slots of 1 KB per (token tile, block): 16 steps (+ group sums)
-  return TYPE == IQ2_XXS ? 16u : 17u;
+  return sx_mins<TYPE>() ? 17u : 16u;
 }
 
 // ---------------------------------------------------------------------------
@@ -110,7 +124,7 @@ __global__ __launch_bounds__(256) void k_sx_prep(const float *__restrict__ x, ui
   const uint32_t hf = (lane >> 1) & 1u, q = lane & 1u;
   *(half4 *)(slot + 16u * (32u * hf + tl) + 8u * q) = hi;
   *(half4 *)(slot + 16u * (32u * hf + 16u + tl) + 8u * q) = lo;
-  if constexpr (TYPE != IQ2_XXS) {
+  if constexpr (sx_mins<TYPE>()) {
     // group sums (16 values for Q2_K, 32 for Q4_K), scaled to the range of x
     constexpr uint32_t GL = TYPE == Q2_K ? 4u : 8u;  // lanes per group
     // the group's lanes: own + lane ^ 1, + lane ^ 2 (quad permutes), and
@@ -199,7 +213,7 @@ __device__ __forceinline__ void sx_fill8(const float4 (&v)[8], uint32_t lane, ui
     *(half4 *)(fr + sx_fx_at(st, 16u * hf + t) + 8u * q) = hi;
     *(half4 *)(fr + sx_fx_at(st, 16u * hf + 8u + t) + 8u * q) = lo;
   }
-  if constexpr (TYPE != IQ2_XXS) {
+  if constexpr (sx_mins<TYPE>()) {
     static_assert(TYPE == Q2_K, "16-value group sums");
     // group sums: the 4 lanes of a group, (own + lane ^ 1) + (lane ^ 2)'s pair
     float sum[8];
@@ -268,6 +282,7 @@ template <int TYPE> struct SxW;
 template <> struct SxW<Q2_K> {
   static constexpr uint32_t BB = 84, DW = 21, ST = 21;
   static constexpr bool MINS = true;
+  static constexpr int FG = 16;  // steps per fold (one scale for the block)
   uint32_t sc[4];
   float d, dm;
   __device__ void block(const uint32_t *r, uint32_t) {
@@ -277,6 +292,7 @@ template <> struct SxW<Q2_K> {
     d = h2f(w & 0xFFFFu);
     dm = 16.f * h2f(w >> 16);  // group sums are stored divided by 16
   }
+  __device__ float scale(int) const { return d; }
   __device__ half8 step(const uint32_t *r, int s, uint32_t h, const uint32_t *) const {
     const int n = s >> 3, hp = s & 1, g = (s >> 1) & 3;
     const uint32_t *p = r + 4 + 8 * n + 4 * hp + 2u * h;
@@ -307,6 +323,7 @@ template <> struct SxW<Q2_K> {
 template <> struct SxW<Q4_K> {
   static constexpr uint32_t BB = 144, DW = 36, ST = 37;
   static constexpr bool MINS = true;
+  static constexpr int FG = 16;
   uint32_t q[3];
   float d, dm;
   __device__ void block(const uint32_t *r, uint32_t) {
@@ -317,6 +334,7 @@ template <> struct SxW<Q4_K> {
     q[1] = r[2];
     q[2] = r[3];
   }
+  __device__ float scale(int) const { return d; }
   __device__ uint32_t scale(uint32_t i) const {
     return i < 4u ? byte_of(q, i) & 63u : (byte_of(q, i + 4u) & 15u) | ((byte_of(q, i - 4u) >> 6) << 4);
   }
@@ -361,6 +379,7 @@ template <> struct SxW<Q4_K> {
 template <> struct SxW<IQ2_XXS> {
   static constexpr uint32_t BB = 66, DW = 17, ST = 17;
   static constexpr bool MINS = false;
+  static constexpr int FG = 16;
   uint32_t a;  // byte offset of the block in r[0] (0 or 2)
   float d, dm;
   __device__ void block(const uint32_t *r, uint32_t off) {
@@ -368,6 +387,7 @@ template <> struct SxW<IQ2_XXS> {
     d = 0.125f * h2f(off ? (r[0] >> 16) : (r[0] & 0xFFFFu));
     dm = 0.f;
   }
+  __device__ float scale(int) const { return d; }
   __device__ half8 step(const uint32_t *r, int s, uint32_t h, const uint32_t *tab) const {
     const uint32_t ib = (uint32_t)s >> 1, o = a + 2u + 8u * ib, sh = o & 3u;
     const uint32_t *p = r + (o >> 2);
@@ -404,6 +424,90 @@ template <> struct SxW<IQ2_XXS> {
     const half2v v2 = __builtin_bit_cast(half2v, g.z ^ m.z) * c2, v3 = __builtin_bit_cast(half2v, g.w ^ m.w) * c2;
     return half8{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
   }
+};
+
+// 8 signed bytes q -> q as fp16 (exact): 1024 + (q + 128) - 1152
+__device__ __forceinline__ half8 dec_signed(uint32_t v0, uint32_t v1) {
+  const half2v o2 = {(_Float16)-1152.f, (_Float16)-1152.f};
+  v0 ^= 0x80808080u;
+  v1 ^= 0x80808080u;
+  const half2v a = h1024_lo(v0) + o2, b = h1024_hi(v0) + o2, c = h1024_lo(v1) + o2, d = h1024_hi(v1) + o2;
+  return half8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+// Q8_0, 256 weights = 8 blocks of 34 bytes, d | q[32] (kernels.wgsl.js:154-160).
+// Step s: block s / 2, quants 16 (s % 2) + 8 h .. + 7 (bytes 34 (s / 2) + 2 +
+// 16 (s % 2) + 8 h ..), u = q. The 8 blocks have their own d: one fold per
+// 2 steps (FG = 2), with that block's d. The 256 weights are 4-byte aligned
+// (rows are 272 (k / 256) bytes); the quants of odd blocks are too, those of
+// even blocks 2 bytes past a dword.
+template <> struct SxW<Q8_0> {
+  static constexpr uint32_t BB = 272, DW = 68, ST = 69;
+  static constexpr bool MINS = false;
+  static constexpr int FG = 2;
+  static constexpr int NP = 0;  // steps read the stage (no register copy of the block)
+  float d, dm, ds[8];
+  __device__ void block(const uint32_t *r, uint32_t) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t w = r[(34 * j) >> 2];
+      ds[j] = h2f((j & 1) ? (w >> 16) : (w & 0xFFFFu));
+    }
+    d = 1.f;
+    dm = 0.f;
+  }
+  __device__ float scale(int g) const { return ds[g]; }
+  __device__ half8 step(const uint32_t *r, int s, uint32_t h, const uint32_t *) const {
+    const uint32_t o = 34u * (uint32_t)(s >> 1) + 2u + 16u * (uint32_t)(s & 1) + 8u * h, sh = o & 3u;
+    const uint32_t *p = r + (o >> 2);
+    return dec_signed(__builtin_amdgcn_alignbyte(p[1], p[0], sh), __builtin_amdgcn_alignbyte(p[2], p[1], sh));
+  }
+  __device__ half8 mins(uint32_t) const { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
+  __device__ void preload(const uint32_t *, uint32_t, uint32_t (&)[1]) const {}
+  __device__ half8 step_pre(const uint32_t (&)[1], int, uint32_t, const uint32_t *) const { return half8{}; }
+};
+
+// Q6_K, 210 bytes: ql[128] | qh[64] | scales[16] (int8) | d
+// (kernels.wgsl.js:269-330). Step s = weights 16 s .. 16 s + 15 of the block:
+// n = s / 8, g = (s / 2) % 4, ql bytes 64 n + 32 (g % 2) + 16 (s % 2) + 8 h ..
+// (nibble g / 2), qh bytes 128 + 32 n + 16 (s % 2) + 8 h .. (bits 2 g), scale
+// s; w = d sc (q - 32). u = q - 32 is exact in fp16 but sc u need not be (up to
+// 127 x 32), so each step is folded with its own d sc (FG = 1). Blocks start
+// at 2-byte aligned offsets (`a`, 0 or 2, as IQ2_XXS).
+template <> struct SxW<Q6_K> {
+  static constexpr uint32_t BB = 210, DW = 53, ST = 53;
+  static constexpr bool MINS = false;
+  static constexpr int FG = 1;
+  static constexpr int NP = 0;
+  uint32_t a, sc[4];
+  float d, dm;
+  __device__ void block(const uint32_t *r, uint32_t off) {
+    a = off;
+    const uint32_t *p = r + ((off + 192u) >> 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[i] = __builtin_amdgcn_alignbyte(p[i + 1], p[i], off);
+    const uint32_t w = r[(off + 208u) >> 2];
+    d = h2f(off ? (w >> 16) : (w & 0xFFFFu));
+    dm = 0.f;
+  }
+  __device__ float scale(int g) const { return d * (float)(int8_t)byte_of(sc, (uint32_t)g); }
+  __device__ half8 step(const uint32_t *r, int s, uint32_t h, const uint32_t *) const {
+    const uint32_t n = (uint32_t)s >> 3, g = ((uint32_t)s >> 1) & 3u, o = 16u * ((uint32_t)s & 1u) + 8u * h;
+    const uint32_t *pq = r + ((a + 64u * n + 32u * (g & 1u) + o) >> 2);
+    const uint32_t *ph = r + ((a + 128u + 32u * n + o) >> 2);
+    const uint32_t q0 = __builtin_amdgcn_alignbyte(pq[1], pq[0], a), q1 = __builtin_amdgcn_alignbyte(pq[2], pq[1], a);
+    const uint32_t h0 = __builtin_amdgcn_alignbyte(ph[1], ph[0], a), h1 = __builtin_amdgcn_alignbyte(ph[2], ph[1], a);
+    const uint32_t ls = 4u * (g >> 1), hs = 2u * g;
+    const uint32_t u0 = ((q0 >> ls) & 0x0F0F0F0Fu) | (((h0 >> hs) & 0x03030303u) << 4);
+    const uint32_t u1 = ((q1 >> ls) & 0x0F0F0F0Fu) | (((h1 >> hs) & 0x03030303u) << 4);
+    // 1024 + q - 1056 = q - 32
+    const half2v o2 = {(_Float16)-1056.f, (_Float16)-1056.f};
+    const half2v e0 = h1024_lo(u0) + o2, e1 = h1024_hi(u0) + o2, e2 = h1024_lo(u1) + o2, e3 = h1024_hi(u1) + o2;
+    return half8{e0.x, e0.y, e1.x, e1.y, e2.x, e2.y, e3.x, e3.y};
+  }
+  __device__ half8 mins(uint32_t) const { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
+  __device__ void preload(const uint32_t *, uint32_t, uint32_t (&)[1]) const {}
+  __device__ half8 step_pre(const uint32_t (&)[1], int, uint32_t, const uint32_t *) const { return half8{}; }
 };
 
 constexpr uint32_t kSxTab = 6144;  // IQ2_XXS tables in LDS
@@ -443,8 +547,10 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
   static_assert(!FX || (TT == 1 && KS == 1), "the fused preparation covers one token tile");
   constexpr uint32_t NS = sx_slots<TYPE>();
   // steps of x fragments loaded ahead (Q4_K's 37-dword rows take 19 staging
-  // offsets per lane: 3 steps ahead at 4 token tiles keep it within the VGPRs)
-  constexpr uint32_t P = TT == 1 ? 16u : TT == 2 ? 8u : TYPE == Q4_K ? 3u : 4u;
+  // offsets per lane: 3 steps ahead at 4 token tiles keep it within the VGPRs;
+  // the types folded per group of steps hold more state: fewer steps ahead)
+  constexpr bool MS = W::FG < 16;
+  constexpr uint32_t P = TT == 1 ? 16u : TT == 2 ? (MS ? 4u : 8u) : TYPE == Q4_K ? 3u : MS ? 2u : 4u;
   constexpr uint32_t ROWS = L::ROWS, ND = L::ND;
   __shared__ __align__(16) uint8_t lds_s[FX ? 16u : L::BYTES];
   extern __shared__ __align__(16) uint8_t lds_d[];
@@ -453,7 +559,8 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // KS = 2: workgroup pairs take the two halves of k and add into y
   const uint32_t kh = blockIdx.x % (uint32_t)KS;
-  const uint32_t rows = wv.rows, nb = wv.bpr, r0 = blockIdx.x / (uint32_t)KS * ROWS, tg = blockIdx.y;
+  // nb: blocks of 256 weights per row (Q8_0 rows hold 8 of its 32-weight blocks in each)
+  const uint32_t rows = wv.rows, nb = wv.k / 256u, r0 = blockIdx.x / (uint32_t)KS * ROWS, tg = blockIdx.y;
   const uint32_t rb = (uint32_t)wv.row_bytes;
   uint32_t *tab = (uint32_t *)lds;
   uint8_t *stage = lds + L::TAB + wave * L::SB;
@@ -577,7 +684,7 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
     // PRE: the weight dwords of all 16 steps in registers before the steps
     // (whose prefetch of x fragments keeps the compiler from hoisting LDS
     // reads); the 4-tile kernels have no registers to spare
-    constexpr bool PRE = !FX && TT <= 2;
+    constexpr bool PRE = !FX && TT <= 2 && W::NP > 0;
     uint32_t pr[RF][PRE ? W::NP : 1];
 #pragma unroll
     for (int f = 0; f < RF; ++f) {
@@ -586,6 +693,13 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
       rp[f] = (const uint32_t *)(stage + 4u * W::ST * (32u * f + j));
       w[f].block(rp[f], a);
       if constexpr (PRE) w[f].preload(rp[f], h, pr[f]);
+    }
+    // the tokens' block scales, for the folds
+    float pv[TT][8];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      pv[tt][0] = pa[tt].x; pv[tt][1] = pa[tt].y; pv[tt][2] = pa[tt].z; pv[tt][3] = pa[tt].w;
+      pv[tt][4] = pb[tt].x; pv[tt][5] = pb[tt].y; pv[tt][6] = pb[tt].z; pv[tt][7] = pb[tt].w;
     }
     float16v D[TT][RF];
 #pragma unroll
@@ -613,23 +727,38 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
       for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int f = 0; f < RF; ++f) {
-          const float16v c = s == 0u ? float16v{} : D[tt][f];
+          const float16v c = s % (uint32_t)W::FG == 0u ? float16v{} : D[tt][f];
           D[tt][f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8[tt], B[f], c, 0, 0, 0);
         }
+      // types with several scales per block: the fold of each group of FG steps
+      if constexpr (W::FG < 16) {
+        if (s % (uint32_t)W::FG == (uint32_t)W::FG - 1u) {
+#pragma unroll
+          for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+            for (int f = 0; f < RF; ++f) {
+              const float sc = w[f].scale((int)(s / (uint32_t)W::FG));
+#pragma unroll
+              for (int v = 0; v < 8; ++v)
+                acc[tt][f][v] = __builtin_fmaf((D[tt][f][v] + D[tt][f][v + 8]) * sc, pv[tt][v], acc[tt][f][v]);
+            }
+        }
+      }
     }
-    // minimum sums, scales of the tokens, and the fold of the block
+    // one scale per block: minimum sums, scales of the tokens, and the fold
+    if constexpr (W::FG == 16) {
 #pragma unroll
-    for (uint32_t tt = 0; tt < (uint32_t)TT; ++tt) {
-      const float pv[8] = {pa[tt].x, pa[tt].y, pa[tt].z, pa[tt].w, pb[tt].x, pb[tt].y, pb[tt].z, pb[tt].w};
+      for (uint32_t tt = 0; tt < (uint32_t)TT; ++tt) {
 #pragma unroll
-      for (int f = 0; f < RF; ++f) {
-        float16v Dm{};
-        if constexpr (W::MINS) Dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[tt], w[f].mins(h), float16v{}, 0, 0, 0);
+        for (int f = 0; f < RF; ++f) {
+          float16v Dm{};
+          if constexpr (W::MINS) Dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[tt], w[f].mins(h), float16v{}, 0, 0, 0);
 #pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          float t = (D[tt][f][v] + D[tt][f][v + 8]) * w[f].d;
-          if constexpr (W::MINS) t = __builtin_fmaf(-(Dm[v] + Dm[v + 8]), w[f].dm, t);
-          acc[tt][f][v] = __builtin_fmaf(t, pv[v], acc[tt][f][v]);
+          for (int v = 0; v < 8; ++v) {
+            float t = (D[tt][f][v] + D[tt][f][v + 8]) * w[f].d;
+            if constexpr (W::MINS) t = __builtin_fmaf(-(Dm[v] + Dm[v + 8]), w[f].dm, t);
+            acc[tt][f][v] = __builtin_fmaf(t, pv[tt][v], acc[tt][f][v]);
+          }
         }
       }
     }
@@ -668,15 +797,19 @@ struct SxPlan {
   uint32_t tt, cfg, groups, row_tiles, nbw;
 };
 
-void sx_tiles(uint32_t tokens, uint32_t &tt, uint32_t &groups) {
+// The types folded per group of steps (Q8_0, Q6_K) take at most 2 token tiles
+// per wave: with 4 their folds' state does not fit the registers.
+uint32_t sx_tt_max(int type) { return type == Q8_0 || type == Q6_K ? 2u : 4u; }
+
+void sx_tiles(int type, uint32_t tokens, uint32_t &tt, uint32_t &groups) {
   const uint32_t ttn = (tokens + 15u) / 16u;
-  tt = ttn <= 1u ? 1u : ttn <= 2u ? 2u : 4u;
+  tt = ttn <= 1u ? 1u : ttn <= 2u || sx_tt_max(type) == 2u ? 2u : 4u;
   groups = (ttn + tt - 1u) / tt;
 }
 
 SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg) {
   SxPlan p;
-  sx_tiles(tokens, p.tt, p.groups);
+  sx_tiles(wv.type, tokens, p.tt, p.groups);
   // measured (C5 shapes): 32 rows x 8 waves up to 32 tokens per tile group;
   // 64 rows x 4 waves for 64 once the token groups give it 256 workgroups
   // (M = 96, 128), else 32 x 8 again (M = 48, 64: 13.9 / 14.1 us against
@@ -685,7 +818,7 @@ SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg) {
   p.cfg = cfg ? (uint32_t)(cfg - 1) : (p.tt == 4u && p.groups * rt64 >= 256u ? 1u : 0u);
   const uint32_t rows_per = p.cfg ? 64u : 32u, nw = p.cfg ? 4u : 8u, ks = p.cfg == 2u ? 2u : 1u;
   p.row_tiles = (wv.rows + rows_per - 1u) / rows_per;
-  p.nbw = ((wv.bpr + ks - 1u) / ks + nw - 1u) / nw;
+  p.nbw = ((wv.k / 256u + ks - 1u) / ks + nw - 1u) / nw;
   return p;
 }
 
@@ -693,7 +826,7 @@ template <int TYPE, int TT, int RF, int NW, int KS>
 hipError_t sx_go(const WeightView &wv, const uint8_t *xa, const float *xp, float *y, uint32_t tokens,
                  const SxPlan &p, hipStream_t s) {
   const uint64_t tiles = (uint64_t)p.groups * p.tt;
-  const uint32_t xa_bytes = (uint32_t)(tiles * wv.bpr * sx_slots<TYPE>() * 1024u);
+  const uint32_t xa_bytes = (uint32_t)(tiles * (wv.k / 256u) * sx_slots<TYPE>() * 1024u);
   hipLaunchKernelGGL((k_sx<TYPE, TT, RF, NW, KS, false>), dim3(p.row_tiles * KS, p.groups), dim3(NW * 64), 0, s, wv,
                      xa, xp, y, tokens, p.nbw, xa_bytes, nullptr);
   return hipGetLastError();
@@ -730,7 +863,7 @@ hipError_t sx_type(const WeightView &wv, const float *x, float *y, uint32_t toke
   // up to 8 tokens of Q2_K / IQ2_XXS with the automatic plan: one launch
   if constexpr (TYPE == Q2_K || TYPE == IQ2_XXS)
     if (cfg == 0 && tokens <= 8u && p.cfg == 0u) return sx_go_fx<TYPE>(wv, x, y, tokens, p, s);
-  const uint32_t tiles = p.groups * p.tt, nb = wv.bpr;
+  const uint32_t tiles = p.groups * p.tt, nb = wv.k / 256u;   // blocks of 256 weights
   uint8_t *xa = scratch;
   float *xp = (float *)(scratch + (uint64_t)tiles * nb * sx_slots<TYPE>() * 1024u);
   const uint32_t yz = p.cfg == 2u ? tokens * wv.rows : 0u;
@@ -738,21 +871,25 @@ hipError_t sx_type(const WeightView &wv, const float *x, float *y, uint32_t toke
   switch (p.tt) {
     case 1: return sx_cfg<TYPE, 1>(wv, xa, xp, y, tokens, p, s);
     case 2: return sx_cfg<TYPE, 2>(wv, xa, xp, y, tokens, p, s);
-    default: return sx_cfg<TYPE, 4>(wv, xa, xp, y, tokens, p, s);
+    default:
+      if constexpr (SxW<TYPE>::FG == 16) return sx_cfg<TYPE, 4>(wv, xa, xp, y, tokens, p, s);
+      return hipErrorInvalidValue;   // not planned (sx_tt_max)
   }
 }
 
 }  // namespace
 
 bool sx_applies(const WeightView &wv, uint32_t tokens) {
-  return (wv.type == Q2_K || wv.type == Q4_K || wv.type == IQ2_XXS) && tokens >= 4u && wv.k % 256u == 0u;
+  const bool t = wv.type == Q2_K || wv.type == Q4_K || wv.type == IQ2_XXS || wv.type == Q8_0 || wv.type == Q6_K;
+  return t && tokens >= 4u && wv.k % 256u == 0u;
 }
 
 size_t sx_x_bytes(int type, uint32_t tokens, uint32_t k) {
   uint32_t tt, groups;
-  sx_tiles(tokens, tt, groups);
+  sx_tiles(type, tokens, tt, groups);
   const uint64_t tiles = (uint64_t)tt * groups, nb = k / 256u;
-  return (size_t)(tiles * nb * (type == IQ2_XXS ? 16u : 17u) * 1024u + tiles * nb * 64u);
+  const uint32_t slots = type == Q2_K || type == Q4_K ? 17u : 16u;   // sx_slots
+  return (size_t)(tiles * nb * slots * 1024u + tiles * nb * 64u);
 }
 
 hipError_t launch_sx(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *scratch, int cfg,
@@ -762,6 +899,8 @@ hipError_t launch_sx(const WeightView &wv, const float *x, float *y, uint32_t to
     case Q2_K: return sx_type<Q2_K>(wv, x, y, tokens, sc, cfg, s);
     case Q4_K: return sx_type<Q4_K>(wv, x, y, tokens, sc, cfg, s);
     case IQ2_XXS: return sx_type<IQ2_XXS>(wv, x, y, tokens, sc, cfg, s);
+    case Q8_0: return sx_type<Q8_0>(wv, x, y, tokens, sc, cfg, s);
+    case Q6_K: return sx_type<Q6_K>(wv, x, y, tokens, sc, cfg, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -55,8 +55,9 @@ extern "C" {
 #define EFF_OPT_SPLIT_CONFIG     4  /* split-x product workgroups (tuning): 0 automatic (default), 1: 32 rows x
                                        8 waves, 2: 64 rows x 4 waves, 3: 64 rows x 4 waves with k halves in two
                                        workgroups added into y */
-#define EFF_OPT_SPLIT_MIN_TOKENS 5  /* Q2_K, Q4_K, IQ2_XXS: tokens >= this run the split-x product, fewer the int8
-                                       matrix-core GEMVs (0: automatic, 5 and 9 for Q4_K (default); else >= 4) */
+#define EFF_OPT_SPLIT_MIN_TOKENS 5  /* Q2_K, Q4_K, IQ2_XXS, Q8_0, Q6_K: tokens >= this run the split-x product, fewer
+                                       the int8 matrix-core GEMVs (0: automatic, 5 for Q2_K and IQ2_XXS, 9 for the
+                                       others (default); else >= 4). Q8_0 only below EFF_OPT_GEMM_MIN_TOKENS */
 #define EFF_OPT_GEMM_CONFIG      6  /* Q8_0 GEMM from 256 tokens, tiles (tuning; tokens x rows, waves along tokens x
                                        rows, LDS stages): 0 automatic (default), 1: 256x256 1x4 3, 2: 128x128 1x4 3,
                                        3: 128x128 1x4 6, 4: 64x128 1x4 4, 5: 128x256 1x4 4, 6: 256x128 2x2 3; every
@@ -87,7 +88,7 @@ typedef struct eff_stats {
   uint64_t dequant;     /* dequant launches */
   uint64_t topk;        /* top-k calls (records + selection; eff_topk, eff_topk_noalloc, eff_qgemv_topk) */
   uint64_t not_applicable;  /* calls answered EFF_NOT_APPLICABLE */
-  uint64_t split;       /* split-x matrix-core launches (Q2_K, Q4_K, IQ2_XXS from EFF_OPT_SPLIT_MIN_TOKENS) */
+  uint64_t split;       /* split-x matrix-core launches (Q2_K, Q4_K, IQ2_XXS, Q8_0, Q6_K from EFF_OPT_SPLIT_MIN_TOKENS) */
   uint64_t fused;       /* fused GEMV launches (eff_qgemv_multi) */
   uint64_t gather;      /* gather launches (eff_gather, eff_gather_norm) */
   uint64_t gemm_x;      /* conversions of x to fp16 for the GEMM (one per eff_qgemm / eff_qgemm_planned /
@@ -280,11 +281,12 @@ int eff_fill_normal(uint32_t seed, float sigma, float *dst, size_t n);
 
 /* Y[tokens][rows] = W (rows x k, quantized) . X[tokens][k]; X and Y are f32.
  * Router of quant.matmul (ops.js:827-1101): tokens <= GEMV max -> GEMV;
- * Q2_K, Q4_K, IQ2_XXS from EFF_OPT_SPLIT_MIN_TOKENS (5; 9 for Q4_K) -> split-x
- * product (f32-accurate; fewer tokens run the int8 matrix-core GEMVs, as accurate);
  * Q8_0/Q8_0R at tokens >= GEMM min -> fp16 MFMA GEMM (the reference's
- * DRIFT/GEMM2 types, kernels.drift.wgsl.js:33); otherwise (Q6_K at every
- * token count, Q8_0 below GEMM min) -> GEMV over token groups, f32-accurate.
+ * DRIFT/GEMM2 types, kernels.drift.wgsl.js:33); Q2_K, Q4_K, IQ2_XXS, Q6_K and
+ * Q8_0 below GEMM min, from EFF_OPT_SPLIT_MIN_TOKENS (5 for Q2_K and IQ2_XXS, 9
+ * for the others) -> split-x product (f32-accurate; fewer tokens run the int8
+ * matrix-core GEMVs, as accurate); otherwise (Q8_0R below GEMM min, k not a
+ * multiple of 256) -> GEMV over token groups, f32-accurate.
  * EFF_E_SHAPE if k % block_elems != 0. */
 int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
                 uint32_t rows, uint32_t k, uint32_t tokens);

@@ -382,7 +382,8 @@ def test_fused_not_applicable_and_errors(ctx, eff):
     assert e.value.code == eff.E_SHAPE
 
 
-# ---- split-x product (Q2_K, Q4_K, IQ2_XXS; from 8 tokens by default, from 4 here) ----
+# ---- split-x product (Q2_K, Q4_K, IQ2_XXS, Q8_0, Q6_K; by default from 5 tokens for Q2_K and IQ2_XXS,
+# from 9 for the others, from 4 here) ----
 
 @pytest.fixture
 def split_from_4(ctx, eff):
@@ -393,6 +394,27 @@ def split_from_4(ctx, eff):
 
 
 SPLIT_TYPES = ["Q2_K", "Q4_K", "IQ2_XXS"]
+
+
+@pytest.mark.parametrize("tname,tokens", [("Q8_0", t) for t in (4, 7, 9, 16, 17, 32, 33, 63)] +
+                         [("Q6_K", t) for t in (4, 7, 9, 16, 17, 33, 64, 100, 129)])
+@pytest.mark.parametrize("k", [2048, 2304])
+def test_split_x_per_block_scales_vs_f64_oracle(ctx, eff, orc, tname, tokens, k, split_from_4):
+    """The split-x product of the types folded per group of steps (Q8_0: a
+    scale per 32 weights, Q6_K: per 16) is f32-accurate at 1 and 2 token tiles
+    and several token groups; rows not a multiple of 32; k = 2304 gives Q6_K
+    rows starting 2 bytes past a dword (an odd number of 210-byte blocks)."""
+    rows = 77
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 700 + tokens + k)
+    x = eff.fill_normal(7000 + tokens + k, 1.0, tokens * k)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    before = ctx.stats()["split"]
+    ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+    assert ctx.stats()["split"] == before + 1
+    check_close(yb.read(np.float32), orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens),
+                f"split-x {tname} M={tokens} k={k}")
+    for b in (wb, xb, yb):
+        b.free()
 
 
 @pytest.mark.parametrize("tname", SPLIT_TYPES)
@@ -521,7 +543,7 @@ def test_router_paths_and_stats(ctx, eff, orc):
     assert after["gemv"] - before["gemv"] == 2
     assert after["split"] - before["split"] == 3
     assert after["skinny"] == before["skinny"] and after["gemm"] == before["gemm"]
-    # Q8_0 keeps the token-group GEMV below 64 tokens and the fp16 GEMM from 64
+    # Q8_0: the split-x product below 64 tokens, the fp16 GEMM from 64
     t8, data8, gguf8, _ = make_weights(eff, "Q8_0", rows, k, 92)
     w8 = ctx.upload(data8)
     before = ctx.stats()
@@ -531,7 +553,10 @@ def test_router_paths_and_stats(ctx, eff, orc):
         ctx.qmatmul(t8, w8, xb, yb, rows, k, tokens)
         check_close(yb.read(np.float32), oracle_fn(orc.Q8_0, gguf8, rows, k, x, tokens), f"matmul Q8_0 T={tokens}")
     after = ctx.stats()
-    assert after["skinny"] - before["skinny"] == 3 and after["gemm"] - before["gemm"] == 1
+    # 33 tokens: the split-x product (f32-accurate, as the reference's tiled
+    # GEMM below DRIFT's threshold); 64: the fp16 GEMM
+    assert after["split"] - before["split"] == 1 and after["gemm"] - before["gemm"] == 1
+    assert after["skinny"] == before["skinny"]
 
 
 def test_router_split_x_threshold(ctx, eff, orc):
@@ -563,7 +588,8 @@ def test_router_split_x_threshold(ctx, eff, orc):
 def test_router_q6_k_prefill_is_f32_accurate(ctx, eff, orc, tokens):
     """Q6_K prefill through quant.matmul stays f32-accurate (the reference's
     fp16 GEMMs read Q8_0/Q4_0 only and its Q6_K prefill runs the f32 generic
-    kernel, ops.js:117-128): against the f64 oracle, no fp16 GEMM launched."""
+    kernel, ops.js:117-128): against the f64 oracle, on the split-x product,
+    no fp16 GEMM launched."""
     rows, k = 1000, 2048
     t, data, gguf, n = make_weights(eff, "Q6_K", rows, k, 600 + tokens)
     x = eff.fill_normal(601 + tokens, 1.0, tokens * k)
@@ -573,7 +599,7 @@ def test_router_q6_k_prefill_is_f32_accurate(ctx, eff, orc, tokens):
     after = ctx.stats()
     check_close(yb.read(np.float32), orc.gemv_f64(orc.Q6_K, gguf, rows, k, x, tokens), f"matmul Q6_K T={tokens}")
     assert after["gemm"] == before["gemm"]
-    assert after["skinny"] - before["skinny"] == (tokens + 15) // 16
+    assert after["split"] - before["split"] == 1 and after["skinny"] == before["skinny"]
     for b in (wb, xb, yb):
         b.free()
 
