@@ -285,13 +285,51 @@ int grow(eff_ctx *ctx, void **p, size_t *have, size_t need, const char *what) {
   return EFF_OK;
 }
 
-// Split-x matrix-core product (Q2_K, Q4_K, IQ2_XXS from 4 tokens, f32-accurate).
+// Split-x matrix-core product (Q2_K, Q4_K, IQ2_XXS, Q8_0, Q6_K from 4 tokens,
+// f32-accurate).
 int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
   int rc = grow(ctx, &ctx->sx_scratch, &ctx->sx_scratch_bytes, sx_x_bytes(wv.type, tokens, wv.k), "split-x");
   if (rc) return rc;
   hipError_t e = launch_sx(wv, x, y, tokens, ctx->sx_scratch, (int)ctx->sx_config, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "split-x launch");
   ++ctx->stats.split;
+  if (sx_x_layout(wv, tokens, (int)ctx->sx_config)) ++ctx->stats.split_x;
+  return EFF_OK;
+}
+
+// The prepared x the router's path for a call reads (eff_qmatmul_x_layout):
+// a split-x layout, the fp16 GEMM's, or 0 where the path reads x itself. The
+// same decisions, in the same order, as eff_qmatmul.
+uint32_t route_layout(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens, size_t *bytes) {
+  *bytes = 0;
+  if (sx_routes(ctx, wv, tokens)) {
+    const uint32_t l = sx_x_layout(wv, tokens, (int)ctx->sx_config);
+    if (l) *bytes = sx_prepared_bytes(l, tokens, wv.k);
+    return l;
+  }
+  const bool gemv = (int64_t)tokens <= ctx->gemv_max_tokens && tokens <= 8;
+  if (!gemv && (int64_t)tokens >= ctx->gemm_min_tokens && router_gemm_type(wv.type)) {
+    const uint32_t cfg = (uint32_t)ctx->gemm_config;
+    *bytes = gemm_x_bytes(wv.type, tokens, tokens, wv.k, wv.rows, cfg);
+    return gemm_x_layout(wv.type, tokens, wv.k, wv.rows, cfg);
+  }
+  return 0u;
+}
+
+// The shape checks of the prepared-x router entry points, and the routing
+// view of the call (type, rows, k; no buffers).
+int matmul_prepared_view(eff_ctx *ctx, int type, uint32_t rows, uint32_t k, uint32_t tokens, WeightView &wv,
+                         const char *who) {
+  if (!type_known(type)) return fail(ctx, EFF_E_TYPE, "%s: unsupported quantization type %d", who, type);
+  if (rows == 0 || k == 0 || tokens == 0)
+    return fail(ctx, EFF_E_INVALID, "%s: empty shape rows=%u k=%u tokens=%u", who, rows, k, tokens);
+  const Geometry g = geometry(type);
+  if (k % g.elems) return fail(ctx, EFF_E_SHAPE, "%s %s: k=%u is not a multiple of %u", who, eff_type_name(type), k, g.elems);
+  wv = WeightView{};
+  wv.type = type;
+  wv.rows = rows;
+  wv.k = k;
+  wv.bpr = k / g.elems;
   return EFF_OK;
 }
 
@@ -885,14 +923,13 @@ int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint
     if (!rc) ++ctx->stats.gemv;
     return rc;
   }
-  // Q2_K, Q4_K, IQ2_XXS: the reference has no f16 GEMM for these types (DRIFT
-  // and GEMM2 read Q8_0/Q4_0 only) and runs its f32 kernel at every token
-  // count; so does this router, on the split-x matrix cores.
+  // Q2_K, Q4_K, IQ2_XXS, Q6_K: the reference has no f16 GEMM for these types
+  // (DRIFT and GEMM2 read Q8_0/Q4_0 only) and runs its f32 kernel at every
+  // token count (ops.js:117-128); so does this router, on the split-x matrix
+  // cores, and for Q8_0 below the GEMM's threshold.
   if (sx_routes(ctx, wv, tokens)) return run_sx(ctx, wv, xp, yp, tokens);
   // The fp16 GEMM is the reference's DRIFT/GEMM2 semantics, which exist for
-  // Q8_0 (and Q4_0) only (kernels.drift.wgsl.js:33, kernels.gemm2.wgsl.js:51);
-  // Q6_K prefill stays on its f32 path there (ops.js:117-128), and here on the
-  // token-group GEMV below at every token count.
+  // Q8_0 (and Q4_0) only (kernels.drift.wgsl.js:33, kernels.gemm2.wgsl.js:51).
   if ((int64_t)tokens >= ctx->gemm_min_tokens && router_gemm_type(type)) {
     rc = run_gemm(ctx, wv, xp, yp, tokens, tokens);
     if (!rc) ++ctx->stats.gemm;
@@ -909,6 +946,88 @@ int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint
     if (rc) return rc;
     ++ctx->stats.skinny;
   }
+  return EFF_OK;
+}
+
+int eff_qmatmul_x_layout(eff_ctx *ctx, int type, uint32_t rows, uint32_t k, uint32_t tokens, size_t *bytes,
+                         uint32_t *layout) {
+  if (!ctx || !bytes || !layout) return EFF_E_INVALID;
+  WeightView wv;
+  const int rc = matmul_prepared_view(ctx, type, rows, k, tokens, wv, "matmul x layout");
+  if (rc) return rc;
+  size_t n = 0;
+  const uint32_t l = route_layout(ctx, wv, tokens, &n);
+  if (!l) {
+    ++ctx->stats.not_applicable;
+    return EFF_NOT_APPLICABLE;
+  }
+  *bytes = n;
+  *layout = l;
+  return EFF_OK;
+}
+
+int eff_qmatmul_prepare_x(eff_ctx *ctx, int type, eff_buf *x, eff_buf *xp, uint32_t rows, uint32_t k,
+                          uint32_t tokens) {
+  if (!ctx) return EFF_E_INVALID;
+  if (!x || !xp) return fail(ctx, EFF_E_INVALID, "matmul prepare x: null buffer");
+  WeightView wv;
+  int rc = matmul_prepared_view(ctx, type, rows, k, tokens, wv, "matmul prepare x");
+  if (rc) return rc;
+  size_t n = 0;
+  const uint32_t l = route_layout(ctx, wv, tokens, &n);
+  if (!l) {
+    ++ctx->stats.not_applicable;
+    return EFF_NOT_APPLICABLE;
+  }
+  if ((uint64_t)tokens * k * 4 > x->size)
+    return fail(ctx, EFF_E_BOUNDS, "matmul prepare x: x needs %llu bytes and the buffer has %zu",
+                (unsigned long long)tokens * k * 4, x->size);
+  if ((uintptr_t)x->ptr & 15) return fail(ctx, EFF_E_INVALID, "matmul prepare x: device buffers must be 16-byte aligned");
+  if ((rc = check_out(ctx, xp, n, "matmul prepare x")) || (rc = use_device(ctx))) return rc;
+  hipError_t e;
+  if (l & kSxLayout) {
+    e = launch_sx_prepare(l, (const float *)x->ptr, tokens, k, xp->ptr, ctx->stream);
+    ++ctx->stats.split_x;
+  } else {
+    e = launch_gemm_x(type, (const float *)x->ptr, tokens, tokens, k, rows, (uint32_t)ctx->gemm_config, xp->ptr,
+                      ctx->stream);
+    ++ctx->stats.gemm_x;
+  }
+  if (e != hipSuccess) return hip_fail(ctx, e, "matmul prepare x launch");
+  return EFF_OK;
+}
+
+int eff_qmatmul_prepared(eff_ctx *ctx, int type, eff_buf *w, eff_buf *xp, eff_buf *y, uint32_t rows, uint32_t k,
+                         uint32_t tokens) {
+  if (!ctx) return EFF_E_INVALID;
+  if (!w || !xp || !y) return fail(ctx, EFF_E_INVALID, "matmul prepared: null buffer");
+  WeightView wv;
+  int rc = matmul_prepared_view(ctx, type, rows, k, tokens, wv, "matmul prepared");
+  if (rc) return rc;
+  size_t n = 0;
+  const uint32_t l = route_layout(ctx, wv, tokens, &n);
+  if (!l) {
+    ++ctx->stats.not_applicable;
+    return EFF_NOT_APPLICABLE;
+  }
+  // the weight view checks against a stand-in x of the call's size (the
+  // product reads xp, checked below)
+  eff_buf xs{};
+  xs.ptr = xp->ptr;
+  xs.size = (size_t)tokens * k * 4;
+  if ((rc = weight_view(ctx, type, w, &xs, y, rows, k, tokens, wv, "matmul prepared")) ||
+      (rc = check_out(ctx, xp, n, "matmul prepared x")) || (rc = use_device(ctx)))
+    return rc;
+  hipError_t e;
+  if (l & kSxLayout) {
+    e = launch_sx_prepared(wv, xp->ptr, (float *)y->ptr, tokens, (int)ctx->sx_config, ctx->stream);
+    ++ctx->stats.split;
+  } else {
+    e = launch_gemm_prepared(wv, (const _Float16 *)xp->ptr, (float *)y->ptr, tokens, tokens,
+                             (uint32_t)ctx->gemm_config, ctx->stream);
+    ++ctx->stats.gemm;
+  }
+  if (e != hipSuccess) return hip_fail(ctx, e, "matmul prepared launch");
   return EFF_OK;
 }
 

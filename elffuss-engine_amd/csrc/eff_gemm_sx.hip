@@ -856,18 +856,18 @@ hipError_t sx_cfg(const WeightView &wv, const uint8_t *xa, const float *xp, floa
   }
 }
 
+// Up to 8 tokens of Q2_K / IQ2_XXS with the automatic plan: one launch, each
+// wave preparing its own block's x.
+bool sx_fx(int type, uint32_t tokens, int cfg, const SxPlan &p) {
+  return (type == Q2_K || type == IQ2_XXS) && cfg == 0 && tokens <= 8u && p.cfg == 0u;
+}
+
+// The product from x prepared in `xa` for `tiles` token tiles (at least the
+// plan's; the tokens' block scales follow the fragments).
 template <int TYPE>
-hipError_t sx_type(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint8_t *scratch, int cfg,
-                   hipStream_t s) {
-  const SxPlan p = sx_plan(wv, tokens, cfg);
-  // up to 8 tokens of Q2_K / IQ2_XXS with the automatic plan: one launch
-  if constexpr (TYPE == Q2_K || TYPE == IQ2_XXS)
-    if (cfg == 0 && tokens <= 8u && p.cfg == 0u) return sx_go_fx<TYPE>(wv, x, y, tokens, p, s);
-  const uint32_t tiles = p.groups * p.tt, nb = wv.k / 256u;   // blocks of 256 weights
-  uint8_t *xa = scratch;
-  float *xp = (float *)(scratch + (uint64_t)tiles * nb * sx_slots<TYPE>() * 1024u);
-  const uint32_t yz = p.cfg == 2u ? tokens * wv.rows : 0u;
-  hipLaunchKernelGGL((k_sx_prep<TYPE>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, wv.k, xa, xp, y, yz);
+hipError_t sx_main(const WeightView &wv, const uint8_t *xa, uint32_t tiles, float *y, uint32_t tokens,
+                   const SxPlan &p, hipStream_t s) {
+  const float *xp = (const float *)(xa + (uint64_t)tiles * (wv.k / 256u) * sx_slots<TYPE>() * 1024u);
   switch (p.tt) {
     case 1: return sx_cfg<TYPE, 1>(wv, xa, xp, y, tokens, p, s);
     case 2: return sx_cfg<TYPE, 2>(wv, xa, xp, y, tokens, p, s);
@@ -876,6 +876,24 @@ hipError_t sx_type(const WeightView &wv, const float *x, float *y, uint32_t toke
       return hipErrorInvalidValue;   // not planned (sx_tt_max)
   }
 }
+
+template <int TYPE>
+hipError_t sx_type(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint8_t *scratch, int cfg,
+                   hipStream_t s) {
+  const SxPlan p = sx_plan(wv, tokens, cfg);
+  if constexpr (TYPE == Q2_K || TYPE == IQ2_XXS)
+    if (sx_fx(TYPE, tokens, cfg, p)) return sx_go_fx<TYPE>(wv, x, y, tokens, p, s);
+  const uint32_t tiles = p.groups * p.tt, nb = wv.k / 256u;   // blocks of 256 weights
+  uint8_t *xa = scratch;
+  float *xp = (float *)(scratch + (uint64_t)tiles * nb * sx_slots<TYPE>() * 1024u);
+  const uint32_t yz = p.cfg == 2u ? tokens * wv.rows : 0u;
+  hipLaunchKernelGGL((k_sx_prep<TYPE>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, wv.k, xa, xp, y, yz);
+  return sx_main<TYPE>(wv, xa, tiles, y, tokens, p, s);
+}
+
+// Token tiles of a prepared x: a multiple of 4 (the most a plan groups), so
+// that the plan of every type of the layout reads inside it.
+uint32_t sx_prepared_tiles(uint32_t tokens) { return (tokens + 63u) / 64u * 4u; }
 
 }  // namespace
 
@@ -890,6 +908,62 @@ size_t sx_x_bytes(int type, uint32_t tokens, uint32_t k) {
   const uint64_t tiles = (uint64_t)tt * groups, nb = k / 256u;
   const uint32_t slots = type == Q2_K || type == Q4_K ? 17u : 16u;   // sx_slots
   return (size_t)(tiles * nb * slots * 1024u + tiles * nb * 64u);
+}
+
+uint32_t sx_x_layout(const WeightView &wv, uint32_t tokens, int cfg) {
+  const SxPlan p = sx_plan(wv, tokens, cfg);
+  if (sx_fx(wv.type, tokens, cfg, p) || p.cfg == 2u) return 0u;
+  switch (wv.type) {
+    case Q2_K: return kSxLayout | 1u;
+    case Q4_K: return kSxLayout | 2u;
+    default: return kSxLayout;
+  }
+}
+
+size_t sx_prepared_bytes(uint32_t layout, uint32_t tokens, uint32_t k) {
+  const uint64_t tiles = sx_prepared_tiles(tokens), nb = k / 256u;
+  const uint32_t slots = layout == kSxLayout ? 16u : 17u;   // sx_slots
+  return (size_t)(tiles * nb * slots * 1024u + tiles * nb * 64u);
+}
+
+hipError_t launch_sx_prepare(uint32_t layout, const float *x, uint32_t tokens, uint32_t k, void *xprep,
+                             hipStream_t s) {
+  const uint32_t tiles = sx_prepared_tiles(tokens), nb = k / 256u;
+  uint8_t *xa = (uint8_t *)xprep;
+  const uint32_t slots = layout == kSxLayout ? 16u : 17u;
+  float *xp = (float *)(xa + (uint64_t)tiles * nb * slots * 1024u);
+  // the layouts differ only in the group sums: IQ2_XXS, Q8_0 and Q6_K read
+  // the same 16 slots
+  switch (layout) {
+    case kSxLayout | 1u:
+      hipLaunchKernelGGL((k_sx_prep<Q2_K>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, k, xa, xp, nullptr, 0u);
+      break;
+    case kSxLayout | 2u:
+      hipLaunchKernelGGL((k_sx_prep<Q4_K>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, k, xa, xp, nullptr, 0u);
+      break;
+    case kSxLayout:
+      hipLaunchKernelGGL((k_sx_prep<IQ2_XXS>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, k, xa, xp, nullptr,
+                         0u);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_sx_prepared(const WeightView &wv, const void *xprep, float *y, uint32_t tokens, int cfg,
+                              hipStream_t s) {
+  const SxPlan p = sx_plan(wv, tokens, cfg);
+  if (p.cfg == 2u) return hipErrorInvalidValue;   // the k halves add into a y their preparation zeroes
+  const uint8_t *xa = (const uint8_t *)xprep;
+  const uint32_t tiles = sx_prepared_tiles(tokens);
+  switch (wv.type) {
+    case Q2_K: return sx_main<Q2_K>(wv, xa, tiles, y, tokens, p, s);
+    case Q4_K: return sx_main<Q4_K>(wv, xa, tiles, y, tokens, p, s);
+    case IQ2_XXS: return sx_main<IQ2_XXS>(wv, xa, tiles, y, tokens, p, s);
+    case Q8_0: return sx_main<Q8_0>(wv, xa, tiles, y, tokens, p, s);
+    case Q6_K: return sx_main<Q6_K>(wv, xa, tiles, y, tokens, p, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_sx(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *scratch, int cfg,

@@ -108,15 +108,29 @@ uint32_t gemm_big_tile_log2(uint32_t tokens, uint32_t cfg);
 hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
                            uint32_t cfg, hipStream_t stream);
 
-// Split-x matrix-core product (eff_gemm_sx.hip): Q2_K, Q4_K, IQ2_XXS from 4
-// tokens, k % 256 == 0, f32-accurate. `scratch` holds sx_x_bytes(...) bytes
-// (x as fp16 hi/lo parts and the block scales). cfg: 0 automatic, 1: 32 rows x
-// 8 waves per workgroup, 2: 64 rows x 4 waves, 3: as 2 with the two halves of k
-// in two workgroups.
+// Split-x matrix-core product (eff_gemm_sx.hip): Q2_K, Q4_K, IQ2_XXS, Q8_0,
+// Q6_K from 4 tokens, k % 256 == 0, f32-accurate. `scratch` holds
+// sx_x_bytes(...) bytes (x as fp16 hi/lo parts and the block scales). cfg: 0
+// automatic, 1: 32 rows x 8 waves per workgroup, 2: 64 rows x 4 waves, 3: as 2
+// with the two halves of k in two workgroups.
 bool sx_applies(const WeightView &wv, uint32_t tokens);
 size_t sx_x_bytes(int type, uint32_t tokens, uint32_t k);
 hipError_t launch_sx(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *scratch, int cfg,
                      hipStream_t stream);
+// The same product in two halves, so that one preparation of x serves every
+// product of that x: sx_x_layout is the layout the product reads (0: none,
+// the one-launch product up to 8 tokens reads x itself; kSxLayout for IQ2_XXS,
+// Q8_0 and Q6_K, | 1 with the group sums of Q2_K, | 2 with those of Q4_K);
+// launch_sx_prepare writes x in it (sx_prepared_bytes), launch_sx_prepared
+// runs the product from it (the same bits as launch_sx; hipErrorInvalidValue
+// for cfg 3, whose k halves add into a y their preparation zeroes).
+constexpr uint32_t kSxLayout = 0x100u;
+uint32_t sx_x_layout(const WeightView &wv, uint32_t tokens, int cfg);
+size_t sx_prepared_bytes(uint32_t layout, uint32_t tokens, uint32_t k);
+hipError_t launch_sx_prepare(uint32_t layout, const float *x, uint32_t tokens, uint32_t k, void *xprep,
+                             hipStream_t stream);
+hipError_t launch_sx_prepared(const WeightView &wv, const void *xprep, float *y, uint32_t tokens, int cfg,
+                              hipStream_t stream);
 
 // Embedding gather: out[t] = dequantized row ids[t] (bit-identical to dequant);
 // with the norm, also nrm[t] = x[t] / sqrt(mean(x[t]^2) + eps) * wn, dim <= kGatherNormMaxDim.

@@ -273,6 +273,7 @@ napi_value Stats(napi_env env, napi_callback_info info) {
   napi_set_named_property(env, o, "fused", make_int(env, (int64_t)s.fused));
   napi_set_named_property(env, o, "gather", make_int(env, (int64_t)s.gather));
   napi_set_named_property(env, o, "gemmX", make_int(env, (int64_t)s.gemm_x));
+  napi_set_named_property(env, o, "splitX", make_int(env, (int64_t)s.split_x));
   return o;
 }
 
@@ -535,6 +536,44 @@ napi_value QGemmPrepared(napi_env env, napi_callback_info info) {
   return status(env, ctx, rc);
 }
 
+// qmatmulXLayout(ctx, type, rows, k, tokens) -> {bytes, layout} | null
+napi_value QMatmulXLayout(napi_env env, napi_callback_info info) {
+  napi_value a[5];
+  get_args(env, info, 5, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  size_t bytes = 0;
+  uint32_t layout = 0;
+  int rc = eff_qmatmul_x_layout(ctx, (int)i64(env, a[1]), (uint32_t)i64(env, a[2]), (uint32_t)i64(env, a[3]),
+                                (uint32_t)i64(env, a[4], 1), &bytes, &layout);
+  if (rc) return status(env, ctx, rc);
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "bytes", make_int(env, (int64_t)bytes));
+  napi_set_named_property(env, o, "layout", make_int(env, (int64_t)layout));
+  return o;
+}
+
+// qmatmulPrepareX(ctx, type, x, xp, rows, k, tokens)
+napi_value QMatmulPrepareX(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  get_args(env, info, 7, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  int rc = eff_qmatmul_prepare_x(ctx, (int)i64(env, a[1]), external<eff_buf>(env, a[2]), external<eff_buf>(env, a[3]),
+                                 (uint32_t)i64(env, a[4]), (uint32_t)i64(env, a[5]), (uint32_t)i64(env, a[6], 1));
+  return status(env, ctx, rc);
+}
+
+// qmatmulPrepared(ctx, type, w, xp, y, rows, k, tokens)
+napi_value QMatmulPrepared(napi_env env, napi_callback_info info) {
+  napi_value a[8];
+  get_args(env, info, 8, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  int rc = eff_qmatmul_prepared(ctx, (int)i64(env, a[1]), external<eff_buf>(env, a[2]), external<eff_buf>(env, a[3]),
+                                external<eff_buf>(env, a[4]), (uint32_t)i64(env, a[5]), (uint32_t)i64(env, a[6]),
+                                (uint32_t)i64(env, a[7], 1));
+  return status(env, ctx, rc);
+}
+
 // qgemvMulti(ctx, type, mode, [w...], x, [y...], [rows...], k, tokens)
 napi_value QGemvMulti(napi_env env, napi_callback_info info) {
   napi_value a[9];
@@ -640,7 +679,8 @@ napi_value Register(napi_env env, napi_value exports) {
       {"topkOutBytes", TopKOutBytes}, {"bufRetire", BufRetire}, {"graphBegin", GraphBegin},
       {"graphEnd", GraphEnd}, {"graphLaunch", GraphLaunch}, {"graphNodes", GraphNodes},
       {"graphDestroy", GraphDestroy}, {"gemmXLayout", GemmXLayout}, {"gemmPrepareX", GemmPrepareX},
-      {"qgemmPrepared", QGemmPrepared},
+      {"qgemmPrepared", QGemmPrepared}, {"qmatmulXLayout", QMatmulXLayout},
+      {"qmatmulPrepareX", QMatmulPrepareX}, {"qmatmulPrepared", QMatmulPrepared},
   };
   for (auto &f : fns) {
     napi_value v;

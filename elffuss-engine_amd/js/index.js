@@ -218,6 +218,9 @@ function createContext(device) {
     const marca = ctx.scratch.length;
     await fn();
     ctx.recycleDesde(marca);
+    // a prepared x from before the recording would be read, not prepared, by
+    // the recorded products, and stale once x is written between replays
+    if (ctx.memoX) ctx.memoX.olvida();
     native.graphBegin(device._ctx);
     ctx._grabando = true;
     let salida;
@@ -602,39 +605,55 @@ function createFusionOps(device, deps) {
 // min option, __ELFFUSS_DRIFT_DESDE, default 64) and rows a multiple of 16.
 const GEMM2_TIPOS = new Set(['Q8_0', 'Q8_0R']);
 
+// Prepared activations with a memo (aF16, ops.gemm2.js:151-196): the same
+// activation feeds several products in a row (the norm's output q, k, v; the
+// FFN's gate and up), and the preparation is the same operation on the same
+// bytes, so reusing it changes no bit. The key is the pool's allocation mark
+// of x (ctx.marcaDe), not the buffer: a buffer lent again gets a new mark. A
+// preparation is reused only while its own buffer is still lent under the
+// mark it was made with (a returned one could be lent to the same call as
+// its output). The library gives the bytes and an id of the layout a product
+// reads (eff_gemm_x_layout, eff_qmatmul_x_layout): a preparation serves every
+// product whose layout id, tokens and k match — the fp16 x of the GEMM, the
+// hi/lo parts of the split-x product. One memo per pool, shared by gemm2 and
+// quant.matmul; four entries, oldest dropped first.
+function memoPreparados(ctx) {
+  if (ctx.memoX) return ctx.memoX;
+  const prestado = (buf) => ctx.scratch.some((e) => e.buf === buf);
+  const memo = [];
+  ctx.memoX = {
+    // the prepared x for `lay` ({bytes, layout}); `prepara(xp)` fills a new one
+    toma(xBuf, lay, tokens, k, label, prepara) {
+      const marca = ctx.marcaDe.get(xBuf);
+      if (marca !== undefined) {
+        for (let i = memo.length - 1; i >= 0; i--) {
+          const m = memo[i];
+          if (m.marca === marca && m.layout === lay.layout && m.tokens === tokens && m.k === k &&
+              ctx.marcaDe.get(m.xp) === m.marcaXp && prestado(m.xp)) return m.xp;
+        }
+      }
+      const xp = ctx.alloc(lay.bytes, label);
+      prepara(xp);
+      if (marca !== undefined) {
+        memo.push({ marca, layout: lay.layout, tokens, k, xp, marcaXp: ctx.marcaDe.get(xp) });
+        if (memo.length > 4) memo.shift();
+      }
+      return xp;
+    },
+    olvida() { memo.length = 0; },
+  };
+  return ctx.memoX;
+}
+
 function createGemm2Ops(ctx) {
   const device = ctx.device;
   const desde = () => device.option(OPT.GEMM_MIN_TOKENS);
-  // x -> fp16 with a memo (aF16, ops.gemm2.js:151-196): the same activation
-  // feeds several GEMMs in a row (the norm's output q, k, v; the FFN's gate
-  // and up), and the conversion is the same operation on the same bytes, so
-  // reusing it changes no bit. The key is the pool's allocation mark of x
-  // (ctx.marcaDe), not the buffer: a buffer lent again gets a new mark. A
-  // conversion is reused only while its own buffer is still lent under the
-  // mark it was made with (a returned one could be lent to the same call as
-  // its output). Here the library gives the bytes and an id of the layout the
-  // GEMM reads (eff_gemm_x_layout): a conversion serves every product whose
-  // layout id, tokens and k match. Four entries, oldest dropped first.
-  const prestado = (buf) => ctx.scratch.some((e) => e.buf === buf);
-  const memo = [];
+  const memo = memoPreparados(ctx);
   function aF16(code, xBuf, rows, k, tokens, lote) {
     const lay = native.gemmXLayout(device._ctx, code, rows, k, tokens, lote);
     if (lay === null) return null;
-    const marca = ctx.marcaDe.get(xBuf);
-    if (marca !== undefined) {
-      for (let i = memo.length - 1; i >= 0; i--) {
-        const m = memo[i];
-        if (m.marca === marca && m.layout === lay.layout && m.tokens === tokens && m.k === k &&
-            ctx.marcaDe.get(m.xh) === m.marcaXh && prestado(m.xh)) return m.xh;
-      }
-    }
-    const xh = ctx.alloc(lay.bytes, 'gemm2.x');
-    native.gemmPrepareX(device._ctx, code, xBuf._h, xh._h, rows, k, tokens, lote);
-    if (marca !== undefined) {
-      memo.push({ marca, layout: lay.layout, tokens, k, xh, marcaXh: ctx.marcaDe.get(xh) });
-      if (memo.length > 4) memo.shift();
-    }
-    return xh;
+    return memo.toma(xBuf, lay, tokens, k, 'gemm2.x',
+      (xh) => native.gemmPrepareX(device._ctx, code, xBuf._h, xh._h, rows, k, tokens, lote));
   }
   const ops = {
     // What this shape would run (null: the caller's usual path).
@@ -646,7 +665,7 @@ function createGemm2Ops(ctx) {
     },
     // Empties the x -> fp16 memo (for benches: so that one measurement does
     // not save conversions another one pays, ops.gemm2.js:265-266).
-    olvida() { memo.length = 0; },
+    olvida() { memo.olvida(); },
     matmul(type, wBuf, xBuf, rows, k, tokens) {
       if (tokens < 4 && tokens < desde()) return Promise.resolve(null);
       const pl = ops.plan(type, rows, k, tokens);
@@ -688,6 +707,7 @@ function createQuantOps(device, opts) {
   const ctx = o.ctx || createContext(device);
   const gemv = createGemvOps(device, { ctx, ampliado: o.gemvAmpliado === true });
   const gemm2 = createGemm2Ops(ctx);
+  const memo = memoPreparados(ctx);
   return {
     // Whole tensor -> f32, bit-exact with the reference decoders (ops.js:813-823).
     dequant(type, wBuf, nBlocks) {
@@ -708,16 +728,29 @@ function createQuantOps(device, opts) {
       return Promise.resolve(dst);
     },
     // Y[tokens][rows] = W . X (ops.js:827-1101); throws when k is not a
-    // multiple of the block, or for an unmarked repacked buffer.
+    // multiple of the block, or for an unmarked repacked buffer. Where the
+    // router's path reads a prepared x (the split-x product, the fp16 GEMM),
+    // the preparation comes from the pool's memo: the products of one
+    // activation prepare it once (the same bits as preparing it per call).
     matmul(type, wBuf, xBuf, rows, k, tokens) {
       const t = tokens === undefined ? 1 : tokens;
       const i = quantInfo(type);
       if (k % i.blockElems !== 0) throw new Error(`matmul ${type}: k=${k} no es múltiplo de ${i.blockElems}`);
       if (TIPOS_R.has(type)) compruebaBufferR(type, wBuf, { bloques: rows * (k / i.blockElems) }, 'matmul');
       const y = ctx.alloc(rows * t * 4, 'matmul.y');
-      native.qmatmul(device._ctx, i.code, wBuf._h, xBuf._h, y._h, rows, k, t);
+      // (below 4 tokens every path reads x itself)
+      const lay = t >= 4 ? native.qmatmulXLayout(device._ctx, i.code, rows, k, t) : null;
+      if (lay === null) {
+        native.qmatmul(device._ctx, i.code, wBuf._h, xBuf._h, y._h, rows, k, t);
+      } else {
+        const xp = memo.toma(xBuf, lay, t, k, 'matmul.x',
+          (p) => native.qmatmulPrepareX(device._ctx, i.code, xBuf._h, p._h, rows, k, t));
+        native.qmatmulPrepared(device._ctx, i.code, wBuf._h, xp._h, y._h, rows, k, t);
+      }
       return Promise.resolve(y);
     },
+    // Empties the memo of prepared activations (gemm2.olvida()).
+    olvida() { memo.olvida(); },
     // The IQ2_XXS grid is part of the library (no upload needed).
     prepare(types) {
       for (const t of new Set(types)) quantInfo(t);

@@ -92,7 +92,12 @@ typedef struct eff_stats {
   uint64_t fused;       /* fused GEMV launches (eff_qgemv_multi) */
   uint64_t gather;      /* gather launches (eff_gather, eff_gather_norm) */
   uint64_t gemm_x;      /* conversions of x to fp16 for the GEMM (one per eff_qgemm / eff_qgemm_planned /
-                           router GEMM call, one per eff_gemm_prepare_x) */
+                           router GEMM call, one per eff_gemm_prepare_x, one per eff_qmatmul_prepare_x
+                           for the GEMM) */
+  uint64_t split_x;     /* preparations of x for the split-x product in a launch of their own (one per
+                           split-x router call but those of Q2_K and IQ2_XXS up to 8 tokens under the
+                           automatic configuration, which prepare x inside the product; one per
+                           eff_qmatmul_prepare_x for it) */
 } eff_stats;
 
 /* ---- types and geometry -------------------------------------------------- */
@@ -290,6 +295,30 @@ int eff_fill_normal(uint32_t seed, float sigma, float *dst, size_t n);
  * EFF_E_SHAPE if k % block_elems != 0. */
 int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
                 uint32_t rows, uint32_t k, uint32_t tokens);
+
+/* eff_qmatmul with x prepared once for several products. The router's
+ * split-x product and fp16 GEMM read x in a prepared form (fp16 hi/lo parts
+ * with block scales; fp16 tiles); the matmuls of one activation (q, k and v;
+ * gate and up) can share it, as the reference shares its fp16 x across the
+ * GEMMs of one activation (aF16, ops.gemm2.js:151-196). An extension of
+ * quant.matmul (ops.js:827-1101), which has no such step; the outputs are its
+ * bits all the same:
+ *  - eff_qmatmul_x_layout: the bytes of the prepared x the router's path for
+ *    this call reads, and an id of its layout: calls whose ids, tokens and k
+ *    agree can share one prepared x (the split-x layouts are shared across
+ *    IQ2_XXS, Q8_0 and Q6_K, and across any rows). EFF_NOT_APPLICABLE where
+ *    the path reads x itself (the GEMVs, including the one-launch split-x
+ *    product up to 8 tokens, and the token groups): run eff_qmatmul.
+ *  - eff_qmatmul_prepare_x: x (tokens x k f32) into xp in that layout.
+ *  - eff_qmatmul_prepared: the product from xp; the same bits as eff_qmatmul
+ *    over the x xp was prepared from (with the same tokens, k and a type of
+ *    the same layout). EFF_NOT_APPLICABLE as eff_qmatmul_x_layout. */
+int eff_qmatmul_x_layout(eff_ctx *ctx, int type, uint32_t rows, uint32_t k, uint32_t tokens, size_t *bytes,
+                         uint32_t *layout);
+int eff_qmatmul_prepare_x(eff_ctx *ctx, int type, eff_buf *x, eff_buf *xp, uint32_t rows, uint32_t k,
+                          uint32_t tokens);
+int eff_qmatmul_prepared(eff_ctx *ctx, int type, eff_buf *w, eff_buf *xp, eff_buf *y, uint32_t rows, uint32_t k,
+                         uint32_t tokens);
 
 /* The decode GEMV alone (quant.gemv.matmul, ops.gemv.js:148-164): f32
  * accumulation, 1..GEMV max tokens. EFF_NOT_APPLICABLE outside that range. */

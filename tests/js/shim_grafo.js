@@ -5,6 +5,9 @@
 //     nothing from the pool; `gemvAmpliado` widens them;
 //   * ctx.recycle() destroys an expired size class without waiting for the
 //     device (the work enqueued before it still runs, and gives its result);
+//   * quant.matmul prepares the split-x product's x once for the products of
+//     one activation (one preparation per layout), with the bits of a
+//     preparation per call;
 //   * ctx.grabaGrafo records a chain of quant.matmul calls, and each replay,
 //     after new x is written, gives the bits of the same chain run eagerly.
 // Prints one JSON line with the figures the Python side checks.
@@ -91,6 +94,40 @@ async function main() {
     out.memo = { q_k_shared: c1 - c0, after_olvida: c2 - c1, new_mark: c3 - c2, no_mark: c4 - c3 };
     ctx.recycle();
     xo.destroy(); wq.destroy(); wk.destroy();
+  }
+
+  // ---- quant.matmul's prepared x (split-x), shared by the products of one x -----
+  {
+    const k = 2048, m = 33;
+    const bytes = { Q4_K: 144, Q6_K: 210, IQ2_XXS: 66 };
+    const mats = [['Q4_K', 256, 31], ['Q6_K', 128, 32], ['IQ2_XXS', 192, 33], ['Q4_K', 96, 34]];
+    const ws = mats.map(([tipo, rows, seed]) => {
+      const b = device.createBuffer({ size: Math.ceil((rows * k / 256 * bytes[tipo] + 4) / 4) * 4, label: tipo });
+      device.queue.writeBuffer(b, 0, eff.quantize(tipo, eff.fillNormal(seed, 0.02, rows * k)));
+      return b;
+    });
+    const xv = eff.fillNormal(35, 1.0, m * k);
+    const x = ops.upload(xv, 'x');                       // a pool buffer: it has a mark
+    const prep = () => device.stats().splitX;
+    const p0 = prep();
+    const ys = [];
+    for (let i = 0; i < mats.length; i++) ys.push(await ops.matmul(mats[i][0], ws[i], x, mats[i][1], k, m));
+    const p1 = prep();
+    ops.olvida();
+    await ops.matmul('Q4_K', ws[0], x, 256, k, m);
+    const p2 = prep();
+    // an x from outside the pool has no mark: prepared per call, the same bits
+    const xo = device.createBuffer({ size: m * k * 4, label: 'xo' });
+    device.queue.writeBuffer(xo, 0, xv);
+    for (let i = 0; i < mats.length; i++) {
+      const y = await ops.matmul(mats[i][0], ws[i], xo, mats[i][1], k, m);
+      assert.deepStrictEqual(Array.from(await rd(y, mats[i][1] * m)), Array.from(await rd(ys[i], mats[i][1] * m)));
+    }
+    const p3 = prep();
+    out.memoSplit = { shared: p1 - p0, after_olvida: p2 - p1, no_mark: p3 - p2 };
+    ctx.recycle();
+    xo.destroy();
+    for (const b of ws) b.destroy();
   }
 
   // ---- recycle() without a device wait ----------------------------------------

@@ -88,7 +88,8 @@ def test_js_shim_gpu(eff, orc, tmp_path):
 def test_js_graph_pool_and_gemv2_applicability():
     """tests/js/shim_grafo.js: gemv ops are null where GEMV2 is (and lend
     nothing), gemm2 converts x once per allocation mark (olvida() clears
-    it), recycle() destroys an expired size class without waiting for the
+    it), quant.matmul prepares the split-x product's x once per layout for the
+    products of one x, recycle() destroys an expired size class without waiting for the
     device, and a recorded chain of 30 quant.matmul calls replays bit-equal to
     the eager chain for each new x (the checks of bits are inside the shim)."""
     r = subprocess.run(["node", os.path.join(HERE, "js", "shim_grafo.js")], capture_output=True, text=True,
@@ -99,6 +100,8 @@ def test_js_graph_pool_and_gemv2_applicability():
     assert out["gemv2"] is True
     # gemm2's aF16 memo: q and k of one x share one conversion; olvida(), a new mark, no mark: one each
     assert out["memo"] == {"q_k_shared": 1, "after_olvida": 1, "new_mark": 1, "no_mark": 2}, out["memo"]
+    # quant.matmul at 33 tokens: Q4_K (twice), Q6_K and IQ2_XXS of one x prepare it twice (two layouts)
+    assert out["memoSplit"] == {"shared": 2, "after_olvida": 1, "no_mark": 4}, out["memoSplit"]
     rc = out["recycle"]
     # 60 GEMMs of 2048 x 8192 x 2048 were still running when recycle() returned
     assert rc["drain_us"] > 2000, rc

@@ -666,6 +666,91 @@ def test_gemm_prepared_x_serves_several_products(ctx, eff, tname, tokens, lote):
     xh.free()
 
 
+@pytest.mark.parametrize("tokens", [9, 33, 100])
+def test_matmul_prepared_x_serves_several_products(ctx, eff, tokens):
+    """The router's x prepared once per layout (eff_qmatmul_prepare_x) serves
+    products of every type of that layout and any rows, each with the bits of
+    eff_qmatmul over x: IQ2_XXS, Q6_K and Q8_0 share one split-x layout, Q2_K
+    and Q4_K have their own (with their group sums), and Q8_0 from the GEMM's
+    threshold reads the fp16 GEMM's. One preparation per layout in all."""
+    k = 2304
+    mats = [("Q2_K", 77), ("Q2_K", 150), ("Q4_K", 96), ("Q4_K", 33), ("IQ2_XXS", 77), ("Q6_K", 64),
+            ("Q8_0", 130), ("Q8_0", 40)]
+    x = eff.fill_normal(8100 + tokens, 1.0, tokens * k)
+    xb = ctx.upload(x)
+    groups = {}
+    for tname, r in mats:
+        nbytes, lay = ctx.qmatmul_x_layout(eff.TYPES[tname], r, k, tokens)
+        groups.setdefault(lay, []).append((tname, r, nbytes))
+    split = {lay for lay in groups if lay >= 0x100}
+    expect = {0x101: {"Q2_K"}, 0x102: {"Q4_K"}, 0x100: {"IQ2_XXS", "Q6_K"} | ({"Q8_0"} if tokens < 64 else set())}
+    assert split == set(expect), groups
+    for lay in split:
+        assert {tname for tname, _, _ in groups[lay]} == expect[lay], (lay, groups[lay])
+        assert len({nb for _, _, nb in groups[lay]}) == 1, groups[lay]   # the bytes follow tokens and k only
+    assert len(groups) == len(split) + (1 if tokens >= 64 else 0)
+    before = ctx.stats()
+    for lay, members in groups.items():
+        tname0, r0, nbytes = members[0]
+        xp = ctx.alloc(max(nb for _, _, nb in members))
+        ctx.qmatmul_prepare_x(eff.TYPES[tname0], xb, xp, r0, k, tokens)
+        for tname, r, _ in members:
+            t, data, _, _ = make_weights(eff, tname, r, k, 8200 + r + tokens)
+            wb, y1, y2 = ctx.upload(data), ctx.alloc(tokens * r * 4), ctx.alloc(tokens * r * 4)
+            ctx.qmatmul_prepared(t, wb, xp, y1, r, k, tokens)
+            ctx.qmatmul(t, wb, xb, y2, r, k, tokens)
+            assert np.array_equal(y1.read(np.uint32), y2.read(np.uint32)), (tname, r, tokens, hex(lay))
+            for b in (wb, y1, y2):
+                b.free()
+        xp.free()
+    after = ctx.stats()
+    n_mats = len(mats)
+    n_gemm = len(groups[min(groups)]) if tokens >= 64 else 0
+    # one preparation per layout, plus the one of each eff_qmatmul beside it
+    assert after["split_x"] - before["split_x"] == len(split) + (n_mats - n_gemm)
+    assert after["gemm_x"] - before["gemm_x"] == (1 + n_gemm if tokens >= 64 else 0)
+    assert after["split"] - before["split"] == 2 * (n_mats - n_gemm)
+    xb.free()
+
+
+def test_matmul_prepared_x_not_applicable_and_errors(ctx, eff):
+    """Calls whose path reads x itself answer NOT_APPLICABLE (the GEMVs, the
+    one-launch split-x product up to 8 tokens, the token groups, the split-x
+    configuration whose k halves add into y); a forced configuration that
+    prepares x gives eff_qmatmul's bits; a short buffer is refused."""
+    k = 2304
+    for tname, r, kk, tokens in [("Q2_K", 64, k, 4), ("Q2_K", 64, k, 8), ("IQ2_XXS", 64, k, 5),
+                                 ("Q4_K", 64, k, 8), ("Q8_0R", 64, k, 33), ("Q8_0", 64, 2080, 33)]:
+        with pytest.raises(eff.NotApplicable):
+            ctx.qmatmul_x_layout(eff.TYPES[tname], r, kk, tokens)
+    t, data, _, _ = make_weights(eff, "Q2_K", 77, k, 8300)
+    wb = ctx.upload(data)
+    try:
+        ctx.set_option(eff.OPT_SPLIT_CONFIG, 3)
+        with pytest.raises(eff.NotApplicable):
+            ctx.qmatmul_x_layout(t, 77, k, 33)
+        ctx.set_option(eff.OPT_SPLIT_CONFIG, 1)      # 32 rows x 8 waves, x prepared, at 8 tokens
+        nbytes, lay = ctx.qmatmul_x_layout(t, 77, k, 8)
+        assert lay == 0x101
+        x = eff.fill_normal(8301, 1.0, 8 * k)
+        xb, xp = ctx.upload(x), ctx.alloc(nbytes)
+        y1, y2 = ctx.alloc(8 * 77 * 4), ctx.alloc(8 * 77 * 4)
+        ctx.qmatmul_prepare_x(t, xb, xp, 77, k, 8)
+        ctx.qmatmul_prepared(t, wb, xp, y1, 77, k, 8)
+        ctx.qmatmul(t, wb, xb, y2, 77, k, 8)
+        assert np.array_equal(y1.read(np.uint32), y2.read(np.uint32))
+        small = ctx.alloc(64)
+        with pytest.raises(eff.EffError):
+            ctx.qmatmul_prepared(t, wb, small, y1, 77, k, 8)                    # xp too small
+        with pytest.raises(eff.EffError):
+            ctx.qmatmul_prepare_x(t, xb, xp, 77, k, 9)                          # x too small
+        for b in (xb, xp, y1, y2, small):
+            b.free()
+    finally:
+        ctx.set_option(eff.OPT_SPLIT_CONFIG, 0)
+        wb.free()
+
+
 def test_read_ticket_snapshots_at_begin(ctx, eff):
     """eff_read_begin enqueues the copy at once: a write enqueued after it is
     not in the snapshot; the buffer can be reused right away."""
