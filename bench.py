@@ -129,6 +129,38 @@ class FusedConfig:
             b.free()
 
 
+class SharedXConfig:
+    """n products of one x (a layer's q, k and v): eff_qmatmul per product,
+    each preparing x for the split-x product, or x prepared once
+    (eff_qmatmul_prepare_x) and eff_qmatmul_prepared per product. The weight
+    copies rotate over the products."""
+
+    def __init__(self, eff, ctx, tname, rows, k, tokens, n, seed, shared):
+        self.inner = Config(eff, ctx, tname, rows, k, tokens, seed)
+        self.copies, self.w_bytes = self.inner.copies, self.inner.w_bytes
+        self.n, self.shared, self.t = n, shared, self.inner.t
+        self.rows, self.k, self.tokens = rows, k, tokens
+        self.xp = ctx.alloc(ctx.qmatmul_x_layout(self.t, rows, k, tokens)[0])
+        self.bytes = n * self.inner.bytes
+        self.flops = n * self.inner.flops
+        self.gemm = self.inner.gemm
+
+    def step(self, ctx, i):
+        c = self.inner
+        if self.shared:
+            ctx.qmatmul_prepare_x(self.t, c.x, self.xp, self.rows, self.k, self.tokens)
+        for j in range(self.n):
+            w = c.w[(i * self.n + j) % c.copies]
+            if self.shared:
+                ctx.qmatmul_prepared(self.t, w, self.xp, c.y, self.rows, self.k, self.tokens)
+            else:
+                ctx.qmatmul(self.t, w, c.x, c.y, self.rows, self.k, self.tokens)
+
+    def free(self):
+        self.inner.free()
+        self.xp.free()
+
+
 class ReadConfig:
     """A plain streaming read of a configuration's weight copies
     (eff_read_floor), rotated like its steps: the floor a GEMV's time is
@@ -536,6 +568,24 @@ def main():
                           "GB/s": round(nbytes / (res["fused"] * 1e-3) / 1e9, 1), "bound": "hbm",
                           "roofline_frac": round(nbytes / (HBM_PEAK_GBS * 1e9) / (res["fused"] * 1e-3), 4),
                           "path": "fused gemv"}
+            print(f"# {key}: {sweep[key]}", file=sys.stderr, flush=True)
+
+    # P1: the router's x prepared once for three products of one activation
+    if not args.no_sweep:
+        for tn, m in (("Q4_K", 32), ("Q2_K", 128)):
+            key = f"P1 q+k+v shared x 3 x {tn} N=8192 K=2048 M={m}"
+            if args.only and args.only not in key:
+                continue
+            res = {}
+            for shared in (True, False):
+                cfg = SharedXConfig(eff, ctx, tn, 8192, 2048, m, 3, 950 + m, shared)
+                res[shared] = time_steps(torch, ctx, cfg, 40, 5, warm_replays=3, timed=3)
+                nbytes, flops = cfg.bytes, cfg.flops
+                cfg.free()
+            sweep[key] = {"us": round(res[True] * 1e3, 2), "separate_us": round(res[False] * 1e3, 2),
+                          "TFLOP/s": round(flops / (res[True] * 1e-3) / 1e12, 2),
+                          "GB/s": round(nbytes / (res[True] * 1e-3) / 1e9, 1),
+                          "path": "split-x, x prepared once (eff_qmatmul_prepare_x + 3 x eff_qmatmul_prepared)"}
             print(f"# {key}: {sweep[key]}", file=sys.stderr, flush=True)
 
     chain = None
