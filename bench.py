@@ -48,8 +48,9 @@ def alg_bytes(eff, tname, rows, k, tokens):
 
 
 class Config:
-    def __init__(self, eff, ctx, tname, rows, k, tokens, seed, topk=0, fused_head=True):
+    def __init__(self, eff, ctx, tname, rows, k, tokens, seed, topk=0, fused_head=True, cpu_path=False):
         self.tname, self.rows, self.k, self.tokens, self.topk = tname, rows, k, tokens, topk
+        self.cpu_path = cpu_path
         self.fused_head = fused_head and tokens == 1
         base = "Q8_0" if tname == "Q8_0R" else tname
         self.t = eff.TYPES[tname]
@@ -83,6 +84,9 @@ class Config:
         if self.topk and self.fused_head:
             # the decode head: the GEMV and the top-k of its logits as one call
             ctx.qgemv_topk(self.t, w, self.x, self.y, self.rows, self.k, self.topk, (), i + 1, self.out)
+            return
+        if self.cpu_path:
+            ctx.qmatmul_cpu_path(self.t, w, self.x, self.y, self.rows, self.k, self.tokens)
             return
         ctx.qmatmul(self.t, w, self.x, self.y, self.rows, self.k, self.tokens)
         if self.topk:
@@ -315,7 +319,7 @@ def time_cpu(fn, seconds):
             return n, dt
 
 
-def cpu_baseline(eff, orc, seconds):
+def cpu_baseline(eff, orc, seconds, ctx=None):
     """The reference CPU path (cpu-kernels.js driven by cpu-trabajo.js) as the
     oracle restates it: x quantized to 8-bit blocks, integer dots against Q8_0
     blocks, a pool of threads claiming row chunks (cpu.js:140-216, 350-381).
@@ -379,6 +383,17 @@ def cpu_baseline(eff, orc, seconds):
     nrm = float(np.linalg.norm(ref))
     out["gap_vs_f64"] = {"config": "C1 Q8_0 N=8192 K=2048 M=1", "rel_l2": float(np.linalg.norm(y - ref)) / nrm,
                          "max_abs_over_norm": float(np.max(np.abs(y - ref))) / nrm}
+    if ctx is not None:
+        # the GPU's product with the CPU path's arithmetic (eff_qmatmul_cpu_path) on the same bytes
+        wb, xb, yb = ctx.upload(w), ctx.upload(xs), ctx.alloc(r * 4)
+        ctx.qmatmul_cpu_path(eff.Q8_0, wb, xb, yb, r, kk, 1)
+        g = yb.read(np.uint32, r)
+        for b in (wb, xb, yb):
+            b.free()
+        yc = y.astype(np.float32).view(np.uint32)
+        out["gpu_cpu_path"] = {"config": "C1 Q8_0 N=8192 K=2048 M=1", "outputs": int(r),
+                               "bits_equal": bool(np.array_equal(g, yc)),
+                               "what": "eff_qmatmul_cpu_path on the GPU against this restatement of the CPU path"}
     return out
 
 
@@ -570,6 +585,21 @@ def main():
                           "path": "fused gemv"}
             print(f"# {key}: {sweep[key]}", file=sys.stderr, flush=True)
 
+    # the CPU path's arithmetic on the GPU (eff_qmatmul_cpu_path): C1 and C3 M=512
+    if not args.no_sweep:
+        for m in (1, 512):
+            key = f"CPU-path arithmetic Q8_0 N=8192 K=2048 M={m}"
+            if args.only and args.only not in key:
+                continue
+            cfg = Config(eff, ctx, "Q8_0", 8192, 2048, m, 300 + 8192 + m, cpu_path=True)
+            t_ms = time_steps(torch, ctx, cfg, 40 if m > 1 else 100, 5, warm_replays=3, timed=3)
+            sweep[key] = {"us": round(t_ms * 1e3, 2), "GB/s": round(cfg.bytes / (t_ms * 1e-3) / 1e9, 1),
+                          "TFLOP/s": round(cfg.flops / (t_ms * 1e-3) / 1e12, 2),
+                          "path": "eff_qmatmul_cpu_path: 8-bit x blocks, int32 block dots, f32 terms in block order "
+                                  "(the bits of the CPU path's restatement)"}
+            cfg.free()
+            print(f"# {key}: {sweep[key]}", file=sys.stderr, flush=True)
+
     # P1: the router's x prepared once for three products of one activation
     if not args.no_sweep:
         for tn, m in (("Q4_K", 32), ("Q2_K", 128)):
@@ -597,7 +627,7 @@ def main():
 
     base = None
     if not args.no_cpu:
-        base = cpu_baseline(eff, ge.oracle(), args.cpu_seconds)
+        base = cpu_baseline(eff, ge.oracle(), args.cpu_seconds, ctx)
 
     line = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,

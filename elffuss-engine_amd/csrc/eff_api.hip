@@ -77,6 +77,8 @@ struct eff_ctx {
   int64_t sx_config = 0;
   int64_t gemm_config = 0;
   int64_t sx_min_tokens = 0;        // 0: the measured default (sx_routes)
+  void *act_scratch = nullptr;      // x in the CPU path's 8-bit blocks (eff_qmatmul_cpu_path)
+  size_t act_scratch_bytes = 0;
   // Pinned staging ring of eff_buf_write: the source bytes are copied here on
   // the calling thread and the device copy is enqueued from here, so a write
   // returns without waiting for the device. `pend` holds the ring ranges whose
@@ -455,6 +457,7 @@ int eff_shutdown(eff_ctx *ctx) {
   if (ctx->topk_scratch) (void)hipFree(ctx->topk_scratch);
   if (ctx->xh_scratch) (void)hipFree(ctx->xh_scratch);
   if (ctx->sx_scratch) (void)hipFree(ctx->sx_scratch);
+  if (ctx->act_scratch) (void)hipFree(ctx->act_scratch);
   for (auto &p : ctx->stage_pend) (void)hipEventDestroy(p.ev);
   for (hipEvent_t ev : ctx->events) (void)hipEventDestroy(ev);
   if (ctx->stage) (void)hipHostFree(ctx->stage);
@@ -1028,6 +1031,28 @@ int eff_qmatmul_prepared(eff_ctx *ctx, int type, eff_buf *w, eff_buf *xp, eff_bu
     ++ctx->stats.gemm;
   }
   if (e != hipSuccess) return hip_fail(ctx, e, "matmul prepared launch");
+  return EFF_OK;
+}
+
+int eff_qmatmul_cpu_path(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y, uint32_t rows, uint32_t k,
+                         uint32_t tokens) {
+  if (!ctx) return EFF_E_INVALID;
+  WeightView wv;
+  int rc = weight_view(ctx, type, w, x, y, rows, k, tokens, wv, "cpu path");
+  if (rc) return rc;
+  if (type != EFF_TYPE_Q8_0) {
+    ++ctx->stats.not_applicable;
+    return EFF_NOT_APPLICABLE;
+  }
+  if ((uint64_t)tokens * (k / 32u) >= (1ull << 31))
+    return fail(ctx, EFF_E_INVALID, "cpu path: %u tokens of %u values are too many blocks", tokens, k);
+  if ((rc = use_device(ctx)) ||
+      (rc = grow(ctx, &ctx->act_scratch, &ctx->act_scratch_bytes, cpu_path_act_bytes(tokens, k), "cpu path x")))
+    return rc;
+  const hipError_t e = launch_cpu_path(wv, (const float *)x->ptr, (float *)y->ptr, tokens, ctx->act_scratch,
+                                       ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "cpu path launch");
+  ++ctx->stats.cpu_path;
   return EFF_OK;
 }
 

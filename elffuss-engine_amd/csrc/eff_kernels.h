@@ -132,6 +132,13 @@ hipError_t launch_sx_prepare(uint32_t layout, const float *x, uint32_t tokens, u
 hipError_t launch_sx_prepared(const WeightView &wv, const void *xprep, float *y, uint32_t tokens, int cfg,
                               hipStream_t stream);
 
+// The reference CPU path's arithmetic for Q8_0 (eff_cpu_path.hip): x into
+// 40-byte 8-bit blocks in `act` (cpu_path_act_bytes(...)), then per row and
+// token the block terms added in block order; the bits of or_cpu_matmul.
+size_t cpu_path_act_bytes(uint32_t tokens, uint32_t k);
+hipError_t launch_cpu_path(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *act,
+                           hipStream_t stream);
+
 // Embedding gather: out[t] = dequantized row ids[t] (bit-identical to dequant);
 // with the norm, also nrm[t] = x[t] / sqrt(mean(x[t]^2) + eps) * wn, dim <= kGatherNormMaxDim.
 constexpr uint32_t kGatherNormMaxDim = 32768;

@@ -44,7 +44,7 @@ class Stats(ctypes.Structure):
     _fields_ = [("gemv", ctypes.c_uint64), ("gemm", ctypes.c_uint64), ("skinny", ctypes.c_uint64),
                 ("dequant", ctypes.c_uint64), ("topk", ctypes.c_uint64), ("not_applicable", ctypes.c_uint64),
                 ("split", ctypes.c_uint64), ("fused", ctypes.c_uint64), ("gather", ctypes.c_uint64),
-                ("gemm_x", ctypes.c_uint64), ("split_x", ctypes.c_uint64)]
+                ("gemm_x", ctypes.c_uint64), ("split_x", ctypes.c_uint64), ("cpu_path", ctypes.c_uint64)]
 
 
 _lib = None
@@ -109,6 +109,7 @@ def lib():
         "eff_gemm_x_layout": ([p, i32, u32, u32, u32, u32, ctypes.POINTER(sz), ctypes.POINTER(u32)], i32),
         "eff_gemm_prepare_x": ([p, i32, p, p, u32, u32, u32, u32], i32),
         "eff_qgemm_prepared": ([p, i32, p, p, p, u32, u32, u32, u32], i32),
+        "eff_qmatmul_cpu_path": ([p, i32, p, p, p, u32, u32, u32], i32),
         "eff_qmatmul_x_layout": ([p, i32, u32, u32, u32, ctypes.POINTER(sz), ctypes.POINTER(u32)], i32),
         "eff_qmatmul_prepare_x": ([p, i32, p, p, u32, u32, u32], i32),
         "eff_qmatmul_prepared": ([p, i32, p, p, p, u32, u32, u32], i32),
@@ -138,7 +139,7 @@ EXPORTED = ("eff_type_from_name eff_type_name eff_type_geometry eff_init eff_shu
             "eff_read_begin eff_read_end eff_read_poll eff_read_error eff_read_release "
             "eff_bytes_reordered eff_bytes_buffer_r eff_blocks_from_buffer eff_scales_from eff_buf_mark_r "
             "eff_buf_blocks_r eff_buf_write_r eff_repack eff_unrepack eff_quantize eff_fill_normal eff_qmatmul eff_qgemv "
-            "eff_qgemm eff_qgemm_planned eff_gemm_x_layout eff_gemm_prepare_x eff_qgemm_prepared eff_qmatmul_x_layout eff_qmatmul_prepare_x eff_qmatmul_prepared eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_noalloc eff_qgemv_topk eff_topk_out_bytes eff_read_floor").split()
+            "eff_qgemm eff_qgemm_planned eff_gemm_x_layout eff_gemm_prepare_x eff_qgemm_prepared eff_qmatmul_x_layout eff_qmatmul_prepare_x eff_qmatmul_prepared eff_qmatmul_cpu_path eff_qgemv_multi eff_dequant eff_gather eff_gather_norm eff_topk eff_topk_noalloc eff_qgemv_topk eff_topk_out_bytes eff_read_floor").split()
 
 
 def type_code(t):
@@ -386,6 +387,10 @@ class Context:
     def qgemm_prepared(self, t, w, xh, y, rows, k, tokens, plan_tokens=None):
         self._check(lib().eff_qgemm_prepared(self.h, type_code(t), w.handle, xh.handle, y.handle, rows, k, tokens,
                                              plan_tokens or tokens))
+
+    def qmatmul_cpu_path(self, t, w, x, y, rows, k, tokens=1):
+        """Y = W X with the reference CPU path's arithmetic (Q8_0; eff_qmatmul_cpu_path)."""
+        self._check(lib().eff_qmatmul_cpu_path(self.h, type_code(t), w.handle, x.handle, y.handle, rows, k, tokens))
 
     def qmatmul_x_layout(self, t, rows, k, tokens):
         """(bytes, layout id) of the x the router's path for this call reads

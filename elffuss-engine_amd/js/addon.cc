@@ -274,6 +274,7 @@ napi_value Stats(napi_env env, napi_callback_info info) {
   napi_set_named_property(env, o, "gather", make_int(env, (int64_t)s.gather));
   napi_set_named_property(env, o, "gemmX", make_int(env, (int64_t)s.gemm_x));
   napi_set_named_property(env, o, "splitX", make_int(env, (int64_t)s.split_x));
+  napi_set_named_property(env, o, "cpuPath", make_int(env, (int64_t)s.cpu_path));
   return o;
 }
 
@@ -536,6 +537,17 @@ napi_value QGemmPrepared(napi_env env, napi_callback_info info) {
   return status(env, ctx, rc);
 }
 
+// qmatmulCpuPath(ctx, type, w, x, y, rows, k, tokens) -> 0 | null
+napi_value QMatmulCpuPath(napi_env env, napi_callback_info info) {
+  napi_value a[8];
+  get_args(env, info, 8, a);
+  eff_ctx *ctx = external<eff_ctx>(env, a[0]);
+  int rc = eff_qmatmul_cpu_path(ctx, (int)i64(env, a[1]), external<eff_buf>(env, a[2]), external<eff_buf>(env, a[3]),
+                                external<eff_buf>(env, a[4]), (uint32_t)i64(env, a[5]), (uint32_t)i64(env, a[6]),
+                                (uint32_t)i64(env, a[7], 1));
+  return status(env, ctx, rc);
+}
+
 // qmatmulXLayout(ctx, type, rows, k, tokens) -> {bytes, layout} | null
 napi_value QMatmulXLayout(napi_env env, napi_callback_info info) {
   napi_value a[5];
@@ -681,6 +693,7 @@ napi_value Register(napi_env env, napi_value exports) {
       {"graphDestroy", GraphDestroy}, {"gemmXLayout", GemmXLayout}, {"gemmPrepareX", GemmPrepareX},
       {"qgemmPrepared", QGemmPrepared}, {"qmatmulXLayout", QMatmulXLayout},
       {"qmatmulPrepareX", QMatmulPrepareX}, {"qmatmulPrepared", QMatmulPrepared},
+      {"qmatmulCpuPath", QMatmulCpuPath},
   };
   for (auto &f : fns) {
     napi_value v;

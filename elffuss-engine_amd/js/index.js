@@ -749,6 +749,21 @@ function createQuantOps(device, opts) {
       }
       return Promise.resolve(y);
     },
+    // Y = W . X for Q8_0 with the reference CPU path's arithmetic (8-bit x
+    // blocks and integer block dots, cpu.js:350-381): the bits cpu-kernels.js
+    // gives, for a caller that needs the GPU and CPU backends to agree; null
+    // for the other types (the CPU path has no kernel for them,
+    // cpu-trabajo.js:31). Not in the reference's quant ops, whose GPU path
+    // is f32 (as quant.matmul here).
+    matmulCPU(type, wBuf, xBuf, rows, k, tokens) {
+      const t = tokens === undefined ? 1 : tokens;
+      const i = quantInfo(type);
+      if (k % i.blockElems !== 0) throw new Error(`matmul ${type}: k=${k} no es múltiplo de ${i.blockElems}`);
+      if (type !== 'Q8_0') return Promise.resolve(null);
+      const y = ctx.alloc(rows * t * 4, 'matmul.y');
+      native.qmatmulCpuPath(device._ctx, i.code, wBuf._h, xBuf._h, y._h, rows, k, t);
+      return Promise.resolve(y);
+    },
     // Empties the memo of prepared activations (gemm2.olvida()).
     olvida() { memo.olvida(); },
     // The IQ2_XXS grid is part of the library (no upload needed).

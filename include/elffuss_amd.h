@@ -98,6 +98,7 @@ typedef struct eff_stats {
                            split-x router call but those of Q2_K and IQ2_XXS up to 8 tokens under the
                            automatic configuration, which prepare x inside the product; one per
                            eff_qmatmul_prepare_x for it) */
+  uint64_t cpu_path;    /* products with the reference CPU path's arithmetic (eff_qmatmul_cpu_path) */
 } eff_stats;
 
 /* ---- types and geometry -------------------------------------------------- */
@@ -319,6 +320,20 @@ int eff_qmatmul_prepare_x(eff_ctx *ctx, int type, eff_buf *x, eff_buf *xp, uint3
                           uint32_t tokens);
 int eff_qmatmul_prepared(eff_ctx *ctx, int type, eff_buf *w, eff_buf *xp, eff_buf *y, uint32_t rows, uint32_t k,
                          uint32_t tokens);
+
+/* Y = W . X for Q8_0 with the reference CPU path's arithmetic (cpu-kernels.js
+ * matvec_q8_0 / matmul_q8_0 via mm, cpu.js:350-381, over the row chunks of
+ * cpu-trabajo.js:27-72), on the GPU: each token's x in 8-bit blocks of 32
+ * (d = max|x| / 127, q = round(x / d) ties away from zero; BACT = 40,
+ * cpu.js:24-27), per block the exact int32 dot of the quants, per row the
+ * terms f32(isum) * (d_w * d_x) added in block order, each operation rounded
+ * on its own. The outputs are the bits of that path as restated and pinned
+ * (or_cpu_matmul); they differ from eff_qmatmul's f32-accurate ones by the
+ * 8-bit activations (about 5e-3 relative L2). EFF_NOT_APPLICABLE for other
+ * types (the CPU path's kernels are Q8_0 and Q4_0, cpu-trabajo.js:31);
+ * EFF_E_SHAPE if k % 32 != 0; EFF_E_INVALID for tokens * k / 32 >= 2^31. */
+int eff_qmatmul_cpu_path(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
+                         uint32_t rows, uint32_t k, uint32_t tokens);
 
 /* The decode GEMV alone (quant.gemv.matmul, ops.gemv.js:148-164): f32
  * accumulation, 1..GEMV max tokens. EFF_NOT_APPLICABLE outside that range. */

@@ -130,6 +130,18 @@ async function main() {
     for (const b of ws) b.destroy();
   }
 
+  // ---- quant.matmulCPU: the CPU path's arithmetic (Q8_0), null for other types -----
+  {
+    const rows = 96, k = 512, m = 3;
+    const wq = ops.upload(eff.quantize('Q8_0', eff.fillNormal(41, 0.02, rows * k)), 'w');
+    const w4 = ops.upload(eff.quantize('Q4_K', eff.fillNormal(42, 0.02, rows * k)), 'w4');
+    const x = ops.upload(eff.fillNormal(43, 1.0, m * k), 'x');
+    const y = await ops.matmulCPU('Q8_0', wq, x, rows, k, m);
+    out.matmulCPU = { q4k_null: (await ops.matmulCPU('Q4_K', w4, x, rows, k, m)) === null,
+      y: Array.from(await rd(y, rows * m)) };
+    ctx.recycle();
+  }
+
   // ---- recycle() without a device wait ----------------------------------------
   {
     const rows = 8192, k = 2048, m = 2048, reps = 60;

@@ -37,6 +37,24 @@ def test_c1_q8_0_gemv_8192x2048(ctx, eff, orc, tname):
     check_close(y, orc.gemv_f64(orc.Q8_0, gguf, 8192, 2048, x, 1), f"C1 {tname}")
 
 
+@pytest.mark.parametrize("tokens", [1, 512])
+def test_c1_c3_cpu_path_product_bit_exact(ctx, eff, orc, tokens):
+    """C1 (one token) and C3 M = 512 through the CPU path's arithmetic
+    (eff_qmatmul_cpu_path): every output bit-equal to the oracle's restatement
+    of cpu-kernels.js (or_cpu_matmul), the path north_star names."""
+    rows, k = 8192, 2048
+    t, data, gguf, n = make_weights(eff, "Q8_0", rows, k, 105 + tokens)
+    x = eff.fill_normal(106 + tokens, 1.0, tokens * k)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    ctx.qmatmul_cpu_path(t, wb, xb, yb, rows, k, tokens)
+    got = yb.read(np.uint32, tokens * rows)
+    for b in (wb, xb, yb):
+        b.free()
+    ref = orc.cpu_matmul(orc.Q8_0, gguf, rows, k, x, tokens, 8)
+    assert np.array_equal(got, ref.view(np.uint32).reshape(-1)), \
+        f"{int(np.sum(got != ref.view(np.uint32).reshape(-1)))} of {got.size} outputs differ"
+
+
 def test_c2_q4_k_gemv_2048x8192(ctx, eff, orc):
     gguf, x, y = run(ctx, eff, "Q4_K", 2048, 8192, 1, 202)
     check_close(y, orc.gemv_f64(orc.Q4_K, gguf, 2048, 8192, x, 1), "C2 Q4_K")

@@ -85,11 +85,11 @@ def test_js_shim_gpu(eff, orc, tmp_path):
 
 
 @pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
-def test_js_graph_pool_and_gemv2_applicability():
+def test_js_graph_pool_and_gemv2_applicability(eff, orc):
     """tests/js/shim_grafo.js: gemv ops are null where GEMV2 is (and lend
     nothing), gemm2 converts x once per allocation mark (olvida() clears
     it), quant.matmul prepares the split-x product's x once per layout for the
-    products of one x, recycle() destroys an expired size class without waiting for the
+    products of one x, quant.matmulCPU gives the CPU path's bits, recycle() destroys an expired size class without waiting for the
     device, and a recorded chain of 30 quant.matmul calls replays bit-equal to
     the eager chain for each new x (the checks of bits are inside the shim)."""
     r = subprocess.run(["node", os.path.join(HERE, "js", "shim_grafo.js")], capture_output=True, text=True,
@@ -102,6 +102,12 @@ def test_js_graph_pool_and_gemv2_applicability():
     assert out["memo"] == {"q_k_shared": 1, "after_olvida": 1, "new_mark": 1, "no_mark": 2}, out["memo"]
     # quant.matmul at 33 tokens: Q4_K (twice), Q6_K and IQ2_XXS of one x prepare it twice (two layouts)
     assert out["memoSplit"] == {"shared": 2, "after_olvida": 1, "no_mark": 4}, out["memoSplit"]
+    # quant.matmulCPU: the CPU path's bits (Q8_0, 96 x 512, 3 tokens), null for Q4_K
+    mc = out["matmulCPU"]
+    assert mc["q4k_null"] is True
+    w = eff.quantize("Q8_0", eff.fill_normal(41, 0.02, 96 * 512))
+    ref = orc.cpu_matmul(orc.Q8_0, w, 96, 512, eff.fill_normal(43, 1.0, 3 * 512), 3, 2)
+    assert mc["y"] == ref.view(np.uint32).reshape(-1).tolist()
     rc = out["recycle"]
     # 60 GEMMs of 2048 x 8192 x 2048 were still running when recycle() returned
     assert rc["drain_us"] > 2000, rc

@@ -751,6 +751,86 @@ def test_matmul_prepared_x_not_applicable_and_errors(ctx, eff):
         wb.free()
 
 
+# ---- the reference CPU path's arithmetic (eff_qmatmul_cpu_path) ----------------------------
+
+@pytest.mark.parametrize("rows,k,tokens", [(77, 32, 1), (300, 2080, 3), (64, 4096, 65), (130, 2048, 7),
+                                           (33, 256, 130)])
+def test_cpu_path_product_bit_exact(ctx, eff, orc, rows, k, tokens):
+    """The CPU path's arithmetic on the GPU gives the bits of the oracle's
+    restatement of it (or_cpu_matmul: 8-bit x blocks, int32 block dots, the
+    f32 terms added in block order): more than 64 blocks per row (two
+    chunks), more than 64 tokens (two and three token chunks), block counts
+    that are not multiples of 64, rows that do not fill the last workgroup."""
+    t, data, gguf, n = make_weights(eff, "Q8_0", rows, k, 1200 + rows + k + tokens)
+    x = eff.fill_normal(1300 + rows + tokens, 1.0, tokens * k)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    before = ctx.stats()["cpu_path"]
+    ctx.qmatmul_cpu_path(t, wb, xb, yb, rows, k, tokens)
+    assert ctx.stats()["cpu_path"] == before + 1
+    ref = orc.cpu_matmul(orc.Q8_0, gguf, rows, k, x, tokens, 4)
+    got = yb.read(np.float32, tokens * rows).reshape(tokens, rows)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
+        f"{int(np.sum(got.view(np.uint32) != ref.view(np.uint32)))} outputs differ"
+    for b in (wb, xb, yb):
+        b.free()
+
+
+def test_cpu_path_product_edge_blocks(ctx, eff, orc):
+    """Blocks whose quantization the CPU path's rounding decides: ties at
+    x / d = n + 1/2 in both signs (max |x| = 127 and 63.5, so 1 / d is exact),
+    an all-zero block (d = 0: zero quants, zero term), one value per block,
+    large and small magnitudes; bit-equal to the restatement, whose block
+    fields are checked here too."""
+    rows, k, tokens = 40, 256, 4
+    x = np.zeros((tokens, k), np.float32)
+    x[0, :32] = [127.0] + [v + 0.5 for v in range(-15, 16)]
+    x[0, 32:64] = [63.5] + [(v + 0.5) / 2 for v in range(-15, 16)]
+    x[1, 64] = -3.0e5                         # one value in its block
+    x[1, 96:128] = np.linspace(-1e-30, 1e-30, 32, dtype=np.float32)
+    x[2] = eff.fill_normal(1401, 1.0, k)
+    x[3] = eff.fill_normal(1402, 1e4, k)
+    x = x.reshape(-1)
+    acts = orc.cpu_quantize_acts(x, k, tokens)
+    assert acts[0]["d"] == 1.0 and list(acts[0]["q"][1:4]) == [-15, -14, -13]   # -14.5 -> -15, -13.5 -> -14
+    assert acts[0]["q"][16] == 1 and acts[0]["q"][15] == -1                       # 0.5 -> 1, -0.5 -> -1
+    assert acts[1]["d"] == 0.5 and acts[1]["q"][16] == 1
+    assert acts[8]["d"] == 0.0 and not acts[8]["q"].any()                        # an all-zero block
+    assert acts[10]["q"][0] == -127 and not acts[10]["q"][1:].any()              # one value in its block
+    t, data, gguf, n = make_weights(eff, "Q8_0", rows, k, 1403)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    ctx.qmatmul_cpu_path(t, wb, xb, yb, rows, k, tokens)
+    ref = orc.cpu_matmul(orc.Q8_0, gguf, rows, k, x, tokens, 2)
+    assert np.array_equal(yb.read(np.uint32, tokens * rows), ref.view(np.uint32).reshape(-1))
+    for b in (wb, xb, yb):
+        b.free()
+
+
+def test_cpu_path_product_gap_and_errors(ctx, eff, orc):
+    """Against the f64 product the CPU path's 8-bit activations cost about
+    5e-3 relative L2, the gap the default router does not have; other types
+    are NOT_APPLICABLE (its kernels are Q8_0 and Q4_0), k not a multiple of
+    32 is a shape error."""
+    rows, k, tokens = 256, 2048, 2
+    t, data, gguf, n = make_weights(eff, "Q8_0", rows, k, 1500)
+    x = eff.fill_normal(1501, 1.0, tokens * k)
+    wb, xb, y1, y2 = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4), ctx.alloc(tokens * rows * 4)
+    ctx.qmatmul_cpu_path(t, wb, xb, y1, rows, k, tokens)
+    ctx.qmatmul(t, wb, xb, y2, rows, k, tokens)
+    ref = orc.gemv_f64(orc.Q8_0, gguf, rows, k, x, tokens)
+    gap = np.linalg.norm(y1.read(np.float32).reshape(ref.shape) - ref) / np.linalg.norm(ref)
+    acc = np.linalg.norm(y2.read(np.float32).reshape(ref.shape) - ref) / np.linalg.norm(ref)
+    print(f"cpu path against f64: {gap:.2e}; default router: {acc:.2e}", flush=True)
+    assert 1e-3 < gap < 2e-2 and acc < 1e-5
+    t4, data4, _, _ = make_weights(eff, "Q4_K", rows, k, 1502)
+    w4 = ctx.upload(data4)
+    with pytest.raises(eff.NotApplicable):
+        ctx.qmatmul_cpu_path(t4, w4, xb, y1, rows, k, tokens)
+    with pytest.raises(eff.EffError):
+        ctx.qmatmul_cpu_path(t, wb, xb, y1, rows, 48, tokens)
+    for b in (wb, xb, y1, y2, w4):
+        b.free()
+
+
 def test_read_ticket_snapshots_at_begin(ctx, eff):
     """eff_read_begin enqueues the copy at once: a write enqueued after it is
     not in the snapshot; the buffer can be reused right away."""

@@ -14,9 +14,9 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-# (type, rows, k, tokens): the int8 matrix-core GEMV, the token-group GEMV, the
-# split-x product, the Q8_0 GEMM and the Q6_K row GEMV
-CASES = [("Q4_K", 300, 2048, 1), ("Q8_0", 520, 1024, 20), ("Q2_K", 256, 1024, 16),
+# (type, rows, k, tokens): the int8 matrix-core GEMV, the token-group GEMV (k
+# not a multiple of 256), the split-x product, the Q8_0 GEMM and the Q6_K row GEMV
+CASES = [("Q4_K", 300, 2048, 1), ("Q8_0", 520, 544, 20), ("Q2_K", 256, 1024, 16),
          ("Q8_0", 600, 544, 300), ("Q6_K", 32800, 512, 1)]
 
 
