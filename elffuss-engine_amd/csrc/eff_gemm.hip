@@ -30,6 +30,14 @@
 // The k order inside an MFMA is free as long as both operands follow it:
 // slot m (16 k) of a step takes, in lane half h, the 8 weights
 // 16 h + 8 (m & 1) .. + 7 of block m / 2 of the step.
+//
+// Q8_0R (QR): the repacked tensor keeps the quants and the scales in two
+// regions (kernels.bloques.wgsl.js:19-35), so a row's step is staged as its
+// 64 quant bytes (four 16-byte chunks from the quant region, 16-byte aligned)
+// and one chunk from the scale region holding its two scales: the same
+// 80-byte LDS row, with the quants aligned and the scales at byte 64. The
+// decoded weights, and so the outputs, are those of the Q8_0 tensor it was
+// repacked from.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -50,7 +58,7 @@ __device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const u
 
 // BM tokens x BN rows per tile. The 4 waves are WM along tokens x 4 / WM
 // along rows; NS stages (3..6), loads issued NS - 1 steps ahead.
-template <uint32_t BM, uint32_t BN, uint32_t WM, uint32_t NS>
+template <uint32_t BM, uint32_t BN, uint32_t WM, uint32_t NS, bool QR>
 __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Float16 *__restrict__ xh,
                                                  float *__restrict__ y, uint32_t tokens, uint32_t row_tiles,
                                                  uint32_t tok_tiles) {
@@ -101,9 +109,11 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
   const uint32_t steps_all = (k + kBK - 1u) / kBK;
   const uint32_t steps = steps_all, last = steps - 1u;
 
-  // Sources: x run of this token tile, weight rows from the tile's first row.
+  // Sources: x run of this token tile, weight rows from the tile's first row
+  // (QR: the whole tensor, addressed by absolute 32-bit offsets).
   const rsrc_t xsrc = make_rsrc(xh + (uint64_t)tt * steps_all * (BM * kBK), (uint64_t)steps_all * kXS);
-  const BufSrc src = make_src(wv, (uint64_t)n0 * wv.bpr);
+  const BufSrc src = make_src(wv, QR ? 0ull : (uint64_t)n0 * wv.bpr);
+  const rsrc_t wsrc = QR ? make_rsrc(wv.w, wv.w_bytes) : src.q;
   const uint32_t rb = (uint32_t)wv.row_bytes;
   const uint32_t rmax = rows - 1u - n0;  // last valid row of the tile (rows past it repeat it)
 
@@ -117,11 +127,20 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
   // W: load j of wave w is load g = w + kNW j of the step (those with
   // g < kWG); its chunk q = 64 g + lane is chunk q % 5 of row q / 5.
   const uint32_t nwl = wave < kWG % kNW || kWG % kNW == 0 ? kWDma : kWDma - 1u;
-  uint32_t wl[kWDma];
+  uint32_t wl[kWDma], ws_[kWDma];   // offset at step 0 and per step
 #pragma unroll
   for (uint32_t j = 0; j < kWDma; ++j) {
-    const uint32_t q = 64u * min(wave + kNW * j, kWG - 1u) + lane, r = q / 5u;
-    wl[j] = min(r, rmax) * rb + 16u * (q - 5u * r);
+    const uint32_t q = 64u * min(wave + kNW * j, kWG - 1u) + lane, r = q / 5u, c = q - 5u * r;
+    const uint32_t row = n0 + min(r, rmax);
+    if constexpr (QR) {
+      // chunks 0..3: quants 32 (row bpr + 2 s) + 16 c; chunk 4: scales at
+      // scales_off + 2 (row bpr + 2 s)
+      wl[j] = c < 4u ? 32u * row * wv.bpr + 16u * c : (uint32_t)wv.scales_off + 2u * row * wv.bpr;
+      ws_[j] = c < 4u ? 64u : 4u;
+    } else {
+      wl[j] = (row - n0) * rb + 16u * c;
+      ws_[j] = 68u;
+    }
   }
   // The loads of one step, in four groups (issued one per k slot, so that
   // the texture unit, shared by the CU's waves, is busy all step long).
@@ -134,7 +153,12 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
         dma16(xsrc, xs + 1024u * slot, ((i & 1u) ? xl1 : xl0) + 1024u * slot, s * kXS);
       } else {
         const uint32_t j = i - kXDma;
-        if (j < nwl) dma16(src.q, ws + 1024u * (wave + kNW * j), wl[j], s * 68u);
+        if (j < nwl) {
+          if constexpr (QR)
+            dma16(wsrc, ws + 1024u * (wave + kNW * j), wl[j] + s * ws_[j], 0u);
+          else
+            dma16(wsrc, ws + 1024u * (wave + kNW * j), wl[j], s * 68u);
+        }
       }
     }
   };
@@ -186,6 +210,11 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
 #pragma unroll
     for (int fj = 0; fj < (int)kFN; ++fj) {
       const uint8_t *rp = ws + brow + fj * (32u * kRB) + 32u * (uint32_t)u + 16u * h;
+      if constexpr (QR) {   // the lane's 16 quants, aligned
+        const u32x4 c = *(const u32x4 *)rp;
+        q[fj][0] = c.x; q[fj][1] = c.y; q[fj][2] = c.z; q[fj][3] = c.w;
+        continue;
+      }
       const u32x4 c0 = *(const u32x4 *)rp, c1 = *(const u32x4 *)(rp + 16);
       if (u == 0) {
         q[fj][0] = __builtin_amdgcn_alignbyte(c0.y, c0.x, 2);
@@ -217,7 +246,9 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
 #pragma unroll
     for (int fj = 0; fj < (int)kFN; ++fj) {
       const uint8_t *rp = ws + brow + fj * (32u * kRB);
-      const uint32_t w0 = lds_u32(rp), w1 = lds_u32(rp + 32);
+      // Q8_0: the scales at bytes 0 and 34 (read as the dwords at 0 and 32);
+      // Q8_0R: both in the dword at 64
+      const uint32_t w0 = lds_u32(rp + (QR ? 64u : 0u)), w1 = QR ? w0 : lds_u32(rp + 32);
       const _Float16 s0 = __builtin_bit_cast(_Float16, (uint16_t)(w0 & 0xFFFFu));
       const _Float16 s1 = full ? __builtin_bit_cast(_Float16, (uint16_t)(w1 >> 16)) : (_Float16)0.0f;
       d0[fj] = half2v{s0, s0};
@@ -337,8 +368,16 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
 template <uint32_t BM, uint32_t BN, uint32_t WM, uint32_t NS>
 hipError_t gemm_q8_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
   const uint32_t tok_tiles = (tokens + BM - 1) / BM, row_tiles = (wv.rows + BN - 1) / BN;
-  hipLaunchKernelGGL((k_gemm_q8<BM, BN, WM, NS>), dim3(row_tiles * tok_tiles), dim3(kNW * 64), 0, s, wv, xh, y, tokens,
-                     row_tiles, tok_tiles);
+  // Q8_0R is addressed from the tensor's first byte with 32-bit offsets: its
+  // quant and scale regions must end below 4 GiB (so does any tensor a buffer
+  // descriptor covers)
+  if (wv.type == Q8_0R && wv.scales_off + 2ull * wv.rows * wv.bpr + 16u >= (1ull << 32)) return hipErrorInvalidValue;
+  if (wv.type == Q8_0R)
+    hipLaunchKernelGGL((k_gemm_q8<BM, BN, WM, NS, true>), dim3(row_tiles * tok_tiles), dim3(kNW * 64), 0, s, wv, xh, y,
+                       tokens, row_tiles, tok_tiles);
+  else
+    hipLaunchKernelGGL((k_gemm_q8<BM, BN, WM, NS, false>), dim3(row_tiles * tok_tiles), dim3(kNW * 64), 0, s, wv, xh,
+                       y, tokens, row_tiles, tok_tiles);
   return hipGetLastError();
 }
 
@@ -361,7 +400,7 @@ uint32_t gemm_q8_choice(uint32_t plan, uint32_t cfg) {
 }  // namespace
 
 bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows) {
-  return type == Q8_0 && tokens >= 256 && k % 32u == 0;
+  return (type == Q8_0 || type == Q8_0R) && tokens >= 256 && k % 32u == 0;
 }
 
 uint32_t gemm_big_tile_log2(uint32_t tokens, uint32_t cfg) {

@@ -276,6 +276,36 @@ def test_gemm_q8_0_tile_configs_same_bits(ctx, eff, orc, tokens, k):
         b.free()
 
 
+@pytest.mark.parametrize("tokens,k", [(256, 2048), (300, 544), (777, 1024), (1100, 96), (2048, 512)])
+def test_gemm_q8_0r_same_bits_as_q8_0(ctx, eff, tokens, k):
+    """The prefill GEMM over a repacked tensor (Q8_0R: quants and scales in
+    two regions, staged into the same LDS rows) gives the bits of the Q8_0
+    tensor it was repacked from, in every tile configuration; k ends in half
+    a step (544: the second block of the last step is absent) or has fewer
+    steps than the pipeline has stages (96)."""
+    rows = 600
+    _, data, gguf, n = make_weights(eff, "Q8_0R", rows, k, 830 + tokens + k)
+    x = eff.fill_normal(831 + tokens, 1.0, tokens * k)
+    wq = ctx.upload(gguf)
+    wr = upload_w(ctx, eff, "Q8_0R", data, n)
+    xb, y0, y1 = ctx.upload(x), ctx.alloc(tokens * rows * 4), ctx.alloc(tokens * rows * 4)
+    before = ctx.stats()["gemm"]
+    ctx.qmatmul(eff.Q8_0, wq, xb, y0, rows, k, tokens)
+    ref = y0.read(np.uint32)
+    try:
+        for cfg in range(0, 7):
+            ctx.set_option(eff.OPT_GEMM_CONFIG, cfg)
+            y1.write(np.full(tokens * rows, 0x7FC00000, np.uint32))
+            ctx.qmatmul(eff.Q8_0R, wr, xb, y1, rows, k, tokens)
+            got = y1.read(np.uint32)
+            assert np.array_equal(got, ref), f"config {cfg}: {np.count_nonzero(got != ref)} outputs differ"
+    finally:
+        ctx.set_option(eff.OPT_GEMM_CONFIG, 0)
+    assert ctx.stats()["gemm"] == before + 8
+    for b in (wq, wr, xb, y0, y1):
+        b.free()
+
+
 # ---- fused decode GEMV (gemv.gateUp, gemv.secciones) -----------------------------------
 
 def silu64(v):
