@@ -467,6 +467,35 @@ template <> struct SxW<Q8_0> {
   __device__ half8 step_pre(const uint32_t (&)[1], int, uint32_t, const uint32_t *) const { return half8{}; }
 };
 
+// Q8_0R, the repacked layout (kernels.bloques.wgsl.js:19-35): the quants of
+// the row's 8 blocks (256 bytes, from the quant region) then their 8 scales
+// (16 bytes, from the scale region) form one staged row of 68 dwords; the
+// decoded weights, and so the outputs, are those of the Q8_0 tensor.
+template <> struct SxW<Q8_0R> {
+  static constexpr uint32_t BB = 0, DW = 68, ST = 69;   // BB: the regions advance by 256 and 16 per block
+  static constexpr bool MINS = false;
+  static constexpr int FG = 2;
+  static constexpr int NP = 0;
+  float d, dm, ds[8];
+  __device__ void block(const uint32_t *r, uint32_t) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t w = r[64 + (j >> 1)];
+      ds[j] = h2f((j & 1) ? (w >> 16) : (w & 0xFFFFu));
+    }
+    d = 1.f;
+    dm = 0.f;
+  }
+  __device__ float scale(int g) const { return ds[g]; }
+  __device__ half8 step(const uint32_t *r, int s, uint32_t h, const uint32_t *) const {
+    const uint32_t *p = r + 8u * (uint32_t)(s >> 1) + 4u * (uint32_t)(s & 1) + 2u * h;
+    return dec_signed(p[0], p[1]);
+  }
+  __device__ half8 mins(uint32_t) const { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
+  __device__ void preload(const uint32_t *, uint32_t, uint32_t (&)[1]) const {}
+  __device__ half8 step_pre(const uint32_t (&)[1], int, uint32_t, const uint32_t *) const { return half8{}; }
+};
+
 // Q6_K, 210 bytes: ql[128] | qh[64] | scales[16] (int8) | d
 // (kernels.wgsl.js:269-330). Step s = weights 16 s .. 16 s + 15 of the block:
 // n = s / 8, g = (s / 2) % 4, ql bytes 64 n + 32 (g % 2) + 16 (s % 2) + 8 h ..
@@ -583,13 +612,22 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
   }
 
   // staging: dword q = 64 i + lane of the stage is dword q % ST of row q / ST
-  // of the tile (the last dwords of a row and of the stage repeat valid ones)
+  // of the tile (the last dwords of a row and of the stage repeat valid ones);
+  // Q8_0R: dwords 0..63 from the quant region (256 bytes further per block),
+  // 64..67 from the scale region (16 bytes further per block)
   const rsrc_t wsrc = make_rsrc(wv.w, wv.w_bytes);
-  uint32_t soff[ND];
+  uint32_t soff[ND], sadv[ND];
 #pragma unroll
   for (uint32_t i = 0; i < ND; ++i) {
     const uint32_t q = 64u * i + lane, rr = q / W::ST, dw = min(q - rr * W::ST, W::DW - 1u);
-    soff[i] = min(r0 + min(rr, ROWS - 1u), rows - 1u) * rb + 4u * dw;
+    const uint32_t row = min(r0 + min(rr, ROWS - 1u), rows - 1u);
+    if constexpr (TYPE == Q8_0R) {
+      soff[i] = dw < 64u ? 32u * row * wv.bpr + 4u * dw : (uint32_t)wv.scales_off + 2u * row * wv.bpr + 4u * (dw - 64u);
+      sadv[i] = dw < 64u ? 256u : 16u;
+    } else {
+      soff[i] = row * rb + 4u * dw;
+      sadv[i] = 0u;
+    }
   }
   const rsrc_t xsrc = make_rsrc(xa, xa_bytes);
   // FX: this wave's raw x, fragments and scales
@@ -624,7 +662,9 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
     const uint32_t bo = bi * W::BB;
 #pragma unroll
     for (uint32_t i = 0; i < ND; ++i) {
-      if constexpr ((W::BB & 3u) == 0u)
+      if constexpr (TYPE == Q8_0R)
+        dma4(wsrc, stage + 256u * i, soff[i] + bi * sadv[i], 0u);
+      else if constexpr ((W::BB & 3u) == 0u)
         dma4(wsrc, stage + 256u * i, soff[i], bo);
       else  // staged from the 4-byte aligned floor of the block's first byte
         dma4(wsrc, stage + 256u * i, (soff[i] + bo) & ~3u, 0u);
@@ -797,9 +837,9 @@ struct SxPlan {
   uint32_t tt, cfg, groups, row_tiles, nbw;
 };
 
-// The types folded per group of steps (Q8_0, Q6_K) take at most 2 token tiles
-// per wave: with 4 their folds' state does not fit the registers.
-uint32_t sx_tt_max(int type) { return type == Q8_0 || type == Q6_K ? 2u : 4u; }
+// The types folded per group of steps (Q8_0, Q8_0R, Q6_K) take at most 2
+// token tiles per wave: with 4 their folds' state does not fit the registers.
+uint32_t sx_tt_max(int type) { return type == Q8_0 || type == Q8_0R || type == Q6_K ? 2u : 4u; }
 
 void sx_tiles(int type, uint32_t tokens, uint32_t &tt, uint32_t &groups) {
   const uint32_t ttn = (tokens + 15u) / 16u;
@@ -898,8 +938,11 @@ uint32_t sx_prepared_tiles(uint32_t tokens) { return (tokens + 63u) / 64u * 4u; 
 }  // namespace
 
 bool sx_applies(const WeightView &wv, uint32_t tokens) {
-  const bool t = wv.type == Q2_K || wv.type == Q4_K || wv.type == IQ2_XXS || wv.type == Q8_0 || wv.type == Q6_K;
-  return t && tokens >= 4u && wv.k % 256u == 0u;
+  const bool t = wv.type == Q2_K || wv.type == Q4_K || wv.type == IQ2_XXS || wv.type == Q8_0 || wv.type == Q8_0R ||
+                 wv.type == Q6_K;
+  // Q8_0R is staged with 32-bit offsets from the tensor's first byte
+  const bool r = wv.type != Q8_0R || wv.scales_off + 2ull * wv.rows * wv.bpr + 16u < (1ull << 32);
+  return t && r && tokens >= 4u && wv.k % 256u == 0u;
 }
 
 size_t sx_x_bytes(int type, uint32_t tokens, uint32_t k) {
@@ -961,6 +1004,7 @@ hipError_t launch_sx_prepared(const WeightView &wv, const void *xprep, float *y,
     case Q4_K: return sx_main<Q4_K>(wv, xa, tiles, y, tokens, p, s);
     case IQ2_XXS: return sx_main<IQ2_XXS>(wv, xa, tiles, y, tokens, p, s);
     case Q8_0: return sx_main<Q8_0>(wv, xa, tiles, y, tokens, p, s);
+    case Q8_0R: return sx_main<Q8_0R>(wv, xa, tiles, y, tokens, p, s);
     case Q6_K: return sx_main<Q6_K>(wv, xa, tiles, y, tokens, p, s);
     default: return hipErrorInvalidValue;
   }
@@ -974,6 +1018,7 @@ hipError_t launch_sx(const WeightView &wv, const float *x, float *y, uint32_t to
     case Q4_K: return sx_type<Q4_K>(wv, x, y, tokens, sc, cfg, s);
     case IQ2_XXS: return sx_type<IQ2_XXS>(wv, x, y, tokens, sc, cfg, s);
     case Q8_0: return sx_type<Q8_0>(wv, x, y, tokens, sc, cfg, s);
+    case Q8_0R: return sx_type<Q8_0R>(wv, x, y, tokens, sc, cfg, s);
     case Q6_K: return sx_type<Q6_K>(wv, x, y, tokens, sc, cfg, s);
     default: return hipErrorInvalidValue;
   }

@@ -88,7 +88,8 @@ typedef struct eff_stats {
   uint64_t dequant;     /* dequant launches */
   uint64_t topk;        /* top-k calls (records + selection; eff_topk, eff_topk_noalloc, eff_qgemv_topk) */
   uint64_t not_applicable;  /* calls answered EFF_NOT_APPLICABLE */
-  uint64_t split;       /* split-x matrix-core launches (Q2_K, Q4_K, IQ2_XXS, Q8_0, Q6_K from EFF_OPT_SPLIT_MIN_TOKENS) */
+  uint64_t split;       /* split-x matrix-core launches (Q2_K, Q4_K, IQ2_XXS, Q8_0, Q8_0R, Q6_K from
+                           EFF_OPT_SPLIT_MIN_TOKENS) */
   uint64_t fused;       /* fused GEMV launches (eff_qgemv_multi) */
   uint64_t gather;      /* gather launches (eff_gather, eff_gather_norm) */
   uint64_t gemm_x;      /* conversions of x to fp16 for the GEMM (one per eff_qgemm / eff_qgemm_planned /
@@ -289,10 +290,11 @@ int eff_fill_normal(uint32_t seed, float sigma, float *dst, size_t n);
  * Router of quant.matmul (ops.js:827-1101): tokens <= GEMV max -> GEMV;
  * Q8_0/Q8_0R at tokens >= GEMM min -> fp16 MFMA GEMM (the reference's
  * DRIFT/GEMM2 types, kernels.drift.wgsl.js:33); Q2_K, Q4_K, IQ2_XXS, Q6_K and
- * Q8_0 below GEMM min, from EFF_OPT_SPLIT_MIN_TOKENS (5 for Q2_K and IQ2_XXS, 9
- * for the others) -> split-x product (f32-accurate; fewer tokens run the int8
- * matrix-core GEMVs, as accurate); otherwise (Q8_0R below GEMM min, k not a
- * multiple of 256) -> GEMV over token groups, f32-accurate.
+ * Q8_0/Q8_0R below GEMM min, from EFF_OPT_SPLIT_MIN_TOKENS (5 for Q2_K and
+ * IQ2_XXS, 9 for the others) -> split-x product (f32-accurate; fewer tokens
+ * run the int8 matrix-core GEMVs, as accurate); otherwise (k not a multiple of
+ * 256) -> GEMV over token groups, f32-accurate. Q8_0R gives the bits of the
+ * Q8_0 tensor it was repacked from on every path.
  * EFF_E_SHAPE if k % block_elems != 0. */
 int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
                 uint32_t rows, uint32_t k, uint32_t tokens);

@@ -447,6 +447,35 @@ def test_split_x_per_block_scales_vs_f64_oracle(ctx, eff, orc, tname, tokens, k,
         b.free()
 
 
+@pytest.mark.parametrize("tokens,k", [(9, 2048), (17, 2304), (33, 2048), (63, 4096)])
+def test_split_x_q8_0r_same_bits_as_q8_0(ctx, eff, tokens, k):
+    """The split-x product over a repacked tensor (Q8_0R: each staged row is
+    its 256 quant bytes from the quant region and 8 scales from the scale
+    region) gives the bits of the Q8_0 tensor it was repacked from, through
+    the router (9 to 63 tokens) and from an x prepared for the Q8_0 product
+    (one layout for both)."""
+    rows = 130
+    _, data, gguf, n = make_weights(eff, "Q8_0R", rows, k, 860 + tokens + k)
+    x = eff.fill_normal(861 + tokens, 1.0, tokens * k)
+    wq, wr = ctx.upload(gguf), upload_w(ctx, eff, "Q8_0R", data, n)
+    xb, y0, y1 = ctx.upload(x), ctx.alloc(tokens * rows * 4), ctx.alloc(tokens * rows * 4)
+    before = ctx.stats()["split"]
+    ctx.qmatmul(eff.Q8_0, wq, xb, y0, rows, k, tokens)
+    ctx.qmatmul(eff.Q8_0R, wr, xb, y1, rows, k, tokens)
+    assert ctx.stats()["split"] == before + 2
+    ref = y0.read(np.uint32)
+    assert np.array_equal(y1.read(np.uint32), ref)
+    nb, lay = ctx.qmatmul_x_layout(eff.Q8_0R, rows, k, tokens)
+    assert lay == 0x100 and (nb, lay) == ctx.qmatmul_x_layout(eff.Q8_0, rows, k, tokens)
+    xp = ctx.alloc(nb)
+    ctx.qmatmul_prepare_x(eff.Q8_0, xb, xp, rows, k, tokens)
+    y1.write(np.full(tokens * rows, 0x7FC00000, np.uint32))
+    ctx.qmatmul_prepared(eff.Q8_0R, wr, xp, y1, rows, k, tokens)
+    assert np.array_equal(y1.read(np.uint32), ref)
+    for b in (wq, wr, xb, y0, y1, xp):
+        b.free()
+
+
 @pytest.mark.parametrize("tname", SPLIT_TYPES)
 @pytest.mark.parametrize("tokens", [4, 7, 16, 17, 33, 64, 100, 129])
 def test_split_x_vs_f64_oracle(ctx, eff, orc, tname, tokens, split_from_4):
@@ -750,7 +779,7 @@ def test_matmul_prepared_x_not_applicable_and_errors(ctx, eff):
     prepares x gives eff_qmatmul's bits; a short buffer is refused."""
     k = 2304
     for tname, r, kk, tokens in [("Q2_K", 64, k, 4), ("Q2_K", 64, k, 8), ("IQ2_XXS", 64, k, 5),
-                                 ("Q4_K", 64, k, 8), ("Q8_0R", 64, k, 33), ("Q8_0", 64, 2080, 33)]:
+                                 ("Q4_K", 64, k, 8), ("Q8_0R", 64, 2080, 33), ("Q8_0", 64, 2080, 33)]:
         with pytest.raises(eff.NotApplicable):
             ctx.qmatmul_x_layout(eff.TYPES[tname], r, kk, tokens)
     t, data, _, _ = make_weights(eff, "Q2_K", 77, k, 8300)
