@@ -230,9 +230,9 @@ bool router_gemm_type(int type) { return type == EFF_TYPE_Q8_0 || type == EFF_TY
 // us against 7.32 / 7.33 for Q2_K / IQ2_XXS); from 5 tokens split-x is as fast
 // or faster for those two types (5: 7.42 / 7.42 against 7.49 / 8.62; 7: 7.52 /
 // 7.56 against 7.75 / 8.90), for Q4_K from 9 (8: 8.66 against 7.90).
-// Q8_0 and Q6_K take it from 9 tokens, where the GEMV would run over token
-// groups; Q8_0 only below the fp16 GEMM's threshold (from there the
-// reference's DRIFT path, whose fp16 roundings the GEMM keeps).
+// Q8_0, Q8_0R and Q6_K take it from 9 tokens, where the GEMV would run over
+// token groups; Q8_0 and Q8_0R only below the fp16 GEMM's threshold (from
+// there the reference's DRIFT path, whose fp16 roundings the GEMM keeps).
 bool sx_routes(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens) {
   const int64_t lo = ctx->sx_min_tokens ? ctx->sx_min_tokens
                                         : (wv.type == Q2_K || wv.type == IQ2_XXS ? 5 : 9);
@@ -287,8 +287,8 @@ int grow(eff_ctx *ctx, void **p, size_t *have, size_t need, const char *what) {
   return EFF_OK;
 }
 
-// Split-x matrix-core product (Q2_K, Q4_K, IQ2_XXS, Q8_0, Q6_K from 4 tokens,
-// f32-accurate).
+// Split-x matrix-core product (Q2_K, Q4_K, IQ2_XXS, Q8_0, Q8_0R, Q6_K from 4
+// tokens, f32-accurate).
 int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
   int rc = grow(ctx, &ctx->sx_scratch, &ctx->sx_scratch_bytes, sx_x_bytes(wv.type, tokens, wv.k), "split-x");
   if (rc) return rc;
