@@ -518,6 +518,7 @@ def main():
         plan = [("C1", "Q8_0", 8192, 2048, 1, 0), ("C1", "Q8_0R", 8192, 2048, 1, 0),
                 ("C2", "Q4_K", 2048, 8192, 1, 0),
                 ("C3", "Q8_0", 8192, 2048, 512, 0), ("C3", "Q8_0", 8192, 2048, 2048, 0),
+                ("C3", "Q8_0R", 8192, 2048, 512, 0),
                 ("C4", "Q6_K", 65536, 2048, 1, 0), ("C4+top40", "Q6_K", 65536, 2048, 1, 40),
                 ("C4+top40 separate", "Q6_K", 65536, 2048, 1, -40)]
         for tn in ("Q2_K", "IQ2_XXS"):
