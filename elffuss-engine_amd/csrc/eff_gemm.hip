@@ -1,4 +1,4 @@
-// Prefill GEMM for Q8_0 weights from 256 tokens:
+// Prefill GEMM for Q8_0 (and Q8_0R) weights from 129 tokens:
 //   Y[t][row] = sum_k fp16(W[row][k]) fp16(X[t][k]), fp32 accumulation
 // (the operand roundings of kernels.drift.wgsl.js:65-142 and the f16 tiles of
 // ops.gemm2.js).
@@ -399,8 +399,12 @@ uint32_t gemm_q8_choice(uint32_t plan, uint32_t cfg) {
 
 }  // namespace
 
+// From 129 tokens: up to 128 the general kernel's one 128-token tile is as
+// fast or faster (C3 shape, us with the conversion, general / this kernel:
+// Q8_0 64 tokens 21.5 / 22.8, 128 22.0 / 22.5; Q8_0R 19.9 / 23.3, 20.5 / 23.0),
+// and from 129 it needs two (160 tokens 39.3 / 22.7, 255 40.1 / 23.7).
 bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows) {
-  return (type == Q8_0 || type == Q8_0R) && tokens >= 256 && k % 32u == 0;
+  return (type == Q8_0 || type == Q8_0R) && tokens > 128 && k % 32u == 0;
 }
 
 uint32_t gemm_big_tile_log2(uint32_t tokens, uint32_t cfg) {

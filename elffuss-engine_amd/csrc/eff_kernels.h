@@ -101,7 +101,7 @@ hipError_t launch_gemm_x(int type, const float *x, uint32_t tokens, uint32_t pla
                          uint32_t cfg, void *xh, hipStream_t stream);
 hipError_t launch_gemm_prepared(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
                                 uint32_t cfg, hipStream_t stream);
-// Q8_0 GEMM with direct-to-LDS staging (>= 256 tokens); x in the
+// Q8_0 / Q8_0R GEMM with direct-to-LDS staging (> 128 tokens); x in the
 // [token tile][k step][2^gemm_big_tile_log2 tokens][64] layout.
 bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows);
 uint32_t gemm_big_tile_log2(uint32_t tokens, uint32_t cfg);
