@@ -853,9 +853,14 @@ SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg) {
   // measured (C5 shapes): 32 rows x 8 waves up to 32 tokens per tile group;
   // 64 rows x 4 waves for 64 once the token groups give it 256 workgroups
   // (M = 96, 128), else 32 x 8 again (M = 48, 64: 13.9 / 14.1 us against
-  // 19.2 / 19.4 for Q2_K); the k halves in two workgroups were slower at every M
-  const uint32_t rt64 = (wv.rows + 63u) / 64u;
-  p.cfg = cfg ? (uint32_t)(cfg - 1) : (p.tt == 4u && p.groups * rt64 >= 256u ? 1u : 0u);
+  // 19.2 / 19.4 for Q2_K); the k halves in two workgroups were slower at every M.
+  // Between one and two rounds of 64-row workgroups (one per CU), 32 x 8 fills
+  // the second round better (M = 129 / 192: Q2_K 30.3 / 30.9 against 34.5 /
+  // 35.1, Q4_K 31.8 / 32.4 against 34.2 / 35.0, IQ2_XXS 30.0 / 30.4 against
+  // 31.6 / 32.4); from two rounds 64 x 4 again (M = 640: Q2_K 81.0 against
+  // 89.1; M = 320 and 448 within 3 % either way).
+  const uint32_t rt64 = (wv.rows + 63u) / 64u, w64 = p.groups * rt64;
+  p.cfg = cfg ? (uint32_t)(cfg - 1) : (p.tt == 4u && w64 >= 256u && !(w64 > 256u && w64 < 512u) ? 1u : 0u);
   const uint32_t rows_per = p.cfg ? 64u : 32u, nw = p.cfg ? 4u : 8u, ks = p.cfg == 2u ? 2u : 1u;
   p.row_tiles = (wv.rows + rows_per - 1u) / rows_per;
   p.nbw = ((wv.k / 256u + ks - 1u) / ks + nw - 1u) / nw;
