@@ -76,6 +76,9 @@ struct eff_ctx {
   size_t sx_scratch_bytes = 0;
   int64_t sx_config = 0;
   int64_t gemm_config = 0;
+  int64_t gemm_split = 0;           // Q8_0 GEMM k slices (0: automatic)
+  void *sk_scratch = nullptr;       // the GEMM's k-slice counters and sums
+  size_t sk_scratch_bytes = 0;
   int64_t sx_min_tokens = 0;        // 0: the measured default (sx_routes)
   void *act_scratch = nullptr;      // x in the CPU path's 8-bit blocks (eff_qmatmul_cpu_path)
   size_t act_scratch_bytes = 0;
@@ -335,12 +338,31 @@ int matmul_prepared_view(eff_ctx *ctx, int type, uint32_t rows, uint32_t k, uint
   return EFF_OK;
 }
 
+// The GEMM's k-slice scratch for a call (null where the call takes no k
+// slices). A new allocation gets its counters zeroed (outside of any graph
+// capture: grow allocates eagerly only); every launch leaves them zero.
+int sk_scratch(eff_ctx *ctx, const WeightView &wv, uint32_t tokens, uint32_t plan, void **out) {
+  *out = nullptr;
+  const size_t need = gemm_sk_bytes(wv.type, tokens, plan, wv.k, wv.rows, (uint32_t)ctx->gemm_config,
+                                    (uint32_t)ctx->gemm_split);
+  if (!need) return EFF_OK;
+  const size_t before = ctx->sk_scratch_bytes;
+  const int rc = grow(ctx, &ctx->sk_scratch, &ctx->sk_scratch_bytes, need, "gemm k-slice");
+  if (rc) return rc;
+  if (ctx->sk_scratch_bytes != before) EFF_HIP(ctx, hipMemsetAsync(ctx->sk_scratch, 0, ctx->sk_scratch_bytes, ctx->stream));
+  *out = ctx->sk_scratch;
+  return EFF_OK;
+}
+
 int run_gemm(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens, uint32_t plan) {
   const uint32_t cfg = (uint32_t)ctx->gemm_config;
   int rc = grow(ctx, &ctx->xh_scratch, &ctx->xh_scratch_bytes,
                 gemm_x_bytes(wv.type, tokens, plan, wv.k, wv.rows, cfg), "gemm x");
   if (rc) return rc;
-  hipError_t e = launch_gemm(wv, x, y, tokens, plan, cfg, ctx->xh_scratch, ctx->stream);
+  void *sk;
+  if ((rc = sk_scratch(ctx, wv, tokens, plan, &sk))) return rc;
+  hipError_t e = launch_gemm(wv, x, y, tokens, plan, cfg, (uint32_t)ctx->gemm_split, ctx->xh_scratch, sk,
+                             ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
   ++ctx->stats.gemm_x;
   return EFF_OK;
@@ -458,6 +480,7 @@ int eff_shutdown(eff_ctx *ctx) {
   if (ctx->xh_scratch) (void)hipFree(ctx->xh_scratch);
   if (ctx->sx_scratch) (void)hipFree(ctx->sx_scratch);
   if (ctx->act_scratch) (void)hipFree(ctx->act_scratch);
+  if (ctx->sk_scratch) (void)hipFree(ctx->sk_scratch);
   for (auto &p : ctx->stage_pend) (void)hipEventDestroy(p.ev);
   for (hipEvent_t ev : ctx->events) (void)hipEventDestroy(ev);
   if (ctx->stage) (void)hipHostFree(ctx->stage);
@@ -512,6 +535,10 @@ int eff_set_option(eff_ctx *ctx, int option, int64_t value) {
     case EFF_OPT_GEMM_CONFIG:
       if (value < 0 || value > 6) return fail(ctx, EFF_E_INVALID, "GEMM configuration must be 0..6, got %lld", (long long)value);
       ctx->gemm_config = value;
+      return EFF_OK;
+    case EFF_OPT_GEMM_SPLIT:
+      if (value < 0 || value > 64) return fail(ctx, EFF_E_INVALID, "GEMM k slices must be 0..64, got %lld", (long long)value);
+      ctx->gemm_split = value;
       return EFF_OK;
     default: return fail(ctx, EFF_E_INVALID, "unknown option %d", option);
   }
@@ -906,8 +933,10 @@ int eff_qgemm_prepared(eff_ctx *ctx, int type, eff_buf *w, eff_buf *xh, eff_buf 
       (rc = check_out(ctx, xh, gemm_x_bytes(type, tokens, plan_tokens, k, rows, cfg), "gemm prepared x")) ||
       (rc = use_device(ctx)))
     return rc;
+  void *sk;
+  if ((rc = sk_scratch(ctx, wv, tokens, plan_tokens, &sk))) return rc;
   const hipError_t e = launch_gemm_prepared(wv, (const _Float16 *)xh->ptr, (float *)y->ptr, tokens, plan_tokens, cfg,
-                                            ctx->stream);
+                                            (uint32_t)ctx->gemm_split, sk, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "gemm prepared launch");
   ++ctx->stats.gemm;
   return EFF_OK;
@@ -1026,8 +1055,10 @@ int eff_qmatmul_prepared(eff_ctx *ctx, int type, eff_buf *w, eff_buf *xp, eff_bu
     e = launch_sx_prepared(wv, xp->ptr, (float *)y->ptr, tokens, (int)ctx->sx_config, ctx->stream);
     ++ctx->stats.split;
   } else {
+    void *sk;
+    if ((rc = sk_scratch(ctx, wv, tokens, tokens, &sk))) return rc;
     e = launch_gemm_prepared(wv, (const _Float16 *)xp->ptr, (float *)y->ptr, tokens, tokens,
-                             (uint32_t)ctx->gemm_config, ctx->stream);
+                             (uint32_t)ctx->gemm_config, (uint32_t)ctx->gemm_split, sk, ctx->stream);
     ++ctx->stats.gemm;
   }
   if (e != hipSuccess) return hip_fail(ctx, e, "matmul prepared launch");

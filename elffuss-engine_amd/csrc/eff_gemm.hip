@@ -53,6 +53,8 @@ namespace {
 constexpr uint32_t kBK = 64;              // k per step
 constexpr uint32_t kRB = 80;              // raw weight bytes per row and stage
 constexpr uint32_t kNW = 4;               // waves per workgroup (one per SIMD)
+// k-slice scratch: a counter per tile (at most 2^16 tiles), then the sums
+constexpr uint32_t kCntBytes = 1u << 18;
 
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const uint32_t *)p; }
 
@@ -61,7 +63,8 @@ __device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const u
 template <uint32_t BM, uint32_t BN, uint32_t WM, uint32_t NS, bool QR>
 __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Float16 *__restrict__ xh,
                                                  float *__restrict__ y, uint32_t tokens, uint32_t row_tiles,
-                                                 uint32_t tok_tiles) {
+                                                 uint32_t tok_tiles, uint32_t ksl, uint32_t per,
+                                                 float *__restrict__ part, uint32_t *__restrict__ cnt) {
   constexpr uint32_t kWM = WM, kWN = kNW / WM;
   static_assert(kNW % WM == 0 && NS >= 3 && NS <= 6, "layout");
   constexpr uint32_t kWS = BN * kRB;                  // weight stage bytes
@@ -98,20 +101,24 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t wm = wave / kWN, wn = wave % kWN;
 
-  // Tiles are dealt so that the workgroups of one XCD (blockIdx % 8) take a
-  // contiguous run of tiles, token tiles fastest: they share x and W slices
-  // through that XCD's L2.
-  const uint32_t ntiles = row_tiles * tok_tiles;
-  uint32_t lin = blockIdx.x;
-  if (ntiles % 8u == 0u) lin = (blockIdx.x % 8u) * (ntiles / 8u) + blockIdx.x / 8u;
+  // Workgroups are dealt so that those of one XCD (blockIdx % 8) take a
+  // contiguous run of (k slice, tile) pairs, token tiles fastest and k slices
+  // slowest: they share x and W slices through that XCD's L2.
+  const uint32_t ntiles = row_tiles * tok_tiles, nwg = ntiles * ksl;
+  uint32_t u = blockIdx.x;
+  if (nwg % 8u == 0u) u = (blockIdx.x % 8u) * (nwg / 8u) + blockIdx.x / 8u;
+  const uint32_t z = u / ntiles, lin = u - z * ntiles;
   const uint32_t n0 = (lin / tok_tiles) * BN, tt = lin % tok_tiles, t0 = tt * BM;
   const uint32_t rows = wv.rows, k = wv.k;
+  // k slice z: steps s0 .. s0 + steps - 1 of 64 (every slice holds one at least)
   const uint32_t steps_all = (k + kBK - 1u) / kBK;
-  const uint32_t steps = steps_all, last = steps - 1u;
+  const uint32_t s0 = z * per, steps = min(per, steps_all - s0), last = steps - 1u;
 
-  // Sources: x run of this token tile, weight rows from the tile's first row
-  // (QR: the whole tensor, addressed by absolute 32-bit offsets).
-  const rsrc_t xsrc = make_rsrc(xh + (uint64_t)tt * steps_all * (BM * kBK), (uint64_t)steps_all * kXS);
+  // Sources: x run of this token tile from the slice's first step, weight
+  // rows from the tile's first row (QR: the whole tensor, addressed by
+  // absolute 32-bit offsets).
+  const rsrc_t xsrc =
+      make_rsrc(xh + ((uint64_t)tt * steps_all + s0) * (BM * kBK), (uint64_t)steps * kXS);
   const BufSrc src = make_src(wv, QR ? 0ull : (uint64_t)n0 * wv.bpr);
   const rsrc_t wsrc = QR ? make_rsrc(wv.w, wv.w_bytes) : src.q;
   const uint32_t rb = (uint32_t)wv.row_bytes;
@@ -135,11 +142,11 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
     if constexpr (QR) {
       // chunks 0..3: quants 32 (row bpr + 2 s) + 16 c; chunk 4: scales at
       // scales_off + 2 (row bpr + 2 s)
-      wl[j] = c < 4u ? 32u * row * wv.bpr + 16u * c : (uint32_t)wv.scales_off + 2u * row * wv.bpr;
       ws_[j] = c < 4u ? 64u : 4u;
+      wl[j] = (c < 4u ? 32u * row * wv.bpr + 16u * c : (uint32_t)wv.scales_off + 2u * row * wv.bpr) + s0 * ws_[j];
     } else {
-      wl[j] = (row - n0) * rb + 16u * c;
       ws_[j] = 68u;
+      wl[j] = (row - n0) * rb + 16u * c + s0 * 68u;
     }
   }
   // The loads of one step, in four groups (issued one per k slot, so that
@@ -272,8 +279,8 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
     }
   };
 
-  // the last step of k holds one block
-  const bool tail_half = (k % kBK) != 0u;
+  // the last step of k (in the last slice) holds one block
+  const bool tail_half = (k % kBK) != 0u && z + 1u == ksl;
   // Step s computes from stage s % NS; the operands of slot m + 1 are read
   // and decoded while the MFMAs of slot m run, and the loads of step
   // s + NS - 1 go to stage tgt (the one step s - 1 read) in four groups.
@@ -344,40 +351,114 @@ __global__ __launch_bounds__(kNW * 64) void k_gemm_q8(WeightView wv, const _Floa
 
   // D[tok][row]: lane holds row (column) n of each fragment and tokens
   // 8 (v / 4) + 4 h + v % 4. The lane number is read again here (an asm
-  // statement the compiler cannot merge with the first read), so that n and
-  // h are not held across the main loop: at 256 x 256 every register is in
-  // use there, and they would be spilled to scratch.
+  // statement the compiler cannot merge with the first read), so that n, h
+  // and the thread index are not held across the main loop: at 256 x 256
+  // every register is in use there, and they would be spilled to scratch.
   uint32_t lane_e;
   __asm__ volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
   const uint32_t ne = lane_e & 31u, he = lane_e >> 5;
-#pragma unroll
-  for (int fj = 0; fj < (int)kFN; ++fj) {
-    const uint32_t row = n0 + kFN * 32u * wn + 32u * fj + ne;
-    if (row >= rows) continue;
+  // outputs v = 4 q .. 4 q + 3 of fragment (fi, fj)
+  auto put = [&](int fi, int fj, int q, float4 v) {
+    const uint32_t row = n0 + kFN * 32u * wn + 32u * (uint32_t)fj + ne;
+    const uint32_t tok = t0 + kFM * 32u * wm + 32u * (uint32_t)fi + 8u * (uint32_t)q + 4u * he;
+    if (row >= rows) return;
+    if (tok < tokens) y[(uint64_t)tok * rows + row] = v.x;
+    if (tok + 1u < tokens) y[(uint64_t)(tok + 1u) * rows + row] = v.y;
+    if (tok + 2u < tokens) y[(uint64_t)(tok + 2u) * rows + row] = v.z;
+    if (tok + 3u < tokens) y[(uint64_t)(tok + 3u) * rows + row] = v.w;
+  };
+  auto mine = [&](int fi, int fj, int q) {
+    return make_float4(acc[fi][fj][4 * q], acc[fi][fj][4 * q + 1], acc[fi][fj][4 * q + 2], acc[fi][fj][4 * q + 3]);
+  };
+  // (256 x 256 tiles take no k slices: their sums would not fit the
+  // registers beside the accumulators)
+  if (BM * BN < 256u * 256u && ksl > 1u) {
+    // k slices: each workgroup of the tile stores its sums (in its register
+    // layout, 16 bytes per lane and store); the last of the tile's ksl
+    // workgroups to arrive adds the slices in slice order, ((s0 + s1) + s2)
+    // ..., which does not depend on the order of arrival, writes y, and
+    // resets the tile's counter to zero for the next launch. The sums are
+    // stored and loaded with the sc1 cache policy (as device-scope atomics
+    // are), which the XCDs' L2 caches do not hold stale, and each wave waits
+    // for its stores to complete before the barrier that precedes the
+    // counter's increment: no fence, whose L2 write-back and invalidation
+    // would take the cached x and W from the workgroups still running.
+    constexpr int kSc1 = 16;   // cache policy bit 4: sc1
+    const uint32_t tid_e = wave * 64u + lane_e;
+    const rsrc_t prs = make_rsrc(part + (uint64_t)lin * ksl * (BM * BN), (uint64_t)ksl * (BM * BN * 4u));
+    auto off = [&](uint32_t zz, int fi, int fj, int q) {
+      return (int)(zz * (BM * BN * 4u) + ((((uint32_t)fi * kFN + fj) * 4u + q) * (kNW * 64u) + tid_e) * 16u);
+    };
 #pragma unroll
     for (int fi = 0; fi < (int)kFM; ++fi)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const uint32_t tok = t0 + kFM * 32u * wm + 32u * fi + 8u * (v >> 2) + 4u * he + (v & 3);
-        if (tok < tokens) y[(uint64_t)tok * rows + row] = acc[fi][fj][v];
-      }
+      for (int fj = 0; fj < (int)kFN; ++fj)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x4 v = {__float_as_uint(acc[fi][fj][4 * q]), __float_as_uint(acc[fi][fj][4 * q + 1]),
+                           __float_as_uint(acc[fi][fj][4 * q + 2]), __float_as_uint(acc[fi][fj][4 * q + 3])};
+          __builtin_amdgcn_raw_buffer_store_b128(v, prs, off(z, fi, fj, q), 0, kSc1);
+        }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();   // every wave is past its loads and LDS reads: st0 is free
+    if (tid_e == 0u)
+      *(uint32_t *)st0 = __hip_atomic_fetch_add(cnt + lin, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (*(const uint32_t *)st0 != ksl - 1u) return;
+    if (tid_e == 0u) __hip_atomic_store(cnt + lin, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // a slice at a time (its own included, complete in memory), its loads
+    // in flight together, added onto the accumulators
+#pragma unroll
+    for (int fi = 0; fi < (int)kFM; ++fi)
+#pragma unroll
+      for (int fj = 0; fj < (int)kFN; ++fj)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(prs, off(0u, fi, fj, q), 0, kSc1);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc[fi][fj][4 * q + c] = __uint_as_float(v[c]);
+        }
+    for (uint32_t zz = 1; zz < ksl; ++zz) {
+#pragma unroll
+      for (int fi = 0; fi < (int)kFM; ++fi)
+#pragma unroll
+        for (int fj = 0; fj < (int)kFN; ++fj)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(prs, off(zz, fi, fj, q), 0, kSc1);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[fi][fj][4 * q + c] += __uint_as_float(v[c]);
+          }
+    }
   }
+#pragma unroll
+  for (int fi = 0; fi < (int)kFM; ++fi)
+#pragma unroll
+    for (int fj = 0; fj < (int)kFN; ++fj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) put(fi, fj, q, mine(fi, fj, q));
 }
 
 
 template <uint32_t BM, uint32_t BN, uint32_t WM, uint32_t NS>
-hipError_t gemm_q8_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, hipStream_t s) {
+hipError_t gemm_q8_go(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t ksl, uint32_t per,
+                      void *scratch, hipStream_t s) {
   const uint32_t tok_tiles = (tokens + BM - 1) / BM, row_tiles = (wv.rows + BN - 1) / BN;
   // Q8_0R is addressed from the tensor's first byte with 32-bit offsets: its
   // quant and scale regions must end below 4 GiB (so does any tensor a buffer
   // descriptor covers)
   if (wv.type == Q8_0R && wv.scales_off + 2ull * wv.rows * wv.bpr + 16u >= (1ull << 32)) return hipErrorInvalidValue;
+  if (ksl > 1u && (!scratch || (uint64_t)tok_tiles * row_tiles > kCntBytes / 4u)) return hipErrorInvalidValue;
+  // scratch: the tiles' arrival counters, then the slices' sums
+  uint32_t *cnt = (uint32_t *)scratch;
+  float *part = scratch ? (float *)((uint8_t *)scratch + kCntBytes) : nullptr;
+  const dim3 grid(row_tiles * tok_tiles * ksl);
   if (wv.type == Q8_0R)
-    hipLaunchKernelGGL((k_gemm_q8<BM, BN, WM, NS, true>), dim3(row_tiles * tok_tiles), dim3(kNW * 64), 0, s, wv, xh, y,
-                       tokens, row_tiles, tok_tiles);
+    hipLaunchKernelGGL((k_gemm_q8<BM, BN, WM, NS, true>), grid, dim3(kNW * 64), 0, s, wv, xh, y, tokens, row_tiles,
+                       tok_tiles, ksl, per, part, cnt);
   else
-    hipLaunchKernelGGL((k_gemm_q8<BM, BN, WM, NS, false>), dim3(row_tiles * tok_tiles), dim3(kNW * 64), 0, s, wv, xh,
-                       y, tokens, row_tiles, tok_tiles);
+    hipLaunchKernelGGL((k_gemm_q8<BM, BN, WM, NS, false>), grid, dim3(kNW * 64), 0, s, wv, xh, y, tokens, row_tiles,
+                       tok_tiles, ksl, per, part, cnt);
   return hipGetLastError();
 }
 
@@ -389,12 +470,47 @@ hipError_t gemm_q8_go(const WeightView &wv, const _Float16 *xh, float *y, uint32
 // stages); 128 x 128 with 3 stages (two workgroups per CU) below 1536
 // (M = 1024: 55.2 against 66.5 for 256 x 256); 256 x 256 from 1536 (M = 2048:
 // 83.9 against 98.9 for 256 x 128 and 106 for 128 x 128).
-uint32_t gemm_q8_choice(uint32_t plan, uint32_t cfg) {
-  if (cfg >= 1 && cfg <= 6) return cfg;
+uint32_t gemm_q8_choice(uint32_t plan) {
   if (plan < 384) return 4u;
   if (plan < 768) return 3u;
   if (plan < 1536) return 2u;
   return 1u;
+}
+
+uint32_t cfg_tiles(uint32_t c, uint32_t plan, uint32_t rows) {
+  const uint32_t bm = c == 1 || c == 6 ? 256u : c == 4 ? 64u : 128u, bn = c == 1 || c == 5 ? 256u : 128u;
+  return ((plan + bm - 1u) / bm) * ((rows + bn - 1u) / bn);
+}
+
+// Tiles and k slices. Few rows leave CUs without a tile (2048 rows, 512
+// tokens: 64 tiles of 128 x 128 on 256 CUs): 256 x 256 tiles give way to
+// 128 x 128 below 256 tiles (their slices' sums would not fit the registers
+// beside the accumulators: 2048 x 8192, 2048 tokens, us: 256 x 256 in 4
+// slices 290, 128 x 128 unsliced 111), and below 192 tiles k is cut into
+// slices of at least 8 steps, about 256 workgroups in all (2048 x 8192, us
+// against unsliced: 129 tokens 25.9 / 68.4, 256 29.1 / 68.1, 512 44.2 /
+// 85.5, 1024 66.0 / 95.5; 4096 x 4096, 512 tokens 41.9 / 49.5). The slices
+// follow the automatic tiles, also under a forced configuration, so that
+// every configuration sums each output in the same order.
+struct BigPlan {
+  uint32_t cfg, ksl, per;
+};
+
+BigPlan big_plan(uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg, uint32_t ksl_opt) {
+  uint32_t c = gemm_q8_choice(plan);
+  if (c == 1u && cfg_tiles(1u, plan, rows) < 256u) c = 2u;
+  const uint32_t steps = (k + kBK - 1u) / kBK, t = cfg_tiles(c, plan, rows);
+  const uint32_t ksl_auto = t < 192u ? min((256u + t / 2u) / t, max(steps / 8u, 1u)) : 1u;
+  BigPlan b;
+  b.cfg = cfg >= 1u && cfg <= 6u ? cfg : c;
+  // 256 x 256 tiles take no k slices: where the automatic choice slices k
+  // they run 128 x 128, and a forced slice count leaves them whole (the
+  // tiles, and so the x layout, do not depend on the forced count)
+  if (b.cfg == 1u && ksl_auto > 1u) b.cfg = 2u;
+  const uint32_t ksl = b.cfg == 1u ? 1u : max(1u, min(ksl_opt ? ksl_opt : ksl_auto, steps));
+  b.per = (steps + ksl - 1u) / ksl;
+  b.ksl = (steps + b.per - 1u) / b.per;
+  return b;
 }
 
 }  // namespace
@@ -407,23 +523,36 @@ bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows) {
   return (type == Q8_0 || type == Q8_0R) && tokens > 128 && k % 32u == 0;
 }
 
-uint32_t gemm_big_tile_log2(uint32_t tokens, uint32_t cfg) {
-  switch (gemm_q8_choice(tokens, cfg)) {
+uint32_t gemm_big_tile_log2(uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg) {
+  switch (big_plan(plan, k, rows, cfg, 0u).cfg) {
     case 1: case 6: return 8u;
     case 4: return 6u;
     default: return 7u;
   }
 }
 
+size_t gemm_big_scratch_bytes(uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg,
+                              uint32_t ksl_opt) {
+  const BigPlan b = big_plan(plan, k, rows, cfg, ksl_opt);
+  if (b.ksl < 2u) return 0;
+  const uint32_t bm = b.cfg == 1 || b.cfg == 6 ? 256u : b.cfg == 4 ? 64u : 128u;
+  const uint32_t bn = b.cfg == 1 || b.cfg == 5 ? 256u : 128u;
+  const uint64_t tiles = (uint64_t)((tokens + bm - 1u) / bm) * ((rows + bn - 1u) / bn);
+  return kCntBytes + (size_t)(tiles * b.ksl * bm * bn * 4u);
+}
+
+uint32_t gemm_big_cnt_bytes() { return kCntBytes; }
+
 hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
-                           uint32_t cfg, hipStream_t s) {
-  switch (gemm_q8_choice(plan, cfg)) {
-    case 1: return gemm_q8_go<256, 256, 1, 3>(wv, xh, y, tokens, s);
-    case 2: return gemm_q8_go<128, 128, 1, 3>(wv, xh, y, tokens, s);
-    case 3: return gemm_q8_go<128, 128, 1, 6>(wv, xh, y, tokens, s);
-    case 4: return gemm_q8_go<64, 128, 1, 4>(wv, xh, y, tokens, s);
-    case 5: return gemm_q8_go<128, 256, 1, 4>(wv, xh, y, tokens, s);
-    case 6: return gemm_q8_go<256, 128, 2, 3>(wv, xh, y, tokens, s);
+                           uint32_t cfg, uint32_t ksl_opt, void *scratch, hipStream_t s) {
+  const BigPlan b = big_plan(plan, wv.k, wv.rows, cfg, ksl_opt);
+  switch (b.cfg) {
+    case 1: return gemm_q8_go<256, 256, 1, 3>(wv, xh, y, tokens, b.ksl, b.per, scratch, s);
+    case 2: return gemm_q8_go<128, 128, 1, 3>(wv, xh, y, tokens, b.ksl, b.per, scratch, s);
+    case 3: return gemm_q8_go<128, 128, 1, 6>(wv, xh, y, tokens, b.ksl, b.per, scratch, s);
+    case 4: return gemm_q8_go<64, 128, 1, 4>(wv, xh, y, tokens, b.ksl, b.per, scratch, s);
+    case 5: return gemm_q8_go<128, 256, 1, 4>(wv, xh, y, tokens, b.ksl, b.per, scratch, s);
+    case 6: return gemm_q8_go<256, 128, 2, 3>(wv, xh, y, tokens, b.ksl, b.per, scratch, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -94,19 +94,28 @@ hipError_t launch_gemv_mt(const WeightView &wv, const float *x, float *y, uint32
 size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg);
 // An id of that layout: equal ids, one prepared x serves both products.
 uint32_t gemm_x_layout(int type, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg);
+// The k-slice scratch of the product (0 bytes: none): the Q8_0 GEMM cuts k
+// into slices over workgroups where the tiles alone leave CUs idle.
+// ksl_opt: forced slice count (EFF_OPT_GEMM_SPLIT; 0 automatic). The scratch
+// starts with counters that must be zero before the first launch; each
+// launch leaves them zero.
+size_t gemm_sk_bytes(int type, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg,
+                     uint32_t ksl_opt);
 hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint32_t plan,
-                       uint32_t cfg, void *xh_scratch, hipStream_t stream);
+                       uint32_t cfg, uint32_t ksl_opt, void *xh_scratch, void *sk_scratch, hipStream_t stream);
 // The two halves of launch_gemm: x into its fp16 layout, and the product from it.
 hipError_t launch_gemm_x(int type, const float *x, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows,
                          uint32_t cfg, void *xh, hipStream_t stream);
 hipError_t launch_gemm_prepared(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
-                                uint32_t cfg, hipStream_t stream);
+                                uint32_t cfg, uint32_t ksl_opt, void *sk_scratch, hipStream_t stream);
 // Q8_0 / Q8_0R GEMM with direct-to-LDS staging (> 128 tokens); x in the
 // [token tile][k step][2^gemm_big_tile_log2 tokens][64] layout.
 bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows);
-uint32_t gemm_big_tile_log2(uint32_t tokens, uint32_t cfg);
+uint32_t gemm_big_tile_log2(uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg);
+size_t gemm_big_scratch_bytes(uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg,
+                              uint32_t ksl_opt);
 hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
-                           uint32_t cfg, hipStream_t stream);
+                           uint32_t cfg, uint32_t ksl_opt, void *scratch, hipStream_t stream);
 
 // Split-x matrix-core product (eff_gemm_sx.hip): Q2_K, Q4_K, IQ2_XXS, Q8_0,
 // Q6_K from 4 tokens, k % 256 == 0, f32-accurate. `scratch` holds

@@ -1028,7 +1028,7 @@ static hipError_t gemm_go(const WeightView &wv, const _Float16 *xh, float *y, ui
 static void gemm_x_tile(int type, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg, uint32_t &bm_log2,
                         uint32_t &bk_log2) {
   if (gemm_big_applies(type, plan, k, rows)) {
-    bm_log2 = gemm_big_tile_log2(plan, cfg);
+    bm_log2 = gemm_big_tile_log2(plan, k, rows, cfg);
     bk_log2 = 6;
   } else if (gemm_wide(type, plan)) {
     bm_log2 = 8; bk_log2 = 6;
@@ -1062,17 +1062,23 @@ hipError_t launch_gemm_x(int type, const float *x, uint32_t tokens, uint32_t pla
   return hipGetLastError();
 }
 
+size_t gemm_sk_bytes(int type, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg,
+                     uint32_t ksl_opt) {
+  return gemm_big_applies(type, plan, k, rows) ? gemm_big_scratch_bytes(tokens, plan, k, rows, cfg, ksl_opt) : 0;
+}
+
 hipError_t launch_gemm(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint32_t plan,
-                       uint32_t cfg, void *xh_scratch, hipStream_t s) {
+                       uint32_t cfg, uint32_t ksl_opt, void *xh_scratch, void *sk_scratch, hipStream_t s) {
   const hipError_t e = launch_gemm_x(wv.type, x, tokens, plan, wv.k, wv.rows, cfg, xh_scratch, s);
   if (e != hipSuccess) return e;
-  return launch_gemm_prepared(wv, (const _Float16 *)xh_scratch, y, tokens, plan, cfg, s);
+  return launch_gemm_prepared(wv, (const _Float16 *)xh_scratch, y, tokens, plan, cfg, ksl_opt, sk_scratch, s);
 }
 
 hipError_t launch_gemm_prepared(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
-                                uint32_t cfg, hipStream_t s) {
+                                uint32_t cfg, uint32_t ksl_opt, void *sk_scratch, hipStream_t s) {
   if (plan < tokens) return hipErrorInvalidValue;
-  if (gemm_big_applies(wv.type, plan, wv.k, wv.rows)) return launch_gemm_big(wv, xh, y, tokens, plan, cfg, s);
+  if (gemm_big_applies(wv.type, plan, wv.k, wv.rows))
+    return launch_gemm_big(wv, xh, y, tokens, plan, cfg, ksl_opt, sk_scratch, s);
   switch (wv.type) {
     case Q8_0: return gemm_go<Q8_0>(wv, xh, y, tokens, plan, s);
     case Q8_0R: return gemm_go<Q8_0R>(wv, xh, y, tokens, plan, s);

@@ -62,6 +62,11 @@ extern "C" {
                                        rows, LDS stages): 0 automatic (default), 1: 256x256 1x4 3, 2: 128x128 1x4 3,
                                        3: 128x128 1x4 6, 4: 64x128 1x4 4, 5: 128x256 1x4 4, 6: 256x128 2x2 3; every
                                        configuration sums each output in the same order (the same bits) */
+#define EFF_OPT_GEMM_SPLIT       7  /* Q8_0 GEMM from 129 tokens, k slices over workgroups (tuning): 0 automatic
+                                       (default: where the tiles leave CUs idle, about 256 workgroups in all,
+                                       slices of 512 k at least), else that many (1: none; 256 x 256 tiles
+                                       take none); the slices' sums are added in slice order, so each count
+                                       gives fixed bits */
 
 /* ---- fused GEMV modes (gemv2Shader `modo`, kernels.gemv.wgsl.js:370-375) -- */
 #define EFF_GEMV_SECTIONS  1  /* 'secciones': ys[i] = W_i x for 2..4 matrices */

@@ -270,9 +270,83 @@ def test_gemm_q8_0_tile_configs_same_bits(ctx, eff, orc, tokens, k):
             assert np.array_equal(y, y0), f"config {cfg}: {np.count_nonzero(y != y0)} outputs differ"
         with pytest.raises(eff.EffError):
             ctx.set_option(eff.OPT_GEMM_CONFIG, 7)
+        # 256 x 256 tiles take no k slices: a forced count leaves the bits
+        ctx.set_option(eff.OPT_GEMM_CONFIG, 1)
+        ctx.set_option(eff.OPT_GEMM_SPLIT, 3)
+        yb.write(np.full(tokens * rows, 0x7FC00000, np.uint32))
+        ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+        assert np.array_equal(yb.read(np.uint32), y0)
     finally:
         ctx.set_option(eff.OPT_GEMM_CONFIG, 0)
+        ctx.set_option(eff.OPT_GEMM_SPLIT, 0)
     for b in (wb, xb, yb):
+        b.free()
+
+
+@pytest.mark.parametrize("tokens,k", [(300, 4096), (200, 4064), (1600, 2080)])
+def test_gemm_q8_0_k_slices(ctx, eff, orc, tokens, k):
+    """Few rows and a long k: the tiles leave CUs idle and k is cut into
+    slices over workgroups (25 tiles of 64 x 128 at 300 tokens: 8 slices;
+    4064 ends in half a step inside the last slice; at 1600 tokens 21 tiles
+    of 256 x 256 take 33 steps in slices of 9, the last shorter). The last workgroup of a tile adds the slices in slice order:
+    every tile configuration gives the automatic choice's bits, a second call
+    the same bits (the arrival counters start from zero again), and forced
+    slice counts (EFF_OPT_GEMM_SPLIT) stay within the fp16 oracle's bound."""
+    rows = 600
+    t, data, gguf, n = make_weights(eff, "Q8_0", rows, k, 860 + tokens)
+    x = eff.fill_normal(861 + tokens, 1.0, tokens * k)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    ref = orc.gemm_f16(orc.Q8_0, gguf, rows, k, x, tokens)
+    ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+    y0 = yb.read(np.uint32)
+    check_close(y0.view(np.float32), ref, f"gemm Q8_0 M={tokens} k={k}")
+    try:
+        for cfg in (0, 1, 2, 3, 4, 5, 6):
+            ctx.set_option(eff.OPT_GEMM_CONFIG, cfg)
+            yb.write(np.full(tokens * rows, 0x7FC00000, np.uint32))
+            ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+            y = yb.read(np.uint32)
+            assert np.array_equal(y, y0), f"config {cfg}: {np.count_nonzero(y != y0)} outputs differ"
+        ctx.set_option(eff.OPT_GEMM_CONFIG, 0)
+        for ks in (1, 2, 3, 64):
+            ctx.set_option(eff.OPT_GEMM_SPLIT, ks)
+            yb.write(np.full(tokens * rows, 0x7FC00000, np.uint32))
+            ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+            check_close(yb.read(np.float32), ref, f"gemm Q8_0 M={tokens} k={k} slices={ks}")
+        with pytest.raises(eff.EffError):
+            ctx.set_option(eff.OPT_GEMM_SPLIT, 65)
+    finally:
+        ctx.set_option(eff.OPT_GEMM_CONFIG, 0)
+        ctx.set_option(eff.OPT_GEMM_SPLIT, 0)
+    for b in (wb, xb, yb):
+        b.free()
+
+
+def test_gemm_q8_0_k_slices_graph_replays(ctx, eff, orc):
+    """A recorded k-sliced GEMM (the x conversion and the product) replayed
+    several times, with eager products of another shape between the replays
+    (which use the same counters): every replay gives the eager bits."""
+    rows, k, tokens = 520, 4096, 260
+    t, data, gguf, n = make_weights(eff, "Q8_0", rows, k, 870)
+    x = eff.fill_normal(871, 1.0, tokens * k)
+    wb, xb, yb, y2 = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4), ctx.alloc(tokens * rows * 4)
+    ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+    y0 = yb.read(np.uint32)
+    check_close(y0.view(np.float32), orc.gemm_f16(orc.Q8_0, gguf, rows, k, x, tokens), "gemm k slices")
+    ctx.graph_begin()
+    ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+    g = ctx.graph_end()
+    try:
+        for r in range(4):
+            yb.write(np.full(tokens * rows, 0x7FC00000, np.uint32))
+            g.launch()
+            ctx.sync()
+            y = yb.read(np.uint32)
+            assert np.array_equal(y, y0), f"replay {r}: {np.count_nonzero(y != y0)} outputs differ"
+            ctx.qgemm(t, wb, xb, y2, rows // 2, k, 200)   # another tile count on the same counters
+    finally:
+        g.destroy()
+    for b in (wb, xb, yb, y2):
         b.free()
 
 
