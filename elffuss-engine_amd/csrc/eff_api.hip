@@ -77,7 +77,8 @@ struct eff_ctx {
   int64_t sx_config = 0;
   int64_t gemm_config = 0;
   int64_t gemm_split = 0;           // Q8_0 GEMM k slices (0: automatic)
-  void *sk_scratch = nullptr;       // the GEMM's k-slice counters and sums
+  int64_t sx_split = 0;             // split-x k slices (0: automatic)
+  void *sk_scratch = nullptr;       // k-slice counters and sums (GEMM and split-x)
   size_t sk_scratch_bytes = 0;
   int64_t sx_min_tokens = 0;        // 0: the measured default (sx_routes)
   void *act_scratch = nullptr;      // x in the CPU path's 8-bit blocks (eff_qmatmul_cpu_path)
@@ -228,21 +229,6 @@ int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_
 // reference's fp16 GEMMs accept (GEMM2_TIPOS, kernels.gemm2.wgsl.js:51).
 bool router_gemm_type(int type) { return type == EFF_TYPE_Q8_0 || type == EFF_TYPE_Q8_0R; }
 
-// The split-x product from 5 tokens (Q4_K: 9); below, the int8 matrix-core
-// GEMVs, which are as accurate and faster at 4 tokens (C5 shapes: 5.75 / 6.72
-// us against 7.32 / 7.33 for Q2_K / IQ2_XXS); from 5 tokens split-x is as fast
-// or faster for those two types (5: 7.42 / 7.42 against 7.49 / 8.62; 7: 7.52 /
-// 7.56 against 7.75 / 8.90), for Q4_K from 9 (8: 8.66 against 7.90).
-// Q8_0, Q8_0R and Q6_K take it from 9 tokens, where the GEMV would run over
-// token groups; Q8_0 and Q8_0R only below the fp16 GEMM's threshold (from
-// there the reference's DRIFT path, whose fp16 roundings the GEMM keeps).
-bool sx_routes(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens) {
-  const int64_t lo = ctx->sx_min_tokens ? ctx->sx_min_tokens
-                                        : (wv.type == Q2_K || wv.type == IQ2_XXS ? 5 : 9);
-  if (router_gemm_type(wv.type) && (int64_t)tokens >= ctx->gemm_min_tokens) return false;
-  return ctx->gemv_kernel == 0 && sx_applies(wv, tokens) && (int64_t)tokens >= lo;
-}
-
 // The 16-row GEMV computes tokens in groups of 4: at 5 and 6 tokens it pays
 // for 8, and the 4-row GEMV (which scales with the token count) is faster
 // (µs, 5 / 6 tokens, 16-row against 4-row: Q8_0 8192 x 2048 9.00 / 9.24
@@ -251,6 +237,30 @@ bool sx_routes(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens) {
 // 12.17 against 11.10 / 12.07); at 4, 7 and 8 tokens the 16-row GEMV is as
 // fast or faster.
 bool mt_routes(uint32_t tokens) { return tokens != 5u && tokens != 6u; }
+
+// The split-x product from 5 tokens (Q4_K: 9); below, the int8 matrix-core
+// GEMVs, which are as accurate and faster at 4 tokens (C5 shapes: 5.75 / 6.72
+// us against 7.32 / 7.33 for Q2_K / IQ2_XXS); from 5 tokens split-x is as fast
+// or faster for those two types (5: 7.42 / 7.42 against 7.49 / 8.62; 7: 7.52 /
+// 7.56 against 7.75 / 8.90), for Q4_K from 9 (8: 8.66 against 7.90).
+// Q8_0, Q8_0R and Q6_K take it from 9 tokens, where the GEMV would run over
+// token groups; Q8_0 and Q8_0R only below the fp16 GEMM's threshold (from
+// there the reference's DRIFT path, whose fp16 roundings the GEMM keeps).
+// Below that, from 4 tokens, also where no int8 matrix-core GEMV fits its x
+// digits into LDS at this k (about 43 K token x k values: 4096 x 14336 from 3
+// tokens, 2048 x 8192 from 6), which would leave the f32 vector GEMV a pass
+// over the weights per token group (Q8_0 4096 x 14336, 8 tokens: 102.9 us).
+bool sx_routes(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens) {
+  const int64_t lo = ctx->sx_min_tokens ? ctx->sx_min_tokens
+                                        : (wv.type == Q2_K || wv.type == IQ2_XXS ? 5 : 9);
+  if (router_gemm_type(wv.type) && (int64_t)tokens >= ctx->gemm_min_tokens) return false;
+  if (ctx->gemv_kernel != 0 || !sx_applies(wv, tokens)) return false;
+  if ((int64_t)tokens >= lo) return true;
+  GemvPlan p;
+  return !gemv_rows_applies(wv, tokens) && !(mt_routes(tokens) && gemv_mt_plan(wv, tokens, p)) &&
+         !gemv_mx_plan(wv, tokens, p);
+}
+
 
 int run_gemv(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
   if (sx_routes(ctx, wv, tokens)) return run_sx(ctx, wv, x, y, tokens);
@@ -290,15 +300,38 @@ int grow(eff_ctx *ctx, void **p, size_t *have, size_t need, const char *what) {
   return EFF_OK;
 }
 
+// The k-slice scratch of a call, `need` bytes (null where the call takes no
+// k slices). A new allocation gets its counters zeroed (outside of any graph
+// capture: grow allocates eagerly only); every launch leaves them zero.
+int sk_get(eff_ctx *ctx, size_t need, void **out) {
+  *out = nullptr;
+  if (!need) return EFF_OK;
+  const size_t before = ctx->sk_scratch_bytes;
+  const int rc = grow(ctx, &ctx->sk_scratch, &ctx->sk_scratch_bytes, need, "gemm k-slice");
+  if (rc) return rc;
+  if (ctx->sk_scratch_bytes != before) EFF_HIP(ctx, hipMemsetAsync(ctx->sk_scratch, 0, ctx->sk_scratch_bytes, ctx->stream));
+  *out = ctx->sk_scratch;
+  return EFF_OK;
+}
+
+// The GEMM's k-slice scratch.
+int sk_scratch(eff_ctx *ctx, const WeightView &wv, uint32_t tokens, uint32_t plan, void **out) {
+  return sk_get(ctx, gemm_sk_bytes(wv.type, tokens, plan, wv.k, wv.rows, (uint32_t)ctx->gemm_config,
+                                   (uint32_t)ctx->gemm_split), out);
+}
+
 // Split-x matrix-core product (Q2_K, Q4_K, IQ2_XXS, Q8_0, Q8_0R, Q6_K from 4
 // tokens, f32-accurate).
 int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
   int rc = grow(ctx, &ctx->sx_scratch, &ctx->sx_scratch_bytes, sx_x_bytes(wv.type, tokens, wv.k), "split-x");
   if (rc) return rc;
-  hipError_t e = launch_sx(wv, x, y, tokens, ctx->sx_scratch, (int)ctx->sx_config, ctx->stream);
+  const uint32_t ks = (uint32_t)ctx->sx_split;
+  void *sk;
+  if ((rc = sk_get(ctx, sx_sk_bytes(wv, tokens, (int)ctx->sx_config, ks), &sk))) return rc;
+  hipError_t e = launch_sx(wv, x, y, tokens, ctx->sx_scratch, (int)ctx->sx_config, ks, sk, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "split-x launch");
   ++ctx->stats.split;
-  if (sx_x_layout(wv, tokens, (int)ctx->sx_config)) ++ctx->stats.split_x;
+  if (sx_x_layout(wv, tokens, (int)ctx->sx_config, ks)) ++ctx->stats.split_x;
   return EFF_OK;
 }
 
@@ -308,7 +341,7 @@ int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_
 uint32_t route_layout(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens, size_t *bytes) {
   *bytes = 0;
   if (sx_routes(ctx, wv, tokens)) {
-    const uint32_t l = sx_x_layout(wv, tokens, (int)ctx->sx_config);
+    const uint32_t l = sx_x_layout(wv, tokens, (int)ctx->sx_config, (uint32_t)ctx->sx_split);
     if (l) *bytes = sx_prepared_bytes(l, tokens, wv.k);
     return l;
   }
@@ -335,22 +368,6 @@ int matmul_prepared_view(eff_ctx *ctx, int type, uint32_t rows, uint32_t k, uint
   wv.rows = rows;
   wv.k = k;
   wv.bpr = k / g.elems;
-  return EFF_OK;
-}
-
-// The GEMM's k-slice scratch for a call (null where the call takes no k
-// slices). A new allocation gets its counters zeroed (outside of any graph
-// capture: grow allocates eagerly only); every launch leaves them zero.
-int sk_scratch(eff_ctx *ctx, const WeightView &wv, uint32_t tokens, uint32_t plan, void **out) {
-  *out = nullptr;
-  const size_t need = gemm_sk_bytes(wv.type, tokens, plan, wv.k, wv.rows, (uint32_t)ctx->gemm_config,
-                                    (uint32_t)ctx->gemm_split);
-  if (!need) return EFF_OK;
-  const size_t before = ctx->sk_scratch_bytes;
-  const int rc = grow(ctx, &ctx->sk_scratch, &ctx->sk_scratch_bytes, need, "gemm k-slice");
-  if (rc) return rc;
-  if (ctx->sk_scratch_bytes != before) EFF_HIP(ctx, hipMemsetAsync(ctx->sk_scratch, 0, ctx->sk_scratch_bytes, ctx->stream));
-  *out = ctx->sk_scratch;
   return EFF_OK;
 }
 
@@ -539,6 +556,11 @@ int eff_set_option(eff_ctx *ctx, int option, int64_t value) {
     case EFF_OPT_GEMM_SPLIT:
       if (value < 0 || value > 64) return fail(ctx, EFF_E_INVALID, "GEMM k slices must be 0..64, got %lld", (long long)value);
       ctx->gemm_split = value;
+      return EFF_OK;
+    case EFF_OPT_SPLIT_SLICES:
+      if (value < 0 || value > 64)
+        return fail(ctx, EFF_E_INVALID, "split-x k slices must be 0..64, got %lld", (long long)value);
+      ctx->sx_split = value;
       return EFF_OK;
     default: return fail(ctx, EFF_E_INVALID, "unknown option %d", option);
   }
@@ -1052,7 +1074,10 @@ int eff_qmatmul_prepared(eff_ctx *ctx, int type, eff_buf *w, eff_buf *xp, eff_bu
     return rc;
   hipError_t e;
   if (l & kSxLayout) {
-    e = launch_sx_prepared(wv, xp->ptr, (float *)y->ptr, tokens, (int)ctx->sx_config, ctx->stream);
+    void *sk;
+    if ((rc = sk_get(ctx, sx_sk_bytes(wv, tokens, (int)ctx->sx_config, (uint32_t)ctx->sx_split), &sk))) return rc;
+    e = launch_sx_prepared(wv, xp->ptr, (float *)y->ptr, tokens, (int)ctx->sx_config, (uint32_t)ctx->sx_split, sk,
+                           ctx->stream);
     ++ctx->stats.split;
   } else {
     void *sk;

@@ -1,4 +1,5 @@
-// Prefill GEMM for Q8_0 (and Q8_0R) weights from 129 tokens:
+// Prefill GEMM for Q8_0 (and Q8_0R) weights from 129 tokens (from 64 below
+// 6144 rows):
 //   Y[t][row] = sum_k fp16(W[row][k]) fp16(X[t][k]), fp32 accumulation
 // (the operand roundings of kernels.drift.wgsl.js:65-142 and the f16 tiles of
 // ops.gemm2.js).
@@ -53,8 +54,7 @@ namespace {
 constexpr uint32_t kBK = 64;              // k per step
 constexpr uint32_t kRB = 80;              // raw weight bytes per row and stage
 constexpr uint32_t kNW = 4;               // waves per workgroup (one per SIMD)
-// k-slice scratch: a counter per tile (at most 2^16 tiles), then the sums
-constexpr uint32_t kCntBytes = 1u << 18;
+constexpr uint32_t kCntBytes = kSliceCntBytes;   // the k-slice counters
 
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const uint32_t *)p; }
 
@@ -518,9 +518,14 @@ BigPlan big_plan(uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg, uint32_
 // From 129 tokens: up to 128 the general kernel's one 128-token tile is as
 // fast or faster (C3 shape, us with the conversion, general / this kernel:
 // Q8_0 64 tokens 21.5 / 22.8, 128 22.0 / 22.5; Q8_0R 19.9 / 23.3, 20.5 / 23.0),
-// and from 129 it needs two (160 tokens 39.3 / 22.7, 255 40.1 / 23.7).
+// and from 129 it needs two (160 tokens 39.3 / 22.7, 255 40.1 / 23.7). Below
+// 6144 rows the general kernel's 32-row tiles are fewer than 192 workgroups,
+// and this kernel's k slices fill the CUs from 64 tokens (us, 64 / 128 tokens,
+// general against this kernel: 2048 x 8192 54.3 / 54.8 against 22.5 / 22.3,
+// 4096 x 14336 86.0 / 86.6 against 31.0 / 42.4, 4096 x 4096 32.6 / 33.0
+// against 18.7 / 20.8, 2048 x 2048 21.1 / 21.4 against 14.0 / 15.3).
 bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows) {
-  return (type == Q8_0 || type == Q8_0R) && tokens > 128 && k % 32u == 0;
+  return (type == Q8_0 || type == Q8_0R) && (tokens > 128 || (rows + 31u) / 32u < 192u) && k % 32u == 0;
 }
 
 uint32_t gemm_big_tile_log2(uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg) {
@@ -540,8 +545,6 @@ size_t gemm_big_scratch_bytes(uint32_t tokens, uint32_t plan, uint32_t k, uint32
   const uint64_t tiles = (uint64_t)((tokens + bm - 1u) / bm) * ((rows + bn - 1u) / bn);
   return kCntBytes + (size_t)(tiles * b.ksl * bm * bn * 4u);
 }
-
-uint32_t gemm_big_cnt_bytes() { return kCntBytes; }
 
 hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
                            uint32_t cfg, uint32_t ksl_opt, void *scratch, hipStream_t s) {

@@ -77,18 +77,11 @@ constexpr uint32_t sx_slots() {  // x slots of 1 KB per (token tile, block): 16 
 // lane L's 16 bytes at 16 L, L = 32 half + 16 part + token % 16.
 // xp[(tt nb + b) 16 + token % 16] = 2^(e - 14) (NaN for a block holding a
 // non-finite x, which makes every output of that token non-finite).
-// With yz > 0 the kernel also zeroes y[0 .. yz) (the main kernel then adds
-// its two k halves into y).
 template <int TYPE>
 __global__ __launch_bounds__(256) void k_sx_prep(const float *__restrict__ x, uint32_t tokens, uint32_t k,
-                                                 uint8_t *__restrict__ xa, float *__restrict__ xp,
-                                                 float *__restrict__ y, uint32_t yz) {
+                                                 uint8_t *__restrict__ xa, float *__restrict__ xp) {
   constexpr uint32_t NS = sx_slots<TYPE>();
   const uint32_t lane = threadIdx.x & 63u, bi = blockIdx.x, nb = k / 256u;
-  {
-    const uint32_t n = gridDim.x * gridDim.y * 256u;
-    for (uint32_t i = (blockIdx.y * gridDim.x + blockIdx.x) * 256u + threadIdx.x; i < yz; i += n) y[i] = 0.f;
-  }
   const uint32_t t = blockIdx.y * 4u + (threadIdx.x >> 6);
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
   if (t < tokens) v = *(const float4 *)(x + (uint64_t)t * k + 256u * bi + 4u * lane);
@@ -566,14 +559,15 @@ constexpr uint32_t sx_fx_bytes() {
   return 8u * 1024u + sx_slots<TYPE>() * kSxFxSlot + 64u;
 }
 
-template <int TYPE, int TT, int RF, int NW, int KS, bool FX>
+template <int TYPE, int TT, int RF, int NW, bool FX>
 __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__restrict__ xa,
                                                 const float *__restrict__ xp, float *__restrict__ y,
                                                 uint32_t tokens, uint32_t nbw, uint32_t xa_bytes,
-                                                const float *__restrict__ xf) {
+                                                const float *__restrict__ xf, uint32_t ksl,
+                                                float *__restrict__ part, uint32_t *__restrict__ cnt) {
   using W = SxW<TYPE>;
   using L = SxLds<TYPE, TT, RF, NW>;
-  static_assert(!FX || (TT == 1 && KS == 1), "the fused preparation covers one token tile");
+  static_assert(!FX || TT == 1, "the fused preparation covers one token tile");
   constexpr uint32_t NS = sx_slots<TYPE>();
   // steps of x fragments loaded ahead (Q4_K's 37-dword rows take 19 staging
   // offsets per lane: 3 steps ahead at 4 token tiles keep it within the VGPRs;
@@ -586,10 +580,11 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
   uint8_t *const lds = FX ? lds_d : lds_s;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, j = lane & 31u, h = lane >> 5;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // KS = 2: workgroup pairs take the two halves of k and add into y
-  const uint32_t kh = blockIdx.x % (uint32_t)KS;
+  // k slices: the ksl workgroups of a row tile (adjacent in x) take slices
+  // of k, summed by the last of them to finish (ksl = 1: one workgroup)
+  const uint32_t kh = blockIdx.x % ksl, rt = blockIdx.x / ksl;
   // nb: blocks of 256 weights per row (Q8_0 rows hold 8 of its 32-weight blocks in each)
-  const uint32_t rows = wv.rows, nb = wv.k / 256u, r0 = blockIdx.x / (uint32_t)KS * ROWS, tg = blockIdx.y;
+  const uint32_t rows = wv.rows, nb = wv.k / 256u, r0 = rt * ROWS, tg = blockIdx.y;
   const uint32_t rb = (uint32_t)wv.row_bytes;
   uint32_t *tab = (uint32_t *)lds;
   uint8_t *stage = lds + L::TAB + wave * L::SB;
@@ -652,7 +647,7 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
 #pragma unroll
       for (int v = 0; v < 8; ++v) acc[tt][f][v] = 0.f;
 
-  const uint32_t bl = kh * nb / (uint32_t)KS, bh = (kh + 1u) * nb / (uint32_t)KS;
+  const uint32_t bl = kh * nb / ksl, bh = (kh + 1u) * nb / ksl;
   const uint32_t b0 = bl + wave * nbw, b1 = min(b0 + nbw, bh);
   for (uint32_t bi = b0; bi < b1; ++bi) {
     // FX: the block's x, token by token, ahead of its weights
@@ -814,27 +809,63 @@ __global__ __launch_bounds__(NW * 64) void k_sx(WeightView wv, const uint8_t *__
 #pragma unroll
       for (int v = 0; v < 8; ++v) red[wave * L::NE + ((tt * RF + f) * 8u + v) * 64u + lane] = acc[tt][f][v];
   __syncthreads();
-  for (uint32_t e = tid; e < L::NE; e += NW * 64u) {
-    float sum = 0.f;
+  constexpr uint32_t NT = NW * 64u, PE = L::NE / NT;   // sums per thread
+  static_assert(L::NE % NT == 0u, "sums per thread");
+  float sum[PE];
 #pragma unroll
-    for (uint32_t w = 0; w < (uint32_t)NW; ++w) sum += red[w * L::NE + e];
+  for (uint32_t i = 0; i < PE; ++i) {
+    sum[i] = 0.f;
+#pragma unroll
+    for (uint32_t w = 0; w < (uint32_t)NW; ++w) sum[i] += red[w * L::NE + tid + NT * i];
+  }
+  if (!FX && ksl > 1u) {
+    // k slices: each workgroup of the tile stores its sums; the last of the
+    // tile's ksl workgroups to arrive adds the slices in slice order, ((s0 +
+    // s1) + s2) ..., which does not depend on the order of arrival, and
+    // resets the tile's counter to zero for the next launch. The sums are
+    // stored and loaded with the sc1 cache policy (as device-scope atomics
+    // are), which the XCDs' L2 caches do not hold stale, and each wave waits
+    // for its stores to complete before the barrier ahead of the counter's
+    // increment (a fence would write back and invalidate the whole L2).
+    constexpr int kSc1 = 16;   // cache policy bit 4: sc1
+    __shared__ uint32_t arrived;
+    const uint32_t lin = tg * (gridDim.x / ksl) + rt;
+    const rsrc_t prs = make_rsrc(part + (uint64_t)lin * ksl * L::NE, (uint64_t)ksl * L::NE * 4u);
+#pragma unroll
+    for (uint32_t i = 0; i < PE; ++i)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sum[i]), prs, (int)((kh * L::NE + tid + NT * i) * 4u), 0,
+                                            kSc1);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0u) arrived = __hip_atomic_fetch_add(cnt + lin, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrived != ksl - 1u) return;
+    if (tid == 0u) __hip_atomic_store(cnt + lin, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (uint32_t i = 0; i < PE; ++i)
+      sum[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, (int)((tid + NT * i) * 4u), 0, kSc1));
+    for (uint32_t zz = 1; zz < ksl; ++zz) {
+#pragma unroll
+      for (uint32_t i = 0; i < PE; ++i)
+        sum[i] += __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(prs, (int)((zz * L::NE + tid + NT * i) * 4u), 0, kSc1));
+    }
+  }
+#pragma unroll
+  for (uint32_t i = 0; i < PE; ++i) {
+    const uint32_t e = tid + NT * i;
     const uint32_t le = e & 63u, v = (e >> 6) & 7u, fr = e >> 9, f = fr % RF, tt = fr / RF;
     const uint32_t row = r0 + 32u * f + (le & 31u);
     const uint32_t tok = (tg * TT + tt) * 16u + 8u * (v >> 2) + 4u * (le >> 5) + (v & 3u);
-    if (row < rows && tok < tokens) {
-      if constexpr (KS == 1)
-        y[(uint64_t)tok * rows + row] = sum;
-      else  // 0 + a + b: the same bits in either order
-        unsafeAtomicAdd(y + (uint64_t)tok * rows + row, sum);
-    }
+    if (row < rows && tok < tokens) y[(uint64_t)tok * rows + row] = sum[i];
   }
 }
 
 // Token tiles of 16 per wave (tt) and token groups (grid y); the x scratch
 // covers groups * tt tiles (tokens past `tokens` are zero).
 struct SxPlan {
-  // cfg 0: 32 rows x 8 waves; 1: 64 rows x 4 waves; 2: 64 rows x 4 waves, k halves in two workgroups
-  uint32_t tt, cfg, groups, row_tiles, nbw;
+  // cfg 0: 32 rows x 8 waves; 1: 64 rows x 4 waves; ksl: k slices per row tile
+  uint32_t tt, cfg, groups, row_tiles, nbw, ksl;
 };
 
 // The types folded per group of steps (Q8_0, Q8_0R, Q6_K) take at most 2
@@ -847,7 +878,7 @@ void sx_tiles(int type, uint32_t tokens, uint32_t &tt, uint32_t &groups) {
   groups = (ttn + tt - 1u) / tt;
 }
 
-SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg) {
+SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg, uint32_t ksl_opt) {
   SxPlan p;
   sx_tiles(wv.type, tokens, p.tt, p.groups);
   // measured (C5 shapes): 32 rows x 8 waves up to 32 tokens per tile group;
@@ -860,20 +891,35 @@ SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg) {
   // 31.6 / 32.4); from two rounds 64 x 4 again (M = 640: Q2_K 81.0 against
   // 89.1; M = 320 and 448 within 3 % either way).
   const uint32_t rt64 = (wv.rows + 63u) / 64u, w64 = p.groups * rt64;
-  p.cfg = cfg ? (uint32_t)(cfg - 1) : (p.tt == 4u && w64 >= 256u && !(w64 > 256u && w64 < 512u) ? 1u : 0u);
-  const uint32_t rows_per = p.cfg ? 64u : 32u, nw = p.cfg ? 4u : 8u, ks = p.cfg == 2u ? 2u : 1u;
+  // cfg 3 (forced): 64 x 4 in two k slices
+  p.cfg = cfg ? (cfg == 3 ? 1u : (uint32_t)(cfg - 1)) : (p.tt == 4u && w64 >= 256u && !(w64 > 256u && w64 < 512u) ? 1u : 0u);
+  const uint32_t rows_per = p.cfg ? 64u : 32u, nw = p.cfg ? 4u : 8u, nb = wv.k / 256u;
   p.row_tiles = (wv.rows + rows_per - 1u) / rows_per;
-  p.nbw = ((wv.k / 256u + ks - 1u) / ks + nw - 1u) / nw;
+  // Below 192 workgroups (few rows: 2048 rows are 64 tiles of 32), k slices
+  // bring the grid to about 256, with 4 blocks of k per slice at least
+  // (us, unsliced / 2 / 4 slices, 2048 x 8192 at 9 and 64 tokens: Q4_K 18.9 /
+  // 13.9 / 11.5 and 38.6 / 24.3 / 18.5, Q8_0 23.9 / 17.2 / 13.6; 4096 x 14336
+  // at 32 tokens, 128 workgroups: Q4_K 42.3 / 27.7 / 30.7, Q6_K 51.3 / 36.3 /
+  // 40.4); from 256 workgroups none (Q4_K 2048 x 8192 at 512 tokens: 69.1 /
+  // 74.0 / 85.7).
+  const uint32_t wgs = p.row_tiles * p.groups;
+  const uint32_t ks_auto = wgs < 192u ? min((256u + wgs / 2u) / wgs, max(nb / 4u, 1u)) : 1u;
+  p.ksl = ksl_opt ? ksl_opt : cfg == 3 ? 2u : ks_auto;
+  p.ksl = max(1u, min(p.ksl, nb));
+  p.nbw = ((nb + p.ksl - 1u) / p.ksl + nw - 1u) / nw;
   return p;
 }
 
-template <int TYPE, int TT, int RF, int NW, int KS>
+template <int TYPE, int TT, int RF, int NW>
 hipError_t sx_go(const WeightView &wv, const uint8_t *xa, const float *xp, float *y, uint32_t tokens,
-                 const SxPlan &p, hipStream_t s) {
+                 const SxPlan &p, void *sk, hipStream_t s) {
   const uint64_t tiles = (uint64_t)p.groups * p.tt;
   const uint32_t xa_bytes = (uint32_t)(tiles * (wv.k / 256u) * sx_slots<TYPE>() * 1024u);
-  hipLaunchKernelGGL((k_sx<TYPE, TT, RF, NW, KS, false>), dim3(p.row_tiles * KS, p.groups), dim3(NW * 64), 0, s, wv,
-                     xa, xp, y, tokens, p.nbw, xa_bytes, nullptr);
+  if (p.ksl > 1u && (!sk || (uint64_t)p.row_tiles * p.groups > kSliceCntBytes / 4u)) return hipErrorInvalidValue;
+  uint32_t *cnt = (uint32_t *)sk;
+  float *part = sk ? (float *)((uint8_t *)sk + kSliceCntBytes) : nullptr;
+  hipLaunchKernelGGL((k_sx<TYPE, TT, RF, NW, false>), dim3(p.row_tiles * p.ksl, p.groups), dim3(NW * 64), 0, s, wv,
+                     xa, xp, y, tokens, p.nbw, xa_bytes, nullptr, p.ksl, part, cnt);
   return hipGetLastError();
 }
 
@@ -884,56 +930,52 @@ hipError_t sx_go_fx(const WeightView &wv, const float *x, float *y, uint32_t tok
   constexpr uint32_t lds = L::TAB + L::WORK + 8u * sx_fx_bytes<TYPE>();
   static_assert(lds + 16u <= kMxMaxLds, "fused split-x LDS");
   static std::atomic<uint64_t> attr{0};
-  const hipError_t e = lds_limit_once((const void *)k_sx<TYPE, 1, 1, 8, 1, true>, (int)lds, attr);
+  const hipError_t e = lds_limit_once((const void *)k_sx<TYPE, 1, 1, 8, true>, (int)lds, attr);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_sx<TYPE, 1, 1, 8, 1, true>), dim3(p.row_tiles, 1), dim3(8 * 64), lds, s, wv, nullptr, nullptr,
-                     y, tokens, p.nbw, 0u, x);
+  hipLaunchKernelGGL((k_sx<TYPE, 1, 1, 8, true>), dim3(p.row_tiles, 1), dim3(8 * 64), lds, s, wv, nullptr, nullptr,
+                     y, tokens, p.nbw, 0u, x, 1u, nullptr, nullptr);
   return hipGetLastError();
 }
 
 template <int TYPE, int TT>
 hipError_t sx_cfg(const WeightView &wv, const uint8_t *xa, const float *xp, float *y, uint32_t tokens,
-                  const SxPlan &p, hipStream_t s) {
-  switch (p.cfg) {
-    case 0: return sx_go<TYPE, TT, 1, 8, 1>(wv, xa, xp, y, tokens, p, s);
-    case 1: return sx_go<TYPE, TT, 2, 4, 1>(wv, xa, xp, y, tokens, p, s);
-    default: return sx_go<TYPE, TT, 2, 4, 2>(wv, xa, xp, y, tokens, p, s);
-  }
+                  const SxPlan &p, void *sk, hipStream_t s) {
+  if (p.cfg == 0u) return sx_go<TYPE, TT, 1, 8>(wv, xa, xp, y, tokens, p, sk, s);
+  return sx_go<TYPE, TT, 2, 4>(wv, xa, xp, y, tokens, p, sk, s);
 }
 
 // Up to 8 tokens of Q2_K / IQ2_XXS with the automatic plan: one launch, each
 // wave preparing its own block's x.
 bool sx_fx(int type, uint32_t tokens, int cfg, const SxPlan &p) {
-  return (type == Q2_K || type == IQ2_XXS) && cfg == 0 && tokens <= 8u && p.cfg == 0u;
+  return (type == Q2_K || type == IQ2_XXS) && cfg == 0 && tokens <= 8u && p.cfg == 0u && p.ksl == 1u;
 }
 
 // The product from x prepared in `xa` for `tiles` token tiles (at least the
 // plan's; the tokens' block scales follow the fragments).
 template <int TYPE>
 hipError_t sx_main(const WeightView &wv, const uint8_t *xa, uint32_t tiles, float *y, uint32_t tokens,
-                   const SxPlan &p, hipStream_t s) {
+                   const SxPlan &p, void *sk, hipStream_t s) {
   const float *xp = (const float *)(xa + (uint64_t)tiles * (wv.k / 256u) * sx_slots<TYPE>() * 1024u);
   switch (p.tt) {
-    case 1: return sx_cfg<TYPE, 1>(wv, xa, xp, y, tokens, p, s);
-    case 2: return sx_cfg<TYPE, 2>(wv, xa, xp, y, tokens, p, s);
+    case 1: return sx_cfg<TYPE, 1>(wv, xa, xp, y, tokens, p, sk, s);
+    case 2: return sx_cfg<TYPE, 2>(wv, xa, xp, y, tokens, p, sk, s);
     default:
-      if constexpr (SxW<TYPE>::FG == 16) return sx_cfg<TYPE, 4>(wv, xa, xp, y, tokens, p, s);
+      if constexpr (SxW<TYPE>::FG == 16) return sx_cfg<TYPE, 4>(wv, xa, xp, y, tokens, p, sk, s);
       return hipErrorInvalidValue;   // not planned (sx_tt_max)
   }
 }
 
 template <int TYPE>
 hipError_t sx_type(const WeightView &wv, const float *x, float *y, uint32_t tokens, uint8_t *scratch, int cfg,
-                   hipStream_t s) {
-  const SxPlan p = sx_plan(wv, tokens, cfg);
+                   uint32_t ksl_opt, void *sk, hipStream_t s) {
+  const SxPlan p = sx_plan(wv, tokens, cfg, ksl_opt);
   if constexpr (TYPE == Q2_K || TYPE == IQ2_XXS)
     if (sx_fx(TYPE, tokens, cfg, p)) return sx_go_fx<TYPE>(wv, x, y, tokens, p, s);
   const uint32_t tiles = p.groups * p.tt, nb = wv.k / 256u;   // blocks of 256 weights
   uint8_t *xa = scratch;
   float *xp = (float *)(scratch + (uint64_t)tiles * nb * sx_slots<TYPE>() * 1024u);
-  const uint32_t yz = p.cfg == 2u ? tokens * wv.rows : 0u;
-  hipLaunchKernelGGL((k_sx_prep<TYPE>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, wv.k, xa, xp, y, yz);
-  return sx_main<TYPE>(wv, xa, tiles, y, tokens, p, s);
+  hipLaunchKernelGGL((k_sx_prep<TYPE>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, wv.k, xa, xp);
+  return sx_main<TYPE>(wv, xa, tiles, y, tokens, p, sk, s);
 }
 
 // Token tiles of a prepared x: a multiple of 4 (the most a plan groups), so
@@ -958,9 +1000,16 @@ size_t sx_x_bytes(int type, uint32_t tokens, uint32_t k) {
   return (size_t)(tiles * nb * slots * 1024u + tiles * nb * 64u);
 }
 
-uint32_t sx_x_layout(const WeightView &wv, uint32_t tokens, int cfg) {
-  const SxPlan p = sx_plan(wv, tokens, cfg);
-  if (sx_fx(wv.type, tokens, cfg, p) || p.cfg == 2u) return 0u;
+size_t sx_sk_bytes(const WeightView &wv, uint32_t tokens, int cfg, uint32_t ksl_opt) {
+  const SxPlan p = sx_plan(wv, tokens, cfg, ksl_opt);
+  if (p.ksl < 2u || sx_fx(wv.type, tokens, cfg, p)) return 0;
+  const uint64_t ne = (uint64_t)p.tt * (p.cfg ? 2u : 1u) * 512u;   // sums per workgroup
+  return kSliceCntBytes + (size_t)((uint64_t)p.row_tiles * p.groups * p.ksl * ne * 4u);
+}
+
+uint32_t sx_x_layout(const WeightView &wv, uint32_t tokens, int cfg, uint32_t ksl_opt) {
+  const SxPlan p = sx_plan(wv, tokens, cfg, ksl_opt);
+  if (sx_fx(wv.type, tokens, cfg, p)) return 0u;
   switch (wv.type) {
     case Q2_K: return kSxLayout | 1u;
     case Q4_K: return kSxLayout | 2u;
@@ -984,14 +1033,13 @@ hipError_t launch_sx_prepare(uint32_t layout, const float *x, uint32_t tokens, u
   // the same 16 slots
   switch (layout) {
     case kSxLayout | 1u:
-      hipLaunchKernelGGL((k_sx_prep<Q2_K>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, k, xa, xp, nullptr, 0u);
+      hipLaunchKernelGGL((k_sx_prep<Q2_K>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, k, xa, xp);
       break;
     case kSxLayout | 2u:
-      hipLaunchKernelGGL((k_sx_prep<Q4_K>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, k, xa, xp, nullptr, 0u);
+      hipLaunchKernelGGL((k_sx_prep<Q4_K>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, k, xa, xp);
       break;
     case kSxLayout:
-      hipLaunchKernelGGL((k_sx_prep<IQ2_XXS>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, k, xa, xp, nullptr,
-                         0u);
+      hipLaunchKernelGGL((k_sx_prep<IQ2_XXS>), dim3(nb, tiles * 4u), dim3(256), 0, s, x, tokens, k, xa, xp);
       break;
     default: return hipErrorInvalidValue;
   }
@@ -999,32 +1047,31 @@ hipError_t launch_sx_prepare(uint32_t layout, const float *x, uint32_t tokens, u
 }
 
 hipError_t launch_sx_prepared(const WeightView &wv, const void *xprep, float *y, uint32_t tokens, int cfg,
-                              hipStream_t s) {
-  const SxPlan p = sx_plan(wv, tokens, cfg);
-  if (p.cfg == 2u) return hipErrorInvalidValue;   // the k halves add into a y their preparation zeroes
+                              uint32_t ksl_opt, void *sk, hipStream_t s) {
+  const SxPlan p = sx_plan(wv, tokens, cfg, ksl_opt);
   const uint8_t *xa = (const uint8_t *)xprep;
   const uint32_t tiles = sx_prepared_tiles(tokens);
   switch (wv.type) {
-    case Q2_K: return sx_main<Q2_K>(wv, xa, tiles, y, tokens, p, s);
-    case Q4_K: return sx_main<Q4_K>(wv, xa, tiles, y, tokens, p, s);
-    case IQ2_XXS: return sx_main<IQ2_XXS>(wv, xa, tiles, y, tokens, p, s);
-    case Q8_0: return sx_main<Q8_0>(wv, xa, tiles, y, tokens, p, s);
-    case Q8_0R: return sx_main<Q8_0R>(wv, xa, tiles, y, tokens, p, s);
-    case Q6_K: return sx_main<Q6_K>(wv, xa, tiles, y, tokens, p, s);
+    case Q2_K: return sx_main<Q2_K>(wv, xa, tiles, y, tokens, p, sk, s);
+    case Q4_K: return sx_main<Q4_K>(wv, xa, tiles, y, tokens, p, sk, s);
+    case IQ2_XXS: return sx_main<IQ2_XXS>(wv, xa, tiles, y, tokens, p, sk, s);
+    case Q8_0: return sx_main<Q8_0>(wv, xa, tiles, y, tokens, p, sk, s);
+    case Q8_0R: return sx_main<Q8_0R>(wv, xa, tiles, y, tokens, p, sk, s);
+    case Q6_K: return sx_main<Q6_K>(wv, xa, tiles, y, tokens, p, sk, s);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_sx(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *scratch, int cfg,
-                     hipStream_t s) {
+                     uint32_t ksl_opt, void *sk, hipStream_t s) {
   uint8_t *sc = (uint8_t *)scratch;
   switch (wv.type) {
-    case Q2_K: return sx_type<Q2_K>(wv, x, y, tokens, sc, cfg, s);
-    case Q4_K: return sx_type<Q4_K>(wv, x, y, tokens, sc, cfg, s);
-    case IQ2_XXS: return sx_type<IQ2_XXS>(wv, x, y, tokens, sc, cfg, s);
-    case Q8_0: return sx_type<Q8_0>(wv, x, y, tokens, sc, cfg, s);
-    case Q8_0R: return sx_type<Q8_0R>(wv, x, y, tokens, sc, cfg, s);
-    case Q6_K: return sx_type<Q6_K>(wv, x, y, tokens, sc, cfg, s);
+    case Q2_K: return sx_type<Q2_K>(wv, x, y, tokens, sc, cfg, ksl_opt, sk, s);
+    case Q4_K: return sx_type<Q4_K>(wv, x, y, tokens, sc, cfg, ksl_opt, sk, s);
+    case IQ2_XXS: return sx_type<IQ2_XXS>(wv, x, y, tokens, sc, cfg, ksl_opt, sk, s);
+    case Q8_0: return sx_type<Q8_0>(wv, x, y, tokens, sc, cfg, ksl_opt, sk, s);
+    case Q8_0R: return sx_type<Q8_0R>(wv, x, y, tokens, sc, cfg, ksl_opt, sk, s);
+    case Q6_K: return sx_type<Q6_K>(wv, x, y, tokens, sc, cfg, ksl_opt, sk, s);
     default: return hipErrorInvalidValue;
   }
 }

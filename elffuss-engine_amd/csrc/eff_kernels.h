@@ -94,6 +94,9 @@ hipError_t launch_gemv_mt(const WeightView &wv, const float *x, float *y, uint32
 size_t gemm_x_bytes(int type, uint32_t tokens, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg);
 // An id of that layout: equal ids, one prepared x serves both products.
 uint32_t gemm_x_layout(int type, uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg);
+// k-slice scratch (the Q8_0 GEMM's and the split-x product's): a counter per
+// output tile (at most 2^16 tiles), then the slices' sums.
+constexpr uint32_t kSliceCntBytes = 1u << 18;
 // The k-slice scratch of the product (0 bytes: none): the Q8_0 GEMM cuts k
 // into slices over workgroups where the tiles alone leave CUs idle.
 // ksl_opt: forced slice count (EFF_OPT_GEMM_SPLIT; 0 automatic). The scratch
@@ -108,7 +111,8 @@ hipError_t launch_gemm_x(int type, const float *x, uint32_t tokens, uint32_t pla
                          uint32_t cfg, void *xh, hipStream_t stream);
 hipError_t launch_gemm_prepared(const WeightView &wv, const _Float16 *xh, float *y, uint32_t tokens, uint32_t plan,
                                 uint32_t cfg, uint32_t ksl_opt, void *sk_scratch, hipStream_t stream);
-// Q8_0 / Q8_0R GEMM with direct-to-LDS staging (> 128 tokens); x in the
+// Q8_0 / Q8_0R GEMM with direct-to-LDS staging (> 128 tokens, and below 6144
+// rows from the GEMM's threshold); x in the
 // [token tile][k step][2^gemm_big_tile_log2 tokens][64] layout.
 bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows);
 uint32_t gemm_big_tile_log2(uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg);
@@ -121,25 +125,27 @@ hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, u
 // Q6_K from 4 tokens, k % 256 == 0, f32-accurate. `scratch` holds
 // sx_x_bytes(...) bytes (x as fp16 hi/lo parts and the block scales). cfg: 0
 // automatic, 1: 32 rows x 8 waves per workgroup, 2: 64 rows x 4 waves, 3: as 2
-// with the two halves of k in two workgroups.
+// with k in two slices. ksl_opt: forced k slices (0 automatic); `sk` holds
+// the k-slice scratch, sx_sk_bytes(...) bytes (none: 0), with the same
+// counters as the GEMM's (gemm_sk_bytes).
 bool sx_applies(const WeightView &wv, uint32_t tokens);
 size_t sx_x_bytes(int type, uint32_t tokens, uint32_t k);
+size_t sx_sk_bytes(const WeightView &wv, uint32_t tokens, int cfg, uint32_t ksl_opt);
 hipError_t launch_sx(const WeightView &wv, const float *x, float *y, uint32_t tokens, void *scratch, int cfg,
-                     hipStream_t stream);
+                     uint32_t ksl_opt, void *sk, hipStream_t stream);
 // The same product in two halves, so that one preparation of x serves every
 // product of that x: sx_x_layout is the layout the product reads (0: none,
 // the one-launch product up to 8 tokens reads x itself; kSxLayout for IQ2_XXS,
 // Q8_0 and Q6_K, | 1 with the group sums of Q2_K, | 2 with those of Q4_K);
 // launch_sx_prepare writes x in it (sx_prepared_bytes), launch_sx_prepared
-// runs the product from it (the same bits as launch_sx; hipErrorInvalidValue
-// for cfg 3, whose k halves add into a y their preparation zeroes).
+// runs the product from it (the same bits as launch_sx).
 constexpr uint32_t kSxLayout = 0x100u;
-uint32_t sx_x_layout(const WeightView &wv, uint32_t tokens, int cfg);
+uint32_t sx_x_layout(const WeightView &wv, uint32_t tokens, int cfg, uint32_t ksl_opt);
 size_t sx_prepared_bytes(uint32_t layout, uint32_t tokens, uint32_t k);
 hipError_t launch_sx_prepare(uint32_t layout, const float *x, uint32_t tokens, uint32_t k, void *xprep,
                              hipStream_t stream);
 hipError_t launch_sx_prepared(const WeightView &wv, const void *xprep, float *y, uint32_t tokens, int cfg,
-                              hipStream_t stream);
+                              uint32_t ksl_opt, void *sk, hipStream_t stream);
 
 // The reference CPU path's arithmetic for Q8_0 (eff_cpu_path.hip): x into
 // 40-byte 8-bit blocks in `act` (cpu_path_act_bytes(...)), then per row and

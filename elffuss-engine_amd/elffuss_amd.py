@@ -21,7 +21,7 @@ E_INVALID, E_TYPE, E_SHAPE, E_MARK, E_BOUNDS, E_DEVICE, E_NOMEM = -1, -2, -3, -4
 Q8_0, Q2_K, Q4_K, Q6_K, IQ2_XXS, Q8_0R = 8, 10, 12, 14, 16, 264
 TYPES = {"Q8_0": Q8_0, "Q2_K": Q2_K, "Q4_K": Q4_K, "Q6_K": Q6_K, "IQ2_XXS": IQ2_XXS, "Q8_0R": Q8_0R}
 OPT_GEMV_MAX_TOKENS, OPT_GEMM_MIN_TOKENS, OPT_GEMV_KERNEL, OPT_SPLIT_CONFIG, OPT_SPLIT_MIN_TOKENS = 1, 2, 3, 4, 5
-OPT_GEMM_CONFIG, OPT_GEMM_SPLIT = 6, 7
+OPT_GEMM_CONFIG, OPT_GEMM_SPLIT, OPT_SPLIT_SLICES = 6, 7, 8
 GEMV_SECTIONS, GEMV_SWIGLU = 1, 2
 TOPK_HEADER, TOPK_P_MAX, TOPK_CAP, TOPK_M_MAX = 8, 128, 256, 192
 TOPK_NOALLOC_SCRATCH_BYTES = 18432

@@ -53,20 +53,23 @@ extern "C" {
 #define EFF_OPT_GEMM_MIN_TOKENS  2  /* tokens >= this go to the fp16 MFMA GEMM (default 64; __ELFFUSS_DRIFT_DESDE) */
 #define EFF_OPT_GEMV_KERNEL      3  /* 0: int8 matrix-core GEMV where it applies (default), 1: f32 vector GEMV */
 #define EFF_OPT_SPLIT_CONFIG     4  /* split-x product workgroups (tuning): 0 automatic (default), 1: 32 rows x
-                                       8 waves, 2: 64 rows x 4 waves, 3: 64 rows x 4 waves with k halves in two
-                                       workgroups added into y */
+                                       8 waves, 2: 64 rows x 4 waves, 3: 64 rows x 4 waves with k in two slices
+                                       (EFF_OPT_SPLIT_SLICES) */
 #define EFF_OPT_SPLIT_MIN_TOKENS 5  /* Q2_K, Q4_K, IQ2_XXS, Q8_0, Q6_K: tokens >= this run the split-x product, fewer
                                        the int8 matrix-core GEMVs (0: automatic, 5 for Q2_K and IQ2_XXS, 9 for the
                                        others (default); else >= 4). Q8_0 only below EFF_OPT_GEMM_MIN_TOKENS */
-#define EFF_OPT_GEMM_CONFIG      6  /* Q8_0 GEMM from 129 tokens, tiles (tuning; tokens x rows, waves along tokens x
-                                       rows, LDS stages): 0 automatic (default), 1: 256x256 1x4 3, 2: 128x128 1x4 3,
+#define EFF_OPT_GEMM_CONFIG      6  /* Q8_0 GEMM from 129 tokens (below 6144 rows from the GEMM's threshold),
+                                       tiles (tuning; tokens x rows, waves along tokens x rows, LDS stages):
+                                       0 automatic (default), 1: 256x256 1x4 3, 2: 128x128 1x4 3,
                                        3: 128x128 1x4 6, 4: 64x128 1x4 4, 5: 128x256 1x4 4, 6: 256x128 2x2 3; every
                                        configuration sums each output in the same order (the same bits) */
-#define EFF_OPT_GEMM_SPLIT       7  /* Q8_0 GEMM from 129 tokens, k slices over workgroups (tuning): 0 automatic
+#define EFF_OPT_GEMM_SPLIT       7  /* the same Q8_0 GEMM, k slices over workgroups (tuning): 0 automatic
                                        (default: where the tiles leave CUs idle, about 256 workgroups in all,
                                        slices of 512 k at least), else that many (1: none; 256 x 256 tiles
                                        take none); the slices' sums are added in slice order, so each count
                                        gives fixed bits */
+#define EFF_OPT_SPLIT_SLICES     8  /* split-x product, k slices over workgroups (tuning): 0 automatic (default),
+                                       else that many (1: none); the slices' sums are added in slice order */
 
 /* ---- fused GEMV modes (gemv2Shader `modo`, kernels.gemv.wgsl.js:370-375) -- */
 #define EFF_GEMV_SECTIONS  1  /* 'secciones': ys[i] = W_i x for 2..4 matrices */

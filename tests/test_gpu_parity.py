@@ -574,7 +574,7 @@ def test_split_x_vs_f64_oracle(ctx, eff, orc, tname, tokens, split_from_4):
 def test_split_x_k_and_configs(ctx, eff, orc, tname, k):
     """One block per row, fewer blocks than waves, many blocks per wave; every
     workgroup configuration (32 rows x 8 waves, 64 rows x 4 waves, and the same
-    with the halves of k in two workgroups) meets the bar."""
+    with k in two slices over two workgroups) meets the bar."""
     rows, tokens = 100, 20
     t, data, gguf, n = make_weights(eff, tname, rows, k, 400 + k)
     x = eff.fill_normal(4000 + k, 1.0, tokens * k)
@@ -589,7 +589,7 @@ def test_split_x_k_and_configs(ctx, eff, orc, tname, k):
             ctx.set_option(eff.OPT_SPLIT_CONFIG, 0)
         got = yb.read(np.uint32)
         check_close(got.view(np.float32), ref, f"split-x {tname} k={k} cfg={cfg}")
-        if cfg == 3:    # two partial sums added into y: the same bits on every call
+        if cfg == 3:    # two slices' sums added in slice order: the same bits on every call
             ctx.set_option(eff.OPT_SPLIT_CONFIG, cfg)
             try:
                 ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
@@ -599,14 +599,52 @@ def test_split_x_k_and_configs(ctx, eff, orc, tname, k):
         yb.free()
 
 
+@pytest.mark.parametrize("tname", SPLIT_TYPES + ["Q8_0", "Q8_0R", "Q6_K"])
+@pytest.mark.parametrize("tokens", [9, 40, 130])
+def test_split_x_k_slices(ctx, eff, orc, tname, tokens):
+    """k slices over workgroups (EFF_OPT_SPLIT_SLICES 2, 3, 7 and 64, more
+    than the 33 blocks of k: one block per slice, some slices empty of
+    blocks for a wave): each meets the f64 bar, and a second call gives the
+    same bits (the tile's last workgroup adds the slices in slice order and
+    leaves the arrival counters at zero)."""
+    rows, k = 200, 8448
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 880 + tokens)
+    x = eff.fill_normal(881 + tokens, 1.0, tokens * k)
+    wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    ref = orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens)
+    gemm_min = 64 if tname in ("Q8_0", "Q8_0R") and tokens >= 64 else None
+    try:
+        if gemm_min:
+            ctx.set_option(eff.OPT_GEMM_MIN_TOKENS, 1000)   # Q8_0 beyond 63 tokens: split-x too
+        for ks in (2, 3, 7, 64):
+            ctx.set_option(eff.OPT_SPLIT_SLICES, ks)
+            before = ctx.stats()["split"]
+            ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+            assert ctx.stats()["split"] == before + 1
+            y0 = yb.read(np.uint32)
+            check_close(y0.view(np.float32), ref, f"split-x {tname} M={tokens} slices={ks}")
+            yb.write(np.full(tokens * rows, 0x7FC00000, np.uint32))
+            ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+            assert np.array_equal(yb.read(np.uint32), y0), f"slices={ks}: a second call differs"
+        with pytest.raises(eff.EffError):
+            ctx.set_option(eff.OPT_SPLIT_SLICES, 65)
+    finally:
+        ctx.set_option(eff.OPT_SPLIT_SLICES, 0)
+        if gemm_min:
+            ctx.set_option(eff.OPT_GEMM_MIN_TOKENS, gemm_min)
+    for b in (wb, xb, yb):
+        b.free()
+
+
 @pytest.mark.parametrize("tname", ["Q2_K", "IQ2_XXS"])
 @pytest.mark.parametrize("tokens,k", [(4, 2304), (8, 2048), (8, 4096), (5, 256)])
 def test_split_x_one_launch_bit_identical(ctx, eff, orc, tname, tokens, k, split_from_4):
     """Up to 8 tokens of Q2_K / IQ2_XXS the product prepares x itself (one
-    launch); the same 32 x 8 plan with the preparation launch
-    (EFF_OPT_SPLIT_CONFIG = 1) gives the same bits, and both meet the f64 bar
-    (one and two blocks per wave, a single block per row)."""
-    rows = 300
+    launch, where the rows give 192 workgroups or more and so no k slices);
+    the same 32 x 8 plan with the preparation launch (EFF_OPT_SPLIT_CONFIG =
+    1) gives the same bits, and both meet the f64 bar (one and two blocks per
+    wave, a single block per row)."""
+    rows = 6200
     t, data, gguf, n = make_weights(eff, tname, rows, k, 500 + tokens + k)
     x = eff.fill_normal(5000 + tokens + k, 1.0, tokens * k)
     wb, xb = ctx.upload(data), ctx.upload(x)
@@ -848,20 +886,30 @@ def test_matmul_prepared_x_serves_several_products(ctx, eff, tokens):
 
 def test_matmul_prepared_x_not_applicable_and_errors(ctx, eff):
     """Calls whose path reads x itself answer NOT_APPLICABLE (the GEMVs, the
-    one-launch split-x product up to 8 tokens, the token groups, the split-x
-    configuration whose k halves add into y); a forced configuration that
-    prepares x gives eff_qmatmul's bits; a short buffer is refused."""
+    one-launch split-x product up to 8 tokens, the token groups); a forced
+    configuration that prepares x (also one with k in two slices) gives
+    eff_qmatmul's bits; a short buffer is refused."""
     k = 2304
-    for tname, r, kk, tokens in [("Q2_K", 64, k, 4), ("Q2_K", 64, k, 8), ("IQ2_XXS", 64, k, 5),
+    # (the one-launch product over 8192 rows: 256 workgroups, no k slices)
+    for tname, r, kk, tokens in [("Q2_K", 64, k, 4), ("Q2_K", 8192, k, 8), ("IQ2_XXS", 8192, k, 5),
                                  ("Q4_K", 64, k, 8), ("Q8_0R", 64, 2080, 33), ("Q8_0", 64, 2080, 33)]:
         with pytest.raises(eff.NotApplicable):
             ctx.qmatmul_x_layout(eff.TYPES[tname], r, kk, tokens)
     t, data, _, _ = make_weights(eff, "Q2_K", 77, k, 8300)
     wb = ctx.upload(data)
     try:
-        ctx.set_option(eff.OPT_SPLIT_CONFIG, 3)
-        with pytest.raises(eff.NotApplicable):
-            ctx.qmatmul_x_layout(t, 77, k, 33)
+        ctx.set_option(eff.OPT_SPLIT_CONFIG, 3)      # 64 rows x 4 waves, k in two slices
+        nbytes, lay = ctx.qmatmul_x_layout(t, 77, k, 33)
+        assert lay == 0x101
+        x = eff.fill_normal(8302, 1.0, 33 * k)
+        xb, xp = ctx.upload(x), ctx.alloc(nbytes)
+        y1, y2 = ctx.alloc(33 * 77 * 4), ctx.alloc(33 * 77 * 4)
+        ctx.qmatmul_prepare_x(t, xb, xp, 77, k, 33)
+        ctx.qmatmul_prepared(t, wb, xp, y1, 77, k, 33)
+        ctx.qmatmul(t, wb, xb, y2, 77, k, 33)
+        assert np.array_equal(y1.read(np.uint32), y2.read(np.uint32))
+        for b in (xb, xp, y1, y2):
+            b.free()
         ctx.set_option(eff.OPT_SPLIT_CONFIG, 1)      # 32 rows x 8 waves, x prepared, at 8 tokens
         nbytes, lay = ctx.qmatmul_x_layout(t, 77, k, 8)
         assert lay == 0x101
