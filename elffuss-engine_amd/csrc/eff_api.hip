@@ -246,7 +246,7 @@ bool mt_routes(uint32_t tokens) { return tokens != 5u && tokens != 6u; }
 // Q8_0, Q8_0R and Q6_K take it from 9 tokens, where the GEMV would run over
 // token groups; Q8_0 and Q8_0R only below the fp16 GEMM's threshold (from
 // there the reference's DRIFT path, whose fp16 roundings the GEMM keeps).
-// Below that, from 4 tokens, also where no int8 matrix-core GEMV fits its x
+// Below that, from 2 tokens, also where no int8 matrix-core GEMV fits its x
 // digits into LDS at this k (about 43 K token x k values: 4096 x 14336 from 3
 // tokens, 2048 x 8192 from 6), which would leave the f32 vector GEMV a pass
 // over the weights per token group (Q8_0 4096 x 14336, 8 tokens: 102.9 us).

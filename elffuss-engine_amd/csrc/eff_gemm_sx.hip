@@ -1,4 +1,4 @@
-// Quantized matrix products from 4 tokens up for Q2_K, Q4_K, IQ2_XXS, Q8_0
+// Quantized matrix products from 2 tokens up for Q2_K, Q4_K, IQ2_XXS, Q8_0
 // and Q6_K, to f32 accuracy (the reference runs the K/IQ types through its f32
 // generic kernel at every token count, ops.js:1013-1099, and Q8_0 below its
 // DRIFT threshold through its f32 tiled GEMM; its f16 GEMMs read Q8_0/Q4_0
@@ -989,7 +989,7 @@ bool sx_applies(const WeightView &wv, uint32_t tokens) {
                  wv.type == Q6_K;
   // Q8_0R is staged with 32-bit offsets from the tensor's first byte
   const bool r = wv.type != Q8_0R || wv.scales_off + 2ull * wv.rows * wv.bpr + 16u < (1ull << 32);
-  return t && r && tokens >= 4u && wv.k % 256u == 0u;
+  return t && r && tokens >= 2u && wv.k % 256u == 0u;
 }
 
 size_t sx_x_bytes(int type, uint32_t tokens, uint32_t k) {

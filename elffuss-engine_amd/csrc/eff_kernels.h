@@ -122,7 +122,7 @@ hipError_t launch_gemm_big(const WeightView &wv, const _Float16 *xh, float *y, u
                            uint32_t cfg, uint32_t ksl_opt, void *scratch, hipStream_t stream);
 
 // Split-x matrix-core product (eff_gemm_sx.hip): Q2_K, Q4_K, IQ2_XXS, Q8_0,
-// Q6_K from 4 tokens, k % 256 == 0, f32-accurate. `scratch` holds
+// Q6_K from 2 tokens, k % 256 == 0, f32-accurate. `scratch` holds
 // sx_x_bytes(...) bytes (x as fp16 hi/lo parts and the block scales). cfg: 0
 // automatic, 1: 32 rows x 8 waves per workgroup, 2: 64 rows x 4 waves, 3: as 2
 // with k in two slices. ksl_opt: forced k slices (0 automatic); `sk` holds

@@ -636,6 +636,29 @@ def test_split_x_k_slices(ctx, eff, orc, tname, tokens):
         b.free()
 
 
+@pytest.mark.parametrize("tname", SPLIT_TYPES + ["Q8_0", "Q6_K"])
+@pytest.mark.parametrize("tokens,k,split", [(3, 16384, True), (2, 32768, True), (2, 14336, False),
+                                            (6, 8192, True), (4, 8192, False)])
+def test_router_split_x_where_gemv_digits_do_not_fit(ctx, eff, orc, tname, tokens, k, split):
+    """Where the int8 matrix-core GEMVs cannot hold x's digits in LDS (3.5
+    bytes per token and k: 3 tokens at k = 16384, 2 at 32768, 6 at 8192),
+    the router takes the split-x product from 2 tokens instead of the f32
+    vector GEMV; where they fit (2 tokens at 14336, 4 at 8192) the GEMV
+    stays. Both meet the f64 bar."""
+    rows = 300
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 890 + tokens + k)
+    x = eff.fill_normal(891 + tokens, 1.0, tokens * k)
+    wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    before = ctx.stats()
+    ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+    after = ctx.stats()
+    assert after["split"] - before["split"] == (1 if split else 0)
+    check_close(yb.read(np.float32), orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens),
+                f"router {tname} M={tokens} k={k}")
+    for b in (wb, xb, yb):
+        b.free()
+
+
 @pytest.mark.parametrize("tname", ["Q2_K", "IQ2_XXS"])
 @pytest.mark.parametrize("tokens,k", [(4, 2304), (8, 2048), (8, 4096), (5, 256)])
 def test_split_x_one_launch_bit_identical(ctx, eff, orc, tname, tokens, k, split_from_4):
