@@ -524,6 +524,10 @@ def main():
         for tn in ("Q2_K", "IQ2_XXS"):
             for m in (1, 8, 32, 128):
                 plan.append(("C5", tn, 8192, 2048, m, 0))
+        # the FFN down projection (C2's 2048 x 8192) beyond one token: few rows, so the split-x product and
+        # the GEMM cut k into slices over workgroups
+        plan += [("C2-shape", "Q8_0", 2048, 8192, 8, 0), ("C2-shape", "Q4_K", 2048, 8192, 64, 0),
+                 ("C2-shape", "Q8_0", 2048, 8192, 512, 0)]
         for tag, tn, r, kk, m, tk in plan:
             key = f"{tag} {tn} N={r} K={kk} M={m}" + (" +top40" if tk else "")
             if args.only and args.only not in key:
