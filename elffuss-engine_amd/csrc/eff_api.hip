@@ -79,6 +79,7 @@ struct eff_ctx {
   int64_t gemm_split = 0;           // Q8_0 GEMM k slices (0: automatic)
   int64_t sx_split = 0;             // split-x k slices (0: automatic)
   void *sk_scratch = nullptr;       // k-slice counters and sums (GEMM and split-x)
+  hipEvent_t order_ev = nullptr;    // orders a newly set stream after the previous one
   size_t sk_scratch_bytes = 0;
   int64_t sx_min_tokens = 0;        // 0: the measured default (sx_routes)
   void *act_scratch = nullptr;      // x in the CPU path's 8-bit blocks (eff_qmatmul_cpu_path)
@@ -498,6 +499,7 @@ int eff_shutdown(eff_ctx *ctx) {
   if (ctx->sx_scratch) (void)hipFree(ctx->sx_scratch);
   if (ctx->act_scratch) (void)hipFree(ctx->act_scratch);
   if (ctx->sk_scratch) (void)hipFree(ctx->sk_scratch);
+  if (ctx->order_ev) (void)hipEventDestroy(ctx->order_ev);
   for (auto &p : ctx->stage_pend) (void)hipEventDestroy(p.ev);
   for (hipEvent_t ev : ctx->events) (void)hipEventDestroy(ev);
   if (ctx->stage) (void)hipHostFree(ctx->stage);
@@ -511,9 +513,27 @@ const char *eff_last_error(const eff_ctx *ctx) { return ctx ? ctx->error.c_str()
 
 void *eff_stream(eff_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 
+// The context's scratch buffers (and the k-slice counters, which must be
+// zero when a launch starts) are reused by every call, so a call on the new
+// stream must not overlap one still queued on the previous stream: the new
+// stream waits for an event recorded on the previous one. A stream being
+// recorded into a graph takes no such wait (its launches run when the graph
+// is replayed, which the caller orders); switching away from a stream being
+// recorded is refused (the recording would lose the calls that follow).
 int eff_set_stream(eff_ctx *ctx, void *hip_stream) {
   if (!ctx) return EFF_E_INVALID;
-  ctx->stream = hip_stream ? (hipStream_t)hip_stream : ctx->own;
+  const hipStream_t next = hip_stream ? (hipStream_t)hip_stream : ctx->own;
+  if (next == ctx->stream) return EFF_OK;
+  int rc = use_device(ctx);
+  if (rc || (rc = refuse_capture(ctx, "set stream"))) return rc;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  EFF_HIP(ctx, hipStreamIsCapturing(next, &cs));
+  if (cs == hipStreamCaptureStatusNone) {
+    if (!ctx->order_ev) EFF_HIP(ctx, hipEventCreateWithFlags(&ctx->order_ev, hipEventDisableTiming));
+    EFF_HIP(ctx, hipEventRecord(ctx->order_ev, ctx->stream));
+    EFF_HIP(ctx, hipStreamWaitEvent(next, ctx->order_ev, 0));
+  }
+  ctx->stream = next;
   return EFF_OK;
 }
 

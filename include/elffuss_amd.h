@@ -142,7 +142,12 @@ const char *eff_last_error(const eff_ctx *ctx);
 void *eff_stream(eff_ctx *ctx);
 
 /* Enqueue on a caller-owned hipStream_t from now on (NULL: back to the
- * context's own stream). The caller keeps ownership. */
+ * context's own stream). The caller keeps ownership. The calls enqueued from
+ * now on wait for those already enqueued on the previous stream (they share
+ * the context's scratch buffers): the new stream waits for an event recorded
+ * on the previous one, unless it is being recorded into a graph (the caller
+ * orders the replays). EFF_E_INVALID while the previous stream is recorded
+ * into a graph. */
 int eff_set_stream(eff_ctx *ctx, void *hip_stream);
 
 /* Wait for everything enqueued on the context's stream. */

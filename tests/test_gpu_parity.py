@@ -350,6 +350,45 @@ def test_gemm_q8_0_k_slices_graph_replays(ctx, eff, orc):
         b.free()
 
 
+def test_set_stream_orders_after_the_previous_stream(ctx, eff):
+    """Calls after eff_set_stream wait for those queued on the previous
+    stream, with which they share the context's scratch (here two k-sliced
+    GEMMs of different tile counts on the same arrival counters): a product
+    queued on the context's stream, a switch to a caller's stream without a
+    sync, another product there, and the switch back; both outputs keep the
+    bits they have on one stream."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so.7")   # the runtime the library already loaded
+    side = ctypes.c_void_p()
+    assert hip.hipStreamCreateWithFlags(ctypes.byref(side), ctypes.c_uint(1)) == 0   # non-blocking, default priority
+    k = 4096
+    shapes = [(600, 300), (520, 200)]   # rows, tokens: 25 and 20 tiles of 64 x 128, k in 8 slices
+    bufs, want = [], []
+    for i, (rows, tokens) in enumerate(shapes):
+        t, data, _, _ = make_weights(eff, "Q8_0", rows, k, 875 + i)
+        wb, xb = ctx.upload(data), ctx.upload(eff.fill_normal(876 + i, 1.0, tokens * k))
+        yb = ctx.alloc(tokens * rows * 4)
+        ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+        want.append(yb.read(np.uint32))
+        bufs.append((t, wb, xb, yb, rows, tokens))
+    for rnd in range(3):
+        for (_, _, _, yb, rows, tokens) in bufs:
+            yb.write(np.full(tokens * rows, 0x7FC00000, np.uint32))
+        t, wb, xb, yb, rows, tokens = bufs[0]
+        ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+        ctx.set_stream(side.value)
+        t, wb, xb, yb, rows, tokens = bufs[1]
+        ctx.qgemm(t, wb, xb, yb, rows, k, tokens)
+        ctx.set_stream(None)
+        for (_, _, _, yb, _, _), w in zip(bufs, want):
+            assert np.array_equal(yb.read(np.uint32), w), rnd
+    ctx.sync()
+    assert hip.hipStreamSynchronize(side) == 0 and hip.hipStreamDestroy(side) == 0
+    for (_, wb, xb, yb, _, _) in bufs:
+        for b in (wb, xb, yb):
+            b.free()
+
+
 @pytest.mark.parametrize("tokens,k", [(256, 2048), (300, 544), (777, 1024), (1100, 96), (2048, 512)])
 def test_gemm_q8_0r_same_bits_as_q8_0(ctx, eff, tokens, k):
     """The prefill GEMM over a repacked tensor (Q8_0R: quants and scales in
