@@ -79,8 +79,8 @@ struct eff_ctx {
   int64_t gemm_split = 0;           // Q8_0 GEMM k slices (0: automatic)
   int64_t sx_split = 0;             // split-x k slices (0: automatic)
   void *sk_scratch = nullptr;       // k-slice counters and sums (GEMM and split-x)
-  hipEvent_t order_ev = nullptr;    // orders a newly set stream after the previous one
   size_t sk_scratch_bytes = 0;
+  hipEvent_t order_ev = nullptr;    // orders a newly set stream after the previous one
   int64_t sx_min_tokens = 0;        // 0: the measured default (sx_routes)
   void *act_scratch = nullptr;      // x in the CPU path's 8-bit blocks (eff_qmatmul_cpu_path)
   size_t act_scratch_bytes = 0;
@@ -308,7 +308,7 @@ int sk_get(eff_ctx *ctx, size_t need, void **out) {
   *out = nullptr;
   if (!need) return EFF_OK;
   const size_t before = ctx->sk_scratch_bytes;
-  const int rc = grow(ctx, &ctx->sk_scratch, &ctx->sk_scratch_bytes, need, "gemm k-slice");
+  const int rc = grow(ctx, &ctx->sk_scratch, &ctx->sk_scratch_bytes, need, "k-slice");
   if (rc) return rc;
   if (ctx->sk_scratch_bytes != before) EFF_HIP(ctx, hipMemsetAsync(ctx->sk_scratch, 0, ctx->sk_scratch_bytes, ctx->stream));
   *out = ctx->sk_scratch;
@@ -321,7 +321,7 @@ int sk_scratch(eff_ctx *ctx, const WeightView &wv, uint32_t tokens, uint32_t pla
                                    (uint32_t)ctx->gemm_split), out);
 }
 
-// Split-x matrix-core product (Q2_K, Q4_K, IQ2_XXS, Q8_0, Q8_0R, Q6_K from 4
+// Split-x matrix-core product (Q2_K, Q4_K, IQ2_XXS, Q8_0, Q8_0R, Q6_K from 2
 // tokens, f32-accurate).
 int run_sx(eff_ctx *ctx, const WeightView &wv, const float *x, float *y, uint32_t tokens) {
   int rc = grow(ctx, &ctx->sx_scratch, &ctx->sx_scratch_bytes, sx_x_bytes(wv.type, tokens, wv.k), "split-x");

@@ -305,9 +305,12 @@ int eff_fill_normal(uint32_t seed, float sigma, float *dst, size_t n);
  * DRIFT/GEMM2 types, kernels.drift.wgsl.js:33); Q2_K, Q4_K, IQ2_XXS, Q6_K and
  * Q8_0/Q8_0R below GEMM min, from EFF_OPT_SPLIT_MIN_TOKENS (5 for Q2_K and
  * IQ2_XXS, 9 for the others) -> split-x product (f32-accurate; fewer tokens
- * run the int8 matrix-core GEMVs, as accurate); otherwise (k not a multiple of
- * 256) -> GEMV over token groups, f32-accurate. Q8_0R gives the bits of the
- * Q8_0 tensor it was repacked from on every path.
+ * run the int8 matrix-core GEMVs, as accurate, and the split-x product from 2
+ * tokens where those cannot hold x's digits in LDS at this k); otherwise (k
+ * not a multiple of 256) -> GEMV over token groups, f32-accurate. Where few
+ * rows leave CUs idle the GEMM and the split-x product cut k into slices over
+ * workgroups (fixed bits for a shape). Q8_0R gives the bits of the Q8_0
+ * tensor it was repacked from on every path.
  * EFF_E_SHAPE if k % block_elems != 0. */
 int eff_qmatmul(eff_ctx *ctx, int type, eff_buf *w, eff_buf *x, eff_buf *y,
                 uint32_t rows, uint32_t k, uint32_t tokens);
