@@ -738,8 +738,9 @@ function createQuantOps(device, opts) {
       if (k % i.blockElems !== 0) throw new Error(`matmul ${type}: k=${k} no es múltiplo de ${i.blockElems}`);
       if (TIPOS_R.has(type)) compruebaBufferR(type, wBuf, { bloques: rows * (k / i.blockElems) }, 'matmul');
       const y = ctx.alloc(rows * t * 4, 'matmul.y');
-      // (below 4 tokens every path reads x itself)
-      const lay = t >= 4 ? native.qmatmulXLayout(device._ctx, i.code, rows, k, t) : null;
+      // (one token: every path reads x itself; from 2 the router says which
+      // prepared x its path reads, if any)
+      const lay = t >= 2 ? native.qmatmulXLayout(device._ctx, i.code, rows, k, t) : null;
       if (lay === null) {
         native.qmatmul(device._ctx, i.code, wBuf._h, xBuf._h, y._h, rows, k, t);
       } else {
