@@ -698,6 +698,37 @@ def test_router_split_x_where_gemv_digits_do_not_fit(ctx, eff, orc, tname, token
         b.free()
 
 
+def test_split_x_k_slices_graph_replays(ctx, eff, orc):
+    """A recorded k-sliced split-x product (its preparation and the product,
+    64 row tiles in 4 slices) replayed several times, with eager sliced
+    products of other shapes between the replays (on the same arrival
+    counters): every replay gives the eager bits, which meet the f64 bar."""
+    rows, k, tokens = 2048, 8192, 32
+    t, data, gguf, n = make_weights(eff, "Q4_K", rows, k, 885)
+    x = eff.fill_normal(886, 1.0, tokens * k)
+    wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    y2 = ctx.alloc(tokens * rows * 4)
+    ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+    y0 = yb.read(np.uint32)
+    check_close(y0.view(np.float32), orc.gemv_f64(orc.Q4_K, gguf, rows, k, x, tokens), "split-x k slices")
+    ctx.qmatmul(t, wb, xb, y2, rows // 2, k, 24)     # grows nothing the recording needs
+    ctx.graph_begin()
+    ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+    g = ctx.graph_end()
+    try:
+        for r in range(4):
+            yb.write(np.full(tokens * rows, 0x7FC00000, np.uint32))
+            g.launch()
+            ctx.sync()
+            got = yb.read(np.uint32)
+            assert np.array_equal(got, y0), f"replay {r}: {np.count_nonzero(got != y0)} outputs differ"
+            ctx.qmatmul(t, wb, xb, y2, rows // 2, k, 24)   # another tile count on the same counters
+    finally:
+        g.destroy()
+    for b in (wb, xb, yb, y2):
+        b.free()
+
+
 @pytest.mark.parametrize("tname", ["Q2_K", "IQ2_XXS"])
 @pytest.mark.parametrize("tokens,k", [(4, 2304), (8, 2048), (8, 4096), (5, 256)])
 def test_split_x_one_launch_bit_identical(ctx, eff, orc, tname, tokens, k, split_from_4):
