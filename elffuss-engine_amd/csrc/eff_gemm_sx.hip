@@ -884,7 +884,7 @@ SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg, uint32_t ksl_opt)
   // measured (C5 shapes): 32 rows x 8 waves up to 32 tokens per tile group;
   // 64 rows x 4 waves for 64 once the token groups give it 256 workgroups
   // (M = 96, 128), else 32 x 8 again (M = 48, 64: 13.9 / 14.1 us against
-  // 19.2 / 19.4 for Q2_K); the k halves in two workgroups were slower at every M.
+  // 19.2 / 19.4 for Q2_K); two k slices over 64 x 4 were slower at every M.
   // Between one and two rounds of 64-row workgroups (one per CU), 32 x 8 fills
   // the second round better (M = 129 / 192: Q2_K 30.3 / 30.9 against 34.5 /
   // 35.1, Q4_K 31.8 / 32.4 against 34.2 / 35.0, IQ2_XXS 30.0 / 30.4 against
