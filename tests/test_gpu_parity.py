@@ -1341,3 +1341,49 @@ def test_read_floor_reads_and_checks_its_arguments(ctx, eff):
         assert e.value.code == code, args
     src.free()
     sink.free()
+
+
+# ---- router over seeded random shapes -----------------------------------------------------
+
+def _random_router_cases(n, seed=20261202):
+    rng = np.random.default_rng(seed)
+    types = ["Q8_0", "Q8_0R", "Q4_K", "Q6_K", "Q2_K", "IQ2_XXS"]
+    ks_256 = [256, 512, 768, 1280, 2304, 4096, 8448, 14336, 16384]
+    ks_32 = [32, 96, 544, 2080]
+    # (at least 3 rows: the bar's max |d| / ||row|| over a single output is its own relative error,
+    # which an f32-accurate sum need not keep below 1e-3 where the output cancels to near zero)
+    rows_l = [3, 7, 33, 100, 257, 600, 1500, 2048, 3000]
+    toks_l = [1, 2, 3, 4, 5, 6, 8, 9, 16, 33, 63, 64, 65, 100, 129, 200, 300]
+    cases = []
+    while len(cases) < n:
+        tname = types[rng.integers(len(types))]
+        kl = ks_256 + (ks_32 if tname in ("Q8_0", "Q8_0R") else [])
+        k, rows, tokens = kl[rng.integers(len(kl))], rows_l[rng.integers(len(rows_l))], toks_l[rng.integers(len(toks_l))]
+        if rows * k * tokens <= 40_000_000:
+            cases.append((tname, rows, k, tokens))
+    return cases
+
+
+@pytest.mark.parametrize("case", range(60))
+def test_router_random_shapes(ctx, eff, orc, case):
+    """60 seeded random (type, rows, k, tokens) through eff_qmatmul, whatever
+    path the router takes (the GEMVs, the token groups, the split-x product
+    with or without k slices, the fp16 GEMM with or without them): each meets
+    its oracle (the fp16-rounded one for Q8_0/Q8_0R from the GEMM's 64
+    tokens, f64 otherwise), and a second call gives the same bits."""
+    tname, rows, k, tokens = _random_router_cases(60)[case]
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 3000 + case)
+    x = eff.fill_normal(3100 + case, 1.0, tokens * k)
+    wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+    y0 = yb.read(np.uint32)
+    if tname in ("Q8_0", "Q8_0R") and tokens >= 64:
+        ref = orc.gemm_f16(orc.Q8_0, gguf, rows, k, x, tokens)
+    else:
+        ref = orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens)
+    check_close(y0.view(np.float32), ref, f"router {tname} rows={rows} k={k} M={tokens}")
+    yb.write(np.full(tokens * rows, 0x7FC00000, np.uint32))
+    ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+    assert np.array_equal(yb.read(np.uint32), y0)
+    for b in (wb, xb, yb):
+        b.free()
