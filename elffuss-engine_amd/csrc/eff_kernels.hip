@@ -647,17 +647,18 @@ template <int TYPE> constexpr int gemm_bk() { return TYPE == Q6_K ? 128 : 64; }
 
 // One thread per 8 halves of the output, laid out as [token tile][k step]
 // [BM tokens][BK k]: the x slice of one tile and k step is one contiguous
-// run of BM * BK halves. Tokens past `tokens` and k past `k` are zero.
+// run of BM * BK halves. Tokens past `tokens` and k past `k` are zero. The
+// grid's y dimension is the token tile (no division in the indexing, which
+// precedes the loads).
 __global__ __launch_bounds__(256) void k_x_to_f16(const float *__restrict__ x, _Float16 *__restrict__ xh,
                                                   uint32_t tokens, uint32_t k, uint32_t bm_log2, uint32_t bk_log2,
-                                                  uint32_t steps, uint64_t n8) {
-  const uint64_t o = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-  if (o >= n8) return;
-  const uint32_t per_blk = 1u << (bm_log2 + bk_log2 - 3u);   // half8 per (tile, step)
-  const uint64_t blk = o >> (bm_log2 + bk_log2 - 3u);
-  const uint32_t in = (uint32_t)(o & (per_blk - 1u));
+                                                  uint32_t steps) {
+  const uint32_t sh = bm_log2 + bk_log2 - 3u;                 // log2 of half8 per (tile, step)
+  const uint32_t ot = blockIdx.x * 256u + threadIdx.x, tile = blockIdx.y;
+  if (ot >= (steps << sh)) return;
+  const uint64_t o = ((uint64_t)tile * steps << sh) + ot;
+  const uint32_t st = ot >> sh, in = ot & ((1u << sh) - 1u);
   const uint32_t t = in >> (bk_log2 - 3u), c = in & ((1u << (bk_log2 - 3u)) - 1u);
-  const uint32_t tile = (uint32_t)(blk / steps), st = (uint32_t)(blk % steps);
   const uint32_t tok = (tile << bm_log2) + t, kk = (st << bk_log2) + 8u * c;
   half8 h = {};
   if (tok < tokens && kk < k) {   // k is a multiple of 32, so all 8 values exist
@@ -1055,10 +1056,11 @@ hipError_t launch_gemm_x(int type, const float *x, uint32_t tokens, uint32_t pla
   if (plan < tokens) return hipErrorInvalidValue;
   uint32_t bm, bk;
   gemm_x_tile(type, plan, k, rows, cfg, bm, bk);
-  const uint32_t steps = (k + (1u << bk) - 1) >> bk;
-  const uint64_t n8 = (uint64_t)gemm_x_bytes(type, tokens, plan, k, rows, cfg) / 16u;
-  hipLaunchKernelGGL(k_x_to_f16, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, s, x, (_Float16 *)xh, tokens, k,
-                     bm, bk, steps, n8);
+  const uint32_t steps = (k + (1u << bk) - 1) >> bk, tiles = (tokens + (1u << bm) - 1) >> bm;
+  const uint64_t per_tile = (uint64_t)steps << (bm + bk - 3u);   // half8 per token tile
+  if (per_tile >= (1ull << 32)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_x_to_f16, dim3((uint32_t)((per_tile + 255) / 256), tiles), dim3(256), 0, s, x,
+                     (_Float16 *)xh, tokens, k, bm, bk, steps);
   return hipGetLastError();
 }
 
