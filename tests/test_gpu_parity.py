@@ -1028,13 +1028,16 @@ def test_matmul_prepared_x_not_applicable_and_errors(ctx, eff):
 # ---- the reference CPU path's arithmetic (eff_qmatmul_cpu_path) ----------------------------
 
 @pytest.mark.parametrize("rows,k,tokens", [(77, 32, 1), (300, 2080, 3), (64, 4096, 65), (130, 2048, 7),
-                                           (33, 256, 130)])
+                                           (33, 256, 130), (77, 2080, 40), (33, 96, 16)])
 def test_cpu_path_product_bit_exact(ctx, eff, orc, rows, k, tokens):
     """The CPU path's arithmetic on the GPU gives the bits of the oracle's
     restatement of it (or_cpu_matmul: 8-bit x blocks, int32 block dots, the
-    f32 terms added in block order): more than 64 blocks per row (two
-    chunks), more than 64 tokens (two and three token chunks), block counts
-    that are not multiples of 64, rows that do not fill the last workgroup."""
+    f32 terms added in block order), below 16 tokens (a wave per row) and
+    from 16 (the block dots on the matrix cores, 8-block chunks staged in
+    LDS): more than 64 blocks per row, more than 64 tokens (two and three
+    token chunks), block counts that are not multiples of 64 or of 8 (a last
+    chunk of one block; 3 blocks in all), rows and tokens that do not fill
+    the last workgroup."""
     t, data, gguf, n = make_weights(eff, "Q8_0", rows, k, 1200 + rows + k + tokens)
     x = eff.fill_normal(1300 + rows + tokens, 1.0, tokens * k)
     wb, xb, yb = ctx.upload(data), ctx.upload(x), ctx.alloc(tokens * rows * 4)
