@@ -22,7 +22,10 @@ const native = require(path.join(__dirname, 'elffuss_amd.node'));
 const muestreo = require(path.join(__dirname, 'muestreo.js'));
 
 const STATUS = { NOT_APPLICABLE: 1, E_INVALID: -1, E_TYPE: -2, E_SHAPE: -3, E_MARK: -4, E_BOUNDS: -5, E_DEVICE: -6 };
-const OPT = { GEMV_MAX_TOKENS: 1, GEMM_MIN_TOKENS: 2, GEMV_KERNEL: 3, SPLIT_CONFIG: 4 };
+const OPT = {
+  GEMV_MAX_TOKENS: 1, GEMM_MIN_TOKENS: 2, GEMV_KERNEL: 3, SPLIT_CONFIG: 4,
+  SPLIT_MIN_TOKENS: 5, GEMM_CONFIG: 6, GEMM_SPLIT: 7, SPLIT_SLICES: 8,
+};
 const GEMV_MODE = { SECTIONS: 1, SWIGLU: 2 };
 const TOPK = { M_MAX: 192, P_MAX: 128, CAP: 256, CABECERA: 8, N_MAX: 1 << 24, POR_TROZO: 4096 };
 
@@ -74,7 +77,7 @@ function requestDevice(opts) {
   const device = {
     _ctx: ctx,
     // the library's defaults (include/elffuss_amd.h); setOption keeps this in step
-    _opts: { 1: 8, 2: 64, 3: 0, 4: 0 },
+    _opts: { 1: 8, 2: 64, 3: 0, 4: 0, 5: 0, 6: 0, 7: 0, 8: 0 },
     features: new Set(['shader-f16']),
     limits: { maxStorageBufferBindingSize: 2 ** 32, maxComputeWorkgroupStorageSize: 163840 },
     createBuffer(desc) {
