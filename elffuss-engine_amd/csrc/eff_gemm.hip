@@ -5,7 +5,7 @@
 // ops.gemm2.js).
 //
 // A workgroup of 4 waves (one per SIMD) computes a BM-token x BN-row tile
-// (64 x 128 to 256 x 256, chosen by the token count: gemm_q8_choice); the
+// (64 x 128 to 256 x 256, chosen by an estimate of each one's time: big_plan); the
 // waves are WM along tokens x 4 / WM along rows, each over (BM / WM / 32) x
 // (BN / (4 / WM) / 32) fragments of v_mfma_f32_32x32x16_f16 (256
 // accumulators for 256 x 256). Each A fragment is read once per k slot and
@@ -462,45 +462,69 @@ hipError_t gemm_q8_go(const WeightView &wv, const _Float16 *xh, float *y, uint32
   return hipGetLastError();
 }
 
-// Tile configurations: tokens x rows per workgroup, waves along tokens, LDS
-// stages. cfg 0 chooses by the plan's token count (C3 shape, 8192 x 2048,
-// us per launch with the x conversion): 64 x 128 with 4 stages below 384
-// tokens (two workgroups per CU; M = 256: 23.8 against 30.5 for 128 x 128);
-// 128 x 128 with 6 stages below 768 (M = 512: 34.5 against 35.3 with 3
-// stages); 128 x 128 with 3 stages (two workgroups per CU) below 1536
-// (M = 1024: 55.2 against 66.5 for 256 x 256); 256 x 256 from 1536 (M = 2048:
-// 83.9 against 98.9 for 256 x 128 and 106 for 128 x 128).
-uint32_t gemm_q8_choice(uint32_t plan) {
-  if (plan < 384) return 4u;
-  if (plan < 768) return 3u;
-  if (plan < 1536) return 2u;
-  return 1u;
-}
+// Tile configurations (tokens x rows per workgroup, waves along tokens, LDS
+// stages): 1: 256 x 256, 1, 3; 2: 128 x 128, 1, 3; 3: 128 x 128, 1, 6;
+// 4: 64 x 128, 1, 4; 5: 128 x 256, 1, 4; 6: 256 x 128, 2, 3. Configurations
+// 2 and 4 fit two workgroups per CU, the others one.
+uint32_t cfg_bm(uint32_t c) { return c == 1u || c == 6u ? 256u : c == 4u ? 64u : 128u; }
+uint32_t cfg_bn(uint32_t c) { return c == 1u || c == 5u ? 256u : 128u; }
 
 uint32_t cfg_tiles(uint32_t c, uint32_t plan, uint32_t rows) {
-  const uint32_t bm = c == 1 || c == 6 ? 256u : c == 4 ? 64u : 128u, bn = c == 1 || c == 5 ? 256u : 128u;
-  return ((plan + bm - 1u) / bm) * ((rows + bn - 1u) / bn);
+  return ((plan + cfg_bm(c) - 1u) / cfg_bm(c)) * ((rows + cfg_bn(c) - 1u) / cfg_bn(c));
 }
 
-// Tiles and k slices. Few rows leave CUs without a tile (2048 rows, 512
-// tokens: 64 tiles of 128 x 128 on 256 CUs): 256 x 256 tiles give way to
-// 128 x 128 below 256 tiles (their slices' sums would not fit the registers
-// beside the accumulators: 2048 x 8192, 2048 tokens, us: 256 x 256 in 4
-// slices 290, 128 x 128 unsliced 111), and below 192 tiles k is cut into
-// slices of at least 8 steps, about 256 workgroups in all (2048 x 8192, us
-// against unsliced: 129 tokens 25.9 / 68.4, 256 29.1 / 68.1, 512 44.2 /
-// 85.5, 1024 66.0 / 95.5; 4096 x 4096, 512 tokens 41.9 / 49.5). The slices
-// follow the automatic tiles, also under a forced configuration, so that
-// every configuration sums each output in the same order.
+// k slices for t tiles of configuration c: none from 192 tiles, else about
+// 256 workgroups in all with slices of 8 steps at least; 256 x 256 tiles take
+// none (their slices' sums do not fit the registers beside the 256
+// accumulators: 2048 x 8192, 2048 tokens, us: in 4 slices 290, 128 x 128
+// unsliced 111). 2048 x 8192, us against unsliced: 129 tokens 25.9 / 68.4,
+// 256 29.1 / 68.1, 512 44.2 / 85.5, 1024 66.0 / 95.5.
+uint32_t cfg_slices(uint32_t c, uint32_t t, uint32_t steps) {
+  return c != 1u && t < 192u ? min((256u + t / 2u) / t, max(steps / 8u, 1u)) : 1u;
+}
+
+// Estimated us of one launch of configuration c in ksl slices. A CU holds
+// n = ceil(workgroups / 256) of them; a workgroup's time is linear in its k
+// steps, alone on its CU or, where two fit, as a pair. The coefficients are a
+// least-squares fit (8% rms error) to 1,100 timed launches: every
+// configuration and slice count at 15 shapes from 1024 x 4096 to 65536 x 2048
+// and 64 to 2048 tokens. Choosing by it, against the token-count rule it
+// replaces (us with the x conversion): 65536 x 2048 at 256 / 512 tokens
+// 139 / 229 -> 85 / 158, 14336 x 4096 at 256 / 1024 65 / 167 -> 53 / 134,
+// 8192 x 8192 at 256 72 -> 61; 0.6% above the best configuration of each
+// shape summed over the sweep (measured again with this choice), the rule
+// 11.5%.
+double cfg_cost(uint32_t c, uint32_t plan, uint32_t rows, uint32_t steps, uint32_t ksl) {
+  static const double one[7][2] = {{0, 0}, {22.9, 1.47}, {6.85, 0.686}, {7.73, 0.643},
+                                   {3.46, 0.534}, {13.5, 1.04}, {13.2, 1.01}};
+  static const double two[7][2] = {{0, 0}, {0, 0}, {6.76, 1.19}, {0, 0}, {3.23, 0.871}, {0, 0}, {0, 0}};
+  const uint32_t per = (steps + ksl - 1u) / ksl;
+  ksl = (steps + per - 1u) / per;
+  const uint64_t n = ((uint64_t)cfg_tiles(c, plan, rows) * ksl + 255u) / 256u;
+  const double single = one[c][0] + one[c][1] * per;
+  double t = two[c][0] > 0 ? (double)(n / 2u) * (two[c][0] + two[c][1] * per) + (double)(n % 2u) * single
+                           : (double)n * single;
+  if (ksl > 1u) t += 6.2 + 2.15e-6 * plan * rows * (ksl - 1u);
+  return t;
+}
+
 struct BigPlan {
   uint32_t cfg, ksl, per;
 };
 
+// The automatic configuration is the one of least estimated time, with its
+// slices; the slice count follows the automatic choice also under a forced
+// configuration, so that every configuration sums each output in the same
+// order (the same bits).
 BigPlan big_plan(uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg, uint32_t ksl_opt) {
-  uint32_t c = gemm_q8_choice(plan);
-  if (c == 1u && cfg_tiles(1u, plan, rows) < 256u) c = 2u;
-  const uint32_t steps = (k + kBK - 1u) / kBK, t = cfg_tiles(c, plan, rows);
-  const uint32_t ksl_auto = t < 192u ? min((256u + t / 2u) / t, max(steps / 8u, 1u)) : 1u;
+  const uint32_t steps = (k + kBK - 1u) / kBK;
+  uint32_t c = 0u, ksl_auto = 1u;
+  double best = 0;
+  for (uint32_t i = 1u; i <= 6u; ++i) {
+    const uint32_t sl = cfg_slices(i, cfg_tiles(i, plan, rows), steps);
+    const double t = cfg_cost(i, plan, rows, steps, sl);
+    if (c == 0u || t < best) c = i, best = t, ksl_auto = sl;
+  }
   BigPlan b;
   b.cfg = cfg >= 1u && cfg <= 6u ? cfg : c;
   // 256 x 256 tiles take no k slices: where the automatic choice slices k
@@ -540,8 +564,7 @@ size_t gemm_big_scratch_bytes(uint32_t tokens, uint32_t plan, uint32_t k, uint32
                               uint32_t ksl_opt) {
   const BigPlan b = big_plan(plan, k, rows, cfg, ksl_opt);
   if (b.ksl < 2u) return 0;
-  const uint32_t bm = b.cfg == 1 || b.cfg == 6 ? 256u : b.cfg == 4 ? 64u : 128u;
-  const uint32_t bn = b.cfg == 1 || b.cfg == 5 ? 256u : 128u;
+  const uint32_t bm = cfg_bm(b.cfg), bn = cfg_bn(b.cfg);
   const uint64_t tiles = (uint64_t)((tokens + bm - 1u) / bm) * ((rows + bn - 1u) / bn);
   return kCntBytes + (size_t)(tiles * b.ksl * bm * bn * 4u);
 }

@@ -287,8 +287,9 @@ def test_gemm_q8_0_tile_configs_same_bits(ctx, eff, orc, tokens, k):
 def test_gemm_q8_0_k_slices(ctx, eff, orc, tokens, k):
     """Few rows and a long k: the tiles leave CUs idle and k is cut into
     slices over workgroups (25 tiles of 64 x 128 at 300 tokens: 8 slices;
-    4064 ends in half a step inside the last slice; at 1600 tokens 21 tiles
-    of 256 x 256 take 33 steps in slices of 9, the last shorter). The last workgroup of a tile adds the slices in slice order:
+    4064 ends in half a step inside the last slice; at 1600 tokens 125 tiles
+    of 64 x 128 take 33 steps in slices of 17 and 16). The last workgroup of
+    a tile adds the slices in slice order:
     every tile configuration gives the automatic choice's bits, a second call
     the same bits (the arrival counters start from zero again), and forced
     slice counts (EFF_OPT_GEMM_SPLIT) stay within the fp16 oracle's bound."""
