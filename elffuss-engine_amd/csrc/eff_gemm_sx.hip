@@ -881,18 +881,27 @@ void sx_tiles(int type, uint32_t tokens, uint32_t &tt, uint32_t &groups) {
 SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg, uint32_t ksl_opt) {
   SxPlan p;
   sx_tiles(wv.type, tokens, p.tt, p.groups);
-  // measured (C5 shapes): 32 rows x 8 waves up to 32 tokens per tile group;
-  // 64 rows x 4 waves for 64 once the token groups give it 256 workgroups
-  // (M = 96, 128), else 32 x 8 again (M = 48, 64: 13.9 / 14.1 us against
-  // 19.2 / 19.4 for Q2_K); two k slices over 64 x 4 were slower at every M.
-  // Between one and two rounds of 64-row workgroups (one per CU), 32 x 8 fills
-  // the second round better (M = 129 / 192: Q2_K 30.3 / 30.9 against 34.5 /
-  // 35.1, Q4_K 31.8 / 32.4 against 34.2 / 35.0, IQ2_XXS 30.0 / 30.4 against
-  // 31.6 / 32.4); from two rounds 64 x 4 again (M = 640: Q2_K 81.0 against
-  // 89.1; M = 320 and 448 within 3 % either way).
-  const uint32_t rt64 = (wv.rows + 63u) / 64u, w64 = p.groups * rt64;
+  // 32 rows x 8 waves, or 64 x 4 (the types of up to 4 token tiles, from 9
+  // tokens) where its estimated time is lower: a CU takes ceil(w / 256)
+  // workgroups of either kind, one of 64 x 4 costing 1.75 of one of 32 x 8
+  // (the rows of two at a higher rate: 0.87-0.92 of the time where both fill
+  // whole rounds), 40% more times the fraction of idle CUs below 256. On 9
+  // shapes from 6144 x 4096 to 32768 x 2048, 9 to 384 tokens (Q2_K, Q4_K)
+  // the choice is 0.1% above the faster of the two summed, the rule before
+  // (64 x 4 only for 4 token tiles and 256 or from 512 of its workgroups)
+  // 2.6%; us, before / now: 28672 x 4096 at 16 tokens Q4_K 38.0 / 30.2,
+  // 14336 x 4096 at 128 69.6 / 60.2, 11008 x 4096 at 64 39.3 / 33.2, 10240
+  // x 2048 at 192 40.0 / 36.4. Q4_K at 2 token tiles and IQ2_XXS at one stay
+  // on 32 x 8 (64 x 4 4-10% slower at every measured shape); 8 or fewer
+  // tokens too (the one-launch product). Two k slices over 64 x 4 were slower
+  // at every M.
+  const uint32_t gr = p.groups, w32 = gr * ((wv.rows + 31u) / 32u), w64 = gr * ((wv.rows + 63u) / 64u);
+  const double t32 = (double)((w32 + 255u) / 256u),
+               t64 = 1.75 * (double)((w64 + 255u) / 256u) * (1.0 + (w64 < 256u ? 0.4 * (1.0 - w64 / 256.0) : 0.0));
+  const bool wide = sx_tt_max(wv.type) == 4u && tokens > 8u && !(wv.type == Q4_K && p.tt == 2u) &&
+                    !(wv.type == IQ2_XXS && p.tt == 1u) && t64 < t32;
   // cfg 3 (forced): 64 x 4 in two k slices
-  p.cfg = cfg ? (cfg == 3 ? 1u : (uint32_t)(cfg - 1)) : (p.tt == 4u && w64 >= 256u && !(w64 > 256u && w64 < 512u) ? 1u : 0u);
+  p.cfg = cfg ? (cfg == 3 ? 1u : (uint32_t)(cfg - 1)) : wide ? 1u : 0u;
   const uint32_t rows_per = p.cfg ? 64u : 32u, nw = p.cfg ? 4u : 8u, nb = wv.k / 256u;
   p.row_tiles = (wv.rows + rows_per - 1u) / rows_per;
   // Below 192 workgroups (few rows: 2048 rows are 64 tiles of 32), k slices
