@@ -1,5 +1,5 @@
-// Prefill GEMM for Q8_0 (and Q8_0R) weights from 129 tokens (from 64 below
-// 6144 rows):
+// Prefill GEMM for Q8_0 (and Q8_0R) weights from 64 tokens (at every token
+// count below 6144 rows):
 //   Y[t][row] = sum_k fp16(W[row][k]) fp16(X[t][k]), fp32 accumulation
 // (the operand roundings of kernels.drift.wgsl.js:65-142 and the f16 tiles of
 // ops.gemm2.js).
@@ -539,17 +539,19 @@ BigPlan big_plan(uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg, uint32_
 
 }  // namespace
 
-// From 129 tokens: up to 128 the general kernel's one 128-token tile is as
-// fast or faster (C3 shape, us with the conversion, general / this kernel:
-// Q8_0 64 tokens 21.5 / 22.8, 128 22.0 / 22.5; Q8_0R 19.9 / 23.3, 20.5 / 23.0),
-// and from 129 it needs two (160 tokens 39.3 / 22.7, 255 40.1 / 23.7). Below
-// 6144 rows the general kernel's 32-row tiles are fewer than 192 workgroups,
-// and this kernel's k slices fill the CUs from 64 tokens (us, 64 / 128 tokens,
-// general against this kernel: 2048 x 8192 54.3 / 54.8 against 22.5 / 22.3,
-// 4096 x 14336 86.0 / 86.6 against 31.0 / 42.4, 4096 x 4096 32.6 / 33.0
-// against 18.7 / 20.8, 2048 x 2048 21.1 / 21.4 against 14.0 / 15.3).
+// From the GEMM's threshold (64 tokens) at every row count, and at any token
+// count below 6144 rows (where the general kernel's 32-row tiles are fewer
+// than 192 workgroups). With the tiles and k slices of big_plan this kernel is
+// the faster from 64 tokens (us, 64 / 128 tokens, general kernel against this
+// one: 8192 x 2048 22.2 / 22.7 against 16.9 / 18.9, 14336 x 4096 60.9 / 62.2
+// against 28.9 / 40.9, 65536 x 2048 140.5 / 144.5 against 48.6 / 60.6, 8192 x
+// 8192 54.8 / 56.1 against 31.3 / 40.2; below 6144 rows: 2048 x 8192 54.3 /
+// 54.8 against 22.5 / 22.3, 4096 x 14336 86.0 / 86.6 against 31.0 / 42.4).
+// Before big_plan estimated each configuration's time, the general kernel's
+// one 128-token tile was as fast up to 128 tokens at 8192 x 2048 (21.5 / 22.0
+// against 22.8 / 22.5), and this kernel took over only from 129 there.
 bool gemm_big_applies(int type, uint32_t tokens, uint32_t k, uint32_t rows) {
-  return (type == Q8_0 || type == Q8_0R) && (tokens > 128 || (rows + 31u) / 32u < 192u) && k % 32u == 0;
+  return (type == Q8_0 || type == Q8_0R) && (tokens >= 64u || (rows + 31u) / 32u < 192u) && k % 32u == 0;
 }
 
 uint32_t gemm_big_tile_log2(uint32_t plan, uint32_t k, uint32_t rows, uint32_t cfg) {

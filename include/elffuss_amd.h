@@ -58,7 +58,7 @@ extern "C" {
 #define EFF_OPT_SPLIT_MIN_TOKENS 5  /* Q2_K, Q4_K, IQ2_XXS, Q8_0, Q6_K: tokens >= this run the split-x product, fewer
                                        the int8 matrix-core GEMVs (0: automatic, 5 for Q2_K and IQ2_XXS, 9 for the
                                        others (default); else >= 4). Q8_0 only below EFF_OPT_GEMM_MIN_TOKENS */
-#define EFF_OPT_GEMM_CONFIG      6  /* Q8_0 GEMM from 129 tokens (below 6144 rows from the GEMM's threshold),
+#define EFF_OPT_GEMM_CONFIG      6  /* Q8_0 GEMM from the GEMM's threshold (below 6144 rows at every count),
                                        tiles (tuning; tokens x rows, waves along tokens x rows, LDS stages):
                                        0 automatic (default), 1: 256x256 1x4 3, 2: 128x128 1x4 3,
                                        3: 128x128 1x4 6, 4: 64x128 1x4 4, 5: 128x256 1x4 4, 6: 256x128 2x2 3; every
