@@ -891,15 +891,20 @@ SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg, uint32_t ksl_opt)
   // (64 x 4 only for 4 token tiles and 256 or from 512 of its workgroups)
   // 2.6%; us, before / now: 28672 x 4096 at 16 tokens Q4_K 38.0 / 30.2,
   // 14336 x 4096 at 128 69.6 / 60.2, 11008 x 4096 at 64 39.3 / 33.2, 10240
-  // x 2048 at 192 40.0 / 36.4. Q4_K at 2 token tiles and IQ2_XXS at one stay
-  // on 32 x 8 (64 x 4 4-10% slower at every measured shape); 8 or fewer
-  // tokens too (the one-launch product). Two k slices over 64 x 4 were slower
-  // at every M.
+  // x 2048 at 192 40.0 / 36.4. IQ2_XXS weighs 64 x 4 at 1.9 (at one token
+  // tile it was 5% slower at 11008 and 14336 rows, 1.2-1.4x faster from 32000);
+  // Q4_K at 2 token tiles stays on 32 x 8 (64 x 4 7-10% slower at every
+  // measured shape), and so does Q4_K at 8 or fewer tokens. At 5-8 tokens
+  // Q2_K and IQ2_XXS take 64 x 4 by the same estimate (us, 5 tokens, the
+  // one-launch product before / now: Q2_K 65536 x 2048 49.2 / 25.7, 32000 x
+  // 4096 41.5 / 26.1; IQ2_XXS 50.8 / 27.4, 42.0 / 26.7). Two k slices over
+  // 64 x 4 were slower at every M.
   const uint32_t gr = p.groups, w32 = gr * ((wv.rows + 31u) / 32u), w64 = gr * ((wv.rows + 63u) / 64u);
   const double t32 = (double)((w32 + 255u) / 256u),
-               t64 = 1.75 * (double)((w64 + 255u) / 256u) * (1.0 + (w64 < 256u ? 0.4 * (1.0 - w64 / 256.0) : 0.0));
-  const bool wide = sx_tt_max(wv.type) == 4u && tokens > 8u && !(wv.type == Q4_K && p.tt == 2u) &&
-                    !(wv.type == IQ2_XXS && p.tt == 1u) && t64 < t32;
+               t64 = (wv.type == IQ2_XXS ? 1.9 : 1.75) * (double)((w64 + 255u) / 256u) *
+                     (1.0 + (w64 < 256u ? 0.4 * (1.0 - w64 / 256.0) : 0.0));
+  const bool wide = sx_tt_max(wv.type) == 4u && (tokens > 8u || wv.type != Q4_K) &&
+                    !(wv.type == Q4_K && p.tt == 2u) && t64 < t32;
   // cfg 3 (forced): 64 x 4 in two k slices
   p.cfg = cfg ? (cfg == 3 ? 1u : (uint32_t)(cfg - 1)) : wide ? 1u : 0u;
   const uint32_t rows_per = p.cfg ? 64u : 32u, nw = p.cfg ? 4u : 8u, nb = wv.k / 256u;
@@ -955,8 +960,14 @@ hipError_t sx_cfg(const WeightView &wv, const uint8_t *xa, const float *xp, floa
 
 // Up to 8 tokens of Q2_K / IQ2_XXS with the automatic plan: one launch, each
 // wave preparing its own block's x.
-bool sx_fx(int type, uint32_t tokens, int cfg, const SxPlan &p) {
-  return (type == Q2_K || type == IQ2_XXS) && cfg == 0 && tokens <= 8u && p.cfg == 0u && p.ksl == 1u;
+// The one-launch product repeats the preparation of x in every workgroup: it
+// saves the preparation's launch where the workgroups times k stay within
+// 256 x 2048 (us, 5 tokens, one launch against two: 8192 x 2048 Q2_K 7.8 /
+// 8.6; 8192 x 8192 20.5 / 18.2, IQ2_XXS 21.6 / 18.1; 16384 x 2048 IQ2_XXS
+// 14.3 / 12.5; 6144 x 4096 11.6 / 11.3).
+bool sx_fx(int type, uint32_t tokens, int cfg, const SxPlan &p, uint32_t k) {
+  return (type == Q2_K || type == IQ2_XXS) && cfg == 0 && tokens <= 8u && p.cfg == 0u && p.ksl == 1u &&
+         (uint64_t)p.row_tiles * p.groups * k <= 256ull * 2048u;
 }
 
 // The product from x prepared in `xa` for `tiles` token tiles (at least the
@@ -979,7 +990,7 @@ hipError_t sx_type(const WeightView &wv, const float *x, float *y, uint32_t toke
                    uint32_t ksl_opt, void *sk, hipStream_t s) {
   const SxPlan p = sx_plan(wv, tokens, cfg, ksl_opt);
   if constexpr (TYPE == Q2_K || TYPE == IQ2_XXS)
-    if (sx_fx(TYPE, tokens, cfg, p)) return sx_go_fx<TYPE>(wv, x, y, tokens, p, s);
+    if (sx_fx(TYPE, tokens, cfg, p, wv.k)) return sx_go_fx<TYPE>(wv, x, y, tokens, p, s);
   const uint32_t tiles = p.groups * p.tt, nb = wv.k / 256u;   // blocks of 256 weights
   uint8_t *xa = scratch;
   float *xp = (float *)(scratch + (uint64_t)tiles * nb * sx_slots<TYPE>() * 1024u);
@@ -1011,14 +1022,14 @@ size_t sx_x_bytes(int type, uint32_t tokens, uint32_t k) {
 
 size_t sx_sk_bytes(const WeightView &wv, uint32_t tokens, int cfg, uint32_t ksl_opt) {
   const SxPlan p = sx_plan(wv, tokens, cfg, ksl_opt);
-  if (p.ksl < 2u || sx_fx(wv.type, tokens, cfg, p)) return 0;
+  if (p.ksl < 2u || sx_fx(wv.type, tokens, cfg, p, wv.k)) return 0;
   const uint64_t ne = (uint64_t)p.tt * (p.cfg ? 2u : 1u) * 512u;   // sums per workgroup
   return kSliceCntBytes + (size_t)((uint64_t)p.row_tiles * p.groups * p.ksl * ne * 4u);
 }
 
 uint32_t sx_x_layout(const WeightView &wv, uint32_t tokens, int cfg, uint32_t ksl_opt) {
   const SxPlan p = sx_plan(wv, tokens, cfg, ksl_opt);
-  if (sx_fx(wv.type, tokens, cfg, p)) return 0u;
+  if (sx_fx(wv.type, tokens, cfg, p, wv.k)) return 0u;
   switch (wv.type) {
     case Q2_K: return kSxLayout | 1u;
     case Q4_K: return kSxLayout | 2u;

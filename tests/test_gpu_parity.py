@@ -731,10 +731,11 @@ def test_split_x_k_slices_graph_replays(ctx, eff, orc):
 
 
 @pytest.mark.parametrize("tname", ["Q2_K", "IQ2_XXS"])
-@pytest.mark.parametrize("tokens,k", [(4, 2304), (8, 2048), (8, 4096), (5, 256)])
+@pytest.mark.parametrize("tokens,k", [(4, 2304), (8, 2048), (8, 2560), (5, 256)])
 def test_split_x_one_launch_bit_identical(ctx, eff, orc, tname, tokens, k, split_from_4):
     """Up to 8 tokens of Q2_K / IQ2_XXS the product prepares x itself (one
-    launch, where the rows give 192 workgroups or more and so no k slices);
+    launch, where the rows give 192 workgroups or more and so no k slices, and
+    the workgroups times k stay within 256 x 2048);
     the same 32 x 8 plan with the preparation launch (EFF_OPT_SPLIT_CONFIG =
     1) gives the same bits, and both meet the f64 bar (one and two blocks per
     wave, a single block per row)."""
@@ -755,6 +756,36 @@ def test_split_x_one_launch_bit_identical(ctx, eff, orc, tname, tokens, k, split
     assert np.array_equal(got[0], got[1])
     check_close(got[0].view(np.float32), orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens),
                 f"split-x one launch {tname} M={tokens} k={k}")
+    wb.free()
+    xb.free()
+
+
+@pytest.mark.parametrize("tname", ["Q2_K", "IQ2_XXS"])
+@pytest.mark.parametrize("tokens", [5, 8])
+def test_split_x_few_tokens_wide_grid(ctx, eff, orc, tname, tokens, split_from_4):
+    """At 5-8 tokens over many rows (32000: 1000 workgroups of 32 rows) the
+    product runs 64 rows x 4 waves with x prepared by its own launch, not the
+    one-launch product: the forced 64 x 4 plan gives the same bits, the x
+    layout answers (no NOT_APPLICABLE), and the f64 bar holds."""
+    rows, k = 32000, 512
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 520 + tokens)
+    x = eff.fill_normal(5200 + tokens, 1.0, tokens * k)
+    wb, xb = ctx.upload(data), ctx.upload(x)
+    nbytes, lay = ctx.qmatmul_x_layout(t, rows, k, tokens)
+    assert lay >= 0x100 and nbytes > 0
+    got = []
+    for cfg in (0, 2):
+        yb = ctx.alloc(tokens * rows * 4)
+        ctx.set_option(eff.OPT_SPLIT_CONFIG, cfg)
+        try:
+            ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+        finally:
+            ctx.set_option(eff.OPT_SPLIT_CONFIG, 0)
+        got.append(yb.read(np.uint32))
+        yb.free()
+    assert np.array_equal(got[0], got[1])
+    check_close(got[0].view(np.float32), orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens),
+                f"split-x 64 x 4 {tname} M={tokens} rows={rows}")
     wb.free()
     xb.free()
 
@@ -984,8 +1015,8 @@ def test_matmul_prepared_x_not_applicable_and_errors(ctx, eff):
     configuration that prepares x (also one with k in two slices) gives
     eff_qmatmul's bits; a short buffer is refused."""
     k = 2304
-    # (the one-launch product over 8192 rows: 256 workgroups, no k slices)
-    for tname, r, kk, tokens in [("Q2_K", 64, k, 4), ("Q2_K", 8192, k, 8), ("IQ2_XXS", 8192, k, 5),
+    # (the one-launch product over 8192 rows: 256 workgroups, no k slices, k = 2048)
+    for tname, r, kk, tokens in [("Q2_K", 64, k, 4), ("Q2_K", 8192, 2048, 8), ("IQ2_XXS", 8192, 2048, 5),
                                  ("Q4_K", 64, k, 8), ("Q8_0R", 64, 2080, 33), ("Q8_0", 64, 2080, 33)]:
         with pytest.raises(eff.NotApplicable):
             ctx.qmatmul_x_layout(eff.TYPES[tname], r, kk, tokens)
