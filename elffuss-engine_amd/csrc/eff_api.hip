@@ -257,6 +257,13 @@ bool sx_routes(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens) {
   if (router_gemm_type(wv.type) && (int64_t)tokens >= ctx->gemm_min_tokens) return false;
   if (ctx->gemv_kernel != 0 || !sx_applies(wv, tokens)) return false;
   if ((int64_t)tokens >= lo) return true;
+  // Q4_K from 7 tokens where k >= 4096, from 5120 rows (us, 7 / 8 tokens,
+  // the 16-row GEMV against the split-x product: 5120 x 5120 30.3 / 31.2
+  // against 18.4, 6144 x 4096 17.3 / 17.9 against 12.7, 14336 x 4096 23.1 /
+  // 23.7 against 19.4 / 19.6, 11008 x 4096 22.7 / 23.2 against 18.7, 32000 x
+  // 4096 34.5 / 37.3 against 30.0 / 30.2; at 4096 x 4096, 65536 x 2048 and
+  // 8192 x 2048 the GEMV stays faster: 10.0 / 10.3 against 10.6 at 4096 x 4096)
+  if (wv.type == Q4_K && !ctx->sx_min_tokens && tokens >= 7u && wv.k >= 4096u && wv.rows >= 5120u) return true;
   GemvPlan p;
   return !gemv_rows_applies(wv, tokens) && !(mt_routes(tokens) && gemv_mt_plan(wv, tokens, p)) &&
          !gemv_mx_plan(wv, tokens, p);

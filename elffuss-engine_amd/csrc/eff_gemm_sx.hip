@@ -894,16 +894,16 @@ SxPlan sx_plan(const WeightView &wv, uint32_t tokens, int cfg, uint32_t ksl_opt)
   // x 2048 at 192 40.0 / 36.4. IQ2_XXS weighs 64 x 4 at 1.9 (at one token
   // tile it was 5% slower at 11008 and 14336 rows, 1.2-1.4x faster from 32000);
   // Q4_K at 2 token tiles stays on 32 x 8 (64 x 4 7-10% slower at every
-  // measured shape), and so does Q4_K at 8 or fewer tokens. At 5-8 tokens
-  // Q2_K and IQ2_XXS take 64 x 4 by the same estimate (us, 5 tokens, the
-  // one-launch product before / now: Q2_K 65536 x 2048 49.2 / 25.7, 32000 x
-  // 4096 41.5 / 26.1; IQ2_XXS 50.8 / 27.4, 42.0 / 26.7). Two k slices over
-  // 64 x 4 were slower at every M.
+  // measured shape), and so does Q4_K at 8 or fewer tokens below k = 4096.
+  // At 5-8 tokens Q2_K and IQ2_XXS take 64 x 4 by the same estimate (us, 5
+  // tokens, the one-launch product before / now: Q2_K 65536 x 2048 49.2 /
+  // 25.7, 32000 x 4096 41.5 / 26.1; IQ2_XXS 50.8 / 27.4, 42.0 / 26.7). Two k
+  // slices over 64 x 4 were slower at every M.
   const uint32_t gr = p.groups, w32 = gr * ((wv.rows + 31u) / 32u), w64 = gr * ((wv.rows + 63u) / 64u);
   const double t32 = (double)((w32 + 255u) / 256u),
                t64 = (wv.type == IQ2_XXS ? 1.9 : 1.75) * (double)((w64 + 255u) / 256u) *
                      (1.0 + (w64 < 256u ? 0.4 * (1.0 - w64 / 256.0) : 0.0));
-  const bool wide = sx_tt_max(wv.type) == 4u && (tokens > 8u || wv.type != Q4_K) &&
+  const bool wide = sx_tt_max(wv.type) == 4u && (tokens > 8u || wv.type != Q4_K || wv.k >= 4096u) &&
                     !(wv.type == Q4_K && p.tt == 2u) && t64 < t32;
   // cfg 3 (forced): 64 x 4 in two k slices
   p.cfg = cfg ? (cfg == 3 ? 1u : (uint32_t)(cfg - 1)) : wide ? 1u : 0u;
