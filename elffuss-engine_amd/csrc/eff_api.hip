@@ -262,8 +262,15 @@ bool sx_routes(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens) {
   // against 18.4, 6144 x 4096 17.3 / 17.9 against 12.7, 14336 x 4096 23.1 /
   // 23.7 against 19.4 / 19.6, 11008 x 4096 22.7 / 23.2 against 18.7, 32000 x
   // 4096 34.5 / 37.3 against 30.0 / 30.2; at 4096 x 4096, 65536 x 2048 and
-  // 8192 x 2048 the GEMV stays faster: 10.0 / 10.3 against 10.6 at 4096 x 4096)
-  if (wv.type == Q4_K && !ctx->sx_min_tokens && tokens >= 7u && wv.k >= 4096u && wv.rows >= 5120u) return true;
+  // 8192 x 2048 the GEMV stays faster: 10.0 / 10.3 against 10.6 at 4096 x 4096).
+  // Q6_K too (us, 7 / 8 tokens: 5120 x 5120 37.8 / 38.6 against 26.3, 6144 x
+  // 4096 22.3 / 22.9 against 16.6 / 16.7, 14336 x 4096 32.7 / 32.9 against
+  // 29.4, 24576 x 4096 47.4 / 48.4 against 42.4; where the GEMV's row tiles
+  // fill the CUs evenly it is faster: 16384 x 4096 26.2 / 27.1 against 30.0,
+  // 32000 x 4096 51.4 against 53.8)
+  if ((wv.type == Q4_K || wv.type == Q6_K) && !ctx->sx_min_tokens && tokens >= 7u && wv.k >= 4096u &&
+      wv.rows >= 5120u)
+    return true;
   GemvPlan p;
   return !gemv_rows_applies(wv, tokens) && !(mt_routes(tokens) && gemv_mt_plan(wv, tokens, p)) &&
          !gemv_mx_plan(wv, tokens, p);
