@@ -390,6 +390,36 @@ def test_set_stream_orders_after_the_previous_stream(ctx, eff):
             b.free()
 
 
+@pytest.mark.parametrize("tokens", [64, 100, 128])
+def test_gemm_q8_0_from_64_tokens_over_many_rows(ctx, eff, orc, tokens):
+    """From 64 tokens the router runs the tiled Q8_0 GEMM at every row count
+    (6200 rows: the general kernel's 32-row tiles would be 194 workgroups):
+    the fp16 oracle's values, Q8_0R's bits equal to Q8_0's, and every forced
+    tile configuration the automatic choice's bits; k ends in half a step."""
+    rows, k = 6200, 2080
+    _, data, gguf, n = make_weights(eff, "Q8_0R", rows, k, 880 + tokens)
+    x = eff.fill_normal(881 + tokens, 1.0, tokens * k)
+    wq, wr = ctx.upload(gguf), upload_w(ctx, eff, "Q8_0R", data, n)
+    xb, y0, y1 = ctx.upload(x), ctx.alloc(tokens * rows * 4), ctx.alloc(tokens * rows * 4)
+    before = ctx.stats()
+    ctx.qmatmul(eff.Q8_0, wq, xb, y0, rows, k, tokens)
+    assert ctx.stats()["gemm"] == before["gemm"] + 1
+    ref = y0.read(np.uint32)
+    check_close(ref.view(np.float32), orc.gemm_f16(orc.Q8_0, gguf, rows, k, x, tokens), f"gemm Q8_0 M={tokens}")
+    try:
+        for cfg in range(0, 7):
+            ctx.set_option(eff.OPT_GEMM_CONFIG, cfg)
+            for t, w in ((eff.Q8_0, wq), (eff.Q8_0R, wr)):
+                y1.write(np.full(tokens * rows, 0x7FC00000, np.uint32))
+                ctx.qmatmul(t, w, xb, y1, rows, k, tokens)
+                got = y1.read(np.uint32)
+                assert np.array_equal(got, ref), f"type {t} config {cfg}: {np.count_nonzero(got != ref)} differ"
+    finally:
+        ctx.set_option(eff.OPT_GEMM_CONFIG, 0)
+    for b in (wq, wr, xb, y0, y1):
+        b.free()
+
+
 @pytest.mark.parametrize("tokens,k", [(256, 2048), (300, 544), (777, 1024), (1100, 96), (2048, 512)])
 def test_gemm_q8_0r_same_bits_as_q8_0(ctx, eff, tokens, k):
     """The prefill GEMM over a repacked tensor (Q8_0R: quants and scales in
