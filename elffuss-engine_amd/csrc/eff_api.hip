@@ -257,19 +257,21 @@ bool sx_routes(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens) {
   if (router_gemm_type(wv.type) && (int64_t)tokens >= ctx->gemm_min_tokens) return false;
   if (ctx->gemv_kernel != 0 || !sx_applies(wv, tokens)) return false;
   if ((int64_t)tokens >= lo) return true;
-  // Q4_K from 7 tokens where k >= 4096, from 5120 rows (us, 7 / 8 tokens,
-  // the 16-row GEMV against the split-x product: 5120 x 5120 30.3 / 31.2
-  // against 18.4, 6144 x 4096 17.3 / 17.9 against 12.7, 14336 x 4096 23.1 /
-  // 23.7 against 19.4 / 19.6, 11008 x 4096 22.7 / 23.2 against 18.7, 32000 x
-  // 4096 34.5 / 37.3 against 30.0 / 30.2; at 4096 x 4096, 65536 x 2048 and
-  // 8192 x 2048 the GEMV stays faster: 10.0 / 10.3 against 10.6 at 4096 x 4096).
-  // Q6_K too (us, 7 / 8 tokens: 5120 x 5120 37.8 / 38.6 against 26.3, 6144 x
-  // 4096 22.3 / 22.9 against 16.6 / 16.7, 14336 x 4096 32.7 / 32.9 against
-  // 29.4, 24576 x 4096 47.4 / 48.4 against 42.4; where the GEMV's row tiles
-  // fill the CUs evenly it is faster: 16384 x 4096 26.2 / 27.1 against 30.0,
-  // 32000 x 4096 51.4 against 53.8)
-  if ((wv.type == Q4_K || wv.type == Q6_K) && !ctx->sx_min_tokens && tokens >= 7u && wv.k >= 4096u &&
-      wv.rows >= 5120u)
+  // From 7 tokens where k > 4096, every type: the 16-row GEMV then holds the
+  // x digits of 7-8 tokens in 97 KB of LDS or more, one workgroup per CU (us,
+  // 7 / 8 tokens, the GEMV against the split-x product: Q8_0 4096 x 4608 20.2 /
+  // 20.8 against 14.5, 5120 x 5120 31.9 / 33.0 against 23.6, 13824 x 5120 45.2 /
+  // 46.8 against 34.8; Q4_K 4096 x 4608 19.1 / 19.6 against 11.6; Q6_K 20.5 /
+  // 20.9 against 16.6 at 4096 x 5120). Where k = 4096, Q4_K and Q6_K from 5120
+  // rows (Q4_K 6144 x 4096 17.3 / 17.9 against 12.7, 14336 x 4096 23.1 / 23.7
+  // against 19.4 / 19.6, 32000 x 4096 34.5 / 37.3 against 30.0 / 30.2; Q6_K
+  // 6144 x 4096 22.3 / 22.9 against 16.6 / 16.7, 14336 x 4096 32.7 / 32.9 against
+  // 29.4; where the GEMV's row tiles fill the CUs evenly it is faster: Q6_K
+  // 16384 x 4096 26.2 / 27.1 against 30.0), not Q8_0 (14336 x 4096 27.6 / 27.9
+  // against 29.1) nor at 4096 rows (Q4_K 10.0 / 10.3 against 10.6). At 5 tokens
+  // the 4-row GEMV stays faster (Q8_0 5120 x 5120 20.8 against 23.6).
+  if (!ctx->sx_min_tokens && tokens >= 7u &&
+      (wv.k > 4096u || (wv.k == 4096u && (wv.type == Q4_K || wv.type == Q6_K) && wv.rows >= 5120u)))
     return true;
   GemvPlan p;
   return !gemv_rows_applies(wv, tokens) && !(mt_routes(tokens) && gemv_mt_plan(wv, tokens, p)) &&

@@ -57,7 +57,8 @@ extern "C" {
                                        (EFF_OPT_SPLIT_SLICES) */
 #define EFF_OPT_SPLIT_MIN_TOKENS 5  /* Q2_K, Q4_K, IQ2_XXS, Q8_0, Q6_K: tokens >= this run the split-x product, fewer
                                        the int8 matrix-core GEMVs (0: automatic, 5 for Q2_K and IQ2_XXS, 9 for the
-                                       others, Q4_K and Q6_K 7 where k >= 4096 from 5120 rows (default); else >= 4).
+                                       others, 7 where k > 4096 and for Q4_K and Q6_K where k = 4096 from 5120
+                                       rows (default); else >= 4).
                                        Q8_0 only below EFF_OPT_GEMM_MIN_TOKENS */
 #define EFF_OPT_GEMM_CONFIG      6  /* Q8_0 GEMM from the GEMM's threshold (below 6144 rows at every count),
                                        tiles (tuning; tokens x rows, waves along tokens x rows, LDS stages):
