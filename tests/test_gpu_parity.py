@@ -729,6 +729,29 @@ def test_router_split_x_where_gemv_digits_do_not_fit(ctx, eff, orc, tname, token
         b.free()
 
 
+@pytest.mark.parametrize("tname", ["Q8_0", "Q4_K", "Q6_K"])
+@pytest.mark.parametrize("tokens,k,rows,split", [(7, 4608, 300, True), (8, 5120, 300, True), (8, 4096, 300, False),
+                                                 (6, 4608, 300, False), (7, 4096, 5200, None)])
+def test_router_split_x_from_7_tokens(ctx, eff, orc, tname, tokens, k, rows, split):
+    """From 7 tokens where k > 4096 every type takes the split-x product (the
+    16-row GEMV would hold 7-8 tokens' x digits in 97 KB of LDS or more); at
+    k = 4096 only Q4_K and Q6_K, and only from 5120 rows; at 6 tokens the
+    GEMV stays. Both meet the f64 bar."""
+    if split is None:
+        split = tname != "Q8_0"
+    t, data, gguf, n = make_weights(eff, tname, rows, k, 900 + tokens + k + rows)
+    x = eff.fill_normal(901 + tokens, 1.0, tokens * k)
+    wb, xb, yb = upload_w(ctx, eff, tname, data, n), ctx.upload(x), ctx.alloc(tokens * rows * 4)
+    before = ctx.stats()
+    ctx.qmatmul(t, wb, xb, yb, rows, k, tokens)
+    after = ctx.stats()
+    assert after["split"] - before["split"] == (1 if split else 0)
+    check_close(yb.read(np.float32), orc.gemv_f64(oracle_type(orc, tname), gguf, rows, k, x, tokens),
+                f"router {tname} M={tokens} k={k} rows={rows}")
+    for b in (wb, xb, yb):
+        b.free()
+
+
 def test_split_x_k_slices_graph_replays(ctx, eff, orc):
     """A recorded k-sliced split-x product (its preparation and the product,
     64 row tiles in 4 slices) replayed several times, with eager sliced
