@@ -268,8 +268,10 @@ bool sx_routes(const eff_ctx *ctx, const WeightView &wv, uint32_t tokens) {
   // 6144 x 4096 22.3 / 22.9 against 16.6 / 16.7, 14336 x 4096 32.7 / 32.9 against
   // 29.4; where the GEMV's row tiles fill the CUs evenly it is faster: Q6_K
   // 16384 x 4096 26.2 / 27.1 against 30.0), not Q8_0 (14336 x 4096 27.6 / 27.9
-  // against 29.1) nor at 4096 rows (Q4_K 10.0 / 10.3 against 10.6). At 5 tokens
-  // the 4-row GEMV stays faster (Q8_0 5120 x 5120 20.8 against 23.6).
+  // against 29.1) nor at 4096 rows (Q4_K 10.0 / 10.3 against 10.6). At 5 and 6
+  // tokens the 4-row GEMV stays (Q8_0 5120 x 5120 at 5: 20.8 against 23.6;
+  // 13824 x 5120 at 6: 27.1 against 34.7; Q4_K at 6 would gain 4-15%, Q6_K
+  // -2 to 8%).
   if (!ctx->sx_min_tokens && tokens >= 7u &&
       (wv.k > 4096u || (wv.k == 4096u && (wv.type == Q4_K || wv.type == Q6_K) && wv.rows >= 5120u)))
     return true;
